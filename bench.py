@@ -1,0 +1,217 @@
+#!/usr/bin/env python3
+"""Per-layer training throughput of the MI355X NF4 LoRA path.
+
+Workload: one Llama-3-8B-shape decoder layer
+(hidden 4096, intermediate 14336, 32 q / 8 kv heads of 128), frozen weights
+N(0, 0.02) stored nf4-g128 (fp32 absmax), LoRA r=16 alpha=32 on all seven
+projections (A = randn*0.02, B ~ N(0, 0.02)), batch 1 x 2048 tokens, bf16
+activations N(0,1) and upstream gradient N(0,1).  One step = the reference's
+StreamingBlockFunction lifecycle: forward without grad, then backward =
+recompute with grad + autograd.grad + fp32 LoRA gradient accumulation.
+Weights are resident in a device slot when the timed region starts.
+Seeds: weights 1234, X 1, dY 2, A 3, B 4.
+
+Prints ONE JSON line (rank 0).  --gpus above 1 is refused: this build runs on
+one GPU.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+METRIC = "train tokens/s per layer fwd+recompute+bwd (Llama-3-8B NF4 layer); % bf16 MFMA peak"
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA (no sparsity)
+PEAK_HBM_GBPS = 8000.0
+
+CONFIGS = {
+    "llama8b": dict(H=4096, I=14336, heads=32, kv=8, D=128, eps=1e-5, r=16, alpha=32.0, B=1, S=2048,
+                    theta=500000.0),
+    "tiny": dict(H=256, I=688, heads=4, kv=4, D=64, eps=1e-5, r=8, alpha=16.0, B=2, S=128,
+                 theta=500000.0),
+}
+PROJ = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
+        "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj")
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def layer_shapes(c):
+    H, I, D = c["H"], c["I"], c["D"]
+    return {"self_attn.q_proj": (c["heads"] * D, H), "self_attn.k_proj": (c["kv"] * D, H),
+            "self_attn.v_proj": (c["kv"] * D, H), "self_attn.o_proj": (H, c["heads"] * D),
+            "mlp.gate_proj": (I, H), "mlp.up_proj": (I, H), "mlp.down_proj": (H, I)}
+
+
+def make_weights(c):
+    import torch
+    g = torch.Generator().manual_seed(1234)
+    w = {}
+    for name, shape in layer_shapes(c).items():
+        w[f"{name}.weight"] = (torch.randn(shape, generator=g) * 0.02).to(torch.bfloat16)
+    w["input_layernorm.weight"] = torch.ones(c["H"], dtype=torch.bfloat16)
+    w["post_attention_layernorm.weight"] = torch.ones(c["H"], dtype=torch.bfloat16)
+    return w
+
+
+def algorithmic_flops(c):
+    M = c["B"] * c["S"]
+    P = sum(n * k for n, k in layer_shapes(c).values())
+    base = 6 * M * P
+    attn = 4 * (4 * c["S"] * c["S"] * c["D"] * c["heads"] * c["B"]) // 2
+    lora = 4 * 2 * M * c["r"] * sum(n + k for n, k in layer_shapes(c).values())
+    return base + attn + lora
+
+
+def cpu_baseline(c, block, tokens):
+    """The reference's CPU training path (device='cpu': decoded bf16 weights,
+    dense_block, recompute + autograd.grad) restated in oracle/layer.py, timed
+    for one layer step at `tokens` tokens on this host's cores."""
+    import numpy as np
+    import torch
+    from oracle import codec as oc
+    from oracle import layer as OL
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    weights = {}
+    for name, entry in block.storage_specs.items():
+        spec = entry["spec"]
+        bits = oc.decode4(block.host_weights[entry["parts"]["payload"]].numpy(),
+                          block.host_weights[entry["parts"]["scales"]].numpy(), spec["numel"],
+                          lut=oc.NF4_LUT)
+        weights[name] = torch.from_numpy(bits.astype(np.int16)).view(torch.bfloat16).view(spec["shape"])
+    for k, v in block.host_weights.items():
+        if not k.startswith("@"):
+            weights[k] = v
+    loras = {n: OL.Lora(n, p.A.detach().cpu(), p.B.detach().cpu(), p.alpha)
+             for n, p in block.adapters.items()}
+    g = torch.Generator().manual_seed(1)
+    hidden = torch.randn(1, tokens, c["H"], generator=g).to(torch.bfloat16)
+    dy = torch.randn(1, tokens, c["H"], generator=torch.Generator().manual_seed(2)).to(torch.bfloat16)
+    rot = OL.rotary(1, tokens, c["D"], c["theta"], torch.bfloat16)
+    mask = OL.causal_mask(1, tokens, torch.bfloat16)
+    kw = dict(heads=c["heads"], kv_heads=c["kv"], head_dim=c["D"], eps=c["eps"])
+    t0 = time.perf_counter()
+    OL.streaming_step(hidden, rot, mask, dy, weights=weights, loras=loras, cfg=kw)
+    dt = time.perf_counter() - t0
+    return {"value": tokens / dt, "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"one layer step (fwd + recompute + bwd) at {tokens} tokens (batch 1) of the "
+                      f"same layer, oracle/layer.py on {cores} host cores, {dt:.2f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="llama8b", choices=sorted(CONFIGS))
+    ap.add_argument("--cpu-tokens", type=int, default=256)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one MI355X; "
+              "see DESIGN.md for how the path would shard", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from spilltune_amd import ops, slots
+    from spilltune_amd.dense import CausalMask
+    from spilltune_amd.recompute import streaming_block
+
+    c = CONFIGS[args.config]
+    dev = torch.device("cuda:0")
+    log(f"building {args.config} layer (nf4-g128, LoRA r={c['r']} on all 7 projections)")
+    t0 = time.perf_counter()
+    weights = make_weights(c)
+    block = slots.make_dense_block(0, weights, codec="nf4-g128", heads=c["heads"], kv_heads=c["kv"],
+                                   head_dim=c["D"], eps=c["eps"], rank=c["r"], alpha=c["alpha"],
+                                   targets=PROJ, device=dev,
+                                   generator=torch.Generator().manual_seed(3))
+    gB = torch.Generator().manual_seed(4)
+    with torch.no_grad():
+        for name in sorted(block.adapters):
+            p = block.adapters[name]
+            p.B.copy_(torch.randn(p.B.shape, generator=gB) * 0.02)
+    session = slots.ResidentSession([block], dev)
+    log(f"layer encoded and resident in {time.perf_counter() - t0:.1f} s "
+        f"({session.capacity / 1e6:.1f} MB slot)")
+
+    B, S, H = c["B"], c["S"], c["H"]
+    X = torch.randn(B, S, H, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16).to(dev)
+    dY = torch.randn(B, S, H, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).to(dev)
+    pos = torch.arange(S, device=dev).float()
+    inv = 1.0 / c["theta"] ** (torch.arange(0, c["D"], 2, device=dev).float() / c["D"])
+    phase = torch.outer(pos, inv)
+    phase = torch.cat((phase, phase), -1)[None].expand(B, S, c["D"])
+    rot = (phase.cos().to(torch.bfloat16).contiguous(), phase.sin().to(torch.bfloat16).contiguous())
+    mask = CausalMask(B, S)
+
+    def step():
+        h = X.detach().requires_grad_(True)
+        with session.run():
+            out = streaming_block(h, rot, mask, block.functional, block.kwargs,
+                                  session.reloader(block), block.adapters, block.index)
+            out.backward(dY)
+        return h
+
+    for i in range(args.warmup):
+        step()
+        if i == 0:
+            torch.cuda.synchronize()
+            log("first step done")
+    torch.cuda.synchronize()
+    ops.TIMER = ops.KernelTimer()
+    t_start = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t_start
+    timer, ops.TIMER = ops.TIMER, None
+    ms = elapsed * 1e3 / args.steps
+    tokens = B * S
+    value = tokens * args.steps / elapsed
+    flops = algorithmic_flops(c)
+    kern = timer.summary()
+    # dominant fused GEMM: largest total time over the timed region
+    key, info = max(kern.items(), key=lambda kv: kv[1]["launches"] * kv[1]["avg_ms"])
+    _, M, N, K = key
+    kflops = 2.0 * M * N * K
+    achieved = kflops / (info["avg_ms"] * 1e-3) / 1e12
+    for k2, v2 in sorted(kern.items(), key=lambda kv: -kv[1]["launches"] * kv[1]["avg_ms"]):
+        tf = 2.0 * k2[1] * k2[2] * k2[3] / (v2["avg_ms"] * 1e-3) / 1e12
+        log(f"  q4gemm {k2[0]:5s} M={k2[1]} N={k2[2]} K={k2[3]}: {v2['launches']} launches, "
+            f"{v2['avg_ms']:.3f} ms avg, {tf:.0f} TFLOP/s ({tf / PEAK_BF16_TFLOPS:.1%})")
+    gemm_ms = sum(v["launches"] * v["avg_ms"] for v in kern.values()) / args.steps
+    log(f"step {ms:.3f} ms, fused q4 GEMMs {gemm_ms:.3f} ms/step; layer "
+        f"{flops / (ms * 1e-3) / 1e12:.0f} TFLOP/s algorithmic")
+
+    result = {
+        "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,0.02) weights -> nf4-g128, N(0,1) activations/grads)",
+        "config": {"workload": f"{args.config}: one decoder layer fwd+recompute+bwd, "
+                               f"{B}x{S} tokens, nf4-g128, LoRA r={c['r']} on 7 projections",
+                   "global_batch": B, "seq_len": S, "hidden": H, "intermediate": c["I"],
+                   "heads": c["heads"], "kv_heads": c["kv"], "parallelism": "single GPU"},
+        "layer_mfma_frac": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "algorithmic_tflop_per_step": round(flops / 1e12, 4),
+        "roofline": {"bound": "mfma", "kernel": f"q4gemm_{key[0]} M={M} N={N} K={K}",
+                     "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "avg_ms": round(info["avg_ms"], 4)},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        log(f"timing the CPU path at {args.cpu_tokens} tokens")
+        result["cpu_baseline"] = cpu_baseline(c, block, args.cpu_tokens)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

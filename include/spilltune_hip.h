@@ -1,0 +1,189 @@
+/*
+ * spilltune_hip.h -- C ABI of the MI355X (gfx950) per-layer NF4 LoRA training
+ * kernels (libspilltune_hip.so).
+ *
+ * Conventions
+ *  - Every pointer is a device pointer owned by the caller (PyTorch tensors in
+ *    the Python host), except `lut16` and `seg_end`, which are host arrays read
+ *    during the call.  bf16 data is passed as uint16_t bit patterns.
+ *  - Matrices are row-major; `ld*` arguments are row strides in elements.
+ *  - Every call is asynchronous on `stream` (a hipStream_t) and stateless, so
+ *    it may be issued from the autograd worker thread.  Nothing allocates:
+ *    scratch comes in through `workspace`/`workspace_bytes`; the matching
+ *    *_workspace_bytes() query says how much a call needs (0 = none).
+ *  - Return value: ST_OK (0) or an ST_E* code; st_last_error() then returns a
+ *    thread-local message.  The Python host maps ST_EINVAL/ST_EUNSUPPORTED to
+ *    ValueError('unsupported_capability: ...') and ST_EDEVICE to RuntimeError,
+ *    as the reference does for its own failures (config.py:34-62).
+ *
+ * Reference interfaces replaced (paths relative to /root/reference/src/
+ * ram_vram_finetune):
+ *  - quantization/codecs.py:158-170 decode_into and the bitsandbytes
+ *    dequantize_4bit call at quantization/nf4_backend.py:312   -> st_dequant4*
+ *  - finetune/lora.py:205-220 LoRAProjection.forward (base F.linear + fp32
+ *    LoRA) and quantization/nf4_backend_cuda.py:888-917 linear_cuda
+ *    (bnb.matmul_4bit)                                      -> st_q4_linear_fwd
+ *  - the autograd VJP of the same projection inside training/recompute.py:
+ *    102-105 (dX = dY W, dA, dB)           -> st_q4_linear_dgrad, st_lora_*
+ *  - adapters/dense.py:115-117 rms, :137-141 rotate, :146-148 eager softmax,
+ *    :153 silu(gate)*up                    -> st_rmsnorm_*, st_rope_*,
+ *                                             st_softmax_causal_*, st_swiglu_*
+ */
+#ifndef SPILLTUNE_HIP_H
+#define SPILLTUNE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* st_stream_t; /* == hipStream_t */
+
+enum {
+  ST_OK = 0,
+  ST_EINVAL = 1,       /* bad shape / pointer / alignment                */
+  ST_EUNSUPPORTED = 2, /* valid request outside what the kernels support  */
+  ST_EDEVICE = 3,      /* HIP runtime / launch failure                    */
+  ST_EWORKSPACE = 4    /* workspace missing or too small                  */
+};
+
+/* storage flags */
+#define ST_FLAG_HI_NIBBLE_FIRST 1 /* element 2i in the high nibble (bitsandbytes) */
+
+/* dtype codes for st_lora_gemm operands */
+#define ST_DTYPE_BF16 0
+#define ST_DTYPE_F32 1
+
+int st_abi_version(void);
+const char* st_last_error(void);
+
+/* ---------------------------------------------------------------- dequant */
+/*
+ * out[i] = bf16_rne(lut16[code_i] * scales[i / group]) for i < numel, codes
+ * packed two per byte (low nibble first unless ST_FLAG_HI_NIBBLE_FIRST),
+ * groups over the FLATTENED tensor (they straddle rows when K % group != 0).
+ * group is 64 or 128.  Replaces codecs.py:158-170 (lut16[c] = c - 8 for
+ * int4-sym-g128) and the NF4 decode of nf4_backend.py:312.
+ */
+int st_dequant4(const uint8_t* payload, const float* scales, int64_t numel, int32_t group,
+                const float* lut16, int32_t flags, uint16_t* out, st_stream_t stream);
+
+/*
+ * bitsandbytes NF4 + double quantisation (nf4_backend.py:184-240 layout):
+ * absmax_j = nested_map[absmax_u8[j]] * nested_absmax[j / 256] + offset (fp32),
+ * out[i] = bf16_rne(lut16[code_i] * absmax_{i / 64}).  nested_map is a 256-entry
+ * device array.  Parity with bitsandbytes itself is unpinned.
+ */
+int st_dequant4_dq(const uint8_t* packed, const uint8_t* absmax_u8, const float* nested_absmax,
+                   const float* nested_map, float offset, int64_t numel, const float* lut16,
+                   int32_t flags, uint16_t* out, st_stream_t stream);
+
+/* ------------------------------------------------- fused projection GEMMs */
+/*
+ * Forward of a frozen 4-bit projection with LoRA (lora.py:218-220):
+ *   base[m,n] = bf16( sum_k x[m,k] * W[n,k] )            (W = dequant, bf16)
+ *   y[m,n]    = bf16( base + lora_scale * sum_j t[m, seg(n)*rank + j] * lora_b[n,j] )
+ *   y[m,n]    = bf16( residual[m,n] + y[m,n] )            (if residual)
+ * W [N,K] is payload/scales in flat groups of 128.  W is dequantised into LDS
+ * inside the GEMM (never written to HBM as bf16) when K % 128 == 0; other K go
+ * through a bf16 copy of W in `workspace` (st_q4_linear_fwd_workspace_bytes).
+ * `t` = x_f32 A^T from st_lora_xa ([M, nseg*rank] fp32) or NULL for no LoRA.
+ * nseg/seg_end describe N-concatenated projections (fused q|k|v, gate|up):
+ * column n belongs to segment s = #{seg_end[i] <= n}; segment ends must be
+ * multiples of 32.  nseg = 1 with seg_end[0] = N for a single projection.
+ */
+int64_t st_q4_linear_fwd_workspace_bytes(int64_t M, int64_t N, int64_t K);
+int st_q4_linear_fwd(const uint16_t* x, int64_t M, int64_t K, int64_t ldx,
+                     const uint8_t* payload, const float* scales, int64_t N,
+                     const float* lut16, int32_t flags,
+                     const float* t, int64_t ldt, const float* lora_b, int32_t rank,
+                     float lora_scale, int32_t nseg, const int64_t* seg_end,
+                     const uint16_t* residual, int64_t ldr,
+                     uint16_t* y, int64_t ldy,
+                     void* workspace, int64_t workspace_bytes, st_stream_t stream);
+
+/*
+ * Input gradient of the same projection (autograd of lora.py:218-220):
+ *   dx[m,k] = bf16( bf16(sum_n dy[m,n] W[n,k]) + bf16(sum_j dt[m,j] lora_a[j,k]) )
+ * with dt = lora_scale * dy_f32 B ([M, lora_k] fp32, from st_lora_bwd_dy;
+ * N-concatenated projections stack their dt columns and lora_a rows) or
+ * dt == NULL for no LoRA term.  W [N,K] as above; dequantised transposed into
+ * LDS when K % 128 == 0.
+ */
+int64_t st_q4_linear_dgrad_workspace_bytes(int64_t M, int64_t N, int64_t K);
+int st_q4_linear_dgrad(const uint16_t* dy, int64_t M, int64_t N, int64_t lddy,
+                       const uint8_t* payload, const float* scales, int64_t K,
+                       const float* lut16, int32_t flags,
+                       const float* dt, int64_t lddt, const float* lora_a, int32_t lora_k,
+                       uint16_t* dx, int64_t lddx,
+                       void* workspace, int64_t workspace_bytes, st_stream_t stream);
+
+/* ------------------------------------------------------- LoRA rank-r work */
+/*
+ * Generic skinny fp32-accumulating product used by the LoRA terms:
+ *   out[m,n] = (accumulate ? out[m,n] : 0) + alpha * sum_k a(m,k) * b(k,n)
+ * a(m,k) = a[m*sam + k*sak], b(k,n) = b[k*sbk + n*sbn], each bf16 or fp32.
+ */
+int64_t st_lora_gemm_workspace_bytes(int64_t Mo, int64_t No, int64_t Kc);
+int st_lora_gemm(int64_t Mo, int64_t No, int64_t Kc,
+                 const void* a, int32_t a_dtype, int64_t sam, int64_t sak,
+                 const void* b, int32_t b_dtype, int64_t sbk, int64_t sbn,
+                 float alpha, float* out, int64_t ldo, int32_t accumulate,
+                 void* workspace, int64_t workspace_bytes, st_stream_t stream);
+
+/* ------------------------------------------------------- layer elementwise */
+/* y = w * bf16(x * rsqrt(mean(x^2) + eps)) (dense.py:115-117); rstd[row] saved. */
+int st_rmsnorm_fwd(const uint16_t* x, const uint16_t* w, int64_t rows, int64_t H, float eps,
+                   uint16_t* y, float* rstd, st_stream_t stream);
+/* dx = bf16(VJP of the above) [+ dres, added in bf16 like autograd's sum]. */
+int st_rmsnorm_bwd(const uint16_t* dy, const uint16_t* x, const uint16_t* w, const float* rstd,
+                   const uint16_t* dres, int64_t rows, int64_t H, uint16_t* dx,
+                   st_stream_t stream);
+
+/*
+ * Rotary embedding (dense.py:137-141) fused with the [B,S,heads,D] ->
+ * [B,heads,S,D] relayout: out = bf16(bf16(x*cos) + bf16(rot(x)*sin)), rot(x) =
+ * cat(-x[D/2:], x[:D/2]); cos/sin are [B,S,D] bf16.  rotate = 0 copies only
+ * (the value projection).  x rows have stride ldx elements.
+ */
+int st_rope_fwd(const uint16_t* x, int64_t ldx, const uint16_t* cos, const uint16_t* sin,
+                int64_t B, int64_t S, int64_t heads, int64_t D, int32_t rotate,
+                uint16_t* out, st_stream_t stream);
+/* VJP of st_rope_fwd: dout [B,heads,S,D] -> dx rows of stride lddx. */
+int st_rope_bwd(const uint16_t* dout, const uint16_t* cos, const uint16_t* sin,
+                int64_t B, int64_t S, int64_t heads, int64_t D, int32_t rotate,
+                uint16_t* dx, int64_t lddx, st_stream_t stream);
+/* [B,heads,S,D] -> [B,S,heads*D] copy (attention output relayout). */
+int st_heads_to_tokens(const uint16_t* x, int64_t B, int64_t S, int64_t heads, int64_t D,
+                       uint16_t* out, st_stream_t stream);
+int st_tokens_to_heads(const uint16_t* x, int64_t B, int64_t S, int64_t heads, int64_t D,
+                       uint16_t* out, st_stream_t stream);
+
+/* a = bf16(bf16(silu(g)) * u) (dense.py:153); g/u rows of stride ldg/ldu. */
+int st_swiglu_fwd(const uint16_t* g, int64_t ldg, const uint16_t* u, int64_t ldu,
+                  int64_t rows, int64_t I, uint16_t* a, int64_t lda, st_stream_t stream);
+int st_swiglu_bwd(const uint16_t* da, int64_t ldda, const uint16_t* g, int64_t ldg,
+                  const uint16_t* u, int64_t ldu, int64_t rows, int64_t I,
+                  uint16_t* dg, int64_t lddg, uint16_t* du, int64_t lddu, st_stream_t stream);
+
+/*
+ * Eager causal softmax of dense.py:146-147 over score rows [nrows, S] (row r
+ * is query position r % S of its head): x = bf16(s * scale); p = bf16(softmax_fp32
+ * over keys c <= r % S), 0 for c > r % S.  stats[r] = (max, sum) for the VJP.
+ */
+int st_softmax_causal_fwd(const uint16_t* s, int64_t nrows, int64_t S, float scale,
+                          uint16_t* p, float* stats, st_stream_t stream);
+/*
+ * VJP through softmax(dtype=fp32).to(bf16) and the scale multiply, using the
+ * fp32 probabilities recomputed from s and stats:
+ *   ds = bf16( bf16(p32 * (dp - sum_c dp_c p32_c)) * scale ).
+ */
+int st_softmax_causal_bwd(const uint16_t* s, const float* stats, const uint16_t* dp,
+                          int64_t nrows, int64_t S, float scale, uint16_t* ds,
+                          st_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SPILLTUNE_HIP_H */

@@ -1,0 +1,152 @@
+// Standalone 4-bit -> bf16 dequantisation (HBM-bound).
+//
+// Replaces the chunked torch decode of codecs.py:158-170 (int4-sym-g128) and
+// the NF4 decode inside bitsandbytes (nf4_backend.py:312).  One fp32 multiply
+// then RNE to bf16 per element: bit-identical to codecs.py:168-170.
+//
+// Layout: each thread owns 16 payload bytes = 32 consecutive elements (they lie
+// in one group for group 64/128), reads one scale, looks the codes up in a
+// 16-entry fp32 codebook held in LDS, and writes 64 bytes of bf16 with four
+// 16-byte stores.  Per element: 0.5 B read + 2 B written (+4/group B scale).
+#include "common.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ unsigned nib(uint32_t w, int e, int hi_first) {
+  int sh = 4 * (e ^ hi_first);
+  return (w >> sh) & 15u;
+}
+
+// 8 elements of one packed dword -> 4 packed bf16x2 words
+__device__ __forceinline__ void decode_dword(uint32_t w, float s, const float* lut, int hi_first,
+                                             uint32_t* o) {
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    float a = lut[nib(w, e, hi_first)] * s;
+    float b = lut[nib(w, e + 1, hi_first)] * s;
+    o[e / 2] = st::pack_bf16x2(a, b);
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void dequant4_vec(const uint4* __restrict__ payload,
+                                                        const float* __restrict__ scales,
+                                                        int64_t nchunks, int group_shift,
+                                                        Lut16 lut, int hi_first,
+                                                        uint4* __restrict__ out) {
+  __shared__ float lut_s[16];
+  if (threadIdx.x < 16) lut_s[threadIdx.x] = lut.v[threadIdx.x];
+  __syncthreads();
+  int64_t c = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (c >= nchunks) return;
+  uint4 p = payload[c];
+  float s = scales[(c * 32) >> group_shift];
+  uint32_t o[16];
+  decode_dword(p.x, s, lut_s, hi_first, o + 0);
+  decode_dword(p.y, s, lut_s, hi_first, o + 4);
+  decode_dword(p.z, s, lut_s, hi_first, o + 8);
+  decode_dword(p.w, s, lut_s, hi_first, o + 12);
+  uint4* dst = out + c * 4;
+  dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
+  dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
+  dst[2] = make_uint4(o[8], o[9], o[10], o[11]);
+  dst[3] = make_uint4(o[12], o[13], o[14], o[15]);
+}
+
+// element-wise tail / unaligned path: one element per thread
+__global__ __launch_bounds__(kThreads) void dequant4_scalar(const uint8_t* __restrict__ payload,
+                                                           const float* __restrict__ scales,
+                                                           int64_t begin, int64_t numel,
+                                                           int group, Lut16 lut, int hi_first,
+                                                           uint16_t* __restrict__ out) {
+  int64_t i = begin + (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= numel) return;
+  unsigned b = payload[i >> 1];
+  unsigned code = (b >> (4 * ((unsigned)(i & 1) ^ (unsigned)hi_first))) & 15u;
+  out[i] = st::f32_to_bf16(lut.v[code] * scales[i / group]);
+}
+
+// bitsandbytes double-quantised absmax, then the same decode (block 64).
+__global__ __launch_bounds__(kThreads) void dequant4_dq(const uint8_t* __restrict__ packed,
+                                                       const uint8_t* __restrict__ absmax_u8,
+                                                       const float* __restrict__ nested_absmax,
+                                                       const float* __restrict__ nested_map,
+                                                       float offset, int64_t numel, Lut16 lut,
+                                                       int hi_first,
+                                                       uint16_t* __restrict__ out) {
+  __shared__ float lut_s[16];
+  if (threadIdx.x < 16) lut_s[threadIdx.x] = lut.v[threadIdx.x];
+  __syncthreads();
+  // 2 elements (one byte) per thread
+  int64_t byte = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  int64_t i0 = byte * 2;
+  if (i0 >= numel) return;
+  int64_t j = i0 / 64;
+  float prod = nested_map[absmax_u8[j]] * nested_absmax[j / 256];
+  float amax = prod + offset;
+  unsigned b = packed[byte];
+  unsigned c0 = hi_first ? (b >> 4) : (b & 15u);
+  unsigned c1 = hi_first ? (b & 15u) : (b >> 4);
+  out[i0] = st::f32_to_bf16(lut_s[c0] * amax);
+  if (i0 + 1 < numel) out[i0 + 1] = st::f32_to_bf16(lut_s[c1] * amax);
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace
+
+namespace st {
+int launch_dequant4(const uint8_t* payload, const float* scales, int64_t numel, int32_t group,
+                    const float* lut16, int32_t flags, uint16_t* out, hipStream_t stream) {
+  Lut16 lut;
+  for (int i = 0; i < 16; ++i) lut.v[i] = lut16[i];
+  int hi = (flags & ST_FLAG_HI_NIBBLE_FIRST) ? 1 : 0;
+  int64_t vec_elems = 0;
+  if (aligned16(payload) && aligned16(out)) {
+    int64_t nchunks = numel / 32;
+    if (nchunks > 0) {
+      int shift = group == 128 ? 7 : 6;
+      dequant4_vec<<<(unsigned)cdiv(nchunks, kThreads), kThreads, 0, stream>>>(
+          (const uint4*)payload, scales, nchunks, shift, lut, hi, (uint4*)out);
+      vec_elems = nchunks * 32;
+    }
+  }
+  if (vec_elems < numel) {
+    int64_t rest = numel - vec_elems;
+    dequant4_scalar<<<(unsigned)cdiv(rest, kThreads), kThreads, 0, stream>>>(
+        payload, scales, vec_elems, numel, group, lut, hi, out);
+  }
+  return check_launch("dequant4");
+}
+}  // namespace st
+
+extern "C" int st_dequant4(const uint8_t* payload, const float* scales, int64_t numel,
+                           int32_t group, const float* lut16, int32_t flags, uint16_t* out,
+                           st_stream_t stream) {
+  ST_CHECK_ARG(numel >= 0, "st_dequant4: negative numel");
+  ST_CHECK_ARG(group == 64 || group == 128, "st_dequant4: group must be 64 or 128, got %d", group);
+  ST_CHECK_ARG(lut16 != nullptr, "st_dequant4: lut16 is NULL");
+  if (numel == 0) return ST_OK;
+  ST_CHECK_ARG(payload && scales && out, "st_dequant4: NULL device pointer");
+  return st::launch_dequant4(payload, scales, numel, group, lut16, flags, out,
+                             (hipStream_t)stream);
+}
+
+extern "C" int st_dequant4_dq(const uint8_t* packed, const uint8_t* absmax_u8,
+                              const float* nested_absmax, const float* nested_map, float offset,
+                              int64_t numel, const float* lut16, int32_t flags, uint16_t* out,
+                              st_stream_t stream) {
+  ST_CHECK_ARG(numel >= 0, "st_dequant4_dq: negative numel");
+  ST_CHECK_ARG(lut16 != nullptr, "st_dequant4_dq: lut16 is NULL");
+  if (numel == 0) return ST_OK;
+  ST_CHECK_ARG(packed && absmax_u8 && nested_absmax && nested_map && out,
+               "st_dequant4_dq: NULL device pointer");
+  Lut16 lut;
+  for (int i = 0; i < 16; ++i) lut.v[i] = lut16[i];
+  int hi = (flags & ST_FLAG_HI_NIBBLE_FIRST) ? 1 : 0;
+  int64_t bytes = st::cdiv(numel, 2);
+  dequant4_dq<<<(unsigned)st::cdiv(bytes, kThreads), kThreads, 0, (hipStream_t)stream>>>(
+      packed, absmax_u8, nested_absmax, nested_map, offset, numel, lut, hi, out);
+  return st::check_launch("dequant4_dq");
+}

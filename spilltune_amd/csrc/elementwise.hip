@@ -1,0 +1,355 @@
+// Decoder-layer elementwise kernels (HBM-bound): RMSNorm, rotary embedding
+// with the head relayout, SwiGLU, and the eager causal softmax of attention.
+//
+// Each forward reproduces the reference's bf16 rounding points
+// (adapters/dense.py:115-153); each backward reproduces the roundings that
+// PyTorch autograd applies to the same graph (bf16 gradients of bf16 ops,
+// fp32 inside the fp32 regions).
+#include <cmath>
+
+#include "common.h"
+
+namespace {
+
+constexpr int NTH = 256;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  __syncthreads();
+  if (l == 0) red[w] = v;
+  __syncthreads();
+  float s = 0.0f;
+  for (int i = 0; i < NTH / 64; ++i) s += red[i];
+  return s;
+}
+
+// ------------------------------------------------------------------ RMSNorm
+__global__ __launch_bounds__(NTH) void rmsnorm_fwd(const uint16_t* __restrict__ x,
+                                                  const uint16_t* __restrict__ w, int64_t H,
+                                                  float eps, uint16_t* __restrict__ y,
+                                                  float* __restrict__ rstd) {
+  __shared__ float red[NTH / 64];
+  const int64_t row = blockIdx.x;
+  const uint16_t* xr = x + row * H;
+  float ss = 0.0f;
+  for (int64_t i = threadIdx.x; i < H; i += NTH) {
+    float v = st::bf16_to_f32(xr[i]);
+    ss += v * v;
+  }
+  ss = block_sum(ss, red);
+  const float r = 1.0f / sqrtf(ss / (float)H + eps);
+  if (threadIdx.x == 0) rstd[row] = r;
+  for (int64_t i = threadIdx.x; i < H; i += NTH) {
+    float n = st::bf16r(st::bf16_to_f32(xr[i]) * r);
+    y[row * H + i] = st::f32_to_bf16(st::bf16_to_f32(w[i]) * n);
+  }
+}
+
+__global__ __launch_bounds__(NTH) void rmsnorm_bwd(const uint16_t* __restrict__ dy,
+                                                  const uint16_t* __restrict__ x,
+                                                  const uint16_t* __restrict__ w,
+                                                  const float* __restrict__ rstd,
+                                                  const uint16_t* __restrict__ dres, int64_t H,
+                                                  uint16_t* __restrict__ dx) {
+  __shared__ float red[NTH / 64];
+  const int64_t row = blockIdx.x;
+  const float r = rstd[row];
+  float dot = 0.0f;
+  for (int64_t i = threadIdx.x; i < H; i += NTH) {
+    float dn = st::bf16r(st::bf16_to_f32(dy[row * H + i]) * st::bf16_to_f32(w[i]));
+    dot += dn * st::bf16_to_f32(x[row * H + i]);
+  }
+  dot = block_sum(dot, red);
+  const float c = r * r * r * dot / (float)H;
+  for (int64_t i = threadIdx.x; i < H; i += NTH) {
+    float dn = st::bf16r(st::bf16_to_f32(dy[row * H + i]) * st::bf16_to_f32(w[i]));
+    float g = st::bf16r(r * dn - st::bf16_to_f32(x[row * H + i]) * c);
+    if (dres) g = st::bf16r(st::bf16_to_f32(dres[row * H + i]) + g);
+    dx[row * H + i] = st::f32_to_bf16(g);
+  }
+}
+
+// ------------------------------------------------------------------ RoPE
+// one thread per (b, s, h, d) element; grid over B*S*heads*D
+__global__ __launch_bounds__(NTH) void rope_fwd(const uint16_t* __restrict__ x, int64_t ldx,
+                                               const uint16_t* __restrict__ cs,
+                                               const uint16_t* __restrict__ sn, int64_t S,
+                                               int64_t heads, int64_t D, int rotate, int64_t total,
+                                               uint16_t* __restrict__ out) {
+  int64_t e = (int64_t)blockIdx.x * NTH + threadIdx.x;
+  if (e >= total) return;
+  int64_t d = e % D, t = e / D;
+  int64_t h = t % heads;
+  t /= heads;
+  int64_t s = t % S, b = t / S;
+  const uint16_t* xr = x + (b * S + s) * ldx + h * D;
+  float v = st::bf16_to_f32(xr[d]);
+  float o = v;
+  if (rotate) {
+    int64_t half = D / 2;
+    float rot = d < half ? -st::bf16_to_f32(xr[d + half]) : st::bf16_to_f32(xr[d - half]);
+    int64_t ci = (b * S + s) * D + d;
+    o = st::bf16r(v * st::bf16_to_f32(cs[ci])) + st::bf16r(rot * st::bf16_to_f32(sn[ci]));
+  }
+  out[((b * heads + h) * S + s) * D + d] = st::f32_to_bf16(o);
+}
+
+__global__ __launch_bounds__(NTH) void rope_bwd(const uint16_t* __restrict__ g,
+                                               const uint16_t* __restrict__ cs,
+                                               const uint16_t* __restrict__ sn, int64_t S,
+                                               int64_t heads, int64_t D, int rotate, int64_t total,
+                                               uint16_t* __restrict__ dx, int64_t lddx) {
+  int64_t e = (int64_t)blockIdx.x * NTH + threadIdx.x;
+  if (e >= total) return;
+  int64_t d = e % D, t = e / D;
+  int64_t h = t % heads;
+  t /= heads;
+  int64_t s = t % S, b = t / S;
+  const uint16_t* gr = g + ((b * heads + h) * S + s) * D;
+  float gv = st::bf16_to_f32(gr[d]);
+  float o = gv;
+  if (rotate) {
+    int64_t half = D / 2;
+    int64_t cb = (b * S + s) * D;
+    float a = st::bf16r(gv * st::bf16_to_f32(cs[cb + d]));
+    // r[d] = gs[d + half] (d < half), -gs[d - half] (d >= half), gs = bf16(g * sin)
+    int64_t dd = d < half ? d + half : d - half;
+    float gs = st::bf16r(st::bf16_to_f32(gr[dd]) * st::bf16_to_f32(sn[cb + dd]));
+    o = a + (d < half ? gs : -gs);
+  }
+  dx[(b * S + s) * lddx + h * D + d] = st::f32_to_bf16(o);
+}
+
+__global__ __launch_bounds__(NTH) void relayout(const uint16_t* __restrict__ x, int64_t S,
+                                               int64_t heads, int64_t D, int64_t total,
+                                               int to_tokens, uint16_t* __restrict__ out) {
+  int64_t e = (int64_t)blockIdx.x * NTH + threadIdx.x;
+  if (e >= total) return;
+  int64_t d = e % D, t = e / D;
+  int64_t h = t % heads;
+  t /= heads;
+  int64_t s = t % S, b = t / S;
+  int64_t tok = ((b * S + s) * heads + h) * D + d;
+  int64_t hd = ((b * heads + h) * S + s) * D + d;
+  if (to_tokens)
+    out[tok] = x[hd];
+  else
+    out[hd] = x[tok];
+}
+
+// ------------------------------------------------------------------ SwiGLU
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+__global__ __launch_bounds__(NTH) void swiglu_fwd(const uint16_t* __restrict__ g, int64_t ldg,
+                                                 const uint16_t* __restrict__ u, int64_t ldu,
+                                                 int64_t I, int64_t total,
+                                                 uint16_t* __restrict__ a, int64_t lda) {
+  int64_t e = (int64_t)blockIdx.x * NTH + threadIdx.x;
+  if (e >= total) return;
+  int64_t r = e / I, c = e % I;
+  float gv = st::bf16_to_f32(g[r * ldg + c]);
+  float s = st::bf16r(gv / (1.0f + expf(-gv)));
+  a[r * lda + c] = st::f32_to_bf16(s * st::bf16_to_f32(u[r * ldu + c]));
+}
+
+__global__ __launch_bounds__(NTH) void swiglu_bwd(const uint16_t* __restrict__ da, int64_t ldda,
+                                                 const uint16_t* __restrict__ g, int64_t ldg,
+                                                 const uint16_t* __restrict__ u, int64_t ldu,
+                                                 int64_t I, int64_t total,
+                                                 uint16_t* __restrict__ dg, int64_t lddg,
+                                                 uint16_t* __restrict__ du, int64_t lddu) {
+  int64_t e = (int64_t)blockIdx.x * NTH + threadIdx.x;
+  if (e >= total) return;
+  int64_t r = e / I, c = e % I;
+  float gv = st::bf16_to_f32(g[r * ldg + c]);
+  float uv = st::bf16_to_f32(u[r * ldu + c]);
+  float dav = st::bf16_to_f32(da[r * ldda + c]);
+  float sg = sigmoidf_(gv);
+  float s = st::bf16r(gv / (1.0f + expf(-gv)));
+  float ds = st::bf16r(dav * uv);
+  du[r * lddu + c] = st::f32_to_bf16(dav * s);
+  dg[r * lddg + c] = st::f32_to_bf16(ds * (sg * (1.0f + gv * (1.0f - sg))));
+}
+
+// ------------------------------------------------------------------ softmax
+// one wave per score row; rows are [nrows, S], query position = row % S
+__global__ __launch_bounds__(NTH) void softmax_causal_fwd(const uint16_t* __restrict__ s,
+                                                         int64_t nrows, int64_t S, float scale,
+                                                         uint16_t* __restrict__ p,
+                                                         float* __restrict__ stats) {
+  const int64_t row = (int64_t)blockIdx.x * (NTH / 64) + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= nrows) return;
+  const int64_t qi = row % S;
+  const uint16_t* sr = s + row * S;
+  uint16_t* pr = p + row * S;
+  float m = -INFINITY;
+  for (int64_t c = lane; c <= qi; c += 64) m = fmaxf(m, st::bf16r(st::bf16_to_f32(sr[c]) * scale));
+  m = wave_max(m);
+  float l = 0.0f;
+  for (int64_t c = lane; c <= qi; c += 64) l += expf(st::bf16r(st::bf16_to_f32(sr[c]) * scale) - m);
+  l = wave_sum(l);
+  const float inv = 1.0f / l;
+  for (int64_t c = lane; c < S; c += 64) {
+    float v = 0.0f;
+    if (c <= qi) v = expf(st::bf16r(st::bf16_to_f32(sr[c]) * scale) - m) * inv;
+    pr[c] = st::f32_to_bf16(v);
+  }
+  if (lane == 0) {
+    stats[2 * row] = m;
+    stats[2 * row + 1] = l;
+  }
+}
+
+__global__ __launch_bounds__(NTH) void softmax_causal_bwd(const uint16_t* __restrict__ s,
+                                                         const float* __restrict__ stats,
+                                                         const uint16_t* __restrict__ dp,
+                                                         int64_t nrows, int64_t S, float scale,
+                                                         uint16_t* __restrict__ ds) {
+  const int64_t row = (int64_t)blockIdx.x * (NTH / 64) + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= nrows) return;
+  const int64_t qi = row % S;
+  const uint16_t* sr = s + row * S;
+  const uint16_t* dr = dp + row * S;
+  const float m = stats[2 * row], inv = 1.0f / stats[2 * row + 1];
+  float dot = 0.0f;
+  for (int64_t c = lane; c <= qi; c += 64) {
+    float pv = expf(st::bf16r(st::bf16_to_f32(sr[c]) * scale) - m) * inv;
+    dot += st::bf16_to_f32(dr[c]) * pv;
+  }
+  dot = wave_sum(dot);
+  for (int64_t c = lane; c < S; c += 64) {
+    float g = 0.0f;
+    if (c <= qi) {
+      float pv = expf(st::bf16r(st::bf16_to_f32(sr[c]) * scale) - m) * inv;
+      g = st::bf16r(st::bf16r(pv * (st::bf16_to_f32(dr[c]) - dot)) * scale);
+    }
+    ds[row * S + c] = st::f32_to_bf16(g);
+  }
+}
+
+unsigned nblk(int64_t total) { return (unsigned)st::cdiv(total, NTH); }
+
+}  // namespace
+
+extern "C" int st_rmsnorm_fwd(const uint16_t* x, const uint16_t* w, int64_t rows, int64_t H,
+                              float eps, uint16_t* y, float* rstd, st_stream_t stream) {
+  ST_CHECK_ARG(rows >= 0 && H > 0, "st_rmsnorm_fwd: bad shape");
+  if (rows == 0) return ST_OK;
+  ST_CHECK_ARG(x && w && y && rstd, "st_rmsnorm_fwd: NULL pointer");
+  rmsnorm_fwd<<<(unsigned)rows, NTH, 0, (hipStream_t)stream>>>(x, w, H, eps, y, rstd);
+  return st::check_launch("rmsnorm_fwd");
+}
+
+extern "C" int st_rmsnorm_bwd(const uint16_t* dy, const uint16_t* x, const uint16_t* w,
+                              const float* rstd, const uint16_t* dres, int64_t rows, int64_t H,
+                              uint16_t* dx, st_stream_t stream) {
+  ST_CHECK_ARG(rows >= 0 && H > 0, "st_rmsnorm_bwd: bad shape");
+  if (rows == 0) return ST_OK;
+  ST_CHECK_ARG(dy && x && w && rstd && dx, "st_rmsnorm_bwd: NULL pointer");
+  rmsnorm_bwd<<<(unsigned)rows, NTH, 0, (hipStream_t)stream>>>(dy, x, w, rstd, dres, H, dx);
+  return st::check_launch("rmsnorm_bwd");
+}
+
+extern "C" int st_rope_fwd(const uint16_t* x, int64_t ldx, const uint16_t* cos,
+                           const uint16_t* sin, int64_t B, int64_t S, int64_t heads, int64_t D,
+                           int32_t rotate, uint16_t* out, st_stream_t stream) {
+  ST_CHECK_ARG(B >= 0 && S >= 0 && heads > 0 && D > 0 && D % 2 == 0, "st_rope_fwd: bad shape");
+  int64_t total = B * S * heads * D;
+  if (total == 0) return ST_OK;
+  ST_CHECK_ARG(x && out && (!rotate || (cos && sin)), "st_rope_fwd: NULL pointer");
+  ST_CHECK_ARG(ldx >= heads * D, "st_rope_fwd: ldx < heads*D");
+  rope_fwd<<<nblk(total), NTH, 0, (hipStream_t)stream>>>(x, ldx, cos, sin, S, heads, D, rotate,
+                                                         total, out);
+  return st::check_launch("rope_fwd");
+}
+
+extern "C" int st_rope_bwd(const uint16_t* dout, const uint16_t* cos, const uint16_t* sin,
+                           int64_t B, int64_t S, int64_t heads, int64_t D, int32_t rotate,
+                           uint16_t* dx, int64_t lddx, st_stream_t stream) {
+  ST_CHECK_ARG(B >= 0 && S >= 0 && heads > 0 && D > 0 && D % 2 == 0, "st_rope_bwd: bad shape");
+  int64_t total = B * S * heads * D;
+  if (total == 0) return ST_OK;
+  ST_CHECK_ARG(dout && dx && (!rotate || (cos && sin)), "st_rope_bwd: NULL pointer");
+  ST_CHECK_ARG(lddx >= heads * D, "st_rope_bwd: lddx < heads*D");
+  rope_bwd<<<nblk(total), NTH, 0, (hipStream_t)stream>>>(dout, cos, sin, S, heads, D, rotate,
+                                                         total, dx, lddx);
+  return st::check_launch("rope_bwd");
+}
+
+extern "C" int st_heads_to_tokens(const uint16_t* x, int64_t B, int64_t S, int64_t heads,
+                                  int64_t D, uint16_t* out, st_stream_t stream) {
+  int64_t total = B * S * heads * D;
+  ST_CHECK_ARG(B >= 0 && S >= 0 && heads >= 0 && D >= 0, "st_heads_to_tokens: bad shape");
+  if (total == 0) return ST_OK;
+  ST_CHECK_ARG(x && out, "st_heads_to_tokens: NULL pointer");
+  relayout<<<nblk(total), NTH, 0, (hipStream_t)stream>>>(x, S, heads, D, total, 1, out);
+  return st::check_launch("heads_to_tokens");
+}
+
+extern "C" int st_tokens_to_heads(const uint16_t* x, int64_t B, int64_t S, int64_t heads,
+                                  int64_t D, uint16_t* out, st_stream_t stream) {
+  int64_t total = B * S * heads * D;
+  ST_CHECK_ARG(B >= 0 && S >= 0 && heads >= 0 && D >= 0, "st_tokens_to_heads: bad shape");
+  if (total == 0) return ST_OK;
+  ST_CHECK_ARG(x && out, "st_tokens_to_heads: NULL pointer");
+  relayout<<<nblk(total), NTH, 0, (hipStream_t)stream>>>(x, S, heads, D, total, 0, out);
+  return st::check_launch("tokens_to_heads");
+}
+
+extern "C" int st_swiglu_fwd(const uint16_t* g, int64_t ldg, const uint16_t* u, int64_t ldu,
+                             int64_t rows, int64_t I, uint16_t* a, int64_t lda,
+                             st_stream_t stream) {
+  ST_CHECK_ARG(rows >= 0 && I > 0, "st_swiglu_fwd: bad shape");
+  int64_t total = rows * I;
+  if (total == 0) return ST_OK;
+  ST_CHECK_ARG(g && u && a, "st_swiglu_fwd: NULL pointer");
+  swiglu_fwd<<<nblk(total), NTH, 0, (hipStream_t)stream>>>(g, ldg, u, ldu, I, total, a, lda);
+  return st::check_launch("swiglu_fwd");
+}
+
+extern "C" int st_swiglu_bwd(const uint16_t* da, int64_t ldda, const uint16_t* g, int64_t ldg,
+                             const uint16_t* u, int64_t ldu, int64_t rows, int64_t I,
+                             uint16_t* dg, int64_t lddg, uint16_t* du, int64_t lddu,
+                             st_stream_t stream) {
+  ST_CHECK_ARG(rows >= 0 && I > 0, "st_swiglu_bwd: bad shape");
+  int64_t total = rows * I;
+  if (total == 0) return ST_OK;
+  ST_CHECK_ARG(da && g && u && dg && du, "st_swiglu_bwd: NULL pointer");
+  swiglu_bwd<<<nblk(total), NTH, 0, (hipStream_t)stream>>>(da, ldda, g, ldg, u, ldu, I, total, dg,
+                                                           lddg, du, lddu);
+  return st::check_launch("swiglu_bwd");
+}
+
+extern "C" int st_softmax_causal_fwd(const uint16_t* s, int64_t nrows, int64_t S, float scale,
+                                     uint16_t* p, float* stats, st_stream_t stream) {
+  ST_CHECK_ARG(nrows >= 0 && S > 0 && nrows % S == 0, "st_softmax_causal_fwd: bad shape");
+  if (nrows == 0) return ST_OK;
+  ST_CHECK_ARG(s && p && stats, "st_softmax_causal_fwd: NULL pointer");
+  softmax_causal_fwd<<<(unsigned)st::cdiv(nrows, NTH / 64), NTH, 0, (hipStream_t)stream>>>(
+      s, nrows, S, scale, p, stats);
+  return st::check_launch("softmax_causal_fwd");
+}
+
+extern "C" int st_softmax_causal_bwd(const uint16_t* s, const float* stats, const uint16_t* dp,
+                                     int64_t nrows, int64_t S, float scale, uint16_t* ds,
+                                     st_stream_t stream) {
+  ST_CHECK_ARG(nrows >= 0 && S > 0 && nrows % S == 0, "st_softmax_causal_bwd: bad shape");
+  if (nrows == 0) return ST_OK;
+  ST_CHECK_ARG(s && stats && dp && ds, "st_softmax_causal_bwd: NULL pointer");
+  softmax_causal_bwd<<<(unsigned)st::cdiv(nrows, NTH / 64), NTH, 0, (hipStream_t)stream>>>(
+      s, stats, dp, nrows, S, scale, ds);
+  return st::check_launch("softmax_causal_bwd");
+}

@@ -1,0 +1,105 @@
+"""Llama/Qwen2 dense decoder block on 4-bit slot weights (HIP path).
+
+``dense_block`` keeps the functional contract of adapters/dense.py:120-153
+(/root/reference/src/ram_vram_finetune): called as
+``functional(hidden_states, position_embeddings, attention_mask, **weights,
+**kwargs)`` by the recompute driver, returns new bf16 hidden states and keeps
+no reference to slot memory.  Differences in *how*, not *what*:
+
+* ``weights['<proj>.weight']`` are :class:`~spilltune_amd.ops.Q4Weight` slot
+  views (packed 4-bit + fp32 scales), dequantised inside the GEMM;
+* LoRA may sit on any of the seven projections (``lora_q`` .. ``lora_down``);
+* when q|k|v (and gate|up) are adjacent in the slot they run as one GEMM over
+  the concatenated rows, and the residual adds run in the o/down epilogues;
+* ``attention_mask`` is a :class:`CausalMask` marker (all-valid causal
+  attention, the only mask the engine builds for unpadded rows) -- the mask
+  is applied structurally by the softmax kernel, exactly as adding
+  ``finfo(bf16).min`` does (exp underflows to 0).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import ops
+
+
+@dataclass(frozen=True)
+class CausalMask:
+    """All-valid causal additive mask of shape [batch, 1, S, S] (dense.py:246-247)."""
+    batch: int
+    length: int
+
+
+def positions_and_masks(valid: torch.Tensor, *, head_dim: int, theta: float, device,
+                        dtype=torch.bfloat16):
+    """Rotary tables (bf16 cos/sin [B,S,D]) and the causal mask marker
+    (dense.py:232-248).  Right padding is rejected (unsupported here)."""
+    if valid.dtype != torch.bool or valid.ndim != 2 or valid.shape[1] < 1:
+        raise ValueError("unsupported_capability: mask must be 2D bool")
+    if not bool(valid.all()):
+        raise ValueError("unsupported_capability: right-padding masks are not supported on the HIP path")
+    batch, length = valid.shape
+    positions = torch.arange(length, device=device).expand(batch, -1)
+    inv = 1.0 / theta ** (torch.arange(0, head_dim, 2, device=device).float() / head_dim)
+    freq = (inv[None, :, None].expand(batch, -1, 1) @ positions[:, None].float()).transpose(1, 2)
+    phase = torch.cat((freq, freq), -1)
+    return (phase.cos().to(dtype), phase.sin().to(dtype)), CausalMask(batch, length)
+
+
+def _weight(weights, name):
+    w = weights[name + ".weight"]
+    if not isinstance(w, ops.Q4Weight):
+        raise TypeError(f"{name}.weight must be a 4-bit slot view (Q4Weight), got {type(w).__name__}")
+    return w
+
+
+def dense_block(hidden_states, position_embeddings, attention_mask, *, heads, kv_heads, head_dim,
+                eps, lora_q=None, lora_k=None, lora_v=None, lora_o=None, lora_gate=None,
+                lora_up=None, lora_down=None, qk_norm=False, feed_forward=None, **weights):
+    if qk_norm or feed_forward is not None:
+        raise ValueError("unsupported_capability: qk_norm/custom feed-forward not on the HIP path")
+    if attention_mask is not None and not isinstance(attention_mask, CausalMask):
+        raise ValueError("unsupported_capability: only the causal mask marker is supported")
+    B, S, Hd = hidden_states.shape
+    cos, sin = position_embeddings
+    x2d = hidden_states.reshape(B * S, Hd)
+    residual = x2d
+    xn = ops.rms_norm(x2d, weights["input_layernorm.weight"], eps)
+
+    wq, wk, wv = (_weight(weights, f"self_attn.{p}_proj") for p in "qkv")
+    qkv = ops.concat_rows([wq, wk, wv])
+    loras_qkv = [lora_q, lora_k, lora_v]
+    if qkv is not None and (all(l is None for l in loras_qkv) or all(l is not None for l in loras_qkv)):
+        y = ops.q4_lora_linear(xn, qkv, loras_qkv)
+        q, k, v = ops.rope_qkv(y, B, S, heads, kv_heads, head_dim, cos, sin)
+    else:
+        q = ops.rope_heads(ops.q4_lora_linear(xn, wq, [lora_q]), 0, B, S, heads, head_dim, cos, sin)
+        k = ops.rope_heads(ops.q4_lora_linear(xn, wk, [lora_k]), 0, B, S, kv_heads, head_dim, cos, sin)
+        v = ops.rope_heads(ops.q4_lora_linear(xn, wv, [lora_v]), 0, B, S, kv_heads, head_dim, cos,
+                           sin, rotate=False)
+
+    attended = ops.causal_attention(q, k, v, ops.attention_scale(head_dim)).reshape(B * S, heads * head_dim)
+    h1 = ops.q4_lora_linear(attended, _weight(weights, "self_attn.o_proj"), [lora_o], residual=residual)
+
+    xn2 = ops.rms_norm(h1, weights["post_attention_layernorm.weight"], eps)
+    wg, wu = _weight(weights, "mlp.gate_proj"), _weight(weights, "mlp.up_proj")
+    gu = ops.concat_rows([wg, wu])
+    loras_gu = [lora_gate, lora_up]
+    inter = wg.out_features
+    if gu is not None and (all(l is None for l in loras_gu) or all(l is not None for l in loras_gu)):
+        act = ops.swiglu(ops.q4_lora_linear(xn2, gu, loras_gu), inter)
+    else:
+        act = ops.swiglu_pair(ops.q4_lora_linear(xn2, wg, [lora_gate]),
+                              ops.q4_lora_linear(xn2, wu, [lora_up]))
+    out = ops.q4_lora_linear(act, _weight(weights, "mlp.down_proj"), [lora_down], residual=h1)
+    return out.view(B, S, Hd)
+
+
+def lora_kwargs(adapters: dict) -> dict:
+    """Map target paths to the functional's ``lora_*`` keyword arguments."""
+    names = {"self_attn.q_proj": "lora_q", "self_attn.k_proj": "lora_k",
+             "self_attn.v_proj": "lora_v", "self_attn.o_proj": "lora_o",
+             "mlp.gate_proj": "lora_gate", "mlp.up_proj": "lora_up", "mlp.down_proj": "lora_down"}
+    return {names[t]: p for t, p in adapters.items()}

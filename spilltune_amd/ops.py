@@ -1,0 +1,514 @@
+"""Differentiable ops of the per-layer path, each one call into the C ABI.
+
+Every forward reproduces the reference expression it replaces and every
+backward the VJP autograd computes for that expression (paths relative to
+/root/reference/src/ram_vram_finetune):
+
+* :func:`q4_lora_linear` -- ``LoRAProjection.forward`` (finetune/lora.py:
+  205-220) on a frozen 4-bit weight, optionally over N-concatenated
+  projections (fused q|k|v or gate|up) and with the decoder residual add
+  (adapters/dense.py:149,153) folded into the epilogue.
+* :func:`rms_norm` -- adapters/dense.py:115-117.
+* :func:`rope_heads` -- adapters/dense.py:127-141 (q/k/v views, transpose,
+  rotate) for one projection output.
+* :func:`causal_attention` -- adapters/dense.py:142-148 (GQA repeat, eager
+  fp32 softmax with the causal mask, relayout to tokens).
+* :func:`swiglu` -- adapters/dense.py:153 ``silu(gate) * up``.
+
+Ops run on the current stream, allocate through PyTorch and never fall back
+to another implementation.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+
+from . import _lib
+from .codecs import GROUP, codebook
+
+_BF16 = torch.bfloat16
+_F32 = torch.float32
+
+
+# ----------------------------------------------------------------- weights
+@dataclass
+class Q4Weight:
+    """A frozen ``[out, in]`` 4-bit matrix resident on the device (views into a
+    slot).  ``segments`` lists the out-widths of N-concatenated projections."""
+    payload: torch.Tensor
+    scales: torch.Tensor
+    shape: tuple
+    codec: str
+    segments: tuple = field(default=())
+    flags: int = 0
+
+    def __post_init__(self):
+        self.shape = tuple(int(s) for s in self.shape)
+        if not self.segments:
+            self.segments = (self.shape[0],)
+        if sum(self.segments) != self.shape[0]:
+            raise ValueError("Q4Weight segments must sum to out_features")
+
+    @property
+    def out_features(self):
+        return self.shape[0]
+
+    @property
+    def in_features(self):
+        return self.shape[1]
+
+    @property
+    def device(self):
+        return self.payload.device
+
+    @property
+    def requires_grad(self):
+        return False
+
+    def lut(self):
+        return _lib.lut_array(codebook(self.codec))
+
+    def dequantize(self) -> torch.Tensor:
+        """bf16 copy of the matrix (for checks / reference-side use only)."""
+        out = torch.empty(self.shape, dtype=_BF16, device=self.device)
+        _lib.call("st_dequant4", _lib.ptr(self.payload), _lib.ptr(self.scales),
+                  self.shape[0] * self.shape[1], GROUP, self.lut(), self.flags,
+                  _lib.ptr(out), _lib.stream_handle(self.device))
+        return out
+
+
+def concat_rows(weights) -> Q4Weight | None:
+    """Zero-copy view of row-concatenated 4-bit weights when their payloads and
+    scales are adjacent in memory and each matrix holds whole groups (then the
+    flat groups of the concatenation are exactly the parts' groups)."""
+    weights = list(weights)
+    if len(weights) < 2 or any(not isinstance(w, Q4Weight) for w in weights):
+        return None
+    first = weights[0]
+    K = first.in_features
+    if any(w.in_features != K or w.codec != first.codec or w.flags != first.flags
+           or len(w.segments) != 1 for w in weights):
+        return None
+    if (K % GROUP) != 0 or any(w.out_features % 32 for w in weights[:-1]):
+        return None  # flat groups must not straddle parts; LoRA segments end on 32-column blocks
+    for a, b in zip(weights, weights[1:]):
+        if a.payload.data_ptr() + a.payload.numel() != b.payload.data_ptr():
+            return None
+        if a.scales.data_ptr() + a.scales.numel() * 4 != b.scales.data_ptr():
+            return None
+    rows = sum(w.out_features for w in weights)
+    base_p, base_s = first.payload, first.scales
+    payload = torch.empty(0, dtype=torch.uint8, device=base_p.device).set_(
+        base_p.untyped_storage(), base_p.storage_offset(), (rows * K // 2,), (1,))
+    scales = torch.empty(0, dtype=_F32, device=base_s.device).set_(
+        base_s.untyped_storage(), base_s.storage_offset(), (rows * K // GROUP,), (1,))
+    return Q4Weight(payload, scales, (rows, K), first.codec,
+                    tuple(w.out_features for w in weights), first.flags)
+
+
+# ----------------------------------------------------------------- timing hook
+class KernelTimer:
+    """Brackets every fused 4-bit GEMM launch with HIP events on the launch
+    stream, keyed ``(pass, M, N, K)``; durations are read after a sync."""
+
+    def __init__(self):
+        self.events = {}
+
+    def record(self, key, fn):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        fn()
+        end.record()
+        self.events.setdefault(key, []).append((start, end))
+
+    def summary(self):
+        out = {}
+        for key, evs in self.events.items():
+            ms = [s.elapsed_time(e) for s, e in evs]
+            out[key] = {"launches": len(ms), "avg_ms": sum(ms) / len(ms)}
+        return out
+
+
+TIMER: KernelTimer | None = None
+
+
+def _launch(key, fn):
+    if TIMER is None:
+        fn()
+    else:
+        TIMER.record(key, fn)
+
+
+# ----------------------------------------------------------------- workspace
+class _Workspace:
+    """Per-device scratch grown on demand through the PyTorch allocator."""
+
+    def __init__(self):
+        self._buf = {}
+
+    def get(self, device, nbytes: int) -> torch.Tensor | None:
+        if nbytes <= 0:
+            return None
+        key = (device.type, device.index)
+        buf = self._buf.get(key)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.empty(int(nbytes * 1.25) + 256, dtype=torch.uint8, device=device)
+            self._buf[key] = buf
+        return buf
+
+
+_ws = _Workspace()
+
+
+def lora_gemm(Mo, No, Kc, a, sam, sak, b, sbk, sbn, alpha, out, accumulate=False):
+    """``out = (accumulate ? out : 0) + alpha * sum_k a(m,k) b(k,n)`` (fp32 out)."""
+    need = _lib.query("st_lora_gemm_workspace_bytes", Mo, No, Kc)
+    ws = _ws.get(out.device, need)
+    dt = {_BF16: _lib.ST_DTYPE_BF16, _F32: _lib.ST_DTYPE_F32}
+    _lib.call("st_lora_gemm", Mo, No, Kc, _lib.ptr(a), dt[a.dtype], sam, sak, _lib.ptr(b),
+              dt[b.dtype], sbk, sbn, float(alpha), _lib.ptr(out), out.stride(0), int(accumulate),
+              _lib.ptr(ws), 0 if ws is None else ws.numel(), _lib.stream_handle(out.device))
+
+
+# ----------------------------------------------------------------- projection
+def _lora_meta(weight: Q4Weight, loras):
+    loras = list(loras) if loras is not None else []
+    if not loras or all(l is None for l in loras):
+        return None
+    if len(loras) != len(weight.segments) or any(l is None for l in loras):
+        raise ValueError("unsupported_capability: fused projections need a LoRA on every segment")
+    ranks = {int(l.rank) for l in loras}
+    scales = {float(l.scale) for l in loras}
+    if len(ranks) != 1 or len(scales) != 1:
+        raise ValueError("unsupported_capability: fused projections need one rank and scale")
+    return ranks.pop(), scales.pop()
+
+
+class _Q4LoRALinear(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, weight, residual, rank, scale, *ab):
+        M, K = x.shape
+        N = weight.out_features
+        dev = x.device
+        stream = _lib.stream_handle(dev)
+        nseg = len(weight.segments)
+        y = torch.empty((M, N), dtype=_BF16, device=dev)
+        T = None
+        if ab:
+            A = [ab[2 * i] for i in range(nseg)]
+            B = [ab[2 * i + 1] for i in range(nseg)]
+            A_cat = A[0].detach() if nseg == 1 else torch.cat([a.detach() for a in A], 0)
+            B_cat = B[0].detach() if nseg == 1 else torch.cat([b.detach() for b in B], 0)
+            A_cat, B_cat = A_cat.contiguous(), B_cat.contiguous()
+            T = torch.empty((M, nseg * rank), dtype=_F32, device=dev)
+            # T = x_f32 A_cat^T   (lora.py:219 inner linear)
+            lora_gemm(M, nseg * rank, K, x, K, 1, A_cat, 1, K, 1.0, T)
+            ends = _lib.i64_array(torch.tensor(weight.segments).cumsum(0).tolist())
+        need = _lib.query("st_q4_linear_fwd_workspace_bytes", M, N, K)
+        ws = _ws.get(dev, need)
+        _launch(("fwd", M, N, K), lambda: _lib.call(
+            "st_q4_linear_fwd", _lib.ptr(x), M, K, K, _lib.ptr(weight.payload),
+            _lib.ptr(weight.scales), N, weight.lut(), weight.flags,
+            _lib.ptr(T), 0 if T is None else T.stride(0),
+            _lib.ptr(B_cat) if ab else None, rank if ab else 0, float(scale),
+            nseg if ab else 0, ends if ab else None,
+            _lib.ptr(residual), 0 if residual is None else residual.stride(0),
+            _lib.ptr(y), N, _lib.ptr(ws), 0 if ws is None else ws.numel(), stream))
+        ctx.weight, ctx.rank, ctx.scale = weight, rank, scale
+        ctx.has_residual = residual is not None
+        ctx.nlora = len(ab)
+        if ab:
+            ctx.save_for_backward(x, T, A_cat, B_cat)
+        else:
+            ctx.save_for_backward(x)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        weight, rank, scale = ctx.weight, ctx.rank, ctx.scale
+        dy = dy.contiguous()
+        M, N = dy.shape
+        K = weight.in_features
+        dev = dy.device
+        stream = _lib.stream_handle(dev)
+        grads_ab = []
+        dT = None
+        A_cat = None
+        if ctx.nlora:
+            x, T, A_cat, B_cat = ctx.saved_tensors
+            nseg = len(weight.segments)
+            dT = torch.empty((M, nseg * rank), dtype=_F32, device=dev)
+            off = 0
+            for s, width in enumerate(weight.segments):
+                dys = dy[:, off:off + width]
+                Bs = B_cat[off:off + width]
+                Ts = T[:, s * rank:(s + 1) * rank]
+                dTs = dT[:, s * rank:(s + 1) * rank]
+                # dT_s = s * dY_s B_s ;  dB_s = s * dY_s^T T_s ;  dA_s = dT_s^T x
+                lora_gemm(M, rank, width, dys, N, 1, Bs, rank, 1, scale, dTs)
+                dB = torch.empty((width, rank), dtype=_F32, device=dev)
+                lora_gemm(width, rank, M, dys, 1, N, Ts, T.stride(0), 1, scale, dB)
+                dA = torch.empty((rank, K), dtype=_F32, device=dev)
+                lora_gemm(rank, K, M, dTs, 1, dT.stride(0), x, K, 1, 1.0, dA)
+                grads_ab += [dA, dB]
+                off += width
+        else:
+            (x,) = ctx.saved_tensors
+        dx = torch.empty((M, K), dtype=_BF16, device=dev)
+        need = _lib.query("st_q4_linear_dgrad_workspace_bytes", M, N, K)
+        ws = _ws.get(dev, need)
+        _launch(("dgrad", M, N, K), lambda: _lib.call(
+            "st_q4_linear_dgrad", _lib.ptr(dy), M, N, N, _lib.ptr(weight.payload),
+            _lib.ptr(weight.scales), K, weight.lut(), weight.flags,
+            _lib.ptr(dT), 0 if dT is None else dT.stride(0), _lib.ptr(A_cat),
+            0 if dT is None else dT.shape[1], _lib.ptr(dx), K,
+            _lib.ptr(ws), 0 if ws is None else ws.numel(), stream))
+        dres = dy if ctx.has_residual else None
+        return (dx, None, dres, None, None, *grads_ab)
+
+
+def q4_lora_linear(x: torch.Tensor, weight: Q4Weight, loras=None, residual=None) -> torch.Tensor:
+    """``bf16(bf16(x W^T) + s (x_f32 A^T) B^T)`` [``+ residual``] for a 2-D bf16 ``x``.
+
+    ``loras`` holds one LoRA object (``A``, ``B``, ``rank``, ``scale``) per
+    segment of ``weight`` or is None."""
+    if x.dtype != _BF16 or x.dim() != 2:
+        raise ValueError("q4_lora_linear expects a 2-D bf16 input")
+    if x.shape[1] != weight.in_features:
+        raise ValueError(f"input width {x.shape[1]} != weight in_features {weight.in_features}")
+    x = x.contiguous()
+    meta = _lora_meta(weight, loras)
+    if residual is not None:
+        residual = residual.contiguous()
+        if residual.shape != (x.shape[0], weight.out_features) or residual.dtype != _BF16:
+            raise ValueError("residual must be a bf16 [M, out_features] tensor")
+    if meta is None:
+        return _Q4LoRALinear.apply(x, weight, residual, 0, 1.0)
+    rank, scale = meta
+    ab = [t for l in loras for t in (l.A, l.B)]
+    for l in loras:
+        if l.A.dtype != _F32 or l.B.dtype != _F32:
+            raise ValueError("LoRA A/B must be fp32")
+    return _Q4LoRALinear.apply(x, weight, residual, rank, scale, *ab)
+
+
+# ----------------------------------------------------------------- RMSNorm
+class _RMSNorm(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, w, eps):
+        rows, H = x.shape
+        y = torch.empty_like(x)
+        rstd = torch.empty(rows, dtype=_F32, device=x.device)
+        _lib.call("st_rmsnorm_fwd", _lib.ptr(x), _lib.ptr(w), rows, H, float(eps), _lib.ptr(y),
+                  _lib.ptr(rstd), _lib.stream_handle(x.device))
+        ctx.save_for_backward(x, w, rstd)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, w, rstd = ctx.saved_tensors
+        dy = dy.contiguous()
+        rows, H = x.shape
+        dx = torch.empty_like(x)
+        _lib.call("st_rmsnorm_bwd", _lib.ptr(dy), _lib.ptr(x), _lib.ptr(w), _lib.ptr(rstd), None,
+                  rows, H, _lib.ptr(dx), _lib.stream_handle(x.device))
+        return dx, None, None
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    if x.dtype != _BF16 or weight.dtype != _BF16:
+        raise ValueError("rms_norm expects bf16 input and weight")
+    return _RMSNorm.apply(x.contiguous(), weight.detach().contiguous(), eps)
+
+
+# ----------------------------------------------------------------- RoPE
+class _RopeHeads(torch.autograd.Function):
+    """Token-major projection output columns -> [B, heads, S, D] (rotated)."""
+
+    @staticmethod
+    def forward(ctx, y, col0, B, S, heads, D, cos, sin, rotate):
+        ld = y.stride(0)
+        out = torch.empty((B, heads, S, D), dtype=_BF16, device=y.device)
+        base = y[:, col0:]
+        _lib.call("st_rope_fwd", _lib.ptr(base), ld, _lib.ptr(cos), _lib.ptr(sin), B, S, heads,
+                  D, int(rotate), _lib.ptr(out), _lib.stream_handle(y.device))
+        ctx.meta = (y.shape, col0, B, S, heads, D, rotate, ld)
+        ctx.save_for_backward(cos, sin)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        shape, col0, B, S, heads, D, rotate, ld = ctx.meta
+        cos, sin = ctx.saved_tensors
+        dout = dout.contiguous()
+        dy = torch.zeros(shape, dtype=_BF16, device=dout.device) if col0 or shape[1] != heads * D \
+            else torch.empty(shape, dtype=_BF16, device=dout.device)
+        _lib.call("st_rope_bwd", _lib.ptr(dout), _lib.ptr(cos), _lib.ptr(sin), B, S, heads, D,
+                  int(rotate), _lib.ptr(dy[:, col0:]), ld, _lib.stream_handle(dout.device))
+        return dy, None, None, None, None, None, None, None, None
+
+
+class _RopeQKV(torch.autograd.Function):
+    """Fused q|k|v projection output -> rotated q, k and plain v in head layout;
+    the VJP writes straight into one fused gradient buffer."""
+
+    @staticmethod
+    def forward(ctx, y, B, S, heads, kv_heads, D, cos, sin):
+        ld = y.stride(0)
+        dev = y.device
+        st = _lib.stream_handle(dev)
+        q = torch.empty((B, heads, S, D), dtype=_BF16, device=dev)
+        k = torch.empty((B, kv_heads, S, D), dtype=_BF16, device=dev)
+        v = torch.empty((B, kv_heads, S, D), dtype=_BF16, device=dev)
+        offs = (0, heads * D, (heads + kv_heads) * D)
+        for out, off, h, rot in ((q, offs[0], heads, 1), (k, offs[1], kv_heads, 1),
+                                 (v, offs[2], kv_heads, 0)):
+            _lib.call("st_rope_fwd", _lib.ptr(y[:, off:]), ld, _lib.ptr(cos), _lib.ptr(sin), B, S,
+                      h, D, rot, _lib.ptr(out), st)
+        ctx.meta = (y.shape, B, S, heads, kv_heads, D, offs)
+        ctx.save_for_backward(cos, sin)
+        return q, k, v
+
+    @staticmethod
+    def backward(ctx, dq, dk, dv):
+        shape, B, S, heads, kv_heads, D, offs = ctx.meta
+        cos, sin = ctx.saved_tensors
+        dev = cos.device
+        st = _lib.stream_handle(dev)
+        dy = torch.empty(shape, dtype=_BF16, device=dev)
+        for g, off, h, rot in ((dq, offs[0], heads, 1), (dk, offs[1], kv_heads, 1),
+                               (dv, offs[2], kv_heads, 0)):
+            g = torch.zeros((B, h, S, D), dtype=_BF16, device=dev) if g is None else g.contiguous()
+            _lib.call("st_rope_bwd", _lib.ptr(g), _lib.ptr(cos), _lib.ptr(sin), B, S, h, D, rot,
+                      _lib.ptr(dy[:, off:]), shape[1], st)
+        return dy, None, None, None, None, None, None, None
+
+
+def rope_qkv(y, B, S, heads, kv_heads, D, cos, sin):
+    return _RopeQKV.apply(y, B, S, heads, kv_heads, D, cos.contiguous(), sin.contiguous())
+
+
+def rope_heads(y, col0, B, S, heads, D, cos, sin, rotate=True):
+    return _RopeHeads.apply(y, col0, B, S, heads, D, cos.contiguous(), sin.contiguous(), rotate)
+
+
+# ----------------------------------------------------------------- attention
+class _CausalAttention(torch.autograd.Function):
+    """Eager GQA attention of dense.py:142-148 with the HIP causal softmax;
+    the score/probability products use torch.matmul on contiguous operands."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, scale):
+        B, H, S, D = q.shape
+        Hkv = k.shape[1]
+        g = H // Hkv
+        dev = q.device
+        st = _lib.stream_handle(dev)
+        qg = q.view(B, Hkv, g * S, D)
+        kt = k.transpose(-1, -2).contiguous()
+        s = torch.matmul(qg, kt)                       # [B, Hkv, g*S, S]
+        p = torch.empty_like(s)
+        stats = torch.empty((B * H * S, 2), dtype=_F32, device=dev)
+        _lib.call("st_softmax_causal_fwd", _lib.ptr(s), B * H * S, S, float(scale), _lib.ptr(p),
+                  _lib.ptr(stats), st)
+        o = torch.matmul(p, v)                         # [B, Hkv, g*S, D]
+        out = torch.empty((B, S, H * D), dtype=_BF16, device=dev)
+        _lib.call("st_heads_to_tokens", _lib.ptr(o), B, S, H, D, _lib.ptr(out), st)
+        ctx.save_for_backward(q, k, v, s, p, stats)
+        ctx.scale = scale
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, s, p, stats = ctx.saved_tensors
+        B, H, S, D = q.shape
+        Hkv = k.shape[1]
+        g = H // Hkv
+        dev = q.device
+        st = _lib.stream_handle(dev)
+        dout = dout.contiguous()
+        do = torch.empty((B, H, S, D), dtype=_BF16, device=dev)
+        _lib.call("st_tokens_to_heads", _lib.ptr(dout), B, S, H, D, _lib.ptr(do), st)
+        dog = do.view(B, Hkv, g * S, D)
+        dp = torch.matmul(dog, v.transpose(-1, -2).contiguous())
+        ds = torch.empty_like(dp)
+        _lib.call("st_softmax_causal_bwd", _lib.ptr(s), _lib.ptr(stats), _lib.ptr(dp), B * H * S,
+                  S, float(ctx.scale), _lib.ptr(ds), st)
+        dq = torch.matmul(ds, k).view(B, H, S, D)
+        qg = q.view(B, Hkv, g * S, D)
+        dkt = torch.matmul(qg.transpose(-1, -2).contiguous(), ds)      # [B, Hkv, D, S]
+        dvt = torch.matmul(dog.transpose(-1, -2).contiguous(), p)      # [B, Hkv, D, S]
+        return dq, dkt.transpose(-1, -2).contiguous(), dvt.transpose(-1, -2).contiguous(), None
+
+
+def causal_attention(q, k, v, scale):
+    """q [B,H,S,D], k/v [B,Hkv,S,D] -> token-major [B,S,H*D]."""
+    return _CausalAttention.apply(q.contiguous(), k.contiguous(), v.contiguous(), float(scale))
+
+
+# ----------------------------------------------------------------- SwiGLU
+class _SwiGLU(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, gu, I, gate_col, up_col):
+        rows = gu.shape[0]
+        ld = gu.stride(0)
+        a = torch.empty((rows, I), dtype=_BF16, device=gu.device)
+        _lib.call("st_swiglu_fwd", _lib.ptr(gu[:, gate_col:]), ld, _lib.ptr(gu[:, up_col:]), ld,
+                  rows, I, _lib.ptr(a), I, _lib.stream_handle(gu.device))
+        ctx.save_for_backward(gu)
+        ctx.meta = (I, gate_col, up_col)
+        return a
+
+    @staticmethod
+    def backward(ctx, da):
+        (gu,) = ctx.saved_tensors
+        I, gate_col, up_col = ctx.meta
+        da = da.contiguous()
+        rows, ld = gu.shape[0], gu.stride(0)
+        dgu = torch.empty_like(gu) if gu.shape[1] == 2 * I else torch.zeros_like(gu)
+        _lib.call("st_swiglu_bwd", _lib.ptr(da), I, _lib.ptr(gu[:, gate_col:]), ld,
+                  _lib.ptr(gu[:, up_col:]), ld, rows, I, _lib.ptr(dgu[:, gate_col:]), ld,
+                  _lib.ptr(dgu[:, up_col:]), ld, _lib.stream_handle(gu.device))
+        return dgu, None, None, None
+
+
+class _SwiGLUPair(torch.autograd.Function):
+    """silu(g) * u on two separate tensors (unfused gate/up projections)."""
+
+    @staticmethod
+    def forward(ctx, g, u):
+        rows, I = g.shape
+        a = torch.empty_like(g)
+        _lib.call("st_swiglu_fwd", _lib.ptr(g), I, _lib.ptr(u), I, rows, I, _lib.ptr(a), I,
+                  _lib.stream_handle(g.device))
+        ctx.save_for_backward(g, u)
+        return a
+
+    @staticmethod
+    def backward(ctx, da):
+        g, u = ctx.saved_tensors
+        da = da.contiguous()
+        rows, I = g.shape
+        dg, du = torch.empty_like(g), torch.empty_like(u)
+        _lib.call("st_swiglu_bwd", _lib.ptr(da), I, _lib.ptr(g), I, _lib.ptr(u), I, rows, I,
+                  _lib.ptr(dg), I, _lib.ptr(du), I, _lib.stream_handle(g.device))
+        return dg, du
+
+
+def swiglu(gu: torch.Tensor, I: int) -> torch.Tensor:
+    """``silu(gu[:, :I]) * gu[:, I:2I]`` for a fused gate|up output."""
+    return _SwiGLU.apply(gu, I, 0, I)
+
+
+def swiglu_pair(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
+    return _SwiGLUPair.apply(g.contiguous(), u.contiguous())
+
+
+def attention_scale(head_dim: int) -> float:
+    return float(head_dim) ** -0.5
+
+
+__all__ = ["Q4Weight", "concat_rows", "q4_lora_linear", "rms_norm", "rope_qkv", "rope_heads",
+           "causal_attention", "swiglu", "swiglu_pair", "lora_gemm", "attention_scale"]

@@ -1,0 +1,108 @@
+"""Streaming recompute driver (mirror of training/recompute.py:16-227 in
+/root/reference/src/ram_vram_finetune).
+
+Forward: borrow the block's weights, run the functional without grad, keep a
+clone of the input.  Backward: borrow again, recompute with grad, call
+``torch.autograd.grad(output, [hidden, A0, B0, ...])`` (adapters in name
+order) and add the adapter gradients into the fp32 ``grad_A``/``grad_B``
+buffers (replace unless accumulating).  Same signature, argument meaning and
+errors as the reference, so an engine can switch implementations freely;
+the weight views it borrows are 4-bit slot views for the HIP functional.
+"""
+from __future__ import annotations
+
+from contextlib import contextmanager
+from typing import Callable, Optional
+
+import torch
+
+
+class StreamingBlockFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, hidden_states, position_embeddings, attention_mask, func_block, func_kwargs,
+                weight_reloader, lora_dict, block_idx, accumulate_adapter_grads=False):
+        _validate_lora_bindings(func_kwargs, lora_dict)
+        ctx.func_block = func_block
+        ctx.func_kwargs = func_kwargs
+        ctx.weight_reloader = weight_reloader
+        ctx.lora_dict = lora_dict
+        ctx.block_idx = block_idx
+        ctx.accumulate_adapter_grads = accumulate_adapter_grads
+        ctx.position_embeddings = position_embeddings
+        ctx.attention_mask = attention_mask
+        ctx.save_for_backward(hidden_states.detach().clone())
+        with _borrow_weights(weight_reloader, "forward") as weights:
+            return _call_functional_block(func_block, hidden_states, position_embeddings,
+                                          attention_mask, weights, func_kwargs)
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        hidden = ctx.saved_tensors[0].detach().requires_grad_(True)
+        ordered = sorted(ctx.lora_dict.values(), key=lambda p: p.name)
+        inputs = [hidden] + [t for p in ordered for t in (p.A, p.B)]
+        with _borrow_weights(ctx.weight_reloader, "backward") as weights:
+            with torch.enable_grad():
+                output = _call_functional_block(ctx.func_block, hidden, ctx.position_embeddings,
+                                                ctx.attention_mask, weights, ctx.func_kwargs)
+            grads = torch.autograd.grad(output, inputs, grad_output, allow_unused=True)
+            if grads[0] is None:
+                raise RuntimeError(f"block {ctx.block_idx} lost its input gradient")
+            for i, proj in enumerate(ordered):
+                ga, gb = grads[1 + 2 * i], grads[2 + 2 * i]
+                if ga is None or gb is None:
+                    missing = [n for n, g in (("A", ga), ("B", gb)) if g is None]
+                    raise RuntimeError(f"block {ctx.block_idx} adapter {proj.name} is disconnected; "
+                                       f"missing gradients for {missing}")
+                if not ctx.accumulate_adapter_grads:
+                    proj.zero_grad()
+                proj.grad_A.add_(ga.detach().to(proj.grad_A))
+                proj.grad_B.add_(gb.detach().to(proj.grad_B))
+        return (grads[0],) + (None,) * 8
+
+
+@contextmanager
+def _borrow_weights(reloader, phase):
+    borrow = getattr(reloader, "borrow", None)
+    if borrow is None:
+        yield reloader()
+    else:
+        with borrow(phase) as weights:
+            yield weights
+
+
+def _call_functional_block(func_block, hidden_states, position_embeddings, attention_mask,
+                           weights, func_kwargs):
+    reserved = {"hidden_states", "position_embeddings", "attention_mask"}
+    dup = reserved.intersection(func_kwargs)
+    if dup:
+        raise TypeError(f"func_kwargs duplicates StreamingBlockFunction arguments: {sorted(dup)}")
+    overlap = set(weights).intersection(func_kwargs)
+    if overlap:
+        raise TypeError(f"weight/functional kwargs overlap: {sorted(overlap)}")
+    for name, weight in weights.items():
+        if getattr(weight, "requires_grad", False):
+            raise ValueError(f"base weight {name!r} must remain frozen")
+    return func_block(hidden_states=hidden_states, position_embeddings=position_embeddings,
+                      attention_mask=attention_mask, **weights, **func_kwargs)
+
+
+def _validate_lora_bindings(func_kwargs, lora_dict):
+    if not isinstance(lora_dict, dict):
+        raise TypeError("lora_dict must be a dict of LoRA projections")
+    expected = [id(v) for v in lora_dict.values()]
+    bound = [id(v) for v in func_kwargs.values() if hasattr(v, "A") and hasattr(v, "grad_A")]
+    if len(expected) != len(set(expected)):
+        raise ValueError("lora_dict contains the same projection more than once")
+    if len(bound) != len(set(bound)):
+        raise ValueError("functional kwargs bind the same LoRA projection more than once")
+    if set(expected) != set(bound):
+        raise ValueError("functional LoRA bindings must be the exact projections exposed "
+                         "to the optimizer/gradient buffers")
+
+
+def streaming_block(hidden_states, position_embeddings, attention_mask, func_block: Callable,
+                    func_kwargs: dict, weight_reloader, lora_dict: dict, block_idx: int, *,
+                    accumulate_adapter_grads: bool = False) -> torch.Tensor:
+    return StreamingBlockFunction.apply(hidden_states, position_embeddings, attention_mask,
+                                        func_block, func_kwargs, weight_reloader, lora_dict,
+                                        block_idx, accumulate_adapter_grads)

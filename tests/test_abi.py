@@ -1,0 +1,60 @@
+"""The C ABI library loads, exports exactly what include/spilltune_hip.h
+declares, and rejects bad arguments before touching the device (CPU only)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from spilltune_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "spilltune_hip.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(st_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = declared_symbols()
+    assert len(names) >= 20
+    for name in names:
+        assert hasattr(lib, name), name
+    assert sorted(_lib.EXPORTED) == names
+
+
+def test_abi_version_and_error_mapping():
+    lib = _lib.load()
+    assert lib.st_abi_version() == 1
+    lut = _lib.lut_array(range(16))
+    with pytest.raises(ValueError, match="group must be 64 or 128"):
+        _lib.call("st_dequant4", None, None, 10, 96, lut, 0, None, None)
+    with pytest.raises(ValueError, match="NULL"):
+        _lib.call("st_dequant4", None, None, 10, 128, lut, 0, None, None)
+    # zero-size work is a no-op that succeeds without a device
+    _lib.call("st_dequant4", None, None, 0, 128, lut, 0, None, None)
+    with pytest.raises(ValueError, match="multiple of 8"):
+        _lib.call("st_q4_linear_dgrad", ctypes.c_void_p(16), 4, 100, 100, ctypes.c_void_p(16),
+                  ctypes.c_void_p(16), 128, lut, 0, None, 0, None, 0, ctypes.c_void_p(16), 128,
+                  None, 0, None)
+    with pytest.raises(ValueError, match="dtype codes"):
+        _lib.call("st_lora_gemm", 4, 4, 4, ctypes.c_void_p(16), 7, 1, 1, ctypes.c_void_p(16), 0,
+                  1, 1, 1.0, ctypes.c_void_p(16), 4, 0, None, 0, None)
+
+
+def test_workspace_queries():
+    assert _lib.query("st_q4_linear_fwd_workspace_bytes", 16, 256, 4096) == 0
+    assert _lib.query("st_q4_linear_fwd_workspace_bytes", 16, 256, 688) == 256 * 688 * 2
+    assert _lib.query("st_q4_linear_dgrad_workspace_bytes", 16, 256, 688) == 256 * 688 * 2
+    ws = _lib.query("st_lora_gemm_workspace_bytes", 2048, 16, 4096)
+    assert ws > 0 and ws % (2048 * 16 * 4) == 0
+
+
+def test_product_does_not_import_the_oracle():
+    root = Path(__file__).resolve().parents[1] / "spilltune_amd"
+    for path in root.rglob("*.py"):
+        src = path.read_text()
+        assert "import oracle" not in src and "from oracle" not in src, path

@@ -1,0 +1,260 @@
+"""HIP kernels vs the CPU oracle, through the C ABI (MI355X only).
+
+Dequantisation must be bit-exact; GEMM/LoRA outputs are compared with the
+oracle's bf16 result allowing for fp32 summation order only (a bf16 ulp)."""
+import os
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from spilltune_amd import _lib, codecs, ops
+
+pytestmark = pytest.mark.gpu
+GOLD = np.load(Path(__file__).parent / "golden" / "codec_vectors.npz")
+BF = torch.bfloat16
+
+
+def lut_for(fmt, oc):
+    return oc.INT4_LUT if fmt.startswith("int4") else oc.NF4_LUT
+
+
+def bits_tensor(bits):
+    return torch.from_numpy(np.asarray(bits, dtype=np.uint16).astype(np.int16)).view(BF)
+
+
+def dequant_dev(payload, scales, numel, fmt, dev, flags=0, group=128, out=None):
+    if out is None:
+        out = torch.empty(numel, dtype=BF, device=dev)
+    lut = _lib.lut_array(codecs.CODEBOOKS[fmt])
+    _lib.call("st_dequant4", _lib.ptr(payload), _lib.ptr(scales), numel, group, lut, flags,
+              _lib.ptr(out), _lib.stream_handle(dev))
+    torch.cuda.synchronize()
+    return out
+
+
+def q4_from_oracle(oc, w32: np.ndarray, fmt, dev):
+    """Encode with the oracle, upload, return (Q4Weight, exact bf16 W on CPU)."""
+    enc = oc.encode_int4 if fmt.startswith("int4") else oc.encode_nf4
+    payload, scales = enc(w32)
+    W = bits_tensor(oc.decode4(payload, scales, w32.size, lut=lut_for(fmt, oc))).view(w32.shape)
+    q = ops.Q4Weight(torch.from_numpy(payload).to(dev), torch.from_numpy(scales).to(dev),
+                     w32.shape, fmt)
+    return q, W
+
+
+@pytest.mark.parametrize("case", range(5))
+@pytest.mark.parametrize("fmt", ["int4-sym-g128", "nf4-g128"])
+def test_dequant_golden_cases_bit_exact(dev, case, fmt):
+    short = "int4" if fmt.startswith("int4") else "nf4"
+    p = torch.from_numpy(GOLD[f"case{case}_{short}_payload"]).to(dev)
+    s = torch.from_numpy(GOLD[f"case{case}_{short}_scales"]).to(dev)
+    n = GOLD[f"case{case}_x"].size
+    got = dequant_dev(p, s, n, fmt, dev).cpu()
+    assert torch.equal(got.view(torch.int16), bits_tensor(GOLD[f"case{case}_{short}_bits"]).view(torch.int16))
+
+
+@pytest.mark.parametrize("fmt", ["int4-sym-g128", "nf4-g128"])
+def test_dequant_codebook_tables_bit_exact(dev, fmt):
+    short = "int4" if fmt.startswith("int4") else "nf4"
+    payload = torch.tensor([c | ((c + 1) << 4) for c in range(0, 16, 2)] * 8, dtype=torch.uint8)
+    for i, s in enumerate(GOLD[f"{short}_table_scales"]):
+        got = dequant_dev(payload.to(dev), torch.tensor([s], dtype=torch.float32).to(dev), 16,
+                          fmt, dev).cpu()
+        assert torch.equal(got.view(torch.int16), bits_tensor(GOLD[f"{short}_table_bits"][i]).view(torch.int16))
+
+
+@pytest.mark.parametrize("fmt", ["int4-sym-g128", "nf4-g128"])
+@pytest.mark.parametrize("hi_first", [False, True])
+@pytest.mark.parametrize("numel", [1, 31, 32, 4096 * 16 + 77, (1 << 21) + 3])
+def test_dequant_random_vs_oracle(dev, oracle_codec, fmt, hi_first, numel):
+    rng = np.random.default_rng(numel)
+    groups = (numel + 127) // 128
+    payload = rng.integers(0, 256, groups * 64, dtype=np.uint8)
+    scales = (rng.standard_normal(groups).astype(np.float32) * 0.05)
+    expect = oracle_codec.decode4(payload, scales, numel, lut=lut_for(fmt, oracle_codec),
+                                  hi_first=hi_first)
+    got = dequant_dev(torch.from_numpy(payload).to(dev), torch.from_numpy(scales).to(dev), numel,
+                      fmt, dev, flags=_lib.ST_FLAG_HI_NIBBLE_FIRST if hi_first else 0)
+    assert torch.equal(got.cpu().view(torch.int16), bits_tensor(expect).view(torch.int16))
+
+
+def test_dequant_unaligned_output_and_group64(dev, oracle_codec):
+    rng = np.random.default_rng(1)
+    n = 64 * 40 + 9
+    payload = rng.integers(0, 256, (n + 1) // 2 + 64, dtype=np.uint8)
+    scales = rng.random((n + 63) // 64, dtype=np.float32)
+    buf = torch.zeros(n + 8, dtype=BF, device=dev)
+    out = buf[1:1 + n]  # 2-byte aligned only: exercises the element-wise path
+    dequant_dev(torch.from_numpy(payload).to(dev), torch.from_numpy(scales).to(dev), n,
+                "nf4-g128", dev, group=64, out=out)
+    expect = oracle_codec.decode4(payload, scales, n, lut=oracle_codec.NF4_LUT, group=64)
+    assert torch.equal(out.cpu().view(torch.int16), bits_tensor(expect).view(torch.int16))
+    assert buf[0].item() == 0 and buf[n + 1:].float().abs().sum().item() == 0
+
+
+def test_dequant_dq_vs_oracle(dev, oracle_codec):
+    rng = np.random.default_rng(2)
+    n = 64 * 1000 + 13
+    packed = rng.integers(0, 256, (n + 1) // 2, dtype=np.uint8)
+    blocks = (n + 63) // 64
+    u8 = rng.integers(0, 256, blocks, dtype=np.uint8)
+    nested = (rng.random((blocks + 255) // 256) + 0.5).astype(np.float32)
+    nmap = np.sort(rng.standard_normal(256)).astype(np.float32)
+    offset = 0.0123
+    expect = oracle_codec.decode4_dq(packed, u8, nested, nmap, offset, n)
+    out = torch.empty(n, dtype=BF, device=dev)
+    t = lambda a: torch.from_numpy(a).to(dev)
+    _lib.call("st_dequant4_dq", _lib.ptr(t(packed)), _lib.ptr(t(u8)), _lib.ptr(t(nested)),
+              _lib.ptr(t(nmap)), offset, n, _lib.lut_array(codecs.NF4_CODEBOOK),
+              _lib.ST_FLAG_HI_NIBBLE_FIRST, _lib.ptr(out), _lib.stream_handle(dev))
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu().view(torch.int16), bits_tensor(expect).view(torch.int16))
+
+
+# ---------------------------------------------------------------- GEMMs
+class _L:
+    def __init__(self, A, B, alpha):
+        self.A, self.B, self.alpha = A, B, alpha
+        self.rank = A.shape[0]
+        self.scale = alpha / self.rank
+
+
+def _close_bf16(got, ref, what):
+    got, ref = got.float().cpu(), ref.float().cpu()
+    err = (got - ref).abs()
+    ulp = ref.abs().clamp_min(2 ** -20) * 2 ** -7
+    frac_bad = (err > ulp + 1e-6).float().mean().item()
+    rel = (err.norm() / ref.norm().clamp_min(1e-20)).item()
+    assert rel < 4e-3 and frac_bad < 1e-3, f"{what}: rel {rel:.3e}, >1ulp fraction {frac_bad:.2e}"
+
+
+SHAPES = [(64, 256, 256), (100, 384, 512), (37, 96, 688), (300, 512, 1024), (1, 128, 128)]
+
+
+@pytest.mark.parametrize("tile", ["128", "256"])
+@pytest.mark.parametrize("fmt", ["nf4-g128", "int4-sym-g128"])
+@pytest.mark.parametrize("M,N,K", SHAPES)
+@pytest.mark.parametrize("lora,residual", [(False, False), (True, False), (True, True)])
+def test_q4_linear_fwd_vs_oracle(dev, oracle_codec, monkeypatch, tile, fmt, M, N, K, lora, residual):
+    monkeypatch.setenv("ST_GEMM_TILE", tile)
+    g = torch.Generator().manual_seed(M * 7 + N + K)
+    w = (torch.randn(N, K, generator=g) * 0.02).numpy()
+    q, W = q4_from_oracle(oracle_codec, w, fmt, dev)
+    x = torch.randn(M, K, generator=g).to(BF)
+    ref = F.linear(x.float(), W.float()).to(BF)
+    lo = None
+    if lora:
+        r = 8
+        lo = _L(torch.randn(r, K, generator=g) * 0.05, torch.randn(N, r, generator=g) * 0.05, 16.0)
+        T = x.float() @ lo.A.T
+        ref = (ref.float() + (T @ lo.B.T) * lo.scale).to(BF)
+        lo_dev = _L(lo.A.to(dev), lo.B.to(dev), 16.0)
+    res = None
+    if residual:
+        res = torch.randn(M, N, generator=g).to(BF)
+        ref = (res.float() + ref.float()).to(BF)
+    y = ops.q4_lora_linear(x.to(dev), q, [lo_dev] if lora else None,
+                           residual=None if res is None else res.to(dev))
+    torch.cuda.synchronize()
+    _close_bf16(y, ref, f"fwd {fmt} {M}x{N}x{K} tile{tile}")
+
+
+@pytest.mark.parametrize("tile", ["128", "256"])
+@pytest.mark.parametrize("M,N,K", [(64, 256, 256), (100, 384, 512), (37, 128, 688), (300, 512, 1024)])
+@pytest.mark.parametrize("lora", [False, True])
+def test_q4_linear_dgrad_and_lora_grads_vs_oracle(dev, oracle_codec, monkeypatch, tile, M, N, K, lora):
+    monkeypatch.setenv("ST_GEMM_TILE", tile)
+    g = torch.Generator().manual_seed(M + N * 3 + K)
+    w = (torch.randn(N, K, generator=g) * 0.02).numpy()
+    q, W = q4_from_oracle(oracle_codec, w, "nf4-g128", dev)
+    x = torch.randn(M, K, generator=g).to(BF)
+    dy = torch.randn(M, N, generator=g).to(BF)
+    r, alpha = 8, 16.0
+    A = torch.randn(r, K, generator=g) * 0.05
+    B = torch.randn(N, r, generator=g) * 0.05
+    # oracle: autograd of lora.py:218-220 on CPU
+    xr = x.clone().requires_grad_(True)
+    Ar, Br = A.clone().requires_grad_(True), B.clone().requires_grad_(True)
+    base = F.linear(xr, W)
+    out = (base.float() + F.linear(F.linear(xr.float(), Ar), Br) * (alpha / r)).to(BF) if lora else base
+    out.backward(dy)
+    xd = x.to(dev).requires_grad_(True)
+    lo = _L(A.to(dev).requires_grad_(True), B.to(dev).requires_grad_(True), alpha)
+    y = ops.q4_lora_linear(xd, q, [lo] if lora else None)
+    y.backward(dy.to(dev))
+    torch.cuda.synchronize()
+    _close_bf16(xd.grad, xr.grad, f"dgrad {M}x{N}x{K}")
+    if lora:
+        torch.testing.assert_close(lo.A.grad.cpu(), Ar.grad, rtol=1e-4, atol=1e-5)
+        torch.testing.assert_close(lo.B.grad.cpu(), Br.grad, rtol=1e-4, atol=1e-5)
+
+
+def test_fused_segments_match_separate_projections(dev, oracle_codec):
+    """q|k|v as one N-concatenated GEMM == three separate GEMMs (same bits for
+    the forward: every output element has the same reduction)."""
+    g = torch.Generator().manual_seed(0)
+    M, K, widths, r = 96, 256, (256, 64, 64), 4
+    ws = [(torch.randn(n, K, generator=g) * 0.02).numpy() for n in widths]
+    qs = [q4_from_oracle(oracle_codec, w, "nf4-g128", dev)[0] for w in ws]
+    payload = torch.cat([q.payload for q in qs])
+    scales = torch.cat([q.scales for q in qs])
+    parts = []
+    po = so = 0
+    for q, n in zip(qs, widths):
+        parts.append(ops.Q4Weight(payload[po:po + q.payload.numel()],
+                                  scales[so:so + q.scales.numel()], (n, K), "nf4-g128"))
+        po += q.payload.numel()
+        so += q.scales.numel()
+    fused = ops.concat_rows(parts)
+    assert fused is not None and fused.segments == widths
+    x = torch.randn(M, K, generator=g).to(BF).to(dev)
+    loras = [_L((torch.randn(r, K, generator=g) * 0.05).to(dev), (torch.randn(n, r, generator=g) * 0.05).to(dev), 8.0)
+             for n in widths]
+    y = ops.q4_lora_linear(x, fused, loras)
+    sep = torch.cat([ops.q4_lora_linear(x, p, [l]) for p, l in zip(parts, loras)], 1)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int16), sep.view(torch.int16))
+
+
+def test_lora_gemm_strided_vs_float64(dev):
+    g = torch.Generator().manual_seed(4)
+    for Mo, No, Kc in [(2048, 16, 4096), (16, 4096, 2048), (4096, 16, 2048), (5, 7, 3), (70, 33, 1000)]:
+        a = torch.randn(Mo, Kc, generator=g).to(BF)
+        b = torch.randn(Kc, No, generator=g)
+        out = torch.empty(Mo, No, device=dev)
+        # a transposed in memory (sam=1) for half the cases to cover both strides
+        if Mo % 2:
+            at = a.T.contiguous().to(dev)
+            ops.lora_gemm(Mo, No, Kc, at, 1, Mo, b.to(dev), No, 1, 0.5, out)
+        else:
+            ops.lora_gemm(Mo, No, Kc, a.to(dev), Kc, 1, b.to(dev), No, 1, 0.5, out)
+        ref = 0.5 * (a.double() @ b.double())
+        torch.cuda.synchronize()
+        torch.testing.assert_close(out.cpu().double(), ref, rtol=1e-5, atol=1e-4 * Kc ** 0.5)
+        acc = out.clone()
+        ops.lora_gemm(Mo, No, Kc, a.to(dev), Kc, 1, b.to(dev), No, 1, 0.5, acc, accumulate=True)
+        torch.testing.assert_close(acc.cpu().double(), 2 * ref, rtol=1e-5, atol=2e-4 * Kc ** 0.5)
+
+
+def test_q4_linear_full_size_vs_torch_fp32(dev):
+    """Llama-3-8B gate|up shape at 2048 tokens against torch fp32 matmul on the
+    dequantised weight (bit-exact dequant is pinned above)."""
+    g = torch.Generator().manual_seed(1234)
+    M, N, K = 2048, 2 * 14336, 4096
+    w = torch.randn(N, K, generator=g) * 0.02
+    rec = codecs.encode(w, "nf4-g128")
+    q = ops.Q4Weight(rec.parts["payload"].to(dev), rec.parts["scales"].to(dev), (N, K), "nf4-g128",
+                     (14336, 14336))
+    W = q.dequantize()
+    x = torch.randn(M, K, generator=g).to(BF).to(dev)
+    y = ops.q4_lora_linear(x, q, None)
+    ref = (x.float() @ W.float().T).to(BF)
+    _close_bf16(y, ref, "full-size gate|up")
+    dy = torch.randn(M, N, generator=g).to(BF).to(dev)
+    xg = x.clone().requires_grad_(True)
+    ops.q4_lora_linear(xg, q, None).backward(dy)
+    ref_dx = (dy.float() @ W.float()).to(BF)
+    _close_bf16(xg.grad, ref_dx, "full-size gate|up dgrad")

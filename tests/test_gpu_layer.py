@@ -1,0 +1,195 @@
+"""One streamed decoder-layer step on the HIP path vs the CPU oracle
+(forward + recompute + backward through StreamingBlockFunction), plus the
+elementwise kernels against the oracle's autograd.  North-star criteria:
+rel. err <= 2e-2 on outputs, cosine >= 0.999 on gradients."""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import layer as OL
+from spilltune_amd import ops, slots
+from spilltune_amd.dense import CausalMask
+from spilltune_amd.recompute import streaming_block
+
+pytestmark = pytest.mark.gpu
+BF = torch.bfloat16
+PROJ = OL.PROJECTIONS
+
+
+def rel(a, b):
+    a, b = a.float().cpu(), b.float().cpu()
+    return ((a - b).norm() / b.norm().clamp_min(1e-30)).item()
+
+
+def cosine(a, b):
+    a, b = a.double().cpu().reshape(-1), b.double().cpu().reshape(-1)
+    return (a @ b / (a.norm() * b.norm()).clamp_min(1e-300)).item()
+
+
+def make_layer(cfg, seed, codec="nf4-g128", b_std=0.02, targets=PROJ):
+    g = torch.Generator().manual_seed(seed)
+    H, I, D, heads, kv = cfg["H"], cfg["I"], cfg["D"], cfg["heads"], cfg["kv"]
+    shapes = {"self_attn.q_proj": (heads * D, H), "self_attn.k_proj": (kv * D, H),
+              "self_attn.v_proj": (kv * D, H), "self_attn.o_proj": (H, heads * D),
+              "mlp.gate_proj": (I, H), "mlp.up_proj": (I, H), "mlp.down_proj": (H, I)}
+    weights = {f"{n}.weight": (torch.randn(s, generator=g) * 0.02).to(BF) for n, s in shapes.items()}
+    weights["input_layernorm.weight"] = (1 + 0.05 * torch.randn(H, generator=g)).to(BF)
+    weights["post_attention_layernorm.weight"] = (1 + 0.05 * torch.randn(H, generator=g)).to(BF)
+    block = slots.make_dense_block(0, weights, codec=codec, heads=heads, kv_heads=kv, head_dim=D,
+                                   eps=cfg["eps"], rank=cfg["r"], alpha=cfg["alpha"],
+                                   targets=targets, device="cuda:0", generator=g)
+    with torch.no_grad():
+        for p in block.adapters.values():
+            p.B.copy_(torch.randn(p.B.shape, generator=g) * b_std)
+    return block, weights
+
+
+def oracle_weights(block, oracle_codec):
+    """bf16 weights exactly as the reference's decode produces them."""
+    out = {}
+    for name, entry in block.storage_specs.items():
+        spec = entry["spec"]
+        p = block.host_weights[entry["parts"]["payload"]].numpy()
+        s = block.host_weights[entry["parts"]["scales"]].numpy()
+        lut = oracle_codec.NF4_LUT if spec["codec"] == "nf4-g128" else oracle_codec.INT4_LUT
+        bits = oracle_codec.decode4(p, s, spec["numel"], lut=lut)
+        out[name] = torch.from_numpy(bits.astype(np.int16)).view(BF).view(spec["shape"])
+    for k, v in block.host_weights.items():
+        if not k.startswith("@"):
+            out[k] = v
+    return out
+
+
+def run_case(cfg, seed, oracle_codec, codec="nf4-g128", streamed=False, targets=PROJ):
+    block, _ = make_layer(cfg, seed, codec, targets=targets)
+    g = torch.Generator().manual_seed(seed + 1)
+    B, S, H = cfg["B"], cfg["S"], cfg["H"]
+    hidden = torch.randn(B, S, H, generator=g).to(BF)
+    dy = torch.randn(B, S, H, generator=g).to(BF)
+    cos, sin = OL.rotary(B, S, cfg["D"], 500000.0, BF)
+    # ---- oracle
+    lor = {n: OL.Lora(n, p.A.detach().cpu(), p.B.detach().cpu(), p.alpha)
+           for n, p in block.adapters.items()}
+    kw = dict(heads=cfg["heads"], kv_heads=cfg["kv"], head_dim=cfg["D"], eps=cfg["eps"])
+    out_ref, gh_ref = OL.streaming_step(hidden, (cos, sin), OL.causal_mask(B, S, BF), dy,
+                                        weights=oracle_weights(block, oracle_codec), loras=lor, cfg=kw)
+    # ---- HIP path through the recompute driver
+    dev = torch.device("cuda:0")
+    if streamed:
+        session = slots.Q4SlotSession([block], dev, host_budget_bytes=1 << 40,
+                                      device_budget_bytes=1 << 40, slots=2)
+    else:
+        session = slots.ResidentSession([block], dev)
+    h = hidden.to(dev).requires_grad_(True)
+    with session.run():
+        out = streaming_block(h, (cos.to(dev), sin.to(dev)), CausalMask(B, S), block.functional,
+                              block.kwargs, session.reloader(block), block.adapters, block.index)
+        out.backward(dy.to(dev))
+    torch.cuda.synchronize()
+    res = {"out": rel(out.detach(), out_ref), "dh": cosine(h.grad, gh_ref)}
+    for n, p in block.adapters.items():
+        res[n + ".A"] = cosine(p.grad_A, lor[n].grad_A)
+        res[n + ".B"] = cosine(p.grad_B, lor[n].grad_B)
+    session.close()
+    return res
+
+
+TINY = dict(H=256, I=688, heads=4, kv=4, D=64, eps=1e-5, r=8, alpha=16.0, B=2, S=128)
+GQA = dict(H=512, I=1024, heads=8, kv=2, D=64, eps=1e-5, r=16, alpha=32.0, B=1, S=192)
+
+
+def _assert(res):
+    assert res["out"] <= 2e-2, res
+    bad = {k: v for k, v in res.items() if k != "out" and v < 0.999}
+    assert not bad, bad
+
+
+@pytest.mark.parametrize("codec", ["nf4-g128", "int4-sym-g128"])
+def test_tiny_llama_layer_step_vs_oracle(oracle_codec, codec):
+    _assert(run_case(TINY, 10, oracle_codec, codec))
+
+
+def test_gqa_layer_step_streamed_vs_oracle(oracle_codec):
+    _assert(run_case(GQA, 20, oracle_codec, streamed=True))
+
+
+def test_reference_default_targets_qvo(oracle_codec):
+    """q/v/o only (the reference's default dense targets): unfused q|k|v path."""
+    _assert(run_case(TINY, 30, oracle_codec,
+                     targets=("self_attn.q_proj", "self_attn.v_proj", "self_attn.o_proj")))
+
+
+def test_llama8b_dims_short_sequence(oracle_codec):
+    cfg = dict(H=4096, I=14336, heads=32, kv=8, D=128, eps=1e-5, r=16, alpha=32.0, B=1, S=64)
+    _assert(run_case(cfg, 40, oracle_codec))
+
+
+# ---------------------------------------------------------------- elementwise
+def test_rmsnorm_fwd_bwd_vs_oracle():
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(64, 1000, generator=g).to(BF)
+    w = (1 + 0.1 * torch.randn(1000, generator=g)).to(BF)
+    dy = torch.randn(64, 1000, generator=g).to(BF)
+    xr = x.clone().requires_grad_(True)
+    yr = OL.rms(xr, w, 1e-5)
+    yr.backward(dy)
+    xd = x.cuda().requires_grad_(True)
+    yd = ops.rms_norm(xd, w.cuda(), 1e-5)
+    yd.backward(dy.cuda())
+    assert rel(yd, yr) < 4e-3 and rel(xd.grad, xr.grad) < 1e-2
+
+
+def test_rope_relayout_vs_oracle():
+    g = torch.Generator().manual_seed(1)
+    B, S, heads, kv, D = 2, 16, 4, 2, 64
+    cos, sin = OL.rotary(B, S, D, 10000.0, BF)
+    y = torch.randn(B * S, (heads + 2 * kv) * D, generator=g).to(BF)
+    yr = y.clone().requires_grad_(True)
+    q = yr[:, :heads * D].reshape(B, S, heads, D).transpose(1, 2)
+    k = yr[:, heads * D:(heads + kv) * D].reshape(B, S, kv, D).transpose(1, 2)
+    v = yr[:, (heads + kv) * D:].reshape(B, S, kv, D).transpose(1, 2)
+    c, s = cos.unsqueeze(1), sin.unsqueeze(1)
+    qr, kr = OL._rotate(q, c, s), OL._rotate(k, c, s)
+    gq, gk, gv = (torch.randn(t.shape, generator=g).to(BF) for t in (qr, kr, v))
+    torch.autograd.backward([qr, kr, v], [gq, gk, gv])
+    yd = y.cuda().requires_grad_(True)
+    qd, kd, vd = ops.rope_qkv(yd, B, S, heads, kv, D, cos.cuda(), sin.cuda())
+    torch.autograd.backward([qd, kd, vd], [gq.cuda(), gk.cuda(), gv.cuda()])
+    for a, b in ((qd, qr), (kd, kr), (vd, v)):
+        assert torch.equal(a.cpu().view(torch.int16), b.contiguous().view(torch.int16))
+    assert torch.equal(yd.grad.cpu().view(torch.int16), yr.grad.view(torch.int16))
+
+
+def test_swiglu_vs_oracle():
+    g = torch.Generator().manual_seed(2)
+    gu = torch.randn(50, 2 * 300, generator=g).to(BF)
+    da = torch.randn(50, 300, generator=g).to(BF)
+    r = gu.clone().requires_grad_(True)
+    a = F.silu(r[:, :300]) * r[:, 300:]
+    a.backward(da)
+    d = gu.cuda().requires_grad_(True)
+    ad = ops.swiglu(d, 300)
+    ad.backward(da.cuda())
+    assert rel(ad, a) < 4e-3 and rel(d.grad, r.grad) < 1e-2
+
+
+def test_causal_attention_vs_oracle():
+    g = torch.Generator().manual_seed(3)
+    B, H, kv, S, D = 2, 8, 2, 96, 64
+    q = torch.randn(B, H, S, D, generator=g).to(BF)
+    k = torch.randn(B, kv, S, D, generator=g).to(BF)
+    v = torch.randn(B, kv, S, D, generator=g).to(BF)
+    do = torch.randn(B, S, H * D, generator=g).to(BF)
+    qr, kr, vr = (t.clone().requires_grad_(True) for t in (q, k, v))
+    rep = lambda t: t[:, :, None].expand(B, kv, H // kv, S, D).reshape(B, H, S, D)
+    scores = (qr @ rep(kr).transpose(-2, -1)) * D ** -0.5
+    p = torch.softmax(scores + OL.causal_mask(B, S, BF), dim=-1, dtype=torch.float32).to(BF)
+    o = (p @ rep(vr)).transpose(1, 2).reshape(B, S, H * D)
+    o.backward(do)
+    qd, kd, vd = (t.cuda().requires_grad_(True) for t in (q, k, v))
+    od = ops.causal_attention(qd, kd, vd, D ** -0.5)
+    od.backward(do.cuda())
+    assert rel(od, o) < 1e-2
+    for a, b in ((qd, qr), (kd, kr), (vd, vr)):
+        assert cosine(a.grad, b.grad) > 0.999
