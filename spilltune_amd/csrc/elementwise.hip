@@ -240,6 +240,179 @@ __global__ __launch_bounds__(NTH) void softmax_causal_bwd(const uint16_t* __rest
   }
 }
 
+// Register-resident variants: one wave per row, 16-byte accesses, the row held
+// in registers (CPL chunks of 8 per lane, S <= 512*CPL); chunks entirely past
+// the causal boundary are not read and are written as zeros.
+template <int CPL>
+__global__ __launch_bounds__(NTH) void softmax_causal_fwd_vec(const uint16_t* __restrict__ s,
+                                                             int64_t nrows, int64_t S,
+                                                             float scale,
+                                                             uint16_t* __restrict__ p,
+                                                             float* __restrict__ stats) {
+  const int64_t row = (int64_t)blockIdx.x * (NTH / 64) + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= nrows) return;
+  const int64_t qi = row % S;
+  const uint4* sr = (const uint4*)(s + row * S);
+  uint4* pr = (uint4*)(p + row * S);
+  const int nch = (int)(S / 8);
+  float x[CPL][8];
+  float m = -INFINITY;
+#pragma unroll
+  for (int t = 0; t < CPL; ++t) {
+    const int ch = lane + 64 * t;
+    const int64_t c0 = (int64_t)ch * 8;
+    if (ch < nch && c0 <= qi) {
+      uint4 q = sr[ch];
+      uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float v = st::bf16r(st::bf16_to_f32((uint16_t)(w[e >> 1] >> (16 * (e & 1)))) * scale);
+        x[t][e] = (c0 + e <= qi) ? v : -INFINITY;
+        m = fmaxf(m, x[t][e]);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[t][e] = -INFINITY;
+    }
+  }
+  m = wave_max(m);
+  float l = 0.0f;
+#pragma unroll
+  for (int t = 0; t < CPL; ++t)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      x[t][e] = expf(x[t][e] - m);  // exp(-inf) = 0 for masked entries
+      l += x[t][e];
+    }
+  l = wave_sum(l);
+  const float inv = 1.0f / l;
+#pragma unroll
+  for (int t = 0; t < CPL; ++t) {
+    const int ch = lane + 64 * t;
+    if (ch < nch)
+      pr[ch] = make_uint4(st::pack_bf16x2(x[t][0] * inv, x[t][1] * inv),
+                          st::pack_bf16x2(x[t][2] * inv, x[t][3] * inv),
+                          st::pack_bf16x2(x[t][4] * inv, x[t][5] * inv),
+                          st::pack_bf16x2(x[t][6] * inv, x[t][7] * inv));
+  }
+  if (lane == 0) {
+    stats[2 * row] = m;
+    stats[2 * row + 1] = l;
+  }
+}
+
+template <int CPL>
+__global__ __launch_bounds__(NTH) void softmax_causal_bwd_vec(const uint16_t* __restrict__ s,
+                                                             const float* __restrict__ stats,
+                                                             const uint16_t* __restrict__ dp,
+                                                             int64_t nrows, int64_t S,
+                                                             float scale,
+                                                             uint16_t* __restrict__ ds) {
+  const int64_t row = (int64_t)blockIdx.x * (NTH / 64) + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= nrows) return;
+  const int64_t qi = row % S;
+  const uint4* sr = (const uint4*)(s + row * S);
+  const uint4* dr = (const uint4*)(dp + row * S);
+  uint4* outr = (uint4*)(ds + row * S);
+  const int nch = (int)(S / 8);
+  const float m = stats[2 * row], inv = 1.0f / stats[2 * row + 1];
+  float pv[CPL][8], gv[CPL][8];
+  float dot = 0.0f;
+#pragma unroll
+  for (int t = 0; t < CPL; ++t) {
+    const int ch = lane + 64 * t;
+    const int64_t c0 = (int64_t)ch * 8;
+    if (ch < nch && c0 <= qi) {
+      uint4 q = sr[ch], g = dr[ch];
+      uint32_t w[4] = {q.x, q.y, q.z, q.w};
+      uint32_t u[4] = {g.x, g.y, g.z, g.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float sv = st::bf16r(st::bf16_to_f32((uint16_t)(w[e >> 1] >> (16 * (e & 1)))) * scale);
+        pv[t][e] = (c0 + e <= qi) ? expf(sv - m) * inv : 0.0f;
+        gv[t][e] = st::bf16_to_f32((uint16_t)(u[e >> 1] >> (16 * (e & 1))));
+        dot += gv[t][e] * pv[t][e];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pv[t][e] = gv[t][e] = 0.0f;
+    }
+  }
+  dot = wave_sum(dot);
+#pragma unroll
+  for (int t = 0; t < CPL; ++t) {
+    const int ch = lane + 64 * t;
+    if (ch >= nch) continue;
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = st::bf16r(st::bf16r(pv[t][e] * (gv[t][e] - dot)) * scale);
+    outr[ch] = make_uint4(st::pack_bf16x2(o[0], o[1]), st::pack_bf16x2(o[2], o[3]),
+                          st::pack_bf16x2(o[4], o[5]), st::pack_bf16x2(o[6], o[7]));
+  }
+}
+
+// 8 elements per thread; all rows/strides multiples of 8 elements
+__global__ __launch_bounds__(NTH) void swiglu_fwd_vec(const uint16_t* __restrict__ g, int64_t ldg,
+                                                     const uint16_t* __restrict__ u, int64_t ldu,
+                                                     int64_t I, int64_t total8,
+                                                     uint16_t* __restrict__ a, int64_t lda) {
+  int64_t e = (int64_t)blockIdx.x * NTH + threadIdx.x;
+  if (e >= total8) return;
+  const int64_t per = I / 8, r = e / per, c = (e % per) * 8;
+  uint4 gq = *(const uint4*)(g + r * ldg + c), uq = *(const uint4*)(u + r * ldu + c);
+  uint32_t gw[4] = {gq.x, gq.y, gq.z, gq.w}, uw[4] = {uq.x, uq.y, uq.z, uq.w}, o[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    float r2[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float gv = st::bf16_to_f32((uint16_t)(gw[k] >> (16 * h)));
+      float uv = st::bf16_to_f32((uint16_t)(uw[k] >> (16 * h)));
+      r2[h] = st::bf16r(gv / (1.0f + expf(-gv))) * uv;
+    }
+    o[k] = st::pack_bf16x2(r2[0], r2[1]);
+  }
+  *(uint4*)(a + r * lda + c) = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+__global__ __launch_bounds__(NTH) void swiglu_bwd_vec(const uint16_t* __restrict__ da, int64_t ldda,
+                                                     const uint16_t* __restrict__ g, int64_t ldg,
+                                                     const uint16_t* __restrict__ u, int64_t ldu,
+                                                     int64_t I, int64_t total8,
+                                                     uint16_t* __restrict__ dg, int64_t lddg,
+                                                     uint16_t* __restrict__ du, int64_t lddu) {
+  int64_t e = (int64_t)blockIdx.x * NTH + threadIdx.x;
+  if (e >= total8) return;
+  const int64_t per = I / 8, r = e / per, c = (e % per) * 8;
+  uint4 aq = *(const uint4*)(da + r * ldda + c), gq = *(const uint4*)(g + r * ldg + c),
+        uq = *(const uint4*)(u + r * ldu + c);
+  uint32_t aw[4] = {aq.x, aq.y, aq.z, aq.w}, gw[4] = {gq.x, gq.y, gq.z, gq.w},
+           uw[4] = {uq.x, uq.y, uq.z, uq.w}, og[4], ou[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    float rg[2], ru[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float gv = st::bf16_to_f32((uint16_t)(gw[k] >> (16 * h)));
+      float uv = st::bf16_to_f32((uint16_t)(uw[k] >> (16 * h)));
+      float dav = st::bf16_to_f32((uint16_t)(aw[k] >> (16 * h)));
+      float sg = sigmoidf_(gv);
+      float sv = st::bf16r(gv / (1.0f + expf(-gv)));
+      float dsv = st::bf16r(dav * uv);
+      ru[h] = dav * sv;
+      rg[h] = dsv * (sg * (1.0f + gv * (1.0f - sg)));
+    }
+    og[k] = st::pack_bf16x2(rg[0], rg[1]);
+    ou[k] = st::pack_bf16x2(ru[0], ru[1]);
+  }
+  *(uint4*)(dg + r * lddg + c) = make_uint4(og[0], og[1], og[2], og[3]);
+  *(uint4*)(du + r * lddu + c) = make_uint4(ou[0], ou[1], ou[2], ou[3]);
+}
+
+bool vec8(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
 unsigned nblk(int64_t total) { return (unsigned)st::cdiv(total, NTH); }
 
 }  // namespace
@@ -316,6 +489,11 @@ extern "C" int st_swiglu_fwd(const uint16_t* g, int64_t ldg, const uint16_t* u, 
   int64_t total = rows * I;
   if (total == 0) return ST_OK;
   ST_CHECK_ARG(g && u && a, "st_swiglu_fwd: NULL pointer");
+  if (I % 8 == 0 && ldg % 8 == 0 && ldu % 8 == 0 && lda % 8 == 0 && vec8(g) && vec8(u) && vec8(a)) {
+    swiglu_fwd_vec<<<nblk(total / 8), NTH, 0, (hipStream_t)stream>>>(g, ldg, u, ldu, I, total / 8,
+                                                                       a, lda);
+    return st::check_launch("swiglu_fwd");
+  }
   swiglu_fwd<<<nblk(total), NTH, 0, (hipStream_t)stream>>>(g, ldg, u, ldu, I, total, a, lda);
   return st::check_launch("swiglu_fwd");
 }
@@ -328,6 +506,12 @@ extern "C" int st_swiglu_bwd(const uint16_t* da, int64_t ldda, const uint16_t* g
   int64_t total = rows * I;
   if (total == 0) return ST_OK;
   ST_CHECK_ARG(da && g && u && dg && du, "st_swiglu_bwd: NULL pointer");
+  if (I % 8 == 0 && ldda % 8 == 0 && ldg % 8 == 0 && ldu % 8 == 0 && lddg % 8 == 0 &&
+      lddu % 8 == 0 && vec8(da) && vec8(g) && vec8(u) && vec8(dg) && vec8(du)) {
+    swiglu_bwd_vec<<<nblk(total / 8), NTH, 0, (hipStream_t)stream>>>(
+        da, ldda, g, ldg, u, ldu, I, total / 8, dg, lddg, du, lddu);
+    return st::check_launch("swiglu_bwd");
+  }
   swiglu_bwd<<<nblk(total), NTH, 0, (hipStream_t)stream>>>(da, ldda, g, ldg, u, ldu, I, total, dg,
                                                            lddg, du, lddu);
   return st::check_launch("swiglu_bwd");
@@ -338,6 +522,15 @@ extern "C" int st_softmax_causal_fwd(const uint16_t* s, int64_t nrows, int64_t S
   ST_CHECK_ARG(nrows >= 0 && S > 0 && nrows % S == 0, "st_softmax_causal_fwd: bad shape");
   if (nrows == 0) return ST_OK;
   ST_CHECK_ARG(s && p && stats, "st_softmax_causal_fwd: NULL pointer");
+  if (S % 8 == 0 && S <= 4096 && vec8(s) && vec8(p)) {
+    const unsigned nb = (unsigned)st::cdiv(nrows, NTH / 64);
+    hipStream_t hs = (hipStream_t)stream;
+    if (S <= 512) softmax_causal_fwd_vec<1><<<nb, NTH, 0, hs>>>(s, nrows, S, scale, p, stats);
+    else if (S <= 1024) softmax_causal_fwd_vec<2><<<nb, NTH, 0, hs>>>(s, nrows, S, scale, p, stats);
+    else if (S <= 2048) softmax_causal_fwd_vec<4><<<nb, NTH, 0, hs>>>(s, nrows, S, scale, p, stats);
+    else softmax_causal_fwd_vec<8><<<nb, NTH, 0, hs>>>(s, nrows, S, scale, p, stats);
+    return st::check_launch("softmax_causal_fwd");
+  }
   softmax_causal_fwd<<<(unsigned)st::cdiv(nrows, NTH / 64), NTH, 0, (hipStream_t)stream>>>(
       s, nrows, S, scale, p, stats);
   return st::check_launch("softmax_causal_fwd");
@@ -349,6 +542,15 @@ extern "C" int st_softmax_causal_bwd(const uint16_t* s, const float* stats, cons
   ST_CHECK_ARG(nrows >= 0 && S > 0 && nrows % S == 0, "st_softmax_causal_bwd: bad shape");
   if (nrows == 0) return ST_OK;
   ST_CHECK_ARG(s && stats && dp && ds, "st_softmax_causal_bwd: NULL pointer");
+  if (S % 8 == 0 && S <= 4096 && vec8(s) && vec8(dp) && vec8(ds)) {
+    const unsigned nb = (unsigned)st::cdiv(nrows, NTH / 64);
+    hipStream_t hs = (hipStream_t)stream;
+    if (S <= 512) softmax_causal_bwd_vec<1><<<nb, NTH, 0, hs>>>(s, stats, dp, nrows, S, scale, ds);
+    else if (S <= 1024) softmax_causal_bwd_vec<2><<<nb, NTH, 0, hs>>>(s, stats, dp, nrows, S, scale, ds);
+    else if (S <= 2048) softmax_causal_bwd_vec<4><<<nb, NTH, 0, hs>>>(s, stats, dp, nrows, S, scale, ds);
+    else softmax_causal_bwd_vec<8><<<nb, NTH, 0, hs>>>(s, stats, dp, nrows, S, scale, ds);
+    return st::check_launch("softmax_causal_bwd");
+  }
   softmax_causal_bwd<<<(unsigned)st::cdiv(nrows, NTH / 64), NTH, 0, (hipStream_t)stream>>>(
       s, stats, dp, nrows, S, scale, ds);
   return st::check_launch("softmax_causal_bwd");

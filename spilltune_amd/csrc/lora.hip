@@ -94,6 +94,121 @@ __global__ __launch_bounds__(NTH) void lora_reduce(int64_t Mo, int64_t No, int k
   out[m * ldo + n] = v;
 }
 
+// ---- fp32-MFMA path for the LoRA shapes: one bf16 operand G is large, the
+// other (S, fp32) has at most 64 columns.  out[m, j] = sum_k g(m,k) S[k, j]
+// with g(m,k) = G[m*ldg + k] (ROW: contraction contiguous, T = x A^T, dT = dY B)
+// or g(m,k) = G[k*ldg + m] (COL: contraction over G's rows, dB = dY^T T,
+// dA^T = x^T dT).  v_mfma_f32_32x32x2_f32 keeps fp32 products and sums.
+constexpr int RK_BM = 128, RK_BK = 32, RK_RP = 64;
+
+template <bool COL>
+__global__ __launch_bounds__(NTH) void lora_rk(int64_t Mo, int64_t R, int64_t Kc,
+                                              const uint16_t* __restrict__ G, int64_t ldg,
+                                              const float* __restrict__ S, int64_t ssk,
+                                              int64_t ssj, int64_t klen, int vec,
+                                              float* __restrict__ part) {
+  __shared__ float Gs[RK_BK][RK_BM + 4];
+  __shared__ float Ss[RK_BK][RK_RP + 4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t m0 = (int64_t)blockIdx.x * RK_BM;
+  const int64_t kb = (int64_t)blockIdx.y * klen;
+  const int64_t ke = kb + klen < Kc ? kb + klen : Kc;
+  const int nb = R > 32 ? 2 : 1;
+  f32x16 acc[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[c][v] = 0.0f;
+  for (int64_t k0 = kb; k0 < ke; k0 += RK_BK) {
+    if (!COL) {  // 128 rows x 32 contraction: 16 consecutive k per thread
+      const int row = tid >> 1, kk = (tid & 1) * 16;
+      const int64_t m = m0 + row, k = k0 + kk;
+      float v[16];
+      if (vec && m < Mo && k + 16 <= ke) {
+        const uint4* src = (const uint4*)(G + m * ldg + k);
+        uint4 q0 = src[0], q1 = src[1];
+        uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = st::bf16_to_f32((uint16_t)(w[i >> 1] >> (16 * (i & 1))));
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          v[i] = (m < Mo && k + i < ke) ? st::bf16_to_f32(G[m * ldg + k + i]) : 0.0f;
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) Gs[kk + i][row] = v[i];
+    } else {  // 32 contraction rows x 128 output columns: 16 consecutive m per thread
+      const int kr = tid >> 3, mc = (tid & 7) * 16;
+      const int64_t k = k0 + kr, m = m0 + mc;
+      float v[16];
+      if (vec && k < ke && m + 16 <= Mo) {
+        const uint4* src = (const uint4*)(G + k * ldg + m);
+        uint4 q0 = src[0], q1 = src[1];
+        uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = st::bf16_to_f32((uint16_t)(w[i >> 1] >> (16 * (i & 1))));
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          v[i] = (k < ke && m + i < Mo) ? st::bf16_to_f32(G[k * ldg + m + i]) : 0.0f;
+      }
+#pragma unroll
+      for (int i = 0; i < 16; i += 4)
+        *(float4*)&Gs[kr][mc + i] = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
+    }
+    for (int e = tid; e < RK_BK * RK_RP; e += NTH) {
+      int kk, j;
+      if (ssk == 1) { kk = e % RK_BK; j = e / RK_BK; } else { j = e % RK_RP; kk = e / RK_RP; }
+      const int64_t k = k0 + kk;
+      Ss[kk][j] = (k < ke && j < R) ? S[k * ssk + j * ssj] : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll 4
+    for (int kk = 0; kk < RK_BK; kk += 2) {
+      const float a = Gs[kk + (lane >> 5)][wave * 32 + (lane & 31)];
+      acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, Ss[kk + (lane >> 5)][lane & 31], acc[0], 0, 0, 0);
+      if (nb > 1)
+        acc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, Ss[kk + (lane >> 5)][32 + (lane & 31)],
+                                                      acc[1], 0, 0, 0);
+    }
+    __syncthreads();
+  }
+  float* dst = part + (int64_t)blockIdx.y * Mo * R;
+  for (int c = 0; c < nb; ++c) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int64_t m = m0 + wave * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+      const int j = c * 32 + (lane & 31);
+      if (m < Mo && j < R) dst[m * R + j] = acc[c][v];
+    }
+  }
+}
+
+// sums the split-K partials [ks][Mo][R] into out[m*so_m + j*so_j]
+__global__ __launch_bounds__(NTH) void lora_rk_reduce(int64_t Mo, int64_t R, int ks,
+                                                     const float* __restrict__ part, float alpha,
+                                                     float* __restrict__ out, int64_t so_m,
+                                                     int64_t so_j, int accumulate) {
+  int64_t e = (int64_t)blockIdx.x * NTH + threadIdx.x;
+  if (e >= Mo * R) return;
+  float s = 0.0f;
+  for (int z = 0; z < ks; ++z) s += part[(int64_t)z * Mo * R + e];
+  const int64_t m = e / R, j = e % R;
+  float v = alpha * s;
+  float* o = out + m * so_m + j * so_j;
+  if (accumulate) v += *o;
+  *o = v;
+}
+
+int rk_ksplit(int64_t Mo, int64_t Kc) {
+  int64_t tiles = st::cdiv(Mo, RK_BM);
+  int64_t ks = st::cdiv(768, tiles);
+  int64_t maxk = st::cdiv(Kc, 128);
+  if (ks > maxk) ks = maxk;
+  if (ks < 1) ks = 1;
+  return (int)ks;
+}
+
 int ksplit_for(int64_t Mo, int64_t No, int64_t Kc) {
   int64_t tiles = st::cdiv(Mo, TM) * st::cdiv(No, TN);
   int64_t ks = st::cdiv(1024, tiles);
@@ -118,7 +233,10 @@ void launch_partial(int64_t Mo, int64_t No, int64_t Kc, const void* a, int64_t s
 
 extern "C" int64_t st_lora_gemm_workspace_bytes(int64_t Mo, int64_t No, int64_t Kc) {
   if (Mo <= 0 || No <= 0 || Kc <= 0) return 0;
-  return (int64_t)ksplit_for(Mo, No, Kc) * Mo * No * 4;
+  int64_t generic = (int64_t)ksplit_for(Mo, No, Kc) * Mo * No * 4;
+  int64_t big = Mo > No ? Mo : No, small = Mo > No ? No : Mo;
+  int64_t rk = (int64_t)rk_ksplit(big, Kc) * big * small * 4;
+  return generic > rk ? generic : rk;
 }
 
 extern "C" int st_lora_gemm(int64_t Mo, int64_t No, int64_t Kc, const void* a, int32_t a_dtype,
@@ -138,6 +256,43 @@ extern "C" int st_lora_gemm(int64_t Mo, int64_t No, int64_t Kc, const void* a, i
     return st::check_launch("lora_reduce");
   }
   ST_CHECK_ARG(a && b, "st_lora_gemm: NULL operand");
+  // fp32-MFMA path: the bf16 operand is contiguous along one of its dims and
+  // the fp32 operand has <= 64 columns of the output.
+  {
+    const uint16_t* G = nullptr;
+    const float* S = nullptr;
+    int64_t ldg = 0, ssk = 0, ssj = 0, big = 0, small = 0, so_m = 0, so_j = 0;
+    int col = -1;
+    if (a_dtype == ST_DTYPE_BF16 && b_dtype == ST_DTYPE_F32 && No <= 64) {
+      G = (const uint16_t*)a; S = (const float*)b; ssk = sbk; ssj = sbn;
+      big = Mo; small = No; so_m = ldo; so_j = 1;
+      if (sak == 1) { col = 0; ldg = sam; } else if (sam == 1) { col = 1; ldg = sak; }
+    } else if (a_dtype == ST_DTYPE_F32 && b_dtype == ST_DTYPE_BF16 && Mo <= 64) {
+      // out^T[n, m] = sum_k b(k, n) a(m, k)
+      G = (const uint16_t*)b; S = (const float*)a; ssk = sak; ssj = sam;
+      big = No; small = Mo; so_m = 1; so_j = ldo;
+      if (sbk == 1) { col = 0; ldg = sbn; } else if (sbn == 1) { col = 1; ldg = sbk; }
+    }
+    if (col >= 0) {
+      int ks = rk_ksplit(big, Kc);
+      int64_t need = (int64_t)ks * big * small * 4;
+      if (!workspace || workspace_bytes < need)
+        return st::fail(ST_EWORKSPACE, "st_lora_gemm: needs %lld workspace bytes", (long long)need);
+      int64_t klen = st::cdiv(st::cdiv(Kc, ks), RK_BK) * RK_BK;
+      int vec = (((uintptr_t)G & 15u) == 0 && ldg % 8 == 0) ? 1 : 0;
+      dim3 grid((unsigned)st::cdiv(big, RK_BM), (unsigned)ks);
+      float* part = (float*)workspace;
+      if (col)
+        lora_rk<true><<<grid, NTH, 0, s>>>(big, small, Kc, G, ldg, S, ssk, ssj, klen, vec, part);
+      else
+        lora_rk<false><<<grid, NTH, 0, s>>>(big, small, Kc, G, ldg, S, ssk, ssj, klen, vec, part);
+      int rc = st::check_launch("lora_rk");
+      if (rc) return rc;
+      lora_rk_reduce<<<(unsigned)st::cdiv(big * small, NTH), NTH, 0, s>>>(
+          big, small, ks, part, alpha, out, so_m, so_j, accumulate);
+      return st::check_launch("lora_rk_reduce");
+    }
+  }
   int ks = ksplit_for(Mo, No, Kc);
   int64_t need = (int64_t)ks * Mo * No * 4;
   if (!workspace || workspace_bytes < need)

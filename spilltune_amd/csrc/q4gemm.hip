@@ -21,7 +21,6 @@
 namespace {
 
 constexpr int BK = 64;
-constexpr int NT = 256;
 
 enum Mode { FWD_Q4 = 0, DGRAD_Q4 = 1, FWD_BF16 = 2, DGRAD_BF16 = 3 };
 
@@ -48,6 +47,7 @@ struct GemmParams {
   float lora_scale;
   int nseg;
   int64_t seg_end[4];
+  int64_t a_bytes, w_bytes, s_bytes;  // extents of A, W (payload or bf16), scales
 };
 
 // LDS address of 16-byte chunk c (0..7) of tile row `row` (row = 64 bf16).
@@ -59,152 +59,234 @@ __device__ __forceinline__ unsigned nib(uint32_t w, int e, int hi_first) {
   return (w >> (4 * (e ^ hi_first))) & 15u;
 }
 
-template <int MODE, int BM, int BN>
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+constexpr uint32_t kOOB = 0x80000000u;  // beyond every buffer: loads return 0
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* ptr, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(ptr), (short)0, (int)bytes,
+                                           0x00020000);
+}
+__device__ __forceinline__ uint4 ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint32_t ld4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+}
+
+// Per-(row, group) decode table: entry c = bf16_rne(codebook[c] * scale), the
+// exact product the reference computes, split into a low-byte plane and a
+// high-byte plane of 16 bytes each so v_perm_b32 can index it by code.
+struct Tbl {
+  uint32_t lo[4], hi[4];
+};
+__device__ __forceinline__ Tbl make_tbl(const Lut16& lut, float s) {
+  uint32_t t[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) t[j] = st::pack_bf16x2(lut.v[2 * j] * s, lut.v[2 * j + 1] * s);
+  Tbl T;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    T.lo[q] = __builtin_amdgcn_perm(t[2 * q + 1], t[2 * q], 0x06040200u);
+    T.hi[q] = __builtin_amdgcn_perm(t[2 * q + 1], t[2 * q], 0x07050301u);
+  }
+  return T;
+}
+// byte i of the result = plane[code_i] for the four codes in the bytes of n
+__device__ __forceinline__ uint32_t sel4(const uint32_t (&pl)[4], uint32_t n7, uint32_t hsel) {
+  uint32_t a = __builtin_amdgcn_perm(pl[1], pl[0], n7);
+  uint32_t b = __builtin_amdgcn_perm(pl[3], pl[2], n7);
+  return __builtin_amdgcn_perm(b, a, hsel);
+}
+// 8 codes of one packed word -> 4 bf16x2 words in element order
+__device__ __forceinline__ void deq8(uint32_t w, const Tbl& T, int hi_first, uint32_t (&o)[4]) {
+  uint32_t ne = w & 0x0F0F0F0Fu;         // low nibbles
+  uint32_t no = (w >> 4) & 0x0F0F0F0Fu;  // high nibbles
+  if (hi_first) { uint32_t t = ne; ne = no; no = t; }
+  // ne = codes of elements 0,2,4,6; no = codes of elements 1,3,5,7
+  const uint32_t se = 0x03020100u | ((ne >> 1) & 0x04040404u);
+  const uint32_t so = 0x03020100u | ((no >> 1) & 0x04040404u);
+  const uint32_t ne7 = ne & 0x07070707u, no7 = no & 0x07070707u;
+  const uint32_t el = sel4(T.lo, ne7, se), eh = sel4(T.hi, ne7, se);
+  const uint32_t ol = sel4(T.lo, no7, so), oh = sel4(T.hi, no7, so);
+  const uint32_t e02 = __builtin_amdgcn_perm(eh, el, 0x05010400u);  // (e0, e2)
+  const uint32_t e46 = __builtin_amdgcn_perm(eh, el, 0x07030602u);  // (e4, e6)
+  const uint32_t o13 = __builtin_amdgcn_perm(oh, ol, 0x05010400u);  // (e1, e3)
+  const uint32_t o57 = __builtin_amdgcn_perm(oh, ol, 0x07030602u);  // (e5, e7)
+  o[0] = __builtin_amdgcn_perm(o13, e02, 0x05040100u);
+  o[1] = __builtin_amdgcn_perm(o13, e02, 0x07060302u);
+  o[2] = __builtin_amdgcn_perm(o57, e46, 0x05040100u);
+  o[3] = __builtin_amdgcn_perm(o57, e46, 0x07060302u);
+}
+
+// WAVES = 4 (2x2 waves) or 8 (2x4 waves: two waves per SIMD, 128x64 each)
+template <int MODE, int BM, int BN, int WAVES>
 struct Tile {
-  static constexpr int WM = BM / 2, WN = BN / 2;
+  static constexpr int NT = 64 * WAVES;
+  static constexpr int WAVES_N = WAVES / 2;
+  static constexpr int WM = BM / 2, WN = BN / WAVES_N;
   static constexpr int FM = WM / 32, FN = WN / 32;
   static constexpr int A_IT = BM * 8 / NT;  // 16-byte chunks per thread
   static constexpr bool Q4 = (MODE == FWD_Q4 || MODE == DGRAD_Q4);
   static constexpr bool DGRAD = (MODE == DGRAD_Q4 || MODE == DGRAD_BF16);
-  static constexpr int BF_IT = BN * 8 / NT;  // FWD_BF16 chunks per thread
-  static constexpr int BQ_IT = BN * 2 / NT;  // FWD_Q4 16-byte payload loads per thread
-  static constexpr int QB = BN / 32;         // dgrad: contraction rows per thread block
+  static constexpr int BF_IT = BN * 8 / NT;        // FWD_BF16 chunks per thread
+  static constexpr int QB = BN * BK / (NT * 8);    // dgrad: contraction rows per thread block
   static constexpr int LDS_CHUNKS = 2 * (BM + BN) * 8;
 };
 
-template <int MODE, int BM, int BN>
-__global__ __launch_bounds__(NT) void gemm_kernel(GemmParams p) {
-  using TL = Tile<MODE, BM, BN>;
+template <int MODE, int BM, int BN, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
+  using TL = Tile<MODE, BM, BN, WAVES>;
+  constexpr int NT = TL::NT;
   constexpr int WM = TL::WM, WN = TL::WN, FM = TL::FM, FN = TL::FN;
   __shared__ uint4 lds[TL::LDS_CHUNKS];
-  __shared__ float lut_s[16];
+  __shared__ float lut_s[16];  // codebook for the transposed (dgrad) dequant
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / TL::WAVES_N, wn = wave % TL::WAVES_N;
   const int64_t tiles_p = st::cdiv(p.P, BN);
   const int64_t t = st::xcd_remap(blockIdx.x, gridDim.x);
   const int64_t m0 = (t / tiles_p) * BM, p0 = (t % tiles_p) * BN;
   const int KT = (int)st::cdiv(p.Q, BK);
 
-  if (TL::Q4 && tid < 16) lut_s[tid] = p.lut.v[tid];
-
   // buffer b: A tile at lds + b*(BM+BN)*8, B tile right after it
   auto As = [&](int b) { return lds + b * (BM + BN) * 8; };
   auto Bs = [&](int b) { return lds + b * (BM + BN) * 8 + BM * 8; };
 
-  // ---- register staging of one k-step ----
-  uint4 ra[TL::A_IT];
-  uint4 rbw[TL::Q4 ? (TL::DGRAD ? 1 : TL::BQ_IT) : (TL::DGRAD ? TL::QB : TL::BF_IT)];
-  uint32_t rqd[TL::DGRAD && TL::Q4 ? TL::QB : 1];
-  float rs[TL::Q4 ? (TL::DGRAD ? TL::QB : TL::BQ_IT) : 1];
+  // ---- buffer resources: out-of-range loads return zero, so the main loop
+  // needs no bounds branches (rows beyond M/P and the contraction tail).
+  const auto rsA = make_rsrc(p.A, p.a_bytes);
+  const auto rsW = make_rsrc(TL::Q4 ? (const void*)p.Wq : (const void*)p.Wb, p.w_bytes);
+  const auto rsS = make_rsrc(p.Ws, p.s_bytes);
 
-  auto load_global = [&](int kt) {
-    const int64_t k0 = (int64_t)kt * BK;
+  // A (activations / upstream gradient): 16-byte chunks, row-major, contraction contiguous
+  uint32_t a_row[TL::A_IT];
+  int a_k[TL::A_IT];
+#pragma unroll
+  for (int i = 0; i < TL::A_IT; ++i) {
+    int id = tid + i * NT, row = id >> 3, c = id & 7;
+    int64_t m = m0 + row;
+    a_row[i] = m < p.M ? (uint32_t)((m * p.lda + c * 8) * 2) : kOOB;
+    a_k[i] = c * 8;
+  }
+  auto load_A = [&](int kt, uint4 (&xr)[TL::A_IT]) {
 #pragma unroll
     for (int i = 0; i < TL::A_IT; ++i) {
-      int id = tid + i * NT, row = id >> 3, c = id & 7;
-      int64_t m = m0 + row, k = k0 + c * 8;
-      ra[i] = (m < p.M && k < p.Q) ? *(const uint4*)(p.A + m * p.lda + k) : make_uint4(0, 0, 0, 0);
+      int k = kt * BK + a_k[i];
+      uint32_t off = (a_row[i] != kOOB && k < p.Q) ? a_row[i] + (uint32_t)(kt * BK * 2) : kOOB;
+      xr[i] = ld16(rsA, off);
     }
-    if constexpr (MODE == FWD_Q4) {
+  };
+  auto store_A = [&](uint4* as, const uint4 (&xr)[TL::A_IT]) {
 #pragma unroll
-      for (int i = 0; i < TL::BQ_IT; ++i) {
-        int id = tid + i * NT, row = id >> 1, h = id & 1;
-        int64_t n = p0 + row, k = k0 + 32 * h;
-        if (n < p.P) {
-          int64_t e = n * p.ldw + k;
-          rbw[i] = *(const uint4*)(p.Wq + (e >> 1));
-          rs[i] = p.Ws[e >> 7];
-        } else {
-          rbw[i] = make_uint4(0x77777777u, 0x77777777u, 0x77777777u, 0x77777777u);
-          rs[i] = 0.0f;
-        }
-      }
+    for (int i = 0; i < TL::A_IT; ++i) {
+      int id = tid + i * NT;
+      as[swz(id >> 3, id & 7)] = xr[i];
+    }
+  };
+
+  // B operand source.  FWD_Q4: thread owns EPT consecutive weights of one W row.
+  constexpr int TPR = NT / BN;          // threads per W row (1 or 2)
+  constexpr int EPT = BK / TPR;         // elements per thread per k-step (64 or 32)
+  constexpr int WQ = TL::Q4 ? (TL::DGRAD ? TL::QB : EPT / 32) : (TL::DGRAD ? TL::QB : TL::BF_IT);
+  constexpr int PB = BN / 8;
+  const int brow = tid / TPR, bsub = tid % TPR;       // FWD_Q4 mapping
+  const int pb = tid % PB, qb = tid / PB;             // DGRAD mapping
+  uint32_t w_row = 0;
+  if constexpr (MODE == FWD_Q4) {
+    int64_t n = p0 + brow;
+    w_row = n < p.P ? (uint32_t)(n * p.ldw + bsub * EPT) : kOOB;  // element index at k = 0
+  }
+
+  struct WRegs {
+    uint4 q[WQ];
+    uint32_t d[TL::DGRAD && TL::Q4 ? TL::QB : 1];
+    float s[TL::Q4 ? (TL::DGRAD ? TL::QB : 1) : 1];
+  };
+  auto load_W = [&](int kt, WRegs& w) {
+    if constexpr (MODE == FWD_Q4) {
+      uint32_t e = w_row + (uint32_t)(kt * BK);
+      uint32_t po = w_row != kOOB ? e >> 1 : kOOB;
+      uint32_t so = w_row != kOOB ? (e >> 7) * 4 : kOOB;
+#pragma unroll
+      for (int i = 0; i < WQ; ++i) w.q[i] = ld16(rsW, po == kOOB ? kOOB : po + 16 * i);
+      w.s[0] = __builtin_bit_cast(float, ld4(rsS, so));
     } else if constexpr (MODE == FWD_BF16) {
 #pragma unroll
-      for (int i = 0; i < TL::BF_IT; ++i) {
+      for (int i = 0; i < WQ; ++i) {
         int id = tid + i * NT, row = id >> 3, c = id & 7;
-        int64_t n = p0 + row, k = k0 + c * 8;
-        rbw[i] = (n < p.P && k < p.Q) ? *(const uint4*)(p.Wb + n * p.ldw + k) : make_uint4(0, 0, 0, 0);
+        int64_t n = p0 + row;
+        int k = kt * BK + c * 8;
+        w.q[i] = ld16(rsW, (n < p.P && k < p.Q) ? (uint32_t)((n * p.ldw + k) * 2) : kOOB);
       }
     } else {
-      constexpr int PB = BN / 8;
-      int pb = tid % PB, qb = tid / PB;
       int64_t pc = p0 + pb * 8;
 #pragma unroll
       for (int i = 0; i < TL::QB; ++i) {
-        int64_t q = k0 + qb * TL::QB + i;
-        bool ok = (pc < p.P) && (q < p.Q);
+        int64_t q = (int64_t)kt * BK + qb * TL::QB + i;
+        bool ok = pc < p.P && q < p.Q;
+        int64_t e = q * p.ldw + pc;
         if constexpr (MODE == DGRAD_Q4) {
-          int64_t e = q * p.ldw + pc;
-          rqd[i] = ok ? *(const uint32_t*)(p.Wq + (e >> 1)) : 0x77777777u;
-          rs[i] = ok ? p.Ws[e >> 7] : 0.0f;
+          w.d[i] = ld4(rsW, ok ? (uint32_t)(e >> 1) : kOOB);
+          w.s[i] = __builtin_bit_cast(float, ld4(rsS, ok ? (uint32_t)((e >> 7) * 4) : kOOB));
         } else {
-          rbw[i] = ok ? *(const uint4*)(p.Wb + q * p.ldw + pc) : make_uint4(0, 0, 0, 0);
+          w.q[i] = ld16(rsW, ok ? (uint32_t)(e * 2) : kOOB);
         }
       }
     }
   };
 
-  auto store_lds = [&](int buf) {
-    uint4* as = As(buf);
-    uint4* bs = Bs(buf);
-#pragma unroll
-    for (int i = 0; i < TL::A_IT; ++i) {
-      int id = tid + i * NT, row = id >> 3, c = id & 7;
-      as[swz(row, c)] = ra[i];
-    }
+  // dequantise / stage one quarter (part = 0..3) of the B tile into LDS
+  Tbl tbl;
+  auto store_B_part = [&](uint4* bs, const WRegs& w, int part) {
     if constexpr (MODE == FWD_Q4) {
+      constexpr int CH = EPT / 8;        // 8-element chunks per thread
+      constexpr int PER = CH / 4;        // chunks per quarter (2 or 1)
 #pragma unroll
-      for (int i = 0; i < TL::BQ_IT; ++i) {
-        int id = tid + i * NT, row = id >> 1, h = id & 1;
-        const float s = rs[i];
-        uint32_t w4[4] = {rbw[i].x, rbw[i].y, rbw[i].z, rbw[i].w};
-#pragma unroll
-        for (int d = 0; d < 4; ++d) {
-          uint32_t o[4];
-#pragma unroll
-          for (int e = 0; e < 8; e += 2)
-            o[e / 2] = st::pack_bf16x2(lut_s[nib(w4[d], e, p.hi_first)] * s,
-                                       lut_s[nib(w4[d], e + 1, p.hi_first)] * s);
-          bs[swz(row, 4 * h + d)] = make_uint4(o[0], o[1], o[2], o[3]);
-        }
+      for (int u = 0; u < PER; ++u) {
+        const int ch = part * PER + u;
+        const uint4 q = w.q[ch / 4];
+        const uint32_t word = (ch & 3) == 0 ? q.x : (ch & 3) == 1 ? q.y : (ch & 3) == 2 ? q.z : q.w;
+        uint32_t o[4];
+        deq8(word, tbl, p.hi_first, o);
+        bs[swz(brow, (bsub * EPT) / 8 + ch)] = make_uint4(o[0], o[1], o[2], o[3]);
       }
     } else if constexpr (MODE == FWD_BF16) {
 #pragma unroll
-      for (int i = 0; i < TL::BF_IT; ++i) {
-        int id = tid + i * NT, row = id >> 3, c = id & 7;
-        bs[swz(row, c)] = rbw[i];
+      for (int i = 0; i < WQ; ++i) {
+        if (i * 4 / WQ != part) continue;
+        int id = tid + i * NT;
+        bs[swz(id >> 3, id & 7)] = w.q[i];
       }
     } else {
-      constexpr int PB = BN / 8;
-      int pb = tid % PB, qb = tid / PB;
-      float v[TL::QB][8];
+      // columns j = 2*part, 2*part+1 of the thread's QB x 8 block, written transposed
 #pragma unroll
-      for (int i = 0; i < TL::QB; ++i) {
-        if constexpr (MODE == DGRAD_Q4) {
+      for (int jj = 0; jj < 2; ++jj) {
+        const int j = 2 * part + jj;
+        float v[TL::QB];
 #pragma unroll
-          for (int j = 0; j < 8; ++j) v[i][j] = lut_s[nib(rqd[i], j, p.hi_first)] * rs[i];
-        } else {
-          uint32_t w4[4] = {rbw[i].x, rbw[i].y, rbw[i].z, rbw[i].w};
-#pragma unroll
-          for (int j = 0; j < 8; ++j)
-            v[i][j] = st::bf16_to_f32((uint16_t)(w4[j >> 1] >> (16 * (j & 1))));
+        for (int i = 0; i < TL::QB; ++i) {
+          if constexpr (MODE == DGRAD_Q4)
+            v[i] = lut_s[nib(w.d[i], j, p.hi_first)] * w.s[i];
+          else {
+            uint32_t word = (j >> 1) == 0 ? w.q[i].x : (j >> 1) == 1 ? w.q[i].y
+                            : (j >> 1) == 2 ? w.q[i].z : w.q[i].w;
+            v[i] = st::bf16_to_f32((uint16_t)(word >> (16 * (j & 1))));
+          }
         }
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        int prow = pb * 8 + j;
+        const int prow = pb * 8 + j;
         if constexpr (TL::QB == 8) {
-          uint4 o = make_uint4(st::pack_bf16x2(v[0][j], v[1][j]), st::pack_bf16x2(v[2][j], v[3][j]),
-                               st::pack_bf16x2(v[4][j], v[5][j]), st::pack_bf16x2(v[6][j], v[7][j]));
-          bs[swz(prow, qb)] = o;
+          bs[swz(prow, qb)] = make_uint4(st::pack_bf16x2(v[0], v[1]), st::pack_bf16x2(v[2], v[3]),
+                                         st::pack_bf16x2(v[4], v[5]), st::pack_bf16x2(v[6], v[7]));
         } else {
-          uint2 o = make_uint2(st::pack_bf16x2(v[0][j], v[1][j]), st::pack_bf16x2(v[2][j], v[3][j]));
-          ((uint2*)&bs[swz(prow, qb >> 1)])[qb & 1] = o;
+          ((uint2*)&bs[swz(prow, qb >> 1)])[qb & 1] =
+              make_uint2(st::pack_bf16x2(v[0], v[1]), st::pack_bf16x2(v[2], v[3]));
         }
       }
     }
+  };
+  auto prep_B = [&](const WRegs& w) {
+    if constexpr (MODE == FWD_Q4) tbl = make_tbl(p.lut, w.s[0]);
   };
 
   f32x16 acc[FM][FN];
@@ -215,16 +297,22 @@ __global__ __launch_bounds__(NT) void gemm_kernel(GemmParams p) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  load_global(0);
-  __syncthreads();  // lut_s visible before the first dequant
-  store_lds(0);
-  __syncthreads();
-
-  for (int kt = 0; kt < KT; ++kt) {
+  // one k-step: MFMAs on LDS buffer `cur`, with the next tile's A stores, B
+  // dequant/stores and the loads two steps ahead placed between them
+  uint4 xr[TL::A_IT];
+  WRegs w0, w1;
+  // new_group: the tile dequantised in this step starts a 128-wide scale group
+  // (even tile index), so its decode table must be rebuilt; odd tiles reuse it.
+  auto body = [&](int kt, WRegs& wnext, WRegs& wfar, bool new_group) {
     const int cur = kt & 1;
-    if (kt + 1 < KT) load_global(kt + 1);
+    uint4* as_n = As(cur ^ 1);
+    uint4* bs_n = Bs(cur ^ 1);
     const uint4* as = As(cur);
     const uint4* bs = Bs(cur);
+    store_A(as_n, xr);
+    load_A(kt + 2, xr);
+    load_W(kt + 2, wfar);
+    if (new_group) prep_B(wnext);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const int c = 2 * s + (lane >> 5);
@@ -240,9 +328,30 @@ __global__ __launch_bounds__(NT) void gemm_kernel(GemmParams p) {
 #pragma unroll
         for (int j = 0; j < FN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+      store_B_part(bs_n, wnext, s);
+      // keep each slice's fragments and dequant work together (bounds live ranges)
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if (kt + 1 < KT) store_lds(cur ^ 1);
     __syncthreads();
+  };
+
+  // prologue: tiles 0 (LDS) and 1 (registers), W for tiles 0 and 1
+  load_A(0, xr);
+  load_W(0, w0);
+  load_W(1, w1);
+  if (TL::Q4 && TL::DGRAD && tid < 16) lut_s[tid] = p.lut.v[tid];
+  __syncthreads();
+  store_A(As(0), xr);
+  prep_B(w0);
+#pragma unroll
+  for (int s = 0; s < 4; ++s) store_B_part(Bs(0), w0, s);
+  load_A(1, xr);
+  __syncthreads();
+
+  // tile kt+1's W sits in w1 (kt even) or w0 (kt odd); W for kt+2 lands in the other
+  for (int kt = 0; kt < KT; kt += 2) {
+    body(kt, w1, w0, false);
+    if (kt + 1 < KT) body(kt + 1, w0, w1, true);
   }
 
   // ---------------- epilogue ----------------
@@ -319,34 +428,41 @@ __global__ __launch_bounds__(NT) void gemm_kernel(GemmParams p) {
   }
 }
 
-template <int MODE, int BM, int BN>
+template <int MODE, int BM, int BN, int WAVES>
 int launch(const GemmParams& p, hipStream_t stream) {
+  constexpr int NT = 64 * WAVES;
   int64_t tiles = st::cdiv(p.M, BM) * st::cdiv(p.P, BN);
   if (tiles > 0x7fffffff) return st::fail(ST_EUNSUPPORTED, "q4gemm: too many tiles");
   if (p.T) {  // the LoRA epilogue stages T and the right operand in the tile's LDS
-    using TL = Tile<MODE, BM, BN>;
+    using TL = Tile<MODE, BM, BN, WAVES>;
     int64_t need = (int64_t)BM * (p.lora_cols + 1) +
                    (TL::DGRAD ? (int64_t)p.lora_k * BN : (int64_t)BN * (p.lora_k + 1));
     if (need > (int64_t)TL::LDS_CHUNKS * 4)
       return st::fail(ST_EUNSUPPORTED, "q4gemm: LoRA epilogue (%d columns) exceeds tile LDS",
                       p.lora_cols);
   }
-  gemm_kernel<MODE, BM, BN><<<(unsigned)tiles, NT, 0, stream>>>(p);
+  gemm_kernel<MODE, BM, BN, WAVES><<<(unsigned)tiles, NT, 0, stream>>>(p);
   return st::check_launch("q4gemm");
 }
 
-int tile_choice(int64_t M, int64_t P) {
-  // 256x256 needs enough tiles to cover the 256 CUs; otherwise 128x128.
+// 256x256 (8 waves) halves the dequant work per MFMA but needs enough tiles to
+// cover the 256 CUs; the transposed-dequant (dgrad) pass stays on 128x128.
+int tile_choice(int mode, int64_t M, int64_t P) {
   const char* env = getenv("ST_GEMM_TILE");
   if (env) return atoi(env);
-  int64_t big = st::cdiv(M, 256) * st::cdiv(P, 256);
-  return big >= 256 ? 256 : 128;
+  if (mode == FWD_Q4 && st::cdiv(M, 256) * st::cdiv(P, 256) >= 192) return 256;
+  return 128;
 }
 
 template <int MODE>
 int dispatch(const GemmParams& p, hipStream_t stream) {
-  if (tile_choice(p.M, p.P) == 256) return launch<MODE, 256, 256>(p, stream);
-  return launch<MODE, 128, 128>(p, stream);
+  // the dense-W fallbacks (K not a multiple of 128) always use 128x128 tiles
+  if constexpr (MODE == FWD_Q4 || MODE == DGRAD_Q4) {
+    const int t = tile_choice(MODE, p.M, p.P);
+    if (t == 256) return launch<MODE, 256, 256, 8>(p, stream);
+    if (t == 2564) return launch<MODE, 256, 256, 4>(p, stream);
+  }
+  return launch<MODE, 128, 128, 4>(p, stream);
 }
 
 int run_gemm(int mode, const GemmParams& p, hipStream_t stream) {
@@ -425,8 +541,12 @@ extern "C" int st_q4_linear_fwd(const uint16_t* x, int64_t M, int64_t K, int64_t
     p.lora_cols = rank * nseg; p.lora_scale = lora_scale; p.nseg = nseg;
   }
   hipStream_t s = (hipStream_t)stream;
+  p.a_bytes = ((M - 1) * ldx + K) * 2;
+  ST_CHECK_ARG(p.a_bytes < (1ll << 31) && N * K * 2 < (1ll << 31),
+               "st_q4_linear_fwd: operands above 2 GiB are not supported");
   if (K % 128 == 0 && al16(payload)) {
     p.Wq = payload; p.Ws = scales; p.ldw = K;
+    p.w_bytes = N * K / 2; p.s_bytes = N * K / 128 * 4;
     return run_gemm(FWD_Q4, p, s);
   }
   // flat groups straddle rows: decode W once into the workspace, bf16 GEMM
@@ -438,6 +558,7 @@ extern "C" int st_q4_linear_fwd(const uint16_t* x, int64_t M, int64_t K, int64_t
   int rc = st::launch_dequant4(payload, scales, N * K, 128, lut16, flags, (uint16_t*)workspace, s);
   if (rc) return rc;
   p.Wb = (const uint16_t*)workspace; p.ldw = K;
+  p.w_bytes = N * K * 2; p.s_bytes = 0;
   return run_gemm(FWD_BF16, p, s);
 }
 
@@ -469,8 +590,13 @@ extern "C" int st_q4_linear_dgrad(const uint16_t* dy, int64_t M, int64_t N, int6
     p.lora_scale = 1.0f;
   }
   hipStream_t s = (hipStream_t)stream;
+  p.a_bytes = ((M - 1) * lddy + N) * 2;
+  ST_CHECK_ARG(p.a_bytes < (1ll << 31) && N * K * 2 < (1ll << 31),
+               "st_q4_linear_dgrad: operands above 2 GiB are not supported");
   if (K % 128 == 0) {
+    ST_CHECK_ARG(((uintptr_t)payload & 3u) == 0, "st_q4_linear_dgrad: payload not 4-byte aligned");
     p.Wq = payload; p.Ws = scales; p.ldw = K;
+    p.w_bytes = N * K / 2; p.s_bytes = N * K / 128 * 4;
     return run_gemm(DGRAD_Q4, p, s);
   }
   int64_t need = N * K * 2;
@@ -481,5 +607,6 @@ extern "C" int st_q4_linear_dgrad(const uint16_t* dy, int64_t M, int64_t N, int6
   int rc = st::launch_dequant4(payload, scales, N * K, 128, lut16, flags, (uint16_t*)workspace, s);
   if (rc) return rc;
   p.Wb = (const uint16_t*)workspace; p.ldw = K;
+  p.w_bytes = N * K * 2; p.s_bytes = 0;
   return run_gemm(DGRAD_BF16, p, s);
 }
