@@ -109,6 +109,55 @@ def cpu_baseline(c, block, tokens, min_seconds=10.0):
                       f"the same layer, oracle/layer.py on {cores} host cores, {dt:.1f} s"}
 
 
+def streamed(c, block, args, X, dY, rot, mask):
+    """N copies of the layer streamed through a 2-slot session: forward over
+    all layers, backward in reverse (each layer loaded per phase, the last
+    forward layer reused), H2D of the packed image on the copy stream."""
+    import torch
+    from spilltune_amd import slots
+    from spilltune_amd.recompute import streaming_block
+    L = args.streamed_layers
+    dev = X.device
+    blocks = [block] + [slots.BlockPlan(i, block.kind, block.functional, dict(block.kwargs),
+                                        block.host_weights, block.adapters, block.storage_specs)
+                        for i in range(1, L)]
+    # every copy gets its own (shared-state) adapters object binding; LoRA state is shared
+    session = slots.Q4SlotSession(blocks, dev, host_budget_bytes=1 << 40,
+                                  device_budget_bytes=1 << 40, slots=2)
+
+    def step():
+        h0 = X.detach().requires_grad_(True)
+        with session.run():
+            h = h0
+            for b in blocks:
+                h = streaming_block(h, rot, mask, b.functional, b.kwargs, session.reloader(b),
+                                    b.adapters, b.index, accumulate_adapter_grads=b.index > 0)
+            h.backward(dY)
+
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize()
+    session.completed_copies = []
+    t0 = time.perf_counter()
+    n = max(2, args.steps // 4)
+    for _ in range(n):
+        step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / n
+    copies = session.completed_copies
+    h2d = sum(cp["bytes"] for cp in copies) / max(sum(cp["copy_cuda_ms"] for cp in copies), 1e-9) / 1e6
+    per_layer_ms = dt * 1e3 / L
+    out = {"layers": L, "slots": 2, "ms_per_step": round(dt * 1e3, 3),
+           "ms_per_layer": round(per_layer_ms, 4),
+           "tokens_per_s_per_layer": round(c["B"] * c["S"] / (per_layer_ms * 1e-3), 1),
+           "h2d_bytes_per_step": int(sum(cp["bytes"] for cp in copies) / n),
+           "h2d_gbps_while_copying": round(h2d, 2), "copies_per_step": len(copies) / n,
+           "cache_hits": session.hits}
+    session.close()
+    log(f"streamed {L} layers: {out}")
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -117,6 +166,9 @@ def main():
     ap.add_argument("--config", default="llama8b", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-tokens", type=int, default=2048)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--streamed-layers", type=int, default=0,
+                    help="also time N layers streamed from pinned host RAM through 2 device "
+                         "slots with one-layer prefetch (reported under 'streamed')")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one MI355X; "
@@ -212,6 +264,8 @@ def main():
                      "avg_ms": round(info["avg_ms"], 4)},
         "cpu_baseline": None,
     }
+    if args.streamed_layers > 0:
+        result["streamed"] = streamed(c, block, args, X, dY, rot, mask)
     if not args.no_cpu_baseline:
         log(f"timing the CPU path at {args.cpu_tokens} tokens")
         result["cpu_baseline"] = cpu_baseline(c, block, args.cpu_tokens)

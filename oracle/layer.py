@@ -204,3 +204,39 @@ def adamw_step(params_grads_states, *, step, lr, beta1=0.9, beta2=0.999, eps=1e-
             v.mul_(beta2).addcmul_(grad, grad, value=1.0 - beta2)
             denom = (v.sqrt() / bc2_sqrt).add_(eps)
             param.addcdiv_(m, denom, value=-step_size)
+
+
+def train_reference(embedding, norm_weight, head, layers, loras, rows, *, cfg, theta, steps,
+                    lr, weight_decay=0.0, token_chunk=64, accumulation=1):
+    """The reference's optimizer-step loop (engine.py:162-182 with microbatch,
+    engine.py:48-79) on the CPU: bf16 layer math through autograd (the
+    per-layer recompute computes the same graph), token-chunked CE, fp32
+    AdamW.  ``layers``: per-layer bf16 weight dicts; ``loras``: per-layer
+    ``{name: Lora}``.  Returns the per-step losses."""
+    import torch.nn.functional as F  # noqa: F811
+    tensors = [(p.A, p) for lo in loras for p in lo.values()] + \
+              [(p.B, p) for lo in loras for p in lo.values()]
+    states = {id(t): (torch.zeros_like(t), torch.zeros_like(t)) for t, _ in tensors}
+    cursor, losses = 0, []
+    for step in range(1, steps + 1):
+        items = [rows[(cursor + i) % len(rows)] for i in range(accumulation)]
+        normalization = sum(int((labels[:, 1:] != -100).sum()) for _, labels in items)
+        for t, _ in tensors:
+            t.grad = None
+        loss = 0.0
+        for ids, labels in items:
+            B, S = ids.shape
+            rot = rotary(B, S, cfg["head_dim"], theta, torch.bfloat16)
+            mask = causal_mask(B, S, torch.bfloat16)
+            hidden = F.embedding(ids, embedding).detach()
+            for w, lo in zip(layers, loras):
+                hidden = dense_block(hidden, rot, mask, weights=w, loras=lo, **cfg)
+            value, grad = causal_lm_terminal(hidden, norm_weight, head, labels, eps=cfg["eps"],
+                                             normalization=normalization, token_chunk=token_chunk)
+            hidden.backward(grad)
+            loss += value
+        adamw_step([(t, t.grad.float(), *states[id(t)]) for t, _ in tensors], step=step, lr=lr,
+                   weight_decay=weight_decay)
+        cursor += accumulation
+        losses.append(loss)
+    return losses

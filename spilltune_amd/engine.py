@@ -1,0 +1,167 @@
+"""Causal-LM training step over 4-bit streamed blocks (mirror of
+training/engine.py:21-195 and finetune/optimizer.py:227-342 in
+/root/reference/src/ram_vram_finetune, without the config/dataset/checkpoint
+I/O around it).
+
+* :func:`forward` -- the per-layer loop through the streaming recompute driver
+  (engine.py:36-45).
+* :func:`microbatch` -- embedding, layers, full-sequence terminal norm,
+  token-chunked head + summed cross-entropy / normaliser, norm VJP, one
+  decoder backward (engine.py:48-79).  The terminal norm is the HIP RMSNorm;
+  the head GEMM and CE are PyTorch ops on the device (a fused terminal kernel
+  is a later row).
+* :class:`AdamW` -- the fp32 update in torch.optim.AdamW's non-foreach order
+  (optimizer.py:324-342), on the device.
+* :func:`train` -- the optimizer-step loop with gradient accumulation over
+  cyclic rows (engine.py:162-182).
+* :class:`DenseModel` -- the adapter surface the engine uses
+  (adapters/protocol.py:23-34) for a Llama-family model whose decoder
+  matrices are stored 4-bit.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn.functional as F
+
+from . import ops, slots
+from .dense import positions_and_masks
+from .recompute import streaming_block
+
+
+def flatten(model) -> dict:
+    """``{"{layer}:{target}": projection}`` (engine.py:21-33)."""
+    result, seen = {}, set()
+    for block in model.blocks:
+        for name, proj in block.adapters.items():
+            key = f"{block.index}:{name}"
+            if key in result or id(proj) in seen:
+                raise ValueError("unsupported_capability: duplicate/shared trainable parameter")
+            result[key] = proj
+            seen.add(id(proj))
+    if not result:
+        raise ValueError("training plan has no trainable projections")
+    return result
+
+
+def forward(model, session, hidden, positions, masks, *, accumulate=False):
+    for block in model.blocks:
+        hidden = streaming_block(hidden, positions, masks[block.kind], block.functional, block.kwargs,
+                                 session.reloader(block), block.adapters, block.index,
+                                 accumulate_adapter_grads=accumulate)
+    return hidden
+
+
+def microbatch(model, session, input_ids, labels, *, normalization, token_chunk, accumulate=False):
+    """Exact shifted summed CE / window token count; one decoder backward."""
+    device = model.device
+    valid = torch.ones_like(input_ids, dtype=torch.bool)
+    positions, masks = model.positions_and_masks(valid)
+    embedded = F.embedding(input_ids.cpu(), model.embedding).to(device).detach().requires_grad_(True)
+    hidden = forward(model, session, embedded, positions, masks, accumulate=accumulate)
+    terminal_input = hidden.detach().requires_grad_(True)
+    normalized = model.terminal_norm(terminal_input)
+    normalized_gradient = torch.zeros_like(normalized)
+    loss_sum = torch.zeros((), device=device)
+    labels = labels.to(device)
+    for start in range(0, input_ids.shape[1] - 1, token_chunk):
+        end = min(start + token_chunk, input_ids.shape[1] - 1)
+        target = labels[:, start + 1:end + 1]
+        if not (target != -100).any():
+            continue
+        h = normalized[:, start:end].detach().requires_grad_(True)
+        logits = F.linear(h, model.head)
+        chunk = F.cross_entropy(logits.float().reshape(-1, logits.shape[-1]), target.reshape(-1),
+                                ignore_index=-100, reduction="sum")
+        (grad,) = torch.autograd.grad(chunk / normalization, h)
+        normalized_gradient[:, start:end].copy_(grad.detach())
+        loss_sum += chunk.detach()
+    (gradient,) = torch.autograd.grad(normalized, terminal_input, normalized_gradient)
+    if not torch.isfinite(loss_sum) or not torch.isfinite(gradient).all():
+        raise FloatingPointError("non-finite causal loss/gradient")
+    hidden.backward(gradient)
+    return float(loss_sum / normalization), embedded.grad.detach().clone()
+
+
+class AdamW:
+    """Bias-corrected fp32 AdamW over LoRA projections (optimizer.py:227-342)."""
+
+    def __init__(self, lr=1e-4, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.0):
+        self.lr, self.beta1, self.beta2, self.eps = lr, beta1, beta2, eps
+        self.weight_decay = weight_decay
+        self.step_count = 0
+
+    def zero_grad(self, projections):
+        for p in projections.values():
+            p.grad_A.zero_()
+            p.grad_B.zero_()
+            p.A.grad = None
+            p.B.grad = None
+
+    def step(self, projections):
+        n = self.step_count + 1
+        step_size = self.lr / (1.0 - self.beta1 ** n)
+        bc2_sqrt = math.sqrt(1.0 - self.beta2 ** n)
+        with torch.no_grad():
+            for p in projections.values():
+                for param, grad, m, v in ((p.A, p.grad_A, p.m_A, p.v_A), (p.B, p.grad_B, p.m_B, p.v_B)):
+                    if self.weight_decay != 0.0:
+                        param.mul_(1.0 - self.lr * self.weight_decay)
+                    m.lerp_(grad, 1.0 - self.beta1)
+                    v.mul_(self.beta2).addcmul_(grad, grad, value=1.0 - self.beta2)
+                    denom = (v.sqrt() / bc2_sqrt).add_(self.eps)
+                    param.addcdiv_(m, denom, value=-step_size)
+        self.step_count = n
+
+
+def train(model, session, rows, *, steps, accumulation=1, lr=1e-4, weight_decay=0.0,
+          token_chunk=64):
+    """Optimizer-step loop with cyclic rows (engine.py:162-182); returns losses."""
+    projections = flatten(model)
+    optimizer = AdamW(lr=lr, weight_decay=weight_decay)
+    cursor, losses = 0, []
+    for _ in range(steps):
+        items = [rows[(cursor + i) % len(rows)] for i in range(accumulation)]
+        normalization = sum(int((labels[:, 1:] != -100).sum()) for _, labels in items)
+        optimizer.zero_grad(projections)
+        loss = 0.0
+        with session.run():
+            for i, (ids, labels) in enumerate(items):
+                micro, _ = microbatch(model, session, ids, labels, normalization=normalization,
+                                      token_chunk=token_chunk, accumulate=i > 0)
+                loss += micro
+            optimizer.step(projections)
+        cursor += accumulation
+        losses.append(loss)
+    return losses
+
+
+class DenseModel:
+    """Llama-family model with 4-bit decoder matrices in slot images: the
+    runtime surface of adapters/dense.py:178-263 the engine needs."""
+
+    def __init__(self, *, embedding, norm, head, layers, heads, kv_heads, head_dim, eps, theta,
+                 rank, alpha, targets, device, codec="nf4-g128", generator=None):
+        self.device = torch.device(device)
+        self.embedding = embedding.to(torch.bfloat16).contiguous()      # stays on the host
+        self.norm = norm.to(torch.bfloat16).to(self.device)
+        self.head = head.to(torch.bfloat16).to(self.device)
+        self.eps, self.theta, self.head_dim = eps, theta, head_dim
+        self.blocks = [slots.make_dense_block(i, w, codec=codec, heads=heads, kv_heads=kv_heads,
+                                              head_dim=head_dim, eps=eps, rank=rank, alpha=alpha,
+                                              targets=targets, device=self.device,
+                                              generator=generator)
+                       for i, w in enumerate(layers)]
+
+    def positions_and_masks(self, valid):
+        rot, mask = positions_and_masks(valid, head_dim=self.head_dim, theta=self.theta,
+                                        device=self.device)
+        return rot, {"full_attention": mask}
+
+    def terminal_norm(self, hidden):
+        B, S, H = hidden.shape
+        return ops.rms_norm(hidden.reshape(B * S, H), self.norm, self.eps).view(B, S, H)
+
+    def close(self):
+        self.blocks.clear()
