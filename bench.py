@@ -166,6 +166,9 @@ def main():
     ap.add_argument("--config", default="llama8b", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-tokens", type=int, default=2048)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run 3 device copies of 256 MiB (the reference kernel for scaling "
+                         "rocprofv3 FETCH_SIZE/WRITE_SIZE counters to bytes) and exit")
     ap.add_argument("--streamed-layers", type=int, default=0,
                     help="also time N layers streamed from pinned host RAM through 2 device "
                          "slots with one-layer prefetch (reported under 'streamed')")
@@ -176,6 +179,14 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.copy_calibration:
+        x = torch.empty(256 * 1024 * 1024, dtype=torch.uint8, device="cuda:0")
+        x.fill_(1)
+        for _ in range(3):
+            x.clone()
+        torch.cuda.synchronize()
+        print("copy calibration: 3 copies of 268435456 bytes", flush=True)
+        return
     from spilltune_amd import ops, slots
     from spilltune_amd.dense import CausalMask
     from spilltune_amd.recompute import streaming_block
@@ -247,6 +258,14 @@ def main():
     log(f"step {ms:.3f} ms, fused q4 GEMMs {gemm_ms:.3f} ms/step; layer "
         f"{flops / (ms * 1e-3) / 1e12:.0f} TFLOP/s algorithmic")
 
+    # HBM traffic of the dominant kernel from the committed rocprofv3 counter runs
+    traffic = None
+    tpath = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "q4gemm_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as fh:
+            rec = json.load(fh)
+        if rec.get("kernel") == f"q4gemm_{key[0]} M={M} N={N} K={K}":
+            traffic = rec["traffic_bytes"]
     result = {
         "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
@@ -260,7 +279,7 @@ def main():
         "algorithmic_tflop_per_step": round(flops / 1e12, 4),
         "roofline": {"bound": "mfma", "kernel": f"q4gemm_{key[0]} M={M} N={N} K={K}",
                      "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
                      "avg_ms": round(info["avg_ms"], 4)},
         "cpu_baseline": None,
     }
