@@ -94,82 +94,145 @@ __global__ __launch_bounds__(NTH) void lora_reduce(int64_t Mo, int64_t No, int k
   out[m * ldo + n] = v;
 }
 
-// ---- fp32-MFMA path for the LoRA shapes: one bf16 operand G is large, the
-// other (S, fp32) has at most 64 columns.  out[m, j] = sum_k g(m,k) S[k, j]
-// with g(m,k) = G[m*ldg + k] (ROW: contraction contiguous, T = x A^T, dT = dY B)
-// or g(m,k) = G[k*ldg + m] (COL: contraction over G's rows, dB = dY^T T,
-// dA^T = x^T dT).  v_mfma_f32_32x32x2_f32 keeps fp32 products and sums.
-constexpr int RK_BM = 128, RK_BK = 32, RK_RP = 64;
+// ---- MFMA path for the LoRA shapes: one bf16 operand G is large, the other
+// (S, fp32) has at most 64 columns.  out[m, j] = sum_k g(m,k) S[k, j] with
+// g(m,k) = G[m*ldg + k] (ROW: contraction contiguous -- T = x A^T, dT = dY B) or
+// g(m,k) = G[k*ldg + m] (COL: contraction over G's rows -- dB = dY^T T,
+// dA^T = x^T dT).  S is split into hi = bf16(s) and lo = bf16(s - hi): bf16
+// products are exact in fp32, so g*hi + g*lo on v_mfma_f32_32x32x16_bf16 with
+// fp32 accumulation carries s to ~16 significant bits (relative error ~2^-17)
+// at bf16 matrix-core rate.
+constexpr int RK_BM = 128, RK_BK = 64, RK_RP = 64;
+constexpr int RK_LD = RK_BK + 8;  // bf16 per LDS row (144 bytes: 16-byte aligned, bank-spread)
 
+// Streaming pipeline: the next chunk's G (4 x 16 bytes per thread) and S are
+// loaded into registers before the current chunk's MFMAs, so each workgroup
+// keeps its loads in flight while it computes.
 template <bool COL>
 __global__ __launch_bounds__(NTH) void lora_rk(int64_t Mo, int64_t R, int64_t Kc,
                                               const uint16_t* __restrict__ G, int64_t ldg,
                                               const float* __restrict__ S, int64_t ssk,
                                               int64_t ssj, int64_t klen, int vec,
                                               float* __restrict__ part) {
-  __shared__ float Gs[RK_BK][RK_BM + 4];
-  __shared__ float Ss[RK_BK][RK_RP + 4];
+  __shared__ __attribute__((aligned(16))) uint16_t Gs[RK_BM * RK_LD];      // [m][k]
+  __shared__ __attribute__((aligned(16))) uint16_t Ss[2 * RK_RP * RK_LD];  // [hi|lo][j][k]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t m0 = (int64_t)blockIdx.x * RK_BM;
   const int64_t kb = (int64_t)blockIdx.y * klen;
   const int64_t ke = kb + klen < Kc ? kb + klen : Kc;
   const int nb = R > 32 ? 2 : 1;
+  const int RP = nb * 32;              // staged S columns
+  const int SIT = RK_BK * RP / NTH;    // S values per thread per chunk (8 or 16)
   f32x16 acc[2];
 #pragma unroll
   for (int c = 0; c < 2; ++c)
 #pragma unroll
     for (int v = 0; v < 16; ++v) acc[c][v] = 0.0f;
-  for (int64_t k0 = kb; k0 < ke; k0 += RK_BK) {
-    if (!COL) {  // 128 rows x 32 contraction: 16 consecutive k per thread
-      const int row = tid >> 1, kk = (tid & 1) * 16;
-      const int64_t m = m0 + row, k = k0 + kk;
-      float v[16];
-      if (vec && m < Mo && k + 16 <= ke) {
-        const uint4* src = (const uint4*)(G + m * ldg + k);
-        uint4 q0 = src[0], q1 = src[1];
-        uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+
+  uint4 gr[4];
+  float sr[16];
+  auto load = [&](int64_t k0) {
+    if (!COL) {  // 128 rows x 64 contraction: 8 chunks of 8 per row, 4 chunks per thread
 #pragma unroll
-        for (int i = 0; i < 16; ++i) v[i] = st::bf16_to_f32((uint16_t)(w[i >> 1] >> (16 * (i & 1))));
-      } else {
+      for (int i = 0; i < 4; ++i) {
+        const int id = tid + i * NTH, row = id >> 3, c = id & 7;
+        const int64_t m = m0 + row, k = k0 + c * 8;
+        if (vec && m < Mo && k + 8 <= ke) {
+          gr[i] = *(const uint4*)(G + m * ldg + k);
+        } else {
+          uint32_t w[4];
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
-          v[i] = (m < Mo && k + i < ke) ? st::bf16_to_f32(G[m * ldg + k + i]) : 0.0f;
+          for (int e = 0; e < 4; ++e) {
+            uint32_t lo = (m < Mo && k + 2 * e < ke) ? G[m * ldg + k + 2 * e] : 0u;
+            uint32_t hi = (m < Mo && k + 2 * e + 1 < ke) ? G[m * ldg + k + 2 * e + 1] : 0u;
+            w[e] = lo | (hi << 16);
+          }
+          gr[i] = make_uint4(w[0], w[1], w[2], w[3]);
+        }
       }
+    } else {  // 64 contraction rows x 128 columns: 4 rows x 8 columns per thread
+      const int kg = tid >> 4, mg = tid & 15;
+      const int64_t m = m0 + mg * 8;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) Gs[kk + i][row] = v[i];
-    } else {  // 32 contraction rows x 128 output columns: 16 consecutive m per thread
-      const int kr = tid >> 3, mc = (tid & 7) * 16;
-      const int64_t k = k0 + kr, m = m0 + mc;
-      float v[16];
-      if (vec && k < ke && m + 16 <= Mo) {
-        const uint4* src = (const uint4*)(G + k * ldg + m);
-        uint4 q0 = src[0], q1 = src[1];
-        uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+      for (int h = 0; h < 4; ++h) {
+        const int64_t k = k0 + kg * 4 + h;
+        if (vec && k < ke && m + 8 <= Mo) {
+          gr[h] = *(const uint4*)(G + k * ldg + m);
+        } else {
+          uint32_t w[4];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) v[i] = st::bf16_to_f32((uint16_t)(w[i >> 1] >> (16 * (i & 1))));
-      } else {
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-          v[i] = (k < ke && m + i < Mo) ? st::bf16_to_f32(G[k * ldg + m + i]) : 0.0f;
+          for (int e = 0; e < 4; ++e) {
+            uint32_t lo = (k < ke && m + 2 * e < Mo) ? G[k * ldg + m + 2 * e] : 0u;
+            uint32_t hi = (k < ke && m + 2 * e + 1 < Mo) ? G[k * ldg + m + 2 * e + 1] : 0u;
+            w[e] = lo | (hi << 16);
+          }
+          gr[h] = make_uint4(w[0], w[1], w[2], w[3]);
+        }
       }
-#pragma unroll
-      for (int i = 0; i < 16; i += 4)
-        *(float4*)&Gs[kr][mc + i] = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
     }
-    for (int e = tid; e < RK_BK * RK_RP; e += NTH) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (i >= SIT) break;
+      const int e = tid + i * NTH;
       int kk, j;
-      if (ssk == 1) { kk = e % RK_BK; j = e / RK_BK; } else { j = e % RK_RP; kk = e / RK_RP; }
+      if (ssk == 1) { kk = e % RK_BK; j = e / RK_BK; } else { j = e % RP; kk = e / RP; }
       const int64_t k = k0 + kk;
-      Ss[kk][j] = (k < ke && j < R) ? S[k * ssk + j * ssj] : 0.0f;
+      sr[i] = (k < ke && j < R) ? S[k * ssk + j * ssj] : 0.0f;
     }
+  };
+  auto store = [&]() {
+    if (!COL) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int id = tid + i * NTH, row = id >> 3, c = id & 7;
+        *(uint4*)&Gs[row * RK_LD + c * 8] = gr[i];
+      }
+    } else {
+      const int kg = tid >> 4, mg = tid & 15;
+      const uint32_t r0[4] = {gr[0].x, gr[0].y, gr[0].z, gr[0].w};
+      const uint32_t r1[4] = {gr[1].x, gr[1].y, gr[1].z, gr[1].w};
+      const uint32_t r2[4] = {gr[2].x, gr[2].y, gr[2].z, gr[2].w};
+      const uint32_t r3[4] = {gr[3].x, gr[3].y, gr[3].z, gr[3].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        // column m+e: rows (k, k+1) and (k+2, k+3) as two bf16 pairs
+        const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+        const uint32_t p01 = __builtin_amdgcn_perm(r1[e >> 1], r0[e >> 1], sel);
+        const uint32_t p23 = __builtin_amdgcn_perm(r3[e >> 1], r2[e >> 1], sel);
+        *(uint2*)&Gs[(mg * 8 + e) * RK_LD + kg * 4] = make_uint2(p01, p23);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (i >= SIT) break;
+      const int e = tid + i * NTH;
+      int kk, j;
+      if (ssk == 1) { kk = e % RK_BK; j = e / RK_BK; } else { j = e % RP; kk = e / RP; }
+      const uint16_t hb = st::f32_to_bf16(sr[i]);
+      const uint16_t lb = st::f32_to_bf16(sr[i] - st::bf16_to_f32(hb));
+      Ss[j * RK_LD + kk] = hb;
+      Ss[(RK_RP + j) * RK_LD + kk] = lb;
+    }
+  };
+
+  if (kb < ke) load(kb);
+  for (int64_t k0 = kb; k0 < ke; k0 += RK_BK) {
+    store();
     __syncthreads();
-#pragma unroll 4
-    for (int kk = 0; kk < RK_BK; kk += 2) {
-      const float a = Gs[kk + (lane >> 5)][wave * 32 + (lane & 31)];
-      acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, Ss[kk + (lane >> 5)][lane & 31], acc[0], 0, 0, 0);
-      if (nb > 1)
-        acc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, Ss[kk + (lane >> 5)][32 + (lane & 31)],
-                                                      acc[1], 0, 0, 0);
+    if (k0 + RK_BK < ke) load(k0 + RK_BK);
+#pragma unroll
+    for (int s = 0; s < RK_BK / 16; ++s) {
+      const int ko = s * 16 + (lane >> 5) * 8;
+      const bf16x8 a = *(const bf16x8*)&Gs[(wave * 32 + (lane & 31)) * RK_LD + ko];
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        if (c >= nb) break;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const bf16x8 b = *(const bf16x8*)&Ss[(h * RK_RP + c * 32 + (lane & 31)) * RK_LD + ko];
+          acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[c], 0, 0, 0);
+        }
+      }
     }
     __syncthreads();
   }
@@ -201,9 +264,10 @@ __global__ __launch_bounds__(NTH) void lora_rk_reduce(int64_t Mo, int64_t R, int
 }
 
 int rk_ksplit(int64_t Mo, int64_t Kc) {
+  // ~512 workgroups, each streaming at least 512 contraction elements (8 chunks)
   int64_t tiles = st::cdiv(Mo, RK_BM);
-  int64_t ks = st::cdiv(768, tiles);
-  int64_t maxk = st::cdiv(Kc, 128);
+  int64_t ks = st::cdiv(512, tiles);
+  int64_t maxk = st::cdiv(Kc, 512);
   if (ks > maxk) ks = maxk;
   if (ks < 1) ks = 1;
   return (int)ks;

@@ -241,19 +241,24 @@ class _Q4LoRALinear(torch.autograd.Function):
             nseg = len(weight.segments)
             dT = torch.empty((M, nseg * rank), dtype=_F32, device=dev)
             off = 0
+            dBs = []
             for s, width in enumerate(weight.segments):
                 dys = dy[:, off:off + width]
                 Bs = B_cat[off:off + width]
                 Ts = T[:, s * rank:(s + 1) * rank]
                 dTs = dT[:, s * rank:(s + 1) * rank]
-                # dT_s = s * dY_s B_s ;  dB_s = s * dY_s^T T_s ;  dA_s = dT_s^T x
+                # dT_s = s * dY_s B_s ;  dB_s = s * dY_s^T T_s
                 lora_gemm(M, rank, width, dys, N, 1, Bs, rank, 1, scale, dTs)
                 dB = torch.empty((width, rank), dtype=_F32, device=dev)
                 lora_gemm(width, rank, M, dys, 1, N, Ts, T.stride(0), 1, scale, dB)
-                dA = torch.empty((rank, K), dtype=_F32, device=dev)
-                lora_gemm(rank, K, M, dTs, 1, dT.stride(0), x, K, 1, 1.0, dA)
-                grads_ab += [dA, dB]
+                dBs.append(dB)
                 off += width
+            # dA_cat = dT_cat^T x for every segment in one product
+            R = nseg * rank
+            dA_cat = torch.empty((R, K), dtype=_F32, device=dev)
+            lora_gemm(R, K, M, dT, 1, R, x, K, 1, 1.0, dA_cat)
+            for s in range(nseg):
+                grads_ab += [dA_cat[s * rank:(s + 1) * rank], dBs[s]]
         else:
             (x,) = ctx.saved_tensors
         dx = torch.empty((M, K), dtype=_BF16, device=dev)
