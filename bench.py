@@ -32,6 +32,9 @@ CONFIGS = {
     "tiny": dict(H=256, I=688, heads=4, kv=4, D=64, eps=1e-5, r=8, alpha=16.0, B=2, S=128,
                  theta=500000.0),
 }
+# Qwen3-MoE-30B-A3B-shape MoE feed-forward
+MOE = dict(H=2048, I=768, E=128, k=8, T=4096, r=8, alpha=16.0, norm=True)
+MOE_METRIC = "train tokens/s per MoE layer fwd+bwd (Qwen3-MoE-30B-A3B shape, NF4 experts)"
 PROJ = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
         "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj")
 
@@ -158,12 +161,134 @@ def streamed(c, block, args, X, dY, rot, mask):
     return out
 
 
+def moe_bench(args):
+    """Config 4: the MoE feed-forward forward + backward on 4096 tokens
+    (router, permutation, grouped 4-bit gate|up and down GEMMs with per-expert
+    LoRA r=8, combine; the VJP through all of them)."""
+    import torch
+    from spilltune_amd import moe, ops
+    c = MOE
+    H, I, E, k, T, r = c["H"], c["I"], c["E"], c["k"], c["T"], c["r"]
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(1234)
+    log(f"building MoE layer: {E} experts of [2x{I}, {H}] + [{H}, {I}], nf4-g128")
+    router = (torch.randn(E, H, generator=g) * H ** -0.5).to(torch.bfloat16)  # logits ~ N(0,1)
+    gate_up = moe.quantize_experts(torch.randn(E, 2 * I, H, generator=g) * 0.02, "nf4-g128", dev)
+    down = moe.quantize_experts(torch.randn(E, H, I, generator=g) * 0.02, "nf4-g128", dev)
+    ga = torch.Generator().manual_seed(3)
+    lgu = moe.make_expert_lora("mlp.experts.gate_up_proj", E, H, 2 * I, rank=r, alpha=c["alpha"],
+                               device=dev, segments=2, generator=ga, b_std=0.02)
+    ld = moe.make_expert_lora("mlp.experts.down_proj", E, I, H, rank=r, alpha=c["alpha"],
+                              device=dev, generator=ga, b_std=0.02)
+    weights = {"mlp.gate.weight": router.to(dev), "mlp.experts.gate_up_proj": gate_up,
+               "mlp.experts.down_proj": down}
+    X = torch.randn(T, H, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16).to(dev)
+    dY = torch.randn(T, H, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).to(dev)
+
+    def step():
+        x = X.detach().requires_grad_(True)
+        out = moe.moe_feed_forward(x, weights, num_experts=E, top_k=k, norm_topk_prob=c["norm"],
+                                   lora_gate_up=lgu, lora_down=ld)
+        out.backward(dY)
+        lgu.A.grad = lgu.B.grad = ld.A.grad = ld.B.grad = None
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    ops.TIMER = ops.KernelTimer()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    timer, ops.TIMER = ops.TIMER, None
+    ms = elapsed * 1e3 / args.steps
+    R = T * k
+    flops = 2 * 2.0 * R * (2 * I * H + H * I) + 2 * 2.0 * T * H * E \
+        + 4 * 2.0 * R * r * ((H + 2 * I) + (I + H))
+    kern = timer.summary()
+    key, info = max(kern.items(), key=lambda kv: kv[1]["launches"] * kv[1]["avg_ms"])
+    _, M, N, K = key
+    achieved = 2.0 * M * N * K / (info["avg_ms"] * 1e-3) / 1e12
+    for k2, v2 in sorted(kern.items(), key=lambda kv: -kv[1]["launches"] * kv[1]["avg_ms"]):
+        tf = 2.0 * k2[1] * k2[2] * k2[3] / (v2["avg_ms"] * 1e-3) / 1e12
+        log(f"  grouped {k2[0]:9s} rows={k2[1]} N={k2[2]} K={k2[3]}: {v2['launches']} launches, "
+            f"{v2['avg_ms']:.3f} ms avg, {tf:.0f} TFLOP/s ({tf / PEAK_BF16_TFLOPS:.1%})")
+    log(f"step {ms:.3f} ms; {flops / (ms * 1e-3) / 1e12:.0f} TFLOP/s algorithmic")
+    result = {
+        "metric": MOE_METRIC, "value": round(T * args.steps / elapsed, 1), "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,0.02) experts -> nf4-g128, router logits ~N(0,1), "
+                "N(0,1) activations/grads)",
+        "config": {"workload": f"moe: Qwen3-MoE-30B-A3B-shape MoE feed-forward fwd+bwd, {T} "
+                               f"tokens, {E} experts top-{k}, nf4-g128, per-expert LoRA r={r}",
+                   "global_batch": 1, "seq_len": T, "hidden": H, "intermediate": I,
+                   "experts": E, "top_k": k, "parallelism": "single GPU"},
+        "layer_mfma_frac": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "algorithmic_tflop_per_step": round(flops / 1e12, 4),
+        "roofline": {"bound": "mfma", "kernel": f"q4grouped_{key[0]} rows={M} N={N} K={K}",
+                     "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None, "avg_ms": round(info["avg_ms"], 4)},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        log(f"timing the CPU path at {args.cpu_tokens} tokens")
+        result["cpu_baseline"] = moe_cpu_baseline(router, gate_up, down, lgu, ld, args.cpu_tokens)
+    print(json.dumps(result), flush=True)
+
+
+def moe_cpu_baseline(router, gate_up, down, lgu, ld, tokens, min_seconds=10.0):
+    """The reference's MoE feed-forward (qwen3_moe.py:95-113, per-expert LoRA)
+    restated in oracle/moe.py, forward + backward on the CPU for `tokens` tokens."""
+    import numpy as np
+    import torch
+    from oracle import codec as oc
+    from oracle import moe as OM
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    c = MOE
+
+    def decode(q):
+        bits = oc.decode4(q.payload.cpu().numpy(), q.scales.cpu().numpy(),
+                          q.experts * q.out_features * q.in_features, lut=oc.NF4_LUT)
+        return torch.from_numpy(bits.astype(np.int16)).view(torch.bfloat16).view(
+            q.experts, q.out_features, q.in_features)
+
+    Wgu, Wd = decode(gate_up), decode(down)
+    r, I = c["r"], c["I"]
+    A_gu = lgu.A.detach().cpu().requires_grad_(True)
+    B_gu = lgu.B.detach().cpu().requires_grad_(True)
+    A_d = ld.A.detach().cpu().requires_grad_(True)
+    B_d = ld.B.detach().cpu().requires_grad_(True)
+    loras = {"gate": (A_gu[:, :r], B_gu[:, :I], lgu.scale), "up": (A_gu[:, r:], B_gu[:, I:], lgu.scale),
+             "down": (A_d, B_d, ld.scale)}
+    x0 = torch.randn(tokens, c["H"], generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
+    dy = torch.randn(tokens, c["H"], generator=torch.Generator().manual_seed(2)).to(torch.bfloat16)
+    rc = router.cpu()
+    steps = 0
+    t0 = time.perf_counter()
+    while True:
+        x = x0.clone().requires_grad_(True)
+        out = OM.qwen3_moe_ffn(x, rc, Wgu, Wd, top_k=c["k"], norm_topk_prob=c["norm"], loras=loras)
+        out.backward(dy)
+        steps += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_seconds or steps >= 64:
+            break
+    return {"value": tokens * steps / dt, "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"{steps} MoE feed-forward fwd+bwd steps at {tokens} tokens of the same "
+                      f"layer, oracle/moe.py on {cores} host cores, {dt:.1f} s"}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="llama8b", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="llama8b", choices=sorted(CONFIGS) + ["moe"])
     ap.add_argument("--cpu-tokens", type=int, default=2048)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -186,6 +311,9 @@ def main():
             x.clone()
         torch.cuda.synchronize()
         print("copy calibration: 3 copies of 268435456 bytes", flush=True)
+        return
+    if args.config == "moe":
+        moe_bench(args)
         return
     from spilltune_amd import ops, slots
     from spilltune_amd.dense import CausalMask

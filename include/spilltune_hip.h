@@ -183,6 +183,109 @@ int st_softmax_causal_bwd(const uint16_t* s, const float* stats, const uint16_t*
                           int64_t nrows, int64_t S, float scale, uint16_t* ds,
                           st_stream_t stream);
 
+/* ---------------------------------------------------------------------
+ * Plain bf16 linear (router logits and their input gradient).
+ * y[M,N] = bf16(x[M,K] . w[N,K]^T);  dx[M,K] = bf16(dy[M,N] . w[N,K]).
+ * Replaces F.linear(flat, weights['mlp.gate.weight']) in
+ * adapters/qwen3_moe.py:97 and its autograd input gradient.
+ * Rows must be 16-byte aligned multiples of 8 elements.
+ * --------------------------------------------------------------------- */
+int st_linear_bf16_fwd(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const uint16_t* w,
+                       int64_t N, int64_t ldw, uint16_t* y, int64_t ldy, st_stream_t stream);
+int st_linear_bf16_dgrad(const uint16_t* dy, int64_t M, int64_t N, int64_t lddy,
+                         const uint16_t* w, int64_t K, int64_t ldw, uint16_t* dx, int64_t lddx,
+                         st_stream_t stream);
+
+/* ---------------------------------------------------------------------
+ * Mixture of experts (adapters/qwen3_moe.py:95-113; adapters/deepseek.py:
+ * 115-176).  Tokens T, picks per token k, experts E; a "pick" is (token t,
+ * slot j) at flat index t*k + j; permuted rows list the picks grouped by
+ * expert (ascending), inside an expert in ascending pick order.
+ * --------------------------------------------------------------------- */
+
+/* Softmax router, qwen3_moe.py:97-100: p = softmax_fp32(logits); top-k by
+ * value (descending; equal values -> lower expert, torch leaves tie order
+ * unspecified); if normalize, w /= sum(w); if round_bf16, w is rounded to
+ * bf16 (the reference's routing.to(logits.dtype)).  logits bf16 [T,E],
+ * E <= 512, k <= 32; weights fp32 [T,k], indices int32 [T,k]. */
+int st_moe_route_softmax(const uint16_t* logits, int64_t tokens, int32_t experts, int32_t top_k,
+                         int32_t normalize, int32_t round_bf16, float* weights, int32_t* indices,
+                         st_stream_t stream);
+/* VJP of the above w.r.t. logits for given picks: dweights fp32 [T,k]
+ * -> dlogits bf16 [T,E] (the autograd of topk/renormalise/softmax). */
+int st_moe_route_softmax_bwd(const uint16_t* logits, const int32_t* indices,
+                             const float* dweights, int64_t tokens, int32_t experts,
+                             int32_t top_k, int32_t normalize, uint16_t* dlogits,
+                             st_stream_t stream);
+/* Sigmoid group-limited router, deepseek.py:115-126 (fp32 logits [T,E],
+ * selection bias [E]); weights = scale * s / (sum s + 1e-20) when normalize. */
+int st_moe_route_sigmoid(const float* logits, const float* bias, int64_t tokens,
+                         int32_t experts, int32_t groups, int32_t group_k, int32_t top_k,
+                         int32_t normalize, float scale, float* weights, int32_t* indices,
+                         st_stream_t stream);
+/* VJP of the sigmoid router weights w.r.t. fp32 logits (selection: none). */
+int st_moe_route_sigmoid_bwd(const float* logits, const int32_t* indices, const float* dweights,
+                             int64_t tokens, int32_t experts, int32_t top_k, int32_t normalize,
+                             float scale, float* dlogits, st_stream_t stream);
+/* Token permutation, the one_hot/where of qwen3_moe.py:101-106:
+ * offsets int32 [E+1] (expert e owns rows [offsets[e], offsets[e+1])),
+ * row_token int32 [T*k] (token of each permuted row), pick_row int32 [T*k]
+ * (permuted row of each pick, -1 for an index outside [0, E)). E <= 1024. */
+int st_moe_permute(const int32_t* indices, int64_t tokens, int32_t top_k, int32_t experts,
+                   int32_t* offsets, int32_t* row_token, int32_t* pick_row, st_stream_t stream);
+/* Weighted combine, qwen3_moe.py:110-111: out[t] = bf16 running sum, in
+ * ascending expert order, of bf16(values[row] * w) over the token's picks
+ * (the roundings of index_add_ into a bf16 output).  values bf16 [rows,H],
+ * weights fp32 [T,k] (bf16-valued for Qwen3), out bf16 [T,H]; H % 8 == 0. */
+int st_moe_combine(const uint16_t* values, int64_t rows, const float* weights,
+                   const int32_t* indices, const int32_t* pick_row, int64_t tokens,
+                   int32_t top_k, int64_t hidden, uint16_t* out, st_stream_t stream);
+/* VJP of combine: dvalues[row] = bf16(dout[t] * w); dweights = sum_h
+ * dout * values (products and sum rounded to bf16 when bf16_weights). */
+int st_moe_combine_bwd(const uint16_t* dout, const uint16_t* values, int64_t rows,
+                       const float* weights, const int32_t* pick_row, int64_t tokens,
+                       int32_t top_k, int64_t hidden, int32_t bf16_weights, uint16_t* dvalues,
+                       float* dweights, st_stream_t stream);
+/* Input gradient of flat[tokens] over all experts: out[t] = bf16(sum_j
+ * rows_in[pick_row[t,j]] + extra[t]) with fp32 accumulation; extra (bf16 or
+ * fp32 [T,H], may be NULL) carries the router's input gradient. */
+int st_moe_gather_sum(const uint16_t* rows_in, int64_t rows, const int32_t* pick_row,
+                      int64_t tokens, int32_t top_k, int64_t hidden, const void* extra,
+                      int32_t extra_dtype, uint16_t* out, st_stream_t stream);
+/* Grouped 4-bit GEMMs (the per-expert F.linear calls of qwen3_moe.py:107-108
+ * with LoRAProjection.forward, finetune/lora.py:205-220, per expert).
+ * Expert e's weight is payload/scales block e ([N,K] each, K % 128 == 0,
+ * contiguous experts); permuted row r of x is x[gather[r]] (gather NULL:
+ * row r).  LoRA: t fp32 [rows, nseg*rank] in permuted order, lora_b fp32
+ * [E, N, rank] (segments stacked along N), lora_a fp32 [E, lora_k, K]. */
+int st_q4_grouped_fwd(const uint16_t* x, int64_t x_rows, int64_t ldx, const int32_t* gather,
+                      int64_t rows, int64_t K, const int32_t* offsets, int32_t groups,
+                      const uint8_t* payload, const float* scales, int64_t N,
+                      const float* lut16, int32_t flags, const float* t, int64_t ldt,
+                      const float* lora_b, int32_t rank, float lora_scale, int32_t nseg,
+                      const int64_t* seg_end, uint16_t* y, int64_t ldy, st_stream_t stream);
+int st_q4_grouped_dgrad(const uint16_t* dy, int64_t lddy, int64_t rows, int64_t N,
+                        const int32_t* offsets, int32_t groups, const uint8_t* payload,
+                        const float* scales, int64_t K, const float* lut16, int32_t flags,
+                        const float* dt, int64_t lddt, const float* lora_a, int32_t lora_k,
+                        uint16_t* dx, int64_t lddx, st_stream_t stream);
+/* Grouped low-rank products over permuted rows (per-expert LoRA), fp32 out.
+ * rows form: out[r, z*R + j] = alpha * sum_{k < seg_len} g[row(r), z*seg_len + k]
+ *            * s[e(r)*s_gstride + (z*seg_len + k)*ssk + j*ssj]
+ * grads form: out[e*o_gstride + (z*seg_len + m)*so_m + j*so_j] (+)= alpha *
+ *            sum_{r in e} g[row(r), z*seg_len + m] * s[r*ssk + (z*R + j)*ssj]
+ * for segments z < nseg, R <= 64; row(r) = gather[r] (NULL: r), bounded by
+ * g_rows.  The grads form writes every expert (zero rows -> 0). */
+int st_moe_lora_rows(int64_t rows, int32_t R, int64_t seg_len, int32_t nseg, const uint16_t* g,
+                     int64_t ldg, int64_t g_rows, const int32_t* gather, const float* s,
+                     int64_t ssk, int64_t ssj, int64_t s_gstride, const int32_t* offsets,
+                     int32_t groups, float alpha, float* out, int64_t ldo, st_stream_t stream);
+int st_moe_lora_grads(int64_t rows, int32_t R, int64_t seg_len, int32_t nseg,
+                      const uint16_t* g, int64_t ldg, int64_t g_rows, const int32_t* gather,
+                      const float* s, int64_t ssk, int64_t ssj, const int32_t* offsets,
+                      int32_t groups, float alpha, float* out, int64_t o_gstride, int64_t so_m,
+                      int64_t so_j, int32_t accumulate, st_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

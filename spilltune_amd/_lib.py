@@ -50,6 +50,25 @@ _SIGNATURES = {
     "st_swiglu_bwd": (_I32, [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P, _I64, _P]),
     "st_softmax_causal_fwd": (_I32, [_P, _I64, _I64, _F, _P, _P, _P]),
     "st_softmax_causal_bwd": (_I32, [_P, _P, _P, _I64, _I64, _F, _P, _P]),
+    "st_linear_bf16_fwd": (_I32, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _P]),
+    "st_linear_bf16_dgrad": (_I32, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _P]),
+    "st_moe_route_softmax": (_I32, [_P, _I64, _I32, _I32, _I32, _I32, _P, _P, _P]),
+    "st_moe_route_softmax_bwd": (_I32, [_P, _P, _P, _I64, _I32, _I32, _I32, _P, _P]),
+    "st_moe_route_sigmoid": (_I32, [_P, _P, _I64, _I32, _I32, _I32, _I32, _I32, _F, _P, _P,
+                                    _P]),
+    "st_moe_route_sigmoid_bwd": (_I32, [_P, _P, _P, _I64, _I32, _I32, _I32, _F, _P, _P]),
+    "st_moe_permute": (_I32, [_P, _I64, _I32, _I32, _P, _P, _P, _P]),
+    "st_moe_combine": (_I32, [_P, _I64, _P, _P, _P, _I64, _I32, _I64, _P, _P]),
+    "st_moe_combine_bwd": (_I32, [_P, _P, _I64, _P, _P, _I64, _I32, _I64, _I32, _P, _P, _P]),
+    "st_moe_gather_sum": (_I32, [_P, _I64, _P, _I64, _I32, _I64, _P, _I32, _P, _P]),
+    "st_q4_grouped_fwd": (_I32, [_P, _I64, _I64, _P, _I64, _I64, _P, _I32, _P, _P, _I64, _P,
+                                 _I32, _P, _I64, _P, _I32, _F, _I32, _P, _P, _I64, _P]),
+    "st_q4_grouped_dgrad": (_I32, [_P, _I64, _I64, _I64, _P, _I32, _P, _P, _I64, _P, _I32, _P,
+                                   _I64, _P, _I32, _P, _I64, _P]),
+    "st_moe_lora_rows": (_I32, [_I64, _I32, _I64, _I32, _P, _I64, _I64, _P, _P, _I64, _I64, _I64,
+                                _P, _I32, _F, _P, _I64, _P]),
+    "st_moe_lora_grads": (_I32, [_I64, _I32, _I64, _I32, _P, _I64, _I64, _P, _P, _I64, _I64, _P,
+                                 _I32, _F, _P, _I64, _I64, _I64, _I32, _P]),
 }
 
 EXPORTED = tuple(_SIGNATURES)

@@ -51,6 +51,48 @@ __device__ __forceinline__ int64_t xcd_remap(int64_t b, int64_t nb) {
   return (b % 8) * (nb / 8) + b / 8;
 }
 
+// Grouped (per-expert) row tiles: group g owns rows [off[g], off[g+1]) and
+// cdiv(rows_g, BM) tiles, numbered consecutively over the groups.  Maps tile
+// `slot` to its group, first row and the group's row end (clamped to `rows`).
+// Every lane of the calling wave gets the same answer; false when `slot` lies
+// beyond the last tile.  Offsets are read as given: rows outside [0, rows)
+// are clamped, so bad offsets cannot move a tile out of bounds.
+__device__ __forceinline__ bool find_group(const int32_t* off, int groups, int BM, int64_t slot,
+                                           int64_t rows, int& grp, int64_t& m0, int64_t& mend) {
+  const int lane = threadIdx.x & 63;
+  int64_t base = 0;
+  for (int c = 0; c < groups; c += 64) {
+    const int e = c + lane;
+    int start = 0, cnt = 0;
+    if (e < groups) {
+      start = off[e];
+      cnt = off[e + 1] - start;
+      if (cnt < 0) cnt = 0;
+    }
+    const int tiles = (cnt + BM - 1) / BM;
+    int inc = tiles;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int v = __shfl_up(inc, d);
+      if (lane >= d) inc += v;
+    }
+    const int exc = inc - tiles;
+    const bool hit = tiles > 0 && slot >= base + exc && slot < base + inc;
+    const unsigned long long b = __ballot(hit);
+    if (b) {
+      const int src = __ffsll((long long)b) - 1;
+      const int64_t s0 = __shfl(start, src), n0 = __shfl(cnt, src), x0 = __shfl(exc, src);
+      grp = c + src;
+      m0 = s0 + (slot - base - x0) * BM;
+      mend = s0 + n0 < rows ? s0 + n0 : rows;
+      if (m0 < 0) m0 = 0;
+      return true;
+    }
+    base += __shfl(inc, 63);
+  }
+  return false;
+}
+
 }  // namespace st
 
 #define ST_CHECK_ARG(cond, ...)                           \

@@ -48,6 +48,12 @@ struct GemmParams {
   int nseg;
   int64_t seg_end[4];
   int64_t a_bytes, w_bytes, s_bytes;  // extents of A, W (payload or bf16), scales
+  // grouped (per-expert) GEMM: rows of group g are [goff[g], goff[g+1]) and use
+  // W/scales/LoRA operand g (strides below); A row r reads source row gather[r]
+  const int32_t* gather;  // nullptr: row r
+  const int32_t* goff;    // nullptr: one group of M rows
+  int ngroups;
+  int64_t w_gstride, s_gstride, l_gstride;  // payload bytes (or bf16 elements), floats, floats
 };
 
 // LDS address of 16-byte chunk c (0..7) of tile row `row` (row = 64 bf16).
@@ -146,7 +152,12 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
   const int wm = wave / TL::WAVES_N, wn = wave % TL::WAVES_N;
   const int64_t tiles_p = st::cdiv(p.P, BN);
   const int64_t t = st::xcd_remap(blockIdx.x, gridDim.x);
-  const int64_t m0 = (t / tiles_p) * BM, p0 = (t % tiles_p) * BN;
+  const int64_t p0 = (t % tiles_p) * BN;
+  int64_t m0 = (t / tiles_p) * BM, mend = p.M;
+  int grp = 0;
+  if (p.goff) {  // whole workgroup leaves together, before any barrier
+    if (!st::find_group(p.goff, p.ngroups, BM, t / tiles_p, p.M, grp, m0, mend)) return;
+  }
   const int KT = (int)st::cdiv(p.Q, BK);
 
   // buffer b: A tile at lds + b*(BM+BN)*8, B tile right after it
@@ -156,8 +167,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
   // ---- buffer resources: out-of-range loads return zero, so the main loop
   // needs no bounds branches (rows beyond M/P and the contraction tail).
   const auto rsA = make_rsrc(p.A, p.a_bytes);
-  const auto rsW = make_rsrc(TL::Q4 ? (const void*)p.Wq : (const void*)p.Wb, p.w_bytes);
-  const auto rsS = make_rsrc(p.Ws, p.s_bytes);
+  const auto rsW = make_rsrc(TL::Q4 ? (const void*)(p.Wq + grp * p.w_gstride)
+                                     : (const void*)(p.Wb + grp * p.w_gstride), p.w_bytes);
+  const auto rsS = make_rsrc(p.Ws + grp * p.s_gstride, p.s_bytes);
+  const float* Lg = p.L + grp * p.l_gstride;
 
   // A (activations / upstream gradient): 16-byte chunks, row-major, contraction contiguous
   uint32_t a_row[TL::A_IT];
@@ -166,7 +179,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
   for (int i = 0; i < TL::A_IT; ++i) {
     int id = tid + i * NT, row = id >> 3, c = id & 7;
     int64_t m = m0 + row;
-    a_row[i] = m < p.M ? (uint32_t)((m * p.lda + c * 8) * 2) : kOOB;
+    if (m < mend && p.gather) m = p.gather[m];
+    a_row[i] = (m0 + row < mend && m >= 0) ? (uint32_t)((m * p.lda + c * 8) * 2) : kOOB;
     a_k[i] = c * 8;
   }
   auto load_A = [&](int kt, uint4 (&xr)[TL::A_IT]) {
@@ -365,19 +379,19 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
     for (int e = tid; e < BM * p.lora_cols; e += NT) {
       int r = e / p.lora_cols, c = e % p.lora_cols;
       int64_t m = m0 + r;
-      Ts[r * tstride + c] = m < p.M ? p.T[m * p.ldt + c] : 0.0f;
+      Ts[r * tstride + c] = m < mend ? p.T[m * p.ldt + c] : 0.0f;
     }
     if (TL::DGRAD) {  // L = A_cat [lora_k, P]
       for (int e = tid; e < p.lora_k * BN; e += NT) {
         int r = e / BN, c = e % BN;
         int64_t pc = p0 + c;
-        Ls[r * lstride + c] = pc < p.P ? p.L[r * p.ldl + pc] : 0.0f;
+        Ls[r * lstride + c] = pc < p.P ? Lg[r * p.ldl + pc] : 0.0f;
       }
     } else {  // L = B_lora [P, rank]
       for (int e = tid; e < BN * p.lora_k; e += NT) {
         int r = e / p.lora_k, c = e % p.lora_k;
         int64_t pc = p0 + r;
-        Ls[r * lstride + c] = pc < p.P ? p.L[pc * p.ldl + c] : 0.0f;
+        Ls[r * lstride + c] = pc < p.P ? Lg[pc * p.ldl + c] : 0.0f;
       }
     }
     __syncthreads();
@@ -412,7 +426,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int64_t m = m0 + rl + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-        if (m < p.M && pcol < p.P) {
+        if (m < mend && pcol < p.P) {
           float y = st::bf16r(acc[i][j][v]);
           if (lora) {
             if (TL::DGRAD)
@@ -609,4 +623,155 @@ extern "C" int st_q4_linear_dgrad(const uint16_t* dy, int64_t M, int64_t N, int6
   p.Wb = (const uint16_t*)workspace; p.ldw = K;
   p.w_bytes = N * K * 2; p.s_bytes = 0;
   return run_gemm(DGRAD_BF16, p, s);
+}
+
+// ---------------------------------------------------------------- grouped (MoE)
+namespace {
+// tiles of a grouped launch: sum_g cdiv(rows_g, BM) <= cdiv(rows, BM) + groups
+template <int MODE>
+int launch_grouped(const GemmParams& p, hipStream_t stream) {
+  constexpr int BM = 128, BN = 128, WAVES = 4;
+  if (p.T) {
+    using TL = Tile<MODE, BM, BN, WAVES>;
+    int64_t need = (int64_t)BM * (p.lora_cols + 1) +
+                   (TL::DGRAD ? (int64_t)p.lora_k * BN : (int64_t)BN * (p.lora_k + 1));
+    if (need > (int64_t)TL::LDS_CHUNKS * 4)
+      return st::fail(ST_EUNSUPPORTED, "q4 grouped: LoRA epilogue (%d columns) exceeds tile LDS",
+                      p.lora_cols);
+  }
+  int64_t tiles = (st::cdiv(p.M, BM) + p.ngroups) * st::cdiv(p.P, BN);
+  if (tiles > 0x7fffffff) return st::fail(ST_EUNSUPPORTED, "q4 grouped: too many tiles");
+  gemm_kernel<MODE, BM, BN, WAVES><<<(unsigned)tiles, 64 * WAVES, 0, stream>>>(p);
+  return st::check_launch("q4 grouped gemm");
+}
+}  // namespace
+
+extern "C" int st_q4_grouped_fwd(const uint16_t* x, int64_t x_rows, int64_t ldx,
+                                 const int32_t* gather, int64_t rows, int64_t K,
+                                 const int32_t* offsets, int32_t groups, const uint8_t* payload,
+                                 const float* scales, int64_t N, const float* lut16, int32_t flags,
+                                 const float* t, int64_t ldt, const float* lora_b, int32_t rank,
+                                 float lora_scale, int32_t nseg, const int64_t* seg_end,
+                                 uint16_t* y, int64_t ldy, st_stream_t stream) {
+  ST_CHECK_ARG(rows >= 0 && N > 0 && K > 0 && groups > 0 && x_rows >= 0,
+               "st_q4_grouped_fwd: bad shape");
+  if (rows == 0) return ST_OK;
+  ST_CHECK_ARG(x && offsets && payload && scales && y && lut16, "st_q4_grouped_fwd: NULL pointer");
+  ST_CHECK_ARG(K % 128 == 0, "st_q4_grouped_fwd: K must be a multiple of 128, got %lld",
+               (long long)K);
+  ST_CHECK_ARG(ldx % 8 == 0 && ldx >= K && al16(x) && al16(payload),
+               "st_q4_grouped_fwd: x rows / payload must be 16-byte aligned");
+  ST_CHECK_ARG(gather || x_rows >= rows, "st_q4_grouped_fwd: x_rows < rows without gather");
+  ST_CHECK_ARG(ldy >= N, "st_q4_grouped_fwd: ldy < N");
+  GemmParams p{};
+  p.A = x; p.lda = ldx; p.M = rows; p.P = N; p.Q = K;
+  p.C = y; p.ldc = ldy;
+  p.hi_first = (flags & ST_FLAG_HI_NIBBLE_FIRST) ? 1 : 0;
+  for (int i = 0; i < 16; ++i) p.lut.v[i] = lut16[i];
+  if (t) {
+    ST_CHECK_ARG(lora_b != nullptr, "st_q4_grouped_fwd: t without lora_b");
+    ST_CHECK_ARG(nseg >= 1 && nseg <= 4 && seg_end, "st_q4_grouped_fwd: nseg must be 1..4");
+    int rc = check_lora_common(rank, (int64_t)rank * nseg);
+    if (rc) return rc;
+    int64_t prev = 0;
+    for (int i = 0; i < nseg; ++i) {
+      ST_CHECK_ARG(seg_end[i] > prev && (seg_end[i] % 32 == 0 || seg_end[i] == N),
+                   "st_q4_grouped_fwd: segment ends must increase and be multiples of 32");
+      prev = seg_end[i];
+      p.seg_end[i] = seg_end[i];
+    }
+    ST_CHECK_ARG(prev == N, "st_q4_grouped_fwd: last segment end must equal N");
+    ST_CHECK_ARG(ldt >= (int64_t)rank * nseg, "st_q4_grouped_fwd: ldt too small");
+    p.T = t; p.ldt = ldt; p.L = lora_b; p.ldl = rank; p.lora_k = rank;
+    p.lora_cols = rank * nseg; p.lora_scale = lora_scale; p.nseg = nseg;
+    p.l_gstride = N * rank;
+  }
+  p.a_bytes = ((x_rows - 1) * ldx + K) * 2;
+  ST_CHECK_ARG(x_rows > 0 && p.a_bytes < (1ll << 31) && N * K * 2 < (1ll << 31),
+               "st_q4_grouped_fwd: operands above 2 GiB are not supported");
+  p.gather = gather; p.goff = offsets; p.ngroups = groups;
+  p.Wq = payload; p.Ws = scales; p.ldw = K;
+  p.w_bytes = N * K / 2; p.s_bytes = N * K / 128 * 4;
+  p.w_gstride = N * K / 2; p.s_gstride = N * K / 128;
+  return launch_grouped<FWD_Q4>(p, (hipStream_t)stream);
+}
+
+extern "C" int st_q4_grouped_dgrad(const uint16_t* dy, int64_t lddy, int64_t rows, int64_t N,
+                                   const int32_t* offsets, int32_t groups, const uint8_t* payload,
+                                   const float* scales, int64_t K, const float* lut16,
+                                   int32_t flags, const float* dt, int64_t lddt,
+                                   const float* lora_a, int32_t lora_k, uint16_t* dx,
+                                   int64_t lddx, st_stream_t stream) {
+  ST_CHECK_ARG(rows >= 0 && N > 0 && K > 0 && groups > 0, "st_q4_grouped_dgrad: bad shape");
+  if (rows == 0) return ST_OK;
+  ST_CHECK_ARG(dy && offsets && payload && scales && dx && lut16,
+               "st_q4_grouped_dgrad: NULL pointer");
+  ST_CHECK_ARG(K % 128 == 0, "st_q4_grouped_dgrad: K must be a multiple of 128");
+  ST_CHECK_ARG(N % 8 == 0, "st_q4_grouped_dgrad: N (contraction) must be a multiple of 8");
+  ST_CHECK_ARG(lddy % 8 == 0 && lddy >= N && al16(dy), "st_q4_grouped_dgrad: dy rows not 16-byte");
+  ST_CHECK_ARG(((uintptr_t)payload & 3u) == 0, "st_q4_grouped_dgrad: payload not 4-byte aligned");
+  ST_CHECK_ARG(lddx >= K, "st_q4_grouped_dgrad: lddx < K");
+  GemmParams p{};
+  p.A = dy; p.lda = lddy; p.M = rows; p.P = K; p.Q = N;
+  p.C = dx; p.ldc = lddx;
+  p.hi_first = (flags & ST_FLAG_HI_NIBBLE_FIRST) ? 1 : 0;
+  for (int i = 0; i < 16; ++i) p.lut.v[i] = lut16[i];
+  if (dt) {
+    ST_CHECK_ARG(lora_a != nullptr, "st_q4_grouped_dgrad: dt without lora_a");
+    int rc = check_lora_common(lora_k, lora_k);
+    if (rc) return rc;
+    ST_CHECK_ARG(lddt >= lora_k, "st_q4_grouped_dgrad: lddt too small");
+    p.T = dt; p.ldt = lddt; p.L = lora_a; p.ldl = K; p.lora_k = lora_k; p.lora_cols = lora_k;
+    p.lora_scale = 1.0f;
+    p.l_gstride = (int64_t)lora_k * K;
+  }
+  p.a_bytes = ((rows - 1) * lddy + N) * 2;
+  ST_CHECK_ARG(p.a_bytes < (1ll << 31) && N * K * 2 < (1ll << 31),
+               "st_q4_grouped_dgrad: operands above 2 GiB are not supported");
+  p.goff = offsets; p.ngroups = groups;
+  p.Wq = payload; p.Ws = scales; p.ldw = K;
+  p.w_bytes = N * K / 2; p.s_bytes = N * K / 128 * 4;
+  p.w_gstride = N * K / 2; p.s_gstride = N * K / 128;
+  return launch_grouped<DGRAD_Q4>(p, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------- plain bf16
+extern "C" int st_linear_bf16_fwd(const uint16_t* x, int64_t M, int64_t K, int64_t ldx,
+                                  const uint16_t* w, int64_t N, int64_t ldw, uint16_t* y,
+                                  int64_t ldy, st_stream_t stream) {
+  ST_CHECK_ARG(M >= 0 && N > 0 && K > 0, "st_linear_bf16_fwd: bad shape");
+  if (M == 0) return ST_OK;
+  ST_CHECK_ARG(x && w && y, "st_linear_bf16_fwd: NULL pointer");
+  ST_CHECK_ARG(K % 8 == 0 && ldx % 8 == 0 && ldw % 8 == 0 && ldx >= K && ldw >= K && al16(x) &&
+                   al16(w) && ldy >= N,
+               "st_linear_bf16_fwd: rows must be 16-byte aligned multiples of 8 elements");
+  GemmParams p{};
+  p.A = x; p.lda = ldx; p.M = M; p.P = N; p.Q = K;
+  p.C = y; p.ldc = ldy;
+  p.Wb = w; p.ldw = ldw;
+  p.a_bytes = ((M - 1) * ldx + K) * 2;
+  p.w_bytes = ((N - 1) * ldw + K) * 2;
+  ST_CHECK_ARG(p.a_bytes < (1ll << 31) && p.w_bytes < (1ll << 31),
+               "st_linear_bf16_fwd: operands above 2 GiB are not supported");
+  return launch<FWD_BF16, 128, 128, 4>(p, (hipStream_t)stream);
+}
+
+extern "C" int st_linear_bf16_dgrad(const uint16_t* dy, int64_t M, int64_t N, int64_t lddy,
+                                    const uint16_t* w, int64_t K, int64_t ldw, uint16_t* dx,
+                                    int64_t lddx, st_stream_t stream) {
+  ST_CHECK_ARG(M >= 0 && N > 0 && K > 0, "st_linear_bf16_dgrad: bad shape");
+  if (M == 0) return ST_OK;
+  ST_CHECK_ARG(dy && w && dx, "st_linear_bf16_dgrad: NULL pointer");
+  ST_CHECK_ARG(N % 8 == 0 && K % 8 == 0 && lddy % 8 == 0 && ldw % 8 == 0 && lddy >= N &&
+                   ldw >= K && al16(dy) && al16(w) && lddx >= K,
+               "st_linear_bf16_dgrad: rows must be 16-byte aligned multiples of 8 elements");
+  GemmParams p{};
+  p.A = dy; p.lda = lddy; p.M = M; p.P = K; p.Q = N;
+  p.C = dx; p.ldc = lddx;
+  p.Wb = w; p.ldw = ldw;
+  p.a_bytes = ((M - 1) * lddy + N) * 2;
+  p.w_bytes = ((N - 1) * ldw + K) * 2;
+  ST_CHECK_ARG(p.a_bytes < (1ll << 31) && p.w_bytes < (1ll << 31),
+               "st_linear_bf16_dgrad: operands above 2 GiB are not supported");
+  return launch<DGRAD_BF16, 128, 128, 4>(p, (hipStream_t)stream);
 }

@@ -1,0 +1,317 @@
+"""MoE HIP path vs the CPU oracle (oracle/moe.py), through the C ABI.
+
+Routers: the picks must be the oracle's lowest-index top-k exactly (ties in
+bf16 logits included) and the weights within a bf16 ulp.  Permutation and
+combine are integer/byte work: exact.  Grouped GEMMs: the oracle's bf16
+result up to fp32 summation order.  The whole feed-forward (forward and
+backward, with per-expert LoRA): outputs rel err <= 2e-2, gradients cosine
+>= 0.999, against the oracle's expert loop run on the GPU's picks."""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import moe as OM
+from spilltune_amd import _lib, moe
+
+pytestmark = pytest.mark.gpu
+BF = torch.bfloat16
+
+
+def _st(dev):
+    return _lib.stream_handle(dev)
+
+
+class _Held:
+    """Device copies kept alive until the test ends (a raw pointer does not
+    keep its tensor alive, and kernels run after the call returns)."""
+
+    def __init__(self, dev):
+        self.dev, self.items = dev, []
+
+    def __call__(self, t):
+        self.items.append(t.to(self.dev))
+        return _lib.ptr(self.items[-1])
+
+
+def _experts(oc, w: torch.Tensor, dev, fmt="nf4-g128"):
+    """Encode [E, N, K] with the oracle; return (Q4Experts, exact bf16 W)."""
+    E, N, K = w.shape
+    w32 = w.reshape(E * N, K).numpy().astype(np.float32)
+    enc = oc.encode_nf4 if fmt == "nf4-g128" else oc.encode_int4
+    payload, scales = enc(w32)
+    lut = oc.NF4_LUT if fmt == "nf4-g128" else oc.INT4_LUT
+    bits = np.asarray(oc.decode4(payload, scales, w32.size, lut=lut), dtype=np.uint16)
+    W = torch.from_numpy(bits.astype(np.int16)).view(BF).view(E, N, K)
+    q = moe.Q4Experts(torch.from_numpy(payload).to(dev), torch.from_numpy(scales).to(dev), E, N,
+                      K, fmt)
+    return q, W
+
+
+def _cos(a, b):
+    a, b = a.detach().double().flatten().cpu(), b.detach().double().flatten().cpu()
+    return float(a @ b / (a.norm() * b.norm()).clamp_min(1e-300))
+
+
+def _rel(a, b):
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return float((a - b).norm() / b.norm().clamp_min(1e-300))
+
+
+# ----------------------------------------------------------------- routers
+@pytest.mark.parametrize("T,E,k,norm", [(300, 128, 8, True), (77, 64, 2, False), (5, 512, 32, True),
+                                        (64, 16, 16, False)])
+def test_route_softmax_picks_and_weights(dev, T, E, k, norm):
+    g = torch.Generator().manual_seed(T + E + k)
+    H_ = _Held(dev)
+    logits = torch.randn(T, E, generator=g).to(BF)        # bf16: many exact ties
+    w = torch.empty(T, k, device=dev)
+    idx = torch.empty(T, k, dtype=torch.int32, device=dev)
+    _lib.call("st_moe_route_softmax", H_(logits), T, E, k, int(norm), 1,
+              _lib.ptr(w), _lib.ptr(idx), _st(dev))
+    torch.cuda.synchronize()
+    probs = F.softmax(logits.float(), dim=-1)
+    _, ref_idx = OM.topk_lowest_index(probs, k)
+    assert torch.equal(idx.cpu().long(), ref_idx)
+    ref = probs.gather(1, ref_idx)
+    if norm:
+        ref = ref / ref.sum(-1, keepdim=True)
+    ref = ref.to(BF).float()
+    assert ((w.cpu() - ref).abs() <= ref.abs() * 2 ** -7 + 1e-30).all()
+
+
+def test_route_softmax_bwd_matches_autograd(dev):
+    g = torch.Generator().manual_seed(2)
+    H_ = _Held(dev)
+    T, H, E, k = 96, 64, 32, 4
+    flat = torch.randn(T, H, generator=g).to(BF)
+    router = torch.randn(E, H, generator=g).to(BF)
+    logits = F.linear(flat, router)
+    for norm in (True, False):
+        _, idx = OM.topk_lowest_index(F.softmax(logits.float(), -1), k)
+        lg = logits.clone().requires_grad_(True)
+        probs = F.softmax(lg, dtype=torch.float32, dim=-1)
+        r = probs.gather(1, idx)
+        if norm:
+            r = r / r.sum(-1, keepdim=True)
+        r = r.to(BF)
+        dw = torch.randn(T, k, generator=g).to(BF)
+        (ref,) = torch.autograd.grad(r, lg, dw)
+        out = torch.empty(T, E, dtype=BF, device=dev)
+        _lib.call("st_moe_route_softmax_bwd", H_(logits),
+                  H_(idx.int()), H_(dw.float()), T, E, k, int(norm),
+                  _lib.ptr(out), _st(dev))
+        torch.cuda.synchronize()
+        assert _rel(out, ref) < 1e-2 and _cos(out, ref) > 0.9999
+
+
+@pytest.mark.parametrize("E,groups,group_k,k", [(256, 8, 4, 8), (64, 8, 3, 6), (32, 4, 2, 5)])
+def test_route_sigmoid_vs_oracle(dev, E, groups, group_k, k):
+    g = torch.Generator().manual_seed(E + k)
+    H_ = _Held(dev)
+    T, H = 200, 96
+    flat = torch.randn(T, H, generator=g).to(BF)
+    wr = torch.randn(E, H, generator=g).to(BF)
+    bias = torch.randn(E, generator=g) * 0.05
+    logits, wref, iref = OM.deepseek_route(flat, wr, bias, groups=groups, group_k=group_k,
+                                           top_k=k, normalize=True, scale=2.5)
+    w = torch.empty(T, k, device=dev)
+    idx = torch.empty(T, k, dtype=torch.int32, device=dev)
+    _lib.call("st_moe_route_sigmoid", H_(logits), H_(bias), T, E,
+              groups, group_k, k, 1, 2.5, _lib.ptr(w), _lib.ptr(idx), _st(dev))
+    torch.cuda.synchronize()
+    got = {(t, int(e)): float(v) for t in range(T) for e, v in zip(idx[t].cpu(), w[t].cpu())}
+    ref = {(t, int(e)): float(v) for t in range(T) for e, v in zip(iref[t], wref[t])}
+    assert got.keys() == ref.keys()
+    for key in ref:
+        assert got[key] == pytest.approx(ref[key], rel=2e-6, abs=1e-7)
+    # VJP w.r.t. the fp32 logits for the same picks
+    lg = logits.clone().requires_grad_(True)
+    wg = OM.deepseek_weights_given(lg, idx.cpu().long(), normalize=True, scale=2.5)
+    dw = torch.randn(T, k, generator=g)
+    (dref,) = torch.autograd.grad(wg, lg, dw)
+    dl = torch.empty(T, E, device=dev)
+    _lib.call("st_moe_route_sigmoid_bwd", H_(logits), _lib.ptr(idx), H_(dw),
+              T, E, k, 1, 2.5, _lib.ptr(dl), _st(dev))
+    torch.cuda.synchronize()
+    torch.testing.assert_close(dl.cpu(), dref, rtol=1e-5, atol=1e-6)
+
+
+# ----------------------------------------------------------------- permutation / combine
+@pytest.mark.parametrize("T,E,k", [(4096, 128, 8), (33, 7, 3), (1, 4, 4), (500, 256, 1)])
+def test_permute_exact(dev, T, E, k):
+    g = torch.Generator().manual_seed(T * k + E)
+    H_ = _Held(dev)
+    hot = max(k, 5)     # skewed load: a third of the tokens pick among the first experts only
+    idx = torch.stack([torch.randperm(hot if t < T // 3 else E, generator=g)[:k]
+                       for t in range(T)]).int()
+    offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    row_token = torch.empty(T * k, dtype=torch.int32, device=dev)
+    pick_row = torch.empty(T * k, dtype=torch.int32, device=dev)
+    _lib.call("st_moe_permute", H_(idx), T, k, E, _lib.ptr(offsets),
+              _lib.ptr(row_token), _lib.ptr(pick_row), _st(dev))
+    torch.cuda.synchronize()
+    flat = idx.flatten().long()
+    counts = torch.bincount(flat, minlength=E)
+    assert torch.equal(offsets.cpu().long(), torch.cat([torch.zeros(1, dtype=torch.long), counts.cumsum(0)]))
+    order = torch.argsort(flat * (T * k) + torch.arange(T * k), stable=True)   # by expert, then pick
+    assert torch.equal(row_token.cpu().long(), order // k)
+    inv = torch.empty_like(order)
+    inv[order] = torch.arange(T * k)
+    assert torch.equal(pick_row.cpu().long(), inv)
+
+
+def test_combine_bit_exact_and_vjp(dev):
+    g = torch.Generator().manual_seed(8)
+    H_ = _Held(dev)
+    T, E, k, H = 257, 16, 4, 264
+    idx = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)]).int()
+    R = T * k
+    v = torch.randn(R, H, generator=g).to(BF)
+    w = torch.rand(T, k, generator=g).to(BF).float()
+    offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    row_token = torch.empty(R, dtype=torch.int32, device=dev)
+    pick_row = torch.empty(R, dtype=torch.int32, device=dev)
+    _lib.call("st_moe_permute", H_(idx), T, k, E, _lib.ptr(offsets),
+              _lib.ptr(row_token), _lib.ptr(pick_row), _st(dev))
+    out = torch.empty(T, H, dtype=BF, device=dev)
+    vd, wd = v.to(dev), w.to(dev)
+    _lib.call("st_moe_combine", _lib.ptr(vd), R, _lib.ptr(wd), H_(idx),
+              _lib.ptr(pick_row), T, k, H, _lib.ptr(out), _st(dev))
+    torch.cuda.synchronize()
+    pr = pick_row.cpu().long().view(T, k)
+    # reference: the oracle's index_add_ loop over experts in ascending order
+    ref = torch.zeros(T, H, dtype=BF)
+    for e in range(E):
+        pos, tok = torch.where(idx.T.long() == e)
+        if tok.numel():
+            val = v[pr[tok, pos]] * w[tok, pos, None].to(BF)
+            ref.index_add_(0, tok, val)
+    assert torch.equal(out.cpu().view(torch.int16), ref.view(torch.int16))
+    # VJP (bf16 weights): autograd of the same expression
+    vr = v.clone().requires_grad_(True)
+    wr = w.to(BF).clone().requires_grad_(True)
+    acc = torch.zeros(T, H, dtype=BF)
+    for e in range(E):
+        pos, tok = torch.where(idx.T.long() == e)
+        if tok.numel():
+            acc = acc.index_add(0, tok, vr[pr[tok, pos]] * wr[tok, pos, None])
+    dout = torch.randn(T, H, generator=g).to(BF)
+    dv_ref, dw_ref = torch.autograd.grad(acc, (vr, wr), dout)
+    dv = torch.empty(R, H, dtype=BF, device=dev)
+    dw = torch.empty(T, k, device=dev)
+    _lib.call("st_moe_combine_bwd", H_(dout), _lib.ptr(vd), R, _lib.ptr(wd),
+              _lib.ptr(pick_row), T, k, H, 1, _lib.ptr(dv), _lib.ptr(dw), _st(dev))
+    torch.cuda.synchronize()
+    assert torch.equal(dv.cpu().view(torch.int16), dv_ref.view(torch.int16))
+    assert ((dw.cpu() - dw_ref.float()).abs() <= dw_ref.float().abs() * 2 ** -7 + 1e-3).all()
+    # gather-sum: input gradient of flat[tokens] over all picks plus an extra term
+    extra = torch.randn(T, H, generator=g).to(BF)
+    gs = torch.empty(T, H, dtype=BF, device=dev)
+    _lib.call("st_moe_gather_sum", _lib.ptr(dv), R, _lib.ptr(pick_row), T, k, H,
+              H_(extra), _lib.ST_DTYPE_BF16, _lib.ptr(gs), _st(dev))
+    torch.cuda.synchronize()
+    ref_gs = (dv.cpu().float()[pr].sum(1) + extra.float()).to(BF)
+    assert _rel(gs, ref_gs) < 4e-3
+
+
+# ----------------------------------------------------------------- grouped GEMMs
+@pytest.mark.parametrize("E,N,K,T,k", [(8, 256, 256, 100, 2), (16, 96, 384, 333, 4),
+                                       (32, 1536, 2048, 512, 8)])
+def test_grouped_fwd_and_dgrad_vs_oracle(dev, oracle_codec, E, N, K, T, k):
+    g = torch.Generator().manual_seed(E + N + K)
+    H_ = _Held(dev)
+    q, W = _experts(oracle_codec, torch.randn(E, N, K, generator=g) * 0.02, dev)
+    x = torch.randn(T, K, generator=g).to(BF)
+    idx = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)]).int()
+    R = T * k
+    offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    row_token = torch.empty(R, dtype=torch.int32, device=dev)
+    pick_row = torch.empty(R, dtype=torch.int32, device=dev)
+    _lib.call("st_moe_permute", H_(idx), T, k, E, _lib.ptr(offsets),
+              _lib.ptr(row_token), _lib.ptr(pick_row), _st(dev))
+    y = torch.empty(R, N, dtype=BF, device=dev)
+    _lib.call("st_q4_grouped_fwd", H_(x), T, K, _lib.ptr(row_token), R, K,
+              _lib.ptr(offsets), E, _lib.ptr(q.payload), _lib.ptr(q.scales), N, q.lut(), 0,
+              None, 0, None, 0, 1.0, 0, None, _lib.ptr(y), N, _st(dev))
+    dy = torch.randn(R, N, generator=g).to(BF)
+    dx = torch.empty(R, K, dtype=BF, device=dev)
+    _lib.call("st_q4_grouped_dgrad", H_(dy), N, R, N, _lib.ptr(offsets), E,
+              _lib.ptr(q.payload), _lib.ptr(q.scales), K, q.lut(), 0, None, 0, None, 0,
+              _lib.ptr(dx), K, _st(dev))
+    torch.cuda.synchronize()
+    off = offsets.cpu().long()
+    tok = row_token.cpu().long()
+    y_ref = torch.empty(R, N, dtype=BF)
+    dx_ref = torch.empty(R, K, dtype=BF)
+    for e in range(E):
+        a, b = int(off[e]), int(off[e + 1])
+        if b > a:
+            y_ref[a:b] = F.linear(x[tok[a:b]].float(), W[e].float()).to(BF)
+            dx_ref[a:b] = (dy[a:b].float() @ W[e].float()).to(BF)
+    for got, ref, what in ((y, y_ref, "fwd"), (dx, dx_ref, "dgrad")):
+        got, ref = got.float().cpu(), ref.float()
+        err = (got - ref).abs()
+        bad = (err > ref.abs() * 2 ** -7 + 1e-6).float().mean().item()
+        assert _rel(got, ref) < 4e-3 and bad < 1e-3, what
+
+
+# ----------------------------------------------------------------- whole feed-forward
+def _oracle_ffn(flat, router, Wgu, Wd, idx, norm, lora):
+    """Oracle forward + VJP on the GPU's picks; returns out and grads."""
+    x = flat.clone().requires_grad_(True)
+    _, routing = OM.qwen3_route_given(x, router, idx, norm_topk_prob=norm)
+    loras, leaves = None, []
+    if lora is not None:
+        A_gu, B_gu, A_d, B_d, r, s_gu, s_d = lora
+        leaves = [t.clone().requires_grad_(True) for t in (A_gu, B_gu, A_d, B_d)]
+        I = Wd.shape[2]
+        loras = {"gate": (leaves[0][:, :r], leaves[1][:, :I], s_gu),
+                 "up": (leaves[0][:, r:], leaves[1][:, I:], s_gu),
+                 "down": (leaves[2], leaves[3], s_d)}
+    out = OM.expert_loop(x, routing, idx, Wgu, Wd, num_experts=Wgu.shape[0], loras=loras)
+    return x, out, leaves
+
+
+@pytest.mark.parametrize("T,H,I,E,k,norm,use_lora", [
+    (64, 256, 128, 8, 2, True, True),
+    (203, 256, 256, 16, 4, False, True),
+    (96, 128, 128, 4, 4, True, False),
+    (256, 2048, 768, 64, 8, True, True),       # config 4 expert shapes, fewer experts/tokens
+])
+def test_moe_ffn_fwd_bwd_vs_oracle(dev, oracle_codec, T, H, I, E, k, norm, use_lora):
+    g = torch.Generator().manual_seed(T + H + I + E)
+    router = (torch.randn(E, H, generator=g) * H ** -0.5).to(BF)
+    qgu, Wgu = _experts(oracle_codec, torch.randn(E, 2 * I, H, generator=g) * 0.02, dev)
+    qd, Wd = _experts(oracle_codec, torch.randn(E, H, I, generator=g) * 0.02, dev)
+    flat = torch.randn(T, H, generator=g).to(BF)
+    r = 8
+    lgu = ld = None
+    if use_lora:
+        lgu = moe.make_expert_lora("mlp.experts.gate_up_proj", E, H, 2 * I, rank=r, alpha=16.0,
+                                   device=dev, segments=2, generator=g, b_std=0.02)
+        ld = moe.make_expert_lora("mlp.experts.down_proj", E, I, H, rank=r, alpha=16.0,
+                                  device=dev, generator=g, b_std=0.02)
+    weights = {"mlp.gate.weight": router.to(dev), "mlp.experts.gate_up_proj": qgu,
+               "mlp.experts.down_proj": qd}
+    xd = flat.to(dev).requires_grad_(True)
+    out, w, idx = moe.moe_feed_forward(xd, weights, num_experts=E, top_k=k, norm_topk_prob=norm,
+                                       lora_gate_up=lgu, lora_down=ld, return_routing=True)
+    dout = torch.randn(T, H, generator=g).to(BF)
+    out.backward(dout.to(dev))
+    torch.cuda.synchronize()
+    idx_c = idx.cpu().long()
+    _, ref_idx = OM.topk_lowest_index(F.softmax(F.linear(flat, router).float(), -1), k)
+    assert torch.equal(idx_c, ref_idx)
+    lora = None
+    if use_lora:
+        lora = (lgu.A.detach().cpu(), lgu.B.detach().cpu(), ld.A.detach().cpu(),
+                ld.B.detach().cpu(), r, lgu.scale, ld.scale)
+    x, ref, leaves = _oracle_ffn(flat, router, Wgu, Wd, idx_c, norm, lora)
+    ref.backward(dout)
+    assert _rel(out, ref) < 2e-2, "output"
+    assert _cos(xd.grad, x.grad) > 0.999, "input grad"
+    if use_lora:
+        for got, leaf, name in ((lgu.A.grad, leaves[0], "A_gu"), (lgu.B.grad, leaves[1], "B_gu"),
+                                (ld.A.grad, leaves[2], "A_d"), (ld.B.grad, leaves[3], "B_d")):
+            assert _cos(got, leaf.grad) > 0.999, name
