@@ -25,9 +25,12 @@
  *    (bnb.matmul_4bit)                                      -> st_q4_linear_fwd
  *  - the autograd VJP of the same projection inside training/recompute.py:
  *    102-105 (dX = dY W, dA, dB)           -> st_q4_linear_dgrad, st_lora_*
- *  - adapters/dense.py:115-117 rms, :137-141 rotate, :146-148 eager softmax,
- *    :153 silu(gate)*up                    -> st_rmsnorm_*, st_rope_*,
- *                                             st_softmax_causal_*, st_swiglu_*
+ *  - adapters/dense.py:115-117 rms, :137-141 rotate, :153 silu(gate)*up
+ *                                          -> st_rmsnorm_*, st_rope_*, st_swiglu_*
+ *  - adapters/dense.py:142-148 eager GQA attention -> st_flash_attn_*
+ *  - adapters/qwen3_moe.py:95-113 and adapters/deepseek.py:115-176 (routers
+ *    and the routed-expert loop)          -> st_moe_*, st_q4_grouped_*,
+ *                                             st_linear_bf16_*
  */
 #ifndef SPILLTUNE_HIP_H
 #define SPILLTUNE_HIP_H
@@ -167,21 +170,30 @@ int st_swiglu_bwd(const uint16_t* da, int64_t ldda, const uint16_t* g, int64_t l
                   const uint16_t* u, int64_t ldu, int64_t rows, int64_t I,
                   uint16_t* dg, int64_t lddg, uint16_t* du, int64_t lddu, st_stream_t stream);
 
-/*
- * Eager causal softmax of dense.py:146-147 over score rows [nrows, S] (row r
- * is query position r % S of its head): x = bf16(s * scale); p = bf16(softmax_fp32
- * over keys c <= r % S), 0 for c > r % S.  stats[r] = (max, sum) for the VJP.
- */
-int st_softmax_causal_fwd(const uint16_t* s, int64_t nrows, int64_t S, float scale,
-                          uint16_t* p, float* stats, st_stream_t stream);
-/*
- * VJP through softmax(dtype=fp32).to(bf16) and the scale multiply, using the
- * fp32 probabilities recomputed from s and stats:
- *   ds = bf16( bf16(p32 * (dp - sum_c dp_c p32_c)) * scale ).
- */
-int st_softmax_causal_bwd(const uint16_t* s, const float* stats, const uint16_t* dp,
-                          int64_t nrows, int64_t S, float scale, uint16_t* ds,
-                          st_stream_t stream);
+/* ---------------------------------------------------------------------
+ * Causal GQA flash attention, replacing the eager chain of
+ * adapters/dense.py:142-148 (repeat k/v over the group, scores = q k^T *
+ * scale + causal mask, fp32 softmax, probabilities @ v, relayout to tokens).
+ * q [B,H,S,D], k/v [B,Hkv,S,D] head-major bf16; D in {64, 128}; S % 8 == 0.
+ * out is token-major [B,S,H*D] bf16; lse [B,H,S] fp32 is the base-2
+ * log-sum-exp of scale*log2(e)*q.k per query (the backward's statistics).
+ * Probabilities are kept in fp32 until the bf16 P.V product (the reference
+ * rounds the normalised probabilities to bf16 first; within bf16 tolerance).
+ * --------------------------------------------------------------------- */
+int64_t st_flash_attn_workspace_bytes(int64_t B, int64_t S, int64_t H, int64_t Hkv, int64_t D,
+                                      int32_t backward);
+int st_flash_attn_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, int64_t B,
+                      int64_t S, int64_t H, int64_t Hkv, int64_t D, float scale, uint16_t* out,
+                      float* lse, void* workspace, int64_t workspace_bytes, st_stream_t stream);
+/* VJP of st_flash_attn_fwd (autograd of dense.py:142-148): from dout
+ * (token-major [B,S,H*D]), the forward's out and lse, writes dq [B,H,S,D]
+ * and dk, dv [B,Hkv,S,D] head-major bf16 (GQA group sums in fp32, one
+ * rounding).  Deterministic: no atomics. */
+int st_flash_attn_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                      const uint16_t* out, const float* lse, const uint16_t* dout, int64_t B,
+                      int64_t S, int64_t H, int64_t Hkv, int64_t D, float scale, uint16_t* dq,
+                      uint16_t* dk, uint16_t* dv, void* workspace, int64_t workspace_bytes,
+                      st_stream_t stream);
 
 /* ---------------------------------------------------------------------
  * Plain bf16 linear (router logits and their input gradient).

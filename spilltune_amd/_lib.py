@@ -48,8 +48,6 @@ _SIGNATURES = {
     "st_tokens_to_heads": (_I32, [_P, _I64, _I64, _I64, _I64, _P, _P]),
     "st_swiglu_fwd": (_I32, [_P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P]),
     "st_swiglu_bwd": (_I32, [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P, _I64, _P]),
-    "st_softmax_causal_fwd": (_I32, [_P, _I64, _I64, _F, _P, _P, _P]),
-    "st_softmax_causal_bwd": (_I32, [_P, _P, _P, _I64, _I64, _F, _P, _P]),
     "st_linear_bf16_fwd": (_I32, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _P]),
     "st_linear_bf16_dgrad": (_I32, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _P]),
     "st_moe_route_softmax": (_I32, [_P, _I64, _I32, _I32, _I32, _I32, _P, _P, _P]),
@@ -67,6 +65,11 @@ _SIGNATURES = {
                                    _I64, _P, _I32, _P, _I64, _P]),
     "st_moe_lora_rows": (_I32, [_I64, _I32, _I64, _I32, _P, _I64, _I64, _P, _P, _I64, _I64, _I64,
                                 _P, _I32, _F, _P, _I64, _P]),
+    "st_flash_attn_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64, _I32]),
+    "st_flash_attn_fwd": (_I32, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _P, _P, _P, _I64,
+                                 _P]),
+    "st_flash_attn_bwd": (_I32, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _P, _P,
+                                 _P, _P, _I64, _P]),
     "st_moe_lora_grads": (_I32, [_I64, _I32, _I64, _I32, _P, _I64, _I64, _P, _P, _I64, _I64, _P,
                                  _I32, _F, _P, _I64, _I64, _I64, _I32, _P]),
 }

@@ -1,5 +1,5 @@
 // Decoder-layer elementwise kernels (HBM-bound): RMSNorm, rotary embedding
-// with the head relayout, SwiGLU, and the eager causal softmax of attention.
+// with the head relayout and SwiGLU.
 //
 // Each forward reproduces the reference's bf16 rounding points
 // (adapters/dense.py:115-153); each backward reproduces the roundings that
@@ -182,176 +182,9 @@ __global__ __launch_bounds__(NTH) void swiglu_bwd(const uint16_t* __restrict__ d
   dg[r * lddg + c] = st::f32_to_bf16(ds * (sg * (1.0f + gv * (1.0f - sg))));
 }
 
-// ------------------------------------------------------------------ softmax
-// one wave per score row; rows are [nrows, S], query position = row % S
-__global__ __launch_bounds__(NTH) void softmax_causal_fwd(const uint16_t* __restrict__ s,
-                                                         int64_t nrows, int64_t S, float scale,
-                                                         uint16_t* __restrict__ p,
-                                                         float* __restrict__ stats) {
-  const int64_t row = (int64_t)blockIdx.x * (NTH / 64) + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (row >= nrows) return;
-  const int64_t qi = row % S;
-  const uint16_t* sr = s + row * S;
-  uint16_t* pr = p + row * S;
-  float m = -INFINITY;
-  for (int64_t c = lane; c <= qi; c += 64) m = fmaxf(m, st::bf16r(st::bf16_to_f32(sr[c]) * scale));
-  m = wave_max(m);
-  float l = 0.0f;
-  for (int64_t c = lane; c <= qi; c += 64) l += expf(st::bf16r(st::bf16_to_f32(sr[c]) * scale) - m);
-  l = wave_sum(l);
-  const float inv = 1.0f / l;
-  for (int64_t c = lane; c < S; c += 64) {
-    float v = 0.0f;
-    if (c <= qi) v = expf(st::bf16r(st::bf16_to_f32(sr[c]) * scale) - m) * inv;
-    pr[c] = st::f32_to_bf16(v);
-  }
-  if (lane == 0) {
-    stats[2 * row] = m;
-    stats[2 * row + 1] = l;
-  }
-}
 
-__global__ __launch_bounds__(NTH) void softmax_causal_bwd(const uint16_t* __restrict__ s,
-                                                         const float* __restrict__ stats,
-                                                         const uint16_t* __restrict__ dp,
-                                                         int64_t nrows, int64_t S, float scale,
-                                                         uint16_t* __restrict__ ds) {
-  const int64_t row = (int64_t)blockIdx.x * (NTH / 64) + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (row >= nrows) return;
-  const int64_t qi = row % S;
-  const uint16_t* sr = s + row * S;
-  const uint16_t* dr = dp + row * S;
-  const float m = stats[2 * row], inv = 1.0f / stats[2 * row + 1];
-  float dot = 0.0f;
-  for (int64_t c = lane; c <= qi; c += 64) {
-    float pv = expf(st::bf16r(st::bf16_to_f32(sr[c]) * scale) - m) * inv;
-    dot += st::bf16_to_f32(dr[c]) * pv;
-  }
-  dot = wave_sum(dot);
-  for (int64_t c = lane; c < S; c += 64) {
-    float g = 0.0f;
-    if (c <= qi) {
-      float pv = expf(st::bf16r(st::bf16_to_f32(sr[c]) * scale) - m) * inv;
-      g = st::bf16r(st::bf16r(pv * (st::bf16_to_f32(dr[c]) - dot)) * scale);
-    }
-    ds[row * S + c] = st::f32_to_bf16(g);
-  }
-}
 
-// Register-resident variants: one wave per row, 16-byte accesses, the row held
-// in registers (CPL chunks of 8 per lane, S <= 512*CPL); chunks entirely past
-// the causal boundary are not read and are written as zeros.
-template <int CPL>
-__global__ __launch_bounds__(NTH) void softmax_causal_fwd_vec(const uint16_t* __restrict__ s,
-                                                             int64_t nrows, int64_t S,
-                                                             float scale,
-                                                             uint16_t* __restrict__ p,
-                                                             float* __restrict__ stats) {
-  const int64_t row = (int64_t)blockIdx.x * (NTH / 64) + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (row >= nrows) return;
-  const int64_t qi = row % S;
-  const uint4* sr = (const uint4*)(s + row * S);
-  uint4* pr = (uint4*)(p + row * S);
-  const int nch = (int)(S / 8);
-  float x[CPL][8];
-  float m = -INFINITY;
-#pragma unroll
-  for (int t = 0; t < CPL; ++t) {
-    const int ch = lane + 64 * t;
-    const int64_t c0 = (int64_t)ch * 8;
-    if (ch < nch && c0 <= qi) {
-      uint4 q = sr[ch];
-      uint32_t w[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float v = st::bf16r(st::bf16_to_f32((uint16_t)(w[e >> 1] >> (16 * (e & 1)))) * scale);
-        x[t][e] = (c0 + e <= qi) ? v : -INFINITY;
-        m = fmaxf(m, x[t][e]);
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) x[t][e] = -INFINITY;
-    }
-  }
-  m = wave_max(m);
-  float l = 0.0f;
-#pragma unroll
-  for (int t = 0; t < CPL; ++t)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      x[t][e] = expf(x[t][e] - m);  // exp(-inf) = 0 for masked entries
-      l += x[t][e];
-    }
-  l = wave_sum(l);
-  const float inv = 1.0f / l;
-#pragma unroll
-  for (int t = 0; t < CPL; ++t) {
-    const int ch = lane + 64 * t;
-    if (ch < nch)
-      pr[ch] = make_uint4(st::pack_bf16x2(x[t][0] * inv, x[t][1] * inv),
-                          st::pack_bf16x2(x[t][2] * inv, x[t][3] * inv),
-                          st::pack_bf16x2(x[t][4] * inv, x[t][5] * inv),
-                          st::pack_bf16x2(x[t][6] * inv, x[t][7] * inv));
-  }
-  if (lane == 0) {
-    stats[2 * row] = m;
-    stats[2 * row + 1] = l;
-  }
-}
 
-template <int CPL>
-__global__ __launch_bounds__(NTH) void softmax_causal_bwd_vec(const uint16_t* __restrict__ s,
-                                                             const float* __restrict__ stats,
-                                                             const uint16_t* __restrict__ dp,
-                                                             int64_t nrows, int64_t S,
-                                                             float scale,
-                                                             uint16_t* __restrict__ ds) {
-  const int64_t row = (int64_t)blockIdx.x * (NTH / 64) + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (row >= nrows) return;
-  const int64_t qi = row % S;
-  const uint4* sr = (const uint4*)(s + row * S);
-  const uint4* dr = (const uint4*)(dp + row * S);
-  uint4* outr = (uint4*)(ds + row * S);
-  const int nch = (int)(S / 8);
-  const float m = stats[2 * row], inv = 1.0f / stats[2 * row + 1];
-  float pv[CPL][8], gv[CPL][8];
-  float dot = 0.0f;
-#pragma unroll
-  for (int t = 0; t < CPL; ++t) {
-    const int ch = lane + 64 * t;
-    const int64_t c0 = (int64_t)ch * 8;
-    if (ch < nch && c0 <= qi) {
-      uint4 q = sr[ch], g = dr[ch];
-      uint32_t w[4] = {q.x, q.y, q.z, q.w};
-      uint32_t u[4] = {g.x, g.y, g.z, g.w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float sv = st::bf16r(st::bf16_to_f32((uint16_t)(w[e >> 1] >> (16 * (e & 1)))) * scale);
-        pv[t][e] = (c0 + e <= qi) ? expf(sv - m) * inv : 0.0f;
-        gv[t][e] = st::bf16_to_f32((uint16_t)(u[e >> 1] >> (16 * (e & 1))));
-        dot += gv[t][e] * pv[t][e];
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) pv[t][e] = gv[t][e] = 0.0f;
-    }
-  }
-  dot = wave_sum(dot);
-#pragma unroll
-  for (int t = 0; t < CPL; ++t) {
-    const int ch = lane + 64 * t;
-    if (ch >= nch) continue;
-    float o[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = st::bf16r(st::bf16r(pv[t][e] * (gv[t][e] - dot)) * scale);
-    outr[ch] = make_uint4(st::pack_bf16x2(o[0], o[1]), st::pack_bf16x2(o[2], o[3]),
-                          st::pack_bf16x2(o[4], o[5]), st::pack_bf16x2(o[6], o[7]));
-  }
-}
 
 // 8 elements per thread; all rows/strides multiples of 8 elements
 __global__ __launch_bounds__(NTH) void swiglu_fwd_vec(const uint16_t* __restrict__ g, int64_t ldg,
@@ -515,43 +348,4 @@ extern "C" int st_swiglu_bwd(const uint16_t* da, int64_t ldda, const uint16_t* g
   swiglu_bwd<<<nblk(total), NTH, 0, (hipStream_t)stream>>>(da, ldda, g, ldg, u, ldu, I, total, dg,
                                                            lddg, du, lddu);
   return st::check_launch("swiglu_bwd");
-}
-
-extern "C" int st_softmax_causal_fwd(const uint16_t* s, int64_t nrows, int64_t S, float scale,
-                                     uint16_t* p, float* stats, st_stream_t stream) {
-  ST_CHECK_ARG(nrows >= 0 && S > 0 && nrows % S == 0, "st_softmax_causal_fwd: bad shape");
-  if (nrows == 0) return ST_OK;
-  ST_CHECK_ARG(s && p && stats, "st_softmax_causal_fwd: NULL pointer");
-  if (S % 8 == 0 && S <= 4096 && vec8(s) && vec8(p)) {
-    const unsigned nb = (unsigned)st::cdiv(nrows, NTH / 64);
-    hipStream_t hs = (hipStream_t)stream;
-    if (S <= 512) softmax_causal_fwd_vec<1><<<nb, NTH, 0, hs>>>(s, nrows, S, scale, p, stats);
-    else if (S <= 1024) softmax_causal_fwd_vec<2><<<nb, NTH, 0, hs>>>(s, nrows, S, scale, p, stats);
-    else if (S <= 2048) softmax_causal_fwd_vec<4><<<nb, NTH, 0, hs>>>(s, nrows, S, scale, p, stats);
-    else softmax_causal_fwd_vec<8><<<nb, NTH, 0, hs>>>(s, nrows, S, scale, p, stats);
-    return st::check_launch("softmax_causal_fwd");
-  }
-  softmax_causal_fwd<<<(unsigned)st::cdiv(nrows, NTH / 64), NTH, 0, (hipStream_t)stream>>>(
-      s, nrows, S, scale, p, stats);
-  return st::check_launch("softmax_causal_fwd");
-}
-
-extern "C" int st_softmax_causal_bwd(const uint16_t* s, const float* stats, const uint16_t* dp,
-                                     int64_t nrows, int64_t S, float scale, uint16_t* ds,
-                                     st_stream_t stream) {
-  ST_CHECK_ARG(nrows >= 0 && S > 0 && nrows % S == 0, "st_softmax_causal_bwd: bad shape");
-  if (nrows == 0) return ST_OK;
-  ST_CHECK_ARG(s && stats && dp && ds, "st_softmax_causal_bwd: NULL pointer");
-  if (S % 8 == 0 && S <= 4096 && vec8(s) && vec8(dp) && vec8(ds)) {
-    const unsigned nb = (unsigned)st::cdiv(nrows, NTH / 64);
-    hipStream_t hs = (hipStream_t)stream;
-    if (S <= 512) softmax_causal_bwd_vec<1><<<nb, NTH, 0, hs>>>(s, stats, dp, nrows, S, scale, ds);
-    else if (S <= 1024) softmax_causal_bwd_vec<2><<<nb, NTH, 0, hs>>>(s, stats, dp, nrows, S, scale, ds);
-    else if (S <= 2048) softmax_causal_bwd_vec<4><<<nb, NTH, 0, hs>>>(s, stats, dp, nrows, S, scale, ds);
-    else softmax_causal_bwd_vec<8><<<nb, NTH, 0, hs>>>(s, stats, dp, nrows, S, scale, ds);
-    return st::check_launch("softmax_causal_bwd");
-  }
-  softmax_causal_bwd<<<(unsigned)st::cdiv(nrows, NTH / 64), NTH, 0, (hipStream_t)stream>>>(
-      s, stats, dp, nrows, S, scale, ds);
-  return st::check_launch("softmax_causal_bwd");
 }

@@ -11,8 +11,8 @@ backward the VJP autograd computes for that expression (paths relative to
 * :func:`rms_norm` -- adapters/dense.py:115-117.
 * :func:`rope_heads` -- adapters/dense.py:127-141 (q/k/v views, transpose,
   rotate) for one projection output.
-* :func:`causal_attention` -- adapters/dense.py:142-148 (GQA repeat, eager
-  fp32 softmax with the causal mask, relayout to tokens).
+* :func:`causal_attention` -- adapters/dense.py:142-148 (GQA repeat, fp32
+  softmax with the causal mask, relayout to tokens) as flash attention.
 * :func:`swiglu` -- adapters/dense.py:153 ``silu(gate) * up``.
 
 Ops run on the current stream, allocate through PyTorch and never fall back
@@ -401,51 +401,39 @@ def rope_heads(y, col0, B, S, heads, D, cos, sin, rotate=True):
 
 # ----------------------------------------------------------------- attention
 class _CausalAttention(torch.autograd.Function):
-    """Eager GQA attention of dense.py:142-148 with the HIP causal softmax;
-    the score/probability products use torch.matmul on contiguous operands."""
+    """GQA causal attention of dense.py:142-148 as flash attention: no
+    [S, S] scores in memory; the backward recomputes probabilities from the
+    saved base-2 log-sum-exp."""
 
     @staticmethod
     def forward(ctx, q, k, v, scale):
         B, H, S, D = q.shape
         Hkv = k.shape[1]
-        g = H // Hkv
         dev = q.device
-        st = _lib.stream_handle(dev)
-        qg = q.view(B, Hkv, g * S, D)
-        kt = k.transpose(-1, -2).contiguous()
-        s = torch.matmul(qg, kt)                       # [B, Hkv, g*S, S]
-        p = torch.empty_like(s)
-        stats = torch.empty((B * H * S, 2), dtype=_F32, device=dev)
-        _lib.call("st_softmax_causal_fwd", _lib.ptr(s), B * H * S, S, float(scale), _lib.ptr(p),
-                  _lib.ptr(stats), st)
-        o = torch.matmul(p, v)                         # [B, Hkv, g*S, D]
         out = torch.empty((B, S, H * D), dtype=_BF16, device=dev)
-        _lib.call("st_heads_to_tokens", _lib.ptr(o), B, S, H, D, _lib.ptr(out), st)
-        ctx.save_for_backward(q, k, v, s, p, stats)
+        lse = torch.empty((B, H, S), dtype=_F32, device=dev)
+        ws = _ws.get(dev, _lib.query("st_flash_attn_workspace_bytes", B, S, H, Hkv, D, 0))
+        _lib.call("st_flash_attn_fwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), B, S, H, Hkv, D,
+                  float(scale), _lib.ptr(out), _lib.ptr(lse), _lib.ptr(ws),
+                  0 if ws is None else ws.numel(), _lib.stream_handle(dev))
+        ctx.save_for_backward(q, k, v, out, lse)
         ctx.scale = scale
         return out
 
     @staticmethod
     def backward(ctx, dout):
-        q, k, v, s, p, stats = ctx.saved_tensors
+        q, k, v, out, lse = ctx.saved_tensors
         B, H, S, D = q.shape
         Hkv = k.shape[1]
-        g = H // Hkv
         dev = q.device
-        st = _lib.stream_handle(dev)
         dout = dout.contiguous()
-        do = torch.empty((B, H, S, D), dtype=_BF16, device=dev)
-        _lib.call("st_tokens_to_heads", _lib.ptr(dout), B, S, H, D, _lib.ptr(do), st)
-        dog = do.view(B, Hkv, g * S, D)
-        dp = torch.matmul(dog, v.transpose(-1, -2).contiguous())
-        ds = torch.empty_like(dp)
-        _lib.call("st_softmax_causal_bwd", _lib.ptr(s), _lib.ptr(stats), _lib.ptr(dp), B * H * S,
-                  S, float(ctx.scale), _lib.ptr(ds), st)
-        dq = torch.matmul(ds, k).view(B, H, S, D)
-        qg = q.view(B, Hkv, g * S, D)
-        dkt = torch.matmul(qg.transpose(-1, -2).contiguous(), ds)      # [B, Hkv, D, S]
-        dvt = torch.matmul(dog.transpose(-1, -2).contiguous(), p)      # [B, Hkv, D, S]
-        return dq, dkt.transpose(-1, -2).contiguous(), dvt.transpose(-1, -2).contiguous(), None
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        ws = _ws.get(dev, _lib.query("st_flash_attn_workspace_bytes", B, S, H, Hkv, D, 1))
+        _lib.call("st_flash_attn_bwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(out),
+                  _lib.ptr(lse), _lib.ptr(dout), B, S, H, Hkv, D, float(ctx.scale), _lib.ptr(dq),
+                  _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(ws), 0 if ws is None else ws.numel(),
+                  _lib.stream_handle(dev))
+        return dq, dk, dv, None
 
 
 def causal_attention(q, k, v, scale):
