@@ -16,7 +16,6 @@ namespace {
 
 constexpr int NTH = 256;
 constexpr int BQ = 128;  // queries per workgroup (4 waves x 32)
-constexpr int BKT = 64;  // keys per tile
 constexpr float LOG2E = 1.4426950408889634f;
 
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
@@ -28,56 +27,106 @@ template <int D>
 __device__ __forceinline__ int kswz(int row, int chunk) {
   return row * (D / 8) + (chunk ^ (row & (D / 8 - 1)));
 }
-// V^T tile [D][64 keys] in LDS, 8-byte chunks (4 keys) XOR-swizzled by d
-__device__ __forceinline__ int vswz8(int d, int kc) { return d * 16 + (kc ^ ((d >> 1) & 15)); }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 // ---------------------------------------------------------------- transpose
-// dst[n][d][s] = src[n][s][d] for n < N heads (64x64 tiles through LDS)
+// Position of key j inside its 16-key group in the staged V^T rows: bits 2
+// and 3 swapped, so the keys {4g..4g+3, 8+4g..8+4g+3} a lane's MFMA operand
+// needs (the row order of a 32x32 accumulator block) are 8 adjacent bf16.
+__host__ __device__ __forceinline__ int vpos(int j) {
+  return (j & ~12) | ((j & 4) << 1) | ((j & 8) >> 1);
+}
+// dst[n][d][vpos(s)] = src[n][s][d] (rows of Sp >= S elements, zero past S)
 __global__ __launch_bounds__(NTH) void transpose_heads(const uint16_t* __restrict__ src,
                                                        uint16_t* __restrict__ dst, int64_t S,
-                                                       int D) {
+                                                       int64_t Sp, int D) {
   __shared__ uint16_t t[64][66];
   const int64_t n = blockIdx.z;
   const int64_t s0 = (int64_t)blockIdx.x * 64, d0 = (int64_t)blockIdx.y * 64;
   const uint16_t* in = src + n * S * D;
-  uint16_t* out = dst + n * S * D;
+  uint16_t* out = dst + n * Sp * D;
   for (int i = threadIdx.x; i < 64 * 64; i += NTH) {
     const int r = i / 64, c = i % 64;
     t[r][c] = (s0 + r < S && d0 + c < D) ? in[(s0 + r) * D + d0 + c] : 0;
   }
   __syncthreads();
   for (int i = threadIdx.x; i < 64 * 64; i += NTH) {
-    const int r = i / 64, c = i % 64;  // r: d, c: s
-    if (d0 + r < D && s0 + c < S) out[(d0 + r) * S + s0 + c] = t[c][r];
+    const int r = i / 64, c = i % 64;  // r: d, c: position in the 64-key block
+    if (d0 + r < D && s0 + c < Sp) out[(d0 + r) * Sp + s0 + c] = t[vpos(c)][r];
   }
 }
 
+// Direct global -> LDS copy of 16 bytes per lane; the 64 lanes of a wave fill
+// 1 KiB of LDS contiguously from `lds_wave` (wave-uniform), so layouts are
+// formed by choosing each lane's source address.
+__device__ __forceinline__ void g2lds16(const uint16_t* src, uint16_t* lds_wave) {
+  __builtin_amdgcn_global_load_lds((const void*)src,
+                                   (__attribute__((address_space(3))) void*)lds_wave, 16, 0, 0);
+}
+
+// Workgroup -> (x, h, b) for a 1-D grid of nx * H * B workgroups.  Blocks are
+// dispatched round-robin over the 8 XCDs; remapping keeps consecutive logical
+// indices on one XCD, and x runs fastest, then the query heads of a KV group,
+// so each XCD streams the K/V of its own KV heads through its own L2.
+struct WgIdx {
+  int x, h, b;
+};
+__device__ __forceinline__ WgIdx wg_index(int nx, int H) {
+  const int64_t L = st::xcd_remap(blockIdx.x, gridDim.x);
+  WgIdx w;
+  w.x = (int)(L % nx);
+  const int64_t hb = L / nx;
+  w.h = (int)(hb % H);
+  w.b = (int)(hb / H);
+  return w;
+}
+
 // ---------------------------------------------------------------- forward
+// LDS tiles use padded rows (one spare 16-byte slot per row) rather than an
+// XOR swizzle: 16-byte operand reads of 16 consecutive rows then hit 16
+// distinct bank groups, and every operand address is a per-lane base plus an
+// immediate.  Direct global->LDS copies fill whole slots, pads included (a
+// pad slot receives a harmless in-bounds copy).
 template <int D>
-__global__ __launch_bounds__(NTH, 2) void fa_fwd(const uint16_t* __restrict__ q,
-                                              const uint16_t* __restrict__ k,
-                                              const uint16_t* __restrict__ vt, int S, int H,
-                                              int Hkv, float sl2, uint16_t* __restrict__ out,
-                                              float* __restrict__ lse) {
+constexpr int KSLOTS = D / 8 + 1;        // 16-byte slots per padded K row
+template <int BKT>
+constexpr int VSLOTS = BKT / 8 + 1;      // per padded V^T row
+constexpr float RESCALE_LOG2 = 8.0f;     // running max may lag by up to 2^8
+
+template <int D, int BKT, int G>
+constexpr int fwd_lds_elems() {
+  return G * 2 * (BKT * KSLOTS<D> + D * VSLOTS<BKT>) * 8;
+}
+
+// G = 1: 4 waves over all keys.  G = 2: 8 waves in two groups of 4 over the
+// same queries, group r taking K/V tiles r, r+2, ...; group 1's softmax state
+// (max, partial sums, O) is merged into group 0's at the end.
+template <int D, int BKT, int G>
+__device__ __forceinline__ void fa_fwd_tile(const uint16_t* __restrict__ q,
+                                            const uint16_t* __restrict__ k,
+                                            const uint16_t* __restrict__ vt, int S, int H,
+                                            int Hkv, float sl2, uint16_t* __restrict__ out,
+                                            float* __restrict__ lse, int qt, int h, int b,
+                                            uint16_t* lds) {
   constexpr int DS = D / 16;   // contraction steps over d
   constexpr int DB = D / 32;   // 32-row d blocks of O^T
-  constexpr int LDK = BKT * D; // bf16 per K tile
-  constexpr int LDV = D * BKT; // bf16 per V^T tile
-  constexpr int PER = D / 32;  // 16-byte chunks per thread per tile (K and V^T each)
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * (LDK + LDV)];
+  constexpr int KS = KSLOTS<D>, VS = VSLOTS<BKT>;
+  constexpr int LK = BKT * KS * 8, LV = D * VS * 8;  // bf16 per padded tile
+  constexpr int KI = BKT * KS / 64, VI = D * VS / 64;  // wave copies (1 KiB each) per tile
+  static_assert((BKT * KS) % 64 == 0 && (D * VS) % 64 == 0, "tiles are whole wave copies");
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int grp = (tid >> 6) / 4, wave = (tid >> 6) % 4;  // key group, wave in group
   const int g = lane >> 5, c = lane & 31;
-  const int qt = gridDim.x - 1 - blockIdx.x;  // longest (diagonal-most) tiles first
-  const int h = blockIdx.y, b = blockIdx.z;
   const int hk = h / (H / Hkv);
   const uint16_t* qb = q + ((int64_t)(b * H + h) * S) * D;
   const uint16_t* kb = k + ((int64_t)(b * Hkv + hk) * S) * D;
-  const uint16_t* vb = vt + ((int64_t)(b * Hkv + hk) * D) * S;
+  const int Sp = (S + 15) & ~15;                // staged V^T row length
+  const uint16_t* vb = vt + ((int64_t)(b * Hkv + hk) * D) * Sp;
   const int q0 = qt * BQ + wave * 32;
   const int myq = q0 + c;
+  uint16_t* glds = lds + grp * 2 * (LK + LV);   // this group's two tile buffers
 
   bf16x8 qf[DS];
 #pragma unroll
@@ -94,112 +143,190 @@ __global__ __launch_bounds__(NTH, 2) void fa_fwd(const uint16_t* __restrict__ q,
 
   const int qlast = min(qt * BQ + BQ, S) - 1;   // last query of the workgroup
   const int ntiles = qlast / BKT + 1;           // causal: keys <= qlast
-  uint4 kr[PER], vr[PER];
-  auto load = [&](int t) {
+  const int nsteps = (ntiles + G - 1) / G;      // group steps (tile u*G + grp)
+  // Rows past S read a clamped (finite) row: those keys are masked out.
+  auto issue = [&](int t, int buf) {
     const int k0 = t * BKT;
+    uint16_t* ks = glds + buf * (LK + LV);
+    uint16_t* vs = ks + LK;
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int id = tid + i * NTH;
-      const int row = id / (D / 8), ch = id % (D / 8);  // K: key row, chunk
-      kr[i] = (k0 + row < S) ? ld_global16(kb + (int64_t)(k0 + row) * D + ch * 8)
-                             : make_uint4(0, 0, 0, 0);
-      const int d = id / 8, kc2 = id % 8;                 // V^T: d row, 16-byte key chunk
-      vr[i] = (k0 + kc2 * 8 < S) ? ld_global16(vb + (int64_t)d * S + k0 + kc2 * 8)
-                                 : make_uint4(0, 0, 0, 0);
+    for (int i = 0; i < (KI + 3) / 4; ++i) {
+      const int wi = i * 4 + wave;
+      if (wi < KI) {
+        const int P = wi * 64 + lane;
+        const int row = min(P / KS, BKT - 1), ch = P % KS;
+        const int key = min(k0 + row, S - 1);
+        g2lds16(kb + (int64_t)key * D + min(ch, D / 8 - 1) * 8, ks + wi * 64 * 8);
+      }
     }
-  };
-  auto store = [&](int buf) {
-    uint16_t* ks = lds + buf * (LDK + LDV);
-    uint16_t* vs = ks + LDK;
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int id = tid + i * NTH;
-      const int row = id / (D / 8), ch = id % (D / 8);
-      *(uint4*)(ks + kswz<D>(row, ch) * 8) = kr[i];
-      const int d = id / 8, kc2 = id % 8;
-      const int f = (d >> 1) & 15;
-      const int slot = kc2 ^ (f >> 1);
-      uint4 w = vr[i];
-      if (f & 1) w = make_uint4(w.z, w.w, w.x, w.y);
-      *(uint4*)(vs + d * BKT + slot * 8) = w;
+    for (int i = 0; i < (VI + 3) / 4; ++i) {
+      const int wi = i * 4 + wave;
+      if (wi < VI) {
+        const int P = wi * 64 + lane;
+        const int d = min(P / VS, D - 1), ch = min(P % VS, BKT / 8 - 1);
+        const int col = min(k0 + ch * 8, Sp - 8);
+        g2lds16(vb + (int64_t)d * Sp + col, vs + wi * 64 * 8);
+      }
     }
   };
 
-  load(0);
-  store(0);
+  if (grp < ntiles) issue(grp, 0);
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  // one barrier per tile: tile t+1 is stored into the other buffer, whose
-  // readers (tile t-1) all passed the previous barrier
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < ntiles) load(t + 1);
-    const uint16_t* ks = lds + buf * (LDK + LDV);
-    const uint16_t* vs = ks + LDK;
+  // one barrier per step: the next tile lands in the other buffer, whose
+  // readers (step u-1) all passed the previous barrier
+  for (int u = 0; u < nsteps; ++u) {
+    const int buf = u & 1;
+    const int t = u * G + grp;
+    if (t + G < ntiles) issue(t + G, buf ^ 1);
+    const uint16_t* ks = glds + buf * (LK + LV);
+    const uint16_t* vs = ks + LK;
+    const uint16_t* kl = ks + (c * KS + g) * 8;   // this lane's K operand row
+    const uint16_t* vl = vs + (c * VS + g) * 8;   // this lane's V^T operand row
     const int k0 = t * BKT;
-    // 32-key blocks, each: S^T = K Q^T, online softmax, O^T += V^T P^T.  A
-    // block wholly above this wave's queries (or past S) is skipped.
+    if (t >= ntiles) {
+      // this group has no tile in the last step
+    } else if (k0 + BKT - 1 <= q0 && k0 + BKT <= S) {
+      // interior tile (every key visible to every query of this wave): the
+      // blocks' MFMA chains are independent and nothing is masked
+      f32x16 sacc[BKT / 32];
 #pragma unroll
-    for (int jb = 0; jb < 2; ++jb) {
-      const int kb0 = k0 + jb * 32;
-      if (kb0 > q0 + 31 || kb0 >= S) continue;  // wave-uniform
-      f32x16 sacc;
+      for (int jb = 0; jb < BKT / 32; ++jb)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) sacc[v] = 0.0f;
+        for (int v = 0; v < 16; ++v) sacc[jb][v] = 0.0f;
 #pragma unroll
-      for (int s = 0; s < DS; ++s) {
-        const bf16x8 a = as_bf16x8(*(const uint4*)(ks + kswz<D>(jb * 32 + c, 2 * s + g) * 8));
-        sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[s], sacc, 0, 0, 0);
-      }
-      const bool diag = kb0 + 31 > q0 || kb0 + 31 >= S;
-      float mt = -INFINITY;
+      for (int s = 0; s < DS; ++s)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int key = kb0 + (v >> 2) * 8 + g * 4 + (v & 3);
-        float x = sacc[v] * sl2;
-        if (diag && (key > myq || key >= S)) x = -INFINITY;
-        sacc[v] = x;
-        mt = fmaxf(mt, x);
-      }
-      mt = fmaxf(mt, __shfl_xor(mt, 32));
-      const float m_new = fmaxf(m_run, mt);
-      if (__ballot(m_new > m_run)) {
-        const float alpha = exp2f(m_run - m_new);
+        for (int jb = 0; jb < BKT / 32; ++jb) {
+          const bf16x8 a = as_bf16x8(*(const uint4*)(kl + (jb * 32 * KS + 2 * s) * 8));
+          sacc[jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[s], sacc[jb], 0, 0, 0);
+        }
+      float mt = sacc[0][0];
+#pragma unroll
+      for (int jb = 0; jb < BKT / 32; ++jb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) mt = fmaxf(mt, sacc[jb][v]);
+      mt = fmaxf(mt, __shfl_xor(mt, 32)) * sl2;
+      if (__ballot(mt > m_run + RESCALE_LOG2)) {
+        const float m_new = fmaxf(m_run, mt);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
 #pragma unroll
         for (int i = 0; i < DB; ++i)
 #pragma unroll
           for (int v = 0; v < 16; ++v) oacc[i][v] *= alpha;
         l_run *= alpha;
+        m_run = m_new;
       }
-      m_run = m_new;
-      bf16x8 pf[2];
+      bf16x8 pf[BKT / 16];
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
+      for (int cc = 0; cc < BKT / 16; ++cc) {
         float p[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          p[e] = exp2f(sacc[8 * hh + e] - m_new);
+          p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[cc >> 1][8 * (cc & 1) + e], sl2, -m_run));
           l_run += p[e];
         }
-        pf[hh] = as_bf16x8(make_uint4(st::pack_bf16x2(p[0], p[1]), st::pack_bf16x2(p[2], p[3]),
+        pf[cc] = as_bf16x8(make_uint4(st::pack_bf16x2(p[0], p[1]), st::pack_bf16x2(p[2], p[3]),
                                       st::pack_bf16x2(p[4], p[5]), st::pack_bf16x2(p[6], p[7])));
       }
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const int cc = jb * 2 + hh;
+      for (int cc = 0; cc < BKT / 16; ++cc)
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
-          const int d = db * 32 + c;
-          const u32x2 lo = *(const u32x2*)(vs + vswz8(d, 4 * cc + g) * 4);
-          const u32x2 hi = *(const u32x2*)(vs + vswz8(d, 4 * cc + 2 + g) * 4);
-          const bf16x8 a = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
-          oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pf[hh], oacc[db], 0, 0, 0);
+          const bf16x8 a = as_bf16x8(*(const uint4*)(vl + (db * 32 * VS + 2 * cc) * 8));
+          oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pf[cc], oacc[db], 0, 0, 0);
+        }
+    } else {
+      // 32-key blocks, each: S^T = K Q^T, online softmax, O^T += V^T P^T.  A
+      // block wholly above this wave's queries (or past S) is skipped.
+  #pragma unroll
+      for (int jb = 0; jb < BKT / 32; ++jb) {
+        const int kb0 = k0 + jb * 32;
+        if (kb0 > q0 + 31 || kb0 >= S) continue;  // wave-uniform
+        f32x16 sacc;
+  #pragma unroll
+        for (int v = 0; v < 16; ++v) sacc[v] = 0.0f;
+  #pragma unroll
+        for (int s = 0; s < DS; ++s) {
+          const bf16x8 a = as_bf16x8(*(const uint4*)(kl + (jb * 32 * KS + 2 * s) * 8));
+          sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[s], sacc, 0, 0, 0);
+        }
+        if (kb0 + 31 > q0 || kb0 + 31 >= S) {  // diagonal / ragged block: mask
+  #pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int key = kb0 + (v >> 2) * 8 + g * 4 + (v & 3);
+            if (key > myq || key >= S) sacc[v] = -INFINITY;
+          }
+        }
+        float mt = sacc[0];
+  #pragma unroll
+        for (int v = 1; v < 16; ++v) mt = fmaxf(mt, sacc[v]);
+        mt = fmaxf(mt, __shfl_xor(mt, 32)) * sl2;
+        // rescale only when some query's max grew by more than 2^8
+        if (__ballot(mt > m_run + RESCALE_LOG2)) {
+          const float m_new = fmaxf(m_run, mt);
+          const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+  #pragma unroll
+          for (int i = 0; i < DB; ++i)
+  #pragma unroll
+            for (int v = 0; v < 16; ++v) oacc[i][v] *= alpha;
+          l_run *= alpha;
+          m_run = m_new;
+        }
+        bf16x8 pf[2];
+  #pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          float p[8];
+  #pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[8 * hh + e], sl2, -m_run));
+            l_run += p[e];
+          }
+          pf[hh] = as_bf16x8(make_uint4(st::pack_bf16x2(p[0], p[1]), st::pack_bf16x2(p[2], p[3]),
+                                        st::pack_bf16x2(p[4], p[5]), st::pack_bf16x2(p[6], p[7])));
+        }
+  #pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const int cc = jb * 2 + hh;
+  #pragma unroll
+          for (int db = 0; db < DB; ++db) {
+            const bf16x8 a = as_bf16x8(*(const uint4*)(vl + (db * 32 * VS + 2 * cc) * 8));
+            oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pf[hh], oacc[db], 0, 0, 0);
+          }
         }
       }
     }
-    if (t + 1 < ntiles) store(buf ^ 1);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
 
+  if (G == 2) {  // group 1 parks (m, l, O) per lane; group 0 merges them
+    float* park = (float*)lds + wave * 64 * (16 * DB + 2);
+    if (grp == 1) {
+#pragma unroll
+      for (int i = 0; i < DB; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) park[(i * 16 + v) * 64 + lane] = oacc[i][v];
+      park[(16 * DB) * 64 + lane] = m_run;
+      park[(16 * DB + 1) * 64 + lane] = l_run;
+    }
+    __syncthreads();
+    if (grp == 0) {
+      const float mb = park[(16 * DB) * 64 + lane], lb = park[(16 * DB + 1) * 64 + lane];
+      const float m = fmaxf(m_run, mb);
+      const float aa = __builtin_amdgcn_exp2f(m_run - m), ab = __builtin_amdgcn_exp2f(mb - m);
+#pragma unroll
+      for (int i = 0; i < DB; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          oacc[i][v] = oacc[i][v] * aa + park[(i * 16 + v) * 64 + lane] * ab;
+      l_run = l_run * aa + lb * ab;
+      m_run = m;
+    }
+    __syncthreads();  // parked values read before the output staging reuses LDS
+    if (grp == 1) return;
+  }
   const float l_tot = l_run + __shfl_xor(l_run, 32);
   const float inv = 1.0f / l_tot;
   if (g == 0 && myq < S) lse[((int64_t)(b * H + h)) * S + myq] = m_run + log2f(l_tot);
@@ -215,7 +342,9 @@ __global__ __launch_bounds__(NTH, 2) void fa_fwd(const uint16_t* __restrict__ q,
                        st::pack_bf16x2(oacc[db][4 * v4 + 2] * inv, oacc[db][4 * v4 + 3] * inv)};
       *(u32x2*)(os + c * LDO + d) = w;
     }
-  __syncthreads();
+  // each wave reads back only its own rows: a wave-level fence suffices
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_wave_barrier();
   const int64_t ld_out = (int64_t)H * D;
   for (int i = lane; i < 32 * (D / 8); i += 64) {
     const int r = i / (D / 8), ch = i % (D / 8);
@@ -226,6 +355,30 @@ __global__ __launch_bounds__(NTH, 2) void fa_fwd(const uint16_t* __restrict__ q,
       *(uint4*)(out + ((int64_t)b * S + qq) * ld_out + (int64_t)h * D + ch * 8) =
           make_uint4(a.x, a.y, bb.x, bb.y);
     }
+  }
+}
+
+// Causal work per 128-query tile grows with its index; with `paired` each
+// workgroup takes tiles i and n-1-i (equal total work per workgroup).
+__device__ __forceinline__ int pair_tile(int x, int it, int nq, int paired) {
+  if (!paired) return nq - 1 - x;  // longest tiles first
+  return it == 0 ? nq - 1 - x : x;
+}
+
+template <int D, int BKT, int G>
+__global__ __launch_bounds__(NTH * G, G == 1 && BKT == 64 ? 2 : 1) void fa_fwd(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+    const uint16_t* __restrict__ vt, int S, int H, int Hkv, float sl2,
+    uint16_t* __restrict__ out, float* __restrict__ lse, int nq, int paired) {
+  __shared__ __attribute__((aligned(16))) uint16_t lds[fwd_lds_elems<D, BKT, G>()];
+  const WgIdx w = wg_index(paired ? (nq + 1) / 2 : nq, H);
+  for (int it = 0; it < 1 + paired; ++it) {
+    const int qt = pair_tile(w.x, it, nq, paired);
+    if (it == 1) {
+      if (qt == pair_tile(w.x, 0, nq, paired)) break;
+      __syncthreads();  // the previous tile's output staging still reads LDS
+    }
+    fa_fwd_tile<D, BKT, G>(q, k, vt, S, H, Hkv, sl2, out, lse, qt, w.h, w.b, lds);
   }
 }
 
@@ -263,20 +416,18 @@ __device__ __forceinline__ bf16x8 tile_tr(const uint16_t* t, int kb, int nb, int
 // dQ (and Delta = rowsum(dO * O)) per 128-query tile: S^T = K Q^T,
 // P^T = exp2(S^T - lse), dP^T = V dO^T, dS^T = P^T (dP^T - Delta),
 // dQ^T += K^T dS^T; keys up to the diagonal.
-template <int D>
-__global__ __launch_bounds__(NTH, 2) void fa_bwd_dq(
+template <int D, int BKT>
+__device__ __forceinline__ void fa_bwd_dq_tile(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ o,
     const uint16_t* __restrict__ dout, const float* __restrict__ lse, int S, int H, int Hkv,
-    float sl2, float scale, float* __restrict__ delta, uint16_t* __restrict__ dq) {
+    float sl2, float scale, float* __restrict__ delta, uint16_t* __restrict__ dq, int qt, int h,
+    int b, uint16_t* lds) {
   constexpr int DS = D / 16, DB = D / 32;
   constexpr int LT = BKT * D;           // bf16 per K (or V) tile
-  constexpr int PER = D / 32;           // 16-byte chunks per thread per tile
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 2 * LT];
+  constexpr int PER = BKT * D / 8 / NTH;  // 16-byte chunks per thread per tile
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, c = lane & 31;
-  const int qt = gridDim.x - 1 - blockIdx.x;
-  const int h = blockIdx.y, b = blockIdx.z;
   const int hk = h / (H / Hkv);
   const int64_t ldt = (int64_t)H * D;  // token-major row stride
   const uint16_t* qb = q + ((int64_t)(b * H + h) * S) * D;
@@ -317,40 +468,33 @@ __global__ __launch_bounds__(NTH, 2) void fa_bwd_dq(
 
   const int qlast = min(qt * BQ + BQ, S) - 1;
   const int ntiles = qlast / BKT + 1;
-  uint4 kr[PER], vr[PER];
-  auto load = [&](int t) {
+  // K and V tiles [key][D] (tswz layout) by direct global -> LDS copies;
+  // rows past S read a clamped (finite) row, masked out below
+  auto issue = [&](int t, int buf) {
     const int k0 = t * BKT;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int id = tid + i * NTH;
-      const int row = id / (D / 8), ch = id % (D / 8);
-      const bool ok = k0 + row < S;
-      kr[i] = ok ? ld_global16(kb + (int64_t)(k0 + row) * D + ch * 8) : make_uint4(0, 0, 0, 0);
-      vr[i] = ok ? ld_global16(vb + (int64_t)(k0 + row) * D + ch * 8) : make_uint4(0, 0, 0, 0);
-    }
-  };
-  auto store = [&](int buf) {
     uint16_t* ks = lds + buf * 2 * LT;
     uint16_t* vs = ks + LT;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      const int id = tid + i * NTH;
-      const int row = id / (D / 8), ch = id % (D / 8);
-      *(uint4*)(ks + tswz<D>(row, ch)) = kr[i];
-      *(uint4*)(vs + tswz<D>(row, ch)) = vr[i];
+      const int P = i * NTH + tid;
+      const int row = P / (D / 8);
+      const int ch = (P % (D / 8)) ^ (((row & 7) << 1) & (D / 8 - 1));
+      const int64_t off = (int64_t)min(k0 + row, S - 1) * D + ch * 8;
+      g2lds16(kb + off, ks + (i * NTH + wave * 64) * 8);
+      g2lds16(vb + off, vs + (i * NTH + wave * 64) * 8);
     }
   };
-  load(0);
-  store(0);
+  issue(0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   for (int t = 0; t < ntiles; ++t) {
     const int buf = t & 1;
-    if (t + 1 < ntiles) load(t + 1);
+    if (t + 1 < ntiles) issue(t + 1, buf ^ 1);
     const uint16_t* ks = lds + buf * 2 * LT;
     const uint16_t* vs = ks + LT;
     const int k0 = t * BKT;
 #pragma unroll
-    for (int jb = 0; jb < 2; ++jb) {
+    for (int jb = 0; jb < BKT / 32; ++jb) {
       const int kb0 = k0 + jb * 32;
       if (kb0 > q0 + 31 || kb0 >= S) continue;
       f32x16 sacc, pacc;
@@ -372,7 +516,7 @@ __global__ __launch_bounds__(NTH, 2) void fa_bwd_dq(
           const int vv = 8 * hh + e;
           const int key = kb0 + (vv >> 2) * 8 + g * 4 + (vv & 3);
           const bool keep = key <= myq && key < S && qok;
-          const float p = keep ? exp2f(sacc[vv] * sl2 - lq) : 0.0f;
+          const float p = keep ? __builtin_amdgcn_exp2f(sacc[vv] * sl2 - lq) : 0.0f;
           ds[e] = p * (pacc[vv] - dl);
         }
         dsf[hh] = as_bf16x8(make_uint4(st::pack_bf16x2(ds[0], ds[1]), st::pack_bf16x2(ds[2], ds[3]),
@@ -385,7 +529,7 @@ __global__ __launch_bounds__(NTH, 2) void fa_bwd_dq(
           dqacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
               tile_tr<D>(ks, jb * 32 + 16 * hh, db * 32, lane), dsf[hh], dqacc[db], 0, 0, 0);
     }
-    if (t + 1 < ntiles) store(buf ^ 1);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
   // dQ = scale * dQ^T^T, staged through LDS as query rows, head-major out
@@ -413,6 +557,26 @@ __global__ __launch_bounds__(NTH, 2) void fa_bwd_dq(
   }
 }
 
+template <int D, int BKT>
+__global__ __launch_bounds__(NTH, BKT == 64 ? 2 : 1) void fa_bwd_dq(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+    const uint16_t* __restrict__ v, const uint16_t* __restrict__ o,
+    const uint16_t* __restrict__ dout, const float* __restrict__ lse, int S, int H, int Hkv,
+    float sl2, float scale, float* __restrict__ delta, uint16_t* __restrict__ dq, int nq,
+    int paired) {
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 2 * BKT * D];
+  const WgIdx w = wg_index(paired ? (nq + 1) / 2 : nq, H);
+  for (int it = 0; it < 1 + paired; ++it) {
+    const int qt = pair_tile(w.x, it, nq, paired);
+    if (it == 1) {
+      if (qt == pair_tile(w.x, 0, nq, paired)) break;
+      __syncthreads();
+    }
+    fa_bwd_dq_tile<D, BKT>(q, k, v, o, dout, lse, S, H, Hkv, sl2, scale, delta, dq, qt, w.h,
+                           w.b, lds);
+  }
+}
+
 // dK, dV of one query head over a 128-key tile (8 waves: 4 key quarters x 2
 // query halves), looping over 64-query tiles from the diagonal down:
 // S = Q K^T, P = exp2(S - lse), dP = dO V^T, dS = P (dP - Delta),
@@ -433,7 +597,8 @@ __global__ __launch_bounds__(NTH2, 2) void fa_bwd_dkdv(
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, c = lane & 31;
   const int kq = wave & 3, qh = wave >> 2;
-  const int kt = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const WgIdx w = wg_index((S + KT2 - 1) / KT2, H);
+  const int kt = w.x, h = w.h, b = w.b;
   const int hk = h / (H / Hkv);
   const int64_t ldt = (int64_t)H * D;
   const uint16_t* qb = q + ((int64_t)(b * H + h) * S) * D;
@@ -465,17 +630,21 @@ __global__ __launch_bounds__(NTH2, 2) void fa_bwd_dkdv(
 
   const int qt_first = k0 / QT2;
   const int qt_end = (S + QT2 - 1) / QT2;
-  uint4 qr[PERQ], gr[PERQ];
   float lr = 0.0f, dr = 0.0f;
-  auto load = [&](int qt) {
+  // Q and dO tiles [query][D] (tswz layout) by direct global -> LDS copies
+  // (rows past S read a clamped row, masked below); lse and Delta via VGPRs
+  auto issue = [&](int qt, int buf) {
     const int q0 = qt * QT2;
+    uint16_t* qs = lds + 2 * LK + buf * 2 * LQ;
+    uint16_t* gs = qs + LQ;
 #pragma unroll
     for (int i = 0; i < PERQ; ++i) {
-      const int id = tid + i * NTH2;
-      const int row = id / (D / 8), ch = id % (D / 8);
-      const bool ok = q0 + row < S;
-      qr[i] = ok ? ld_global16(qb + (int64_t)(q0 + row) * D + ch * 8) : make_uint4(0, 0, 0, 0);
-      gr[i] = ok ? ld_global16(gb + (int64_t)(q0 + row) * ldt + ch * 8) : make_uint4(0, 0, 0, 0);
+      const int P = i * NTH2 + tid;
+      const int row = P / (D / 8);
+      const int ch = (P % (D / 8)) ^ (((row & 7) << 1) & (D / 8 - 1));
+      const int qq = min(q0 + row, S - 1);
+      g2lds16(qb + (int64_t)qq * D + ch * 8, qs + (i * NTH2 + wave * 64) * 8);
+      g2lds16(gb + (int64_t)qq * ldt + ch * 8, gs + (i * NTH2 + wave * 64) * 8);
     }
     if (tid < QT2) {
       const bool ok = q0 + tid < S;
@@ -483,26 +652,18 @@ __global__ __launch_bounds__(NTH2, 2) void fa_bwd_dkdv(
       dr = ok ? delta[srow + q0 + tid] : 0.0f;
     }
   };
-  auto store = [&](int buf) {
-    uint16_t* qs = lds + 2 * LK + buf * 2 * LQ;
-    uint16_t* gs = qs + LQ;
-#pragma unroll
-    for (int i = 0; i < PERQ; ++i) {
-      const int id = tid + i * NTH2;
-      const int row = id / (D / 8), ch = id % (D / 8);
-      *(uint4*)(qs + tswz<D>(row, ch)) = qr[i];
-      *(uint4*)(gs + tswz<D>(row, ch)) = gr[i];
-    }
+  auto stats = [&](int buf) {
     if (tid < QT2) { lse_s[buf][tid] = lr; dl_s[buf][tid] = dr; }
   };
   if (qt_first < qt_end) {
-    load(qt_first);
-    store(0);
+    issue(qt_first, 0);
+    stats(0);
   }
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   for (int qt = qt_first; qt < qt_end; ++qt) {
     const int buf = (qt - qt_first) & 1;
-    if (qt + 1 < qt_end) load(qt + 1);
+    if (qt + 1 < qt_end) issue(qt + 1, buf ^ 1);
     const uint16_t* qs = lds + 2 * LK + buf * 2 * LQ;
     const uint16_t* gs = qs + LQ;
     const int qw0 = qt * QT2 + qh * 32;   // this wave's queries
@@ -529,7 +690,7 @@ __global__ __launch_bounds__(NTH2, 2) void fa_bwd_dkdv(
           const int r = qh * 32 + (vv >> 2) * 8 + g * 4 + (vv & 3);  // query row in tile
           const int qq = qt * QT2 + r;
           const bool keep = mykey <= qq && mykey < S && qq < S;
-          const float p = keep ? exp2f(sacc[vv] * sl2 - lse_s[buf][r]) : 0.0f;
+          const float p = keep ? __builtin_amdgcn_exp2f(sacc[vv] * sl2 - lse_s[buf][r]) : 0.0f;
           p8[e] = p;
           d8[e] = p * (pacc[vv] - dl_s[buf][r]);
         }
@@ -548,7 +709,8 @@ __global__ __launch_bounds__(NTH2, 2) void fa_bwd_dkdv(
               tile_tr<D>(qs, qh * 32 + 16 * hh, db * 32, lane), dsf[hh], dkacc[db], 0, 0, 0);
         }
     }
-    if (qt + 1 < qt_end) store(buf ^ 1);
+    if (qt + 1 < qt_end) stats(buf ^ 1);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
   // the two query halves of each key quarter: qh = 1 parks its sums in LDS,
@@ -616,12 +778,26 @@ __global__ __launch_bounds__(NTH) void fa_bwd_reduce(const float* __restrict__ d
 
 bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// pair light and heavy query tiles in one workgroup when the unpaired grid
+// would fit the GPU in one round anyway (then its longest tile sets the time)
+// keys per K/V tile (64: two workgroups per CU; 128: one, 128 KiB of LDS)
+int kv_tile() {
+  const char* env = getenv("ST_FA_BKT");
+  return env && atoi(env) == 128 ? 128 : 64;
+}
+
+int pair_mode(int nq, int64_t heads) {
+  const char* env = getenv("ST_FA_PAIRED");
+  if (env) return atoi(env) ? 1 : 0;
+  return nq >= 4 && nq * heads <= 1024 ? 1 : 0;
+}
+
 }  // namespace
 
 extern "C" int64_t st_flash_attn_workspace_bytes(int64_t B, int64_t S, int64_t H, int64_t Hkv,
                                                  int64_t D, int32_t backward) {
-  const int64_t kv = B * Hkv * S * D * 2;
-  if (!backward) return kv + 256;  // V^T
+  const int64_t kv = B * Hkv * ((S + 15) & ~15) * D * 2;
+  if (!backward) return kv + 256;  // key-permuted V^T
   // Delta [B,H,S] fp32, then fp32 dK and dV partials per query head
   const int64_t dl = (B * H * S * 4 + 255) / 256 * 256;
   return 256 + dl + 2 * B * H * S * D * 4;
@@ -646,16 +822,28 @@ extern "C" int st_flash_attn_fwd(const uint16_t* q, const uint16_t* k, const uin
                     (long long)need);
   hipStream_t s = (hipStream_t)stream;
   uint16_t* vt = (uint16_t*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
-  transpose_heads<<<dim3((unsigned)st::cdiv(S, 64), (unsigned)st::cdiv(D, 64),
-                         (unsigned)(B * Hkv)), NTH, 0, s>>>(v, vt, S, (int)D);
+  const int64_t Sp = (S + 15) & ~15;
+  transpose_heads<<<dim3((unsigned)st::cdiv(Sp, 64), (unsigned)st::cdiv(D, 64),
+                         (unsigned)(B * Hkv)), NTH, 0, s>>>(v, vt, S, Sp, (int)D);
   int rc = st::check_launch("transpose_heads");
   if (rc) return rc;
-  dim3 grid((unsigned)st::cdiv(S, BQ), (unsigned)H, (unsigned)B);
+  const int nq = (int)st::cdiv(S, BQ);
+  const int paired = pair_mode(nq, B * H);
+  dim3 grid((unsigned)((paired ? (nq + 1) / 2 : nq) * H * B));
   const float sl2 = scale * LOG2E;
-  if (D == 128)
-    fa_fwd<128><<<grid, NTH, 0, s>>>(q, k, vt, (int)S, (int)H, (int)Hkv, sl2, out, lse);
+  // paired schedules use two key groups (8 waves) so each SIMD still holds two waves
+  if (D == 128 && paired)
+    fa_fwd<128, 64, 2><<<grid, NTH * 2, 0, s>>>(q, k, vt, (int)S, (int)H, (int)Hkv, sl2, out,
+                                                lse, nq, paired);
+  else if (D == 128)
+    fa_fwd<128, 64, 1><<<grid, NTH, 0, s>>>(q, k, vt, (int)S, (int)H, (int)Hkv, sl2, out, lse,
+                                            nq, paired);
+  else if (paired)
+    fa_fwd<64, 64, 2><<<grid, NTH * 2, 0, s>>>(q, k, vt, (int)S, (int)H, (int)Hkv, sl2, out,
+                                               lse, nq, paired);
   else
-    fa_fwd<64><<<grid, NTH, 0, s>>>(q, k, vt, (int)S, (int)H, (int)Hkv, sl2, out, lse);
+    fa_fwd<64, 64, 1><<<grid, NTH, 0, s>>>(q, k, vt, (int)S, (int)H, (int)Hkv, sl2, out, lse,
+                                           nq, paired);
   return st::check_launch("fa_fwd");
 }
 
@@ -684,18 +872,24 @@ extern "C" int st_flash_attn_bwd(const uint16_t* q, const uint16_t* k, const uin
   float* dk_part = (float*)(base + (B * H * S * 4 + 255) / 256 * 256);
   float* dv_part = dk_part + B * H * S * D;
   const float sl2 = scale * LOG2E;
-  dim3 g1((unsigned)st::cdiv(S, BQ), (unsigned)H, (unsigned)B);
-  dim3 g2((unsigned)st::cdiv(S, KT2), (unsigned)H, (unsigned)B);
+  const int nq = (int)st::cdiv(S, BQ);
+  const int paired = pair_mode(nq, B * H);
+  dim3 g1((unsigned)((paired ? (nq + 1) / 2 : nq) * H * B));
+  dim3 g2((unsigned)(st::cdiv(S, KT2) * H * B));
   if (D == 128) {
-    fa_bwd_dq<128><<<g1, NTH, 0, s>>>(q, k, v, out, dout, lse, (int)S, (int)H, (int)Hkv, sl2,
-                                      scale, delta, dq);
+    if (kv_tile() == 128)
+      fa_bwd_dq<128, 128><<<g1, NTH, 0, s>>>(q, k, v, out, dout, lse, (int)S, (int)H, (int)Hkv,
+                                             sl2, scale, delta, dq, nq, paired);
+    else
+      fa_bwd_dq<128, 64><<<g1, NTH, 0, s>>>(q, k, v, out, dout, lse, (int)S, (int)H, (int)Hkv,
+                                            sl2, scale, delta, dq, nq, paired);
     int rc = st::check_launch("fa_bwd_dq");
     if (rc) return rc;
     fa_bwd_dkdv<128><<<g2, NTH2, 0, s>>>(q, k, v, dout, lse, delta, (int)S, (int)H, (int)Hkv,
                                          sl2, scale, dk_part, dv_part);
   } else {
-    fa_bwd_dq<64><<<g1, NTH, 0, s>>>(q, k, v, out, dout, lse, (int)S, (int)H, (int)Hkv, sl2,
-                                     scale, delta, dq);
+    fa_bwd_dq<64, 64><<<g1, NTH, 0, s>>>(q, k, v, out, dout, lse, (int)S, (int)H, (int)Hkv,
+                                         sl2, scale, delta, dq, nq, paired);
     int rc = st::check_launch("fa_bwd_dq");
     if (rc) return rc;
     fa_bwd_dkdv<64><<<g2, NTH2, 0, s>>>(q, k, v, dout, lse, delta, (int)S, (int)H, (int)Hkv,
