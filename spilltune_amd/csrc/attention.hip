@@ -416,7 +416,7 @@ __device__ __forceinline__ bf16x8 tile_tr(const uint16_t* t, int kb, int nb, int
 // dQ (and Delta = rowsum(dO * O)) per 128-query tile: S^T = K Q^T,
 // P^T = exp2(S^T - lse), dP^T = V dO^T, dS^T = P^T (dP^T - Delta),
 // dQ^T += K^T dS^T; keys up to the diagonal.
-template <int D, int BKT>
+template <int D, int BKT, int G>
 __device__ __forceinline__ void fa_bwd_dq_tile(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ o,
@@ -426,7 +426,9 @@ __device__ __forceinline__ void fa_bwd_dq_tile(
   constexpr int DS = D / 16, DB = D / 32;
   constexpr int LT = BKT * D;           // bf16 per K (or V) tile
   constexpr int PER = BKT * D / 8 / NTH;  // 16-byte chunks per thread per tile
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int grp = (tid >> 6) / 4, wave = (tid >> 6) % 4;  // key group, wave in group
+  const int gtid = tid % NTH;
   const int g = lane >> 5, c = lane & 31;
   const int hk = h / (H / Hkv);
   const int64_t ldt = (int64_t)H * D;  // token-major row stride
@@ -437,6 +439,7 @@ __device__ __forceinline__ void fa_bwd_dq_tile(
   const int myq = q0 + c;
   const bool qok = myq < S;
   const int64_t trow = ((int64_t)b * S + myq) * ldt + (int64_t)h * D;
+  uint16_t* glds = lds + grp * 2 * 2 * LT;  // this group's two K|V buffers
 
   bf16x8 qf[DS], dof[DS];
   float dl = 0.0f;
@@ -457,7 +460,7 @@ __device__ __forceinline__ void fa_bwd_dq_tile(
   }
   dl += __shfl_xor(dl, 32);
   const int64_t srow = (int64_t)(b * H + h) * S;
-  if (g == 0 && qok) delta[srow + myq] = dl;
+  if (grp == 0 && g == 0 && qok) delta[srow + myq] = dl;
   const float lq = qok ? lse[srow + myq] : 0.0f;
 
   f32x16 dqacc[DB];
@@ -468,15 +471,16 @@ __device__ __forceinline__ void fa_bwd_dq_tile(
 
   const int qlast = min(qt * BQ + BQ, S) - 1;
   const int ntiles = qlast / BKT + 1;
+  const int nsteps = (ntiles + G - 1) / G;
   // K and V tiles [key][D] (tswz layout) by direct global -> LDS copies;
   // rows past S read a clamped (finite) row, masked out below
   auto issue = [&](int t, int buf) {
     const int k0 = t * BKT;
-    uint16_t* ks = lds + buf * 2 * LT;
+    uint16_t* ks = glds + buf * 2 * LT;
     uint16_t* vs = ks + LT;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      const int P = i * NTH + tid;
+      const int P = i * NTH + gtid;
       const int row = P / (D / 8);
       const int ch = (P % (D / 8)) ^ (((row & 7) << 1) & (D / 8 - 1));
       const int64_t off = (int64_t)min(k0 + row, S - 1) * D + ch * 8;
@@ -484,53 +488,78 @@ __device__ __forceinline__ void fa_bwd_dq_tile(
       g2lds16(vb + off, vs + (i * NTH + wave * 64) * 8);
     }
   };
-  issue(0, 0);
+  // one 32-key block: S^T, dP^T, dS^T (masked when `edge`), dQ^T += K^T dS^T
+  auto block = [&](const uint16_t* ks, const uint16_t* vs, int jb, int kb0, bool edge) {
+    f32x16 sacc, pacc;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) { sacc[e] = 0.0f; pacc[e] = 0.0f; }
+#pragma unroll
+    for (int s = 0; s < DS; ++s) {
+      sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_row<D>(ks, jb * 32 + c, s, g), qf[s],
+                                                     sacc, 0, 0, 0);
+      pacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_row<D>(vs, jb * 32 + c, s, g), dof[s],
+                                                     pacc, 0, 0, 0);
+    }
+    bf16x8 dsf[2];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      float ds[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int vv = 8 * hh + e;
+        const int key = kb0 + (vv >> 2) * 8 + g * 4 + (vv & 3);
+        const bool keep = !edge || (key <= myq && key < S && qok);
+        const float p = keep ? __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[vv], sl2, -lq)) : 0.0f;
+        ds[e] = p * (pacc[vv] - dl);
+      }
+      dsf[hh] = as_bf16x8(make_uint4(st::pack_bf16x2(ds[0], ds[1]), st::pack_bf16x2(ds[2], ds[3]),
+                                     st::pack_bf16x2(ds[4], ds[5]), st::pack_bf16x2(ds[6], ds[7])));
+    }
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+        dqacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            tile_tr<D>(ks, jb * 32 + 16 * hh, db * 32, lane), dsf[hh], dqacc[db], 0, 0, 0);
+  };
+  if (grp < ntiles) issue(grp, 0);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < ntiles) issue(t + 1, buf ^ 1);
-    const uint16_t* ks = lds + buf * 2 * LT;
+  for (int u = 0; u < nsteps; ++u) {
+    const int buf = u & 1;
+    const int t = u * G + grp;
+    if (t + G < ntiles) issue(t + G, buf ^ 1);
+    const uint16_t* ks = glds + buf * 2 * LT;
     const uint16_t* vs = ks + LT;
     const int k0 = t * BKT;
+    if (t < ntiles) {
 #pragma unroll
-    for (int jb = 0; jb < BKT / 32; ++jb) {
-      const int kb0 = k0 + jb * 32;
-      if (kb0 > q0 + 31 || kb0 >= S) continue;
-      f32x16 sacc, pacc;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) { sacc[e] = 0.0f; pacc[e] = 0.0f; }
-#pragma unroll
-      for (int s = 0; s < DS; ++s) {
-        sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_row<D>(ks, jb * 32 + c, s, g), qf[s],
-                                                       sacc, 0, 0, 0);
-        pacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_row<D>(vs, jb * 32 + c, s, g), dof[s],
-                                                       pacc, 0, 0, 0);
+      for (int jb = 0; jb < BKT / 32; ++jb) {
+        const int kb0 = k0 + jb * 32;
+        if (kb0 > q0 + 31 || kb0 >= S) continue;  // wave-uniform
+        block(ks, vs, jb, kb0, kb0 + 31 > q0 || kb0 + 31 >= S || q0 + 31 >= S);
       }
-      bf16x8 dsf[2];
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        float ds[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int vv = 8 * hh + e;
-          const int key = kb0 + (vv >> 2) * 8 + g * 4 + (vv & 3);
-          const bool keep = key <= myq && key < S && qok;
-          const float p = keep ? __builtin_amdgcn_exp2f(sacc[vv] * sl2 - lq) : 0.0f;
-          ds[e] = p * (pacc[vv] - dl);
-        }
-        dsf[hh] = as_bf16x8(make_uint4(st::pack_bf16x2(ds[0], ds[1]), st::pack_bf16x2(ds[2], ds[3]),
-                                       st::pack_bf16x2(ds[4], ds[5]), st::pack_bf16x2(ds[6], ds[7])));
-      }
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-        for (int db = 0; db < DB; ++db)
-          dqacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-              tile_tr<D>(ks, jb * 32 + 16 * hh, db * 32, lane), dsf[hh], dqacc[db], 0, 0, 0);
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+  }
+  if (G == 2) {  // dQ is additive over keys: group 1 parks, group 0 adds
+    float* park = (float*)lds + wave * 64 * (16 * DB);
+    if (grp == 1) {
+#pragma unroll
+      for (int i = 0; i < DB; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) park[(i * 16 + e) * 64 + lane] = dqacc[i][e];
+    }
+    __syncthreads();
+    if (grp == 0) {
+#pragma unroll
+      for (int i = 0; i < DB; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) dqacc[i][e] += park[(i * 16 + e) * 64 + lane];
+    }
+    __syncthreads();
+    if (grp == 1) return;
   }
   // dQ = scale * dQ^T^T, staged through LDS as query rows, head-major out
   constexpr int LDO = D + 8;
@@ -544,7 +573,8 @@ __device__ __forceinline__ void fa_bwd_dq_tile(
                        st::pack_bf16x2(dqacc[db][4 * v4 + 2] * scale, dqacc[db][4 * v4 + 3] * scale)};
       *(u32x2*)(os + c * LDO + d) = w;
     }
-  __syncthreads();
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_wave_barrier();  // each wave reads back only its own rows
   uint16_t* dqb = dq + ((int64_t)(b * H + h) * S) * D;
   for (int i = lane; i < 32 * (D / 8); i += 64) {
     const int r = i / (D / 8), ch = i % (D / 8);
@@ -556,15 +586,14 @@ __device__ __forceinline__ void fa_bwd_dq_tile(
     }
   }
 }
-
-template <int D, int BKT>
-__global__ __launch_bounds__(NTH, BKT == 64 ? 2 : 1) void fa_bwd_dq(
+template <int D, int BKT, int G>
+__global__ __launch_bounds__(NTH * G, G == 1 && BKT == 64 ? 2 : 1) void fa_bwd_dq(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ o,
     const uint16_t* __restrict__ dout, const float* __restrict__ lse, int S, int H, int Hkv,
     float sl2, float scale, float* __restrict__ delta, uint16_t* __restrict__ dq, int nq,
     int paired) {
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 2 * BKT * D];
+  __shared__ __attribute__((aligned(16))) uint16_t lds[G * 2 * 2 * BKT * D];
   const WgIdx w = wg_index(paired ? (nq + 1) / 2 : nq, H);
   for (int it = 0; it < 1 + paired; ++it) {
     const int qt = pair_tile(w.x, it, nq, paired);
@@ -572,8 +601,8 @@ __global__ __launch_bounds__(NTH, BKT == 64 ? 2 : 1) void fa_bwd_dq(
       if (qt == pair_tile(w.x, 0, nq, paired)) break;
       __syncthreads();
     }
-    fa_bwd_dq_tile<D, BKT>(q, k, v, o, dout, lse, S, H, Hkv, sl2, scale, delta, dq, qt, w.h,
-                           w.b, lds);
+    fa_bwd_dq_tile<D, BKT, G>(q, k, v, o, dout, lse, S, H, Hkv, sl2, scale, delta, dq, qt, w.h,
+                              w.b, lds);
   }
 }
 
@@ -584,21 +613,18 @@ __global__ __launch_bounds__(NTH, BKT == 64 ? 2 : 1) void fa_bwd_dq(
 constexpr int KT2 = 128, QT2 = 64, NTH2 = 512;
 
 template <int D>
-__global__ __launch_bounds__(NTH2, 2) void fa_bwd_dkdv(
+__device__ __forceinline__ void fa_bwd_dkdv_tile(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, int S, int H, int Hkv,
-    float sl2, float scale, float* __restrict__ dk_part, float* __restrict__ dv_part) {
+    float sl2, float scale, float* __restrict__ dk_part, float* __restrict__ dv_part, int kt,
+    int h, int b, uint16_t* lds, float (*lse_s)[QT2], float (*dl_s)[QT2]) {
   constexpr int DS = D / 16, DB = D / 32;
   constexpr int LK = KT2 * D, LQ = QT2 * D;
   constexpr int PERQ = QT2 * D / 8 / NTH2;   // 16-byte chunks per thread per Q (dO) tile
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * LK + 2 * 2 * LQ];
-  __shared__ float lse_s[2][QT2], dl_s[2][QT2];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, c = lane & 31;
   const int kq = wave & 3, qh = wave >> 2;
-  const WgIdx w = wg_index((S + KT2 - 1) / KT2, H);
-  const int kt = w.x, h = w.h, b = w.b;
   const int hk = h / (H / Hkv);
   const int64_t ldt = (int64_t)H * D;
   const uint16_t* qb = q + ((int64_t)(b * H + h) * S) * D;
@@ -750,6 +776,29 @@ __global__ __launch_bounds__(NTH2, 2) void fa_bwd_dkdv(
   }
 }
 
+// key tiles kt and n-1-kt in one workgroup: the causal query range of the two
+// sums to a constant, so every workgroup does the same work
+template <int D>
+__global__ __launch_bounds__(NTH2, 2) void fa_bwd_dkdv(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+    const uint16_t* __restrict__ v, const uint16_t* __restrict__ dout,
+    const float* __restrict__ lse, const float* __restrict__ delta, int S, int H, int Hkv,
+    float sl2, float scale, float* __restrict__ dk_part, float* __restrict__ dv_part, int nk,
+    int paired) {
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * KT2 * D + 2 * 2 * QT2 * D];
+  __shared__ float lse_s[2][QT2], dl_s[2][QT2];
+  const WgIdx w = wg_index(paired ? (nk + 1) / 2 : nk, H);
+  for (int it = 0; it < 1 + paired; ++it) {
+    const int kt = paired ? (it == 0 ? w.x : nk - 1 - w.x) : w.x;
+    if (it == 1) {
+      if (kt == w.x) break;
+      __syncthreads();  // the previous tile's partial sums still occupy LDS
+    }
+    fa_bwd_dkdv_tile<D>(q, k, v, dout, lse, delta, S, H, Hkv, sl2, scale, dk_part, dv_part, kt,
+                        w.h, w.b, lds, lse_s, dl_s);
+  }
+}
+
 // dk[b,hk] = bf16(sum over the group's query heads of dk_part), same for dv
 __global__ __launch_bounds__(NTH) void fa_bwd_reduce(const float* __restrict__ dk_part,
                                                      const float* __restrict__ dv_part,
@@ -780,12 +829,6 @@ bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 // pair light and heavy query tiles in one workgroup when the unpaired grid
 // would fit the GPU in one round anyway (then its longest tile sets the time)
-// keys per K/V tile (64: two workgroups per CU; 128: one, 128 KiB of LDS)
-int kv_tile() {
-  const char* env = getenv("ST_FA_BKT");
-  return env && atoi(env) == 128 ? 128 : 64;
-}
-
 int pair_mode(int nq, int64_t heads) {
   const char* env = getenv("ST_FA_PAIRED");
   if (env) return atoi(env) ? 1 : 0;
@@ -875,25 +918,31 @@ extern "C" int st_flash_attn_bwd(const uint16_t* q, const uint16_t* k, const uin
   const int nq = (int)st::cdiv(S, BQ);
   const int paired = pair_mode(nq, B * H);
   dim3 g1((unsigned)((paired ? (nq + 1) / 2 : nq) * H * B));
-  dim3 g2((unsigned)(st::cdiv(S, KT2) * H * B));
+  const int nk = (int)st::cdiv(S, KT2);
+  const int paired_k = pair_mode(nk, B * H);
+  dim3 g2((unsigned)((paired_k ? (nk + 1) / 2 : nk) * H * B));
   if (D == 128) {
-    if (kv_tile() == 128)
-      fa_bwd_dq<128, 128><<<g1, NTH, 0, s>>>(q, k, v, out, dout, lse, (int)S, (int)H, (int)Hkv,
-                                             sl2, scale, delta, dq, nq, paired);
+    if (paired)
+      fa_bwd_dq<128, 64, 2><<<g1, NTH * 2, 0, s>>>(q, k, v, out, dout, lse, (int)S, (int)H,
+                                                   (int)Hkv, sl2, scale, delta, dq, nq, paired);
     else
-      fa_bwd_dq<128, 64><<<g1, NTH, 0, s>>>(q, k, v, out, dout, lse, (int)S, (int)H, (int)Hkv,
-                                            sl2, scale, delta, dq, nq, paired);
+      fa_bwd_dq<128, 64, 1><<<g1, NTH, 0, s>>>(q, k, v, out, dout, lse, (int)S, (int)H, (int)Hkv,
+                                               sl2, scale, delta, dq, nq, paired);
     int rc = st::check_launch("fa_bwd_dq");
     if (rc) return rc;
     fa_bwd_dkdv<128><<<g2, NTH2, 0, s>>>(q, k, v, dout, lse, delta, (int)S, (int)H, (int)Hkv,
-                                         sl2, scale, dk_part, dv_part);
+                                         sl2, scale, dk_part, dv_part, nk, paired_k);
   } else {
-    fa_bwd_dq<64, 64><<<g1, NTH, 0, s>>>(q, k, v, out, dout, lse, (int)S, (int)H, (int)Hkv,
-                                         sl2, scale, delta, dq, nq, paired);
+    if (paired)
+      fa_bwd_dq<64, 64, 2><<<g1, NTH * 2, 0, s>>>(q, k, v, out, dout, lse, (int)S, (int)H,
+                                                  (int)Hkv, sl2, scale, delta, dq, nq, paired);
+    else
+      fa_bwd_dq<64, 64, 1><<<g1, NTH, 0, s>>>(q, k, v, out, dout, lse, (int)S, (int)H, (int)Hkv,
+                                              sl2, scale, delta, dq, nq, paired);
     int rc = st::check_launch("fa_bwd_dq");
     if (rc) return rc;
     fa_bwd_dkdv<64><<<g2, NTH2, 0, s>>>(q, k, v, dout, lse, delta, (int)S, (int)H, (int)Hkv,
-                                        sl2, scale, dk_part, dv_part);
+                                        sl2, scale, dk_part, dv_part, nk, paired_k);
   }
   int rc = st::check_launch("fa_bwd_dkdv");
   if (rc) return rc;
