@@ -263,11 +263,18 @@ __global__ __launch_bounds__(NTH) void lora_rk_reduce(int64_t Mo, int64_t R, int
   *o = v;
 }
 
+int env_int(const char* name, int dflt) {
+  const char* e = getenv(name);
+  return e ? atoi(e) : dflt;
+}
+
 int rk_ksplit(int64_t Mo, int64_t Kc) {
-  // ~512 workgroups, each streaming at least 512 contraction elements (8 chunks)
+  // enough workgroups to keep loads in flight on every CU, each streaming at
+  // least `chunk` contraction elements
+  static const int target = env_int("ST_RK_WG", 512), chunk = env_int("ST_RK_CHUNK", 512);
   int64_t tiles = st::cdiv(Mo, RK_BM);
-  int64_t ks = st::cdiv(512, tiles);
-  int64_t maxk = st::cdiv(Kc, 512);
+  int64_t ks = st::cdiv(target, tiles);
+  int64_t maxk = st::cdiv(Kc, chunk);
   if (ks > maxk) ks = maxk;
   if (ks < 1) ks = 1;
   return (int)ks;

@@ -61,6 +61,32 @@ __device__ __forceinline__ int swz(int row, int c) {
   return row * 8 + (c ^ (row & 7) ^ ((row >> 3) & 7));
 }
 
+// DGRAD_Q4 B tile: row n (contraction) of BN bf16 = BN/8 16-byte chunks;
+// chunk c stored at c ^ 2*(n & 7) so that both the 16-byte dequant stores of
+// 8 consecutive rows and the transposing reads of 4 rows x 32 bytes hit
+// distinct banks.  Index in 16-byte units; BN is a template constant.
+#define dswz(n, c) ((n) * (BN / 8) + ((c) ^ (((n) & 7) << 1)))
+
+// Transposed B operand from the [n][k] tile: lane (column k = kc + lane%32,
+// half g = lane/32) gets rows n = n0 + 8g + s for s = 0..7.
+// ds_read_b64_tr_b16: within 16 lanes, lane i receives element (i % 4) of the
+// 4-element rows supplied by lanes 4j + i/4, j = 0..3.
+template <int BN>
+__device__ __forceinline__ bf16x8 b_tr_impl(const uint4* bs, int n0, int kc, int lane) {
+  typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
+  const int G = lane >> 4, i = lane & 15, g = lane >> 5;
+  const int col = kc + 16 * (G & 1) + 4 * (i & 3);
+  v4bf r[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int n = n0 + 8 * g + 4 * h + (i >> 2);
+    const uint16_t* e = (const uint16_t*)(bs + dswz(n, col >> 3)) + (col & 7);
+    r[h] = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) v4bf*)e);
+  }
+  return __builtin_shufflevector(r[0], r[1], 0, 1, 2, 3, 4, 5, 6, 7);
+}
+#define b_tr(bs, n0, kc, lane) b_tr_impl<BN>(bs, n0, kc, lane)
+
 __device__ __forceinline__ unsigned nib(uint32_t w, int e, int hi_first) {
   return (w >> (4 * (e ^ hi_first))) & 15u;
 }
@@ -136,7 +162,7 @@ struct Tile {
   static constexpr bool Q4 = (MODE == FWD_Q4 || MODE == DGRAD_Q4);
   static constexpr bool DGRAD = (MODE == DGRAD_Q4 || MODE == DGRAD_BF16);
   static constexpr int BF_IT = BN * 8 / NT;        // FWD_BF16 chunks per thread
-  static constexpr int QB = BN * BK / (NT * 8);    // dgrad: contraction rows per thread block
+  static constexpr int QB = BN * BK / (NT * 8);    // DGRAD_BF16: contraction rows per thread block
   static constexpr int LDS_CHUNKS = 2 * (BM + BN) * 8;
 };
 
@@ -146,7 +172,6 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
   constexpr int NT = TL::NT;
   constexpr int WM = TL::WM, WN = TL::WN, FM = TL::FM, FN = TL::FN;
   __shared__ uint4 lds[TL::LDS_CHUNKS];
-  __shared__ float lut_s[16];  // codebook for the transposed (dgrad) dequant
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / TL::WAVES_N, wn = wave % TL::WAVES_N;
@@ -202,20 +227,27 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
   // B operand source.  FWD_Q4: thread owns EPT consecutive weights of one W row.
   constexpr int TPR = NT / BN;          // threads per W row (1 or 2)
   constexpr int EPT = BK / TPR;         // elements per thread per k-step (64 or 32)
-  constexpr int WQ = TL::Q4 ? (TL::DGRAD ? TL::QB : EPT / 32) : (TL::DGRAD ? TL::QB : TL::BF_IT);
+  // DGRAD_Q4: the B tile is W[n][k] for BK contraction rows n and BN output
+  // columns k, kept in that (natural) orientation; each thread dequantises
+  // 32 consecutive k of one row n, and the MFMA operand is read transposed.
+  constexpr int DTR = BN / 32;          // DGRAD_Q4 threads per contraction row
+  constexpr int WQ = MODE == FWD_Q4 ? EPT / 32 : MODE == DGRAD_Q4 ? 1
+                     : (TL::DGRAD ? TL::QB : TL::BF_IT);
   constexpr int PB = BN / 8;
   const int brow = tid / TPR, bsub = tid % TPR;       // FWD_Q4 mapping
-  const int pb = tid % PB, qb = tid / PB;             // DGRAD mapping
+  const int drow = tid / DTR, dsub = tid % DTR;       // DGRAD_Q4 mapping
+  const int pb = tid % PB, qb = tid / PB;             // DGRAD_BF16 mapping
   uint32_t w_row = 0;
   if constexpr (MODE == FWD_Q4) {
     int64_t n = p0 + brow;
     w_row = n < p.P ? (uint32_t)(n * p.ldw + bsub * EPT) : kOOB;  // element index at k = 0
   }
+  const bool dcol_ok = p0 + dsub * 32 < p.P;
+  static_assert(MODE != DGRAD_Q4 || NT / DTR == BK, "DGRAD_Q4: one thread row per contraction row");
 
   struct WRegs {
     uint4 q[WQ];
-    uint32_t d[TL::DGRAD && TL::Q4 ? TL::QB : 1];
-    float s[TL::Q4 ? (TL::DGRAD ? TL::QB : 1) : 1];
+    float s[1];
   };
   auto load_W = [&](int kt, WRegs& w) {
     if constexpr (MODE == FWD_Q4) {
@@ -233,6 +265,12 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
         int k = kt * BK + c * 8;
         w.q[i] = ld16(rsW, (n < p.P && k < p.Q) ? (uint32_t)((n * p.ldw + k) * 2) : kOOB);
       }
+    } else if constexpr (MODE == DGRAD_Q4) {
+      const int64_t n = (int64_t)kt * BK + drow;
+      const bool ok = dcol_ok && n < p.Q;
+      const int64_t e = n * p.ldw + p0 + dsub * 32;   // 32-aligned: one uint4, one scale
+      w.q[0] = ld16(rsW, ok ? (uint32_t)(e >> 1) : kOOB);
+      w.s[0] = __builtin_bit_cast(float, ld4(rsS, ok ? (uint32_t)((e >> 7) * 4) : kOOB));
     } else {
       int64_t pc = p0 + pb * 8;
 #pragma unroll
@@ -240,12 +278,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
         int64_t q = (int64_t)kt * BK + qb * TL::QB + i;
         bool ok = pc < p.P && q < p.Q;
         int64_t e = q * p.ldw + pc;
-        if constexpr (MODE == DGRAD_Q4) {
-          w.d[i] = ld4(rsW, ok ? (uint32_t)(e >> 1) : kOOB);
-          w.s[i] = __builtin_bit_cast(float, ld4(rsS, ok ? (uint32_t)((e >> 7) * 4) : kOOB));
-        } else {
-          w.q[i] = ld16(rsW, ok ? (uint32_t)(e * 2) : kOOB);
-        }
+        w.q[i] = ld16(rsW, ok ? (uint32_t)(e * 2) : kOOB);
       }
     }
   };
@@ -265,6 +298,12 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
         deq8(word, tbl, p.hi_first, o);
         bs[swz(brow, (bsub * EPT) / 8 + ch)] = make_uint4(o[0], o[1], o[2], o[3]);
       }
+    } else if constexpr (MODE == DGRAD_Q4) {
+      const uint4 q = w.q[0];
+      const uint32_t word = part == 0 ? q.x : part == 1 ? q.y : part == 2 ? q.z : q.w;
+      uint32_t o[4];
+      deq8(word, tbl, p.hi_first, o);
+      bs[dswz(drow, dsub * 4 + part)] = make_uint4(o[0], o[1], o[2], o[3]);
     } else if constexpr (MODE == FWD_BF16) {
 #pragma unroll
       for (int i = 0; i < WQ; ++i) {
@@ -280,13 +319,9 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
         float v[TL::QB];
 #pragma unroll
         for (int i = 0; i < TL::QB; ++i) {
-          if constexpr (MODE == DGRAD_Q4)
-            v[i] = lut_s[nib(w.d[i], j, p.hi_first)] * w.s[i];
-          else {
-            uint32_t word = (j >> 1) == 0 ? w.q[i].x : (j >> 1) == 1 ? w.q[i].y
-                            : (j >> 1) == 2 ? w.q[i].z : w.q[i].w;
-            v[i] = st::bf16_to_f32((uint16_t)(word >> (16 * (j & 1))));
-          }
+          uint32_t word = (j >> 1) == 0 ? w.q[i].x : (j >> 1) == 1 ? w.q[i].y
+                          : (j >> 1) == 2 ? w.q[i].z : w.q[i].w;
+          v[i] = st::bf16_to_f32((uint16_t)(word >> (16 * (j & 1))));
         }
         const int prow = pb * 8 + j;
         if constexpr (TL::QB == 8) {
@@ -300,7 +335,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
     }
   };
   auto prep_B = [&](const WRegs& w) {
-    if constexpr (MODE == FWD_Q4) tbl = make_tbl(p.lut, w.s[0]);
+    if constexpr (MODE == FWD_Q4 || MODE == DGRAD_Q4) tbl = make_tbl(p.lut, w.s[0]);
   };
 
   f32x16 acc[FM][FN];
@@ -326,7 +361,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
     store_A(as_n, xr);
     load_A(kt + 2, xr);
     load_W(kt + 2, wfar);
-    if (new_group) prep_B(wnext);
+    if (new_group || MODE == DGRAD_Q4) prep_B(wnext);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const int c = 2 * s + (lane >> 5);
@@ -335,8 +370,12 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
       for (int i = 0; i < FM; ++i)
         a[i] = __builtin_bit_cast(bf16x8, as[swz(wm * WM + i * 32 + (lane & 31), c)]);
 #pragma unroll
-      for (int j = 0; j < FN; ++j)
-        b[j] = __builtin_bit_cast(bf16x8, bs[swz(wn * WN + j * 32 + (lane & 31), c)]);
+      for (int j = 0; j < FN; ++j) {
+        if constexpr (MODE == DGRAD_Q4)
+          b[j] = b_tr(bs, s * 16, wn * WN + j * 32, lane);
+        else
+          b[j] = __builtin_bit_cast(bf16x8, bs[swz(wn * WN + j * 32 + (lane & 31), c)]);
+      }
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -353,7 +392,6 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
   load_A(0, xr);
   load_W(0, w0);
   load_W(1, w1);
-  if (TL::Q4 && TL::DGRAD && tid < 16) lut_s[tid] = p.lut.v[tid];
   __syncthreads();
   store_A(As(0), xr);
   prep_B(w0);
@@ -460,10 +498,11 @@ int launch(const GemmParams& p, hipStream_t stream) {
 }
 
 // 256x256 (8 waves) halves the dequant work per MFMA but needs enough tiles to
-// cover the 256 CUs; the transposed-dequant (dgrad) pass stays on 128x128.
+// cover the 256 CUs.
 int tile_choice(int mode, int64_t M, int64_t P) {
   const char* env = getenv("ST_GEMM_TILE");
   if (env) return atoi(env);
+  // the transposed-operand dgrad runs out of registers at 256x256 (8 waves)
   if (mode == FWD_Q4 && st::cdiv(M, 256) * st::cdiv(P, 256) >= 192) return 256;
   return 128;
 }
@@ -474,7 +513,8 @@ int dispatch(const GemmParams& p, hipStream_t stream) {
   if constexpr (MODE == FWD_Q4 || MODE == DGRAD_Q4) {
     const int t = tile_choice(MODE, p.M, p.P);
     if (t == 256) return launch<MODE, 256, 256, 8>(p, stream);
-    if (t == 2564) return launch<MODE, 256, 256, 4>(p, stream);
+    if constexpr (MODE == FWD_Q4)
+      if (t == 2564) return launch<MODE, 256, 256, 4>(p, stream);
   }
   return launch<MODE, 128, 128, 4>(p, stream);
 }
