@@ -106,10 +106,11 @@ def _rotate(x, cos, sin):
 
 
 def dense_block(hidden, rotary_tables, mask, *, heads, kv_heads, head_dim, eps,
-                weights: dict, loras: dict):
+                weights: dict, loras: dict, feed_forward=None):
     """One Llama decoder block (dense.py:120-153); ``weights`` holds bf16 matrices
     keyed ``<proj>.weight`` plus the two norm vectors, ``loras`` maps projection
-    names to :class:`Lora` (absent projections have no adapter)."""
+    names to :class:`Lora` (absent projections have no adapter).  A
+    ``feed_forward(x, weights)`` replaces the SwiGLU MLP (dense.py:152)."""
     def linear(x, name):
         return lora_linear(x, weights[name + ".weight"], loras.get(name))
 
@@ -134,6 +135,8 @@ def dense_block(hidden, rotary_tables, mask, *, heads, kv_heads, head_dim, eps,
     x = residual + linear(attended, "self_attn.o_proj")
     residual = x
     x = rms(x, weights["post_attention_layernorm.weight"], eps)
+    if feed_forward is not None:
+        return residual + feed_forward(x, weights)
     act = F.silu(linear(x, "mlp.gate_proj")) * linear(x, "mlp.up_proj")
     return residual + linear(act, "mlp.down_proj")
 

@@ -58,8 +58,8 @@ def _weight(weights, name):
 def dense_block(hidden_states, position_embeddings, attention_mask, *, heads, kv_heads, head_dim,
                 eps, lora_q=None, lora_k=None, lora_v=None, lora_o=None, lora_gate=None,
                 lora_up=None, lora_down=None, qk_norm=False, feed_forward=None, **weights):
-    if qk_norm or feed_forward is not None:
-        raise ValueError("unsupported_capability: qk_norm/custom feed-forward not on the HIP path")
+    if qk_norm:
+        raise ValueError("unsupported_capability: qk_norm not on the HIP path")
     if attention_mask is not None and not isinstance(attention_mask, CausalMask):
         raise ValueError("unsupported_capability: only the causal mask marker is supported")
     B, S, Hd = hidden_states.shape
@@ -84,6 +84,8 @@ def dense_block(hidden_states, position_embeddings, attention_mask, *, heads, kv
     h1 = ops.q4_lora_linear(attended, _weight(weights, "self_attn.o_proj"), [lora_o], residual=residual)
 
     xn2 = ops.rms_norm(h1, weights["post_attention_layernorm.weight"], eps)
+    if feed_forward is not None:  # e.g. the MoE block (dense.py:152)
+        return (h1 + feed_forward(xn2.view(B, S, Hd), weights).reshape(B * S, Hd)).view(B, S, Hd)
     wg, wu = _weight(weights, "mlp.gate_proj"), _weight(weights, "mlp.up_proj")
     gu = ops.concat_rows([wg, wu])
     loras_gu = [lora_gate, lora_up]

@@ -315,3 +315,64 @@ def test_moe_ffn_fwd_bwd_vs_oracle(dev, oracle_codec, T, H, I, E, k, norm, use_l
         for got, leaf, name in ((lgu.A.grad, leaves[0], "A_gu"), (lgu.B.grad, leaves[1], "B_gu"),
                                 (ld.A.grad, leaves[2], "A_d"), (ld.B.grad, leaves[3], "B_d")):
             assert _cos(got, leaf.grad) > 0.999, name
+
+
+def test_dense_block_with_moe_feed_forward(dev, oracle_codec):
+    """A Qwen3-MoE-style decoder block: the HIP dense functional with the MoE
+    feed-forward hook (dense.py:152) vs the oracle block with the oracle MoE."""
+    import functools
+    from oracle import layer as OL
+    from spilltune_amd import dense, ops
+    g = torch.Generator().manual_seed(77)
+    B, S, H, heads, kv, D, E, I, k, r = 1, 96, 256, 4, 2, 64, 8, 128, 2, 8
+    exact, wts = {}, {}
+    for name, shape in (("self_attn.q_proj", (heads * D, H)), ("self_attn.k_proj", (kv * D, H)),
+                        ("self_attn.v_proj", (kv * D, H)), ("self_attn.o_proj", (H, heads * D))):
+        w32 = (torch.randn(shape, generator=g) * 0.02).numpy()
+        payload, scales = oracle_codec.encode_nf4(w32)
+        bits = np.asarray(oracle_codec.decode4(payload, scales, w32.size, lut=oracle_codec.NF4_LUT),
+                          dtype=np.uint16)
+        exact[name + ".weight"] = torch.from_numpy(bits.astype(np.int16)).view(BF).view(shape)
+        wts[name + ".weight"] = ops.Q4Weight(torch.from_numpy(payload).to(dev),
+                                             torch.from_numpy(scales).to(dev), shape, "nf4-g128")
+    for nm in ("input_layernorm.weight", "post_attention_layernorm.weight"):
+        exact[nm] = (1 + 0.05 * torch.randn(H, generator=g)).to(BF)
+        wts[nm] = exact[nm].to(dev)
+    router = (torch.randn(E, H, generator=g) * 3 * H ** -0.5).to(BF)   # well-separated logits
+    qgu, Wgu = _experts(oracle_codec, torch.randn(E, 2 * I, H, generator=g) * 0.02, dev)
+    qd, Wd = _experts(oracle_codec, torch.randn(E, H, I, generator=g) * 0.02, dev)
+    wts.update({"mlp.gate.weight": router.to(dev), "mlp.experts.gate_up_proj": qgu,
+                "mlp.experts.down_proj": qd})
+    lgu = moe.make_expert_lora("mlp.experts.gate_up_proj", E, H, 2 * I, rank=r, alpha=16.0,
+                               device=dev, segments=2, generator=g, b_std=0.02)
+    ld = moe.make_expert_lora("mlp.experts.down_proj", E, I, H, rank=r, alpha=16.0, device=dev,
+                              generator=g, b_std=0.02)
+    hidden = torch.randn(B, S, H, generator=g).to(BF)
+    dy = torch.randn(B, S, H, generator=g).to(BF)
+    cos, sin = OL.rotary(B, S, D, 500000.0, BF)
+    # HIP path
+    ff = functools.partial(moe.moe_feed_forward, num_experts=E, top_k=k, norm_topk_prob=True,
+                           lora_gate_up=lgu, lora_down=ld)
+    h = hidden.to(dev).requires_grad_(True)
+    out = dense.dense_block(h, (cos.to(dev), sin.to(dev)), dense.CausalMask(B, S), heads=heads,
+                            kv_heads=kv, head_dim=D, eps=1e-6, feed_forward=ff, **wts)
+    out.backward(dy.to(dev))
+    torch.cuda.synchronize()
+    # oracle
+    leaves = [t.detach().cpu().clone().requires_grad_(True) for t in (lgu.A, lgu.B, ld.A, ld.B)]
+    loras = {"gate": (leaves[0][:, :r], leaves[1][:, :I], lgu.scale),
+             "up": (leaves[0][:, r:], leaves[1][:, I:], lgu.scale),
+             "down": (leaves[2], leaves[3], ld.scale)}
+    ffr = lambda x, w: M_ffn(x, router, Wgu, Wd, k, loras)
+    x = hidden.clone().requires_grad_(True)
+    ref = OL.dense_block(x, (cos, sin), OL.causal_mask(B, S, BF), heads=heads, kv_heads=kv,
+                         head_dim=D, eps=1e-6, weights=exact, loras={}, feed_forward=ffr)
+    ref.backward(dy)
+    assert _rel(out, ref) < 2e-2
+    assert _cos(h.grad, x.grad) > 0.999
+    for got, leaf in zip((lgu.A.grad, lgu.B.grad, ld.A.grad, ld.B.grad), leaves):
+        assert _cos(got, leaf.grad) > 0.999
+
+
+def M_ffn(x, router, Wgu, Wd, k, loras):
+    return OM.qwen3_moe_ffn(x, router, Wgu, Wd, top_k=k, norm_topk_prob=True, loras=loras)
