@@ -44,6 +44,50 @@ __device__ __forceinline__ float bf16r(float x) { return bf16_to_f32(f32_to_bf16
 
 __host__ __device__ __forceinline__ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Buffer-resource loads: 32-bit byte offsets into a buffer of `bytes` bytes
+// (below 2 GiB); an offset at or beyond the extent (kOOB is beyond every one)
+// reads as zero, so tiles need no bounds branches.
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+constexpr uint32_t kOOB = 0x80000000u;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* ptr, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(ptr), (short)0, (int)bytes,
+                                           0x00020000);
+}
+__device__ __forceinline__ uint4 ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint32_t ld4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+}
+
+// Transposed-operand tile: rows n (the contraction) of BN bf16 held as BN/8
+// 16-byte chunks, chunk c of row n at n*(BN/8) + (c ^ 2*(n & 7)).  Both the
+// 16-byte stores of one row per quarter-wave and the transposing operand
+// reads below hit distinct banks.  Index in 16-byte units.
+template <int BN>
+__device__ __forceinline__ int trswz(int n, int c) {
+  return n * (BN / 8) + (c ^ ((n & 7) << 1));
+}
+// MFMA 32x32x16 operand from such a tile: lane (column kc + lane%32, half
+// g = lane/32) gets rows n0 + 8g + s, s = 0..7.  ds_read_b64_tr_b16: within
+// 16 lanes, lane i receives element (i % 4) of the 4-element rows supplied
+// by lanes 4j + i/4, j = 0..3.
+template <int BN>
+__device__ __forceinline__ bf16x8 tr_operand(const uint4* bs, int n0, int kc, int lane) {
+  typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
+  const int G = lane >> 4, i = lane & 15, g = lane >> 5;
+  const int col = kc + 16 * (G & 1) + 4 * (i & 3);
+  v4bf r[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int n = n0 + 8 * g + 4 * h + (i >> 2);
+    const uint16_t* e = (const uint16_t*)(bs + trswz<BN>(n, col >> 3)) + (col & 7);
+    r[h] = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) v4bf*)e);
+  }
+  return __builtin_shufflevector(r[0], r[1], 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
 // XCD-aware block remap: consecutive logical tiles land on the same XCD so they
 // share that XCD's L2 (blocks are dispatched round-robin over the 8 XCDs).
 __device__ __forceinline__ int64_t xcd_remap(int64_t b, int64_t nb) {

@@ -104,140 +104,136 @@ __global__ __launch_bounds__(NTH) void lora_reduce(int64_t Mo, int64_t No, int k
 // at bf16 matrix-core rate.
 constexpr int RK_BM = 128, RK_BK = 64, RK_RP = 64;
 constexpr int RK_LD = RK_BK + 8;  // bf16 per LDS row (144 bytes: 16-byte aligned, bank-spread)
+constexpr int RK_PF = 3;          // chunks of loads in flight per workgroup
 
-// Streaming pipeline: the next chunk's G (4 x 16 bytes per thread) and S are
-// loaded into registers before the current chunk's MFMAs, so each workgroup
-// keeps its loads in flight while it computes.
-template <bool COL>
+// Streaming pipeline: a ring of RK_PF chunks of G (4 x 16 bytes per thread)
+// and S lives in registers; as soon as a chunk is staged into LDS its slot is
+// refilled with the chunk RK_PF steps ahead, so each workgroup keeps about
+// RK_PF x 16 KiB of loads in flight while it computes.  Loads go through
+// buffer resources with 32-bit offsets (operand extents below 2 GiB, checked
+// by the host); rows or chunks out of range read as zero.  The host routes
+// only 16-byte-aligned G with rows (ROW form: contraction; COL form: output)
+// a multiple of 8 elements here.
+template <bool COL, bool SK1, int NB>
 __global__ __launch_bounds__(NTH) void lora_rk(int64_t Mo, int64_t R, int64_t Kc,
                                               const uint16_t* __restrict__ G, int64_t ldg,
-                                              const float* __restrict__ S, int64_t ssk,
-                                              int64_t ssj, int64_t klen, int vec,
-                                              float* __restrict__ part) {
-  __shared__ __attribute__((aligned(16))) uint16_t Gs[RK_BM * RK_LD];      // [m][k]
+                                              int64_t g_bytes, const float* __restrict__ S,
+                                              int64_t ssk, int64_t ssj, int64_t s_bytes,
+                                              int64_t klen, float* __restrict__ part) {
+  // ROW: [m][k] rows of RK_LD; COL: [k][m] in the transposed-operand layout
+  __shared__ __attribute__((aligned(16))) uint16_t Gs[RK_BM * RK_LD];
   __shared__ __attribute__((aligned(16))) uint16_t Ss[2 * RK_RP * RK_LD];  // [hi|lo][j][k]
+  constexpr int RP = NB * 32;            // staged S columns
+  constexpr int SIT = RK_BK * RP / NTH;  // S values per thread per chunk (8 or 16)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t m0 = (int64_t)blockIdx.x * RK_BM;
-  const int64_t kb = (int64_t)blockIdx.y * klen;
-  const int64_t ke = kb + klen < Kc ? kb + klen : Kc;
-  const int nb = R > 32 ? 2 : 1;
-  const int RP = nb * 32;              // staged S columns
-  const int SIT = RK_BK * RP / NTH;    // S values per thread per chunk (8 or 16)
-  f32x16 acc[2];
+  const int kb = (int)((int64_t)blockIdx.y * klen);
+  const int ke = (int)(kb + klen < Kc ? kb + klen : Kc);
+  const auto rsG = st::make_rsrc(G, g_bytes);
+  const auto rsS = st::make_rsrc(S, s_bytes);
+  const uint32_t ldg2 = (uint32_t)ldg * 2, ssk4 = (uint32_t)ssk * 4, ssj4 = (uint32_t)ssj * 4;
+  f32x16 acc[NB];
 #pragma unroll
-  for (int c = 0; c < 2; ++c)
+  for (int c = 0; c < NB; ++c)
 #pragma unroll
     for (int v = 0; v < 16; ++v) acc[c][v] = 0.0f;
 
-  uint4 gr[4];
-  float sr[16];
-  auto load = [&](int64_t k0) {
-    if (!COL) {  // 128 rows x 64 contraction: 8 chunks of 8 per row, 4 chunks per thread
+  // G: per-thread byte offset at contraction 0 (kOOB beyond Mo) and the
+  // contraction offset of each of its four 16-byte pieces within a step
+  uint32_t gbase[4];
+  int gk[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int id = tid + i * NTH, row = id >> 3, c = id & 7;
-        const int64_t m = m0 + row, k = k0 + c * 8;
-        if (vec && m < Mo && k + 8 <= ke) {
-          gr[i] = *(const uint4*)(G + m * ldg + k);
-        } else {
-          uint32_t w[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            uint32_t lo = (m < Mo && k + 2 * e < ke) ? G[m * ldg + k + 2 * e] : 0u;
-            uint32_t hi = (m < Mo && k + 2 * e + 1 < ke) ? G[m * ldg + k + 2 * e + 1] : 0u;
-            w[e] = lo | (hi << 16);
-          }
-          gr[i] = make_uint4(w[0], w[1], w[2], w[3]);
-        }
-      }
+  for (int i = 0; i < 4; ++i) {
+    if (!COL) {  // 128 rows x 64 contraction: 8 pieces of 8 per row, 4 pieces per thread
+      const int id = tid + i * NTH, row = id >> 3, c = id & 7;
+      const int64_t m = m0 + row;
+      gbase[i] = m < Mo ? (uint32_t)(m * ldg * 2) + c * 16 : st::kOOB;
+      gk[i] = c * 8;
     } else {  // 64 contraction rows x 128 columns: 4 rows x 8 columns per thread
-      const int kg = tid >> 4, mg = tid & 15;
-      const int64_t m = m0 + mg * 8;
+      const int64_t m = m0 + (tid & 15) * 8;
+      gbase[i] = m < Mo ? (uint32_t)(m * 2) : st::kOOB;
+      gk[i] = (tid >> 4) * 4 + i;
+    }
+  }
+  // S value i of a thread: (contraction kk, column j).  SK1 (S contiguous
+  // along the contraction): kk = tid % 64, j = tid / 64 + 4i; otherwise
+  // j = tid % RP, kk = tid / RP + (NTH / RP) i.
+  auto s_kk = [&](int i) { return SK1 ? (tid & 63) : tid / RP + (NTH / RP) * i; };
+  auto s_j = [&](int i) { return SK1 ? (tid >> 6) + 4 * i : tid % RP; };
+
+  uint4 gr[RK_PF][4];
+  float sr[RK_PF][SIT];
+  auto load = [&](int k0, uint4 (&g)[4], float (&sv)[SIT]) {
 #pragma unroll
-      for (int h = 0; h < 4; ++h) {
-        const int64_t k = k0 + kg * 4 + h;
-        if (vec && k < ke && m + 8 <= Mo) {
-          gr[h] = *(const uint4*)(G + k * ldg + m);
-        } else {
-          uint32_t w[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            uint32_t lo = (k < ke && m + 2 * e < Mo) ? G[k * ldg + m + 2 * e] : 0u;
-            uint32_t hi = (k < ke && m + 2 * e + 1 < Mo) ? G[k * ldg + m + 2 * e + 1] : 0u;
-            w[e] = lo | (hi << 16);
-          }
-          gr[h] = make_uint4(w[0], w[1], w[2], w[3]);
-        }
-      }
+    for (int i = 0; i < 4; ++i) {
+      const int k = k0 + gk[i];
+      uint32_t off = st::kOOB;
+      if (gbase[i] != st::kOOB && k < ke)
+        off = COL ? gbase[i] + (uint32_t)k * ldg2 : gbase[i] + (uint32_t)k0 * 2;
+      g[i] = st::ld16(rsG, off);
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      if (i >= SIT) break;
-      const int e = tid + i * NTH;
-      int kk, j;
-      if (ssk == 1) { kk = e % RK_BK; j = e / RK_BK; } else { j = e % RP; kk = e / RP; }
-      const int64_t k = k0 + kk;
-      sr[i] = (k < ke && j < R) ? S[k * ssk + j * ssj] : 0.0f;
+    for (int i = 0; i < SIT; ++i) {
+      const int k = k0 + s_kk(i), j = s_j(i);
+      const uint32_t off =
+          (k < ke && j < R) ? (uint32_t)k * ssk4 + (uint32_t)j * ssj4 : st::kOOB;
+      sv[i] = __builtin_bit_cast(float, st::ld4(rsS, off));
     }
   };
-  auto store = [&]() {
+  auto store = [&](const uint4 (&g)[4], const float (&sv)[SIT]) {
     if (!COL) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int id = tid + i * NTH, row = id >> 3, c = id & 7;
-        *(uint4*)&Gs[row * RK_LD + c * 8] = gr[i];
+        *(uint4*)&Gs[row * RK_LD + c * 8] = g[i];
       }
-    } else {
+    } else {  // [contraction][column] as loaded; the MFMA operand is read transposed
       const int kg = tid >> 4, mg = tid & 15;
-      const uint32_t r0[4] = {gr[0].x, gr[0].y, gr[0].z, gr[0].w};
-      const uint32_t r1[4] = {gr[1].x, gr[1].y, gr[1].z, gr[1].w};
-      const uint32_t r2[4] = {gr[2].x, gr[2].y, gr[2].z, gr[2].w};
-      const uint32_t r3[4] = {gr[3].x, gr[3].y, gr[3].z, gr[3].w};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        // column m+e: rows (k, k+1) and (k+2, k+3) as two bf16 pairs
-        const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-        const uint32_t p01 = __builtin_amdgcn_perm(r1[e >> 1], r0[e >> 1], sel);
-        const uint32_t p23 = __builtin_amdgcn_perm(r3[e >> 1], r2[e >> 1], sel);
-        *(uint2*)&Gs[(mg * 8 + e) * RK_LD + kg * 4] = make_uint2(p01, p23);
-      }
+      for (int h = 0; h < 4; ++h) ((uint4*)Gs)[st::trswz<RK_BM>(kg * 4 + h, mg)] = g[h];
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      if (i >= SIT) break;
-      const int e = tid + i * NTH;
-      int kk, j;
-      if (ssk == 1) { kk = e % RK_BK; j = e / RK_BK; } else { j = e % RP; kk = e / RP; }
-      const uint16_t hb = st::f32_to_bf16(sr[i]);
-      const uint16_t lb = st::f32_to_bf16(sr[i] - st::bf16_to_f32(hb));
+    for (int i = 0; i < SIT; ++i) {
+      const int kk = s_kk(i), j = s_j(i);
+      const uint16_t hb = st::f32_to_bf16(sv[i]);
+      const uint16_t lb = st::f32_to_bf16(sv[i] - st::bf16_to_f32(hb));
       Ss[j * RK_LD + kk] = hb;
       Ss[(RK_RP + j) * RK_LD + kk] = lb;
     }
   };
 
-  if (kb < ke) load(kb);
-  for (int64_t k0 = kb; k0 < ke; k0 += RK_BK) {
-    store();
-    __syncthreads();
-    if (k0 + RK_BK < ke) load(k0 + RK_BK);
 #pragma unroll
-    for (int s = 0; s < RK_BK / 16; ++s) {
-      const int ko = s * 16 + (lane >> 5) * 8;
-      const bf16x8 a = *(const bf16x8*)&Gs[(wave * 32 + (lane & 31)) * RK_LD + ko];
+  for (int c = 0; c < RK_PF; ++c)
+    if (kb + c * RK_BK < ke) load(kb + c * RK_BK, gr[c], sr[c]);
+  for (int kg = kb; kg < ke; kg += RK_PF * RK_BK) {
 #pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        if (c >= nb) break;
+    for (int c = 0; c < RK_PF; ++c) {
+      const int k0 = kg + c * RK_BK;
+      if (k0 >= ke) break;
+      store(gr[c], sr[c]);
+      __syncthreads();
+      if (k0 + RK_PF * RK_BK < ke) load(k0 + RK_PF * RK_BK, gr[c], sr[c]);
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const bf16x8 b = *(const bf16x8*)&Ss[(h * RK_RP + c * 32 + (lane & 31)) * RK_LD + ko];
-          acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[c], 0, 0, 0);
-        }
+      for (int s = 0; s < RK_BK / 16; ++s) {
+        const int ko = s * 16 + (lane >> 5) * 8;
+        const bf16x8 a =
+            COL ? st::tr_operand<RK_BM>((const uint4*)Gs, s * 16, wave * 32, lane)
+                : *(const bf16x8*)&Gs[(wave * 32 + (lane & 31)) * RK_LD + ko];
+#pragma unroll
+        for (int cc = 0; cc < NB; ++cc)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const bf16x8 b =
+                *(const bf16x8*)&Ss[(h * RK_RP + cc * 32 + (lane & 31)) * RK_LD + ko];
+            acc[cc] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[cc], 0, 0, 0);
+          }
       }
+      __syncthreads();
     }
-    __syncthreads();
   }
   float* dst = part + (int64_t)blockIdx.y * Mo * R;
-  for (int c = 0; c < nb; ++c) {
+#pragma unroll
+  for (int c = 0; c < NB; ++c) {
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       const int64_t m = m0 + wave * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
@@ -254,8 +250,19 @@ __global__ __launch_bounds__(NTH) void lora_rk_reduce(int64_t Mo, int64_t R, int
                                                      int64_t so_j, int accumulate) {
   int64_t e = (int64_t)blockIdx.x * NTH + threadIdx.x;
   if (e >= Mo * R) return;
+  // eight loads in flight, summed in ascending z (a fixed order: deterministic)
+  const float* p = part + e;
+  const int64_t st = Mo * R;
   float s = 0.0f;
-  for (int z = 0; z < ks; ++z) s += part[(int64_t)z * Mo * R + e];
+  int z = 0;
+  for (; z + 8 <= ks; z += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = p[(z + u) * st];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s += v[u];
+  }
+  for (; z < ks; ++z) s += p[z * st];
   const int64_t m = e / R, j = e % R;
   float v = alpha * s;
   float* o = out + m * so_m + j * so_j;
@@ -271,7 +278,7 @@ int env_int(const char* name, int dflt) {
 int rk_ksplit(int64_t Mo, int64_t Kc) {
   // enough workgroups to keep loads in flight on every CU, each streaming at
   // least `chunk` contraction elements
-  static const int target = env_int("ST_RK_WG", 512), chunk = env_int("ST_RK_CHUNK", 512);
+  static const int target = env_int("ST_RK_WG", 512), chunk = env_int("ST_RK_CHUNK", 256);
   int64_t tiles = st::cdiv(Mo, RK_BM);
   int64_t ks = st::cdiv(target, tiles);
   int64_t maxk = st::cdiv(Kc, chunk);
@@ -344,19 +351,31 @@ extern "C" int st_lora_gemm(int64_t Mo, int64_t No, int64_t Kc, const void* a, i
       big = No; small = Mo; so_m = 1; so_j = ldo;
       if (sbk == 1) { col = 0; ldg = sbn; } else if (sbn == 1) { col = 1; ldg = sbk; }
     }
-    if (col >= 0) {
+    // the streaming kernel takes 16-byte vector rows and 32-bit buffer offsets
+    const int64_t g_bytes = col ? ((Kc - 1) * ldg + big) * 2 : ((big - 1) * ldg + Kc) * 2;
+    const int64_t s_bytes = ((Kc - 1) * ssk + (small - 1) * ssj + 1) * 4;
+    const bool vec = ((uintptr_t)G & 15u) == 0 && ldg % 8 == 0 && (col ? big : Kc) % 8 == 0 &&
+                     ssk >= 0 && ssj >= 0 && g_bytes < (1ll << 31) && s_bytes < (1ll << 31);
+    if (col >= 0 && vec) {
       int ks = rk_ksplit(big, Kc);
       int64_t need = (int64_t)ks * big * small * 4;
       if (!workspace || workspace_bytes < need)
         return st::fail(ST_EWORKSPACE, "st_lora_gemm: needs %lld workspace bytes", (long long)need);
       int64_t klen = st::cdiv(st::cdiv(Kc, ks), RK_BK) * RK_BK;
-      int vec = (((uintptr_t)G & 15u) == 0 && ldg % 8 == 0) ? 1 : 0;
       dim3 grid((unsigned)st::cdiv(big, RK_BM), (unsigned)ks);
       float* part = (float*)workspace;
-      if (col)
-        lora_rk<true><<<grid, NTH, 0, s>>>(big, small, Kc, G, ldg, S, ssk, ssj, klen, vec, part);
-      else
-        lora_rk<false><<<grid, NTH, 0, s>>>(big, small, Kc, G, ldg, S, ssk, ssj, klen, vec, part);
+      auto go = [&](auto kern) {
+        kern<<<grid, NTH, 0, s>>>(big, small, Kc, G, ldg, g_bytes, S, ssk, ssj, s_bytes, klen,
+                                  part);
+      };
+      const bool sk1 = ssk == 1, nb2 = small > 32;
+      if (col) {
+        if (sk1) nb2 ? go(lora_rk<true, true, 2>) : go(lora_rk<true, true, 1>);
+        else nb2 ? go(lora_rk<true, false, 2>) : go(lora_rk<true, false, 1>);
+      } else {
+        if (sk1) nb2 ? go(lora_rk<false, true, 2>) : go(lora_rk<false, true, 1>);
+        else nb2 ? go(lora_rk<false, false, 2>) : go(lora_rk<false, false, 1>);
+      }
       int rc = st::check_launch("lora_rk");
       if (rc) return rc;
       lora_rk_reduce<<<(unsigned)st::cdiv(big * small, NTH), NTH, 0, s>>>(

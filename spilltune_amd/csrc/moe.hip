@@ -587,19 +587,10 @@ __global__ __launch_bounds__(NTH) void grouped_rk(GroupedRk a) {
         const int id = tid + i * NTH, row = id >> 3, c = id & 7;
         *(uint4*)&Gs[row * GK_LD + c * 8] = gr[i];
       }
-    } else {
+    } else {  // [contraction][column] as loaded; the MFMA operand is read transposed
       const int kg = tid >> 4, mg = tid & 15;
-      const uint32_t r0[4] = {gr[0].x, gr[0].y, gr[0].z, gr[0].w};
-      const uint32_t r1[4] = {gr[1].x, gr[1].y, gr[1].z, gr[1].w};
-      const uint32_t r2[4] = {gr[2].x, gr[2].y, gr[2].z, gr[2].w};
-      const uint32_t r3[4] = {gr[3].x, gr[3].y, gr[3].z, gr[3].w};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-        const uint32_t p01 = __builtin_amdgcn_perm(r1[e >> 1], r0[e >> 1], sel);
-        const uint32_t p23 = __builtin_amdgcn_perm(r3[e >> 1], r2[e >> 1], sel);
-        *(uint2*)&Gs[(mg * 8 + e) * GK_LD + kg * 4] = make_uint2(p01, p23);
-      }
+      for (int h = 0; h < 4; ++h) ((uint4*)Gs)[st::trswz<GK_BM>(kg * 4 + h, mg)] = gr[h];
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -622,7 +613,9 @@ __global__ __launch_bounds__(NTH) void grouped_rk(GroupedRk a) {
 #pragma unroll
     for (int s = 0; s < GK_BK / 16; ++s) {
       const int ko = s * 16 + (lane >> 5) * 8;
-      const bf16x8 av = *(const bf16x8*)&Gs[(wave * 32 + (lane & 31)) * GK_LD + ko];
+      const bf16x8 av =
+          COL ? st::tr_operand<GK_BM>((const uint4*)Gs, s * 16, wave * 32, lane)
+              : *(const bf16x8*)&Gs[(wave * 32 + (lane & 31)) * GK_LD + ko];
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         if (c >= nb) break;

@@ -7,13 +7,14 @@
 // The packed weight is streamed from HBM (0.53 B/element), dequantised in
 // registers (codebook in LDS, one fp32 multiply + RNE per element, the exact
 // arithmetic of codecs.py:168-170) and written to LDS as bf16, so W never
-// exists in HBM as bf16.  Both LDS tiles are stored contraction-contiguous
-// (16-byte chunks, XOR swizzled) so one fragment-read path serves both passes:
-// the forward dequantises W rows as they lie; the dgrad dequantises 8x8 (or
-// 4x8) blocks and writes them transposed.
+// exists in HBM as bf16.  The A tile and the forward B tile are stored
+// contraction-contiguous in padded 144-byte rows; the dgrad B tile keeps W's
+// natural [contraction][output] orientation and its MFMA operand is read with
+// the transposing ds_read_b64_tr_b16.
 //
-// Tiling: 256 threads = 2x2 waves, BK = 64, LDS double buffered, one barrier
-// per k-step.  MFMA v_mfma_f32_32x32x16_bf16 (8 bf16 per lane per operand).
+// Tiling: 128x128 (4 waves, 2x2) or 256x256 (8 waves, 2x4, two per SIMD),
+// BK = 64, LDS double buffered, one barrier per k-step; operand fragments are
+// read one 16-wide slice ahead of the MFMAs (v_mfma_f32_32x32x16_bf16).
 // The LoRA epilogue runs on v_mfma_f32_32x32x2_f32 (fp32 operands and
 // accumulation), so the adapter term keeps the reference's fp32 arithmetic.
 #include "common.h"
@@ -56,55 +57,26 @@ struct GemmParams {
   int64_t w_gstride, s_gstride, l_gstride;  // payload bytes (or bf16 elements), floats, floats
 };
 
-// LDS address of 16-byte chunk c (0..7) of tile row `row` (row = 64 bf16).
-__device__ __forceinline__ int swz(int row, int c) {
-  return row * 8 + (c ^ (row & 7) ^ ((row >> 3) & 7));
-}
+// LDS tile rows hold 64 bf16 (8 chunks of 16 bytes) plus one chunk of padding:
+// a 144-byte stride puts the 16 rows of each quarter-wave of a fragment read
+// on distinct banks, and every fragment of a wave is its lane base plus an
+// immediate offset.  Index in 16-byte units.
+constexpr int RS = 9;
+__device__ __forceinline__ int pad(int row, int c) { return row * RS + c; }
 
-// DGRAD_Q4 B tile: row n (contraction) of BN bf16 = BN/8 16-byte chunks;
-// chunk c stored at c ^ 2*(n & 7) so that both the 16-byte dequant stores of
-// 8 consecutive rows and the transposing reads of 4 rows x 32 bytes hit
-// distinct banks.  Index in 16-byte units; BN is a template constant.
-#define dswz(n, c) ((n) * (BN / 8) + ((c) ^ (((n) & 7) << 1)))
-
-// Transposed B operand from the [n][k] tile: lane (column k = kc + lane%32,
-// half g = lane/32) gets rows n = n0 + 8g + s for s = 0..7.
-// ds_read_b64_tr_b16: within 16 lanes, lane i receives element (i % 4) of the
-// 4-element rows supplied by lanes 4j + i/4, j = 0..3.
-template <int BN>
-__device__ __forceinline__ bf16x8 b_tr_impl(const uint4* bs, int n0, int kc, int lane) {
-  typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
-  const int G = lane >> 4, i = lane & 15, g = lane >> 5;
-  const int col = kc + 16 * (G & 1) + 4 * (i & 3);
-  v4bf r[2];
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int n = n0 + 8 * g + 4 * h + (i >> 2);
-    const uint16_t* e = (const uint16_t*)(bs + dswz(n, col >> 3)) + (col & 7);
-    r[h] = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) v4bf*)e);
-  }
-  return __builtin_shufflevector(r[0], r[1], 0, 1, 2, 3, 4, 5, 6, 7);
-}
-#define b_tr(bs, n0, kc, lane) b_tr_impl<BN>(bs, n0, kc, lane)
+// DGRAD_Q4 B tile: W[n][k] rows of BN bf16 in the transposed-operand layout
+// (st::trswz / st::tr_operand).
+#define dswz(n, c) st::trswz<BN>(n, c)
+#define b_tr(bs, n0, kc, lane) st::tr_operand<BN>(bs, n0, kc, lane)
 
 __device__ __forceinline__ unsigned nib(uint32_t w, int e, int hi_first) {
   return (w >> (4 * (e ^ hi_first))) & 15u;
 }
 
-typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-constexpr uint32_t kOOB = 0x80000000u;  // beyond every buffer: loads return 0
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* ptr, int64_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(ptr), (short)0, (int)bytes,
-                                           0x00020000);
-}
-__device__ __forceinline__ uint4 ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
-  return make_uint4(v.x, v.y, v.z, v.w);
-}
-__device__ __forceinline__ uint32_t ld4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
-}
+using st::kOOB;
+using st::ld16;
+using st::ld4;
+using st::make_rsrc;
 
 // Per-(row, group) decode table: entry c = bf16_rne(codebook[c] * scale), the
 // exact product the reference computes, split into a low-byte plane and a
@@ -163,7 +135,7 @@ struct Tile {
   static constexpr bool DGRAD = (MODE == DGRAD_Q4 || MODE == DGRAD_BF16);
   static constexpr int BF_IT = BN * 8 / NT;        // FWD_BF16 chunks per thread
   static constexpr int QB = BN * BK / (NT * 8);    // DGRAD_BF16: contraction rows per thread block
-  static constexpr int LDS_CHUNKS = 2 * (BM + BN) * 8;
+  static constexpr int LDS_CHUNKS = 2 * (BM + BN) * RS;
 };
 
 template <int MODE, int BM, int BN, int WAVES>
@@ -185,9 +157,9 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
   }
   const int KT = (int)st::cdiv(p.Q, BK);
 
-  // buffer b: A tile at lds + b*(BM+BN)*8, B tile right after it
-  auto As = [&](int b) { return lds + b * (BM + BN) * 8; };
-  auto Bs = [&](int b) { return lds + b * (BM + BN) * 8 + BM * 8; };
+  // buffer b: A tile at lds + b*(BM+BN)*RS, B tile right after it
+  auto As = [&](int b) { return lds + b * (BM + BN) * RS; };
+  auto Bs = [&](int b) { return lds + b * (BM + BN) * RS + BM * RS; };
 
   // ---- buffer resources: out-of-range loads return zero, so the main loop
   // needs no bounds branches (rows beyond M/P and the contraction tail).
@@ -220,7 +192,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
 #pragma unroll
     for (int i = 0; i < TL::A_IT; ++i) {
       int id = tid + i * NT;
-      as[swz(id >> 3, id & 7)] = xr[i];
+      as[pad(id >> 3, id & 7)] = xr[i];
     }
   };
 
@@ -296,7 +268,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
         const uint32_t word = (ch & 3) == 0 ? q.x : (ch & 3) == 1 ? q.y : (ch & 3) == 2 ? q.z : q.w;
         uint32_t o[4];
         deq8(word, tbl, p.hi_first, o);
-        bs[swz(brow, (bsub * EPT) / 8 + ch)] = make_uint4(o[0], o[1], o[2], o[3]);
+        bs[pad(brow, (bsub * EPT) / 8 + ch)] = make_uint4(o[0], o[1], o[2], o[3]);
       }
     } else if constexpr (MODE == DGRAD_Q4) {
       const uint4 q = w.q[0];
@@ -309,7 +281,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
       for (int i = 0; i < WQ; ++i) {
         if (i * 4 / WQ != part) continue;
         int id = tid + i * NT;
-        bs[swz(id >> 3, id & 7)] = w.q[i];
+        bs[pad(id >> 3, id & 7)] = w.q[i];
       }
     } else {
       // columns j = 2*part, 2*part+1 of the thread's QB x 8 block, written transposed
@@ -325,10 +297,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
         }
         const int prow = pb * 8 + j;
         if constexpr (TL::QB == 8) {
-          bs[swz(prow, qb)] = make_uint4(st::pack_bf16x2(v[0], v[1]), st::pack_bf16x2(v[2], v[3]),
+          bs[pad(prow, qb)] = make_uint4(st::pack_bf16x2(v[0], v[1]), st::pack_bf16x2(v[2], v[3]),
                                          st::pack_bf16x2(v[4], v[5]), st::pack_bf16x2(v[6], v[7]));
         } else {
-          ((uint2*)&bs[swz(prow, qb >> 1)])[qb & 1] =
+          ((uint2*)&bs[pad(prow, qb >> 1)])[qb & 1] =
               make_uint2(st::pack_bf16x2(v[0], v[1]), st::pack_bf16x2(v[2], v[3]));
         }
       }
@@ -346,10 +318,39 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  // one k-step: MFMAs on LDS buffer `cur`, with the next tile's A stores, B
-  // dequant/stores and the loads two steps ahead placed between them
+  // MFMA operand fragments of one 16-wide contraction slice s (0..3) of a tile
+  auto read_frags = [&](const uint4* as, const uint4* bs, int s, bf16x8 (&a)[FM],
+                        bf16x8 (&b)[FN]) {
+    const int c = 2 * s + (lane >> 5);
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+      a[i] = __builtin_bit_cast(bf16x8, as[pad(wm * WM + i * 32 + (lane & 31), c)]);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      if constexpr (MODE == DGRAD_Q4)
+        b[j] = b_tr(bs, s * 16, wn * WN + j * 32, lane);
+      else
+        b[j] = __builtin_bit_cast(bf16x8, bs[pad(wn * WN + j * 32 + (lane & 31), c)]);
+    }
+  };
+  auto mfmas = [&](const bf16x8 (&a)[FM], const bf16x8 (&b)[FN]) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+  };
+
+  // One k-step on LDS buffer `cur` (tile kt), staging tile kt+1 into the other
+  // buffer and loading tile kt+2 into registers.  Fragments are read one slice
+  // ahead of the MFMAs that use them (f0 = slices 0 and 2, f1 = slices 1 and 3),
+  // so LDS latency hides behind the previous slice's MFMAs.  The single barrier
+  // sits before the last slice: by then every wave has written its part of
+  // tile kt+1 and has finished (waitcnt) its reads of tile kt, so slice 3 can
+  // already fetch slice 0 of tile kt+1, and the next step may overwrite `cur`.
   uint4 xr[TL::A_IT];
   WRegs w0, w1;
+  bf16x8 fa0[FM], fb0[FN], fa1[FM], fb1[FN];
   // new_group: the tile dequantised in this step starts a 128-wide scale group
   // (even tile index), so its decode table must be rebuilt; odd tiles reuse it.
   auto body = [&](int kt, WRegs& wnext, WRegs& wfar, bool new_group) {
@@ -362,30 +363,22 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
     load_A(kt + 2, xr);
     load_W(kt + 2, wfar);
     if (new_group || MODE == DGRAD_Q4) prep_B(wnext);
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int c = 2 * s + (lane >> 5);
-      bf16x8 a[FM], b[FN];
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-        a[i] = __builtin_bit_cast(bf16x8, as[swz(wm * WM + i * 32 + (lane & 31), c)]);
-#pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        if constexpr (MODE == DGRAD_Q4)
-          b[j] = b_tr(bs, s * 16, wn * WN + j * 32, lane);
-        else
-          b[j] = __builtin_bit_cast(bf16x8, bs[swz(wn * WN + j * 32 + (lane & 31), c)]);
-      }
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
-      store_B_part(bs_n, wnext, s);
-      // keep each slice's fragments and dequant work together (bounds live ranges)
-      __builtin_amdgcn_sched_barrier(0);
-    }
+    read_frags(as, bs, 1, fa1, fb1);
+    mfmas(fa0, fb0);
+    store_B_part(bs_n, wnext, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(as, bs, 2, fa0, fb0);
+    mfmas(fa1, fb1);
+    store_B_part(bs_n, wnext, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(as, bs, 3, fa1, fb1);
+    mfmas(fa0, fb0);
+    store_B_part(bs_n, wnext, 2);
+    store_B_part(bs_n, wnext, 3);
     __syncthreads();
+    read_frags(as_n, bs_n, 0, fa0, fb0);
+    mfmas(fa1, fb1);
+    __builtin_amdgcn_sched_barrier(0);
   };
 
   // prologue: tiles 0 (LDS) and 1 (registers), W for tiles 0 and 1
@@ -399,12 +392,16 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
   for (int s = 0; s < 4; ++s) store_B_part(Bs(0), w0, s);
   load_A(1, xr);
   __syncthreads();
+  read_frags(As(0), Bs(0), 0, fa0, fb0);
 
   // tile kt+1's W sits in w1 (kt even) or w0 (kt odd); W for kt+2 lands in the other
   for (int kt = 0; kt < KT; kt += 2) {
     body(kt, w1, w0, false);
     if (kt + 1 < KT) body(kt + 1, w0, w1, true);
   }
+  // the last step's slice-3 reads of the (unused) next buffer must finish
+  // before the epilogue reuses LDS
+  __syncthreads();
 
   // ---------------- epilogue ----------------
   const bool lora = p.T != nullptr;
