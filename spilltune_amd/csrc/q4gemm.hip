@@ -123,12 +123,12 @@ __device__ __forceinline__ void deq8(uint32_t w, const Tbl& T, int hi_first, uin
   o[3] = __builtin_amdgcn_perm(o57, e46, 0x07060302u);
 }
 
-// WAVES = 4 (2x2 waves) or 8 (2x4 waves: two waves per SIMD, 128x64 each)
-template <int MODE, int BM, int BN, int WAVES>
+// WAVES = 4 or 8 (two waves per SIMD), arranged WAVES_M x (WAVES / WAVES_M)
+template <int MODE, int BM, int BN, int WAVES, int WAVES_M>
 struct Tile {
   static constexpr int NT = 64 * WAVES;
-  static constexpr int WAVES_N = WAVES / 2;
-  static constexpr int WM = BM / 2, WN = BN / WAVES_N;
+  static constexpr int WAVES_N = WAVES / WAVES_M;
+  static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
   static constexpr int FM = WM / 32, FN = WN / 32;
   static constexpr int A_IT = BM * 8 / NT;  // 16-byte chunks per thread
   static constexpr bool Q4 = (MODE == FWD_Q4 || MODE == DGRAD_Q4);
@@ -138,9 +138,9 @@ struct Tile {
   static constexpr int LDS_CHUNKS = 2 * (BM + BN) * RS;
 };
 
-template <int MODE, int BM, int BN, int WAVES>
+template <int MODE, int BM, int BN, int WAVES, int WAVES_M>
 __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
-  using TL = Tile<MODE, BM, BN, WAVES>;
+  using TL = Tile<MODE, BM, BN, WAVES, WAVES_M>;
   constexpr int NT = TL::NT;
   constexpr int WM = TL::WM, WN = TL::WN, FM = TL::FM, FN = TL::FN;
   __shared__ uint4 lds[TL::LDS_CHUNKS];
@@ -197,14 +197,17 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
   };
 
   // B operand source.  FWD_Q4: thread owns EPT consecutive weights of one W row.
-  constexpr int TPR = NT / BN;          // threads per W row (1 or 2)
-  constexpr int EPT = BK / TPR;         // elements per thread per k-step (64 or 32)
+  constexpr int TPR = NT / BN;          // threads per W row (1, 2 or 4)
+  constexpr int EPT = BK / TPR;         // elements per thread per k-step (64, 32 or 16)
   // DGRAD_Q4: the B tile is W[n][k] for BK contraction rows n and BN output
   // columns k, kept in that (natural) orientation; each thread dequantises
-  // 32 consecutive k of one row n, and the MFMA operand is read transposed.
-  constexpr int DTR = BN / 32;          // DGRAD_Q4 threads per contraction row
-  constexpr int WQ = MODE == FWD_Q4 ? EPT / 32 : MODE == DGRAD_Q4 ? 1
-                     : (TL::DGRAD ? TL::QB : TL::BF_IT);
+  // DE consecutive k of one row n, and the MFMA operand is read transposed.
+  constexpr int DE = BN * BK / NT;      // DGRAD_Q4 elements per thread per k-step (32 or 16)
+  constexpr int DTR = BN / DE;          // DGRAD_Q4 threads per contraction row
+  // packed 4-bit words (8 codes each) per thread per k-step
+  constexpr int NW = MODE == FWD_Q4 ? EPT / 8 : MODE == DGRAD_Q4 ? DE / 8 : 1;
+  static_assert(!TL::Q4 || NW == 2 || NW % 4 == 0, "packed W loads are 8 bytes or whole 16-byte pieces");
+  constexpr int WQ = TL::Q4 ? 1 : (TL::DGRAD ? TL::QB : TL::BF_IT);
   constexpr int PB = BN / 8;
   const int brow = tid / TPR, bsub = tid % TPR;       // FWD_Q4 mapping
   const int drow = tid / DTR, dsub = tid % DTR;       // DGRAD_Q4 mapping
@@ -214,20 +217,37 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
     int64_t n = p0 + brow;
     w_row = n < p.P ? (uint32_t)(n * p.ldw + bsub * EPT) : kOOB;  // element index at k = 0
   }
-  const bool dcol_ok = p0 + dsub * 32 < p.P;
+  const bool dcol_ok = p0 + dsub * DE < p.P;
   static_assert(MODE != DGRAD_Q4 || NT / DTR == BK, "DGRAD_Q4: one thread row per contraction row");
 
   struct WRegs {
-    uint4 q[WQ];
+    uint4 q[WQ];      // bf16 modes
+    uint32_t w[NW];   // 4-bit modes
     float s[1];
+  };
+  // NW packed words from byte offset po (kOOB: zeros)
+  auto load_words = [&](uint32_t po, uint32_t (&w)[NW]) {
+    if constexpr (NW == 2) {
+      const uint2 v = st::ld8(rsW, po);
+      w[0] = v.x;
+      w[1] = v.y;
+    } else {
+#pragma unroll
+      for (int i = 0; i < NW / 4; ++i) {
+        const uint4 v = ld16(rsW, po == kOOB ? kOOB : po + 16 * i);
+        w[4 * i] = v.x;
+        w[4 * i + 1] = v.y;
+        w[4 * i + 2] = v.z;
+        w[4 * i + 3] = v.w;
+      }
+    }
   };
   auto load_W = [&](int kt, WRegs& w) {
     if constexpr (MODE == FWD_Q4) {
       uint32_t e = w_row + (uint32_t)(kt * BK);
       uint32_t po = w_row != kOOB ? e >> 1 : kOOB;
       uint32_t so = w_row != kOOB ? (e >> 7) * 4 : kOOB;
-#pragma unroll
-      for (int i = 0; i < WQ; ++i) w.q[i] = ld16(rsW, po == kOOB ? kOOB : po + 16 * i);
+      load_words(po, w.w);
       w.s[0] = __builtin_bit_cast(float, ld4(rsS, so));
     } else if constexpr (MODE == FWD_BF16) {
 #pragma unroll
@@ -240,8 +260,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
     } else if constexpr (MODE == DGRAD_Q4) {
       const int64_t n = (int64_t)kt * BK + drow;
       const bool ok = dcol_ok && n < p.Q;
-      const int64_t e = n * p.ldw + p0 + dsub * 32;   // 32-aligned: one uint4, one scale
-      w.q[0] = ld16(rsW, ok ? (uint32_t)(e >> 1) : kOOB);
+      const int64_t e = n * p.ldw + p0 + dsub * DE;   // DE-aligned: one scale group
+      load_words(ok ? (uint32_t)(e >> 1) : kOOB, w.w);
       w.s[0] = __builtin_bit_cast(float, ld4(rsS, ok ? (uint32_t)((e >> 7) * 4) : kOOB));
     } else {
       int64_t pc = p0 + pb * 8;
@@ -258,24 +278,18 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
   // dequantise / stage one quarter (part = 0..3) of the B tile into LDS
   Tbl tbl;
   auto store_B_part = [&](uint4* bs, const WRegs& w, int part) {
-    if constexpr (MODE == FWD_Q4) {
-      constexpr int CH = EPT / 8;        // 8-element chunks per thread
-      constexpr int PER = CH / 4;        // chunks per quarter (2 or 1)
+    if constexpr (TL::Q4) {
+      // 8-element chunk ch goes out in quarter ch*4/NW (two chunks per quarter
+      // for NW = 8, quarters 0 and 2 for NW = 2)
 #pragma unroll
-      for (int u = 0; u < PER; ++u) {
-        const int ch = part * PER + u;
-        const uint4 q = w.q[ch / 4];
-        const uint32_t word = (ch & 3) == 0 ? q.x : (ch & 3) == 1 ? q.y : (ch & 3) == 2 ? q.z : q.w;
+      for (int ch = 0; ch < NW; ++ch) {
+        if (ch * 4 / NW != part) continue;
         uint32_t o[4];
-        deq8(word, tbl, p.hi_first, o);
-        bs[pad(brow, (bsub * EPT) / 8 + ch)] = make_uint4(o[0], o[1], o[2], o[3]);
+        deq8(w.w[ch], tbl, p.hi_first, o);
+        const int idx =
+            MODE == FWD_Q4 ? pad(brow, (bsub * EPT) / 8 + ch) : dswz(drow, dsub * NW + ch);
+        bs[idx] = make_uint4(o[0], o[1], o[2], o[3]);
       }
-    } else if constexpr (MODE == DGRAD_Q4) {
-      const uint4 q = w.q[0];
-      const uint32_t word = part == 0 ? q.x : part == 1 ? q.y : part == 2 ? q.z : q.w;
-      uint32_t o[4];
-      deq8(word, tbl, p.hi_first, o);
-      bs[dswz(drow, dsub * 4 + part)] = make_uint4(o[0], o[1], o[2], o[3]);
     } else if constexpr (MODE == FWD_BF16) {
 #pragma unroll
       for (int i = 0; i < WQ; ++i) {
@@ -477,30 +491,32 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
   }
 }
 
-template <int MODE, int BM, int BN, int WAVES>
+template <int MODE, int BM, int BN, int WAVES, int WAVES_M = 2>
 int launch(const GemmParams& p, hipStream_t stream) {
   constexpr int NT = 64 * WAVES;
   int64_t tiles = st::cdiv(p.M, BM) * st::cdiv(p.P, BN);
   if (tiles > 0x7fffffff) return st::fail(ST_EUNSUPPORTED, "q4gemm: too many tiles");
   if (p.T) {  // the LoRA epilogue stages T and the right operand in the tile's LDS
-    using TL = Tile<MODE, BM, BN, WAVES>;
+    using TL = Tile<MODE, BM, BN, WAVES, WAVES_M>;
     int64_t need = (int64_t)BM * (p.lora_cols + 1) +
                    (TL::DGRAD ? (int64_t)p.lora_k * BN : (int64_t)BN * (p.lora_k + 1));
     if (need > (int64_t)TL::LDS_CHUNKS * 4)
       return st::fail(ST_EUNSUPPORTED, "q4gemm: LoRA epilogue (%d columns) exceeds tile LDS",
                       p.lora_cols);
   }
-  gemm_kernel<MODE, BM, BN, WAVES><<<(unsigned)tiles, NT, 0, stream>>>(p);
+  gemm_kernel<MODE, BM, BN, WAVES, WAVES_M><<<(unsigned)tiles, NT, 0, stream>>>(p);
   return st::check_launch("q4gemm");
 }
 
-// 256x256 (8 waves) halves the dequant work per MFMA but needs enough tiles to
-// cover the 256 CUs.
+// 256-row tiles halve the dequant work per MFMA against 128-row ones but need
+// enough tiles to cover the 256 CUs: 256x256 (8 waves, 2x4) where that gives
+// >= 192 tiles, else 256x128 (8 waves, 4x2), else 128x128 (4 waves).
 int tile_choice(int mode, int64_t M, int64_t P) {
   const char* env = getenv("ST_GEMM_TILE");
   if (env) return atoi(env);
   // the transposed-operand dgrad runs out of registers at 256x256 (8 waves)
   if (mode == FWD_Q4 && st::cdiv(M, 256) * st::cdiv(P, 256) >= 192) return 256;
+  if (st::cdiv(M, 256) * st::cdiv(P, 128) >= 192) return 2561;
   return 128;
 }
 
@@ -510,6 +526,7 @@ int dispatch(const GemmParams& p, hipStream_t stream) {
   if constexpr (MODE == FWD_Q4 || MODE == DGRAD_Q4) {
     const int t = tile_choice(MODE, p.M, p.P);
     if (t == 256) return launch<MODE, 256, 256, 8>(p, stream);
+    if (t == 2561) return launch<MODE, 256, 128, 8, 4>(p, stream);
     if constexpr (MODE == FWD_Q4)
       if (t == 2564) return launch<MODE, 256, 256, 4>(p, stream);
   }
@@ -669,7 +686,7 @@ template <int MODE>
 int launch_grouped(const GemmParams& p, hipStream_t stream) {
   constexpr int BM = 128, BN = 128, WAVES = 4;
   if (p.T) {
-    using TL = Tile<MODE, BM, BN, WAVES>;
+    using TL = Tile<MODE, BM, BN, WAVES, 2>;
     int64_t need = (int64_t)BM * (p.lora_cols + 1) +
                    (TL::DGRAD ? (int64_t)p.lora_k * BN : (int64_t)BN * (p.lora_k + 1));
     if (need > (int64_t)TL::LDS_CHUNKS * 4)
@@ -678,7 +695,7 @@ int launch_grouped(const GemmParams& p, hipStream_t stream) {
   }
   int64_t tiles = (st::cdiv(p.M, BM) + p.ngroups) * st::cdiv(p.P, BN);
   if (tiles > 0x7fffffff) return st::fail(ST_EUNSUPPORTED, "q4 grouped: too many tiles");
-  gemm_kernel<MODE, BM, BN, WAVES><<<(unsigned)tiles, 64 * WAVES, 0, stream>>>(p);
+  gemm_kernel<MODE, BM, BN, WAVES, 2><<<(unsigned)tiles, 64 * WAVES, 0, stream>>>(p);
   return st::check_launch("q4 grouped gemm");
 }
 }  // namespace
