@@ -67,12 +67,15 @@ __device__ __forceinline__ uint32_t ld4(__amdgpu_buffer_rsrc_t r, uint32_t off) 
 }
 
 // Transposed-operand tile: rows n (the contraction) of BN bf16 held as BN/8
-// 16-byte chunks, chunk c of row n at n*(BN/8) + (c ^ 2*(n & 7)).  Both the
-// 16-byte stores of one row per quarter-wave and the transposing operand
-// reads below hit distinct banks.  Index in 16-byte units.
+// 16-byte chunks, chunk c of row n at n*(BN/8) + (c ^ 5*(n & 3)).  XOR with
+// 5r moves bits 0-1 and 2-3 of the chunk by the row's r = n & 3, so each
+// quarter-wave of 16-byte stores (one row x 16 chunks, two rows x 8 even or
+// odd chunks, or four rows x 4 chunks 4 apart) and each half-wave of the
+// transposing reads below (4 rows x 4 consecutive chunks) covers all 64
+// banks once.  Index in 16-byte units; BN >= 128.
 template <int BN>
 __device__ __forceinline__ int trswz(int n, int c) {
-  return n * (BN / 8) + (c ^ ((n & 7) << 1));
+  return n * (BN / 8) + (c ^ (5 * (n & 3)));
 }
 // MFMA 32x32x16 operand from such a tile: lane (column kc + lane%32, half
 // g = lane/32) gets rows n0 + 8g + s, s = 0..7.  ds_read_b64_tr_b16: within

@@ -69,10 +69,6 @@ __device__ __forceinline__ int pad(int row, int c) { return row * RS + c; }
 #define dswz(n, c) st::trswz<BN>(n, c)
 #define b_tr(bs, n0, kc, lane) st::tr_operand<BN>(bs, n0, kc, lane)
 
-__device__ __forceinline__ unsigned nib(uint32_t w, int e, int hi_first) {
-  return (w >> (4 * (e ^ hi_first))) & 15u;
-}
-
 using st::kOOB;
 using st::ld16;
 using st::ld4;
@@ -102,12 +98,14 @@ __device__ __forceinline__ uint32_t sel4(const uint32_t (&pl)[4], uint32_t n7, u
   uint32_t b = __builtin_amdgcn_perm(pl[3], pl[2], n7);
   return __builtin_amdgcn_perm(b, a, hsel);
 }
-// 8 codes of one packed word -> 4 bf16x2 words in element order
-__device__ __forceinline__ void deq8(uint32_t w, const Tbl& T, int hi_first, uint32_t (&o)[4]) {
-  uint32_t ne = w & 0x0F0F0F0Fu;         // low nibbles
-  uint32_t no = (w >> 4) & 0x0F0F0F0Fu;  // high nibbles
-  if (hi_first) { uint32_t t = ne; ne = no; no = t; }
+// 8 codes of one packed word -> 4 bf16x2 words in element order.  sh_e / sh_o
+// = 0 / 4 when the low nibble of a byte holds the even element, 4 / 0 when
+// the high nibble does.
+__device__ __forceinline__ void deq8(uint32_t w, const Tbl& T, uint32_t sh_e, uint32_t sh_o,
+                                     uint32_t (&o)[4]) {
   // ne = codes of elements 0,2,4,6; no = codes of elements 1,3,5,7
+  const uint32_t ne = (w >> sh_e) & 0x0F0F0F0Fu;
+  const uint32_t no = (w >> sh_o) & 0x0F0F0F0Fu;
   const uint32_t se = 0x03020100u | ((ne >> 1) & 0x04040404u);
   const uint32_t so = 0x03020100u | ((no >> 1) & 0x04040404u);
   const uint32_t ne7 = ne & 0x07070707u, no7 = no & 0x07070707u;
@@ -137,6 +135,89 @@ struct Tile {
   static constexpr int QB = BN * BK / (NT * 8);    // DGRAD_BF16: contraction rows per thread block
   static constexpr int LDS_CHUNKS = 2 * (BM + BN) * RS;
 };
+
+// Epilogue shared by the GEMM kernels: y = bf16(acc) (+ LoRA term, + residual)
+// for this tile; waves with `has_acc` false only help stage the LoRA operands.
+// LDS (`lds`, at least BM*(lora_cols+1) + the LoRA right operand floats) is
+// reused, so the caller has finished every LDS read of the main loop.
+template <bool DGRAD, int BM, int BN, int NT, int FM, int FN, int WM, int WN>
+__device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const f32x16 (&acc)[FM][FN],
+                                              uint4* lds, int64_t m0, int64_t mend, int64_t p0,
+                                              int wm, int wn, int tid, int lane, bool has_acc,
+                                              const float* Lg) {
+  const bool lora = p.T != nullptr;
+  float* Ts = (float*)lds;
+  const int tstride = p.lora_cols + 1;
+  float* Ls = Ts + BM * tstride;
+  const int lstride = DGRAD ? BN : (p.lora_k + 1);
+  if (lora) {
+    // stage T rows [m0, m0+BM) x [0, lora_cols) and the LoRA right operand
+    for (int e = tid; e < BM * p.lora_cols; e += NT) {
+      int r = e / p.lora_cols, c = e % p.lora_cols;
+      int64_t m = m0 + r;
+      Ts[r * tstride + c] = m < mend ? p.T[m * p.ldt + c] : 0.0f;
+    }
+    if (DGRAD) {  // L = A_cat [lora_k, P]
+      for (int e = tid; e < p.lora_k * BN; e += NT) {
+        int r = e / BN, c = e % BN;
+        int64_t pc = p0 + c;
+        Ls[r * lstride + c] = pc < p.P ? Lg[r * p.ldl + pc] : 0.0f;
+      }
+    } else {  // L = B_lora [P, rank]
+      for (int e = tid; e < BN * p.lora_k; e += NT) {
+        int r = e / p.lora_k, c = e % p.lora_k;
+        int64_t pc = p0 + r;
+        Ls[r * lstride + c] = pc < p.P ? Lg[pc * p.ldl + c] : 0.0f;
+      }
+    }
+    __syncthreads();
+  }
+  if (!has_acc) return;
+
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int cl = wn * WN + j * 32;  // tile-local first column of this block
+    const int64_t pcol = p0 + cl + (lane & 31);
+    int coff = 0;
+    if (lora && !DGRAD) {
+      int64_t pblk = p0 + cl;
+      int s = 0;
+      for (int q = 0; q < p.nseg; ++q) s += (p.seg_end[q] <= pblk) ? 1 : 0;
+      coff = s * p.lora_k;
+    }
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int rl = wm * WM + i * 32;
+      f32x16 la;
+      if (lora) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) la[v] = 0.0f;
+        for (int kk = 0; kk < p.lora_k; kk += 2) {
+          int kx = kk + (lane >> 5);
+          float av = Ts[(rl + (lane & 31)) * tstride + coff + kx];
+          float bv = DGRAD ? Ls[kx * lstride + cl + (lane & 31)]
+                           : Ls[(cl + (lane & 31)) * lstride + kx];
+          la = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, la, 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t m = m0 + rl + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+        if (m < mend && pcol < p.P) {
+          float y = st::bf16r(acc[i][j][v]);
+          if (lora) {
+            if (DGRAD)
+              y = st::bf16r(y + st::bf16r(la[v]));
+            else
+              y = st::bf16r(y + la[v] * p.lora_scale);
+          }
+          if (p.R) y = st::bf16r(st::bf16_to_f32(p.R[m * p.ldr + pcol]) + y);
+          p.C[m * p.ldc + pcol] = st::f32_to_bf16(y);
+        }
+      }
+    }
+  }
+}
 
 template <int MODE, int BM, int BN, int WAVES, int WAVES_M>
 __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
@@ -180,11 +261,15 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
     a_row[i] = (m0 + row < mend && m >= 0) ? (uint32_t)((m * p.lda + c * 8) * 2) : kOOB;
     a_k[i] = c * 8;
   }
+  // a_row + offset stays at or beyond kOOB for rows outside the tile range;
+  // only a contraction tail (Q not a multiple of BK) needs per-chunk checks.
+  // Tiles past the last one are loaded (in bounds or zero) but never used.
   auto load_A = [&](int kt, uint4 (&xr)[TL::A_IT]) {
+    const bool tail = (int64_t)(kt + 1) * BK > p.Q && kt < KT;
 #pragma unroll
     for (int i = 0; i < TL::A_IT; ++i) {
-      int k = kt * BK + a_k[i];
-      uint32_t off = (a_row[i] != kOOB && k < p.Q) ? a_row[i] + (uint32_t)(kt * BK * 2) : kOOB;
+      uint32_t off = a_row[i] + (uint32_t)(kt * BK * 2);
+      if (tail && kt * BK + a_k[i] >= p.Q) off = kOOB;
       xr[i] = ld16(rsA, off);
     }
   };
@@ -212,10 +297,16 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
   const int brow = tid / TPR, bsub = tid % TPR;       // FWD_Q4 mapping
   const int drow = tid / DTR, dsub = tid % DTR;       // DGRAD_Q4 mapping
   const int pb = tid % PB, qb = tid / PB;             // DGRAD_BF16 mapping
-  uint32_t w_row = 0;
+  // FWD_Q4 byte offsets at k = 0 of the thread's packed weights and of its
+  // row's first scale (kOOB beyond P).  K (= ldw) is a multiple of 128 here,
+  // so k-step kt adds kt*BK/2 payload bytes and scale group kt/2.
+  uint32_t w_po = kOOB, w_so = kOOB;
   if constexpr (MODE == FWD_Q4) {
     int64_t n = p0 + brow;
-    w_row = n < p.P ? (uint32_t)(n * p.ldw + bsub * EPT) : kOOB;  // element index at k = 0
+    if (n < p.P) {
+      w_po = (uint32_t)((n * p.ldw + bsub * EPT) >> 1);
+      w_so = (uint32_t)((n * p.ldw) >> 7) * 4;
+    }
   }
   const bool dcol_ok = p0 + dsub * DE < p.P;
   static_assert(MODE != DGRAD_Q4 || NT / DTR == BK, "DGRAD_Q4: one thread row per contraction row");
@@ -234,7 +325,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
     } else {
 #pragma unroll
       for (int i = 0; i < NW / 4; ++i) {
-        const uint4 v = ld16(rsW, po == kOOB ? kOOB : po + 16 * i);
+        const uint4 v = ld16(rsW, po + 16 * i);
         w[4 * i] = v.x;
         w[4 * i + 1] = v.y;
         w[4 * i + 2] = v.z;
@@ -244,11 +335,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
   };
   auto load_W = [&](int kt, WRegs& w) {
     if constexpr (MODE == FWD_Q4) {
-      uint32_t e = w_row + (uint32_t)(kt * BK);
-      uint32_t po = w_row != kOOB ? e >> 1 : kOOB;
-      uint32_t so = w_row != kOOB ? (e >> 7) * 4 : kOOB;
-      load_words(po, w.w);
-      w.s[0] = __builtin_bit_cast(float, ld4(rsS, so));
+      load_words(w_po + (uint32_t)(kt * (BK / 2)), w.w);
+      w.s[0] = __builtin_bit_cast(float, ld4(rsS, w_so + (uint32_t)(kt >> 1) * 4));
     } else if constexpr (MODE == FWD_BF16) {
 #pragma unroll
       for (int i = 0; i < WQ; ++i) {
@@ -277,6 +365,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
 
   // dequantise / stage one quarter (part = 0..3) of the B tile into LDS
   Tbl tbl;
+  const uint32_t sh_e = p.hi_first ? 4u : 0u;
   auto store_B_part = [&](uint4* bs, const WRegs& w, int part) {
     if constexpr (TL::Q4) {
       // 8-element chunk ch goes out in quarter ch*4/NW (two chunks per quarter
@@ -285,7 +374,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
       for (int ch = 0; ch < NW; ++ch) {
         if (ch * 4 / NW != part) continue;
         uint32_t o[4];
-        deq8(w.w[ch], tbl, p.hi_first, o);
+        deq8(w.w[ch], tbl, sh_e, 4u - sh_e, o);
         const int idx =
             MODE == FWD_Q4 ? pad(brow, (bsub * EPT) / 8 + ch) : dswz(drow, dsub * NW + ch);
         bs[idx] = make_uint4(o[0], o[1], o[2], o[3]);
@@ -417,78 +506,264 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
   // before the epilogue reuses LDS
   __syncthreads();
 
-  // ---------------- epilogue ----------------
-  const bool lora = p.T != nullptr;
-  float* Ts = (float*)lds;
-  const int tstride = p.lora_cols + 1;
-  float* Ls = Ts + BM * tstride;
-  const int lstride = TL::DGRAD ? BN : (p.lora_k + 1);
-  if (lora) {
-    // stage T rows [m0, m0+BM) x [0, lora_cols) and the LoRA right operand
-    for (int e = tid; e < BM * p.lora_cols; e += NT) {
-      int r = e / p.lora_cols, c = e % p.lora_cols;
-      int64_t m = m0 + r;
-      Ts[r * tstride + c] = m < mend ? p.T[m * p.ldt + c] : 0.0f;
-    }
-    if (TL::DGRAD) {  // L = A_cat [lora_k, P]
-      for (int e = tid; e < p.lora_k * BN; e += NT) {
-        int r = e / BN, c = e % BN;
-        int64_t pc = p0 + c;
-        Ls[r * lstride + c] = pc < p.P ? Lg[r * p.ldl + pc] : 0.0f;
-      }
-    } else {  // L = B_lora [P, rank]
-      for (int e = tid; e < BN * p.lora_k; e += NT) {
-        int r = e / p.lora_k, c = e % p.lora_k;
-        int64_t pc = p0 + r;
-        Ls[r * lstride + c] = pc < p.P ? Lg[pc * p.ldl + c] : 0.0f;
-      }
-    }
-    __syncthreads();
-  }
+  gemm_epilogue<TL::DGRAD, BM, BN, NT, FM, FN, WM, WN>(p, acc, lds, m0, mend, p0, wm, wn, tid,
+                                                       lane, true, Lg);
+}
 
+// s_waitcnt for at most VM vector-memory and LGKM LDS/scalar operations in
+// flight (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt 7 = no wait,
+// lgkmcnt in bits 11:8; VM = 63 / LGKM = 15 leave that counter alone)
+template <int VM, int LGKM = 15>
+__device__ __forceinline__ void wait_cnt() {
+  static_assert(VM >= 0 && VM < 64 && LGKM >= 0 && LGKM < 16, "counter range");
+  __builtin_amdgcn_s_waitcnt((VM & 15) | (7 << 4) | (LGKM << 8) | ((VM >> 4) << 14));
+}
+// Workgroup barrier without the fence of __syncthreads (which would also wait
+// for every LDS DMA in flight): the caller first waits for exactly the
+// operations other waves depend on.  The memory clobber keeps the compiler
+// from moving memory accesses across it.
+__device__ __forceinline__ void bar() { asm volatile("s_barrier" ::: "memory"); }
+
+// Warp-specialised 256x128 tile, 8 waves in two roles.  Waves 0-3 (one per
+// SIMD) only read operand fragments and issue MFMAs on a 2x2 grid of 128x64
+// wave tiles; waves 4-7 (the other wave of each SIMD) move data:
+//  - A (activations / upstream gradient) goes HBM/L2 -> LDS by buffer DMA
+//    (no VGPRs, no ds_write).  Each DMA moves 8 rows x 128 bytes (whole cache
+//    lines) into 1 KiB of LDS; chunk c of row r sits at position
+//    c ^ ((r >> 1) & 7), chosen through each lane's source address, so the
+//    16 rows of a quarter-wave fragment read hit distinct banks.  A ring of
+//    WS_DA stages gives each DMA WS_DA-1 k-steps to land.
+//  - W streams through a register ring of WS_PW k-steps, is dequantised and
+//    written to a double-buffered B tile (forward: fragment-major like A;
+//    dgrad: the transposed-operand layout read with ds_read_b64_tr_b16).
+// The roles meet at one barrier per k-step; each role's registers are live
+// only in its own branch.
+constexpr int WS_DA = 3, WS_PW = 4;
+template <int MODE>
+__global__ __launch_bounds__(512) void gemm_ws_kernel(GemmParams p) {
+  static_assert(MODE == FWD_Q4 || MODE == DGRAD_Q4, "4-bit modes only");
+  constexpr int BM = 256, BN = 128, NT = 512, NP = 256;  // NP: producer threads
+  constexpr int WM = 128, WN = 64, FM = 4, FN = 2;
+  constexpr int A_ST = BM * BK / 8;  // 16-byte units per A stage (32 fragments)
+  constexpr int B_ST = BN * BK / 8;  // per B buffer
+  // separate LDS objects, so the compiler can tell the A DMAs from the B stores
+  __shared__ uint4 ldsA[WS_DA * A_ST];
+  __shared__ uint4 ldsB[2 * B_ST];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t tiles_p = st::cdiv(p.P, BN);
+  const int64_t t = st::xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t p0 = (t % tiles_p) * BN;
+  int64_t m0 = (t / tiles_p) * BM, mend = p.M;
+  int grp = 0;
+  if (p.goff) {  // whole workgroup leaves together, before any barrier
+    if (!st::find_group(p.goff, p.ngroups, BM, t / tiles_p, p.M, grp, m0, mend)) return;
+  }
+  const int KT = (int)st::cdiv(p.Q, BK);
+  uint4* const As0 = ldsA;  // stage a at As0 + a*A_ST
+  uint4* const Bs0 = ldsB;  // buffer b at Bs0 + b*B_ST
+  const float* Lg = p.L + grp * p.l_gstride;
+  const int wm = wave >> 1, wn = wave & 1;  // consumer wave grid
+  f32x16 acc[FM][FN];
+
+  if (wave >= 4) {
+    // ------------------------------------------------------------ producer
+    const int pw = wave - 4, ptid = tid - NP;
+    const auto rsA = make_rsrc(p.A, p.a_bytes);
+    const auto rsW = make_rsrc(p.Wq + grp * p.w_gstride, p.w_bytes);
+    const auto rsS = make_rsrc(p.Ws + grp * p.s_gstride, p.s_bytes);
+    // A: producer wave pw moves rows 64*pw + 8*q + l/8 (q < 8) of each stage;
+    // lane l fills position l%8 of its row, i.e. chunk (l%8) ^ ((row>>1) & 7).
+    uint32_t a_row[8];
+    int a_c[8];
 #pragma unroll
-  for (int j = 0; j < FN; ++j) {
-    const int cl = wn * WN + j * 32;  // tile-local first column of this block
-    const int64_t pcol = p0 + cl + (lane & 31);
-    int coff = 0;
-    if (lora && !TL::DGRAD) {
-      int64_t pblk = p0 + cl;
-      int s = 0;
-      for (int q = 0; q < p.nseg; ++q) s += (p.seg_end[q] <= pblk) ? 1 : 0;
-      coff = s * p.lora_k;
+    for (int q = 0; q < 8; ++q) {
+      const int row = 64 * pw + 8 * q + (lane >> 3);
+      int64_t m = m0 + row;
+      if (m < mend && p.gather) m = p.gather[m];
+      a_c[q] = (lane & 7) ^ ((row >> 1) & 7);
+      a_row[q] = (m0 + row < mend && m >= 0) ? (uint32_t)((m * p.lda + a_c[q] * 8) * 2) : kOOB;
+    }
+    auto dma_A = [&](int kt) {
+      uint4* st_base = As0 + (kt % WS_DA) * A_ST;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const bool ok = a_row[q] != kOOB && kt * BK + a_c[q] * 8 < p.Q;
+        const uint32_t off = ok ? a_row[q] + (uint32_t)(kt * BK * 2) : kOOB;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rsA, (__attribute__((address_space(3))) void*)(st_base + (8 * pw + q) * 64), 16, off,
+            0, 0, 0);
+      }
+    };
+    // W: 32 consecutive weights (16 packed bytes, one scale) per thread per
+    // k-step.  FWD: W row n = p0 + ptid%128, k = kt*BK + 32*(ptid/128);
+    // DGRAD: contraction row n = kt*BK + ptid/4, columns p0 + 32*(ptid%4).
+    const int brow = MODE == FWD_Q4 ? ptid & 127 : ptid >> 2;
+    const int bsub = MODE == FWD_Q4 ? ptid >> 7 : ptid & 3;
+    uint32_t w_po = kOOB, w_so = kOOB;
+    if constexpr (MODE == FWD_Q4) {
+      const int64_t n = p0 + brow;
+      if (n < p.P) {
+        w_po = (uint32_t)((n * p.ldw + bsub * 32) >> 1);
+        w_so = (uint32_t)((n * p.ldw) >> 7) * 4;
+      }
+    }
+    const bool dcol_ok = p0 + bsub * 32 < p.P;
+    struct WR {
+      uint4 q;
+      float s;
+    };
+    auto load_W = [&](int kt, WR& w) {
+      if constexpr (MODE == FWD_Q4) {
+        w.q = ld16(rsW, w_po + (uint32_t)(kt * (BK / 2)));
+        w.s = __builtin_bit_cast(float, ld4(rsS, w_so + (uint32_t)(kt >> 1) * 4));
+      } else {
+        const int64_t n = (int64_t)kt * BK + brow;
+        const bool ok = dcol_ok && n < p.Q;
+        const int64_t e = n * p.ldw + p0 + bsub * 32;
+        w.q = ld16(rsW, ok ? (uint32_t)(e >> 1) : kOOB);
+        w.s = __builtin_bit_cast(float, ld4(rsS, ok ? (uint32_t)((e >> 7) * 4) : kOOB));
+      }
+    };
+    Tbl tbl;
+    const uint32_t sh_e = p.hi_first ? 4u : 0u;
+    auto store_B = [&](uint4* bs, const WR& w) {
+      const uint32_t words[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
+#pragma unroll
+      for (int ch = 0; ch < 4; ++ch) {
+        uint32_t o[4];
+        deq8(words[ch], tbl, sh_e, 4u - sh_e, o);
+        int idx;
+        if constexpr (MODE == FWD_Q4) {
+          // fragment (n-block brow/32, slice 2*bsub + ch/2), lane brow%32 + 32*(ch&1)
+          idx = ((brow >> 5) * 4 + 2 * bsub + (ch >> 1)) * 64 + (brow & 31) + 32 * (ch & 1);
+        } else {
+          idx = st::trswz<BN>(brow, bsub * 4 + ch);
+        }
+        bs[idx] = make_uint4(o[0], o[1], o[2], o[3]);
+      }
+    };
+
+    // prologue: A stages for tiles 0 .. WS_DA-2, W ring for tiles 0 .. WS_PW-1,
+    // B buffer 0 for tile 0.  Each step issues 8 DMAs and 2 W loads.
+    WR wr[WS_PW];
+#pragma unroll
+    for (int j = 0; j < WS_DA - 1; ++j) dma_A(j);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < WS_PW; ++j) load_W(j, wr[j]);
+    tbl = make_tbl(p.lut, wr[0].s);
+    store_B(Bs0, wr[0]);
+    load_W(WS_PW, wr[0]);
+    __builtin_amdgcn_sched_barrier(0);
+    wait_cnt<0, 0>();
+    __syncthreads();
+    // step kt (between barriers kt-1 and kt): DMA tile kt+WS_DA-1 into the
+    // stage tile kt-1 used (free since barrier kt-1), stage tile kt+1's B into
+    // buffer (kt+1)&1 (its tile kt-1 was last read before barrier kt-1), and
+    // make sure tile kt+1's A has landed before barrier kt.  Tile kt+1's DMAs
+    // came one step earlier; at most the 10 operations of this step follow.
+    auto step = [&](int kt, int u) {
+      dma_A(kt + WS_DA - 1);
+      __builtin_amdgcn_sched_barrier(0);
+      const int nb = u & 1;
+      if (MODE == DGRAD_Q4 || nb == 0) tbl = make_tbl(p.lut, wr[u].s);
+      store_B(Bs0 + nb * B_ST, wr[u]);
+      load_W(kt + 1 + WS_PW, wr[u]);
+      __builtin_amdgcn_sched_barrier(0);
+      wait_cnt<10, 0>();  // tile kt+1's A has landed, this step's B stores are done
+      bar();
+    };
+    // whole groups of WS_PW steps carry no conditions (static ring slots)
+    int kt = 0;
+    for (; kt + WS_PW <= KT; kt += WS_PW) {
+#pragma unroll
+      for (int v = 0; v < WS_PW; ++v) step(kt + v, (v + 1) % WS_PW);
     }
 #pragma unroll
-    for (int i = 0; i < FM; ++i) {
-      const int rl = wm * WM + i * 32;
-      f32x16 la;
-      if (lora) {
+    for (int v = 0; v < WS_PW - 1; ++v)
+      if (kt + v < KT) step(kt + v, (v + 1) % WS_PW);
+    // the DMAs of the last steps (tiles past the end) must land before the
+    // epilogue reuses LDS
+    wait_cnt<0>();
+  } else {
+    // ------------------------------------------------------------ consumer
 #pragma unroll
-        for (int v = 0; v < 16; ++v) la[v] = 0.0f;
-        for (int kk = 0; kk < p.lora_k; kk += 2) {
-          int kx = kk + (lane >> 5);
-          float av = Ts[(rl + (lane & 31)) * tstride + coff + kx];
-          float bv = TL::DGRAD ? Ls[kx * lstride + cl + (lane & 31)]
-                               : Ls[(cl + (lane & 31)) * lstride + kx];
-          la = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, la, 0, 0, 0);
-        }
-      }
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int64_t m = m0 + rl + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-        if (m < mend && pcol < p.P) {
-          float y = st::bf16r(acc[i][j][v]);
-          if (lora) {
-            if (TL::DGRAD)
-              y = st::bf16r(y + st::bf16r(la[v]));
-            else
-              y = st::bf16r(y + la[v] * p.lora_scale);
-          }
-          if (p.R) y = st::bf16r(st::bf16_to_f32(p.R[m * p.ldr + pcol]) + y);
-          p.C[m * p.ldc + pcol] = st::f32_to_bf16(y);
-        }
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+    // A: row wm*WM + 32i + lane%32, chunk 2s + lane/32 at its swizzled
+    // position (the row's bits 1-3 come from lane%32 alone); B fragment-major
+    // (forward) or transposed (dgrad)
+    const int a_lane = (wm * WM + (lane & 31)) * 8, a_f = ((lane & 31) >> 1) & 7;
+    auto read_frags = [&](const uint4* as, const uint4* bs, int s, bf16x8 (&a)[FM],
+                          bf16x8 (&b)[FN]) {
+      const uint4* ap = as + a_lane + ((2 * s + (lane >> 5)) ^ a_f);
+#pragma unroll
+      for (int i = 0; i < FM; ++i) a[i] = __builtin_bit_cast(bf16x8, ap[i * 32 * 8]);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        if constexpr (MODE == DGRAD_Q4)
+          b[j] = st::tr_operand<BN>(bs, s * 16, wn * WN + j * 32, lane);
+        else
+          b[j] = __builtin_bit_cast(bf16x8, bs[((wn * FN + j) * 4 + s) * 64 + lane]);
       }
+    };
+    auto mfmas = [&](const bf16x8 (&a)[FM], const bf16x8 (&b)[FN]) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+    };
+    bf16x8 fa0[FM], fb0[FN], fa1[FM], fb1[FN];
+    __syncthreads();
+    read_frags(As0, Bs0, 0, fa0, fb0);
+    // fragments one slice ahead; the barrier before slice 3 (as in gemm_kernel)
+    auto step = [&](int kt, int cur) {
+      const uint4* as = As0 + (kt % WS_DA) * A_ST;
+      const uint4* bs = Bs0 + cur * B_ST;
+      read_frags(as, bs, 1, fa1, fb1);
+      mfmas(fa0, fb0);
+      __builtin_amdgcn_sched_barrier(0);
+      read_frags(as, bs, 2, fa0, fb0);
+      mfmas(fa1, fb1);
+      __builtin_amdgcn_sched_barrier(0);
+      read_frags(as, bs, 3, fa1, fb1);
+      mfmas(fa0, fb0);
+      wait_cnt<63, 0>();  // this tile's last fragment reads are done
+      bar();
+      read_frags(As0 + ((kt + 1) % WS_DA) * A_ST, Bs0 + (cur ^ 1) * B_ST, 0, fa0, fb0);
+      mfmas(fa1, fb1);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    for (int kt = 0; kt < KT; kt += 2) {
+      step(kt, 0);
+      if (kt + 1 < KT) step(kt + 1, 1);
     }
   }
+  // every wave's last LDS reads are done before the epilogue reuses LDS
+  __syncthreads();
+  gemm_epilogue<MODE == DGRAD_Q4, BM, BN, NT, FM, FN, WM, WN>(p, acc, ldsA, m0, mend, p0, wm, wn,
+                                                              tid, lane, wave < 4, Lg);
+}
+
+template <int MODE>
+int launch_ws(const GemmParams& p, hipStream_t stream) {
+  constexpr int BM = 256, BN = 128;
+  int64_t tiles = st::cdiv(p.M, BM) * st::cdiv(p.P, BN);
+  if (tiles > 0x7fffffff) return st::fail(ST_EUNSUPPORTED, "q4gemm: too many tiles");
+  if (p.T) {
+    const int64_t need = (int64_t)BM * (p.lora_cols + 1) +
+                         (MODE == DGRAD_Q4 ? (int64_t)p.lora_k * BN : (int64_t)BN * (p.lora_k + 1));
+    if (need > (int64_t)WS_DA * BM * BK / 8 * 4)
+      return st::fail(ST_EUNSUPPORTED, "q4gemm: LoRA epilogue (%d columns) exceeds tile LDS",
+                      p.lora_cols);
+  }
+  gemm_ws_kernel<MODE><<<(unsigned)tiles, 512, 0, stream>>>(p);
+  return st::check_launch("q4gemm");
 }
 
 template <int MODE, int BM, int BN, int WAVES, int WAVES_M = 2>
@@ -509,14 +784,16 @@ int launch(const GemmParams& p, hipStream_t stream) {
 }
 
 // 256-row tiles halve the dequant work per MFMA against 128-row ones but need
-// enough tiles to cover the 256 CUs: 256x256 (8 waves, 2x4) where that gives
-// >= 192 tiles, else 256x128 (8 waves, 4x2), else 128x128 (4 waves).
+// enough tiles to cover the 256 CUs.  Forward with >= 192 tiles of 256x256:
+// the 256x256 8-wave kernel; otherwise the warp-specialised 256x128 kernel
+// (2562) where it yields >= 192 tiles; else 128x128 (4 waves).  ST_GEMM_TILE
+// forces one (128, 256, 2561 = 256x128 8 waves, 2562, 2564 = 256x256 4 waves).
 int tile_choice(int mode, int64_t M, int64_t P) {
   const char* env = getenv("ST_GEMM_TILE");
   if (env) return atoi(env);
   // the transposed-operand dgrad runs out of registers at 256x256 (8 waves)
   if (mode == FWD_Q4 && st::cdiv(M, 256) * st::cdiv(P, 256) >= 192) return 256;
-  if (st::cdiv(M, 256) * st::cdiv(P, 128) >= 192) return 2561;
+  if (st::cdiv(M, 256) * st::cdiv(P, 128) >= 192) return 2562;
   return 128;
 }
 
@@ -527,6 +804,7 @@ int dispatch(const GemmParams& p, hipStream_t stream) {
     const int t = tile_choice(MODE, p.M, p.P);
     if (t == 256) return launch<MODE, 256, 256, 8>(p, stream);
     if (t == 2561) return launch<MODE, 256, 128, 8, 4>(p, stream);
+    if (t == 2562) return launch_ws<MODE>(p, stream);
     if constexpr (MODE == FWD_Q4)
       if (t == 2564) return launch<MODE, 256, 256, 4>(p, stream);
   }

@@ -135,7 +135,7 @@ def _close_bf16(got, ref, what):
 SHAPES = [(64, 256, 256), (100, 384, 512), (37, 96, 688), (300, 512, 1024), (1, 128, 128)]
 
 
-@pytest.mark.parametrize("tile", ["128", "2561", "256"])
+@pytest.mark.parametrize("tile", ["128", "2561", "2562", "256"])
 @pytest.mark.parametrize("fmt", ["nf4-g128", "int4-sym-g128"])
 @pytest.mark.parametrize("M,N,K", SHAPES)
 @pytest.mark.parametrize("lora,residual", [(False, False), (True, False), (True, True)])
@@ -163,7 +163,7 @@ def test_q4_linear_fwd_vs_oracle(dev, oracle_codec, monkeypatch, tile, fmt, M, N
     _close_bf16(y, ref, f"fwd {fmt} {M}x{N}x{K} tile{tile}")
 
 
-@pytest.mark.parametrize("tile", ["128", "2561", "256"])
+@pytest.mark.parametrize("tile", ["128", "2561", "2562", "256"])
 @pytest.mark.parametrize("M,N,K", [(64, 256, 256), (100, 384, 512), (37, 128, 688), (300, 512, 1024)])
 @pytest.mark.parametrize("lora", [False, True])
 def test_q4_linear_dgrad_and_lora_grads_vs_oracle(dev, oracle_codec, monkeypatch, tile, M, N, K, lora):
