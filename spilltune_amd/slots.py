@@ -151,7 +151,7 @@ class Q4SlotSession:
     asynchronous = True
 
     def __init__(self, blocks, device, *, host_budget_bytes, device_budget_bytes, slots=2,
-                 prefetch=True, pin=True):
+                 prefetch=True, pin=True, image_loader=None):
         self.device = torch.device(device)
         if self.device.type != "cuda":
             raise ValueError("unsupported_capability: the 4-bit slot session requires a GPU device")
@@ -169,10 +169,14 @@ class Q4SlotSession:
             raise MemoryError("resource_budget: a multi-block plan needs two slots")
         self.positions = {id(b): i for i, b in enumerate(self.blocks)}
         self.prefetch = prefetch
+        # image_loader(block, layout, out) fills a block's image itself (an
+        # archive streams its files straight into the pinned buffer);
+        # default: pack the block's host tensors
+        fill = image_loader or pack_image
         self.images = {}
         for b in self.blocks:
             img = torch.empty(self.layouts[id(b)].nbytes, dtype=torch.uint8, pin_memory=pin)
-            pack_image(b, self.layouts[id(b)], img)
+            fill(b, self.layouts[id(b)], img)
             self.images[id(b)] = img
         self.pinned_capacity_bytes = self.host_bytes if pin else 0
         self.upload_capacity = 0
@@ -379,6 +383,26 @@ class ResidentSession:
         self.views.clear()
 
 
+def make_archive_block(reader, index: int, *, heads: int, kv_heads: int, head_dim: int,
+                       eps: float, rank: int, alpha: float, targets, device, functional=None,
+                       generator=None, prefix: str | None = None) -> BlockPlan:
+    """A BlockPlan for layer ``index`` of an ``archive.ArchiveReader``: storage
+    specs from the archive manifest, raw entries as meta tensors (layout only);
+    pass ``reader.image_loader(prefix)`` to the session to fill its image."""
+    from .dense import dense_block, lora_kwargs
+    from .lora import create_lora_for_block
+    prefix = prefix if prefix is not None else f"model.layers.{index}."
+    host, specs = reader.block_host_weights(prefix)
+    shapes = {n: tuple(v["spec"]["shape"]) for n, v in specs.items()}
+    adapters = create_lora_for_block(index, "full_attention", shapes, rank=rank, alpha=alpha,
+                                     device=device, targets=tuple(targets), architecture="llama",
+                                     generator=generator)
+    kwargs = {"heads": heads, "kv_heads": kv_heads, "head_dim": head_dim, "eps": eps,
+              **lora_kwargs(adapters)}
+    return BlockPlan(index, "full_attention", functional or dense_block, kwargs, host, adapters,
+                     specs)
+
+
 def make_dense_block(index: int, weights: dict, *, codec: str, heads: int, kv_heads: int,
                      head_dim: int, eps: float, rank: int, alpha: float, targets, device,
                      functional=None, generator=None) -> BlockPlan:
@@ -410,4 +434,4 @@ def make_dense_block(index: int, weights: dict, *, codec: str, heads: int, kv_he
 
 
 __all__ = ["BlockPlan", "SlotLayout", "plan_layout", "pack_image", "views_of", "Q4SlotSession",
-           "ResidentSession", "make_dense_block"]
+           "ResidentSession", "make_dense_block", "make_archive_block"]
