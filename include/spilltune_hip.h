@@ -208,6 +208,19 @@ int st_linear_bf16_dgrad(const uint16_t* dy, int64_t M, int64_t N, int64_t lddy,
                          const uint16_t* w, int64_t K, int64_t ldw, uint16_t* dx, int64_t lddx,
                          st_stream_t stream);
 
+/* Causal-LM terminal, one row of logits per workgroup, in place
+ * (training/engine.py:58-75; quantization/native_terminal.py:11-32 replace
+ * logits.float() -> F.cross_entropy(sum, ignore_index) and its VJP):
+ *   loss_rows[r] = logsumexp(x_r) - x_r[labels[r]]   (0 for ignore_index rows)
+ *   logits[r][c] <- bf16((softmax(x_r)[c] - [c == labels[r]]) * grad_scale)
+ * with x_r the fp32 values of the bf16 row (row stride ld >= vocab).  Labels
+ * must be ignore_index or in [0, vocab) (checked by the caller); grad_scale is
+ * 1/normalization.  Pair with st_linear_bf16_fwd (logits = h head^T) before
+ * and st_linear_bf16_dgrad (dh = dlogits head) after. */
+int st_cross_entropy_rows(uint16_t* logits, int64_t rows, int64_t vocab, int64_t ld,
+                          const int64_t* labels, int64_t ignore_index, float grad_scale,
+                          float* loss_rows, st_stream_t stream);
+
 /* ---------------------------------------------------------------------
  * Mixture of experts (adapters/qwen3_moe.py:95-113; adapters/deepseek.py:
  * 115-176).  Tokens T, picks per token k, experts E; a "pick" is (token t,

@@ -7,9 +7,11 @@ I/O around it).
   (engine.py:36-45).
 * :func:`microbatch` -- embedding, layers, full-sequence terminal norm,
   token-chunked head + summed cross-entropy / normaliser, norm VJP, one
-  decoder backward (engine.py:48-79).  The terminal norm is the HIP RMSNorm;
-  the head GEMM and CE are PyTorch ops on the device (a fused terminal kernel
-  is a later row).
+  decoder backward (engine.py:48-79).  The terminal runs on the HIP path:
+  RMSNorm kernels for the norm and its VJP, and ``ops.chunked_causal_loss``
+  (native_terminal.py:11-47) -- per token chunk a bf16 head GEMM, one
+  in-place cross-entropy/gradient pass over the bf16 logits and a bf16 GEMM
+  back to the hidden size.
 * :class:`AdamW` -- the fp32 update in torch.optim.AdamW's non-foreach order
   (optimizer.py:324-342), on the device.
 * :func:`train` -- the optimizer-step loop with gradient accumulation over
@@ -62,26 +64,15 @@ def microbatch(model, session, input_ids, labels, *, normalization, token_chunk,
     hidden = forward(model, session, embedded, positions, masks, accumulate=accumulate)
     terminal_input = hidden.detach().requires_grad_(True)
     normalized = model.terminal_norm(terminal_input)
-    normalized_gradient = torch.zeros_like(normalized)
-    loss_sum = torch.zeros((), device=device)
-    labels = labels.to(device)
-    for start in range(0, input_ids.shape[1] - 1, token_chunk):
-        end = min(start + token_chunk, input_ids.shape[1] - 1)
-        target = labels[:, start + 1:end + 1]
-        if not (target != -100).any():
-            continue
-        h = normalized[:, start:end].detach().requires_grad_(True)
-        logits = F.linear(h, model.head)
-        chunk = F.cross_entropy(logits.float().reshape(-1, logits.shape[-1]), target.reshape(-1),
-                                ignore_index=-100, reduction="sum")
-        (grad,) = torch.autograd.grad(chunk / normalization, h)
-        normalized_gradient[:, start:end].copy_(grad.detach())
-        loss_sum += chunk.detach()
-    (gradient,) = torch.autograd.grad(normalized, terminal_input, normalized_gradient)
-    if not torch.isfinite(loss_sum) or not torch.isfinite(gradient).all():
+    chunks = ops.supervised_chunk_intervals(labels, token_chunk)
+    loss = ops.chunked_causal_loss(normalized, model.head, labels.to(device),
+                                   normalization=normalization, token_chunk=token_chunk,
+                                   supervised_chunks=chunks)
+    (gradient,) = torch.autograd.grad(loss, terminal_input)
+    if not torch.isfinite(loss) or not torch.isfinite(gradient).all():
         raise FloatingPointError("non-finite causal loss/gradient")
     hidden.backward(gradient)
-    return float(loss_sum / normalization), embedded.grad.detach().clone()
+    return float(loss.detach()), embedded.grad.detach().clone()
 
 
 class AdamW:

@@ -20,6 +20,8 @@ to another implementation.
 """
 from __future__ import annotations
 
+import math
+
 from dataclasses import dataclass, field
 
 import torch
@@ -328,6 +330,103 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     return _RMSNorm.apply(x.contiguous(), weight.detach().contiguous(), eps)
 
 
+# ----------------------------------------------------------------- terminal
+def linear_bf16(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """``y = bf16(x w^T)`` on the MFMA GEMM (fp32 accumulation)."""
+    M, K = x.shape
+    N = w.shape[0]
+    y = torch.empty((M, N), dtype=_BF16, device=x.device)
+    _lib.call("st_linear_bf16_fwd", _lib.ptr(x), M, K, x.stride(0), _lib.ptr(w), N, w.stride(0),
+              _lib.ptr(y), N, _lib.stream_handle(x.device))
+    return y
+
+
+def linear_bf16_dgrad(dy: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """``dx = bf16(dy w)`` on the MFMA GEMM (fp32 accumulation)."""
+    M, N = dy.shape
+    K = w.shape[1]
+    dx = torch.empty((M, K), dtype=_BF16, device=dy.device)
+    _lib.call("st_linear_bf16_dgrad", _lib.ptr(dy), M, N, dy.stride(0), _lib.ptr(w), K,
+              w.stride(0), _lib.ptr(dx), K, _lib.stream_handle(dy.device))
+    return dx
+
+
+def supervised_chunk_intervals(labels: torch.Tensor, token_chunk: int) -> tuple:
+    """Token chunks [start, end) of the shifted targets that hold at least one
+    supervised label (native_terminal.py:44-46), from host labels."""
+    if type(token_chunk) is not int or token_chunk < 1:
+        raise ValueError("invalid terminal token chunk")
+    labels = labels.cpu()
+    S = labels.shape[1]
+    return tuple((start, min(start + token_chunk, S - 1)) for start in range(0, S - 1, token_chunk)
+                 if bool((labels[:, start + 1:min(start + token_chunk, S - 1) + 1] != -100).any()))
+
+
+class _ChunkedCE(torch.autograd.Function):
+    """Shifted, token-chunked causal-LM loss over the frozen head
+    (quantization/native_terminal.py:11-37): per chunk one bf16 head GEMM,
+    one in-place cross-entropy/gradient pass over the bf16 logits
+    (``st_cross_entropy_rows``) and one bf16 GEMM back to the hidden size.
+    The forward returns sum(CE)/normalization and keeps the full VJP; the
+    backward scales it."""
+
+    @staticmethod
+    def forward(ctx, normalized, head, labels, normalization, token_chunk, chunks):
+        if type(token_chunk) is not int or token_chunk < 1 or not math.isfinite(normalization) \
+                or normalization <= 0:
+            raise ValueError("invalid terminal token chunk/normalization")
+        if labels.shape != normalized.shape[:2] or head.requires_grad:
+            raise ValueError("invalid terminal labels/trainable frozen head")
+        if normalized.dtype != _BF16 or head.dtype != _BF16:
+            raise ValueError("terminal expects bf16 hidden states and head")
+        B, S, H = normalized.shape
+        V = head.shape[0]
+        dev = normalized.device
+        labels = labels.to(dev, torch.int64)
+        bad = ((labels < 0) & (labels != -100)) | (labels >= V)
+        if bool(bad.any()):
+            raise ValueError("terminal labels must be -100 or in [0, vocab)")
+        head = head.detach().contiguous()
+        vjp = torch.zeros_like(normalized)
+        total = torch.zeros((), dtype=_F32, device=dev)
+        scale = float(torch.tensor(1.0, dtype=_F32) / normalization)
+        stream = _lib.stream_handle(dev)
+        # rows per pass: the logits block stays below the GEMM's 2 GiB operand limit
+        max_rows = max(1, ((1 << 31) - 1) // (2 * V))
+        for start, end in chunks:
+            h = normalized[:, start:end].detach().contiguous().view(-1, H)
+            target = labels[:, start + 1:end + 1].contiguous().view(-1)
+            dh = torch.empty_like(h)
+            for r0 in range(0, h.shape[0], max_rows):
+                r1 = min(r0 + max_rows, h.shape[0])
+                logits = linear_bf16(h[r0:r1], head)
+                loss_rows = torch.empty(r1 - r0, dtype=_F32, device=dev)
+                _lib.call("st_cross_entropy_rows", _lib.ptr(logits), r1 - r0, V, V,
+                          _lib.ptr(target[r0:r1]), -100, scale, _lib.ptr(loss_rows), stream)
+                dh[r0:r1].copy_(linear_bf16_dgrad(logits, head))
+                total += loss_rows.sum()
+                del logits, loss_rows
+            vjp[:, start:end].copy_(dh.view(B, end - start, H))
+        ctx.save_for_backward(vjp)
+        return total / normalization
+
+    @staticmethod
+    def backward(ctx, grad):
+        (vjp,) = ctx.saved_tensors
+        return vjp * grad, None, None, None, None, None
+
+
+def chunked_causal_loss(normalized, head, labels, *, normalization, token_chunk,
+                        supervised_chunks=None):
+    """``sum CE(shifted) / normalization`` with the chunked terminal above
+    (native_terminal.py:39-47); chunk intervals default to those of the host
+    labels."""
+    if supervised_chunks is None:
+        supervised_chunks = supervised_chunk_intervals(labels, token_chunk)
+    return _ChunkedCE.apply(normalized, head, labels, normalization, token_chunk,
+                            tuple(supervised_chunks))
+
+
 # ----------------------------------------------------------------- RoPE
 class _RopeHeads(torch.autograd.Function):
     """Token-major projection output columns -> [B, heads, S, D] (rotated)."""
@@ -504,4 +603,6 @@ def attention_scale(head_dim: int) -> float:
 
 
 __all__ = ["Q4Weight", "concat_rows", "q4_lora_linear", "rms_norm", "rope_qkv", "rope_heads",
-           "causal_attention", "swiglu", "swiglu_pair", "lora_gemm", "attention_scale"]
+           "causal_attention", "swiglu", "swiglu_pair", "lora_gemm", "attention_scale",
+           "linear_bf16", "linear_bf16_dgrad", "supervised_chunk_intervals",
+           "chunked_causal_loss"]
