@@ -15,7 +15,9 @@ I/O around it).
 * :class:`AdamW` -- the fp32 update in torch.optim.AdamW's non-foreach order
   (optimizer.py:324-342), on the device.
 * :func:`train` -- the optimizer-step loop with gradient accumulation over
-  cyclic rows (engine.py:162-182).
+  cyclic rows (engine.py:162-182), microbatch-major as the reference or
+  layer-major (:func:`window_layer_major`: one layer load per phase per
+  accumulation window instead of one per microbatch, same results).
 * :class:`DenseModel` -- the adapter surface the engine uses
   (adapters/protocol.py:23-34) for a Llama-family model whose decoder
   matrices are stored 4-bit.
@@ -29,7 +31,7 @@ import torch.nn.functional as F
 
 from . import ops, slots
 from .dense import positions_and_masks
-from .recompute import streaming_block
+from .recompute import _borrow_weights, _call_functional_block, streaming_block
 
 
 def flatten(model) -> dict:
@@ -75,6 +77,66 @@ def microbatch(model, session, input_ids, labels, *, normalization, token_chunk,
     return float(loss.detach()), embedded.grad.detach().clone()
 
 
+def window_layer_major(model, session, items, *, normalization, token_chunk):
+    """One gradient-accumulation window processed layer by layer, so each
+    layer's 4-bit image crosses PCIe once per phase instead of once per
+    microbatch (the reference streams every layer for every microbatch,
+    engine.py:168-178):
+
+    * forward: every microbatch through layer i (no grad) before layer i+1,
+      keeping each microbatch's layer inputs (one bf16 [B,S,H] per layer and
+      microbatch, as the recompute driver saves);
+    * terminal per microbatch, in order (as ``microbatch``);
+    * backward: per layer in reverse, the recompute + VJP of every microbatch
+      in order, adding adapter gradients (the first microbatch replaces).
+
+    For each layer the fp32 adapter-gradient sums take the microbatches in the
+    same order as the microbatch-major loop, so the gradients and losses are
+    the same bits.  Returns the per-microbatch losses."""
+    device = model.device
+    mbs = []
+    for ids, labels in items:
+        valid = torch.ones_like(ids, dtype=torch.bool)
+        positions, masks = model.positions_and_masks(valid)
+        embedded = F.embedding(ids.cpu(), model.embedding).to(device)
+        mbs.append({"pos": positions, "masks": masks, "h": [embedded], "labels": labels})
+    for block in model.blocks:
+        with _borrow_weights(session.reloader(block), "forward") as weights, torch.no_grad():
+            for mb in mbs:
+                mb["h"].append(_call_functional_block(block.functional, mb["h"][-1], mb["pos"],
+                                                      mb["masks"][block.kind], weights,
+                                                      block.kwargs))
+    losses = []
+    for mb in mbs:
+        terminal_input = mb["h"].pop().detach().requires_grad_(True)
+        normalized = model.terminal_norm(terminal_input)
+        loss = ops.chunked_causal_loss(
+            normalized, model.head, mb["labels"].to(device), normalization=normalization,
+            token_chunk=token_chunk,
+            supervised_chunks=ops.supervised_chunk_intervals(mb["labels"], token_chunk))
+        (mb["g"],) = torch.autograd.grad(loss, terminal_input)
+        if not torch.isfinite(loss) or not torch.isfinite(mb["g"]).all():
+            raise FloatingPointError("non-finite causal loss/gradient")
+        losses.append(float(loss.detach()))
+    for block in reversed(model.blocks):
+        ordered = sorted(block.adapters.values(), key=lambda p: p.name)
+        with _borrow_weights(session.reloader(block), "backward") as weights:
+            for k, mb in enumerate(mbs):
+                hidden = mb["h"].pop().detach().requires_grad_(True)
+                with torch.enable_grad():
+                    out = _call_functional_block(block.functional, hidden, mb["pos"],
+                                                 mb["masks"][block.kind], weights, block.kwargs)
+                grads = torch.autograd.grad(out, [hidden] + [t for p in ordered for t in (p.A, p.B)],
+                                            mb["g"])
+                for i, proj in enumerate(ordered):
+                    if k == 0:
+                        proj.zero_grad()
+                    proj.grad_A.add_(grads[1 + 2 * i].detach().to(proj.grad_A))
+                    proj.grad_B.add_(grads[2 + 2 * i].detach().to(proj.grad_B))
+                mb["g"] = grads[0]
+    return losses
+
+
 class AdamW:
     """Bias-corrected fp32 AdamW over LoRA projections (optimizer.py:227-342)."""
 
@@ -107,8 +169,10 @@ class AdamW:
 
 
 def train(model, session, rows, *, steps, accumulation=1, lr=1e-4, weight_decay=0.0,
-          token_chunk=64):
-    """Optimizer-step loop with cyclic rows (engine.py:162-182); returns losses."""
+          token_chunk=64, layer_major=False):
+    """Optimizer-step loop with cyclic rows (engine.py:162-182); returns losses.
+    ``layer_major`` runs each accumulation window with ``window_layer_major``
+    (same results, one layer load per phase per window)."""
     projections = flatten(model)
     optimizer = AdamW(lr=lr, weight_decay=weight_decay)
     cursor, losses = 0, []
@@ -118,10 +182,17 @@ def train(model, session, rows, *, steps, accumulation=1, lr=1e-4, weight_decay=
         optimizer.zero_grad(projections)
         loss = 0.0
         with session.run():
-            for i, (ids, labels) in enumerate(items):
-                micro, _ = microbatch(model, session, ids, labels, normalization=normalization,
-                                      token_chunk=token_chunk, accumulate=i > 0)
-                loss += micro
+            if layer_major:
+                for micro in window_layer_major(model, session, items,
+                                                normalization=normalization,
+                                                token_chunk=token_chunk):
+                    loss += micro
+            else:
+                for i, (ids, labels) in enumerate(items):
+                    micro, _ = microbatch(model, session, ids, labels,
+                                          normalization=normalization, token_chunk=token_chunk,
+                                          accumulate=i > 0)
+                    loss += micro
             optimizer.step(projections)
         cursor += accumulation
         losses.append(loss)

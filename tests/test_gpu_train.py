@@ -95,3 +95,44 @@ def test_tiny_llama_50_step_loss_curve_matches_oracle(oracle_codec, streamed):
     if streamed:
         assert session.hits > 0 and session.reloads == steps * 2 * CFG["layers"]
     session.close()
+
+
+def test_layer_major_window_same_bits_fewer_loads():
+    """Gradient accumulation over 3 microbatches, 4 streamed layers in 2 slots:
+    the layer-major window gives the same losses and adapter parameters (bit
+    for bit) as the reference's microbatch-major loop, with about a third of
+    the layer loads."""
+    layers, emb, norm, head = tiny_weights(1234)
+    layers = layers + tiny_weights(4321)[0]  # 4 layers
+    dev = torch.device("cuda:0")
+    gd = torch.Generator().manual_seed(7)
+    rows = []
+    for _ in range(3):
+        ids = torch.randint(0, CFG["vocab"], (2, 128), generator=gd)
+        rows.append((ids, ids.clone()))
+    results = []
+    for layer_major in (False, True):
+        model = engine.DenseModel(embedding=emb, norm=norm, head=head, layers=layers,
+                                  heads=CFG["heads"], kv_heads=CFG["kv"], head_dim=CFG["D"],
+                                  eps=CFG["eps"], theta=CFG["theta"], rank=CFG["r"],
+                                  alpha=CFG["alpha"], targets=TARGETS, device=dev)
+        g = torch.Generator().manual_seed(3)
+        with torch.no_grad():
+            for block in model.blocks:
+                for name in sorted(block.adapters):
+                    p = block.adapters[name]
+                    p.A.copy_(torch.randn(p.A.shape, generator=g) * 0.05)
+                    p.B.copy_(torch.randn(p.B.shape, generator=g) * 0.02)
+        session = slots.Q4SlotSession(model.blocks, dev, host_budget_bytes=1 << 34,
+                                      device_budget_bytes=1 << 34, slots=2)
+        losses = engine.train(model, session, rows, steps=3, accumulation=3, lr=2e-3,
+                              token_chunk=64, layer_major=layer_major)
+        params = {f"{b.index}:{n}": (p.A.detach().cpu(), p.B.detach().cpu())
+                  for b in model.blocks for n, p in b.adapters.items()}
+        results.append((losses, params, session.reloads))
+        session.close()
+    (l0, p0, r0), (l1, p1, r1) = results
+    assert l0 == l1, (l0, l1)
+    for k in p0:
+        assert torch.equal(p0[k][0], p1[k][0]) and torch.equal(p0[k][1], p1[k][1]), k
+    assert r1 * 2 < r0, (r0, r1)
