@@ -106,20 +106,27 @@ def _rotate(x, cos, sin):
 
 
 def dense_block(hidden, rotary_tables, mask, *, heads, kv_heads, head_dim, eps,
-                weights: dict, loras: dict, feed_forward=None):
-    """One Llama decoder block (dense.py:120-153); ``weights`` holds bf16 matrices
-    keyed ``<proj>.weight`` plus the two norm vectors, ``loras`` maps projection
-    names to :class:`Lora` (absent projections have no adapter).  A
-    ``feed_forward(x, weights)`` replaces the SwiGLU MLP (dense.py:152)."""
+                weights: dict, loras: dict, feed_forward=None, qk_norm=False):
+    """One Llama/Qwen3 decoder block (dense.py:120-153); ``weights`` holds bf16
+    matrices keyed ``<proj>.weight`` plus the norm vectors, ``loras`` maps
+    projection names to :class:`Lora` (absent projections have no adapter).
+    ``qk_norm`` (Qwen3) normalises each head of q and k over head_dim with
+    ``self_attn.q_norm.weight`` / ``k_norm.weight`` before RoPE, on the
+    [B, S, heads, D] view (dense.py:128-133).  A ``feed_forward(x, weights)``
+    replaces the SwiGLU MLP (dense.py:152)."""
     def linear(x, name):
         return lora_linear(x, weights[name + ".weight"], loras.get(name))
 
     residual = hidden
     x = rms(hidden, weights["input_layernorm.weight"], eps)
     shape = (*x.shape[:-1], -1, head_dim)
-    q = linear(x, "self_attn.q_proj").view(shape).transpose(1, 2)
-    k = linear(x, "self_attn.k_proj").view(shape).transpose(1, 2)
+    q = linear(x, "self_attn.q_proj").view(shape)
+    k = linear(x, "self_attn.k_proj").view(shape)
     v = linear(x, "self_attn.v_proj").view(shape).transpose(1, 2)
+    if qk_norm:
+        q = rms(q, weights["self_attn.q_norm.weight"], eps)
+        k = rms(k, weights["self_attn.k_norm.weight"], eps)
+    q, k = q.transpose(1, 2), k.transpose(1, 2)
     cos, sin = (t.unsqueeze(1) for t in rotary_tables)
     q, k = _rotate(q, cos, sin), _rotate(k, cos, sin)
     group = heads // kv_heads

@@ -1,4 +1,4 @@
-"""Llama/Qwen2 dense decoder block on 4-bit slot weights (HIP path).
+"""Llama/Qwen2/Qwen3 dense decoder block on 4-bit slot weights (HIP path).
 
 ``dense_block`` keeps the functional contract of adapters/dense.py:120-153
 (/root/reference/src/ram_vram_finetune): called as
@@ -11,6 +11,8 @@ no reference to slot memory.  Differences in *how*, not *what*:
 * LoRA may sit on any of the seven projections (``lora_q`` .. ``lora_down``);
 * when q|k|v (and gate|up) are adjacent in the slot they run as one GEMM over
   the concatenated rows, and the residual adds run in the o/down epilogues;
+* ``qk_norm`` (Qwen3): each head of q and k is RMS-normalised over head_dim
+  by the HIP RMSNorm kernel before RoPE;
 * ``attention_mask`` is a :class:`CausalMask` marker (all-valid causal
   attention, the only mask the engine builds for unpadded rows) -- the mask
   is applied structurally by the softmax kernel, exactly as adding
@@ -58,8 +60,6 @@ def _weight(weights, name):
 def dense_block(hidden_states, position_embeddings, attention_mask, *, heads, kv_heads, head_dim,
                 eps, lora_q=None, lora_k=None, lora_v=None, lora_o=None, lora_gate=None,
                 lora_up=None, lora_down=None, qk_norm=False, feed_forward=None, **weights):
-    if qk_norm:
-        raise ValueError("unsupported_capability: qk_norm not on the HIP path")
     if attention_mask is not None and not isinstance(attention_mask, CausalMask):
         raise ValueError("unsupported_capability: only the causal mask marker is supported")
     B, S, Hd = hidden_states.shape
@@ -68,15 +68,28 @@ def dense_block(hidden_states, position_embeddings, attention_mask, *, heads, kv
     residual = x2d
     xn = ops.rms_norm(x2d, weights["input_layernorm.weight"], eps)
 
+    def head_norm(t, name):  # Qwen3: RMSNorm of every head over head_dim (dense.py:128-133)
+        if not qk_norm:
+            return t
+        rows = t.shape[0]
+        return ops.rms_norm(t.reshape(-1, head_dim), weights[name], eps).reshape(rows, -1)
+
     wq, wk, wv = (_weight(weights, f"self_attn.{p}_proj") for p in "qkv")
     qkv = ops.concat_rows([wq, wk, wv])
     loras_qkv = [lora_q, lora_k, lora_v]
     if qkv is not None and (all(l is None for l in loras_qkv) or all(l is not None for l in loras_qkv)):
         y = ops.q4_lora_linear(xn, qkv, loras_qkv)
+        if qk_norm:
+            nq, nk = heads * head_dim, kv_heads * head_dim
+            y = torch.cat((head_norm(y[:, :nq], "self_attn.q_norm.weight"),
+                           head_norm(y[:, nq:nq + nk], "self_attn.k_norm.weight"),
+                           y[:, nq + nk:]), 1)
         q, k, v = ops.rope_qkv(y, B, S, heads, kv_heads, head_dim, cos, sin)
     else:
-        q = ops.rope_heads(ops.q4_lora_linear(xn, wq, [lora_q]), 0, B, S, heads, head_dim, cos, sin)
-        k = ops.rope_heads(ops.q4_lora_linear(xn, wk, [lora_k]), 0, B, S, kv_heads, head_dim, cos, sin)
+        q = ops.rope_heads(head_norm(ops.q4_lora_linear(xn, wq, [lora_q]), "self_attn.q_norm.weight"),
+                           0, B, S, heads, head_dim, cos, sin)
+        k = ops.rope_heads(head_norm(ops.q4_lora_linear(xn, wk, [lora_k]), "self_attn.k_norm.weight"),
+                           0, B, S, kv_heads, head_dim, cos, sin)
         v = ops.rope_heads(ops.q4_lora_linear(xn, wv, [lora_v]), 0, B, S, kv_heads, head_dim, cos,
                            sin, rotate=False)
 

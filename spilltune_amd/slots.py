@@ -385,7 +385,7 @@ class ResidentSession:
 
 def make_archive_block(reader, index: int, *, heads: int, kv_heads: int, head_dim: int,
                        eps: float, rank: int, alpha: float, targets, device, functional=None,
-                       generator=None, prefix: str | None = None) -> BlockPlan:
+                       generator=None, prefix: str | None = None, qk_norm: bool = False) -> BlockPlan:
     """A BlockPlan for layer ``index`` of an ``archive.ArchiveReader``: storage
     specs from the archive manifest, raw entries as meta tensors (layout only);
     pass ``reader.image_loader(prefix)`` to the session to fill its image."""
@@ -399,13 +399,15 @@ def make_archive_block(reader, index: int, *, heads: int, kv_heads: int, head_di
                                      generator=generator)
     kwargs = {"heads": heads, "kv_heads": kv_heads, "head_dim": head_dim, "eps": eps,
               **lora_kwargs(adapters)}
+    if qk_norm:
+        kwargs["qk_norm"] = True
     return BlockPlan(index, "full_attention", functional or dense_block, kwargs, host, adapters,
                      specs)
 
 
 def make_dense_block(index: int, weights: dict, *, codec: str, heads: int, kv_heads: int,
                      head_dim: int, eps: float, rank: int, alpha: float, targets, device,
-                     functional=None, generator=None) -> BlockPlan:
+                     functional=None, generator=None, qk_norm: bool = False) -> BlockPlan:
     """Encode one dense decoder layer (``weights``: name -> CPU fp32/bf16 tensor,
     HF names without the ``model.layers.{i}.`` prefix) into a BlockPlan whose
     host weights are the flattened 4-bit records (codecs.flatten layout of the
@@ -429,6 +431,8 @@ def make_dense_block(index: int, weights: dict, *, codec: str, heads: int, kv_he
                                      generator=generator)
     kwargs = {"heads": heads, "kv_heads": kv_heads, "head_dim": head_dim, "eps": eps,
               **lora_kwargs(adapters)}
+    if qk_norm:  # Qwen3 (dense.py:128-133); q_norm/k_norm vectors travel as raw entries
+        kwargs["qk_norm"] = True
     return BlockPlan(index, "full_attention", functional or dense_block, kwargs, host, adapters,
                      specs)
 

@@ -27,7 +27,7 @@ def cosine(a, b):
     return (a @ b / (a.norm() * b.norm()).clamp_min(1e-300)).item()
 
 
-def make_layer(cfg, seed, codec="nf4-g128", b_std=0.02, targets=PROJ):
+def make_layer(cfg, seed, codec="nf4-g128", b_std=0.02, targets=PROJ, qk_norm=False):
     g = torch.Generator().manual_seed(seed)
     H, I, D, heads, kv = cfg["H"], cfg["I"], cfg["D"], cfg["heads"], cfg["kv"]
     shapes = {"self_attn.q_proj": (heads * D, H), "self_attn.k_proj": (kv * D, H),
@@ -36,9 +36,12 @@ def make_layer(cfg, seed, codec="nf4-g128", b_std=0.02, targets=PROJ):
     weights = {f"{n}.weight": (torch.randn(s, generator=g) * 0.02).to(BF) for n, s in shapes.items()}
     weights["input_layernorm.weight"] = (1 + 0.05 * torch.randn(H, generator=g)).to(BF)
     weights["post_attention_layernorm.weight"] = (1 + 0.05 * torch.randn(H, generator=g)).to(BF)
+    if qk_norm:
+        weights["self_attn.q_norm.weight"] = (1 + 0.1 * torch.randn(D, generator=g)).to(BF)
+        weights["self_attn.k_norm.weight"] = (1 + 0.1 * torch.randn(D, generator=g)).to(BF)
     block = slots.make_dense_block(0, weights, codec=codec, heads=heads, kv_heads=kv, head_dim=D,
                                    eps=cfg["eps"], rank=cfg["r"], alpha=cfg["alpha"],
-                                   targets=targets, device="cuda:0", generator=g)
+                                   targets=targets, device="cuda:0", generator=g, qk_norm=qk_norm)
     with torch.no_grad():
         for p in block.adapters.values():
             p.B.copy_(torch.randn(p.B.shape, generator=g) * b_std)
@@ -61,8 +64,9 @@ def oracle_weights(block, oracle_codec):
     return out
 
 
-def run_case(cfg, seed, oracle_codec, codec="nf4-g128", streamed=False, targets=PROJ):
-    block, _ = make_layer(cfg, seed, codec, targets=targets)
+def run_case(cfg, seed, oracle_codec, codec="nf4-g128", streamed=False, targets=PROJ,
+             qk_norm=False):
+    block, _ = make_layer(cfg, seed, codec, targets=targets, qk_norm=qk_norm)
     g = torch.Generator().manual_seed(seed + 1)
     B, S, H = cfg["B"], cfg["S"], cfg["H"]
     hidden = torch.randn(B, S, H, generator=g).to(BF)
@@ -71,7 +75,8 @@ def run_case(cfg, seed, oracle_codec, codec="nf4-g128", streamed=False, targets=
     # ---- oracle
     lor = {n: OL.Lora(n, p.A.detach().cpu(), p.B.detach().cpu(), p.alpha)
            for n, p in block.adapters.items()}
-    kw = dict(heads=cfg["heads"], kv_heads=cfg["kv"], head_dim=cfg["D"], eps=cfg["eps"])
+    kw = dict(heads=cfg["heads"], kv_heads=cfg["kv"], head_dim=cfg["D"], eps=cfg["eps"],
+              qk_norm=qk_norm)
     out_ref, gh_ref = OL.streaming_step(hidden, (cos, sin), OL.causal_mask(B, S, BF), dy,
                                         weights=oracle_weights(block, oracle_codec), loras=lor, cfg=kw)
     # ---- HIP path through the recompute driver
@@ -117,6 +122,14 @@ def test_gqa_layer_step_streamed_vs_oracle(oracle_codec):
 def test_reference_default_targets_qvo(oracle_codec):
     """q/v/o only (the reference's default dense targets): unfused q|k|v path."""
     _assert(run_case(TINY, 30, oracle_codec,
+                     targets=("self_attn.q_proj", "self_attn.v_proj", "self_attn.o_proj")))
+
+
+def test_qwen3_qk_norm_layer_step_vs_oracle(oracle_codec):
+    """Qwen3 block: per-head q/k RMSNorm before RoPE, fused q|k|v and the
+    separate-projection path (q/v/o targets)."""
+    _assert(run_case(GQA, 50, oracle_codec, streamed=True, qk_norm=True))
+    _assert(run_case(TINY, 51, oracle_codec, qk_norm=True,
                      targets=("self_attn.q_proj", "self_attn.v_proj", "self_attn.o_proj")))
 
 

@@ -14,15 +14,21 @@ from oracle import layer as L
 PROJ = L.PROJECTIONS
 
 
-def _hf_layer(cfg, weights, loras, dtype):
-    from transformers.models.llama.configuration_llama import LlamaConfig
-    from transformers.models.llama.modeling_llama import LlamaDecoderLayer, LlamaRotaryEmbedding
-    c = LlamaConfig(hidden_size=cfg["H"], intermediate_size=cfg["I"],
-                    num_attention_heads=cfg["heads"], num_key_value_heads=cfg["kv"],
-                    head_dim=cfg["D"], num_hidden_layers=1, vocab_size=32,
-                    rms_norm_eps=cfg["eps"], rope_theta=cfg["theta"])
+def _hf_layer(cfg, weights, loras, dtype, family="llama"):
+    if family == "llama":
+        from transformers.models.llama.configuration_llama import LlamaConfig as Config
+        from transformers.models.llama.modeling_llama import (LlamaDecoderLayer as Layer,
+                                                              LlamaRotaryEmbedding as Rotary)
+    else:
+        from transformers.models.qwen3.configuration_qwen3 import Qwen3Config as Config
+        from transformers.models.qwen3.modeling_qwen3 import (Qwen3DecoderLayer as Layer,
+                                                              Qwen3RotaryEmbedding as Rotary)
+    c = Config(hidden_size=cfg["H"], intermediate_size=cfg["I"],
+               num_attention_heads=cfg["heads"], num_key_value_heads=cfg["kv"],
+               head_dim=cfg["D"], num_hidden_layers=1, vocab_size=32,
+               rms_norm_eps=cfg["eps"], rope_theta=cfg["theta"])
     c._attn_implementation = "eager"
-    layer = LlamaDecoderLayer(c, 0).to(dtype)
+    layer = Layer(c, 0).to(dtype)
     sd = {k: v.to(dtype) for k, v in weights.items()}
     layer.load_state_dict(sd, strict=True)
     layer.requires_grad_(False)
@@ -47,11 +53,11 @@ def _hf_layer(cfg, weights, loras, dtype):
         w = Projection(getattr(mod, leaf), lora)
         setattr(mod, leaf, w)
         wrapped[name] = w
-    rot = LlamaRotaryEmbedding(c)
+    rot = Rotary(c)
     return layer, wrapped, rot
 
 
-def _setup(dtype, seed=0, S=9, B=2):
+def _setup(dtype, seed=0, S=9, B=2, qk_norm=False):
     g = torch.Generator().manual_seed(seed)
     cfg = dict(H=64, I=96, heads=4, kv=2, D=16, eps=1e-5, theta=10000.0)
     H, I, D = cfg["H"], cfg["I"], cfg["D"]
@@ -61,6 +67,9 @@ def _setup(dtype, seed=0, S=9, B=2):
     weights = {f"{n}.weight": torch.randn(s, generator=g) * 0.1 for n, s in shapes.items()}
     weights["input_layernorm.weight"] = 1 + 0.1 * torch.randn(H, generator=g)
     weights["post_attention_layernorm.weight"] = 1 + 0.1 * torch.randn(H, generator=g)
+    if qk_norm:
+        weights["self_attn.q_norm.weight"] = 1 + 0.1 * torch.randn(D, generator=g)
+        weights["self_attn.k_norm.weight"] = 1 + 0.1 * torch.randn(D, generator=g)
     loras = {n: L.Lora(n, torch.randn(4, s[1], generator=g) * 0.1,
                        torch.randn(s[0], 4, generator=g) * 0.1, alpha=8.0) for n, s in shapes.items()}
     hidden = torch.randn(B, S, H, generator=g)
@@ -68,11 +77,14 @@ def _setup(dtype, seed=0, S=9, B=2):
     return cfg, weights, loras, hidden.to(dtype), dy.to(dtype)
 
 
+@pytest.mark.parametrize("family", ["llama", "qwen3"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_dense_block_matches_transformers_llama_layer(dtype):
-    cfg, weights, loras, hidden, dy = _setup(dtype)
+def test_dense_block_matches_transformers_layer(dtype, family):
+    """Llama, and Qwen3 with per-head q/k RMSNorm (qk_norm)."""
+    qk = family == "qwen3"
+    cfg, weights, loras, hidden, dy = _setup(dtype, qk_norm=qk)
     B, S = hidden.shape[:2]
-    layer, wrapped, rot = _hf_layer(cfg, weights, loras, dtype)
+    layer, wrapped, rot = _hf_layer(cfg, weights, loras, dtype, family)
     pos = torch.arange(S)[None].expand(B, -1)
     cos, sin = rot(hidden, pos)
     cos, sin = cos.to(dtype), sin.to(dtype)
@@ -87,7 +99,8 @@ def test_dense_block_matches_transformers_llama_layer(dtype):
     torch.testing.assert_close(ours_rot[0], cos, **tol)
     torch.testing.assert_close(ours_rot[1], sin, **tol)
     w = {k: v.to(dtype) for k, v in weights.items()}
-    kw = dict(heads=cfg["heads"], kv_heads=cfg["kv"], head_dim=cfg["D"], eps=cfg["eps"])
+    kw = dict(heads=cfg["heads"], kv_heads=cfg["kv"], head_dim=cfg["D"], eps=cfg["eps"],
+              qk_norm=qk)
     out, gh = L.streaming_step(hidden, ours_rot, mask, dy, weights=w, loras=loras, cfg=kw)
     torch.testing.assert_close(out, ref.detach(), **tol)
     torch.testing.assert_close(gh, h.grad, **tol)
