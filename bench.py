@@ -32,6 +32,11 @@ CONFIGS = {
     "tiny": dict(H=256, I=688, heads=4, kv=4, D=64, eps=1e-5, r=8, alpha=16.0, B=2, S=128,
                  theta=500000.0),
 }
+# full streamed Qwen3-8B-shape training step
+QWEN3 = dict(H=4096, I=12288, heads=32, kv=8, D=128, eps=1e-6, r=16, alpha=32.0, layers=36,
+             vocab=151936, S=4096, accumulation=4, theta=1000000.0, token_chunk=1024)
+QWEN3_METRIC = ("train tokens/s, full streamed Qwen3-8B-shape step (36 nf4-g128 layers from "
+                "pinned host RAM, 2 device slots, grad accumulation 4)")
 # Qwen3-MoE-30B-A3B-shape MoE feed-forward
 MOE = dict(H=2048, I=768, E=128, k=8, T=4096, r=8, alpha=16.0, norm=True)
 MOE_METRIC = "train tokens/s per MoE layer fwd+bwd (Qwen3-MoE-30B-A3B shape, NF4 experts)"
@@ -161,6 +166,113 @@ def streamed(c, block, args, X, dY, rot, mask):
     return out
 
 
+def synthetic_q4_block(index, c, device, generator, codec="nf4-g128"):
+    """A Qwen3 decoder layer whose 4-bit records are synthetic bytes (random
+    codes, scales |N(0,1)| * 0.02 / 0.7): the streamed step's cost does not
+    depend on the values, and 36 real encodes would dominate the setup."""
+    import torch
+    from spilltune_amd import codecs, slots
+    from spilltune_amd.dense import dense_block, lora_kwargs
+    from spilltune_amd.lora import create_lora_for_block
+    host, specs = {}, {}
+    for name, shape in layer_shapes(c).items():
+        n = shape[0] * shape[1]
+        groups = n // codecs.GROUP
+        key = f"{name}.weight"
+        host[f"@{key}/payload"] = torch.randint(0, 256, (groups * codecs.STRIDE,), dtype=torch.uint8,
+                                                generator=generator)
+        host[f"@{key}/scales"] = torch.randn(groups, generator=generator).abs() * (0.02 / 0.7) + 1e-3
+        specs[key] = {"spec": {"version": 1, "shape": list(shape), "dtype": "bfloat16",
+                               "codec": codec, "group_size": codecs.GROUP, "numel": n},
+                      "parts": {"payload": f"@{key}/payload", "scales": f"@{key}/scales"}}
+    for name in ("input_layernorm.weight", "post_attention_layernorm.weight"):
+        host[name] = torch.ones(c["H"], dtype=torch.bfloat16)
+    for name in ("self_attn.q_norm.weight", "self_attn.k_norm.weight"):
+        host[name] = torch.ones(c["D"], dtype=torch.bfloat16)
+    adapters = create_lora_for_block(index, "full_attention", dict(layer_shapes(c)), rank=c["r"],
+                                     alpha=c["alpha"], device=device, targets=PROJ,
+                                     architecture="llama", generator=generator)
+    with torch.no_grad():
+        for name in sorted(adapters):
+            p = adapters[name]
+            p.B.copy_(torch.randn(p.B.shape, generator=generator) * 0.02)
+    kwargs = {"heads": c["heads"], "kv_heads": c["kv"], "head_dim": c["D"], "eps": c["eps"],
+              "qk_norm": True, **lora_kwargs(adapters)}
+    return slots.BlockPlan(index, "full_attention", dense_block, kwargs, host, adapters, specs)
+
+
+def qwen3_stream_bench(args):
+    """Config 3: the full streamed training step -- 36 Qwen3-8B-shape layers
+    in pinned host RAM, 2 device slots with one-layer prefetch on the copy
+    stream, 4 microbatches of 4096 tokens per optimizer step processed
+    layer-major (one layer load per phase per step), terminal RMSNorm +
+    token-chunked head/CE on the HIP path, fp32 AdamW on the adapters."""
+    import torch
+    from spilltune_amd import engine, slots
+    c = QWEN3
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(1234)
+    t0 = time.perf_counter()
+    log(f"building {c['layers']} synthetic nf4-g128 Qwen3-8B-shape layers")
+    blocks = [synthetic_q4_block(i, c, dev, g) for i in range(c["layers"])]
+    embedding = (torch.randn(c["vocab"], c["H"], generator=g) * 0.02).to(torch.bfloat16)
+    head = (torch.randn(c["vocab"], c["H"], generator=g) * 0.02).to(torch.bfloat16)
+    model = engine.DenseModel(embedding=embedding, norm=torch.ones(c["H"], dtype=torch.bfloat16),
+                              head=head, blocks=blocks, heads=c["heads"], kv_heads=c["kv"],
+                              head_dim=c["D"], eps=c["eps"], theta=c["theta"], rank=c["r"],
+                              alpha=c["alpha"], targets=PROJ, device=dev)
+    session = slots.Q4SlotSession(model.blocks, dev, host_budget_bytes=1 << 40,
+                                  device_budget_bytes=1 << 40, slots=2)
+    gd = torch.Generator().manual_seed(1)
+    rows = []
+    for _ in range(c["accumulation"]):
+        ids = torch.randint(0, c["vocab"], (1, c["S"]), generator=gd)
+        rows.append((ids, ids.clone()))
+    log(f"model ready in {time.perf_counter() - t0:.1f} s: {session.host_bytes / 1e9:.2f} GB pinned "
+        f"images, {session.capacity / 1e6:.1f} MB per slot")
+    steps = max(1, min(args.steps, 3))
+    kw = dict(accumulation=c["accumulation"], lr=1e-5, token_chunk=c["token_chunk"],
+              layer_major=True)
+    engine.train(model, session, rows, steps=1, **kw)  # warmup: first loads, allocator
+    torch.cuda.synchronize()
+    session.completed_copies = []
+    reloads0 = session.reloads
+    t1 = time.perf_counter()
+    losses = engine.train(model, session, rows, steps=steps, **kw)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t1) / steps
+    copies = session.completed_copies
+    tokens = c["S"] * c["accumulation"]
+    P = sum(n * k for n, k in layer_shapes(c).values())
+    M = tokens
+    flops = c["layers"] * (6 * M * P + 4 * (4 * c["S"] * c["S"] * c["D"] * c["heads"] * c["accumulation"]) // 2
+                           + 4 * 2 * M * c["r"] * sum(n + k for n, k in layer_shapes(c).values())) \
+        + 2 * 2 * M * c["vocab"] * c["H"]
+    h2d = sum(cp["bytes"] for cp in copies)
+    gbps = h2d / max(sum(cp["copy_cuda_ms"] for cp in copies), 1e-9) / 1e6
+    log(f"step {dt:.3f} s, losses {losses}, {flops / dt / 1e12:.0f} TFLOP/s algorithmic, "
+        f"H2D {h2d / steps / 1e9:.2f} GB/step at {gbps:.1f} GB/s while copying")
+    result = {
+        "metric": QWEN3_METRIC, "value": round(tokens / dt, 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": steps, "warmup": 1, "ms_per_step": round(dt * 1e3, 2), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random nf4-g128 codes and scales, N(0,0.02) embedding/head, random "
+                "token ids)",
+        "config": {"workload": f"qwen3-stream: {c['layers']} Qwen3-8B-shape layers (qk_norm), "
+                               f"seq {c['S']}, accumulation {c['accumulation']}, vocab {c['vocab']}, "
+                               f"LoRA r={c['r']} on 7 projections, 2 slots, layer-major window",
+                   "global_batch": c["accumulation"], "seq_len": c["S"], "hidden": c["H"],
+                   "intermediate": c["I"], "parallelism": "single GPU"},
+        "layer_mfma_frac": round(flops / dt / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "algorithmic_tflop_per_step": round(flops / 1e12, 2),
+        "h2d": {"bytes_per_step": int(h2d / steps), "gbps_while_copying": round(gbps, 2),
+                "layer_loads_per_step": (session.reloads - reloads0) / steps},
+        "roofline": None, "cpu_baseline": None,
+    }
+    session.close()
+    print(json.dumps(result), flush=True)
+
+
 def moe_bench(args):
     """Config 4: the MoE feed-forward forward + backward on 4096 tokens
     (router, permutation, grouped 4-bit gate|up and down GEMMs with per-expert
@@ -288,7 +400,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="llama8b", choices=sorted(CONFIGS) + ["moe"])
+    ap.add_argument("--config", default="llama8b",
+                    choices=sorted(CONFIGS) + ["moe", "qwen3-stream"])
     ap.add_argument("--cpu-tokens", type=int, default=2048)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -314,6 +427,9 @@ def main():
         return
     if args.config == "moe":
         moe_bench(args)
+        return
+    if args.config == "qwen3-stream":
+        qwen3_stream_bench(args)
         return
     from spilltune_amd import ops, slots
     from spilltune_amd.dense import CausalMask

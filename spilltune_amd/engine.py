@@ -203,18 +203,24 @@ class DenseModel:
     """Llama-family model with 4-bit decoder matrices in slot images: the
     runtime surface of adapters/dense.py:178-263 the engine needs."""
 
-    def __init__(self, *, embedding, norm, head, layers, heads, kv_heads, head_dim, eps, theta,
-                 rank, alpha, targets, device, codec="nf4-g128", generator=None):
+    def __init__(self, *, embedding, norm, head, layers=None, heads, kv_heads, head_dim, eps,
+                 theta, rank, alpha, targets, device, codec="nf4-g128", generator=None,
+                 blocks=None, qk_norm=False):
+        """``layers``: per-layer weight dicts, encoded here; or ``blocks``:
+        prebuilt BlockPlans (e.g. ``slots.make_archive_block``)."""
         self.device = torch.device(device)
         self.embedding = embedding.to(torch.bfloat16).contiguous()      # stays on the host
         self.norm = norm.to(torch.bfloat16).to(self.device)
         self.head = head.to(torch.bfloat16).to(self.device)
         self.eps, self.theta, self.head_dim = eps, theta, head_dim
-        self.blocks = [slots.make_dense_block(i, w, codec=codec, heads=heads, kv_heads=kv_heads,
-                                              head_dim=head_dim, eps=eps, rank=rank, alpha=alpha,
-                                              targets=targets, device=self.device,
-                                              generator=generator)
-                       for i, w in enumerate(layers)]
+        if (layers is None) == (blocks is None):
+            raise ValueError("DenseModel needs exactly one of layers / blocks")
+        self.blocks = list(blocks) if blocks is not None else [
+            slots.make_dense_block(i, w, codec=codec, heads=heads, kv_heads=kv_heads,
+                                   head_dim=head_dim, eps=eps, rank=rank, alpha=alpha,
+                                   targets=targets, device=self.device, generator=generator,
+                                   qk_norm=qk_norm)
+            for i, w in enumerate(layers)]
 
     def positions_and_masks(self, valid):
         rot, mask = positions_and_masks(valid, head_dim=self.head_dim, theta=self.theta,
