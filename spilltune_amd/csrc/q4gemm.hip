@@ -538,7 +538,7 @@ __device__ __forceinline__ void bar() { asm volatile("s_barrier" ::: "memory"); 
 //    dgrad: the transposed-operand layout read with ds_read_b64_tr_b16).
 // The roles meet at one barrier per k-step; each role's registers are live
 // only in its own branch.
-constexpr int WS_DA = 3, WS_PW = 4;
+constexpr int WS_DA = 4, WS_PW = 4;
 template <int MODE>
 __global__ __launch_bounds__(512) void gemm_ws_kernel(GemmParams p) {
   static_assert(MODE == FWD_Q4 || MODE == DGRAD_Q4, "4-bit modes only");
@@ -661,8 +661,10 @@ __global__ __launch_bounds__(512) void gemm_ws_kernel(GemmParams p) {
     // step kt (between barriers kt-1 and kt): DMA tile kt+WS_DA-1 into the
     // stage tile kt-1 used (free since barrier kt-1), stage tile kt+1's B into
     // buffer (kt+1)&1 (its tile kt-1 was last read before barrier kt-1), and
-    // make sure tile kt+1's A has landed before barrier kt.  Tile kt+1's DMAs
-    // came one step earlier; at most the 10 operations of this step follow.
+    // make sure tile kt+1's A has landed before barrier kt.  vmcnt counts in
+    // issue order and each step issues 10 operations; tile kt+1's DMAs came
+    // WS_DA-2 steps earlier, so at most the 10*(WS_DA-2) operations of the
+    // later steps may still be in flight (every load gets WS_DA-2 steps).
     auto step = [&](int kt, int u) {
       dma_A(kt + WS_DA - 1);
       __builtin_amdgcn_sched_barrier(0);
@@ -671,7 +673,7 @@ __global__ __launch_bounds__(512) void gemm_ws_kernel(GemmParams p) {
       store_B(Bs0 + nb * B_ST, wr[u]);
       load_W(kt + 1 + WS_PW, wr[u]);
       __builtin_amdgcn_sched_barrier(0);
-      wait_cnt<10, 0>();  // tile kt+1's A has landed, this step's B stores are done
+      wait_cnt<10 * (WS_DA - 2), 0>();  // tile kt+1's A landed; this step's B stores done
       bar();
     };
     // whole groups of WS_PW steps carry no conditions (static ring slots)
