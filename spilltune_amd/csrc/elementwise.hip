@@ -35,6 +35,84 @@ __device__ float block_sum(float v, float* red) {
 }
 
 // ------------------------------------------------------------------ RMSNorm
+// 8 bf16 in a 16-byte vector <-> fp32 values
+__device__ __forceinline__ void unpack8(uint4 q, float (&f)[8]) {
+  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    f[2 * e] = __uint_as_float(w[e] << 16);
+    f[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+  }
+}
+__device__ __forceinline__ uint4 pack8(const float (&f)[8]) {
+  return make_uint4(st::pack_bf16x2(f[0], f[1]), st::pack_bf16x2(f[2], f[3]),
+                    st::pack_bf16x2(f[4], f[5]), st::pack_bf16x2(f[6], f[7]));
+}
+
+// Vector forms (H % 8 == 0, 16-byte aligned rows): 8 elements per thread per
+// access, same per-element rounding as the scalar kernels below.
+__global__ __launch_bounds__(NTH) void rmsnorm_fwd_vec(const uint16_t* __restrict__ x,
+                                                      const uint16_t* __restrict__ w, int64_t H,
+                                                      float eps, uint16_t* __restrict__ y,
+                                                      float* __restrict__ rstd) {
+  __shared__ float red[NTH / 64];
+  const int64_t row = blockIdx.x;
+  const uint16_t* xr = x + row * H;
+  float ss = 0.0f;
+  for (int64_t i = threadIdx.x * 8; i < H; i += NTH * 8) {
+    float v[8];
+    unpack8(*(const uint4*)(xr + i), v);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
+  }
+  ss = block_sum(ss, red);
+  const float r = 1.0f / sqrtf(ss / (float)H + eps);
+  if (threadIdx.x == 0) rstd[row] = r;
+  for (int64_t i = threadIdx.x * 8; i < H; i += NTH * 8) {
+    float v[8], g[8], o[8];
+    unpack8(*(const uint4*)(xr + i), v);
+    unpack8(*(const uint4*)(w + i), g);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = g[e] * st::bf16r(v[e] * r);
+    *(uint4*)(y + row * H + i) = pack8(o);
+  }
+}
+
+__global__ __launch_bounds__(NTH) void rmsnorm_bwd_vec(const uint16_t* __restrict__ dy,
+                                                      const uint16_t* __restrict__ x,
+                                                      const uint16_t* __restrict__ w,
+                                                      const float* __restrict__ rstd,
+                                                      const uint16_t* __restrict__ dres, int64_t H,
+                                                      uint16_t* __restrict__ dx) {
+  __shared__ float red[NTH / 64];
+  const int64_t row = blockIdx.x;
+  const float r = rstd[row];
+  float dot = 0.0f;
+  for (int64_t i = threadIdx.x * 8; i < H; i += NTH * 8) {
+    float d[8], v[8], g[8];
+    unpack8(*(const uint4*)(dy + row * H + i), d);
+    unpack8(*(const uint4*)(x + row * H + i), v);
+    unpack8(*(const uint4*)(w + i), g);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dot += st::bf16r(d[e] * g[e]) * v[e];
+  }
+  dot = block_sum(dot, red);
+  const float c = r * r * r * dot / (float)H;
+  for (int64_t i = threadIdx.x * 8; i < H; i += NTH * 8) {
+    float d[8], v[8], g[8], o[8], rs[8];
+    unpack8(*(const uint4*)(dy + row * H + i), d);
+    unpack8(*(const uint4*)(x + row * H + i), v);
+    unpack8(*(const uint4*)(w + i), g);
+    if (dres) unpack8(*(const uint4*)(dres + row * H + i), rs);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      o[e] = st::bf16r(r * st::bf16r(d[e] * g[e]) - v[e] * c);
+      if (dres) o[e] = rs[e] + o[e];
+    }
+    *(uint4*)(dx + row * H + i) = pack8(o);
+  }
+}
+
 __global__ __launch_bounds__(NTH) void rmsnorm_fwd(const uint16_t* __restrict__ x,
                                                   const uint16_t* __restrict__ w, int64_t H,
                                                   float eps, uint16_t* __restrict__ y,
@@ -129,6 +207,74 @@ __global__ __launch_bounds__(NTH) void rope_bwd(const uint16_t* __restrict__ g,
     o = a + (d < half ? gs : -gs);
   }
   dx[(b * S + s) * lddx + h * D + d] = st::f32_to_bf16(o);
+}
+
+// Vector forms: one workgroup per token (b, s); a thread handles 8 consecutive
+// elements (16 bytes) of one head and reads the partner chunk half a head
+// away, so there is no per-element index arithmetic.  Same rounding points as
+// rope_fwd / rope_bwd.  Needs D % 16 == 0 and 16-byte aligned rows.
+__global__ __launch_bounds__(NTH) void rope_fwd_vec(const uint16_t* __restrict__ x, int64_t ldx,
+                                                   const uint16_t* __restrict__ cs,
+                                                   const uint16_t* __restrict__ sn, int S,
+                                                   int heads, int D, int rotate,
+                                                   uint16_t* __restrict__ out) {
+  const int64_t t = blockIdx.x;  // token b*S + s
+  const int64_t b = t / S, s = t % S;
+  const int CH = D / 8, half = CH / 2;
+  for (int i = threadIdx.x; i < heads * CH; i += NTH) {
+    const int h = i / CH, c = i % CH;
+    const uint16_t* xr = x + t * ldx + h * D;
+    float v[8], o[8];
+    unpack8(*(const uint4*)(xr + c * 8), v);
+    if (rotate) {
+      float p[8], cv[8], sv[8];
+      unpack8(*(const uint4*)(xr + (c < half ? c + half : c - half) * 8), p);
+      unpack8(*(const uint4*)(cs + t * D + c * 8), cv);
+      unpack8(*(const uint4*)(sn + t * D + c * 8), sv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float rot = c < half ? -p[e] : p[e];
+        o[e] = st::bf16r(v[e] * cv[e]) + st::bf16r(rot * sv[e]);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = v[e];
+    }
+    *(uint4*)(out + ((b * heads + h) * S + s) * D + c * 8) = pack8(o);
+  }
+}
+
+__global__ __launch_bounds__(NTH) void rope_bwd_vec(const uint16_t* __restrict__ g,
+                                                   const uint16_t* __restrict__ cs,
+                                                   const uint16_t* __restrict__ sn, int S,
+                                                   int heads, int D, int rotate,
+                                                   uint16_t* __restrict__ dx, int64_t lddx) {
+  const int64_t t = blockIdx.x;
+  const int64_t b = t / S, s = t % S;
+  const int CH = D / 8, half = CH / 2;
+  for (int i = threadIdx.x; i < heads * CH; i += NTH) {
+    const int h = i / CH, c = i % CH;
+    const uint16_t* gr = g + ((b * heads + h) * S + s) * D;
+    float gv[8], o[8];
+    unpack8(*(const uint4*)(gr + c * 8), gv);
+    if (rotate) {
+      const int pc = c < half ? c + half : c - half;
+      float gp[8], cv[8], sp[8];
+      unpack8(*(const uint4*)(gr + pc * 8), gp);
+      unpack8(*(const uint4*)(cs + t * D + c * 8), cv);
+      unpack8(*(const uint4*)(sn + t * D + pc * 8), sp);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float a = st::bf16r(gv[e] * cv[e]);
+        const float gs = st::bf16r(gp[e] * sp[e]);
+        o[e] = a + (c < half ? gs : -gs);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = gv[e];
+    }
+    *(uint4*)(dx + t * lddx + h * D + c * 8) = pack8(o);
+  }
 }
 
 __global__ __launch_bounds__(NTH) void relayout(const uint16_t* __restrict__ x, int64_t S,
@@ -255,7 +401,10 @@ extern "C" int st_rmsnorm_fwd(const uint16_t* x, const uint16_t* w, int64_t rows
   ST_CHECK_ARG(rows >= 0 && H > 0, "st_rmsnorm_fwd: bad shape");
   if (rows == 0) return ST_OK;
   ST_CHECK_ARG(x && w && y && rstd, "st_rmsnorm_fwd: NULL pointer");
-  rmsnorm_fwd<<<(unsigned)rows, NTH, 0, (hipStream_t)stream>>>(x, w, H, eps, y, rstd);
+  if (H % 8 == 0 && H >= NTH * 8 / 4 && (((uintptr_t)x | (uintptr_t)w | (uintptr_t)y) & 15u) == 0)
+    rmsnorm_fwd_vec<<<(unsigned)rows, NTH, 0, (hipStream_t)stream>>>(x, w, H, eps, y, rstd);
+  else
+    rmsnorm_fwd<<<(unsigned)rows, NTH, 0, (hipStream_t)stream>>>(x, w, H, eps, y, rstd);
   return st::check_launch("rmsnorm_fwd");
 }
 
@@ -265,7 +414,11 @@ extern "C" int st_rmsnorm_bwd(const uint16_t* dy, const uint16_t* x, const uint1
   ST_CHECK_ARG(rows >= 0 && H > 0, "st_rmsnorm_bwd: bad shape");
   if (rows == 0) return ST_OK;
   ST_CHECK_ARG(dy && x && w && rstd && dx, "st_rmsnorm_bwd: NULL pointer");
-  rmsnorm_bwd<<<(unsigned)rows, NTH, 0, (hipStream_t)stream>>>(dy, x, w, rstd, dres, H, dx);
+  if (H % 8 == 0 && H >= NTH * 8 / 4 &&
+      (((uintptr_t)dy | (uintptr_t)x | (uintptr_t)w | (uintptr_t)dres | (uintptr_t)dx) & 15u) == 0)
+    rmsnorm_bwd_vec<<<(unsigned)rows, NTH, 0, (hipStream_t)stream>>>(dy, x, w, rstd, dres, H, dx);
+  else
+    rmsnorm_bwd<<<(unsigned)rows, NTH, 0, (hipStream_t)stream>>>(dy, x, w, rstd, dres, H, dx);
   return st::check_launch("rmsnorm_bwd");
 }
 
@@ -277,8 +430,14 @@ extern "C" int st_rope_fwd(const uint16_t* x, int64_t ldx, const uint16_t* cos,
   if (total == 0) return ST_OK;
   ST_CHECK_ARG(x && out && (!rotate || (cos && sin)), "st_rope_fwd: NULL pointer");
   ST_CHECK_ARG(ldx >= heads * D, "st_rope_fwd: ldx < heads*D");
-  rope_fwd<<<nblk(total), NTH, 0, (hipStream_t)stream>>>(x, ldx, cos, sin, S, heads, D, rotate,
-                                                         total, out);
+  const bool vec = D % 16 == 0 && ldx % 8 == 0 && S <= 0x7fffffff && heads * D <= 0x7fffffff &&
+                   (((uintptr_t)x | (uintptr_t)out | (uintptr_t)cos | (uintptr_t)sin) & 15u) == 0;
+  if (vec && B * S <= 0x7fffffff)
+    rope_fwd_vec<<<(unsigned)(B * S), NTH, 0, (hipStream_t)stream>>>(x, ldx, cos, sin, (int)S,
+                                                                     (int)heads, (int)D, rotate, out);
+  else
+    rope_fwd<<<nblk(total), NTH, 0, (hipStream_t)stream>>>(x, ldx, cos, sin, S, heads, D, rotate,
+                                                           total, out);
   return st::check_launch("rope_fwd");
 }
 
@@ -290,8 +449,15 @@ extern "C" int st_rope_bwd(const uint16_t* dout, const uint16_t* cos, const uint
   if (total == 0) return ST_OK;
   ST_CHECK_ARG(dout && dx && (!rotate || (cos && sin)), "st_rope_bwd: NULL pointer");
   ST_CHECK_ARG(lddx >= heads * D, "st_rope_bwd: lddx < heads*D");
-  rope_bwd<<<nblk(total), NTH, 0, (hipStream_t)stream>>>(dout, cos, sin, S, heads, D, rotate,
-                                                         total, dx, lddx);
+  const bool vec = D % 16 == 0 && lddx % 8 == 0 && S <= 0x7fffffff && heads * D <= 0x7fffffff &&
+                   (((uintptr_t)dout | (uintptr_t)dx | (uintptr_t)cos | (uintptr_t)sin) & 15u) == 0;
+  if (vec && B * S <= 0x7fffffff)
+    rope_bwd_vec<<<(unsigned)(B * S), NTH, 0, (hipStream_t)stream>>>(dout, cos, sin, (int)S,
+                                                                     (int)heads, (int)D, rotate,
+                                                                     dx, lddx);
+  else
+    rope_bwd<<<nblk(total), NTH, 0, (hipStream_t)stream>>>(dout, cos, sin, S, heads, D, rotate,
+                                                           total, dx, lddx);
   return st::check_launch("rope_bwd");
 }
 
