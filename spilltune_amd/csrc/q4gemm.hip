@@ -136,10 +136,49 @@ struct Tile {
   static constexpr int LDS_CHUNKS = 2 * (BM + BN) * RS;
 };
 
+// Copies a rows x cols block of fp32 values into LDS, dst[r*ls + c] = element
+// (row0 + r, col0 + c) of a row-major array with row stride ld read through
+// rs; rows r >= vrows and columns c >= vcols read as zero.  Each thread keeps
+// eight loads in flight before its LDS writes, and walks its elements
+// e = tid + NT*i as (r, c) pairs without divisions.
+template <int NT>
+__device__ __forceinline__ void stage_f32(float* dst, int ls, __amdgpu_buffer_rsrc_t rs,
+                                          int64_t ld, int64_t row0, int64_t col0, int rows,
+                                          int cols, int64_t vrows, int64_t vcols, int tid) {
+  const int total = rows * cols;
+  int r = tid / cols, c = tid % cols;
+  const int dr = NT / cols, dc = NT % cols;
+  for (int e0 = 0; e0 < total; e0 += 8 * NT) {
+    float v[8];
+    int d[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const bool in = e0 + u * NT + tid < total;
+      const bool ok = in && r < vrows && c < vcols;
+      v[u] = __builtin_bit_cast(
+          float, ld4(rs, ok ? (uint32_t)(((row0 + r) * ld + col0 + c) * 4) : kOOB));
+      d[u] = in ? r * ls + c : -1;
+      r += dr;
+      c += dc;
+      if (c >= cols) {
+        c -= cols;
+        ++r;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (d[u] >= 0) dst[d[u]] = v[u];
+  }
+}
+
 // Epilogue shared by the GEMM kernels: y = bf16(acc) (+ LoRA term, + residual)
 // for this tile; waves with `has_acc` false only help stage the LoRA operands.
 // LDS (`lds`, at least BM*(lora_cols+1) + the LoRA right operand floats) is
 // reused, so the caller has finished every LDS read of the main loop.
+// Residual loads and output stores go through buffer resources with masked
+// 32-bit offsets (the host keeps C and R below 2 GiB): a 32x32 block's 16
+// residual loads are all in flight before the LoRA products, and rows or
+// columns outside the problem are skipped without branches.
 template <bool DGRAD, int BM, int BN, int NT, int FM, int FN, int WM, int WN>
 __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const f32x16 (&acc)[FM][FN],
                                               uint4* lds, int64_t m0, int64_t mend, int64_t p0,
@@ -151,33 +190,28 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const f32x16 
   float* Ls = Ts + BM * tstride;
   const int lstride = DGRAD ? BN : (p.lora_k + 1);
   if (lora) {
-    // stage T rows [m0, m0+BM) x [0, lora_cols) and the LoRA right operand
-    for (int e = tid; e < BM * p.lora_cols; e += NT) {
-      int r = e / p.lora_cols, c = e % p.lora_cols;
-      int64_t m = m0 + r;
-      Ts[r * tstride + c] = m < mend ? p.T[m * p.ldt + c] : 0.0f;
-    }
-    if (DGRAD) {  // L = A_cat [lora_k, P]
-      for (int e = tid; e < p.lora_k * BN; e += NT) {
-        int r = e / BN, c = e % BN;
-        int64_t pc = p0 + c;
-        Ls[r * lstride + c] = pc < p.P ? Lg[r * p.ldl + pc] : 0.0f;
-      }
-    } else {  // L = B_lora [P, rank]
-      for (int e = tid; e < BN * p.lora_k; e += NT) {
-        int r = e / p.lora_k, c = e % p.lora_k;
-        int64_t pc = p0 + r;
-        Ls[r * lstride + c] = pc < p.P ? Lg[pc * p.ldl + c] : 0.0f;
-      }
-    }
+    // T rows [m0, m0+BM) x [0, lora_cols) and the LoRA right operand
+    // (dgrad: A_cat [lora_k, P] columns p0..; forward: B_lora [P, rank] rows p0..)
+    stage_f32<NT>(Ts, tstride, make_rsrc(p.T, 0x7fffffff), p.ldt, m0, 0, BM, p.lora_cols,
+                  mend - m0, p.lora_cols, tid);
+    if (DGRAD)
+      stage_f32<NT>(Ls, lstride, make_rsrc(Lg, 0x7fffffff), p.ldl, 0, p0, p.lora_k, BN, p.lora_k,
+                    p.P - p0, tid);
+    else
+      stage_f32<NT>(Ls, lstride, make_rsrc(Lg, 0x7fffffff), p.ldl, p0, 0, BN, p.lora_k, p.P - p0,
+                    p.lora_k, tid);
     __syncthreads();
   }
   if (!has_acc) return;
+  const auto rsC = make_rsrc(p.C, 0x7fffffff);
+  const auto rsR = make_rsrc(p.R, 0x7fffffff);
+  const uint32_t ldc2 = (uint32_t)p.ldc * 2, ldr2 = (uint32_t)p.ldr * 2;
 
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
     const int cl = wn * WN + j * 32;  // tile-local first column of this block
     const int64_t pcol = p0 + cl + (lane & 31);
+    const bool colok = pcol < p.P;
     int coff = 0;
     if (lora && !DGRAD) {
       int64_t pblk = p0 + cl;
@@ -188,6 +222,17 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const f32x16 
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
       const int rl = wm * WM + i * 32;
+      const int64_t rbase = m0 + rl + (lane >> 5) * 4;  // row of v = 0
+      // element v sits at row rbase + dv(v), dv = (v/4)*8 + v%4
+      auto ok = [&](int v) { return colok && rbase + (v >> 2) * 8 + (v & 3) < mend; };
+      uint16_t rv[16];  // raw bf16: converted where used, after the LoRA products
+      if (p.R) {
+        const uint32_t rb = (uint32_t)((rbase * p.ldr + pcol) * 2);
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          rv[v] = __builtin_amdgcn_raw_buffer_load_b16(
+              rsR, (int)(ok(v) ? rb + (uint32_t)((v >> 2) * 8 + (v & 3)) * ldr2 : kOOB), 0, 0);
+      }
       f32x16 la;
       if (lora) {
 #pragma unroll
@@ -200,20 +245,20 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const f32x16 
           la = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, la, 0, 0, 0);
         }
       }
+      const uint32_t cb = (uint32_t)((rbase * p.ldc + pcol) * 2);
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int64_t m = m0 + rl + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-        if (m < mend && pcol < p.P) {
-          float y = st::bf16r(acc[i][j][v]);
-          if (lora) {
-            if (DGRAD)
-              y = st::bf16r(y + st::bf16r(la[v]));
-            else
-              y = st::bf16r(y + la[v] * p.lora_scale);
-          }
-          if (p.R) y = st::bf16r(st::bf16_to_f32(p.R[m * p.ldr + pcol]) + y);
-          p.C[m * p.ldc + pcol] = st::f32_to_bf16(y);
+        float y = st::bf16r(acc[i][j][v]);
+        if (lora) {
+          if (DGRAD)
+            y = st::bf16r(y + st::bf16r(la[v]));
+          else
+            y = st::bf16r(y + la[v] * p.lora_scale);
         }
+        if (p.R) y = st::bf16r(st::bf16_to_f32(rv[v]) + y);
+        __builtin_amdgcn_raw_buffer_store_b16(
+            st::f32_to_bf16(y), rsC,
+            (int)(ok(v) ? cb + (uint32_t)((v >> 2) * 8 + (v & 3)) * ldc2 : kOOB), 0, 0);
       }
     }
   }
@@ -752,6 +797,17 @@ __global__ __launch_bounds__(512) void gemm_ws_kernel(GemmParams p) {
                                                               tid, lane, wave < 4, Lg);
 }
 
+// The epilogue addresses C, the residual, T and the LoRA right operand with
+// 32-bit byte offsets.
+int check_epilogue_extents(const GemmParams& p) {
+  const int64_t lim = 1ll << 31;
+  bool ok = ((p.M - 1) * p.ldc + p.P) * 2 < lim;
+  if (p.R) ok = ok && ((p.M - 1) * p.ldr + p.P) * 2 < lim;
+  if (p.T) ok = ok && (p.M * p.ldt + p.lora_cols) * 4 < lim &&
+                (p.P + p.lora_k) * (p.ldl + 1) * 4 < lim;
+  return ok ? ST_OK : st::fail(ST_EUNSUPPORTED, "q4gemm: output, residual or LoRA operand above 2 GiB");
+}
+
 template <int MODE>
 int launch_ws(const GemmParams& p, hipStream_t stream) {
   constexpr int BM = 256, BN = 128;
@@ -764,6 +820,7 @@ int launch_ws(const GemmParams& p, hipStream_t stream) {
       return st::fail(ST_EUNSUPPORTED, "q4gemm: LoRA epilogue (%d columns) exceeds tile LDS",
                       p.lora_cols);
   }
+  if (int rc = check_epilogue_extents(p)) return rc;
   gemm_ws_kernel<MODE><<<(unsigned)tiles, 512, 0, stream>>>(p);
   return st::check_launch("q4gemm");
 }
@@ -781,6 +838,7 @@ int launch(const GemmParams& p, hipStream_t stream) {
       return st::fail(ST_EUNSUPPORTED, "q4gemm: LoRA epilogue (%d columns) exceeds tile LDS",
                       p.lora_cols);
   }
+  if (int rc = check_epilogue_extents(p)) return rc;
   gemm_kernel<MODE, BM, BN, WAVES, WAVES_M><<<(unsigned)tiles, NT, 0, stream>>>(p);
   return st::check_launch("q4gemm");
 }
@@ -799,11 +857,77 @@ int tile_choice(int mode, int64_t M, int64_t P) {
   return 128;
 }
 
+int cu_count() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+// Forward output columns [c0, c1) of p as a GEMM of its own (c0 a multiple
+// of 128): W rows and LoRA B rows move by c0, the segments (and T columns)
+// that end before c0 drop out.
+GemmParams column_slice(const GemmParams& p, int64_t c0, int64_t c1) {
+  GemmParams q = p;
+  q.P = c1 - c0;
+  q.C = p.C + c0;
+  if (p.R) q.R = p.R + c0;
+  q.Wq = p.Wq + c0 * p.ldw / 2;
+  q.Ws = p.Ws + c0 * p.ldw / 128;
+  q.w_bytes = p.w_bytes - c0 * p.ldw / 2;
+  q.s_bytes = p.s_bytes - c0 * p.ldw / 128 * 4;
+  if (p.T) {
+    q.L = p.L + c0 * p.ldl;
+    int drop = 0;
+    while (drop < p.nseg && p.seg_end[drop] <= c0) ++drop;
+    q.nseg = p.nseg - drop;
+    for (int i = 0; i < q.nseg; ++i) q.seg_end[i] = p.seg_end[i + drop] - c0;
+    q.T = p.T + (int64_t)drop * p.lora_k;
+    q.lora_cols = q.nseg * p.lora_k;
+  }
+  return q;
+}
+
+// Tail balancing for the 256x256 forward.  A launch of `tiles` one-per-CU
+// tiles takes cdiv(tiles, CUs) rounds; when the last round is partly idle,
+// the columns of the whole rounds keep the 256x256 tile and the leftover
+// columns run as a second launch of 256x128 warp-specialised tiles (measured
+// at ~0.6 of a 256x256 round per round).  Returns the split column (0: no
+// split).  ST_GEMM_SPLIT=0 disables it.  (A 256x128 dgrad with a 128x128 tail
+// measured no faster, so the dgrad is not split.)
+int64_t split_column(int t, int64_t M, int64_t P) {
+  const char* env = getenv("ST_GEMM_SPLIT");
+  if ((env && !atoi(env)) || t != 256) return 0;
+  const int64_t cus = cu_count();
+  const int64_t mt = st::cdiv(M, 256), tiles = mt * st::cdiv(P, 256);
+  if (tiles <= cus || tiles % cus == 0) return 0;
+  const int64_t full = tiles / cus * cus;
+  if (full % mt) return 0;
+  const int64_t c1 = full / mt * 256;
+  if (c1 >= P) return 0;
+  const int64_t t2 = mt * st::cdiv(P - c1, 128);
+  const double split = (double)(full / cus) + 0.6 * (double)st::cdiv(t2, cus);
+  return split < (double)st::cdiv(tiles, cus) ? c1 : 0;
+}
+
 template <int MODE>
 int dispatch(const GemmParams& p, hipStream_t stream) {
   // the dense-W fallbacks (K not a multiple of 128) always use 128x128 tiles
   if constexpr (MODE == FWD_Q4 || MODE == DGRAD_Q4) {
     const int t = tile_choice(MODE, p.M, p.P);
+    if constexpr (MODE == FWD_Q4) {
+      if (const int64_t c1 = split_column(t, p.M, p.P)) {
+        const int rc = launch<MODE, 256, 256, 8>(column_slice(p, 0, c1), stream);
+        return rc ? rc : launch_ws<MODE>(column_slice(p, c1, p.P), stream);
+      }
+    }
     if (t == 256) return launch<MODE, 256, 256, 8>(p, stream);
     if (t == 2561) return launch<MODE, 256, 128, 8, 4>(p, stream);
     if (t == 2562) return launch_ws<MODE>(p, stream);
@@ -975,6 +1099,7 @@ int launch_grouped(const GemmParams& p, hipStream_t stream) {
   }
   int64_t tiles = (st::cdiv(p.M, BM) + p.ngroups) * st::cdiv(p.P, BN);
   if (tiles > 0x7fffffff) return st::fail(ST_EUNSUPPORTED, "q4 grouped: too many tiles");
+  if (int rc = check_epilogue_extents(p)) return rc;
   gemm_kernel<MODE, BM, BN, WAVES, 2><<<(unsigned)tiles, 64 * WAVES, 0, stream>>>(p);
   return st::check_launch("q4 grouped gemm");
 }

@@ -270,3 +270,36 @@ def test_q4_linear_full_size_vs_torch_fp32(dev):
     ops.q4_lora_linear(xg, q, None).backward(dy)
     ref_dx = (dy.float() @ W.float()).to(BF)
     _close_bf16(xg.grad, ref_dx, "full-size gate|up dgrad")
+
+
+@pytest.mark.parametrize("segments", [(16384, 33024), (32896, 33024)])
+def test_q4_linear_tail_split_matches_single_launch(dev, oracle_codec, monkeypatch, segments):
+    """Shapes whose last round of tiles would leave CUs idle run as two
+    launches over column ranges (256x256 tiles, then 256x128 ones).  Every
+    output element keeps its reduction order, so the split result equals the
+    single launch bit for bit, LoRA segments (one ending before the split
+    column, one straddling it) and residual included."""
+    g = torch.Generator().manual_seed(77)
+    M, K = 512, 256
+    N = segments[-1]
+    w = (torch.randn(N, K, generator=g) * 0.02).numpy()
+    q, W = q4_from_oracle(oracle_codec, w, "nf4-g128", dev)
+    q = ops.Q4Weight(q.payload, q.scales, (N, K), "nf4-g128",
+                     (segments[0], segments[1] - segments[0]))
+    x = torch.randn(M, K, generator=g).to(BF).to(dev)
+    res = torch.randn(M, N, generator=g).to(BF).to(dev)
+    loras = [_L((torch.randn(8, K, generator=g) * 0.05).to(dev),
+                (torch.randn(n, 8, generator=g) * 0.05).to(dev), 16.0) for n in q.segments]
+    outs = []
+    for split in ("1", "0"):
+        monkeypatch.setenv("ST_GEMM_SPLIT", split)
+        outs.append(ops.q4_lora_linear(x, q, loras, residual=res))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    # lora.py:218-220: bf16 base, fp32 adapter term, bf16 sum; then the residual
+    ref = (x.float().cpu() @ W.float().T).to(BF).float()
+    off = 0
+    for lo, n in zip(loras, q.segments):
+        ref[:, off:off + n] += (x.float().cpu() @ lo.A.cpu().T) @ lo.B.cpu().T * lo.scale
+        off += n
+    _close_bf16(outs[0], (ref.to(BF).float() + res.float().cpu()).to(BF), "split fwd")
