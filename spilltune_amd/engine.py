@@ -128,11 +128,17 @@ def window_layer_major(model, session, items, *, normalization, token_chunk):
                                                  mb["masks"][block.kind], weights, block.kwargs)
                 grads = torch.autograd.grad(out, [hidden] + [t for p in ordered for t in (p.A, p.B)],
                                             mb["g"])
-                for i, proj in enumerate(ordered):
-                    if k == 0:
-                        proj.zero_grad()
-                    proj.grad_A.add_(grads[1 + 2 * i].detach().to(proj.grad_A))
-                    proj.grad_B.add_(grads[2 + 2 * i].detach().to(proj.grad_B))
+                dst = [t for p in ordered for t in (p.grad_A, p.grad_B)]
+                src = [g.detach().to(d) for g, d in zip(grads[1:], dst)]
+                # the first microbatch replaces (zero + add), later ones accumulate
+                if k == 0:
+                    for p in ordered:
+                        for t in (p.A.grad, p.B.grad):
+                            if t is not None:
+                                t.zero_()
+                    torch._foreach_copy_(dst, src)
+                else:
+                    torch._foreach_add_(dst, src)
                 mb["g"] = grads[0]
     return losses
 

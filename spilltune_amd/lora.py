@@ -123,4 +123,36 @@ def create_lora_for_block(block_idx: int, block_type: str, weight_shapes: dict, 
             out_features=out_f, A=A, B=B, grad_A=torch.zeros_like(A), grad_B=torch.zeros_like(B),
             m_A=torch.zeros_like(A), v_A=torch.zeros_like(A), m_B=torch.zeros_like(B),
             v_B=torch.zeros_like(B))
+    share_fused_storage(adapters)
     return adapters
+
+
+# projections the dense functional runs as one N-concatenated GEMM
+FUSED_GROUPS = (("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj"),
+                ("mlp.gate_proj", "mlp.up_proj"))
+
+
+def share_fused_storage(adapters: dict, groups=FUSED_GROUPS) -> None:
+    """Place the ``A`` (and ``B``) tensors of each fused group in one
+    contiguous buffer, in segment order, so the fused GEMM reads
+    ``A_cat [sum r, K]`` and ``B_cat [sum N, r]`` as views instead of
+    concatenating them on every call.  Each ``A``/``B`` stays a leaf tensor
+    of its own (a view of the shared buffer) with the same values; optimizer
+    updates in place land in the shared buffer.  Groups whose members differ
+    in rank, width, device or are missing are left alone."""
+    for group in groups:
+        projs = [adapters.get(n) for n in group]
+        if any(p is None for p in projs):
+            continue
+        p0 = projs[0]
+        if any(p.rank != p0.rank or p.in_features != p0.in_features or p.A.device != p0.A.device
+               for p in projs):
+            continue
+        A_all = torch.cat([p.A.detach() for p in projs], 0)
+        B_all = torch.cat([p.B.detach() for p in projs], 0)
+        ra = rb = 0
+        for p in projs:
+            p.A = A_all[ra:ra + p.rank].requires_grad_(True)
+            p.B = B_all[rb:rb + p.out_features].requires_grad_(True)
+            ra += p.rank
+            rb += p.out_features

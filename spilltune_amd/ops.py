@@ -188,6 +188,25 @@ def _lora_meta(weight: Q4Weight, loras):
     return ranks.pop(), scales.pop()
 
 
+def _stack_rows(ts):
+    """Detached ``cat(ts, 0)`` of contiguous 2-D tensors of one width: a view
+    when they already lie back to back in one storage (the layout
+    ``lora.share_fused_storage`` gives fused groups), else a copy."""
+    t0 = ts[0].detach()
+    if len(ts) == 1:
+        return t0.contiguous()
+    width = t0.shape[1]
+    off = t0.storage_offset()
+    ptr = t0.untyped_storage().data_ptr()
+    for t in ts:
+        if (not t.is_contiguous() or t.dim() != 2 or t.shape[1] != width or t.dtype != t0.dtype
+                or t.untyped_storage().data_ptr() != ptr or t.storage_offset() != off):
+            return torch.cat([x.detach() for x in ts], 0).contiguous()
+        off += t.numel()
+    rows = sum(t.shape[0] for t in ts)
+    return t0.as_strided((rows, width), (width, 1), t0.storage_offset())
+
+
 class _Q4LoRALinear(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, weight, residual, rank, scale, *ab):
@@ -201,9 +220,7 @@ class _Q4LoRALinear(torch.autograd.Function):
         if ab:
             A = [ab[2 * i] for i in range(nseg)]
             B = [ab[2 * i + 1] for i in range(nseg)]
-            A_cat = A[0].detach() if nseg == 1 else torch.cat([a.detach() for a in A], 0)
-            B_cat = B[0].detach() if nseg == 1 else torch.cat([b.detach() for b in B], 0)
-            A_cat, B_cat = A_cat.contiguous(), B_cat.contiguous()
+            A_cat, B_cat = _stack_rows(A), _stack_rows(B)
             T = torch.empty((M, nseg * rank), dtype=_F32, device=dev)
             # T = x_f32 A_cat^T   (lora.py:219 inner linear)
             lora_gemm(M, nseg * rank, K, x, K, 1, A_cat, 1, K, 1.0, T)

@@ -47,6 +47,7 @@ class StreamingBlockFunction(torch.autograd.Function):
             grads = torch.autograd.grad(output, inputs, grad_output, allow_unused=True)
             if grads[0] is None:
                 raise RuntimeError(f"block {ctx.block_idx} lost its input gradient")
+            dst, src = [], []
             for i, proj in enumerate(ordered):
                 ga, gb = grads[1 + 2 * i], grads[2 + 2 * i]
                 if ga is None or gb is None:
@@ -54,9 +55,17 @@ class StreamingBlockFunction(torch.autograd.Function):
                     raise RuntimeError(f"block {ctx.block_idx} adapter {proj.name} is disconnected; "
                                        f"missing gradients for {missing}")
                 if not ctx.accumulate_adapter_grads:
-                    proj.zero_grad()
-                proj.grad_A.add_(ga.detach().to(proj.grad_A))
-                proj.grad_B.add_(gb.detach().to(proj.grad_B))
+                    for t in (proj.A.grad, proj.B.grad):
+                        if t is not None:
+                            t.zero_()
+                dst += [proj.grad_A, proj.grad_B]
+                src += [ga.detach().to(proj.grad_A), gb.detach().to(proj.grad_B)]
+            # one multi-tensor launch for every adapter: replace (zero + add in
+            # the reference) or accumulate
+            if ctx.accumulate_adapter_grads:
+                torch._foreach_add_(dst, src)
+            else:
+                torch._foreach_copy_(dst, src)
         return (grads[0],) + (None,) * 8
 
 
