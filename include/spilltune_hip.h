@@ -91,7 +91,7 @@ int st_dequant4_dq(const uint8_t* packed, const uint8_t* absmax_u8, const float*
  * W [N,K] is payload/scales in flat groups of 128.  W is dequantised into LDS
  * inside the GEMM (never written to HBM as bf16) when K % 128 == 0; other K go
  * through a bf16 copy of W in `workspace` (st_q4_linear_fwd_workspace_bytes).
- * `t` = x_f32 A^T from st_lora_xa ([M, nseg*rank] fp32) or NULL for no LoRA.
+ * `t` = x_f32 A_cat^T from st_lora_gemm ([M, nseg*rank] fp32) or NULL for no LoRA.
  * nseg/seg_end describe N-concatenated projections (fused q|k|v, gate|up):
  * column n belongs to segment s = #{seg_end[i] <= n}; segment ends must be
  * multiples of 32.  nseg = 1 with seg_end[0] = N for a single projection.
@@ -134,6 +134,26 @@ int st_lora_gemm(int64_t Mo, int64_t No, int64_t Kc,
                  const void* b, int32_t b_dtype, int64_t sbk, int64_t sbn,
                  float alpha, float* out, int64_t ldo, int32_t accumulate,
                  void* workspace, int64_t workspace_bytes, st_stream_t stream);
+
+/*
+ * The two products of the LoRA VJP that read dY (the autograd of
+ * finetune/lora.py:219 inside training/recompute.py:102-105), for a
+ * projection of nseg N-concatenated segments (ends seg_end[], rank r each):
+ *   dt[m, s*r + j] = scale * sum_{n in seg s} dy_f32[m, n] * b[n, j]
+ *   db[n, j]       = scale * sum_m dy_f32[m, n] * t[m, s*r + j]   (n in seg s)
+ * dy [M, N] bf16 (lddy), b [N, r] fp32 (the segments' B stacked), t [M, nseg*r]
+ * fp32 (ldt; the forward's x_f32 A_cat^T), dt [M, nseg*r] (lddt), db [N, r].
+ * All 2*nseg products run in one launch, their split-K sums in one more (fixed
+ * order).  nseg <= 4, r <= 64; segment starts and widths must be multiples of
+ * 8 (the workspace query returns 0 otherwise: use st_lora_gemm per product).
+ */
+int64_t st_lora_bwd_dy_workspace_bytes(int64_t M, int64_t N, int32_t rank, int32_t nseg,
+                                       const int64_t* seg_end);
+int st_lora_bwd_dy(const uint16_t* dy, int64_t M, int64_t N, int64_t lddy,
+                   const float* b, const float* t, int64_t ldt, int32_t rank,
+                   int32_t nseg, const int64_t* seg_end, float scale,
+                   float* dt, int64_t lddt, float* db,
+                   void* workspace, int64_t workspace_bytes, st_stream_t stream);
 
 /* ------------------------------------------------------- layer elementwise */
 /* y = w * bf16(x * rsqrt(mean(x^2) + eps)) (dense.py:115-117); rstd[row] saved. */

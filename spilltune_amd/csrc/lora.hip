@@ -114,20 +114,22 @@ constexpr int RK_PF = 3;          // chunks of loads in flight per workgroup
 // by the host); rows or chunks out of range read as zero.  The host routes
 // only 16-byte-aligned G with rows (ROW form: contraction; COL form: output)
 // a multiple of 8 elements here.
+// One workgroup's share: output rows [tile*RK_BM, +RK_BM) over contraction
+// chunk [split*klen, +klen), written to partial slice `split`.  Gs / Ss: the
+// caller's LDS (ROW: G as [m][k] rows of RK_LD; COL: [k][m] in the
+// transposed-operand layout; S as [hi|lo][j][k]).
 template <bool COL, bool SK1, int NB>
-__global__ __launch_bounds__(NTH) void lora_rk(int64_t Mo, int64_t R, int64_t Kc,
-                                              const uint16_t* __restrict__ G, int64_t ldg,
-                                              int64_t g_bytes, const float* __restrict__ S,
-                                              int64_t ssk, int64_t ssj, int64_t s_bytes,
-                                              int64_t klen, float* __restrict__ part) {
-  // ROW: [m][k] rows of RK_LD; COL: [k][m] in the transposed-operand layout
-  __shared__ __attribute__((aligned(16))) uint16_t Gs[RK_BM * RK_LD];
-  __shared__ __attribute__((aligned(16))) uint16_t Ss[2 * RK_RP * RK_LD];  // [hi|lo][j][k]
+__device__ __forceinline__ void rk_tile(int64_t Mo, int64_t R, int64_t Kc,
+                                        const uint16_t* __restrict__ G, int64_t ldg,
+                                        int64_t g_bytes, const float* __restrict__ S, int64_t ssk,
+                                        int64_t ssj, int64_t s_bytes, int64_t klen,
+                                        float* __restrict__ part, int64_t tile, int64_t split,
+                                        uint16_t* __restrict__ Gs, uint16_t* __restrict__ Ss) {
   constexpr int RP = NB * 32;            // staged S columns
   constexpr int SIT = RK_BK * RP / NTH;  // S values per thread per chunk (8 or 16)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t m0 = (int64_t)blockIdx.x * RK_BM;
-  const int kb = (int)((int64_t)blockIdx.y * klen);
+  const int64_t m0 = tile * RK_BM;
+  const int kb = (int)(split * klen);
   const int ke = (int)(kb + klen < Kc ? kb + klen : Kc);
   const auto rsG = st::make_rsrc(G, g_bytes);
   const auto rsS = st::make_rsrc(S, s_bytes);
@@ -231,7 +233,7 @@ __global__ __launch_bounds__(NTH) void lora_rk(int64_t Mo, int64_t R, int64_t Kc
       __syncthreads();
     }
   }
-  float* dst = part + (int64_t)blockIdx.y * Mo * R;
+  float* dst = part + split * Mo * R;
 #pragma unroll
   for (int c = 0; c < NB; ++c) {
 #pragma unroll
@@ -241,6 +243,88 @@ __global__ __launch_bounds__(NTH) void lora_rk(int64_t Mo, int64_t R, int64_t Kc
       if (m < Mo && j < R) dst[m * R + j] = acc[c][v];
     }
   }
+}
+
+template <bool COL, bool SK1, int NB>
+__global__ __launch_bounds__(NTH) void lora_rk(int64_t Mo, int64_t R, int64_t Kc,
+                                              const uint16_t* __restrict__ G, int64_t ldg,
+                                              int64_t g_bytes, const float* __restrict__ S,
+                                              int64_t ssk, int64_t ssj, int64_t s_bytes,
+                                              int64_t klen, float* __restrict__ part) {
+  __shared__ __attribute__((aligned(16))) uint16_t Gs[RK_BM * RK_LD];
+  __shared__ __attribute__((aligned(16))) uint16_t Ss[2 * RK_RP * RK_LD];
+  rk_tile<COL, SK1, NB>(Mo, R, Kc, G, ldg, g_bytes, S, ssk, ssj, s_bytes, klen, part, blockIdx.x,
+                        blockIdx.y, Gs, Ss);
+}
+
+// ---- several rank-r products in one launch (the backward of a fused
+// projection: dT_s = dY_s B_s and dB_s = dY_s^T T_s for every segment s).
+// Each problem is a lora_rk product with its own operands, split count and
+// partial slice; workgroup b runs problem p when wg0[p] <= b < wg0[p+1], and
+// one reduction launch sums every problem's partials into its output.
+constexpr int RK_MAXP = 8;
+struct RkProblem {
+  const uint16_t* G;
+  const float* S;
+  float* part;   // [ks][big][R]
+  float* out;    // out[m*so_m + j*so_j] (+)= alpha * sum
+  int64_t ldg, g_bytes, ssk, ssj, s_bytes, big, R, Kc, klen, so_m, so_j;
+  int64_t wg0, e0;  // first workgroup / first reduction element of the problem
+  int col, tiles, ks;
+  float alpha;
+};
+struct RkBatch {
+  RkProblem p[RK_MAXP];
+  int n, accumulate;
+  int64_t wgs, elems;
+};
+
+__device__ __forceinline__ int rk_find(const RkBatch& b, int64_t v, bool by_elem) {
+  int i = 0;
+#pragma unroll
+  for (int q = 1; q < RK_MAXP; ++q)
+    if (q < b.n && v >= (by_elem ? b.p[q].e0 : b.p[q].wg0)) i = q;
+  return i;
+}
+
+template <int NB>
+__global__ __launch_bounds__(NTH) void lora_rk_batch(const RkBatch b) {
+  __shared__ __attribute__((aligned(16))) uint16_t Gs[RK_BM * RK_LD];
+  __shared__ __attribute__((aligned(16))) uint16_t Ss[2 * RK_RP * RK_LD];
+  const int i = rk_find(b, blockIdx.x, false);
+  const RkProblem& q = b.p[i];
+  const int64_t w = blockIdx.x - q.wg0;
+  const int64_t tile = w % q.tiles, split = w / q.tiles;
+  if (q.col)
+    rk_tile<true, false, NB>(q.big, q.R, q.Kc, q.G, q.ldg, q.g_bytes, q.S, q.ssk, q.ssj,
+                             q.s_bytes, q.klen, q.part, tile, split, Gs, Ss);
+  else
+    rk_tile<false, false, NB>(q.big, q.R, q.Kc, q.G, q.ldg, q.g_bytes, q.S, q.ssk, q.ssj,
+                              q.s_bytes, q.klen, q.part, tile, split, Gs, Ss);
+}
+
+// sums each problem's partials in ascending split order (as lora_rk_reduce)
+__global__ __launch_bounds__(NTH) void lora_rk_reduce_batch(const RkBatch b) {
+  const int64_t e = (int64_t)blockIdx.x * NTH + threadIdx.x;
+  if (e >= b.elems) return;
+  const RkProblem& q = b.p[rk_find(b, e, true)];
+  const int64_t le = e - q.e0, st = q.big * q.R;
+  const float* p = q.part + le;
+  float s = 0.0f;
+  int z = 0;
+  for (; z + 8 <= q.ks; z += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = p[(z + u) * st];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s += v[u];
+  }
+  for (; z < q.ks; ++z) s += p[z * st];
+  const int64_t m = le / q.R, j = le % q.R;
+  float v = q.alpha * s;
+  float* o = q.out + m * q.so_m + j * q.so_j;
+  if (b.accumulate) v += *o;
+  *o = v;
 }
 
 // sums the split-K partials [ks][Mo][R] into out[m*so_m + j*so_j]
@@ -401,4 +485,118 @@ extern "C" int st_lora_gemm(int64_t Mo, int64_t No, int64_t Kc, const void* a, i
   lora_reduce<<<(unsigned)st::cdiv(Mo * No, NTH), NTH, 0, s>>>(Mo, No, ks, part, alpha, out, ldo,
                                                                accumulate);
   return st::check_launch("lora_reduce");
+}
+
+// ------------------------------------------- backward rank-r products of dY
+namespace {
+
+// Problems 2s (dT_s, ROW over dY's segment columns) and 2s+1 (dB_s, COL over
+// dY's rows) for segment s; pointers are filled only when `fill` is set.
+// Returns the partial floats needed, or -1 when an operand breaks the
+// streaming kernel's layout rules (16-byte rows, 32-bit offsets).
+int64_t plan_bwd_dy(RkBatch& b, bool fill, const uint16_t* dy, int64_t M, int64_t N,
+                    int64_t lddy, const float* B, const float* T, int64_t ldt, int r, int nseg,
+                    const int64_t* seg_end, float scale, float* dt, int64_t lddt, float* db,
+                    float* part) {
+  b = RkBatch{};
+  b.n = 2 * nseg;
+  int64_t wgs = 0, elems = 0, floats = 0, start = 0;
+  for (int s = 0; s < nseg; ++s) {
+    const int64_t width = seg_end[s] - start;
+    for (int h = 0; h < 2; ++h) {
+      RkProblem& q = b.p[2 * s + h];
+      q.col = h;
+      q.R = r;
+      q.big = h ? width : M;
+      q.Kc = h ? M : width;
+      q.ldg = lddy;
+      q.g_bytes = ((M - 1) * lddy + width) * 2;
+      q.ssk = h ? ldt : r;
+      q.ssj = 1;
+      q.s_bytes = h ? ((M - 1) * ldt + (int64_t)(s + 1) * r - (int64_t)s * r) * 4 : width * r * 4;
+      q.so_m = h ? r : lddt;
+      q.so_j = 1;
+      q.alpha = scale;
+      q.tiles = (int)st::cdiv(q.big, RK_BM);
+      q.ks = rk_ksplit(q.big, q.Kc);
+      q.klen = st::cdiv(st::cdiv(q.Kc, q.ks), RK_BK) * RK_BK;
+      q.wg0 = wgs;
+      q.e0 = elems;
+      const bool vec = (start % 8) == 0 && lddy % 8 == 0 && (h ? width : width) % 8 == 0 &&
+                       q.g_bytes < (1ll << 31) && q.s_bytes < (1ll << 31);
+      if (!vec) return -1;
+      if (fill) {
+        q.G = dy + start;
+        q.S = h ? T + (int64_t)s * r : B + start * r;
+        q.out = h ? db + start * r : dt + (int64_t)s * r;
+        q.part = part + floats;
+      }
+      wgs += (int64_t)q.tiles * q.ks;
+      elems += q.big * q.R;
+      floats += (int64_t)q.ks * q.big * q.R;
+    }
+    start = seg_end[s];
+  }
+  b.wgs = wgs;
+  b.elems = elems;
+  return floats;
+}
+
+int check_segments(int64_t N, int32_t nseg, const int64_t* seg_end) {
+  if (nseg < 1 || nseg > RK_MAXP / 2 || !seg_end)
+    return st::fail(ST_EINVAL, "st_lora_bwd_dy: nseg must be 1..%d", RK_MAXP / 2);
+  int64_t prev = 0;
+  for (int i = 0; i < nseg; ++i) {
+    if (seg_end[i] <= prev) return st::fail(ST_EINVAL, "st_lora_bwd_dy: segment ends must increase");
+    prev = seg_end[i];
+  }
+  if (prev != N) return st::fail(ST_EINVAL, "st_lora_bwd_dy: last segment end must equal N");
+  return ST_OK;
+}
+
+}  // namespace
+
+extern "C" int64_t st_lora_bwd_dy_workspace_bytes(int64_t M, int64_t N, int32_t rank,
+                                                  int32_t nseg, const int64_t* seg_end) {
+  if (M <= 0 || N <= 0 || rank <= 0 || check_segments(N, nseg, seg_end)) return 0;
+  RkBatch b;
+  const int64_t floats = plan_bwd_dy(b, false, nullptr, M, N, N, nullptr, nullptr,
+                                     (int64_t)nseg * rank, rank, nseg, seg_end, 1.0f, nullptr, 0,
+                                     nullptr, nullptr);
+  return floats < 0 ? 0 : floats * 4;
+}
+
+extern "C" int st_lora_bwd_dy(const uint16_t* dy, int64_t M, int64_t N, int64_t lddy,
+                              const float* b, const float* t, int64_t ldt, int32_t rank,
+                              int32_t nseg, const int64_t* seg_end, float scale, float* dt,
+                              int64_t lddt, float* db, void* workspace, int64_t workspace_bytes,
+                              st_stream_t stream) {
+  ST_CHECK_ARG(M >= 0 && N > 0, "st_lora_bwd_dy: bad shape");
+  ST_CHECK_ARG(rank >= 1 && rank <= 64, "st_lora_bwd_dy: rank must be 1..64");
+  if (int rc = check_segments(N, nseg, seg_end)) return rc;
+  if (M == 0) return ST_OK;
+  ST_CHECK_ARG(dy && b && t && dt && db, "st_lora_bwd_dy: NULL pointer");
+  ST_CHECK_ARG(lddy >= N && ldt >= (int64_t)nseg * rank && lddt >= (int64_t)nseg * rank,
+               "st_lora_bwd_dy: leading dimension too small");
+  ST_CHECK_ARG(((uintptr_t)dy & 15u) == 0, "st_lora_bwd_dy: dy must be 16-byte aligned");
+  RkBatch bt;
+  const int64_t floats = plan_bwd_dy(bt, true, dy, M, N, lddy, b, t, ldt, rank, nseg, seg_end,
+                                     scale, dt, lddt, db, (float*)workspace);
+  if (floats < 0)
+    return st::fail(ST_EUNSUPPORTED,
+                    "st_lora_bwd_dy: segments need 8-element-aligned starts and widths, "
+                    "rows a multiple of 8 and operands below 2 GiB");
+  if (!workspace || workspace_bytes < floats * 4)
+    return st::fail(ST_EWORKSPACE, "st_lora_bwd_dy: needs %lld workspace bytes",
+                    (long long)(floats * 4));
+  ST_CHECK_ARG(bt.wgs <= 0x7fffffff, "st_lora_bwd_dy: too many workgroups");
+  hipStream_t s = (hipStream_t)stream;
+  if (rank > 32)
+    lora_rk_batch<2><<<(unsigned)bt.wgs, NTH, 0, s>>>(bt);
+  else
+    lora_rk_batch<1><<<(unsigned)bt.wgs, NTH, 0, s>>>(bt);
+  int rc = st::check_launch("lora_rk_batch");
+  if (rc) return rc;
+  lora_rk_reduce_batch<<<(unsigned)st::cdiv(bt.elems, NTH), NTH, 0, s>>>(bt);
+  return st::check_launch("lora_rk_reduce_batch");
 }

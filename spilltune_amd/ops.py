@@ -259,18 +259,29 @@ class _Q4LoRALinear(torch.autograd.Function):
             x, T, A_cat, B_cat = ctx.saved_tensors
             nseg = len(weight.segments)
             dT = torch.empty((M, nseg * rank), dtype=_F32, device=dev)
-            off = 0
+            dB_all = torch.empty((N, rank), dtype=_F32, device=dev)
+            # dT_s = s * dY_s B_s and dB_s = s * dY_s^T T_s for every segment:
+            # one launch of partial products and one reduction
+            ends = _lib.i64_array(torch.tensor(weight.segments).cumsum(0).tolist())
+            need = _lib.query("st_lora_bwd_dy_workspace_bytes", M, N, rank, nseg, ends)
+            if need > 0:
+                ws = _ws.get(dev, need)
+                _lib.call("st_lora_bwd_dy", _lib.ptr(dy), M, N, N, _lib.ptr(B_cat), _lib.ptr(T),
+                          T.stride(0), rank, nseg, ends, float(scale), _lib.ptr(dT), dT.stride(0),
+                          _lib.ptr(dB_all), _lib.ptr(ws), ws.numel(), stream)
+            else:  # segment layouts the batched kernel does not take: one product at a time
+                off = 0
+                for s, width in enumerate(weight.segments):
+                    dys = dy[:, off:off + width]
+                    lora_gemm(M, rank, width, dys, N, 1, B_cat[off:off + width], rank, 1, scale,
+                              dT[:, s * rank:(s + 1) * rank])
+                    lora_gemm(width, rank, M, dys, 1, N, T[:, s * rank:(s + 1) * rank],
+                              T.stride(0), 1, scale, dB_all[off:off + width])
+                    off += width
             dBs = []
-            for s, width in enumerate(weight.segments):
-                dys = dy[:, off:off + width]
-                Bs = B_cat[off:off + width]
-                Ts = T[:, s * rank:(s + 1) * rank]
-                dTs = dT[:, s * rank:(s + 1) * rank]
-                # dT_s = s * dY_s B_s ;  dB_s = s * dY_s^T T_s
-                lora_gemm(M, rank, width, dys, N, 1, Bs, rank, 1, scale, dTs)
-                dB = torch.empty((width, rank), dtype=_F32, device=dev)
-                lora_gemm(width, rank, M, dys, 1, N, Ts, T.stride(0), 1, scale, dB)
-                dBs.append(dB)
+            off = 0
+            for width in weight.segments:
+                dBs.append(dB_all[off:off + width])
                 off += width
             # dA_cat = dT_cat^T x for every segment in one product
             R = nseg * rank

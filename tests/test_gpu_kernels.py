@@ -303,3 +303,49 @@ def test_q4_linear_tail_split_matches_single_launch(dev, oracle_codec, monkeypat
         ref[:, off:off + n] += (x.float().cpu() @ lo.A.cpu().T) @ lo.B.cpu().T * lo.scale
         off += n
     _close_bf16(outs[0], (ref.to(BF).float() + res.float().cpu()).to(BF), "split fwd")
+
+
+@pytest.mark.parametrize("widths,rank", [((512, 128, 128), 16), ((1024, 1024), 8), ((384,), 40)])
+def test_lora_bwd_dy_matches_per_product(dev, widths, rank):
+    """st_lora_bwd_dy (every segment's dT and dB in one launch) gives the bits of
+    the per-product st_lora_gemm calls (same splits, same summation order),
+    and both match float64."""
+    g = torch.Generator().manual_seed(sum(widths) + rank)
+    M, N, nseg = 300, sum(widths), len(widths)
+    dy = torch.randn(M, N, generator=g).to(BF).to(dev)
+    B = (torch.randn(N, rank, generator=g) * 0.1).to(dev)
+    T = torch.randn(M, nseg * rank, generator=g).to(dev)
+    scale = 0.75
+    ends = _lib.i64_array(torch.tensor(widths).cumsum(0).tolist())
+    need = _lib.query("st_lora_bwd_dy_workspace_bytes", M, N, rank, nseg, ends)
+    assert need > 0
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    dT = torch.empty(M, nseg * rank, device=dev)
+    dB = torch.empty(N, rank, device=dev)
+    _lib.call("st_lora_bwd_dy", _lib.ptr(dy), M, N, N, _lib.ptr(B), _lib.ptr(T), T.stride(0), rank,
+              nseg, ends, scale, _lib.ptr(dT), dT.stride(0), _lib.ptr(dB), _lib.ptr(ws), need,
+              _lib.stream_handle(dev))
+    dT2, dB2 = torch.empty_like(dT), torch.empty_like(dB)
+    off = 0
+    for s, w in enumerate(widths):
+        dys = dy[:, off:off + w]
+        ops.lora_gemm(M, rank, w, dys, N, 1, B[off:off + w], rank, 1, scale,
+                      dT2[:, s * rank:(s + 1) * rank])
+        ops.lora_gemm(w, rank, M, dys, 1, N, T[:, s * rank:(s + 1) * rank], T.stride(0), 1, scale,
+                      dB2[off:off + w])
+        off += w
+    torch.cuda.synchronize()
+    assert torch.equal(dT, dT2) and torch.equal(dB, dB2)
+    off = 0
+    for s, w in enumerate(widths):
+        dys = dy[:, off:off + w].double()
+        torch.testing.assert_close(dT[:, s * rank:(s + 1) * rank].double(),
+                                   scale * dys @ B[off:off + w].double(), rtol=1e-5,
+                                   atol=1e-4 * w ** 0.5)
+        torch.testing.assert_close(dB[off:off + w].double(),
+                                   scale * dys.T @ T[:, s * rank:(s + 1) * rank].double(),
+                                   rtol=1e-5, atol=1e-4 * M ** 0.5)
+        off += w
+    # a segment start off the 8-element grid is refused by the query (callers fall back)
+    bad = _lib.i64_array([100, N])
+    assert _lib.query("st_lora_bwd_dy_workspace_bytes", M, N, rank, 2, bad) == 0
