@@ -318,10 +318,19 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
       xr[i] = ld16(rsA, off);
     }
   };
+  // LDS store addresses are rebuilt from an opaque copy of tid at each use
+  // (a few VALU) rather than kept live across the loop, where they would be
+  // the first values the 256x256 tile spills.
+  auto fresh_tid = [&]() {
+    int t = tid;
+    asm volatile("" : "+v"(t));
+    return t;
+  };
   auto store_A = [&](uint4* as, const uint4 (&xr)[TL::A_IT]) {
+    const int ot = fresh_tid();
 #pragma unroll
     for (int i = 0; i < TL::A_IT; ++i) {
-      int id = tid + i * NT;
+      int id = ot + i * NT;
       as[pad(id >> 3, id & 7)] = xr[i];
     }
   };
@@ -420,8 +429,9 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
         if (ch * 4 / NW != part) continue;
         uint32_t o[4];
         deq8(w.w[ch], tbl, sh_e, 4u - sh_e, o);
-        const int idx =
-            MODE == FWD_Q4 ? pad(brow, (bsub * EPT) / 8 + ch) : dswz(drow, dsub * NW + ch);
+        const int ot = fresh_tid();
+        const int idx = MODE == FWD_Q4 ? pad(ot / TPR, ((ot % TPR) * EPT) / 8 + ch)
+                                       : dswz(ot / DTR, (ot % DTR) * NW + ch);
         bs[idx] = make_uint4(o[0], o[1], o[2], o[3]);
       }
     } else if constexpr (MODE == FWD_BF16) {
@@ -469,16 +479,17 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
   // MFMA operand fragments of one 16-wide contraction slice s (0..3) of a tile
   auto read_frags = [&](const uint4* as, const uint4* bs, int s, bf16x8 (&a)[FM],
                         bf16x8 (&b)[FN]) {
-    const int c = 2 * s + (lane >> 5);
+    const int ln = fresh_tid() & 63;  // rebuilt per call, like the store addresses
+    const int c = 2 * s + (ln >> 5);
 #pragma unroll
     for (int i = 0; i < FM; ++i)
-      a[i] = __builtin_bit_cast(bf16x8, as[pad(wm * WM + i * 32 + (lane & 31), c)]);
+      a[i] = __builtin_bit_cast(bf16x8, as[pad(wm * WM + i * 32 + (ln & 31), c)]);
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
       if constexpr (MODE == DGRAD_Q4)
-        b[j] = b_tr(bs, s * 16, wn * WN + j * 32, lane);
+        b[j] = b_tr(bs, s * 16, wn * WN + j * 32, ln);
       else
-        b[j] = __builtin_bit_cast(bf16x8, bs[pad(wn * WN + j * 32 + (lane & 31), c)]);
+        b[j] = __builtin_bit_cast(bf16x8, bs[pad(wn * WN + j * 32 + (ln & 31), c)]);
     }
   };
   auto mfmas = [&](const bf16x8 (&a)[FM], const bf16x8 (&b)[FN]) {
