@@ -65,8 +65,7 @@ def dense_block(hidden_states, position_embeddings, attention_mask, *, heads, kv
     B, S, Hd = hidden_states.shape
     cos, sin = position_embeddings
     x2d = hidden_states.reshape(B * S, Hd)
-    residual = x2d
-    xn = ops.rms_norm(x2d, weights["input_layernorm.weight"], eps)
+    residual, xn = ops.rms_norm_residual(x2d, weights["input_layernorm.weight"], eps)
 
     def head_norm(t, name):  # Qwen3: RMSNorm of every head over head_dim (dense.py:128-133)
         if not qk_norm:
@@ -96,7 +95,7 @@ def dense_block(hidden_states, position_embeddings, attention_mask, *, heads, kv
     attended = ops.causal_attention(q, k, v, ops.attention_scale(head_dim)).reshape(B * S, heads * head_dim)
     h1 = ops.q4_lora_linear(attended, _weight(weights, "self_attn.o_proj"), [lora_o], residual=residual)
 
-    xn2 = ops.rms_norm(h1, weights["post_attention_layernorm.weight"], eps)
+    h1, xn2 = ops.rms_norm_residual(h1, weights["post_attention_layernorm.weight"], eps)
     if feed_forward is not None:  # e.g. the MoE block (dense.py:152)
         return (h1 + feed_forward(xn2.view(B, S, Hd), weights).reshape(B * S, Hd)).view(B, S, Hd)
     wg, wu = _weight(weights, "mlp.gate_proj"), _weight(weights, "mlp.up_proj")

@@ -358,6 +358,45 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     return _RMSNorm.apply(x.contiguous(), weight.detach().contiguous(), eps)
 
 
+class _RMSNormResidual(torch.autograd.Function):
+    """``(x, rms_norm(x))`` for a hidden state that also feeds a residual add
+    (dense.py:120-153: ``residual = hidden`` next to ``rms(hidden)``).  The
+    first output is ``x`` itself; the backward returns ``d_residual + VJP``
+    from one st_rmsnorm_bwd call (its ``dres``), the sum autograd would
+    otherwise form with a separate bf16 add."""
+
+    @staticmethod
+    def forward(ctx, x, w, eps):
+        ctx.set_materialize_grads(False)
+        rows, H = x.shape
+        y = torch.empty_like(x)
+        rstd = torch.empty(rows, dtype=_F32, device=x.device)
+        _lib.call("st_rmsnorm_fwd", _lib.ptr(x), _lib.ptr(w), rows, H, float(eps), _lib.ptr(y),
+                  _lib.ptr(rstd), _lib.stream_handle(x.device))
+        ctx.save_for_backward(x, w, rstd)
+        return x, y
+
+    @staticmethod
+    def backward(ctx, dres, dy):
+        x, w, rstd = ctx.saved_tensors
+        if dy is None:
+            return dres, None, None
+        dy = dy.contiguous()
+        dres = None if dres is None else dres.contiguous()
+        rows, H = x.shape
+        dx = torch.empty_like(x)
+        _lib.call("st_rmsnorm_bwd", _lib.ptr(dy), _lib.ptr(x), _lib.ptr(w), _lib.ptr(rstd),
+                  _lib.ptr(dres), rows, H, _lib.ptr(dx), _lib.stream_handle(x.device))
+        return dx, None, None
+
+
+def rms_norm_residual(x: torch.Tensor, weight: torch.Tensor, eps: float):
+    """``(x, rms_norm(x))`` with the residual gradient folded into the norm's VJP."""
+    if x.dtype != _BF16 or weight.dtype != _BF16:
+        raise ValueError("rms_norm expects bf16 input and weight")
+    return _RMSNormResidual.apply(x.contiguous(), weight.detach().contiguous(), eps)
+
+
 # ----------------------------------------------------------------- terminal
 def linear_bf16(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     """``y = bf16(x w^T)`` on the MFMA GEMM (fp32 accumulation)."""
@@ -632,5 +671,6 @@ def attention_scale(head_dim: int) -> float:
 
 __all__ = ["Q4Weight", "concat_rows", "q4_lora_linear", "rms_norm", "rope_qkv", "rope_heads",
            "causal_attention", "swiglu", "swiglu_pair", "lora_gemm", "attention_scale",
+           "rms_norm_residual",
            "linear_bf16", "linear_bf16_dgrad", "supervised_chunk_intervals",
            "chunked_causal_loss"]
