@@ -9,7 +9,7 @@
 // with a/b either bf16 or fp32.  The contraction is split across blocks into
 // fp32 partials in the caller's workspace and summed in a fixed order by a
 // second kernel, so results are deterministic run to run.
-#include "common.h"
+#include "rank_r.h"
 
 namespace {
 
@@ -95,29 +95,17 @@ __global__ __launch_bounds__(NTH) void lora_reduce(int64_t Mo, int64_t No, int k
 }
 
 // ---- MFMA path for the LoRA shapes: one bf16 operand G is large, the other
-// (S, fp32) has at most 64 columns.  out[m, j] = sum_k g(m,k) S[k, j] with
-// g(m,k) = G[m*ldg + k] (ROW: contraction contiguous -- T = x A^T, dT = dY B) or
-// g(m,k) = G[k*ldg + m] (COL: contraction over G's rows -- dB = dY^T T,
-// dA^T = x^T dT).  S is split into hi = bf16(s) and lo = bf16(s - hi): bf16
-// products are exact in fp32, so g*hi + g*lo on v_mfma_f32_32x32x16_bf16 with
-// fp32 accumulation carries s to ~16 significant bits (relative error ~2^-17)
-// at bf16 matrix-core rate.
-constexpr int RK_BM = 128, RK_BK = 64, RK_RP = 64;
-constexpr int RK_LD = RK_BK + 8;  // bf16 per LDS row (144 bytes: 16-byte aligned, bank-spread)
-constexpr int RK_PF = 3;          // chunks of loads in flight per workgroup
+// (S, fp32) has at most 64 columns; st::rk_accumulate (rank_r.h) streams it.
+// T = x A^T and dT = dY B are ROW forms (contraction contiguous), dB = dY^T T
+// and dA^T = x^T dT COL forms (contraction over G's rows).
+using st::RK_BM;
+using st::RK_BK;
+using st::RK_LD;
+using st::RK_RP;
+static_assert(st::RK_NTH == NTH, "rank-r tiles run on NTH-thread workgroups");
 
-// Streaming pipeline: a ring of RK_PF chunks of G (4 x 16 bytes per thread)
-// and S lives in registers; as soon as a chunk is staged into LDS its slot is
-// refilled with the chunk RK_PF steps ahead, so each workgroup keeps about
-// RK_PF x 16 KiB of loads in flight while it computes.  Loads go through
-// buffer resources with 32-bit offsets (operand extents below 2 GiB, checked
-// by the host); rows or chunks out of range read as zero.  The host routes
-// only 16-byte-aligned G with rows (ROW form: contraction; COL form: output)
-// a multiple of 8 elements here.
 // One workgroup's share: output rows [tile*RK_BM, +RK_BM) over contraction
-// chunk [split*klen, +klen), written to partial slice `split`.  Gs / Ss: the
-// caller's LDS (ROW: G as [m][k] rows of RK_LD; COL: [k][m] in the
-// transposed-operand layout; S as [hi|lo][j][k]).
+// chunk [split*klen, +klen), written to partial slice `split`.
 template <bool COL, bool SK1, int NB>
 __device__ __forceinline__ void rk_tile(int64_t Mo, int64_t R, int64_t Kc,
                                         const uint16_t* __restrict__ G, int64_t ldg,
@@ -125,121 +113,23 @@ __device__ __forceinline__ void rk_tile(int64_t Mo, int64_t R, int64_t Kc,
                                         int64_t ssj, int64_t s_bytes, int64_t klen,
                                         float* __restrict__ part, int64_t tile, int64_t split,
                                         uint16_t* __restrict__ Gs, uint16_t* __restrict__ Ss) {
-  constexpr int RP = NB * 32;            // staged S columns
-  constexpr int SIT = RK_BK * RP / NTH;  // S values per thread per chunk (8 or 16)
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t m0 = tile * RK_BM;
   const int kb = (int)(split * klen);
   const int ke = (int)(kb + klen < Kc ? kb + klen : Kc);
-  const auto rsG = st::make_rsrc(G, g_bytes);
-  const auto rsS = st::make_rsrc(S, s_bytes);
-  const uint32_t ldg2 = (uint32_t)ldg * 2, ssk4 = (uint32_t)ssk * 4, ssj4 = (uint32_t)ssj * 4;
   f32x16 acc[NB];
 #pragma unroll
   for (int c = 0; c < NB; ++c)
 #pragma unroll
     for (int v = 0; v < 16; ++v) acc[c][v] = 0.0f;
-
-  // G: per-thread byte offset at contraction 0 (kOOB beyond Mo) and the
-  // contraction offset of each of its four 16-byte pieces within a step
-  uint32_t gbase[4];
-  int gk[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    if (!COL) {  // 128 rows x 64 contraction: 8 pieces of 8 per row, 4 pieces per thread
-      const int id = tid + i * NTH, row = id >> 3, c = id & 7;
-      const int64_t m = m0 + row;
-      gbase[i] = m < Mo ? (uint32_t)(m * ldg * 2) + c * 16 : st::kOOB;
-      gk[i] = c * 8;
-    } else {  // 64 contraction rows x 128 columns: 4 rows x 8 columns per thread
-      const int64_t m = m0 + (tid & 15) * 8;
-      gbase[i] = m < Mo ? (uint32_t)(m * 2) : st::kOOB;
-      gk[i] = (tid >> 4) * 4 + i;
-    }
-  }
-  // S value i of a thread: (contraction kk, column j).  SK1 (S contiguous
-  // along the contraction): kk = tid % 64, j = tid / 64 + 4i; otherwise
-  // j = tid % RP, kk = tid / RP + (NTH / RP) i.
-  auto s_kk = [&](int i) { return SK1 ? (tid & 63) : tid / RP + (NTH / RP) * i; };
-  auto s_j = [&](int i) { return SK1 ? (tid >> 6) + 4 * i : tid % RP; };
-
-  uint4 gr[RK_PF][4];
-  float sr[RK_PF][SIT];
-  auto load = [&](int k0, uint4 (&g)[4], float (&sv)[SIT]) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int k = k0 + gk[i];
-      uint32_t off = st::kOOB;
-      if (gbase[i] != st::kOOB && k < ke)
-        off = COL ? gbase[i] + (uint32_t)k * ldg2 : gbase[i] + (uint32_t)k0 * 2;
-      g[i] = st::ld16(rsG, off);
-    }
-#pragma unroll
-    for (int i = 0; i < SIT; ++i) {
-      const int k = k0 + s_kk(i), j = s_j(i);
-      const uint32_t off =
-          (k < ke && j < R) ? (uint32_t)k * ssk4 + (uint32_t)j * ssj4 : st::kOOB;
-      sv[i] = __builtin_bit_cast(float, st::ld4(rsS, off));
-    }
-  };
-  auto store = [&](const uint4 (&g)[4], const float (&sv)[SIT]) {
-    if (!COL) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int id = tid + i * NTH, row = id >> 3, c = id & 7;
-        *(uint4*)&Gs[row * RK_LD + c * 8] = g[i];
-      }
-    } else {  // [contraction][column] as loaded; the MFMA operand is read transposed
-      const int kg = tid >> 4, mg = tid & 15;
-#pragma unroll
-      for (int h = 0; h < 4; ++h) ((uint4*)Gs)[st::trswz<RK_BM>(kg * 4 + h, mg)] = g[h];
-    }
-#pragma unroll
-    for (int i = 0; i < SIT; ++i) {
-      const int kk = s_kk(i), j = s_j(i);
-      const uint16_t hb = st::f32_to_bf16(sv[i]);
-      const uint16_t lb = st::f32_to_bf16(sv[i] - st::bf16_to_f32(hb));
-      Ss[j * RK_LD + kk] = hb;
-      Ss[(RK_RP + j) * RK_LD + kk] = lb;
-    }
-  };
-
-#pragma unroll
-  for (int c = 0; c < RK_PF; ++c)
-    if (kb + c * RK_BK < ke) load(kb + c * RK_BK, gr[c], sr[c]);
-  for (int kg = kb; kg < ke; kg += RK_PF * RK_BK) {
-#pragma unroll
-    for (int c = 0; c < RK_PF; ++c) {
-      const int k0 = kg + c * RK_BK;
-      if (k0 >= ke) break;
-      store(gr[c], sr[c]);
-      __syncthreads();
-      if (k0 + RK_PF * RK_BK < ke) load(k0 + RK_PF * RK_BK, gr[c], sr[c]);
-#pragma unroll
-      for (int s = 0; s < RK_BK / 16; ++s) {
-        const int ko = s * 16 + (lane >> 5) * 8;
-        const bf16x8 a =
-            COL ? st::tr_operand<RK_BM>((const uint4*)Gs, s * 16, wave * 32, lane)
-                : *(const bf16x8*)&Gs[(wave * 32 + (lane & 31)) * RK_LD + ko];
-#pragma unroll
-        for (int cc = 0; cc < NB; ++cc)
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const bf16x8 b =
-                *(const bf16x8*)&Ss[(h * RK_RP + cc * 32 + (lane & 31)) * RK_LD + ko];
-            acc[cc] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[cc], 0, 0, 0);
-          }
-      }
-      __syncthreads();
-    }
-  }
+  st::rk_accumulate<COL, SK1, NB, false>(acc, Mo, R, m0, kb, ke, G, ldg, g_bytes, 0, S, ssk, ssj,
+                                         s_bytes, nullptr, 0, nullptr, 0, Gs, Ss);
   float* dst = part + split * Mo * R;
 #pragma unroll
   for (int c = 0; c < NB; ++c) {
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      const int64_t m = m0 + wave * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-      const int j = c * 32 + (lane & 31);
+      const int64_t m = m0 + st::rk_row(v);
+      const int j = st::rk_col(c);
       if (m < Mo && j < R) dst[m * R + j] = acc[c][v];
     }
   }

@@ -3,7 +3,7 @@
 // token permutation, the weighted combine in the reference's bf16 order and
 // its VJP, the gather-sum of permuted input gradients, and the grouped
 // low-rank (LoRA) products over permuted rows.
-#include "common.h"
+#include "rank_r.h"
 
 namespace {
 
@@ -267,11 +267,14 @@ __global__ __launch_bounds__(NTH) void route_sigmoid_bwd(const float* __restrict
 // all (token, slot) picks, takes its offset from the prefix, then places its
 // picks in ascending (token, slot) order: row_token[row] = token of the pick,
 // pick_row[token * k + slot] = its permuted row (-1 for an out-of-range
-// expert).  Deterministic, no global atomics.
-__global__ __launch_bounds__(NTH) void permute(const int32_t* __restrict__ idx, int64_t n, int k,
-                                               int E, int32_t* __restrict__ offsets,
-                                               int32_t* __restrict__ row_token,
-                                               int32_t* __restrict__ pick_row) {
+// expert).  Deterministic, no global atomics.  1024 threads per workgroup:
+// the ordered pass is a serial walk over all picks in workgroup-sized steps.
+constexpr int NTHP = 1024;
+__global__ __launch_bounds__(NTHP) void permute(const int32_t* __restrict__ idx, int64_t n, int k,
+                                                int E, int32_t* __restrict__ offsets,
+                                                int32_t* __restrict__ row_token,
+                                                int32_t* __restrict__ pick_row) {
+  constexpr int NTH = NTHP;
   __shared__ int hist[1024];
   __shared__ int wsum[NTH / 64];
   __shared__ int base_s;
@@ -651,7 +654,98 @@ __global__ __launch_bounds__(NTH) void grouped_rk(GroupedRk a) {
   }
 }
 
+// Streaming version of grouped_rk for 16-byte-aligned G rows (multiples of 8
+// elements) below 2 GiB: st::rk_accumulate's prefetch ring and buffer loads.
+// COL forms with a gather stage the group's source rows in LDS, GK_IDX at a
+// time.  Same outputs, roundings and summation order per output as
+// grouped_rk (ascending contraction in 64-wide MFMA steps).
+constexpr int GK_IDX = 2048;
+
+template <bool COL, bool SK1, int NB, bool GATHER>
+__global__ __launch_bounds__(st::RK_NTH) void grouped_rk_stream(GroupedRk a, int64_t g_bytes) {
+  __shared__ __attribute__((aligned(16))) uint16_t Gs[st::RK_BM * st::RK_LD];
+  __shared__ __attribute__((aligned(16))) uint16_t Ss[2 * st::RK_RP * st::RK_LD];
+  __shared__ int idx[COL && GATHER ? GK_IDX : 1];
+  const int tid = threadIdx.x;
+  const int z = blockIdx.z;
+  int grp = 0;
+  int64_t m0, mend, kb, ke, gcol0 = (int64_t)z * a.seg_len;
+  const float* S = a.S;
+  if (!COL) {
+    if (!st::find_group(a.offsets, a.groups, st::RK_BM, blockIdx.x, a.rows, grp, m0, mend)) return;
+    kb = 0;
+    ke = a.seg_len;
+    S += grp * a.s_gstride + (int64_t)z * a.seg_len * a.ssk;
+  } else {
+    grp = blockIdx.y;
+    m0 = (int64_t)blockIdx.x * st::RK_BM;
+    mend = a.seg_len;
+    kb = a.offsets[grp];
+    ke = a.offsets[grp + 1];
+    if (kb < 0) kb = 0;
+    if (ke > a.rows) ke = a.rows;
+    S += (int64_t)z * a.R * a.ssj;
+  }
+  f32x16 acc[NB];
+#pragma unroll
+  for (int c = 0; c < NB; ++c)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[c][v] = 0.0f;
+  if constexpr (COL && GATHER) {
+    for (int64_t s0 = kb; s0 < ke; s0 += GK_IDX) {
+      const int64_t s1 = s0 + GK_IDX < ke ? s0 + GK_IDX : ke;
+      __syncthreads();  // the previous range's loads have read idx
+      for (int64_t i = tid; i < s1 - s0; i += st::RK_NTH) idx[i] = a.gather[s0 + i];
+      __syncthreads();
+      st::rk_accumulate<true, SK1, NB, true>(acc, mend, a.R, m0, (int)s0, (int)s1, a.G, a.ldg,
+                                             g_bytes, gcol0, S, a.ssk, a.ssj, 0x7fffffff,
+                                             nullptr, a.g_rows, idx, (int)s0, Gs, Ss);
+    }
+  } else {
+    // the valid mask of the contraction / rows is exact: S reads use an
+    // open extent, every offset they form is in range
+    st::rk_accumulate<COL, SK1, NB, GATHER>(acc, mend, a.R, m0, (int)kb, (int)ke, a.G, a.ldg,
+                                            g_bytes, gcol0, S, a.ssk, a.ssj, 0x7fffffff,
+                                            a.gather, a.g_rows, nullptr, 0, Gs, Ss);
+  }
+  float* dst = a.out;
+  if (!COL)
+    dst += (int64_t)z * a.R * a.so_j;
+  else
+    dst += grp * a.o_gstride + (int64_t)z * a.seg_len * a.so_m;
+#pragma unroll
+  for (int c = 0; c < NB; ++c) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int64_t m = m0 + st::rk_row(v);
+      const int j = st::rk_col(c);
+      if (m < mend && j < a.R) {
+        float* o = dst + m * a.so_m + j * a.so_j;
+        const float val = a.alpha * acc[c][v];
+        *o = a.accumulate ? *o + val : val;
+      }
+    }
+  }
+}
+
 bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Launches the streaming kernel when G qualifies; returns false otherwise.
+template <bool COL>
+bool launch_grouped_stream(const GroupedRk& a, dim3 grid, hipStream_t stream) {
+  const int64_t g_bytes = a.g_rows * a.ldg * 2;
+  if (!a.vec || g_bytes >= (1ll << 31)) return false;
+  const bool sk1 = a.ssk == 1, nb2 = a.R > 32, gat = a.gather != nullptr;
+  auto go = [&](auto kern) { kern<<<grid, st::RK_NTH, 0, stream>>>(a, g_bytes); };
+  if (nb2) {
+    if (gat) sk1 ? go(grouped_rk_stream<COL, true, 2, true>) : go(grouped_rk_stream<COL, false, 2, true>);
+    else sk1 ? go(grouped_rk_stream<COL, true, 2, false>) : go(grouped_rk_stream<COL, false, 2, false>);
+  } else {
+    if (gat) sk1 ? go(grouped_rk_stream<COL, true, 1, true>) : go(grouped_rk_stream<COL, false, 1, true>);
+    else sk1 ? go(grouped_rk_stream<COL, true, 1, false>) : go(grouped_rk_stream<COL, false, 1, false>);
+  }
+  return true;
+}
 
 }  // namespace
 
@@ -722,7 +816,7 @@ extern "C" int st_moe_permute(const int32_t* indices, int64_t tokens, int32_t to
   ST_CHECK_ARG(tokens * top_k < (1ll << 31), "st_moe_permute: too many picks");
   ST_CHECK_ARG(offsets && (tokens == 0 || (indices && row_token && pick_row)),
                "st_moe_permute: NULL pointer");
-  permute<<<(unsigned)experts, NTH, 0, (hipStream_t)stream>>>(
+  permute<<<(unsigned)experts, NTHP, 0, (hipStream_t)stream>>>(
       indices, tokens * top_k, top_k, experts, offsets, row_token, pick_row);
   return st::check_launch("permute");
 }
@@ -794,7 +888,8 @@ extern "C" int st_moe_lora_rows(int64_t rows, int32_t R, int64_t seg_len, int32_
   a.out = out; a.so_m = ldo; a.so_j = 1; a.alpha = alpha; a.accumulate = 0;
   a.vec = (al16(g) && ldg % 8 == 0 && seg_len % 8 == 0) ? 1 : 0;
   dim3 grid((unsigned)(st::cdiv(rows, GK_BM) + groups), 1, (unsigned)nseg);
-  grouped_rk<false><<<grid, NTH, 0, (hipStream_t)stream>>>(a);
+  if (!launch_grouped_stream<false>(a, grid, (hipStream_t)stream))
+    grouped_rk<false><<<grid, NTH, 0, (hipStream_t)stream>>>(a);
   return st::check_launch("grouped_rk rows");
 }
 
@@ -817,6 +912,7 @@ extern "C" int st_moe_lora_grads(int64_t rows, int32_t R, int64_t seg_len, int32
   a.alpha = alpha; a.accumulate = accumulate;
   a.vec = (al16(g) && ldg % 8 == 0 && seg_len % 8 == 0) ? 1 : 0;
   dim3 grid((unsigned)st::cdiv(seg_len, GK_BM), (unsigned)groups, (unsigned)nseg);
-  grouped_rk<true><<<grid, NTH, 0, (hipStream_t)stream>>>(a);
+  if (!launch_grouped_stream<true>(a, grid, (hipStream_t)stream))
+    grouped_rk<true><<<grid, NTH, 0, (hipStream_t)stream>>>(a);
   return st::check_launch("grouped_rk grads");
 }
