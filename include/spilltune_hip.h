@@ -122,6 +122,22 @@ int st_q4_linear_dgrad(const uint16_t* dy, int64_t M, int64_t N, int64_t lddy,
                        uint16_t* dx, int64_t lddx,
                        void* workspace, int64_t workspace_bytes, st_stream_t stream);
 
+/*
+ * The same input gradient for a projection that reads silu(gate) * up of a
+ * fused gate|up pre-activation gu [M, 2I] (row stride ldgu): instead of dx,
+ * the epilogue applies the SwiGLU VJP of dense.py:153 to each bf16 dx value
+ * (the roundings of st_swiglu_bwd) and writes dgu[m, i] = dgate and
+ * dgu[m, I + i] = dup (row stride lddgu).  I is this projection's in_features.
+ * gu and dgu must be 16-byte aligned with ldgu, lddgu and I multiples of 8
+ * (ST_EUNSUPPORTED otherwise).
+ */
+int st_q4_linear_dgrad_swiglu(const uint16_t* dy, int64_t M, int64_t N, int64_t lddy,
+                              const uint8_t* payload, const float* scales, int64_t I,
+                              const float* lut16, int32_t flags,
+                              const float* dt, int64_t lddt, const float* lora_a, int32_t lora_k,
+                              const uint16_t* gu, int64_t ldgu, uint16_t* dgu, int64_t lddgu,
+                              void* workspace, int64_t workspace_bytes, st_stream_t stream);
+
 /* ------------------------------------------------------- LoRA rank-r work */
 /*
  * Generic skinny fp32-accumulating product used by the LoRA terms:

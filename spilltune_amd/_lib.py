@@ -37,6 +37,8 @@ _SIGNATURES = {
     "st_q4_linear_dgrad_workspace_bytes": (_I64, [_I64, _I64, _I64]),
     "st_q4_linear_dgrad": (_I32, [_P, _I64, _I64, _I64, _P, _P, _I64, _P, _I32, _P, _I64, _P,
                                   _I32, _P, _I64, _P, _I64, _P]),
+    "st_q4_linear_dgrad_swiglu": (_I32, [_P, _I64, _I64, _I64, _P, _P, _I64, _P, _I32, _P, _I64,
+                                         _P, _I32, _P, _I64, _P, _I64, _P, _I64, _P]),
     "st_lora_gemm_workspace_bytes": (_I64, [_I64, _I64, _I64]),
     "st_lora_gemm": (_I32, [_I64, _I64, _I64, _P, _I32, _I64, _I64, _P, _I32, _I64, _I64, _F, _P,
                             _I64, _I32, _P, _I64, _P]),

@@ -42,6 +42,22 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float x) {
 // round an fp32 value through bf16 and back (models a bf16 tensor op result)
 __device__ __forceinline__ float bf16r(float x) { return bf16_to_f32(f32_to_bf16(x)); }
 
+// SwiGLU VJP of one element of a = silu(g) * u (bf16 tensors) for the
+// upstream value y, with autograd's roundings through bf16 tensors: the silu
+// output and the silu-gradient input dsv = y * u are bf16, dg and du are
+// returned in fp32 for the caller to round.  The sigmoid uses the hardware
+// 2^x and reciprocal (a few fp32 ulp, far below the bf16 resolution of every
+// result) instead of a libm exp and two IEEE divisions: the backward runs it
+// in GEMM epilogues, where those took most of the VALU time.  Infinite g
+// gives torch's NaN/inf results.
+__device__ __forceinline__ void swiglu_vjp(float g, float u, float y, float& dg, float& du) {
+  const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.44269504088896341f));
+  const float sv = bf16r(g * sg);
+  const float dsv = bf16r(y * u);
+  du = y * sv;
+  dg = dsv * (sg * (1.0f + g * (1.0f - sg)));
+}
+
 __host__ __device__ __forceinline__ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Buffer-resource loads: 32-bit byte offsets into a buffer of `bytes` bytes

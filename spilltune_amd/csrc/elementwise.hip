@@ -295,8 +295,6 @@ __global__ __launch_bounds__(NTH) void relayout(const uint16_t* __restrict__ x, 
 }
 
 // ------------------------------------------------------------------ SwiGLU
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
-
 __global__ __launch_bounds__(NTH) void swiglu_fwd(const uint16_t* __restrict__ g, int64_t ldg,
                                                  const uint16_t* __restrict__ u, int64_t ldu,
                                                  int64_t I, int64_t total,
@@ -321,11 +319,10 @@ __global__ __launch_bounds__(NTH) void swiglu_bwd(const uint16_t* __restrict__ d
   float gv = st::bf16_to_f32(g[r * ldg + c]);
   float uv = st::bf16_to_f32(u[r * ldu + c]);
   float dav = st::bf16_to_f32(da[r * ldda + c]);
-  float sg = sigmoidf_(gv);
-  float s = st::bf16r(gv / (1.0f + expf(-gv)));
-  float ds = st::bf16r(dav * uv);
-  du[r * lddu + c] = st::f32_to_bf16(dav * s);
-  dg[r * lddg + c] = st::f32_to_bf16(ds * (sg * (1.0f + gv * (1.0f - sg))));
+  float dgv, duv;
+  st::swiglu_vjp(gv, uv, dav, dgv, duv);
+  du[r * lddu + c] = st::f32_to_bf16(duv);
+  dg[r * lddg + c] = st::f32_to_bf16(dgv);
 }
 
 
@@ -377,11 +374,7 @@ __global__ __launch_bounds__(NTH) void swiglu_bwd_vec(const uint16_t* __restrict
       float gv = st::bf16_to_f32((uint16_t)(gw[k] >> (16 * h)));
       float uv = st::bf16_to_f32((uint16_t)(uw[k] >> (16 * h)));
       float dav = st::bf16_to_f32((uint16_t)(aw[k] >> (16 * h)));
-      float sg = sigmoidf_(gv);
-      float sv = st::bf16r(gv / (1.0f + expf(-gv)));
-      float dsv = st::bf16r(dav * uv);
-      ru[h] = dav * sv;
-      rg[h] = dsv * (sg * (1.0f + gv * (1.0f - sg)));
+      st::swiglu_vjp(gv, uv, dav, rg[h], ru[h]);
     }
     og[k] = st::pack_bf16x2(rg[0], rg[1]);
     ou[k] = st::pack_bf16x2(ru[0], ru[1]);

@@ -17,6 +17,8 @@
 // read one 16-wide slice ahead of the MFMAs (v_mfma_f32_32x32x16_bf16).
 // The LoRA epilogue runs on v_mfma_f32_32x32x2_f32 (fp32 operands and
 // accumulation), so the adapter term keeps the reference's fp32 arithmetic.
+#include <type_traits>
+
 #include "common.h"
 
 namespace {
@@ -55,6 +57,15 @@ struct GemmParams {
   const int32_t* goff;    // nullptr: one group of M rows
   int ngroups;
   int64_t w_gstride, s_gstride, l_gstride;  // payload bytes (or bf16 elements), floats, floats
+  // dgrad only: C = the gradient of a fused gate|up pre-activation [M, 2*swi_I]
+  // (row stride ldc) instead of dX; the epilogue applies the SwiGLU VJP to
+  // each dX value with gate|up read from swi_gu (row stride swi_ld)
+  const uint16_t* swi_gu;
+  int64_t swi_ld, swi_I;
+  // set by the launcher: the epilogue stages each 32x32 block through LDS
+  // and moves 16-byte rows (C, residual, gate|up 16-byte aligned with row
+  // strides and P multiples of 8, and the staging fits the tile's LDS)
+  int vec_epi;
 };
 
 // LDS tile rows hold 64 bf16 (8 chunks of 16 bytes) plus one chunk of padding:
@@ -171,6 +182,21 @@ __device__ __forceinline__ void stage_f32(float* dst, int ls, __amdgpu_buffer_rs
   }
 }
 
+struct EpiIn {
+  uint4 a0, a1, b0, b1;
+};
+
+// Per-wave LDS staging of the vector epilogue (dwords), placed after the LoRA
+// operands the epilogue stages (16-byte aligned).
+constexpr int EPI_STG = 16 * 36;
+template <bool DGRAD, int BM, int BN>
+__host__ __device__ __forceinline__ int64_t epi_stage_offset(const GemmParams& p) {
+  if (!p.T) return 0;
+  const int64_t f = (int64_t)BM * (p.lora_cols + 1) +
+                    (DGRAD ? (int64_t)p.lora_k * BN : (int64_t)BN * (p.lora_k + 1));
+  return (f + 3) & ~(int64_t)3;
+}
+
 // Epilogue shared by the GEMM kernels: y = bf16(acc) (+ LoRA term, + residual)
 // for this tile; waves with `has_acc` false only help stage the LoRA operands.
 // LDS (`lds`, at least BM*(lora_cols+1) + the LoRA right operand floats) is
@@ -205,13 +231,28 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const f32x16 
   if (!has_acc) return;
   const auto rsC = make_rsrc(p.C, 0x7fffffff);
   const auto rsR = make_rsrc(p.R, 0x7fffffff);
+  const auto rsG = make_rsrc(p.swi_gu, 0x7fffffff);
   const uint32_t ldc2 = (uint32_t)p.ldc * 2, ldr2 = (uint32_t)p.ldr * 2;
+  // this wave's staging area for one 32x32 block: 16 row pairs x 36 dwords
+  // (dword = the bf16 values of rows 2q, 2q+1 of one column; 36 makes the
+  // 16-byte row-pair reads of a quarter-wave cover all 64 banks once)
+  uint32_t* stg = (uint32_t*)lds + epi_stage_offset<DGRAD, BM, BN>(p) + (tid >> 6) * EPI_STG;
 
+  // LoRA term of block (i, j) on v_mfma_f32_32x32x2_f32
+  auto lora_term = [&](int rl, int cl, int coff) {
+    f32x16 la;
 #pragma unroll
-  for (int j = 0; j < FN; ++j) {
-    const int cl = wn * WN + j * 32;  // tile-local first column of this block
-    const int64_t pcol = p0 + cl + (lane & 31);
-    const bool colok = pcol < p.P;
+    for (int v = 0; v < 16; ++v) la[v] = 0.0f;
+    for (int kk = 0; kk < p.lora_k; kk += 2) {
+      int kx = kk + (lane >> 5);
+      float av = Ts[(rl + (lane & 31)) * tstride + coff + kx];
+      float bv = DGRAD ? Ls[kx * lstride + cl + (lane & 31)]
+                       : Ls[(cl + (lane & 31)) * lstride + kx];
+      la = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, la, 0, 0, 0);
+    }
+    return la;
+  };
+  auto seg_off = [&](int cl) {
     int coff = 0;
     if (lora && !DGRAD) {
       int64_t pblk = p0 + cl;
@@ -219,49 +260,194 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const f32x16 
       for (int q = 0; q < p.nseg; ++q) s += (p.seg_end[q] <= pblk) ? 1 : 0;
       coff = s * p.lora_k;
     }
+    return coff;
+  };
+
+  // VEC: block staged through LDS, each lane then owns rows 2q, 2q+1 (q =
+  // lane % 16) x columns 8k..8k+7 (k = lane / 16) of the block and moves
+  // them with 16-byte accesses.  Otherwise one 2-byte access per element.
+  // Separate copies of the loop nest per mode keep each fully unrolled.
+  // VEC operands of block (i, j) for this lane's rows 2q, 2q+1 and 8 columns:
+  // residual rows in a0, a1, or (SWI) gate rows in a0, a1 and up rows in b0, b1
+  auto fetch = [&](auto swi, int i, int j) {
+    constexpr bool SWI = decltype(swi)::value;
+    const int q = lane & 15, kc = lane >> 4;
+    const int64_t row0 = m0 + wm * WM + i * 32 + 2 * q, col = p0 + wn * WN + j * 32 + 8 * kc;
+    const bool cok = col < p.P;
+    const bool ok0 = cok && row0 < mend, ok1 = cok && row0 + 1 < mend;
+    EpiIn in;
+    in.a0 = in.a1 = in.b0 = in.b1 = make_uint4(0, 0, 0, 0);
+    if (SWI) {
+      const uint32_t gb = (uint32_t)((row0 * p.swi_ld + col) * 2);
+      const uint32_t ldg2 = (uint32_t)p.swi_ld * 2, uo = (uint32_t)p.swi_I * 2;
+      in.a0 = ld16(rsG, ok0 ? gb : kOOB);
+      in.a1 = ld16(rsG, ok1 ? gb + ldg2 : kOOB);
+      in.b0 = ld16(rsG, ok0 ? gb + uo : kOOB);
+      in.b1 = ld16(rsG, ok1 ? gb + ldg2 + uo : kOOB);
+    } else if (p.R) {
+      const uint32_t rb = (uint32_t)((row0 * p.ldr + col) * 2);
+      in.a0 = ld16(rsR, ok0 ? rb : kOOB);
+      in.a1 = ld16(rsR, ok1 ? rb + ldr2 : kOOB);
+    }
+    return in;
+  };
+
+  auto blocks = [&](auto swi, auto vec) {
+    constexpr bool SWI = decltype(swi)::value, VEC = decltype(vec)::value;
+    EpiIn cur;
+    if constexpr (VEC) cur = fetch(swi, 0, 0);
 #pragma unroll
-    for (int i = 0; i < FM; ++i) {
-      const int rl = wm * WM + i * 32;
-      const int64_t rbase = m0 + rl + (lane >> 5) * 4;  // row of v = 0
-      // element v sits at row rbase + dv(v), dv = (v/4)*8 + v%4
-      auto ok = [&](int v) { return colok && rbase + (v >> 2) * 8 + (v & 3) < mend; };
-      uint16_t rv[16];  // raw bf16: converted where used, after the LoRA products
-      if (p.R) {
-        const uint32_t rb = (uint32_t)((rbase * p.ldr + pcol) * 2);
+    for (int j = 0; j < FN; ++j) {
+      const int cl = wn * WN + j * 32;  // tile-local first column of this block
+      const int coff = seg_off(cl);
 #pragma unroll
-        for (int v = 0; v < 16; ++v)
-          rv[v] = __builtin_amdgcn_raw_buffer_load_b16(
-              rsR, (int)(ok(v) ? rb + (uint32_t)((v >> 2) * 8 + (v & 3)) * ldr2 : kOOB), 0, 0);
-      }
-      f32x16 la;
-      if (lora) {
+      for (int i = 0; i < FM; ++i) {
+        const int rl = wm * WM + i * 32;
+        if constexpr (VEC) {
+          const int q = lane & 15, kc = lane >> 4;
+          const int64_t row0 = m0 + rl + 2 * q, col = p0 + cl + 8 * kc;
+          const bool cok = col < p.P;
+          const bool ok0 = cok && row0 < mend, ok1 = cok && row0 + 1 < mend;
+          // this block's operands were issued one block ahead; issue the next one's
+          const EpiIn in = cur;
+          if (j * FM + i + 1 < FM * FN)
+            cur = fetch(swi, (j * FM + i + 1) % FM, (j * FM + i + 1) / FM);
+          const uint4 &r0 = in.a0, &r1 = in.a1, &g0 = in.a0, &g1 = in.a1, &u0 = in.b0,
+                      &u1 = in.b1;
+          f32x16 la;
+          if (lora) la = lora_term(rl, cl, coff);
+          // y = bf16(acc) (+ LoRA) into the staging area, two rows per dword
 #pragma unroll
-        for (int v = 0; v < 16; ++v) la[v] = 0.0f;
-        for (int kk = 0; kk < p.lora_k; kk += 2) {
-          int kx = kk + (lane >> 5);
-          float av = Ts[(rl + (lane & 31)) * tstride + coff + kx];
-          float bv = DGRAD ? Ls[kx * lstride + cl + (lane & 31)]
-                           : Ls[(cl + (lane & 31)) * lstride + kx];
-          la = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, la, 0, 0, 0);
+          for (int qq = 0; qq < 4; ++qq)
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+              float y2[2];
+#pragma unroll
+              for (int h = 0; h < 2; ++h) {
+                const int v = 4 * qq + 2 * t + h;
+                float y = st::bf16r(acc[i][j][v]);
+                if (lora) {
+                  if (DGRAD)
+                    y = st::bf16r(y + st::bf16r(la[v]));
+                  else
+                    y = st::bf16r(y + la[v] * p.lora_scale);
+                }
+                y2[h] = y;
+              }
+              const int pr = qq * 4 + (lane >> 5) * 2 + t;  // row pair
+              stg[pr * 36 + (lane & 31)] = st::pack_bf16x2(y2[0], y2[1]);
+            }
+          // the wave reads back only its own area: LDS accesses of one wave
+          // complete in order, the fence keeps the compiler from moving them
+          __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+          const uint4 lo4 = *(const uint4*)&stg[q * 36 + 8 * kc];
+          const uint4 hi4 = *(const uint4*)&stg[q * 36 + 8 * kc + 4];
+          // dword c of the pair holds (row 2q, row 2q+1) of column 8k + c
+          const uint32_t d[8] = {lo4.x, lo4.y, lo4.z, lo4.w, hi4.x, hi4.y, hi4.z, hi4.w};
+          uint32_t e0[4], e1[4];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            e0[c] = __builtin_amdgcn_perm(d[2 * c + 1], d[2 * c], 0x05040100u);
+            e1[c] = __builtin_amdgcn_perm(d[2 * c + 1], d[2 * c], 0x07060302u);
+          }
+          __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");  // before the next block's writes
+          const uint32_t cb = (uint32_t)((row0 * p.ldc + col) * 2);
+          auto emit = [&](const uint32_t (&e)[4], bool okr, uint32_t off, const uint4& rr,
+                          const uint4& gg, const uint4& uu) {
+            float yv[8];
+            const uint32_t ew[4] = {e[0], e[1], e[2], e[3]};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              yv[2 * c] = __uint_as_float(ew[c] << 16);
+              yv[2 * c + 1] = __uint_as_float(ew[c] & 0xffff0000u);
+            }
+            if constexpr (SWI) {
+              // SwiGLU VJP of dense.py:153 on the bf16 dX value (st::swiglu_vjp,
+              // as the standalone SwiGLU backward)
+              const uint32_t gw[4] = {gg.x, gg.y, gg.z, gg.w}, uw[4] = {uu.x, uu.y, uu.z, uu.w};
+              uint32_t og[4], ou[4];
+#pragma unroll
+              for (int c = 0; c < 4; ++c) {
+                float rg[2], ru[2];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                  const float gv = st::bf16_to_f32((uint16_t)(gw[c] >> (16 * h)));
+                  const float uv = st::bf16_to_f32((uint16_t)(uw[c] >> (16 * h)));
+                  st::swiglu_vjp(gv, uv, yv[2 * c + h], rg[h], ru[h]);
+                }
+                og[c] = st::pack_bf16x2(rg[0], rg[1]);
+                ou[c] = st::pack_bf16x2(ru[0], ru[1]);
+              }
+              const uint32_t uo = (uint32_t)p.swi_I * 2;
+              __builtin_amdgcn_raw_buffer_store_b128(
+                  st::u32x4{og[0], og[1], og[2], og[3]}, rsC, (int)(okr ? off : kOOB), 0, 0);
+              __builtin_amdgcn_raw_buffer_store_b128(
+                  st::u32x4{ou[0], ou[1], ou[2], ou[3]}, rsC, (int)(okr ? off + uo : kOOB), 0, 0);
+            } else {
+              uint32_t o[4];
+              if (p.R) {
+                const uint32_t rw[4] = {rr.x, rr.y, rr.z, rr.w};
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                  o[c] = st::pack_bf16x2(
+                      st::bf16_to_f32((uint16_t)rw[c]) + yv[2 * c],
+                      st::bf16_to_f32((uint16_t)(rw[c] >> 16)) + yv[2 * c + 1]);
+              } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) o[c] = ew[c];
+              }
+              __builtin_amdgcn_raw_buffer_store_b128(st::u32x4{o[0], o[1], o[2], o[3]}, rsC,
+                                                     (int)(okr ? off : kOOB), 0, 0);
+            }
+          };
+          emit(e0, ok0, cb, r0, g0, u0);
+          emit(e1, ok1, cb + ldc2, r1, g1, u1);
+        } else {
+          const int64_t pcol = p0 + cl + (lane & 31);
+          const bool colok = pcol < p.P;
+          const int64_t rbase = m0 + rl + (lane >> 5) * 4;  // row of v = 0
+          // element v sits at row rbase + dv(v), dv = (v/4)*8 + v%4
+          auto ok = [&](int v) { return colok && rbase + (v >> 2) * 8 + (v & 3) < mend; };
+          uint16_t rv[16];  // raw bf16: converted where used, after the LoRA products
+          if (p.R) {
+            const uint32_t rb = (uint32_t)((rbase * p.ldr + pcol) * 2);
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+              rv[v] = __builtin_amdgcn_raw_buffer_load_b16(
+                  rsR, (int)(ok(v) ? rb + (uint32_t)((v >> 2) * 8 + (v & 3)) * ldr2 : kOOB), 0,
+                  0);
+          }
+          f32x16 la;
+          if (lora) la = lora_term(rl, cl, coff);
+          const uint32_t cb = (uint32_t)((rbase * p.ldc + pcol) * 2);
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            float y = st::bf16r(acc[i][j][v]);
+            if (lora) {
+              if (DGRAD)
+                y = st::bf16r(y + st::bf16r(la[v]));
+              else
+                y = st::bf16r(y + la[v] * p.lora_scale);
+            }
+            if (p.R) y = st::bf16r(st::bf16_to_f32(rv[v]) + y);
+            __builtin_amdgcn_raw_buffer_store_b16(
+                st::f32_to_bf16(y), rsC,
+                (int)(ok(v) ? cb + (uint32_t)((v >> 2) * 8 + (v & 3)) * ldc2 : kOOB), 0, 0);
+          }
         }
-      }
-      const uint32_t cb = (uint32_t)((rbase * p.ldc + pcol) * 2);
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        float y = st::bf16r(acc[i][j][v]);
-        if (lora) {
-          if (DGRAD)
-            y = st::bf16r(y + st::bf16r(la[v]));
-          else
-            y = st::bf16r(y + la[v] * p.lora_scale);
-        }
-        if (p.R) y = st::bf16r(st::bf16_to_f32(rv[v]) + y);
-        __builtin_amdgcn_raw_buffer_store_b16(
-            st::f32_to_bf16(y), rsC,
-            (int)(ok(v) ? cb + (uint32_t)((v >> 2) * 8 + (v & 3)) * ldc2 : kOOB), 0, 0);
       }
     }
+  };
+  if constexpr (DGRAD) {
+    if (p.swi_gu) {  // the launcher only sets swi_gu with vec_epi
+      blocks(std::true_type{}, std::true_type{});
+      return;
+    }
   }
+  if (p.vec_epi)
+    blocks(std::false_type{}, std::true_type{});
+  else
+    blocks(std::false_type{}, std::false_type{});
 }
 
 template <int MODE, int BM, int BN, int WAVES, int WAVES_M>
@@ -808,12 +994,40 @@ __global__ __launch_bounds__(512) void gemm_ws_kernel(GemmParams p) {
                                                               tid, lane, wave < 4, Lg);
 }
 
+// Chooses the epilogue's access width (GemmParams::vec_epi): 16-byte rows
+// need C, the residual and gate|up 16-byte aligned with row strides, P and
+// the gate|up split multiples of 8, and `waves` staging areas after the LoRA
+// operands within the tile's `lds_dwords`.  ST_GEMM_VEC_EPI=0 keeps 2-byte
+// accesses where the epilogue has them (every case but the SwiGLU VJP).
+template <bool DGRAD, int BM, int BN>
+int choose_epilogue(GemmParams& p, int64_t lds_dwords, int waves) {
+  auto a16 = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
+  bool ok = p.P % 8 == 0 && p.ldc % 8 == 0 && a16(p.C) &&
+            epi_stage_offset<DGRAD, BM, BN>(p) + (int64_t)waves * EPI_STG <= lds_dwords;
+  if (p.R) ok = ok && p.ldr % 8 == 0 && a16(p.R);
+  if (p.swi_gu) {
+    ok = ok && p.swi_ld % 8 == 0 && p.swi_I % 8 == 0 && a16(p.swi_gu);
+    if (!ok)
+      return st::fail(ST_EUNSUPPORTED,
+                      "q4gemm: SwiGLU epilogue needs 16-byte aligned gate|up and output rows "
+                      "(strides and width multiples of 8) and LDS beside the LoRA operands");
+    p.vec_epi = 1;
+    return ST_OK;
+  }
+  const char* env = getenv("ST_GEMM_VEC_EPI");
+  p.vec_epi = (ok && !(env && atoi(env) == 0)) ? 1 : 0;
+  return ST_OK;
+}
+
 // The epilogue addresses C, the residual, T and the LoRA right operand with
 // 32-bit byte offsets.
 int check_epilogue_extents(const GemmParams& p) {
   const int64_t lim = 1ll << 31;
   bool ok = ((p.M - 1) * p.ldc + p.P) * 2 < lim;
   if (p.R) ok = ok && ((p.M - 1) * p.ldr + p.P) * 2 < lim;
+  if (p.swi_gu)
+    ok = ok && ((p.M - 1) * p.ldc + 2 * p.swi_I) * 2 < lim &&
+         ((p.M - 1) * p.swi_ld + 2 * p.swi_I) * 2 < lim;
   if (p.T) ok = ok && (p.M * p.ldt + p.lora_cols) * 4 < lim &&
                 (p.P + p.lora_k) * (p.ldl + 1) * 4 < lim;
   return ok ? ST_OK : st::fail(ST_EUNSUPPORTED, "q4gemm: output, residual or LoRA operand above 2 GiB");
@@ -832,7 +1046,10 @@ int launch_ws(const GemmParams& p, hipStream_t stream) {
                       p.lora_cols);
   }
   if (int rc = check_epilogue_extents(p)) return rc;
-  gemm_ws_kernel<MODE><<<(unsigned)tiles, 512, 0, stream>>>(p);
+  GemmParams q = p;
+  if (int rc = choose_epilogue<MODE == DGRAD_Q4, BM, BN>(q, (int64_t)WS_DA * BM * BK / 8 * 4, 4))
+    return rc;
+  gemm_ws_kernel<MODE><<<(unsigned)tiles, 512, 0, stream>>>(q);
   return st::check_launch("q4gemm");
 }
 
@@ -850,7 +1067,10 @@ int launch(const GemmParams& p, hipStream_t stream) {
                       p.lora_cols);
   }
   if (int rc = check_epilogue_extents(p)) return rc;
-  gemm_kernel<MODE, BM, BN, WAVES, WAVES_M><<<(unsigned)tiles, NT, 0, stream>>>(p);
+  using TL = Tile<MODE, BM, BN, WAVES, WAVES_M>;
+  GemmParams q = p;
+  if (int rc = choose_epilogue<TL::DGRAD, BM, BN>(q, (int64_t)TL::LDS_CHUNKS * 4, WAVES)) return rc;
+  gemm_kernel<MODE, BM, BN, WAVES, WAVES_M><<<(unsigned)tiles, NT, 0, stream>>>(q);
   return st::check_launch("q4gemm");
 }
 
@@ -1045,12 +1265,12 @@ extern "C" int st_q4_linear_fwd(const uint16_t* x, int64_t M, int64_t K, int64_t
   return run_gemm(FWD_BF16, p, s);
 }
 
-extern "C" int st_q4_linear_dgrad(const uint16_t* dy, int64_t M, int64_t N, int64_t lddy,
-                                  const uint8_t* payload, const float* scales, int64_t K,
-                                  const float* lut16, int32_t flags, const float* dt,
-                                  int64_t lddt, const float* lora_a, int32_t lora_k,
-                                  uint16_t* dx, int64_t lddx, void* workspace,
-                                  int64_t workspace_bytes, st_stream_t stream) {
+static int dgrad_impl(const uint16_t* dy, int64_t M, int64_t N, int64_t lddy,
+                      const uint8_t* payload, const float* scales, int64_t K, const float* lut16,
+                      int32_t flags, const float* dt, int64_t lddt, const float* lora_a,
+                      int32_t lora_k, uint16_t* dx, int64_t lddx, const uint16_t* gu,
+                      int64_t ldgu, void* workspace, int64_t workspace_bytes,
+                      st_stream_t stream) {
   ST_CHECK_ARG(M >= 0 && N > 0 && K > 0, "st_q4_linear_dgrad: bad shape");
   if (M == 0) return ST_OK;
   ST_CHECK_ARG(dy && payload && scales && dx && lut16, "st_q4_linear_dgrad: NULL pointer");
@@ -1058,10 +1278,14 @@ extern "C" int st_q4_linear_dgrad(const uint16_t* dy, int64_t M, int64_t N, int6
                (long long)N);
   ST_CHECK_ARG(K % 8 == 0, "st_q4_linear_dgrad: K must be a multiple of 8");
   ST_CHECK_ARG(lddy % 8 == 0 && lddy >= N && al16(dy), "st_q4_linear_dgrad: dy rows not 16-byte");
-  ST_CHECK_ARG(lddx >= K, "st_q4_linear_dgrad: lddx < K");
+  ST_CHECK_ARG(lddx >= (gu ? 2 * K : K), "st_q4_linear_dgrad: output row stride too small");
   GemmParams p{};
   p.A = dy; p.lda = lddy; p.M = M; p.P = K; p.Q = N;
   p.C = dx; p.ldc = lddx;
+  if (gu) {
+    ST_CHECK_ARG(ldgu >= 2 * K, "st_q4_linear_dgrad_swiglu: ldgu < 2 * K");
+    p.swi_gu = gu; p.swi_ld = ldgu; p.swi_I = K;
+  }
   p.hi_first = (flags & ST_FLAG_HI_NIBBLE_FIRST) ? 1 : 0;
   for (int i = 0; i < 16; ++i) p.lut.v[i] = lut16[i];
   if (dt) {
@@ -1094,6 +1318,28 @@ extern "C" int st_q4_linear_dgrad(const uint16_t* dy, int64_t M, int64_t N, int6
   return run_gemm(DGRAD_BF16, p, s);
 }
 
+extern "C" int st_q4_linear_dgrad(const uint16_t* dy, int64_t M, int64_t N, int64_t lddy,
+                                  const uint8_t* payload, const float* scales, int64_t K,
+                                  const float* lut16, int32_t flags, const float* dt,
+                                  int64_t lddt, const float* lora_a, int32_t lora_k,
+                                  uint16_t* dx, int64_t lddx, void* workspace,
+                                  int64_t workspace_bytes, st_stream_t stream) {
+  return dgrad_impl(dy, M, N, lddy, payload, scales, K, lut16, flags, dt, lddt, lora_a, lora_k,
+                    dx, lddx, nullptr, 0, workspace, workspace_bytes, stream);
+}
+
+extern "C" int st_q4_linear_dgrad_swiglu(const uint16_t* dy, int64_t M, int64_t N, int64_t lddy,
+                                         const uint8_t* payload, const float* scales, int64_t I,
+                                         const float* lut16, int32_t flags, const float* dt,
+                                         int64_t lddt, const float* lora_a, int32_t lora_k,
+                                         const uint16_t* gu, int64_t ldgu, uint16_t* dgu,
+                                         int64_t lddgu, void* workspace, int64_t workspace_bytes,
+                                         st_stream_t stream) {
+  ST_CHECK_ARG(gu != nullptr, "st_q4_linear_dgrad_swiglu: NULL gate|up");
+  return dgrad_impl(dy, M, N, lddy, payload, scales, I, lut16, flags, dt, lddt, lora_a, lora_k,
+                    dgu, lddgu, gu, ldgu, workspace, workspace_bytes, stream);
+}
+
 // ---------------------------------------------------------------- grouped (MoE)
 namespace {
 // tiles of a grouped launch: sum_g cdiv(rows_g, BM) <= cdiv(rows, BM) + groups
@@ -1111,7 +1357,10 @@ int launch_grouped(const GemmParams& p, hipStream_t stream) {
   int64_t tiles = (st::cdiv(p.M, BM) + p.ngroups) * st::cdiv(p.P, BN);
   if (tiles > 0x7fffffff) return st::fail(ST_EUNSUPPORTED, "q4 grouped: too many tiles");
   if (int rc = check_epilogue_extents(p)) return rc;
-  gemm_kernel<MODE, BM, BN, WAVES, 2><<<(unsigned)tiles, 64 * WAVES, 0, stream>>>(p);
+  using TL = Tile<MODE, BM, BN, WAVES, 2>;
+  GemmParams q = p;
+  if (int rc = choose_epilogue<TL::DGRAD, BM, BN>(q, (int64_t)TL::LDS_CHUNKS * 4, WAVES)) return rc;
+  gemm_kernel<MODE, BM, BN, WAVES, 2><<<(unsigned)tiles, 64 * WAVES, 0, stream>>>(q);
   return st::check_launch("q4 grouped gemm");
 }
 }  // namespace

@@ -102,12 +102,16 @@ def dense_block(hidden_states, position_embeddings, attention_mask, *, heads, kv
     gu = ops.concat_rows([wg, wu])
     loras_gu = [lora_gate, lora_up]
     inter = wg.out_features
+    wd = _weight(weights, "mlp.down_proj")
     if gu is not None and (all(l is None for l in loras_gu) or all(l is not None for l in loras_gu)):
-        act = ops.swiglu(ops.q4_lora_linear(xn2, gu, loras_gu), inter)
+        # down reads silu(gate) * up of the fused gate|up output; its input-
+        # gradient GEMM applies the SwiGLU VJP in the epilogue
+        out = ops.q4_lora_linear(ops.q4_lora_linear(xn2, gu, loras_gu), wd, [lora_down],
+                                 residual=h1, swiglu=True)
     else:
         act = ops.swiglu_pair(ops.q4_lora_linear(xn2, wg, [lora_gate]),
                               ops.q4_lora_linear(xn2, wu, [lora_up]))
-    out = ops.q4_lora_linear(act, _weight(weights, "mlp.down_proj"), [lora_down], residual=h1)
+        out = ops.q4_lora_linear(act, wd, [lora_down], residual=h1)
     return out.view(B, S, Hd)
 
 

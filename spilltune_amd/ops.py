@@ -209,7 +209,14 @@ def _stack_rows(ts):
 
 class _Q4LoRALinear(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, weight, residual, rank, scale, *ab):
+    def forward(ctx, x, weight, residual, rank, scale, swiglu_I, *ab):
+        gu = None
+        if swiglu_I:  # x is a fused gate|up pre-activation: the input is silu(gate) * up
+            gu = x
+            x = torch.empty((gu.shape[0], swiglu_I), dtype=_BF16, device=gu.device)
+            _lib.call("st_swiglu_fwd", _lib.ptr(gu), gu.stride(0), _lib.ptr(gu[:, swiglu_I:]),
+                      gu.stride(0), gu.shape[0], swiglu_I, _lib.ptr(x), swiglu_I,
+                      _lib.stream_handle(gu.device))
         M, K = x.shape
         N = weight.out_features
         dev = x.device
@@ -238,10 +245,11 @@ class _Q4LoRALinear(torch.autograd.Function):
         ctx.weight, ctx.rank, ctx.scale = weight, rank, scale
         ctx.has_residual = residual is not None
         ctx.nlora = len(ab)
+        ctx.swiglu_I = swiglu_I
         if ab:
-            ctx.save_for_backward(x, T, A_cat, B_cat)
+            ctx.save_for_backward(x, T, A_cat, B_cat, gu)
         else:
-            ctx.save_for_backward(x)
+            ctx.save_for_backward(x, gu)
         return y
 
     @staticmethod
@@ -256,7 +264,7 @@ class _Q4LoRALinear(torch.autograd.Function):
         dT = None
         A_cat = None
         if ctx.nlora:
-            x, T, A_cat, B_cat = ctx.saved_tensors
+            x, T, A_cat, B_cat, gu = ctx.saved_tensors
             nseg = len(weight.segments)
             dT = torch.empty((M, nseg * rank), dtype=_F32, device=dev)
             dB_all = torch.empty((N, rank), dtype=_F32, device=dev)
@@ -290,43 +298,59 @@ class _Q4LoRALinear(torch.autograd.Function):
             for s in range(nseg):
                 grads_ab += [dA_cat[s * rank:(s + 1) * rank], dBs[s]]
         else:
-            (x,) = ctx.saved_tensors
-        dx = torch.empty((M, K), dtype=_BF16, device=dev)
+            x, gu = ctx.saved_tensors
         need = _lib.query("st_q4_linear_dgrad_workspace_bytes", M, N, K)
         ws = _ws.get(dev, need)
-        _launch(("dgrad", M, N, K), lambda: _lib.call(
-            "st_q4_linear_dgrad", _lib.ptr(dy), M, N, N, _lib.ptr(weight.payload),
-            _lib.ptr(weight.scales), K, weight.lut(), weight.flags,
-            _lib.ptr(dT), 0 if dT is None else dT.stride(0), _lib.ptr(A_cat),
-            0 if dT is None else dT.shape[1], _lib.ptr(dx), K,
-            _lib.ptr(ws), 0 if ws is None else ws.numel(), stream))
+        lora_args = (_lib.ptr(dT), 0 if dT is None else dT.stride(0), _lib.ptr(A_cat),
+                     0 if dT is None else dT.shape[1])
+        if ctx.swiglu_I:
+            # the dgrad epilogue applies the SwiGLU VJP: the gradient of gate|up
+            dx = torch.empty_like(gu)
+            _launch(("dgrad", M, N, K), lambda: _lib.call(
+                "st_q4_linear_dgrad_swiglu", _lib.ptr(dy), M, N, N, _lib.ptr(weight.payload),
+                _lib.ptr(weight.scales), K, weight.lut(), weight.flags, *lora_args,
+                _lib.ptr(gu), gu.stride(0), _lib.ptr(dx), dx.stride(0),
+                _lib.ptr(ws), 0 if ws is None else ws.numel(), stream))
+        else:
+            dx = torch.empty((M, K), dtype=_BF16, device=dev)
+            _launch(("dgrad", M, N, K), lambda: _lib.call(
+                "st_q4_linear_dgrad", _lib.ptr(dy), M, N, N, _lib.ptr(weight.payload),
+                _lib.ptr(weight.scales), K, weight.lut(), weight.flags, *lora_args,
+                _lib.ptr(dx), K, _lib.ptr(ws), 0 if ws is None else ws.numel(), stream))
         dres = dy if ctx.has_residual else None
-        return (dx, None, dres, None, None, *grads_ab)
+        return (dx, None, dres, None, None, None, *grads_ab)
 
 
-def q4_lora_linear(x: torch.Tensor, weight: Q4Weight, loras=None, residual=None) -> torch.Tensor:
+def q4_lora_linear(x: torch.Tensor, weight: Q4Weight, loras=None, residual=None,
+                   swiglu: bool = False) -> torch.Tensor:
     """``bf16(bf16(x W^T) + s (x_f32 A^T) B^T)`` [``+ residual``] for a 2-D bf16 ``x``.
 
     ``loras`` holds one LoRA object (``A``, ``B``, ``rank``, ``scale``) per
-    segment of ``weight`` or is None."""
+    segment of ``weight`` or is None.  ``swiglu``: ``x`` is a fused gate|up
+    pre-activation ``[M, 2I]`` and the projection reads ``silu(gate) * up``
+    (dense.py:153); the backward applies the SwiGLU VJP inside the input-
+    gradient GEMM and returns the gradient of gate|up."""
     if x.dtype != _BF16 or x.dim() != 2:
         raise ValueError("q4_lora_linear expects a 2-D bf16 input")
-    if x.shape[1] != weight.in_features:
-        raise ValueError(f"input width {x.shape[1]} != weight in_features {weight.in_features}")
+    width = x.shape[1] // 2 if swiglu else x.shape[1]
+    if width != weight.in_features or (swiglu and x.shape[1] != 2 * width):
+        raise ValueError(f"input width {x.shape[1]} does not match weight in_features "
+                         f"{weight.in_features}{' (gate|up)' if swiglu else ''}")
     x = x.contiguous()
+    swiglu_I = width if swiglu else 0
     meta = _lora_meta(weight, loras)
     if residual is not None:
         residual = residual.contiguous()
         if residual.shape != (x.shape[0], weight.out_features) or residual.dtype != _BF16:
             raise ValueError("residual must be a bf16 [M, out_features] tensor")
     if meta is None:
-        return _Q4LoRALinear.apply(x, weight, residual, 0, 1.0)
+        return _Q4LoRALinear.apply(x, weight, residual, 0, 1.0, swiglu_I)
     rank, scale = meta
     ab = [t for l in loras for t in (l.A, l.B)]
     for l in loras:
         if l.A.dtype != _F32 or l.B.dtype != _F32:
             raise ValueError("LoRA A/B must be fp32")
-    return _Q4LoRALinear.apply(x, weight, residual, rank, scale, *ab)
+    return _Q4LoRALinear.apply(x, weight, residual, rank, scale, swiglu_I, *ab)
 
 
 # ----------------------------------------------------------------- RMSNorm

@@ -349,3 +349,33 @@ def test_lora_bwd_dy_matches_per_product(dev, widths, rank):
     # a segment start off the 8-element grid is refused by the query (callers fall back)
     bad = _lib.i64_array([100, N])
     assert _lib.query("st_lora_bwd_dy_workspace_bytes", M, N, rank, 2, bad) == 0
+
+
+@pytest.mark.parametrize("I,lora", [(512, True), (384, False), (688, True)])
+def test_swiglu_input_projection_matches_separate_ops(dev, oracle_codec, I, lora):
+    """q4_lora_linear(gate|up, W, swiglu=True) == q4_lora_linear(swiglu(gate|up), W):
+    the forward and every gradient bit for bit (the dgrad epilogue applies the
+    SwiGLU VJP with st_swiglu_bwd's roundings), on the 4-bit path and on the
+    bf16 fallback (I % 128 != 0)."""
+    g = torch.Generator().manual_seed(I)
+    M, H = 200, 256
+    w = (torch.randn(H, I, generator=g) * 0.02).numpy()
+    q, _ = q4_from_oracle(oracle_codec, w, "nf4-g128", dev)
+    gu0 = torch.randn(M, 2 * I, generator=g).to(BF).to(dev)
+    dy = torch.randn(M, H, generator=g).to(BF).to(dev)
+    A = torch.randn(8, I, generator=g) * 0.05
+    Bm = torch.randn(H, 8, generator=g) * 0.05
+    outs = []
+    for fused in (True, False):
+        gu = gu0.clone().requires_grad_(True)
+        lo = _L(A.to(dev).requires_grad_(True), Bm.to(dev).requires_grad_(True), 16.0) if lora else None
+        if fused:
+            y = ops.q4_lora_linear(gu, q, [lo] if lora else None, swiglu=True)
+        else:
+            y = ops.q4_lora_linear(ops.swiglu(gu, I), q, [lo] if lora else None)
+        y.backward(dy)
+        outs.append((y, gu.grad) + ((lo.A.grad, lo.B.grad) if lora else ()))
+    torch.cuda.synchronize()
+    for a, b in zip(*outs):
+        assert torch.equal(a.view(torch.int32) if a.dtype == torch.float32 else a.view(torch.int16),
+                           b.view(torch.int32) if b.dtype == torch.float32 else b.view(torch.int16))
