@@ -305,6 +305,39 @@ def test_q4_linear_tail_split_matches_single_launch(dev, oracle_codec, monkeypat
     _close_bf16(outs[0], (ref.to(BF).float() + res.float().cpu()).to(BF), "split fwd")
 
 
+@pytest.mark.parametrize("tile", ["128", "2562", "256"])
+@pytest.mark.parametrize("M,N,K", [(300, 512, 1024), (77, 200, 256), (64, 100, 256)])
+def test_vector_epilogue_matches_2byte_epilogue(dev, oracle_codec, monkeypatch, tile, M, N, K):
+    """The epilogue that stages each 32x32 block through LDS and moves 16-byte
+    rows gives the bits of the one that moves 2-byte elements: forward with
+    the LoRA term and a residual, dgrad with the LoRA term, ragged row tiles.
+    N = 100 (not a multiple of 8) takes the 2-byte path either way; its dgrad
+    is not run (the dgrad contraction must be a multiple of 8)."""
+    monkeypatch.setenv("ST_GEMM_TILE", tile)
+    g = torch.Generator().manual_seed(M + N + K)
+    w = (torch.randn(N, K, generator=g) * 0.02).numpy()
+    q, _ = q4_from_oracle(oracle_codec, w, "nf4-g128", dev)
+    x = torch.randn(M, K, generator=g).to(BF).to(dev)
+    res = torch.randn(M, N, generator=g).to(BF).to(dev)
+    dy = torch.randn(M, N, generator=g).to(BF).to(dev)
+    A = (torch.randn(8, K, generator=g) * 0.05).to(dev)
+    Bm = (torch.randn(N, 8, generator=g) * 0.05).to(dev)
+    outs = []
+    for vec in ("1", "0"):
+        monkeypatch.setenv("ST_GEMM_VEC_EPI", vec)
+        xd = x.clone().requires_grad_(True)
+        lo = _L(A.clone().requires_grad_(True), Bm.clone().requires_grad_(True), 16.0)
+        y = ops.q4_lora_linear(xd, q, [lo], residual=res)
+        if N % 8 == 0:
+            y.backward(dy)
+            outs.append((y, xd.grad))
+        else:
+            outs.append((y,))
+    torch.cuda.synchronize()
+    for a, b in zip(*outs):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
 @pytest.mark.parametrize("widths,rank", [((512, 128, 128), 16), ((1024, 1024), 8), ((384,), 40)])
 def test_lora_bwd_dy_matches_per_product(dev, widths, rank):
     """st_lora_bwd_dy (every segment's dT and dB in one launch) gives the bits of
