@@ -1019,6 +1019,13 @@ int choose_epilogue(GemmParams& p, int64_t lds_dwords, int waves) {
   return ST_OK;
 }
 
+// Row-tile slots of a launch: grouped launches (per-expert row ranges) take
+// sum_g cdiv(rows_g, BM) <= cdiv(rows, BM) + groups; slots past the last
+// group's tiles exit at once.
+int64_t row_tiles(const GemmParams& p, int BM) {
+  return st::cdiv(p.M, BM) + (p.goff ? p.ngroups : 0);
+}
+
 // The epilogue addresses C, the residual, T and the LoRA right operand with
 // 32-bit byte offsets.
 int check_epilogue_extents(const GemmParams& p) {
@@ -1036,7 +1043,7 @@ int check_epilogue_extents(const GemmParams& p) {
 template <int MODE>
 int launch_ws(const GemmParams& p, hipStream_t stream) {
   constexpr int BM = 256, BN = 128;
-  int64_t tiles = st::cdiv(p.M, BM) * st::cdiv(p.P, BN);
+  int64_t tiles = row_tiles(p, BM) * st::cdiv(p.P, BN);
   if (tiles > 0x7fffffff) return st::fail(ST_EUNSUPPORTED, "q4gemm: too many tiles");
   if (p.T) {
     const int64_t need = (int64_t)BM * (p.lora_cols + 1) +
@@ -1056,7 +1063,7 @@ int launch_ws(const GemmParams& p, hipStream_t stream) {
 template <int MODE, int BM, int BN, int WAVES, int WAVES_M = 2>
 int launch(const GemmParams& p, hipStream_t stream) {
   constexpr int NT = 64 * WAVES;
-  int64_t tiles = st::cdiv(p.M, BM) * st::cdiv(p.P, BN);
+  int64_t tiles = row_tiles(p, BM) * st::cdiv(p.P, BN);
   if (tiles > 0x7fffffff) return st::fail(ST_EUNSUPPORTED, "q4gemm: too many tiles");
   if (p.T) {  // the LoRA epilogue stages T and the right operand in the tile's LDS
     using TL = Tile<MODE, BM, BN, WAVES, WAVES_M>;
@@ -1342,26 +1349,17 @@ extern "C" int st_q4_linear_dgrad_swiglu(const uint16_t* dy, int64_t M, int64_t 
 
 // ---------------------------------------------------------------- grouped (MoE)
 namespace {
-// tiles of a grouped launch: sum_g cdiv(rows_g, BM) <= cdiv(rows, BM) + groups
+// Grouped (per-expert) launches take the dense kernels' tiles; ST_GROUPED_TILE
+// forces one (128, 2561, 2562, 256 = forward only).
 template <int MODE>
 int launch_grouped(const GemmParams& p, hipStream_t stream) {
-  constexpr int BM = 128, BN = 128, WAVES = 4;
-  if (p.T) {
-    using TL = Tile<MODE, BM, BN, WAVES, 2>;
-    int64_t need = (int64_t)BM * (p.lora_cols + 1) +
-                   (TL::DGRAD ? (int64_t)p.lora_k * BN : (int64_t)BN * (p.lora_k + 1));
-    if (need > (int64_t)TL::LDS_CHUNKS * 4)
-      return st::fail(ST_EUNSUPPORTED, "q4 grouped: LoRA epilogue (%d columns) exceeds tile LDS",
-                      p.lora_cols);
-  }
-  int64_t tiles = (st::cdiv(p.M, BM) + p.ngroups) * st::cdiv(p.P, BN);
-  if (tiles > 0x7fffffff) return st::fail(ST_EUNSUPPORTED, "q4 grouped: too many tiles");
-  if (int rc = check_epilogue_extents(p)) return rc;
-  using TL = Tile<MODE, BM, BN, WAVES, 2>;
-  GemmParams q = p;
-  if (int rc = choose_epilogue<TL::DGRAD, BM, BN>(q, (int64_t)TL::LDS_CHUNKS * 4, WAVES)) return rc;
-  gemm_kernel<MODE, BM, BN, WAVES, 2><<<(unsigned)tiles, 64 * WAVES, 0, stream>>>(q);
-  return st::check_launch("q4 grouped gemm");
+  const char* env = getenv("ST_GROUPED_TILE");
+  const int t = env ? atoi(env) : 128;
+  if (t == 2562) return launch_ws<MODE>(p, stream);
+  if (t == 2561) return launch<MODE, 256, 128, 8, 4>(p, stream);
+  if constexpr (MODE == FWD_Q4)
+    if (t == 256) return launch<MODE, 256, 256, 8>(p, stream);
+  return launch<MODE, 128, 128, 4>(p, stream);
 }
 }  // namespace
 
