@@ -5,6 +5,8 @@ round trip, corruption/format/shape rejection, explicit format selection)
 on a config-1-shaped tiny Llama checkpoint; runs without a GPU."""
 import hashlib
 import json
+import sys
+from pathlib import Path
 
 import pytest
 import torch
@@ -67,6 +69,31 @@ def test_identity_tracks_source_and_storage(tmp_path):
     d = archive.export_quantized(src2, tmp_path / "d", "llama", "nf4-g128")
     assert d["source_identity"] != a["source_identity"]
     assert d["storage_identity"] != a["storage_identity"]
+
+
+def test_identities_match_the_reference_loader(tmp_path):
+    """Source, storage and base identities of an int4-sym-g128 export equal the
+    ones the reference's own loader computed for the same synthetic checkpoint
+    (quantization/storage.py:89-165; tests/golden/archive_identity.json,
+    written by tests/golden/make_archive_identity.py), and reading the archive
+    back reproduces the base identity from the stored bytes."""
+    sys.path.insert(0, str(Path(__file__).resolve().parent / "golden"))
+    import make_archive_identity as gold
+
+    golden = json.loads(gold.FIXTURE.read_text())
+    report = gold.checkpoint(tmp_path / "src")
+    # the bound configuration the reader hashes is the exported text config
+    (tmp_path / "src" / "config.json").write_text(json.dumps(report["text_config"]))
+    info = archive.export_quantized(tmp_path / "src", tmp_path / "out", "llama", gold.MODE,
+                                    report=report)
+    assert info["source_identity"] == golden["source_identity"]
+    assert info["storage_identity"] == golden["storage_identity"]
+    assert info["stored_bytes"] == golden["stored_bytes"]
+    assert info["quantized_matrices"] == golden["quantized_tensors"]
+    reader = archive.ArchiveReader(tmp_path / "out", "llama", gold.MODE)
+    for key in report["required"]:
+        reader.read(key)
+    assert reader.finish() == golden["identity"]
 
 
 def test_image_loader_fills_the_packed_layout_in_any_order(exported):
