@@ -132,6 +132,27 @@ __device__ __forceinline__ void deq8(uint32_t w, const Tbl& T, uint32_t sh_e, ui
   o[3] = __builtin_amdgcn_perm(o57, e46, 0x07060302u);
 }
 
+// deq8 with the nibble order fixed at compile time: the codes are first put
+// in element order (e0..e3 | e4..e7), so each output word is one v_perm of a
+// low-byte and a high-byte lookup (29 VALU per 8 weights instead of 32).
+// Same table entries, so the same bf16 values as deq8.
+template <bool HI>
+__device__ __forceinline__ void deq8o(uint32_t w, const Tbl& T, uint32_t (&o)[4]) {
+  const uint32_t ne = (HI ? w >> 4 : w) & 0x0F0F0F0Fu;   // codes of elements 0,2,4,6
+  const uint32_t no = (HI ? w : w >> 4) & 0x0F0F0F0Fu;   // codes of elements 1,3,5,7
+  const uint32_t ca = __builtin_amdgcn_perm(no, ne, 0x05010400u);  // e0 e1 e2 e3
+  const uint32_t cb = __builtin_amdgcn_perm(no, ne, 0x07030602u);  // e4 e5 e6 e7
+  const uint32_t sa = 0x03020100u | ((ca >> 1) & 0x04040404u);
+  const uint32_t sb = 0x03020100u | ((cb >> 1) & 0x04040404u);
+  const uint32_t a7 = ca & 0x07070707u, b7 = cb & 0x07070707u;
+  const uint32_t la = sel4(T.lo, a7, sa), ha = sel4(T.hi, a7, sa);
+  const uint32_t lb = sel4(T.lo, b7, sb), hb = sel4(T.hi, b7, sb);
+  o[0] = __builtin_amdgcn_perm(ha, la, 0x05010400u);
+  o[1] = __builtin_amdgcn_perm(ha, la, 0x07030602u);
+  o[2] = __builtin_amdgcn_perm(hb, lb, 0x05010400u);
+  o[3] = __builtin_amdgcn_perm(hb, lb, 0x07030602u);
+}
+
 // WAVES = 4 or 8 (two waves per SIMD), arranged WAVES_M x (WAVES / WAVES_M)
 template <int MODE, int BM, int BN, int WAVES, int WAVES_M>
 struct Tile {
@@ -994,6 +1015,210 @@ __global__ __launch_bounds__(512) void gemm_ws_kernel(GemmParams p) {
                                                               tid, lane, wave < 4, Lg);
 }
 
+// Register-operand forward, 256x256 tile.  In the forward the MFMA B operand
+// of a lane is 8 consecutive contraction elements of one W row, i.e. one
+// packed 32-bit word, so W goes HBM/L2 -> VGPRs -> dequantised straight into
+// B operands with no LDS traffic at all; only A is staged in LDS.  Each wave
+// owns 32*FN output columns for all 256 rows (FN = 2: 4 waves, one per SIMD,
+// 256 accumulators each; FN = 1: 8 waves), so no two waves dequantise the
+// same W element.  Within a k-step of 64 the contraction index is permuted
+// alike for both operands: slice s, lane half h takes k = 32h + 8s .. +7, so
+// a lane's W for the whole k-step is one 16-byte load (32 codes, one scale)
+// and A chunk 4h + s.  Products are the same; only the order of the fp32
+// accumulation inside the k-step differs from the LDS-operand kernels.
+//  - A: RB_ST stages of 256 rows x 64 by buffer DMA (the swizzled whole-line
+//    layout of gemm_ws_kernel); tile kt+RB_ST is issued after the barrier of
+//    step kt into the stage tile kt has just released.
+//  - W: a ring of RB_ST register sets, also issued RB_ST tiles ahead.
+// One barrier per k-step, before the last slice: by then every wave has read
+// all of tile kt's fragments, and tile kt+1 has landed.  The k-loop is
+// unrolled by RB_ST (even), so ring slots and scale-group parity are static;
+// the launcher requires K % (RB_ST * 64) == 0.
+constexpr int RB_ST = 4;
+// Instruction order of one slice section (sched_group_barrier masks: 0x008
+// MFMA, 0x100 LDS read, 0x020 vector-memory read, 0x002 VALU): each MFMA is
+// followed by a share of the next slice's LDS reads and dequantisation, so
+// the fragment reads are issued early and the VALU co-issues with the MFMAs
+// of one wave.  VM adds the section's DMAs and W loads.
+#define RB_G(mask, n) __builtin_amdgcn_sched_group_barrier(mask, n, 0)
+template <int FN, bool VM>
+__device__ __forceinline__ void rb_order() {
+  static_assert(FN == 1 || FN == 2, "one or two B fragments per wave");
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    RB_G(0x008, 1);
+    if constexpr (VM) RB_G(0x020, 1);
+    RB_G(0x100, 1);
+    RB_G(0x002, FN == 2 ? 3 : 4);
+    if constexpr (FN == 2) {
+      RB_G(0x008, 1);
+      if constexpr (VM) RB_G(0x020, 1);
+      RB_G(0x002, 4);
+    }
+  }
+}
+#undef RB_G
+template <int FN, int WAVES, bool HI>
+__global__ __launch_bounds__(64 * WAVES) void gemm_rb_kernel(GemmParams p) {
+  constexpr int BM = 256, NT = 64 * WAVES, WN = 32 * FN, BN = WN * WAVES;
+  constexpr int FM = 8, WM = 256;
+  constexpr int A_ST = BM * BK / 8;       // 16-byte units per A stage
+  constexpr int DMA_W = BM / 8 / WAVES;   // DMAs (8 rows each) per wave per stage
+  constexpr int NSTEP = DMA_W + 2 * FN;   // vector-memory operations issued per step
+  __shared__ uint4 ldsA[RB_ST * A_ST];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t tiles_p = st::cdiv(p.P, BN);
+  const int64_t t = st::xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t p0 = (t % tiles_p) * BN;
+  const int64_t m0 = (t / tiles_p) * BM, mend = p.M;
+  const int KT = (int)(p.Q / BK);
+  const auto rsA = make_rsrc(p.A, p.a_bytes);
+  const auto rsW = make_rsrc(p.Wq, p.w_bytes);
+  const auto rsS = make_rsrc(p.Ws, p.s_bytes);
+
+  // A DMA: wave w moves rows 8*(w*DMA_W + q) + lane/8 of each stage; lane l
+  // fills position l%8 of its row, i.e. chunk (l%8) ^ ((row>>1) & 7).  Rows
+  // beyond M start at kOOB and stay out of range; tiles past the last one
+  // (K % 64 == 0) read rows' later bytes or zeros and are never used.
+  uint32_t a_row[DMA_W];
+#pragma unroll
+  for (int q = 0; q < DMA_W; ++q) {
+    const int row = 8 * (wave * DMA_W + q) + (lane >> 3);
+    const int c = (lane & 7) ^ ((row >> 1) & 7);
+    a_row[q] = m0 + row < mend ? (uint32_t)(((m0 + row) * p.lda + c * 8) * 2) : kOOB;
+  }
+  auto dma_A = [&](int kt) {
+    uint4* st_base = ldsA + (kt % RB_ST) * A_ST;
+#pragma unroll
+    for (int q = 0; q < DMA_W; ++q) {
+      const uint32_t off = a_row[q] + (uint32_t)(kt * BK * 2);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rsA, (__attribute__((address_space(3))) void*)(st_base + (wave * DMA_W + q) * 64), 16,
+          off, 0, 0, 0);
+    }
+  };
+
+  // W: column n_j = p0 + wave*WN + 32j + lane%32, contraction half h = lane/32.
+  // K (= ldw) is a multiple of 128: k-step kt adds 32 payload bytes, scale
+  // group kt/2.  Loads past the end of W read zeros or W's own bytes (unused).
+  const int h = lane >> 5;
+  uint32_t w_po[FN], w_so[FN];
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int64_t n = p0 + wave * WN + 32 * j + (lane & 31);
+    w_po[j] = n < p.P ? (uint32_t)((n * p.ldw + 32 * h) >> 1) : kOOB;
+    w_so[j] = n < p.P ? (uint32_t)((n * p.ldw) >> 7) * 4 : kOOB;
+  }
+  struct WR {
+    uint4 q[FN];
+    float s[FN];
+  };
+  auto load_W = [&](int kt, WR& w) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      w.q[j] = ld16(rsW, w_po[j] + (uint32_t)(kt * (BK / 2)));
+      w.s[j] = __builtin_bit_cast(float, ld4(rsS, w_so[j] + (uint32_t)(kt >> 1) * 4));
+    }
+  };
+  Tbl tbl[FN];
+  auto make_tbls = [&](const WR& w) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j) tbl[j] = make_tbl(p.lut, w.s[j]);
+  };
+  auto deq_B = [&](const WR& w, int s, bf16x8 (&b)[FN]) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const uint32_t word = s == 0 ? w.q[j].x : s == 1 ? w.q[j].y : s == 2 ? w.q[j].z : w.q[j].w;
+      uint32_t o[4];
+      deq8o<HI>(word, tbl[j], o);
+      b[j] = __builtin_bit_cast(bf16x8, make_uint4(o[0], o[1], o[2], o[3]));
+    }
+  };
+  // A fragment i of slice s: row 32i + lane%32, chunk 4h + s at its swizzled
+  // position (bits 1-3 of the row come from lane%32 alone)
+  const int a_lane = (lane & 31) * 8, a_f = ((lane & 31) >> 1) & 7;
+  auto read_A = [&](int kt, int s, bf16x8 (&a)[FM]) {
+    const uint4* ap = ldsA + (kt % RB_ST) * A_ST + a_lane + ((4 * h + s) ^ a_f);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) a[i] = __builtin_bit_cast(bf16x8, ap[i * 32 * 8]);
+  };
+
+  f32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+  auto mfmas = [&](const bf16x8 (&a)[FM], const bf16x8 (&b)[FN]) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+  };
+
+  WR wr[RB_ST];
+  bf16x8 fa0[FM], fb0[FN], fa1[FM], fb1[FN];
+  // prologue: tiles 0..RB_ST-1 issued, tile 0 landed everywhere
+#pragma unroll
+  for (int j = 0; j < RB_ST; ++j) {
+    dma_A(j);
+    load_W(j, wr[j]);
+  }
+  wait_cnt<NSTEP * (RB_ST - 1)>();
+  bar();
+  make_tbls(wr[0]);
+  read_A(0, 0, fa0);
+  deq_B(wr[0], 0, fb0);
+
+  // step kt, W of tile kt in wr[u] (u = kt % RB_ST): slices 0-2 with the next
+  // slice's operands read ahead; then wait for tile kt+1 (issued RB_ST-1
+  // steps ago; the NSTEP operations of each of the RB_ST-2 later steps may
+  // stay in flight) and for this wave's fragment reads, barrier, refill the
+  // released stage and W set with tile kt+RB_ST, and read slice 0 of tile
+  // kt+1 under slice 3's MFMAs.
+  auto step = [&](int kt, int u) {
+    read_A(kt, 1, fa1);
+    deq_B(wr[u], 1, fb1);
+    mfmas(fa0, fb0);
+    rb_order<FN, false>();
+    __builtin_amdgcn_sched_barrier(0);
+    read_A(kt, 2, fa0);
+    deq_B(wr[u], 2, fb0);
+    mfmas(fa1, fb1);
+    rb_order<FN, false>();
+    __builtin_amdgcn_sched_barrier(0);
+    read_A(kt, 3, fa1);
+    deq_B(wr[u], 3, fb1);
+    mfmas(fa0, fb0);
+    rb_order<FN, false>();
+    __builtin_amdgcn_sched_barrier(0);
+    wait_cnt<NSTEP * (RB_ST - 2), 0>();
+    bar();
+    dma_A(kt + RB_ST);
+    load_W(kt + RB_ST, wr[u]);
+    const int un = (u + 1) % RB_ST;
+    if ((u & 1) == 1) make_tbls(wr[un]);  // tile kt+1 starts a scale group
+    read_A(kt + 1, 0, fa0);
+    deq_B(wr[un], 0, fb0);
+    mfmas(fa1, fb1);
+    rb_order<FN, true>();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  for (int kt = 0; kt < KT; kt += RB_ST) {
+#pragma unroll
+    for (int v = 0; v < RB_ST; ++v) step(kt + v, v);
+  }
+  // the DMAs of tiles past the end must land before the epilogue reuses LDS
+  wait_cnt<0>();
+  __syncthreads();
+  gemm_epilogue<false, BM, BN, NT, FM, FN, WM, WN>(p, acc, ldsA, m0, mend, p0, 0, wave, tid, lane,
+                                                   true, p.L);
+}
+
 // Chooses the epilogue's access width (GemmParams::vec_epi): 16-byte rows
 // need C, the residual and gate|up 16-byte aligned with row strides, P and
 // the gate|up split multiples of 8, and `waves` staging areas after the LoRA
@@ -1060,6 +1285,28 @@ int launch_ws(const GemmParams& p, hipStream_t stream) {
   return st::check_launch("q4gemm");
 }
 
+template <int FN, int WAVES>
+int launch_rb(const GemmParams& p, hipStream_t stream) {
+  constexpr int BM = 256, BN = 32 * FN * WAVES, NT = 64 * WAVES;
+  constexpr int64_t lds_dwords = (int64_t)RB_ST * BM * BK / 8 * 4;
+  const int64_t tiles = st::cdiv(p.M, BM) * st::cdiv(p.P, BN);
+  if (tiles > 0x7fffffff) return st::fail(ST_EUNSUPPORTED, "q4gemm: too many tiles");
+  if (p.Q % (RB_ST * BK) || p.goff || p.gather)
+    return st::fail(ST_EUNSUPPORTED, "q4gemm: register-operand tile needs K %% %d == 0, dense rows",
+                    RB_ST * BK);
+  if (p.T && (int64_t)BM * (p.lora_cols + 1) + (int64_t)BN * (p.lora_k + 1) > lds_dwords)
+    return st::fail(ST_EUNSUPPORTED, "q4gemm: LoRA epilogue (%d columns) exceeds tile LDS",
+                    p.lora_cols);
+  if (int rc = check_epilogue_extents(p)) return rc;
+  GemmParams q = p;
+  if (int rc = choose_epilogue<false, BM, BN>(q, lds_dwords, NT / 64)) return rc;
+  if (q.hi_first)
+    gemm_rb_kernel<FN, WAVES, true><<<(unsigned)tiles, NT, 0, stream>>>(q);
+  else
+    gemm_rb_kernel<FN, WAVES, false><<<(unsigned)tiles, NT, 0, stream>>>(q);
+  return st::check_launch("q4gemm");
+}
+
 template <int MODE, int BM, int BN, int WAVES, int WAVES_M = 2>
 int launch(const GemmParams& p, hipStream_t stream) {
   constexpr int NT = 64 * WAVES;
@@ -1083,9 +1330,12 @@ int launch(const GemmParams& p, hipStream_t stream) {
 
 // 256-row tiles halve the dequant work per MFMA against 128-row ones but need
 // enough tiles to cover the 256 CUs.  Forward with >= 192 tiles of 256x256:
-// the 256x256 8-wave kernel; otherwise the warp-specialised 256x128 kernel
-// (2562) where it yields >= 192 tiles; else 128x128 (4 waves).  ST_GEMM_TILE
-// forces one (128, 256, 2561 = 256x128 8 waves, 2562, 2564 = 256x256 4 waves).
+// the 256x256 register-operand kernel (the LDS-operand 8-wave kernel with
+// ST_GEMM_RB=0); otherwise the warp-specialised 256x128 kernel (2562) where it
+// yields >= 192 tiles; else 128x128 (4 waves).  ST_GEMM_TILE forces one (128,
+// 256, 2561 = 256x128 8 waves, 2562, 2564 = 256x256 4 waves; forward only:
+// register-operand 2565 = 256x256 4 waves, 2566 = 256x256 8 waves, 2567 =
+// 256x128 4 waves).
 int tile_choice(int mode, int64_t M, int64_t P) {
   const char* env = getenv("ST_GEMM_TILE");
   if (env) return atoi(env);
@@ -1161,16 +1411,32 @@ int dispatch(const GemmParams& p, hipStream_t stream) {
   if constexpr (MODE == FWD_Q4 || MODE == DGRAD_Q4) {
     const int t = tile_choice(MODE, p.M, p.P);
     if constexpr (MODE == FWD_Q4) {
+      // 256x256 forward: register-operand kernel (8 waves) unless
+      // ST_GEMM_RB=0; its column tail runs on the register-operand 256x128
+      // tile, which sums each output in the same order, so a split stays
+      // bit-identical to one launch
+      const char* rbe = getenv("ST_GEMM_RB");
+      const bool rb = (!rbe || atoi(rbe)) && p.Q % (RB_ST * BK) == 0;
       if (const int64_t c1 = split_column(t, p.M, p.P)) {
-        const int rc = launch<MODE, 256, 256, 8>(column_slice(p, 0, c1), stream);
-        return rc ? rc : launch_ws<MODE>(column_slice(p, c1, p.P), stream);
+        const GemmParams head = column_slice(p, 0, c1), tail = column_slice(p, c1, p.P);
+        if (rb) {
+          const int rc = launch_rb<1, 8>(head, stream);
+          return rc ? rc : launch_rb<1, 4>(tail, stream);
+        }
+        const int rc = launch<MODE, 256, 256, 8>(head, stream);
+        return rc ? rc : launch_ws<MODE>(tail, stream);
       }
+      if (t == 256 && rb) return launch_rb<1, 8>(p, stream);
     }
     if (t == 256) return launch<MODE, 256, 256, 8>(p, stream);
     if (t == 2561) return launch<MODE, 256, 128, 8, 4>(p, stream);
     if (t == 2562) return launch_ws<MODE>(p, stream);
-    if constexpr (MODE == FWD_Q4)
+    if constexpr (MODE == FWD_Q4) {
       if (t == 2564) return launch<MODE, 256, 256, 4>(p, stream);
+      if (t == 2565 && p.Q % (RB_ST * BK) == 0) return launch_rb<2, 4>(p, stream);
+      if (t == 2566 && p.Q % (RB_ST * BK) == 0) return launch_rb<1, 8>(p, stream);
+      if (t == 2567 && p.Q % (RB_ST * BK) == 0) return launch_rb<1, 4>(p, stream);
+    }
   }
   return launch<MODE, 128, 128, 4>(p, stream);
 }

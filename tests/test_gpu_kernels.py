@@ -135,7 +135,7 @@ def _close_bf16(got, ref, what):
 SHAPES = [(64, 256, 256), (100, 384, 512), (37, 96, 688), (300, 512, 1024), (1, 128, 128)]
 
 
-@pytest.mark.parametrize("tile", ["128", "2561", "2562", "256"])
+@pytest.mark.parametrize("tile", ["128", "2561", "2562", "256", "2565", "2566", "2567"])
 @pytest.mark.parametrize("fmt", ["nf4-g128", "int4-sym-g128"])
 @pytest.mark.parametrize("M,N,K", SHAPES)
 @pytest.mark.parametrize("lora,residual", [(False, False), (True, False), (True, True)])
@@ -272,13 +272,17 @@ def test_q4_linear_full_size_vs_torch_fp32(dev):
     _close_bf16(xg.grad, ref_dx, "full-size gate|up dgrad")
 
 
+@pytest.mark.parametrize("rb", ["1", "0"])
 @pytest.mark.parametrize("segments", [(16384, 33024), (32896, 33024)])
-def test_q4_linear_tail_split_matches_single_launch(dev, oracle_codec, monkeypatch, segments):
+def test_q4_linear_tail_split_matches_single_launch(dev, oracle_codec, monkeypatch, segments, rb):
     """Shapes whose last round of tiles would leave CUs idle run as two
-    launches over column ranges (256x256 tiles, then 256x128 ones).  Every
-    output element keeps its reduction order, so the split result equals the
-    single launch bit for bit, LoRA segments (one ending before the split
-    column, one straddling it) and residual included."""
+    launches over column ranges (256x256 tiles, then 256x128 ones: the
+    register-operand pair by default, ST_GEMM_RB=0 the LDS-operand kernel and
+    the warp-specialised one).  Every output element keeps its reduction
+    order, so the split result equals the single launch bit for bit, LoRA
+    segments (one ending before the split column, one straddling it) and
+    residual included."""
+    monkeypatch.setenv("ST_GEMM_RB", rb)
     g = torch.Generator().manual_seed(77)
     M, K = 512, 256
     N = segments[-1]
