@@ -1064,7 +1064,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_rb_kernel(GemmParams p) {
   constexpr int FM = 8, WM = 256;
   constexpr int A_ST = BM * BK / 8;       // 16-byte units per A stage
   constexpr int DMA_W = BM / 8 / WAVES;   // DMAs (8 rows each) per wave per stage
-  constexpr int NSTEP = DMA_W + 2 * FN;   // vector-memory operations issued per step
+  // vector-memory operations issued per step: the DMAs, FN W loads, and FN
+  // scale loads for a tile that starts a scale group (even tiles); two
+  // consecutive steps issue RB_PAIR of them
+  constexpr int RB_PAIR = 2 * DMA_W + 3 * FN;
   __shared__ uint4 ldsA[RB_ST * A_ST];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1115,11 +1118,13 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_rb_kernel(GemmParams p) {
     uint4 q[FN];
     float s[FN];
   };
-  auto load_W = [&](int kt, WR& w) {
+  // the scale of a group is loaded with its first (even) tile only
+  auto load_W = [&](int kt, WR& w, bool group_start) {
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
       w.q[j] = ld16(rsW, w_po[j] + (uint32_t)(kt * (BK / 2)));
-      w.s[j] = __builtin_bit_cast(float, ld4(rsS, w_so[j] + (uint32_t)(kt >> 1) * 4));
+      if (group_start)
+        w.s[j] = __builtin_bit_cast(float, ld4(rsS, w_so[j] + (uint32_t)(kt >> 1) * 4));
     }
   };
   Tbl tbl[FN];
@@ -1166,9 +1171,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_rb_kernel(GemmParams p) {
 #pragma unroll
   for (int j = 0; j < RB_ST; ++j) {
     dma_A(j);
-    load_W(j, wr[j]);
+    load_W(j, wr[j], (j & 1) == 0);
   }
-  wait_cnt<NSTEP * (RB_ST - 1)>();
+  static_assert(RB_ST == 4, "the waits below count two step pairs");
+  wait_cnt<RB_PAIR + DMA_W + FN>();  // tiles 1-3 may be in flight
   bar();
   make_tbls(wr[0]);
   read_A(0, 0, fa0);
@@ -1176,8 +1182,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_rb_kernel(GemmParams p) {
 
   // step kt, W of tile kt in wr[u] (u = kt % RB_ST): slices 0-2 with the next
   // slice's operands read ahead; then wait for tile kt+1 (issued RB_ST-1
-  // steps ago; the NSTEP operations of each of the RB_ST-2 later steps may
-  // stay in flight) and for this wave's fragment reads, barrier, refill the
+  // steps ago; the operations of the RB_ST-2 = 2 later steps, one of each
+  // parity, may stay in flight) and for this wave's fragment reads, barrier, refill the
   // released stage and W set with tile kt+RB_ST, and read slice 0 of tile
   // kt+1 under slice 3's MFMAs.
   auto step = [&](int kt, int u) {
@@ -1196,10 +1202,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_rb_kernel(GemmParams p) {
     mfmas(fa0, fb0);
     rb_order<FN, false>();
     __builtin_amdgcn_sched_barrier(0);
-    wait_cnt<NSTEP * (RB_ST - 2), 0>();
+    wait_cnt<RB_PAIR, 0>();
     bar();
     dma_A(kt + RB_ST);
-    load_W(kt + RB_ST, wr[u]);
+    load_W(kt + RB_ST, wr[u], (u & 1) == 0);
     const int un = (u + 1) % RB_ST;
     if ((u & 1) == 1) make_tbls(wr[un]);  // tile kt+1 starts a scale group
     read_A(kt + 1, 0, fa0);
