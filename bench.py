@@ -273,6 +273,116 @@ def qwen3_stream_bench(args):
     print(json.dumps(result), flush=True)
 
 
+def memory_bench(args):
+    """HBM-bound kernels of the config-2 layer at their real shapes: the
+    standalone 4-bit dequant of all seven matrices (st_dequant4) and the LoRA
+    rank-r products of the layer step (st_lora_gemm for T = x A^T and
+    dA = dT^T x, st_lora_bwd_dy for dT and dB), each timed with HIP events on
+    its launch stream over repeated calls.  Bytes are algorithmic: every
+    operand read once and every result written once."""
+    import torch
+    from spilltune_amd import _lib, codecs, ops
+    c = CONFIGS["llama8b"]
+    dev = torch.device("cuda:0")
+    stream = _lib.stream_handle(dev)
+    M, r = c["B"] * c["S"], c["r"]
+    g = torch.Generator().manual_seed(1234)
+    shapes = layer_shapes(c)
+    lut = _lib.lut_array(codecs.NF4_CODEBOOK)
+    reps = max(args.steps, 20)
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        ev0.record()
+        for _ in range(reps):
+            fn()
+        ev1.record()
+        torch.cuda.synchronize()
+        return ev0.elapsed_time(ev1) / reps  # ms
+
+    kernels = []
+
+    def report(name, nbytes, ms):
+        gbps = nbytes / (ms * 1e-3) / 1e9
+        kernels.append({"kernel": name, "bytes": int(nbytes), "ms": round(ms, 4),
+                        "gbps": round(gbps, 1), "frac": round(gbps / PEAK_HBM_GBPS, 4)})
+        log(f"  {name}: {nbytes / 1e6:.1f} MB in {ms * 1e3:.1f} us, {gbps:.0f} GB/s "
+            f"({100 * gbps / PEAK_HBM_GBPS:.1f}% of {PEAK_HBM_GBPS:.0f})")
+
+    # ---- standalone dequant of the whole layer (codecs.py:158-170 as one kernel per matrix)
+    parts = []
+    for name, (n, k) in shapes.items():
+        numel = n * k
+        pay = torch.randint(0, 256, (numel // 2,), dtype=torch.uint8, generator=g).to(dev)
+        sc = (torch.rand(numel // 128, generator=g) * 0.02 + 0.01).to(dev)
+        out = torch.empty(numel, dtype=torch.bfloat16, device=dev)
+        parts.append((pay, sc, numel, out))
+
+    def dequant_layer():
+        for pay, sc, numel, out in parts:
+            _lib.call("st_dequant4", _lib.ptr(pay), _lib.ptr(sc), numel, 128, lut, 0,
+                      _lib.ptr(out), stream)
+    P = sum(n * k for n, k in shapes.values())
+    report("st_dequant4 (7 matrices, nf4-g128 -> bf16)", P // 2 + P // 128 * 4 + 2 * P,
+           timed(dequant_layer))
+    dq_gbps = kernels[-1]["gbps"]
+    del parts
+
+    # ---- LoRA products at the layer's fused-projection shapes
+    groups = {"q|k|v": (("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj"), 4096),
+              "o": (("self_attn.o_proj",), 4096), "gate|up": (("mlp.gate_proj", "mlp.up_proj"), 4096),
+              "down": (("mlp.down_proj",), c["I"])}
+    for gname, (names, K) in groups.items():
+        widths = [shapes[n][0] for n in names]
+        N, R = sum(widths), r * len(names)
+        x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
+        dy = torch.randn(M, N, generator=g).to(torch.bfloat16).to(dev)
+        A_cat = (torch.randn(R, K, generator=g) * 0.02).to(dev)
+        B_cat = (torch.randn(N, r, generator=g) * 0.02).to(dev)
+        T = torch.empty(M, R, dtype=torch.float32, device=dev)
+        dT = torch.empty(M, R, dtype=torch.float32, device=dev)
+        dB = torch.empty(N, r, dtype=torch.float32, device=dev)
+        dA = torch.empty(R, K, dtype=torch.float32, device=dev)
+        report(f"LoRA T = x A^T ({gname}: {M}x{K} . {R}x{K})", M * K * 2 + R * K * 4 + M * R * 4,
+               timed(lambda: ops.lora_gemm(M, R, K, x, K, 1, A_cat, 1, K, 1.0, T)))
+        ends = _lib.i64_array(torch.tensor(widths).cumsum(0).tolist())
+        need = _lib.query("st_lora_bwd_dy_workspace_bytes", M, N, r, len(names), ends)
+        ws = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
+        report(f"LoRA dT, dB (st_lora_bwd_dy, {gname}: dY {M}x{N})",
+               M * N * 2 + M * R * 4 * 2 + N * r * 4 * 2,
+               timed(lambda: _lib.call("st_lora_bwd_dy", _lib.ptr(dy), M, N, N, _lib.ptr(B_cat),
+                                       _lib.ptr(T), R, r, len(names), ends, 2.0, _lib.ptr(dT), R,
+                                       _lib.ptr(dB), _lib.ptr(ws), ws.numel(), stream)))
+        report(f"LoRA dA = dT^T x ({gname}: {R}x{M} . {M}x{K})", M * K * 2 + M * R * 4 + R * K * 4,
+               timed(lambda: ops.lora_gemm(R, K, M, dT, 1, R, x, K, 1, 1.0, dA)))
+    lora = [k for k in kernels if k["kernel"].startswith("LoRA")]
+    lbytes = sum(k["bytes"] for k in lora)
+    lms = sum(k["ms"] for k in lora)
+    log(f"  LoRA products of one layer pass set: {lbytes / 1e6:.1f} MB in {lms * 1e3:.1f} us, "
+        f"{lbytes / (lms * 1e-3) / 1e9:.0f} GB/s")
+    result = {
+        "metric": "HBM GB/s of the memory-bound kernels (standalone nf4-g128 dequant of one "
+                  "Llama-3-8B layer; LoRA rank-r products at the layer's shapes)",
+        "value": dq_gbps, "unit": "GB/s", "n_gpus": 1, "steps": reps, "warmup": 3,
+        "ms_per_step": kernels[0]["ms"], "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "u8->bf16 / bf16 x fp32",
+        "data": "synthetic (random nf4-g128 codes and scales; N(0,1) activations, N(0,0.02) adapters)",
+        "config": {"workload": f"memory: dequant of the {P} weights of one Llama-3-8B layer; LoRA "
+                               f"r={r} products at {M} tokens", "parallelism": "single GPU"},
+        "kernels": kernels,
+        "lora_total": {"bytes": lbytes, "ms": round(lms, 4),
+                       "gbps": round(lbytes / (lms * 1e-3) / 1e9, 1)},
+        "roofline": {"bound": "hbm", "kernel": "st_dequant4", "achieved": dq_gbps,
+                     "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                     "frac": round(dq_gbps / PEAK_HBM_GBPS, 4), "traffic": None},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(result), flush=True)
+
+
 def moe_bench(args):
     """Config 4: the MoE feed-forward forward + backward on 4096 tokens
     (router, permutation, grouped 4-bit gate|up and down GEMMs with per-expert
@@ -401,7 +511,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="llama8b",
-                    choices=sorted(CONFIGS) + ["moe", "qwen3-stream"])
+                    choices=sorted(CONFIGS) + ["moe", "qwen3-stream", "memory"])
     ap.add_argument("--cpu-tokens", type=int, default=2048)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -430,6 +540,9 @@ def main():
         return
     if args.config == "qwen3-stream":
         qwen3_stream_bench(args)
+        return
+    if args.config == "memory":
+        memory_bench(args)
         return
     from spilltune_amd import ops, slots
     from spilltune_amd.dense import CausalMask

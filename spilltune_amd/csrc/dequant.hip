@@ -4,15 +4,51 @@
 // the NF4 decode inside bitsandbytes (nf4_backend.py:312).  One fp32 multiply
 // then RNE to bf16 per element: bit-identical to codecs.py:168-170.
 //
-// Layout: each thread owns 16 payload bytes = 32 consecutive elements (they lie
-// in one group for group 64/128), reads one scale, looks the codes up in a
-// 16-entry fp32 codebook held in LDS, and writes 64 bytes of bf16 with four
-// 16-byte stores.  Per element: 0.5 B read + 2 B written (+4/group B scale).
+// Default kernel (dequant4_word): one packed word = 8 consecutive elements per
+// lane per step (a word never straddles a group of 64/128), decoded through
+// the per-scale v_perm table of decode4.h and written as one 16-byte store, so
+// each store instruction of a wave writes 1 KiB of whole cache lines.  The
+// earlier form (dequant4_vec: 16 payload bytes per lane, codebook in LDS, four
+// 16-byte stores 64 bytes apart) stays behind ST_DEQUANT_KERNEL=0.
+// Per element: 0.5 B read + 2 B written (+4/group B scale).
 #include "common.h"
+#include "decode4.h"
 
 namespace {
 
 constexpr int kThreads = 256;
+
+// Register-table form, one packed word (8 codes) per lane per step: every
+// 4-byte load instruction of a wave reads 256 contiguous bytes and every
+// 16-byte store writes 1 KiB in one piece (whole cache lines, where the
+// 64-byte-per-lane form leaves each store instruction 16 bytes per 64).
+// Each lane builds the v_perm table of its word's scale (decode4.h): the
+// same bf16_rne(codebook[c] * s) as the reference.  A workgroup covers
+// RW consecutive words per lane (4 KiB of payload per 256 threads at RW=4).
+constexpr int RW = 4;
+template <bool HI>
+__global__ __launch_bounds__(kThreads) void dequant4_word(const uint32_t* __restrict__ payload,
+                                                         const float* __restrict__ scales,
+                                                         int64_t nwords, int group_shift,
+                                                         Lut16 lut, uint4* __restrict__ out) {
+  const int64_t w0 = (int64_t)blockIdx.x * (RW * kThreads) + threadIdx.x;
+  uint32_t p[RW];
+  float s[RW];
+#pragma unroll
+  for (int j = 0; j < RW; ++j) {
+    const int64_t w = w0 + j * kThreads;
+    p[j] = w < nwords ? payload[w] : 0u;
+    s[j] = w < nwords ? scales[(w * 8) >> group_shift] : 0.0f;
+  }
+#pragma unroll
+  for (int j = 0; j < RW; ++j) {
+    const int64_t w = w0 + j * kThreads;
+    if (w >= nwords) continue;
+    uint32_t o[4];
+    st::deq8o<HI>(p[j], st::make_tbl(lut, s[j]), o);
+    out[w] = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
 
 __device__ __forceinline__ unsigned nib(uint32_t w, int e, int hi_first) {
   int sh = 4 * (e ^ hi_first);
@@ -103,10 +139,27 @@ int launch_dequant4(const uint8_t* payload, const float* scales, int64_t numel, 
   for (int i = 0; i < 16; ++i) lut.v[i] = lut16[i];
   int hi = (flags & ST_FLAG_HI_NIBBLE_FIRST) ? 1 : 0;
   int64_t vec_elems = 0;
-  if (aligned16(payload) && aligned16(out)) {
+  // ST_DEQUANT_KERNEL=0: the LDS-codebook kernel (64 output bytes per lane)
+  static const int kind = [] {
+    const char* e = getenv("ST_DEQUANT_KERNEL");
+    return e ? atoi(e) : 1;
+  }();
+  const int shift = group == 128 ? 7 : 6;
+  if (kind != 0 && ((uintptr_t)payload & 3u) == 0 && aligned16(out)) {
+    const int64_t nwords = numel / 8;
+    if (nwords > 0) {
+      const unsigned blocks = (unsigned)cdiv(nwords, RW * kThreads);
+      if (hi)
+        dequant4_word<true><<<blocks, kThreads, 0, stream>>>((const uint32_t*)payload, scales,
+                                                             nwords, shift, lut, (uint4*)out);
+      else
+        dequant4_word<false><<<blocks, kThreads, 0, stream>>>((const uint32_t*)payload, scales,
+                                                              nwords, shift, lut, (uint4*)out);
+      vec_elems = nwords * 8;
+    }
+  } else if (aligned16(payload) && aligned16(out)) {
     int64_t nchunks = numel / 32;
     if (nchunks > 0) {
-      int shift = group == 128 ? 7 : 6;
       dequant4_vec<<<(unsigned)cdiv(nchunks, kThreads), kThreads, 0, stream>>>(
           (const uint4*)payload, scales, nchunks, shift, lut, hi, (uint4*)out);
       vec_elems = nchunks * 32;
