@@ -979,15 +979,15 @@ constexpr int RB_ST = 4;
 // the fragment reads are issued early and the VALU co-issues with the MFMAs
 // of one wave.  VM adds the section's DMAs and W loads.
 #define RB_G(mask, n) __builtin_amdgcn_sched_group_barrier(mask, n, 0)
-template <int FN, bool VM>
+template <int FN, bool VM, int FM = 8>
 __device__ __forceinline__ void rb_order() {
   static_assert(FN == 1 || FN == 2, "one or two B fragments per wave");
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < FM; ++i) {
     RB_G(0x008, 1);
     if constexpr (VM) RB_G(0x020, 1);
     RB_G(0x100, 1);
-    RB_G(0x002, FN == 2 ? 3 : 4);
+    RB_G(0x002, (FN == 2 ? 3 : 4) * 8 / FM);
     if constexpr (FN == 2) {
       RB_G(0x008, 1);
       if constexpr (VM) RB_G(0x020, 1);
@@ -996,10 +996,10 @@ __device__ __forceinline__ void rb_order() {
   }
 }
 #undef RB_G
-template <int FN, int WAVES, bool HI>
-__global__ __launch_bounds__(64 * WAVES) void gemm_rb_kernel(GemmParams p) {
-  constexpr int BM = 256, NT = 64 * WAVES, WN = 32 * FN, BN = WN * WAVES;
-  constexpr int FM = 8, WM = 256;
+template <int FN, int WAVES, bool HI, int FM = 8>
+__global__ __launch_bounds__(64 * WAVES, FM == 4 ? 2 : 1) void gemm_rb_kernel(GemmParams p) {
+  constexpr int BM = 32 * FM, NT = 64 * WAVES, WN = 32 * FN, BN = WN * WAVES;
+  constexpr int WM = BM;
   constexpr int A_ST = BM * BK / 8;       // 16-byte units per A stage
   constexpr int DMA_W = BM / 8 / WAVES;   // DMAs (8 rows each) per wave per stage
   // vector-memory operations issued per step: the DMAs, FN W loads, and FN
@@ -1128,17 +1128,17 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_rb_kernel(GemmParams p) {
     read_A(kt, 1, fa1);
     deq_B(wr[u], 1, fb1);
     mfmas(fa0, fb0);
-    rb_order<FN, false>();
+    rb_order<FN, false, FM>();
     __builtin_amdgcn_sched_barrier(0);
     read_A(kt, 2, fa0);
     deq_B(wr[u], 2, fb0);
     mfmas(fa1, fb1);
-    rb_order<FN, false>();
+    rb_order<FN, false, FM>();
     __builtin_amdgcn_sched_barrier(0);
     read_A(kt, 3, fa1);
     deq_B(wr[u], 3, fb1);
     mfmas(fa0, fb0);
-    rb_order<FN, false>();
+    rb_order<FN, false, FM>();
     __builtin_amdgcn_sched_barrier(0);
     wait_cnt<RB_PAIR, 0>();
     bar();
@@ -1149,7 +1149,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_rb_kernel(GemmParams p) {
     read_A(kt + 1, 0, fa0);
     deq_B(wr[un], 0, fb0);
     mfmas(fa1, fb1);
-    rb_order<FN, true>();
+    rb_order<FN, true, FM>();
     __builtin_amdgcn_sched_barrier(0);
   };
   for (int kt = 0; kt < KT; kt += RB_ST) {
@@ -1229,9 +1229,9 @@ int launch_ws(const GemmParams& p, hipStream_t stream) {
   return st::check_launch("q4gemm");
 }
 
-template <int FN, int WAVES>
+template <int FN, int WAVES, int FM = 8>
 int launch_rb(const GemmParams& p, hipStream_t stream) {
-  constexpr int BM = 256, BN = 32 * FN * WAVES, NT = 64 * WAVES;
+  constexpr int BM = 32 * FM, BN = 32 * FN * WAVES, NT = 64 * WAVES;
   constexpr int64_t lds_dwords = (int64_t)RB_ST * BM * BK / 8 * 4;
   const int64_t tiles = st::cdiv(p.M, BM) * st::cdiv(p.P, BN);
   if (tiles > 0x7fffffff) return st::fail(ST_EUNSUPPORTED, "q4gemm: too many tiles");
@@ -1245,9 +1245,9 @@ int launch_rb(const GemmParams& p, hipStream_t stream) {
   GemmParams q = p;
   if (int rc = choose_epilogue<false, BM, BN>(q, lds_dwords, NT / 64)) return rc;
   if (q.hi_first)
-    gemm_rb_kernel<FN, WAVES, true><<<(unsigned)tiles, NT, 0, stream>>>(q);
+    gemm_rb_kernel<FN, WAVES, true, FM><<<(unsigned)tiles, NT, 0, stream>>>(q);
   else
-    gemm_rb_kernel<FN, WAVES, false><<<(unsigned)tiles, NT, 0, stream>>>(q);
+    gemm_rb_kernel<FN, WAVES, false, FM><<<(unsigned)tiles, NT, 0, stream>>>(q);
   return st::check_launch("q4gemm");
 }
 
@@ -1279,7 +1279,9 @@ int launch(const GemmParams& p, hipStream_t stream) {
 // yields >= 192 tiles; else 128x128 (4 waves).  ST_GEMM_TILE forces one (128,
 // 256, 2561 = 256x128 8 waves, 2562, 2564 = 256x256 4 waves; forward only:
 // register-operand 2565 = 256x256 4 waves, 2566 = 256x256 8 waves, 2567 =
-// 256x128 4 waves).
+// 256x128 4 waves, 2568 = 128x256 8 waves).  For the N = 4096 forwards (o,
+// down) the 256x128 register-operand and the 128x256 tiles measured no faster
+// than the warp-specialised kernel.
 int tile_choice(int mode, int64_t M, int64_t P) {
   const char* env = getenv("ST_GEMM_TILE");
   if (env) return atoi(env);
@@ -1380,6 +1382,7 @@ int dispatch(const GemmParams& p, hipStream_t stream) {
       if (t == 2565 && p.Q % (RB_ST * BK) == 0) return launch_rb<2, 4>(p, stream);
       if (t == 2566 && p.Q % (RB_ST * BK) == 0) return launch_rb<1, 8>(p, stream);
       if (t == 2567 && p.Q % (RB_ST * BK) == 0) return launch_rb<1, 4>(p, stream);
+      if (t == 2568 && p.Q % (RB_ST * BK) == 0) return launch_rb<1, 8, 4>(p, stream);
     }
   }
   return launch<MODE, 128, 128, 4>(p, stream);

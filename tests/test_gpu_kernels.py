@@ -135,7 +135,7 @@ def _close_bf16(got, ref, what):
 SHAPES = [(64, 256, 256), (100, 384, 512), (37, 96, 688), (300, 512, 1024), (1, 128, 128)]
 
 
-@pytest.mark.parametrize("tile", ["128", "2561", "2562", "256", "2565", "2566", "2567"])
+@pytest.mark.parametrize("tile", ["128", "2561", "2562", "256", "2565", "2566", "2567", "2568"])
 @pytest.mark.parametrize("fmt", ["nf4-g128", "int4-sym-g128"])
 @pytest.mark.parametrize("M,N,K", SHAPES)
 @pytest.mark.parametrize("lora,residual", [(False, False), (True, False), (True, True)])
