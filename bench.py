@@ -40,6 +40,11 @@ QWEN3_METRIC = ("train tokens/s, full streamed Qwen3-8B-shape step (36 nf4-g128 
 # Qwen3-MoE-30B-A3B-shape MoE feed-forward
 MOE = dict(H=2048, I=768, E=128, k=8, T=4096, r=8, alpha=16.0, norm=True)
 MOE_METRIC = "train tokens/s per MoE layer fwd+bwd (Qwen3-MoE-30B-A3B shape, NF4 experts)"
+# the MoE feed-forward of the DeepSeek-V3-shape layer
+DSMOE = dict(H=7168, I=2048, E=256, k=8, groups=8, group_k=4, scale=2.5, T=2048, r=8, alpha=16.0,
+             shared_I=2048)
+DSMOE_METRIC = ("train tokens/s per DeepSeek-V3-shape MoE feed-forward fwd+recompute+bwd "
+                "(256 NF4 routed experts + shared expert)")
 PROJ = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
         "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj")
 
@@ -383,6 +388,116 @@ def memory_bench(args):
     print(json.dumps(result), flush=True)
 
 
+def deepseek_moe_bench(args):
+    """Config 5's MoE feed-forward: 2048 tokens through the sigmoid group-limited
+    router (8 groups, best 4, top-8, bias, normalised, x2.5), 256 routed nf4-g128
+    experts of [2x2048, 7168] + [7168, 2048] and the shared expert (same shape)
+    with LoRA r=8 on its gate/up/down (BASELINE: LoRA on the shared expert, not
+    on the routed ones).  One step = forward without grad + forward with grad
+    + backward (the StreamingBlockFunction lifecycle).  The experts are
+    synthetic packed bytes (random codes, scales in [0.01, 0.03)): the cost
+    does not depend on the values, and encoding 11.3 G weights on the host
+    would dominate the setup."""
+    import torch
+    from spilltune_amd import moe, ops
+    c = DSMOE
+    H, I, E, k, T, r = c["H"], c["I"], c["E"], c["k"], c["T"], c["r"]
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(1234)
+
+    def packed(experts, n, kk):
+        pay = torch.randint(0, 256, (experts * n * kk // 2,), dtype=torch.uint8, device=dev,
+                            generator=g)
+        sc = torch.rand(experts * n * kk // 128, device=dev, generator=g) * 0.02 + 0.01
+        return pay, sc
+    log(f"building DeepSeek-V3-shape MoE: {E} experts of [2x{I}, {H}] + [{H}, {I}], nf4-g128")
+    gu_p, gu_s = packed(E, 2 * I, H)
+    d_p, d_s = packed(E, H, I)
+    gate_up = moe.Q4Experts(gu_p, gu_s, E, 2 * I, H, "nf4-g128")
+    down = moe.Q4Experts(d_p, d_s, E, H, I, "nf4-g128")
+    Is = c["shared_I"]
+    shared = {}
+    for nm, (n, kk) in (("gate_proj", (Is, H)), ("up_proj", (Is, H)), ("down_proj", (H, Is))):
+        pay, sc = packed(1, n, kk)
+        shared[f"mlp.shared_experts.{nm}.weight"] = ops.Q4Weight(pay, sc, (n, kk), "nf4-g128")
+    gc = torch.Generator().manual_seed(3)
+    router = (torch.randn(E, H, generator=gc) * H ** -0.5).to(torch.bfloat16).to(dev)
+    bias = (torch.randn(E, generator=gc) * 0.01).to(dev)
+
+    class _L:
+        def __init__(self, fin, fout):
+            self.rank, self.scale = r, c["alpha"] / r
+            self.A = (torch.randn(r, fin, generator=gc) * 0.02).to(dev).requires_grad_(True)
+            self.B = (torch.randn(fout, r, generator=gc) * 0.02).to(dev).requires_grad_(True)
+    ls = {"gate": _L(H, Is), "up": _L(H, Is), "down": _L(Is, H)}
+    weights = {"mlp.gate.weight": router, "mlp.gate.e_score_correction_bias": bias,
+               "mlp.experts.gate_up_proj": gate_up, "mlp.experts.down_proj": down, **shared}
+    X = torch.randn(T, H, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16).to(dev)
+    dY = torch.randn(T, H, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).to(dev)
+
+    def ff(x):
+        return moe.deepseek_moe_feed_forward(x, weights, num_experts=E, top_k=k,
+                                             groups=c["groups"], group_k=c["group_k"],
+                                             normalize=True, scale=c["scale"], lora_shared=ls)
+
+    def step():
+        with torch.no_grad():
+            ff(X)
+        x = X.detach().requires_grad_(True)
+        ff(x).backward(dY)
+        for l in ls.values():
+            l.A.grad = l.B.grad = None
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    ops.TIMER = ops.KernelTimer()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    timer, ops.TIMER = ops.TIMER, None
+    ms = elapsed * 1e3 / args.steps
+    R = T * k
+    fwd = 2.0 * R * (2 * I * H + H * I) + 2.0 * T * 3 * Is * H + 2.0 * T * H * E
+    flops = 3 * fwd
+    kern = timer.summary()
+    key, info = max(kern.items(), key=lambda kv: kv[1]["launches"] * kv[1]["avg_ms"])
+    _, M, N, K = key
+    achieved = 2.0 * M * N * K / (info["avg_ms"] * 1e-3) / 1e12
+    for k2, v2 in sorted(kern.items(), key=lambda kv: -kv[1]["launches"] * kv[1]["avg_ms"]):
+        tf = 2.0 * k2[1] * k2[2] * k2[3] / (v2["avg_ms"] * 1e-3) / 1e12
+        log(f"  {k2[0]:9s} rows={k2[1]} N={k2[2]} K={k2[3]}: {v2['launches']} launches, "
+            f"{v2['avg_ms']:.3f} ms avg, {tf:.0f} TFLOP/s ({tf / PEAK_BF16_TFLOPS:.1%})")
+    layer_bytes = (gu_p.numel() + d_p.numel() + 4 * (gu_s.numel() + d_s.numel()) +
+                   sum(w.payload.numel() + 4 * w.scales.numel() for w in shared.values()))
+    log(f"step {ms:.3f} ms; {flops / (ms * 1e-3) / 1e12:.0f} TFLOP/s algorithmic; "
+        f"{layer_bytes / 1e9:.2f} GB of 4-bit experts per layer")
+    result = {
+        "metric": DSMOE_METRIC, "value": round(T * args.steps / elapsed, 1), "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random nf4-g128 codes and scales; router ~N(0, H^-1/2), bias "
+                "~N(0, 0.01); N(0,1) activations/grads)",
+        "config": {"workload": f"deepseek-moe: DeepSeek-V3-shape MoE feed-forward, {T} tokens, "
+                               f"{E} experts top-{k} (sigmoid, {c['groups']} groups, best "
+                               f"{c['group_k']}), shared expert with LoRA r={r}, nf4-g128, "
+                               "fwd + recompute + bwd",
+                   "global_batch": 1, "seq_len": T, "hidden": H, "intermediate": I,
+                   "experts": E, "top_k": k, "parallelism": "single GPU"},
+        "layer_mfma_frac": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "algorithmic_tflop_per_step": round(flops / 1e12, 4),
+        "expert_bytes_per_layer": int(layer_bytes),
+        "roofline": {"bound": "mfma", "kernel": f"{key[0]} rows={M} N={N} K={K}",
+                     "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None, "avg_ms": round(info["avg_ms"], 4)},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(result), flush=True)
+
+
 def moe_bench(args):
     """Config 4: the MoE feed-forward forward + backward on 4096 tokens
     (router, permutation, grouped 4-bit gate|up and down GEMMs with per-expert
@@ -511,7 +626,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="llama8b",
-                    choices=sorted(CONFIGS) + ["moe", "qwen3-stream", "memory"])
+                    choices=sorted(CONFIGS) + ["moe", "deepseek-moe", "qwen3-stream", "memory"])
     ap.add_argument("--cpu-tokens", type=int, default=2048)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -543,6 +658,9 @@ def main():
         return
     if args.config == "memory":
         memory_bench(args)
+        return
+    if args.config == "deepseek-moe":
+        deepseek_moe_bench(args)
         return
     from spilltune_amd import ops, slots
     from spilltune_amd.dense import CausalMask

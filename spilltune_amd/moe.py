@@ -32,7 +32,7 @@ import torch
 
 from . import _lib
 from .codecs import GROUP, codebook, encode
-from .ops import _launch
+from .ops import _launch, lora_gemm
 
 _BF16 = torch.bfloat16
 _F32 = torch.float32
@@ -156,8 +156,8 @@ def _stream(dev):
 
 class _MoEFeedForward(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, flat, router, gate_up, down, cfg, *lora):
-        top_k, norm, gu_rank, gu_scale, d_rank, d_scale = cfg
+    def forward(ctx, flat, router, bias, gate_up, down, cfg, *lora):
+        top_k, norm, gu_rank, gu_scale, d_rank, d_scale, sig, groups, group_k, rscale = cfg
         T, H = flat.shape
         E = gate_up.experts
         I = down.in_features
@@ -167,13 +167,23 @@ class _MoEFeedForward(torch.autograd.Function):
         lut_gu, lut_d = gate_up.lut(), down.lut()
         has_lora = bool(lora)
         # 1. router
-        logits = torch.empty((T, E), dtype=_BF16, device=dev)
-        _lib.call("st_linear_bf16_fwd", _lib.ptr(flat), T, H, H, _lib.ptr(router), E, H,
-                  _lib.ptr(logits), E, st)
         weights = torch.empty((T, top_k), dtype=_F32, device=dev)
         indices = torch.empty((T, top_k), dtype=_I32, device=dev)
-        _lib.call("st_moe_route_softmax", _lib.ptr(logits), T, E, top_k, int(norm), 1,
-                  _lib.ptr(weights), _lib.ptr(indices), st)
+        if sig:
+            # deepseek.py:117-125: fp32 logits F.linear(hidden.float(), weight.float())
+            # (bf16 products are exact in fp32; fp32 accumulation), sigmoid
+            # group-limited selection with the bias, fp32 weights * scale
+            logits = torch.empty((T, E), dtype=_F32, device=dev)
+            lora_gemm(T, E, H, flat, H, 1, router, 1, H, 1.0, logits)
+            _lib.call("st_moe_route_sigmoid", _lib.ptr(logits), _lib.ptr(bias), T, E, groups,
+                      group_k, top_k, int(norm), float(rscale), _lib.ptr(weights),
+                      _lib.ptr(indices), st)
+        else:
+            logits = torch.empty((T, E), dtype=_BF16, device=dev)
+            _lib.call("st_linear_bf16_fwd", _lib.ptr(flat), T, H, H, _lib.ptr(router), E, H,
+                      _lib.ptr(logits), E, st)
+            _lib.call("st_moe_route_softmax", _lib.ptr(logits), T, E, top_k, int(norm), 1,
+                      _lib.ptr(weights), _lib.ptr(indices), st)
         # 2. permutation
         offsets = torch.empty(E + 1, dtype=_I32, device=dev)
         row_token = torch.empty(R, dtype=_I32, device=dev)
@@ -225,7 +235,7 @@ class _MoEFeedForward(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dout, _dlogits, _dweights, _dindices):
         gate_up, down, cfg, has_lora = ctx.meta
-        top_k, norm, gu_rank, gu_scale, d_rank, d_scale = cfg
+        top_k, norm, gu_rank, gu_scale, d_rank, d_scale, sig, groups, group_k, rscale = cfg
         (flat, router, logits, weights, indices, offsets, row_token, pick_row, gu, h, v,
          T_gu, T_d, A_gu, B_gu, A_d, B_d) = ctx.saved_tensors
         dout = dout.contiguous()
@@ -237,8 +247,11 @@ class _MoEFeedForward(torch.autograd.Function):
         # combine VJP
         dv = torch.empty((R, H), dtype=_BF16, device=dev)
         dw = torch.empty((T, top_k), dtype=_F32, device=dev)
+        # bf16 routing weights (Qwen3) round the products and the sum; DeepSeek's
+        # fp32 weights promote value * weight to fp32
         _lib.call("st_moe_combine_bwd", _lib.ptr(dout), _lib.ptr(v), R, _lib.ptr(weights),
-                  _lib.ptr(pick_row), T, top_k, H, 1, _lib.ptr(dv), _lib.ptr(dw), st)
+                  _lib.ptr(pick_row), T, top_k, H, 0 if sig else 1, _lib.ptr(dv), _lib.ptr(dw),
+                  st)
         grads = []
         dT_d = dT_gu = None
         if has_lora:
@@ -284,6 +297,17 @@ class _MoEFeedForward(torch.autograd.Function):
             gate_up.flags, _lib.ptr(dT_gu), 2 * gu_rank if has_lora else 0, _lib.ptr(A_gu),
             2 * gu_rank if has_lora else 0, _lib.ptr(dxs), H, st))
         # router VJP and the input gradient over every use of flat
+        if sig:
+            # the router is frozen; its input gradient is fp32 dlogits @ W
+            dlogits = torch.empty((T, E), dtype=_F32, device=dev)
+            _lib.call("st_moe_route_sigmoid_bwd", _lib.ptr(logits), _lib.ptr(indices),
+                      _lib.ptr(dw), T, E, top_k, int(norm), float(rscale), _lib.ptr(dlogits), st)
+            drouter = torch.empty((T, H), dtype=_F32, device=dev)
+            lora_gemm(T, H, E, dlogits, E, 1, router, H, 1, 1.0, drouter)
+            dflat = torch.empty((T, H), dtype=_BF16, device=dev)
+            _lib.call("st_moe_gather_sum", _lib.ptr(dxs), R, _lib.ptr(pick_row), T, top_k, H,
+                      _lib.ptr(drouter), _lib.ST_DTYPE_F32, _lib.ptr(dflat), st)
+            return (dflat, None, None, None, None, None, *grads)
         dlogits = torch.empty((T, E), dtype=_BF16, device=dev)
         _lib.call("st_moe_route_softmax_bwd", _lib.ptr(logits), _lib.ptr(indices), _lib.ptr(dw),
                   T, E, top_k, int(norm), _lib.ptr(dlogits), st)
@@ -301,7 +325,7 @@ class _MoEFeedForward(torch.autograd.Function):
         dflat = torch.empty((T, H), dtype=_BF16, device=dev)
         _lib.call("st_moe_gather_sum", _lib.ptr(dxs), R, _lib.ptr(pick_row), T, top_k, H,
                   _lib.ptr(drouter), _lib.ST_DTYPE_BF16, _lib.ptr(dflat), st)
-        return (dflat, None, None, None, None, *grads)
+        return (dflat, None, None, None, None, None, *grads)
 
 
 def moe_feed_forward(hidden, weights, *, num_experts, top_k, norm_topk_prob, lora_gate_up=None,
@@ -328,17 +352,83 @@ def moe_feed_forward(hidden, weights, *, num_experts, top_k, norm_topk_prob, lor
     if (gate_up.experts, gate_up.out_features, gate_up.in_features) != (E, 2 * I, H) or \
             (down.experts, down.out_features) != (E, H) or E != num_experts:
         raise ValueError("expert shapes do not match the router")
+    cfg, lora = _lora_cfg(top_k, norm_topk_prob, lora_gate_up, lora_down,
+                          (False, 0, 0, 1.0))
+    out, _, w, idx = _MoEFeedForward.apply(flat.contiguous(), router.detach().contiguous(), None,
+                                           gate_up, down, cfg, *lora)
+    out = out.reshape(shape)
+    return (out, w, idx) if return_routing else out
+
+
+def _lora_cfg(top_k, normalize, lora_gate_up, lora_down, router_cfg):
     if (lora_gate_up is None) != (lora_down is None):
         raise ValueError("unsupported_capability: LoRA on gate_up and down together or not at all")
-    cfg = (int(top_k), bool(norm_topk_prob), 0, 1.0, 0, 1.0)
-    lora = ()
-    if lora_gate_up is not None:
-        if lora_gate_up.segments != 2 or lora_down.segments != 1:
-            raise ValueError("gate_up LoRA needs 2 segments, down LoRA 1")
-        cfg = (int(top_k), bool(norm_topk_prob), lora_gate_up.rank, lora_gate_up.scale,
-               lora_down.rank, lora_down.scale)
-        lora = (lora_gate_up.A, lora_gate_up.B, lora_down.A, lora_down.B)
-    out, _, w, idx = _MoEFeedForward.apply(flat.contiguous(), router.detach().contiguous(),
-                                           gate_up, down, cfg, *lora)
+    if lora_gate_up is None:
+        return (int(top_k), bool(normalize), 0, 1.0, 0, 1.0) + router_cfg, ()
+    if lora_gate_up.segments != 2 or lora_down.segments != 1:
+        raise ValueError("gate_up LoRA needs 2 segments, down LoRA 1")
+    return ((int(top_k), bool(normalize), lora_gate_up.rank, lora_gate_up.scale, lora_down.rank,
+             lora_down.scale) + router_cfg,
+            (lora_gate_up.A, lora_gate_up.B, lora_down.A, lora_down.B))
+
+
+def deepseek_moe_feed_forward(hidden, weights, *, num_experts, top_k, groups, group_k,
+                              normalize, scale, lora_gate_up=None, lora_down=None,
+                              lora_shared=None, return_routing=False):
+    """The MoE part of ``deepseek_block`` (adapters/deepseek.py:115-126,
+    158-174) on 4-bit experts: ``route`` (fp32 sigmoid scores, selection by
+    score + ``e_score_correction_bias`` among the ``group_k`` best of
+    ``groups`` expert groups, weights = scores of the picks, renormalised when
+    ``normalize``, times ``scale``), the routed experts combined in ascending
+    expert order with ``bf16(value * weight)`` accumulated into bf16
+    (``index_add_``), plus the shared expert ``mlp.shared_experts.*`` when its
+    weights are given: returns ``out + shared(x)`` in bf16, the operand the
+    reference adds to the residual.
+
+    ``weights``: ``mlp.gate.weight`` (bf16 ``[E, H]``, frozen),
+    ``mlp.gate.e_score_correction_bias`` (``[E]``), ``mlp.experts.gate_up_proj``
+    / ``mlp.experts.down_proj`` (:class:`Q4Experts`) and optionally
+    ``mlp.shared_experts.{gate,up,down}_proj.weight`` (:class:`~spilltune_amd.ops.Q4Weight`).
+    ``lora_shared`` optionally maps ``"gate"``, ``"up"``, ``"down"`` to LoRA
+    projections of the shared expert; ``lora_gate_up``/``lora_down`` adapt
+    every routed expert (this build's extension, as for Qwen3)."""
+    from . import ops
+    router = weights["mlp.gate.weight"]
+    bias = weights["mlp.gate.e_score_correction_bias"]
+    gate_up = weights["mlp.experts.gate_up_proj"]
+    down = weights["mlp.experts.down_proj"]
+    if not isinstance(gate_up, Q4Experts) or not isinstance(down, Q4Experts):
+        raise ValueError("unsupported_capability: experts must be Q4Experts")
+    shape = hidden.shape
+    flat = hidden.reshape(-1, shape[-1])
+    if flat.dtype != _BF16 or router.dtype != _BF16:
+        raise ValueError("deepseek_moe_feed_forward expects bf16 hidden states and router")
+    E, H = router.shape
+    I = down.in_features
+    if (gate_up.experts, gate_up.out_features, gate_up.in_features) != (E, 2 * I, H) or \
+            (down.experts, down.out_features) != (E, H) or E != num_experts or \
+            tuple(bias.shape) != (E,):
+        raise ValueError("expert shapes do not match the router")
+    cfg, lora = _lora_cfg(top_k, normalize, lora_gate_up, lora_down,
+                          (True, int(groups), int(group_k), float(scale)))
+    flat = flat.contiguous()
+    out, _, w, idx = _MoEFeedForward.apply(flat, router.detach().contiguous(),
+                                           bias.detach().float().contiguous(), gate_up, down,
+                                           cfg, *lora)
+    prefix = "mlp.shared_experts."
+    if prefix + "gate_proj.weight" in weights:
+        ls = lora_shared or {}
+        wg, wu = weights[prefix + "gate_proj.weight"], weights[prefix + "up_proj.weight"]
+        wd = weights[prefix + "down_proj.weight"]
+        lg, lu, ldn = ls.get("gate"), ls.get("up"), ls.get("down")
+        gu = ops.concat_rows([wg, wu])
+        if gu is not None and (lg is None) == (lu is None):
+            shared = ops.q4_lora_linear(ops.q4_lora_linear(flat, gu, [lg, lu]), wd, [ldn],
+                                        swiglu=True)
+        else:
+            act = ops.swiglu_pair(ops.q4_lora_linear(flat, wg, [lg]),
+                                  ops.q4_lora_linear(flat, wu, [lu]))
+            shared = ops.q4_lora_linear(act, wd, [ldn])
+        out = out + shared  # deepseek.py:174, bf16
     out = out.reshape(shape)
     return (out, w, idx) if return_routing else out

@@ -317,6 +317,97 @@ def test_moe_ffn_fwd_bwd_vs_oracle(dev, oracle_codec, T, H, I, E, k, norm, use_l
             assert _cos(got, leaf.grad) > 0.999, name
 
 
+class _SharedLora:
+    """LoRA of one shared-expert projection: fp32 leaves A [r, in], B [out, r]."""
+
+    def __init__(self, g, r, fin, fout, alpha, dev):
+        self.rank, self.scale = r, alpha / r
+        self.A = (torch.randn(r, fin, generator=g) * 0.05).to(dev).requires_grad_(True)
+        self.B = (torch.randn(fout, r, generator=g) * 0.05).to(dev).requires_grad_(True)
+
+
+def _q4_dense(oc, w, dev):
+    from spilltune_amd import ops
+    w32 = w.numpy().astype(np.float32)
+    payload, scales = oc.encode_nf4(w32)
+    bits = np.asarray(oc.decode4(payload, scales, w32.size, lut=oc.NF4_LUT), dtype=np.uint16)
+    exact = torch.from_numpy(bits.astype(np.int16)).view(BF).view(w.shape)
+    return ops.Q4Weight(torch.from_numpy(payload).to(dev), torch.from_numpy(scales).to(dev),
+                        tuple(w.shape), "nf4-g128"), exact
+
+
+@pytest.mark.parametrize("T,H,I,E,groups,group_k,k,expert_lora", [
+    (128, 256, 128, 16, 4, 2, 4, True),
+    (77, 128, 128, 32, 8, 4, 8, False),
+])
+def test_deepseek_moe_ffn_fwd_bwd_vs_oracle(dev, oracle_codec, T, H, I, E, groups, group_k, k,
+                                            expert_lora):
+    """deepseek.py:115-126,158-174: sigmoid group-limited routing with the
+    selection bias, fp32 routing weights, the routed experts and the shared
+    expert (with LoRA on its three projections), forward and backward, vs the
+    oracle on the GPU's picks; the picks equal the oracle router's."""
+    from oracle import layer as OL
+    g = torch.Generator().manual_seed(T + E + k)
+    router = (torch.randn(E, H, generator=g) * 3 * H ** -0.5).to(BF)   # well-separated scores
+    bias = torch.randn(E, generator=g) * 0.1
+    qgu, Wgu = _experts(oracle_codec, torch.randn(E, 2 * I, H, generator=g) * 0.02, dev)
+    qd, Wd = _experts(oracle_codec, torch.randn(E, H, I, generator=g) * 0.02, dev)
+    Is = 2 * I
+    qsg, Wsg = _q4_dense(oracle_codec, torch.randn(Is, H, generator=g) * 0.02, dev)
+    qsu, Wsu = _q4_dense(oracle_codec, torch.randn(Is, H, generator=g) * 0.02, dev)
+    qsd, Wsd = _q4_dense(oracle_codec, torch.randn(H, Is, generator=g) * 0.02, dev)
+    flat = torch.randn(T, H, generator=g).to(BF)
+    dout = torch.randn(T, H, generator=g).to(BF)
+    r = 8
+    lgu = ld = None
+    if expert_lora:
+        lgu = moe.make_expert_lora("mlp.experts.gate_up_proj", E, H, 2 * I, rank=r, alpha=16.0,
+                                   device=dev, segments=2, generator=g, b_std=0.02)
+        ld = moe.make_expert_lora("mlp.experts.down_proj", E, I, H, rank=r, alpha=16.0,
+                                  device=dev, generator=g, b_std=0.02)
+    ls = {"gate": _SharedLora(g, r, H, Is, 16.0, dev), "up": _SharedLora(g, r, H, Is, 16.0, dev),
+          "down": _SharedLora(g, r, Is, H, 16.0, dev)}
+    weights = {"mlp.gate.weight": router.to(dev), "mlp.gate.e_score_correction_bias": bias.to(dev),
+               "mlp.experts.gate_up_proj": qgu, "mlp.experts.down_proj": qd,
+               "mlp.shared_experts.gate_proj.weight": qsg, "mlp.shared_experts.up_proj.weight": qsu,
+               "mlp.shared_experts.down_proj.weight": qsd}
+    xd = flat.to(dev).requires_grad_(True)
+    out, w, idx = moe.deepseek_moe_feed_forward(
+        xd, weights, num_experts=E, top_k=k, groups=groups, group_k=group_k, normalize=True,
+        scale=2.5, lora_gate_up=lgu, lora_down=ld, lora_shared=ls, return_routing=True)
+    out.backward(dout.to(dev))
+    torch.cuda.synchronize()
+    idx_c = idx.cpu().long()
+    _, _, ref_idx = OM.deepseek_route(flat, router, bias, groups=groups, group_k=group_k, top_k=k,
+                                      normalize=True, scale=2.5)
+    assert torch.equal(idx_c.sort(1)[0], ref_idx.sort(1)[0])
+    # oracle on the GPU's picks
+    x = flat.clone().requires_grad_(True)
+    logits = F.linear(x.float(), router.float())
+    routing = OM.deepseek_weights_given(logits, idx_c, normalize=True, scale=2.5)
+    torch.testing.assert_close(w.cpu(), routing.detach(), rtol=1e-5, atol=1e-6)
+    loras, leaves = None, []
+    if expert_lora:
+        leaves = [t.detach().cpu().clone().requires_grad_(True) for t in (lgu.A, lgu.B, ld.A, ld.B)]
+        loras = {"gate": (leaves[0][:, :r], leaves[1][:, :I], lgu.scale),
+                 "up": (leaves[0][:, r:], leaves[1][:, I:], lgu.scale),
+                 "down": (leaves[2], leaves[3], ld.scale)}
+    routed = OM.expert_loop(x, routing, idx_c, Wgu, Wd, num_experts=E, loras=loras)
+    sl = {n: OL.Lora(n, l.A.detach().cpu(), l.B.detach().cpu(), 16.0) for n, l in ls.items()}
+    act = F.silu(OL.lora_linear(x, Wsg, sl["gate"])) * OL.lora_linear(x, Wsu, sl["up"])
+    ref = routed + OL.lora_linear(act, Wsd, sl["down"])
+    ref.backward(dout)
+    assert _rel(out, ref) < 2e-2, "output"
+    assert _cos(xd.grad, x.grad) > 0.999, "input grad"
+    for n in ("gate", "up", "down"):
+        assert _cos(ls[n].A.grad, sl[n].A.grad) > 0.999, f"shared {n} A"
+        assert _cos(ls[n].B.grad, sl[n].B.grad) > 0.999, f"shared {n} B"
+    if expert_lora:
+        for got, leaf, name in ((lgu.A.grad, leaves[0], "A_gu"), (lgu.B.grad, leaves[1], "B_gu"),
+                                (ld.A.grad, leaves[2], "A_d"), (ld.B.grad, leaves[3], "B_d")):
+            assert _cos(got, leaf.grad) > 0.999, name
+
+
 def test_dense_block_with_moe_feed_forward(dev, oracle_codec):
     """A Qwen3-MoE-style decoder block: the HIP dense functional with the MoE
     feed-forward hook (dense.py:152) vs the oracle block with the oracle MoE."""
