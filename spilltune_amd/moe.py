@@ -170,11 +170,16 @@ class _MoEFeedForward(torch.autograd.Function):
         weights = torch.empty((T, top_k), dtype=_F32, device=dev)
         indices = torch.empty((T, top_k), dtype=_I32, device=dev)
         if sig:
-            # deepseek.py:117-125: fp32 logits F.linear(hidden.float(), weight.float())
-            # (bf16 products are exact in fp32; fp32 accumulation), sigmoid
-            # group-limited selection with the bias, fp32 weights * scale
+            # deepseek.py:117-125: fp32 logits F.linear(hidden.float(), weight.float()),
+            # sigmoid group-limited selection with the bias, fp32 weights * scale
+            # (bf16 products are exact in fp32; fp32 accumulation): the frozen
+            # router as fp32 (bf16-valued, so the kernel's hi/lo split of it is
+            # exact) in slices of 64 experts on the streaming MFMA rank-r kernel
             logits = torch.empty((T, E), dtype=_F32, device=dev)
-            lora_gemm(T, E, H, flat, H, 1, router, 1, H, 1.0, logits)
+            wf = router.float()
+            for e0 in range(0, E, 64):
+                e1 = min(E, e0 + 64)
+                lora_gemm(T, e1 - e0, H, flat, H, 1, wf[e0:e1], 1, H, 1.0, logits[:, e0:e1])
             _lib.call("st_moe_route_sigmoid", _lib.ptr(logits), _lib.ptr(bias), T, E, groups,
                       group_k, top_k, int(norm), float(rscale), _lib.ptr(weights),
                       _lib.ptr(indices), st)
