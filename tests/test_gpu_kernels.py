@@ -163,6 +163,30 @@ def test_q4_linear_fwd_vs_oracle(dev, oracle_codec, monkeypatch, tile, fmt, M, N
     _close_bf16(y, ref, f"fwd {fmt} {M}x{N}x{K} tile{tile}")
 
 
+@pytest.mark.parametrize("tile", ["128", "2561", "2562", "256", "2566", "2568"])
+@pytest.mark.parametrize("M,N,K", [(100, 384, 512), (300, 512, 1024)])
+def test_q4_linear_high_nibble_first_vs_oracle(dev, oracle_codec, monkeypatch, tile, M, N, K):
+    """bitsandbytes' packing (element 2i in the HIGH nibble of byte i,
+    ST_FLAG_HI_NIBBLE_FIRST): forward and dgrad on every tile equal the
+    oracle's decode of the same bytes, as for the low-nibble-first format."""
+    monkeypatch.setenv("ST_GEMM_TILE", tile)
+    g = torch.Generator().manual_seed(M + N + K + 1)
+    w32 = (torch.randn(N, K, generator=g) * 0.02).numpy()
+    payload, scales = oracle_codec.encode_nf4(w32, hi_first=True)
+    W = bits_tensor(oracle_codec.decode4(payload, scales, w32.size, lut=oracle_codec.NF4_LUT,
+                                         hi_first=True)).view(N, K)
+    q = ops.Q4Weight(torch.from_numpy(payload).to(dev), torch.from_numpy(scales).to(dev),
+                     (N, K), "nf4-g128", flags=_lib.ST_FLAG_HI_NIBBLE_FIRST)
+    x = torch.randn(M, K, generator=g).to(BF)
+    dy = torch.randn(M, N, generator=g).to(BF)
+    xd = x.to(dev).requires_grad_(True)
+    y = ops.q4_lora_linear(xd, q, None)
+    y.backward(dy.to(dev))
+    torch.cuda.synchronize()
+    _close_bf16(y, F.linear(x.float(), W.float()).to(BF), f"hi-first fwd tile{tile}")
+    _close_bf16(xd.grad, (dy.float() @ W.float()).to(BF), f"hi-first dgrad tile{tile}")
+
+
 @pytest.mark.parametrize("tile", ["128", "2561", "2562", "256"])
 @pytest.mark.parametrize("M,N,K", [(64, 256, 256), (100, 384, 512), (37, 128, 688), (300, 512, 1024)])
 @pytest.mark.parametrize("lora", [False, True])
