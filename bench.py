@@ -416,10 +416,17 @@ def deepseek_moe_bench(args):
     gate_up = moe.Q4Experts(gu_p, gu_s, E, 2 * I, H, "nf4-g128")
     down = moe.Q4Experts(d_p, d_s, E, H, I, "nf4-g128")
     Is = c["shared_I"]
-    shared = {}
-    for nm, (n, kk) in (("gate_proj", (Is, H)), ("up_proj", (Is, H)), ("down_proj", (H, Is))):
-        pay, sc = packed(1, n, kk)
-        shared[f"mlp.shared_experts.{nm}.weight"] = ops.Q4Weight(pay, sc, (n, kk), "nf4-g128")
+    # gate and up back to back (as a slot image lays a fused group out), so the
+    # shared expert runs as one gate|up GEMM with the SwiGLU VJP in the down dgrad
+    gu_pay, gu_sc = packed(1, 2 * Is, H)
+    half_p, half_s = Is * H // 2, Is * H // 128
+    dn_pay, dn_sc = packed(1, H, Is)
+    shared = {
+        "mlp.shared_experts.gate_proj.weight": ops.Q4Weight(gu_pay[:half_p], gu_sc[:half_s],
+                                                            (Is, H), "nf4-g128"),
+        "mlp.shared_experts.up_proj.weight": ops.Q4Weight(gu_pay[half_p:], gu_sc[half_s:],
+                                                          (Is, H), "nf4-g128"),
+        "mlp.shared_experts.down_proj.weight": ops.Q4Weight(dn_pay, dn_sc, (H, Is), "nf4-g128")}
     gc = torch.Generator().manual_seed(3)
     router = (torch.randn(E, H, generator=gc) * H ** -0.5).to(torch.bfloat16).to(dev)
     bias = (torch.randn(E, generator=gc) * 0.01).to(dev)
