@@ -193,6 +193,18 @@ int st_rope_fwd(const uint16_t* x, int64_t ldx, const uint16_t* cos, const uint1
 int st_rope_bwd(const uint16_t* dout, const uint16_t* cos, const uint16_t* sin,
                 int64_t B, int64_t S, int64_t heads, int64_t D, int32_t rotate,
                 uint16_t* dx, int64_t lddx, st_stream_t stream);
+/* st_rope_fwd of a fused q|k|v projection output in one launch (dense.py:135-141
+ * for q and k, the plain view/transpose for v): x rows of stride ldx hold the
+ * heads*D query, kv_heads*D key and kv_heads*D value columns; q [B,heads,S,D],
+ * k and v [B,kv_heads,S,D].  Same results as three st_rope_fwd calls. */
+int st_rope_qkv_fwd(const uint16_t* x, int64_t ldx, const uint16_t* cos, const uint16_t* sin,
+                    int64_t B, int64_t S, int64_t heads, int64_t kv_heads, int64_t D,
+                    uint16_t* q, uint16_t* k, uint16_t* v, st_stream_t stream);
+/* VJP of st_rope_qkv_fwd: dq, dk, dv head-major -> dx rows of stride lddx. */
+int st_rope_qkv_bwd(const uint16_t* dq, const uint16_t* dk, const uint16_t* dv,
+                    const uint16_t* cos, const uint16_t* sin, int64_t B, int64_t S,
+                    int64_t heads, int64_t kv_heads, int64_t D, uint16_t* dx, int64_t lddx,
+                    st_stream_t stream);
 /* [B,heads,S,D] -> [B,S,heads*D] copy (attention output relayout). */
 int st_heads_to_tokens(const uint16_t* x, int64_t B, int64_t S, int64_t heads, int64_t D,
                        uint16_t* out, st_stream_t stream);

@@ -213,6 +213,56 @@ __global__ __launch_bounds__(NTH) void rope_bwd(const uint16_t* __restrict__ g,
 // elements (16 bytes) of one head and reads the partner chunk half a head
 // away, so there is no per-element index arithmetic.  Same rounding points as
 // rope_fwd / rope_bwd.  Needs D % 16 == 0 and 16-byte aligned rows.
+// One 8-element chunk c of a head row xr (D elements) rotated with the token's
+// cos/sin rows: o = bf16(x*cos) + bf16(rotate_half(x)*sin) (dense.py:141),
+// or copied when !rotate; written to dst.
+__device__ __forceinline__ void rope_chunk_fwd(const uint16_t* xr, const uint16_t* csr,
+                                               const uint16_t* snr, int c, int half, int rotate,
+                                               uint16_t* dst) {
+  float v[8], o[8];
+  unpack8(*(const uint4*)(xr + c * 8), v);
+  if (rotate) {
+    float p[8], cv[8], sv[8];
+    unpack8(*(const uint4*)(xr + (c < half ? c + half : c - half) * 8), p);
+    unpack8(*(const uint4*)(csr + c * 8), cv);
+    unpack8(*(const uint4*)(snr + c * 8), sv);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float rot = c < half ? -p[e] : p[e];
+      o[e] = st::bf16r(v[e] * cv[e]) + st::bf16r(rot * sv[e]);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = v[e];
+  }
+  *(uint4*)dst = pack8(o);
+}
+
+// VJP of rope_chunk_fwd for chunk c of a head-major gradient row gr.
+__device__ __forceinline__ void rope_chunk_bwd(const uint16_t* gr, const uint16_t* csr,
+                                               const uint16_t* snr, int c, int half, int rotate,
+                                               uint16_t* dst) {
+  float gv[8], o[8];
+  unpack8(*(const uint4*)(gr + c * 8), gv);
+  if (rotate) {
+    const int pc = c < half ? c + half : c - half;
+    float gp[8], cv[8], sp[8];
+    unpack8(*(const uint4*)(gr + pc * 8), gp);
+    unpack8(*(const uint4*)(csr + c * 8), cv);
+    unpack8(*(const uint4*)(snr + pc * 8), sp);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float a = st::bf16r(gv[e] * cv[e]);
+      const float gs = st::bf16r(gp[e] * sp[e]);
+      o[e] = a + (c < half ? gs : -gs);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = gv[e];
+  }
+  *(uint4*)dst = pack8(o);
+}
+
 __global__ __launch_bounds__(NTH) void rope_fwd_vec(const uint16_t* __restrict__ x, int64_t ldx,
                                                    const uint16_t* __restrict__ cs,
                                                    const uint16_t* __restrict__ sn, int S,
@@ -223,24 +273,8 @@ __global__ __launch_bounds__(NTH) void rope_fwd_vec(const uint16_t* __restrict__
   const int CH = D / 8, half = CH / 2;
   for (int i = threadIdx.x; i < heads * CH; i += NTH) {
     const int h = i / CH, c = i % CH;
-    const uint16_t* xr = x + t * ldx + h * D;
-    float v[8], o[8];
-    unpack8(*(const uint4*)(xr + c * 8), v);
-    if (rotate) {
-      float p[8], cv[8], sv[8];
-      unpack8(*(const uint4*)(xr + (c < half ? c + half : c - half) * 8), p);
-      unpack8(*(const uint4*)(cs + t * D + c * 8), cv);
-      unpack8(*(const uint4*)(sn + t * D + c * 8), sv);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float rot = c < half ? -p[e] : p[e];
-        o[e] = st::bf16r(v[e] * cv[e]) + st::bf16r(rot * sv[e]);
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = v[e];
-    }
-    *(uint4*)(out + ((b * heads + h) * S + s) * D + c * 8) = pack8(o);
+    rope_chunk_fwd(x + t * ldx + h * D, cs + t * D, sn + t * D, c, half, rotate,
+                   out + ((b * heads + h) * S + s) * D + c * 8);
   }
 }
 
@@ -254,26 +288,56 @@ __global__ __launch_bounds__(NTH) void rope_bwd_vec(const uint16_t* __restrict__
   const int CH = D / 8, half = CH / 2;
   for (int i = threadIdx.x; i < heads * CH; i += NTH) {
     const int h = i / CH, c = i % CH;
-    const uint16_t* gr = g + ((b * heads + h) * S + s) * D;
-    float gv[8], o[8];
-    unpack8(*(const uint4*)(gr + c * 8), gv);
-    if (rotate) {
-      const int pc = c < half ? c + half : c - half;
-      float gp[8], cv[8], sp[8];
-      unpack8(*(const uint4*)(gr + pc * 8), gp);
-      unpack8(*(const uint4*)(cs + t * D + c * 8), cv);
-      unpack8(*(const uint4*)(sn + t * D + pc * 8), sp);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float a = st::bf16r(gv[e] * cv[e]);
-        const float gs = st::bf16r(gp[e] * sp[e]);
-        o[e] = a + (c < half ? gs : -gs);
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = gv[e];
-    }
-    *(uint4*)(dx + t * lddx + h * D + c * 8) = pack8(o);
+    rope_chunk_bwd(g + ((b * heads + h) * S + s) * D, cs + t * D, sn + t * D, c, half, rotate,
+                   dx + t * lddx + h * D + c * 8);
+  }
+}
+
+// q, k and v of one fused q|k|v row in one launch: segment 0 = the Hq query
+// heads (rotated), 1 = the Hkv key heads (rotated), 2 = the Hkv value heads
+// (copied), each to its own head-major tensor [B, heads, S, D].
+struct QkvHeads {
+  const uint16_t* g[3];  // backward: head-major gradients of q, k, v
+  uint16_t* o[3];        // forward: head-major q, k, v
+  int h[3];
+};
+__global__ __launch_bounds__(NTH) void rope_qkv_fwd_vec(const uint16_t* __restrict__ x,
+                                                       int64_t ldx,
+                                                       const uint16_t* __restrict__ cs,
+                                                       const uint16_t* __restrict__ sn, int S,
+                                                       int D, QkvHeads qh) {
+  const int64_t t = blockIdx.x;
+  const int64_t b = t / S, s = t % S;
+  const int CH = D / 8, half = CH / 2;
+  const int n0 = qh.h[0] * CH, n1 = n0 + qh.h[1] * CH, n2 = n1 + qh.h[2] * CH;
+  for (int i = threadIdx.x; i < n2; i += NTH) {
+    const int seg = i < n0 ? 0 : i < n1 ? 1 : 2;
+    const int j = i - (seg == 0 ? 0 : seg == 1 ? n0 : n1);
+    const int h = j / CH, c = j % CH;
+    const int heads = seg == 0 ? qh.h[0] : seg == 1 ? qh.h[1] : qh.h[2];
+    uint16_t* out = seg == 0 ? qh.o[0] : seg == 1 ? qh.o[1] : qh.o[2];
+    const int col = (seg == 0 ? 0 : seg == 1 ? n0 : n1) * 8 + h * D;  // column of the head in x
+    rope_chunk_fwd(x + t * ldx + col, cs + t * D, sn + t * D, c, half, seg < 2,
+                   out + ((b * heads + h) * S + s) * D + c * 8);
+  }
+}
+__global__ __launch_bounds__(NTH) void rope_qkv_bwd_vec(const uint16_t* __restrict__ cs,
+                                                       const uint16_t* __restrict__ sn, int S,
+                                                       int D, QkvHeads qh,
+                                                       uint16_t* __restrict__ dx, int64_t lddx) {
+  const int64_t t = blockIdx.x;
+  const int64_t b = t / S, s = t % S;
+  const int CH = D / 8, half = CH / 2;
+  const int n0 = qh.h[0] * CH, n1 = n0 + qh.h[1] * CH, n2 = n1 + qh.h[2] * CH;
+  for (int i = threadIdx.x; i < n2; i += NTH) {
+    const int seg = i < n0 ? 0 : i < n1 ? 1 : 2;
+    const int j = i - (seg == 0 ? 0 : seg == 1 ? n0 : n1);
+    const int h = j / CH, c = j % CH;
+    const int heads = seg == 0 ? qh.h[0] : seg == 1 ? qh.h[1] : qh.h[2];
+    const uint16_t* g = seg == 0 ? qh.g[0] : seg == 1 ? qh.g[1] : qh.g[2];
+    const int col = (seg == 0 ? 0 : seg == 1 ? n0 : n1) * 8 + h * D;
+    rope_chunk_bwd(g + ((b * heads + h) * S + s) * D, cs + t * D, sn + t * D, c, half, seg < 2,
+                   dx + t * lddx + col + c * 8);
   }
 }
 
@@ -452,6 +516,63 @@ extern "C" int st_rope_bwd(const uint16_t* dout, const uint16_t* cos, const uint
     rope_bwd<<<nblk(total), NTH, 0, (hipStream_t)stream>>>(dout, cos, sin, S, heads, D, rotate,
                                                            total, dx, lddx);
   return st::check_launch("rope_bwd");
+}
+
+extern "C" int st_rope_qkv_fwd(const uint16_t* x, int64_t ldx, const uint16_t* cos,
+                               const uint16_t* sin, int64_t B, int64_t S, int64_t heads,
+                               int64_t kv_heads, int64_t D, uint16_t* q, uint16_t* k,
+                               uint16_t* v, st_stream_t stream) {
+  ST_CHECK_ARG(B >= 0 && S >= 0 && heads > 0 && kv_heads > 0 && D > 0 && D % 2 == 0,
+               "st_rope_qkv_fwd: bad shape");
+  if (B * S == 0) return ST_OK;
+  ST_CHECK_ARG(x && cos && sin && q && k && v, "st_rope_qkv_fwd: NULL pointer");
+  const int64_t width = (heads + 2 * kv_heads) * D;
+  ST_CHECK_ARG(ldx >= width, "st_rope_qkv_fwd: ldx < (heads + 2*kv_heads)*D");
+  const bool vec = D % 16 == 0 && ldx % 8 == 0 && B * S <= 0x7fffffff && width <= 0x7fffffff &&
+                   (((uintptr_t)x | (uintptr_t)cos | (uintptr_t)sin | (uintptr_t)q |
+                     (uintptr_t)k | (uintptr_t)v) & 15u) == 0;
+  if (!vec) {  // one launch per segment
+    int rc = st_rope_fwd(x, ldx, cos, sin, B, S, heads, D, 1, q, stream);
+    if (!rc) rc = st_rope_fwd(x + heads * D, ldx, cos, sin, B, S, kv_heads, D, 1, k, stream);
+    if (!rc)
+      rc = st_rope_fwd(x + (heads + kv_heads) * D, ldx, cos, sin, B, S, kv_heads, D, 0, v, stream);
+    return rc;
+  }
+  QkvHeads qh{};
+  qh.o[0] = q; qh.o[1] = k; qh.o[2] = v;
+  qh.h[0] = (int)heads; qh.h[1] = (int)kv_heads; qh.h[2] = (int)kv_heads;
+  rope_qkv_fwd_vec<<<(unsigned)(B * S), NTH, 0, (hipStream_t)stream>>>(x, ldx, cos, sin, (int)S,
+                                                                      (int)D, qh);
+  return st::check_launch("rope_qkv_fwd");
+}
+
+extern "C" int st_rope_qkv_bwd(const uint16_t* dq, const uint16_t* dk, const uint16_t* dv,
+                               const uint16_t* cos, const uint16_t* sin, int64_t B, int64_t S,
+                               int64_t heads, int64_t kv_heads, int64_t D, uint16_t* dx,
+                               int64_t lddx, st_stream_t stream) {
+  ST_CHECK_ARG(B >= 0 && S >= 0 && heads > 0 && kv_heads > 0 && D > 0 && D % 2 == 0,
+               "st_rope_qkv_bwd: bad shape");
+  if (B * S == 0) return ST_OK;
+  ST_CHECK_ARG(dq && dk && dv && cos && sin && dx, "st_rope_qkv_bwd: NULL pointer");
+  const int64_t width = (heads + 2 * kv_heads) * D;
+  ST_CHECK_ARG(lddx >= width, "st_rope_qkv_bwd: lddx < (heads + 2*kv_heads)*D");
+  const bool vec = D % 16 == 0 && lddx % 8 == 0 && B * S <= 0x7fffffff && width <= 0x7fffffff &&
+                   (((uintptr_t)dq | (uintptr_t)dk | (uintptr_t)dv | (uintptr_t)cos |
+                     (uintptr_t)sin | (uintptr_t)dx) & 15u) == 0;
+  if (!vec) {
+    int rc = st_rope_bwd(dq, cos, sin, B, S, heads, D, 1, dx, lddx, stream);
+    if (!rc) rc = st_rope_bwd(dk, cos, sin, B, S, kv_heads, D, 1, dx + heads * D, lddx, stream);
+    if (!rc)
+      rc = st_rope_bwd(dv, cos, sin, B, S, kv_heads, D, 0, dx + (heads + kv_heads) * D, lddx,
+                       stream);
+    return rc;
+  }
+  QkvHeads qh{};
+  qh.g[0] = dq; qh.g[1] = dk; qh.g[2] = dv;
+  qh.h[0] = (int)heads; qh.h[1] = (int)kv_heads; qh.h[2] = (int)kv_heads;
+  rope_qkv_bwd_vec<<<(unsigned)(B * S), NTH, 0, (hipStream_t)stream>>>(cos, sin, (int)S, (int)D,
+                                                                      qh, dx, lddx);
+  return st::check_launch("rope_qkv_bwd");
 }
 
 extern "C" int st_heads_to_tokens(const uint16_t* x, int64_t B, int64_t S, int64_t heads,

@@ -558,10 +558,8 @@ class _RopeQKV(torch.autograd.Function):
         k = torch.empty((B, kv_heads, S, D), dtype=_BF16, device=dev)
         v = torch.empty((B, kv_heads, S, D), dtype=_BF16, device=dev)
         offs = (0, heads * D, (heads + kv_heads) * D)
-        for out, off, h, rot in ((q, offs[0], heads, 1), (k, offs[1], kv_heads, 1),
-                                 (v, offs[2], kv_heads, 0)):
-            _lib.call("st_rope_fwd", _lib.ptr(y[:, off:]), ld, _lib.ptr(cos), _lib.ptr(sin), B, S,
-                      h, D, rot, _lib.ptr(out), st)
+        _lib.call("st_rope_qkv_fwd", _lib.ptr(y), ld, _lib.ptr(cos), _lib.ptr(sin), B, S, heads,
+                  kv_heads, D, _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), st)
         ctx.meta = (y.shape, B, S, heads, kv_heads, D, offs)
         ctx.save_for_backward(cos, sin)
         return q, k, v
@@ -573,11 +571,10 @@ class _RopeQKV(torch.autograd.Function):
         dev = cos.device
         st = _lib.stream_handle(dev)
         dy = torch.empty(shape, dtype=_BF16, device=dev)
-        for g, off, h, rot in ((dq, offs[0], heads, 1), (dk, offs[1], kv_heads, 1),
-                               (dv, offs[2], kv_heads, 0)):
-            g = torch.zeros((B, h, S, D), dtype=_BF16, device=dev) if g is None else g.contiguous()
-            _lib.call("st_rope_bwd", _lib.ptr(g), _lib.ptr(cos), _lib.ptr(sin), B, S, h, D, rot,
-                      _lib.ptr(dy[:, off:]), shape[1], st)
+        gs = [torch.zeros((B, h, S, D), dtype=_BF16, device=dev) if g is None else g.contiguous()
+              for g, h in ((dq, heads), (dk, kv_heads), (dv, kv_heads))]
+        _lib.call("st_rope_qkv_bwd", *(_lib.ptr(g) for g in gs), _lib.ptr(cos), _lib.ptr(sin), B,
+                  S, heads, kv_heads, D, _lib.ptr(dy), shape[1], st)
         return dy, None, None, None, None, None, None, None
 
 

@@ -440,3 +440,37 @@ def test_swiglu_input_projection_matches_separate_ops(dev, oracle_codec, I, lora
     for a, b in zip(*outs):
         assert torch.equal(a.view(torch.int32) if a.dtype == torch.float32 else a.view(torch.int16),
                            b.view(torch.int32) if b.dtype == torch.float32 else b.view(torch.int16))
+
+
+@pytest.mark.parametrize("D,pad", [(128, 0), (64, 0), (64, 4)])
+def test_rope_qkv_fused_matches_separate_calls(dev, D, pad):
+    """st_rope_qkv_fwd/bwd (one launch for q, k and v of a fused q|k|v row)
+    give the bits of three st_rope_fwd/bwd calls; pad = 4 makes the row
+    stride not a multiple of 8 (the per-segment path)."""
+    g = torch.Generator().manual_seed(D + pad)
+    B, S, H, Hkv = 2, 40, 4, 2
+    W = (H + 2 * Hkv) * D
+    big = torch.randn(B * S, W + pad, generator=g).to(BF).to(dev)
+    y = big[:, :W]
+    ang = torch.randn(B, S, D, generator=g)
+    cos, sin = ang.cos().to(BF).to(dev), ang.sin().to(BF).to(dev)
+    st = _lib.stream_handle(dev)
+    outs = [torch.empty(B, h, S, D, dtype=BF, device=dev) for h in (H, Hkv, Hkv)]
+    _lib.call("st_rope_qkv_fwd", _lib.ptr(y), y.stride(0), _lib.ptr(cos), _lib.ptr(sin), B, S, H,
+              Hkv, D, *(_lib.ptr(o) for o in outs), st)
+    refs = [torch.empty_like(o) for o in outs]
+    for r, off, h, rot in zip(refs, (0, H * D, (H + Hkv) * D), (H, Hkv, Hkv), (1, 1, 0)):
+        _lib.call("st_rope_fwd", _lib.ptr(y[:, off:]), y.stride(0), _lib.ptr(cos), _lib.ptr(sin),
+                  B, S, h, D, rot, _lib.ptr(r), st)
+    grads = [torch.randn(o.shape, generator=g).to(BF).to(dev) for o in outs]
+    dbig = torch.zeros(B * S, W + pad, dtype=BF, device=dev)
+    dx = dbig[:, :W]
+    _lib.call("st_rope_qkv_bwd", *(_lib.ptr(t) for t in grads), _lib.ptr(cos), _lib.ptr(sin), B, S,
+              H, Hkv, D, _lib.ptr(dx), dx.stride(0), st)
+    dref = torch.zeros_like(dbig)
+    for gr, off, h, rot in zip(grads, (0, H * D, (H + Hkv) * D), (H, Hkv, Hkv), (1, 1, 0)):
+        _lib.call("st_rope_bwd", _lib.ptr(gr), _lib.ptr(cos), _lib.ptr(sin), B, S, h, D, rot,
+                  _lib.ptr(dref[:, off:]), dref.stride(0), st)
+    torch.cuda.synchronize()
+    for a, b in zip(outs + [dbig], refs + [dref]):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
