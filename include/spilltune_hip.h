@@ -72,16 +72,6 @@ const char* st_last_error(void);
 int st_dequant4(const uint8_t* payload, const float* scales, int64_t numel, int32_t group,
                 const float* lut16, int32_t flags, uint16_t* out, st_stream_t stream);
 
-/*
- * bitsandbytes NF4 + double quantisation (nf4_backend.py:184-240 layout):
- * absmax_j = nested_map[absmax_u8[j]] * nested_absmax[j / 256] + offset (fp32),
- * out[i] = bf16_rne(lut16[code_i] * absmax_{i / 64}).  nested_map is a 256-entry
- * device array.  Parity with bitsandbytes itself is unpinned.
- */
-int st_dequant4_dq(const uint8_t* packed, const uint8_t* absmax_u8, const float* nested_absmax,
-                   const float* nested_map, float offset, int64_t numel, const float* lut16,
-                   int32_t flags, uint16_t* out, st_stream_t stream);
-
 /* ------------------------------------------------- fused projection GEMMs */
 /*
  * Forward of a frozen 4-bit projection with LoRA (lora.py:218-220):

@@ -12,6 +12,5 @@ as the timed restatement of the reference's CPU training path).
   causal-LM terminal and the AdamW update.
 
 Pinning status (what each function is checked against) is listed in the
-module headers; the only function without an independent pin is the
-bitsandbytes double-quantised decode (``decode4_dq``): parity unpinned.
+module headers; every function has an independent pin.
 """

@@ -16,12 +16,6 @@
  *                  Dettmers et al. 2023, arXiv:2305.14314, appendix E) in place
  *                  of code-8.  The reference compares its table against the
  *                  bitsandbytes one at nf4_backend.py:252-255.
- *   nf4-g64-dq     bitsandbytes 0.50.2 NF4 + double quantisation as described by
- *                  nf4_backend.py:184-240 (blocksize 64, nested block 256,
- *                  uint8 absmax codes into a 256-entry fp32 map, fp32 nested
- *                  absmax and fp32 offset; element 2i in the HIGH nibble).
- *                  bitsandbytes is not installed here and no reference test pins
- *                  its bytes: parity of this decode is UNPINNED.
  *
  * Every decode is value = bf16_rne( fp32(code_value) * fp32(scale_of_group) ),
  * i.e. one IEEE fp32 multiply followed by round-to-nearest-even to bfloat16,
@@ -69,25 +63,6 @@ void st_oracle_decode4(const uint8_t* payload, const float* scales, int64_t nume
   for (int64_t i = 0; i < numel; ++i) {
     float v = lut16[nibble(payload, i, hi_first)] * scales[i / group];
     out[i] = st_oracle_bf16_rne(v);
-  }
-}
-
-/*
- * bitsandbytes double-quantised absmax: absmax_j = map[u8_j]*nested[j/256] + offset
- * (both steps fp32), then out[i] = bf16(lut[code_i] * absmax_{i/64}).
- * Parity UNPINNED (no reference test or vector covers it).
- */
-void st_oracle_decode4_dq(const uint8_t* packed, const uint8_t* absmax_u8,
-                          const float* nested_absmax, const float* nested_map,
-                          float offset, int64_t numel, const float* lut16, int hi_first,
-                          uint16_t* out) {
-  int64_t blocks = (numel + 63) / 64;
-  for (int64_t j = 0; j < blocks; ++j) {
-    float prod = nested_map[absmax_u8[j]] * nested_absmax[j / 256];
-    float amax = prod + offset;
-    int64_t end = (j + 1) * 64 < numel ? (j + 1) * 64 : numel;
-    for (int64_t i = j * 64; i < end; ++i)
-      out[i] = st_oracle_bf16_rne(lut16[nibble(packed, i, hi_first)] * amax);
   }
 }
 

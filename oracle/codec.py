@@ -12,8 +12,6 @@ Pinning:
 * ``decode4`` with the NF4 codebook: brute force of all 16 codes x edge
   scales against Python float arithmetic, the invariants |w| <= absmax,
   code 7 -> +0, codes 0/15 -> -/+absmax.
-* ``decode4_dq``: bitsandbytes 0.50.2 is absent and no reference test pins it:
-  parity UNPINNED; only its closed form is restated.
 """
 from __future__ import annotations
 
@@ -55,8 +53,6 @@ def lib():
         I64 = ctypes.c_int64
         L.st_oracle_decode4.argtypes = [P, P, I64, ctypes.c_int, P, ctypes.c_int, P]
         L.st_oracle_decode4.restype = None
-        L.st_oracle_decode4_dq.argtypes = [P, P, P, P, ctypes.c_float, I64, P, ctypes.c_int, P]
-        L.st_oracle_decode4_dq.restype = None
         L.st_oracle_encode_int4.argtypes = [P, I64, P, P]
         L.st_oracle_encode_int4.restype = ctypes.c_int
         L.st_oracle_encode_nf4.argtypes = [P, I64, ctypes.c_int, P, P]
@@ -87,21 +83,6 @@ def decode4(payload: np.ndarray, scales: np.ndarray, numel: int, *, lut: np.ndar
     out = np.empty(numel, dtype=np.uint16)
     lib().st_oracle_decode4(_ptr(payload), _ptr(scales), numel, group, _ptr(lut),
                             int(hi_first), _ptr(out))
-    return out
-
-
-def decode4_dq(packed, absmax_u8, nested_absmax, nested_map, offset: float, numel: int,
-               *, lut: np.ndarray = NF4_LUT, hi_first: bool = True) -> np.ndarray:
-    """bitsandbytes NF4+DQ decode restated (parity UNPINNED)."""
-    packed = np.ascontiguousarray(packed, dtype=np.uint8)
-    absmax_u8 = np.ascontiguousarray(absmax_u8, dtype=np.uint8)
-    nested_absmax = np.ascontiguousarray(nested_absmax, dtype=np.float32)
-    nested_map = np.ascontiguousarray(nested_map, dtype=np.float32)
-    lut = np.ascontiguousarray(lut, dtype=np.float32)
-    out = np.empty(numel, dtype=np.uint16)
-    lib().st_oracle_decode4_dq(_ptr(packed), _ptr(absmax_u8), _ptr(nested_absmax),
-                               _ptr(nested_map), ctypes.c_float(offset), numel, _ptr(lut),
-                               int(hi_first), _ptr(out))
     return out
 
 

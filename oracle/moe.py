@@ -114,6 +114,13 @@ def qwen3_moe_ffn(hidden, router_weight, gate_up, down, *, top_k, norm_topk_prob
 def deepseek_route(hidden, weight, bias, *, groups, group_k, top_k, normalize, scale):
     """fp32 sigmoid group-limited router (deepseek.py:115-126)."""
     logits = F.linear(hidden.reshape(-1, hidden.shape[-1]).float(), weight.float())
+    return deepseek_select(logits, bias, groups=groups, group_k=group_k, top_k=top_k,
+                           normalize=normalize, scale=scale)
+
+
+def deepseek_select(logits, bias, *, groups, group_k, top_k, normalize, scale):
+    """The selection and weights of :func:`deepseek_route` (deepseek.py:118-126)
+    from given fp32 logits; returns ``(logits, weights, indices)``."""
     scores = logits.sigmoid()
     choice = scores + bias.float()
     group_scores = choice.view(-1, groups, choice.shape[-1] // groups).topk(2, dim=-1)[0].sum(-1)

@@ -30,7 +30,6 @@ _SIGNATURES = {
     "st_abi_version": (_I32, []),
     "st_last_error": (ctypes.c_char_p, []),
     "st_dequant4": (_I32, [_P, _P, _I64, _I32, _P, _I32, _P, _P]),
-    "st_dequant4_dq": (_I32, [_P, _P, _P, _P, _F, _I64, _P, _I32, _P, _P]),
     "st_q4_linear_fwd_workspace_bytes": (_I64, [_I64, _I64, _I64]),
     "st_q4_linear_fwd": (_I32, [_P, _I64, _I64, _I64, _P, _P, _I64, _P, _I32, _P, _I64, _P, _I32,
                                 _F, _I32, _P, _P, _I64, _P, _I64, _P, _I64, _P]),

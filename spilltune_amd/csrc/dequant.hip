@@ -103,31 +103,6 @@ __global__ __launch_bounds__(kThreads) void dequant4_scalar(const uint8_t* __res
   out[i] = st::f32_to_bf16(lut.v[code] * scales[i / group]);
 }
 
-// bitsandbytes double-quantised absmax, then the same decode (block 64).
-__global__ __launch_bounds__(kThreads) void dequant4_dq(const uint8_t* __restrict__ packed,
-                                                       const uint8_t* __restrict__ absmax_u8,
-                                                       const float* __restrict__ nested_absmax,
-                                                       const float* __restrict__ nested_map,
-                                                       float offset, int64_t numel, Lut16 lut,
-                                                       int hi_first,
-                                                       uint16_t* __restrict__ out) {
-  __shared__ float lut_s[16];
-  if (threadIdx.x < 16) lut_s[threadIdx.x] = lut.v[threadIdx.x];
-  __syncthreads();
-  // 2 elements (one byte) per thread
-  int64_t byte = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  int64_t i0 = byte * 2;
-  if (i0 >= numel) return;
-  int64_t j = i0 / 64;
-  float prod = nested_map[absmax_u8[j]] * nested_absmax[j / 256];
-  float amax = prod + offset;
-  unsigned b = packed[byte];
-  unsigned c0 = hi_first ? (b >> 4) : (b & 15u);
-  unsigned c1 = hi_first ? (b & 15u) : (b >> 4);
-  out[i0] = st::f32_to_bf16(lut_s[c0] * amax);
-  if (i0 + 1 < numel) out[i0 + 1] = st::f32_to_bf16(lut_s[c1] * amax);
-}
-
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 }  // namespace
@@ -186,20 +161,3 @@ extern "C" int st_dequant4(const uint8_t* payload, const float* scales, int64_t 
                              (hipStream_t)stream);
 }
 
-extern "C" int st_dequant4_dq(const uint8_t* packed, const uint8_t* absmax_u8,
-                              const float* nested_absmax, const float* nested_map, float offset,
-                              int64_t numel, const float* lut16, int32_t flags, uint16_t* out,
-                              st_stream_t stream) {
-  ST_CHECK_ARG(numel >= 0, "st_dequant4_dq: negative numel");
-  ST_CHECK_ARG(lut16 != nullptr, "st_dequant4_dq: lut16 is NULL");
-  if (numel == 0) return ST_OK;
-  ST_CHECK_ARG(packed && absmax_u8 && nested_absmax && nested_map && out,
-               "st_dequant4_dq: NULL device pointer");
-  Lut16 lut;
-  for (int i = 0; i < 16; ++i) lut.v[i] = lut16[i];
-  int hi = (flags & ST_FLAG_HI_NIBBLE_FIRST) ? 1 : 0;
-  int64_t bytes = st::cdiv(numel, 2);
-  dequant4_dq<<<(unsigned)st::cdiv(bytes, kThreads), kThreads, 0, (hipStream_t)stream>>>(
-      packed, absmax_u8, nested_absmax, nested_map, offset, numel, lut, hi, out);
-  return st::check_launch("dequant4_dq");
-}

@@ -67,7 +67,7 @@ def microbatch(model, session, input_ids, labels, *, normalization, token_chunk,
     terminal_input = hidden.detach().requires_grad_(True)
     normalized = model.terminal_norm(terminal_input)
     chunks = ops.supervised_chunk_intervals(labels, token_chunk)
-    loss = ops.chunked_causal_loss(normalized, model.head, labels.to(device),
+    loss = ops.chunked_causal_loss(normalized, model.head, labels,
                                    normalization=normalization, token_chunk=token_chunk,
                                    supervised_chunks=chunks)
     (gradient,) = torch.autograd.grad(loss, terminal_input)
@@ -111,7 +111,7 @@ def window_layer_major(model, session, items, *, normalization, token_chunk):
         terminal_input = mb["h"].pop().detach().requires_grad_(True)
         normalized = model.terminal_norm(terminal_input)
         loss = ops.chunked_causal_loss(
-            normalized, model.head, mb["labels"].to(device), normalization=normalization,
+            normalized, model.head, mb["labels"], normalization=normalization,
             token_chunk=token_chunk,
             supervised_chunks=ops.supervised_chunk_intervals(mb["labels"], token_chunk))
         (mb["g"],) = torch.autograd.grad(loss, terminal_input)

@@ -154,6 +154,31 @@ def _stream(dev):
     return _lib.stream_handle(dev)
 
 
+def sigmoid_router_logits(flat: torch.Tensor, router: torch.Tensor) -> torch.Tensor:
+    """fp32 router logits ``F.linear(flat.float(), router.float())`` of
+    deepseek.py:117 for bf16 ``flat [T, H]`` and a bf16 or fp32 ``router [E, H]``.
+
+    They run in slices of 64 experts on the streaming MFMA rank-r kernel,
+    which splits its fp32 operand into bf16 hi + lo parts (16 significant
+    bits).  A bf16 router passes that split exactly; an fp32 router (the
+    reference keeps DeepSeek routers in fp32) is first split as
+    ``w = bf16(w) + r``, where ``r`` holds at most 16 significant bits, so both
+    parts pass exactly: every product is the fp32 product, summed in fp32."""
+    T, H = flat.shape
+    E = router.shape[0]
+    logits = torch.empty((T, E), dtype=_F32, device=flat.device)
+    parts = [router.float()]
+    if router.dtype == _F32:
+        hi = router.to(_BF16).float()
+        parts = [hi, router - hi]
+    for e0 in range(0, E, 64):
+        e1 = min(E, e0 + 64)
+        for i, wp in enumerate(parts):
+            lora_gemm(T, e1 - e0, H, flat, H, 1, wp[e0:e1], 1, H, 1.0, logits[:, e0:e1],
+                      accumulate=i > 0)
+    return logits
+
+
 class _MoEFeedForward(torch.autograd.Function):
     @staticmethod
     def forward(ctx, flat, router, bias, gate_up, down, cfg, *lora):
@@ -172,14 +197,7 @@ class _MoEFeedForward(torch.autograd.Function):
         if sig:
             # deepseek.py:117-125: fp32 logits F.linear(hidden.float(), weight.float()),
             # sigmoid group-limited selection with the bias, fp32 weights * scale
-            # (bf16 products are exact in fp32; fp32 accumulation): the frozen
-            # router as fp32 (bf16-valued, so the kernel's hi/lo split of it is
-            # exact) in slices of 64 experts on the streaming MFMA rank-r kernel
-            logits = torch.empty((T, E), dtype=_F32, device=dev)
-            wf = router.float()
-            for e0 in range(0, E, 64):
-                e1 = min(E, e0 + 64)
-                lora_gemm(T, e1 - e0, H, flat, H, 1, wf[e0:e1], 1, H, 1.0, logits[:, e0:e1])
+            logits = sigmoid_router_logits(flat, router)
             _lib.call("st_moe_route_sigmoid", _lib.ptr(logits), _lib.ptr(bias), T, E, groups,
                       group_k, top_k, int(norm), float(rscale), _lib.ptr(weights),
                       _lib.ptr(indices), st)
@@ -390,7 +408,8 @@ def deepseek_moe_feed_forward(hidden, weights, *, num_experts, top_k, groups, gr
     weights are given: returns ``out + shared(x)`` in bf16, the operand the
     reference adds to the residual.
 
-    ``weights``: ``mlp.gate.weight`` (bf16 ``[E, H]``, frozen),
+    ``weights``: ``mlp.gate.weight`` (fp32 or bf16 ``[E, H]``, frozen; the
+    reference keeps DeepSeek routers in fp32, deepseek.py:81-83),
     ``mlp.gate.e_score_correction_bias`` (``[E]``), ``mlp.experts.gate_up_proj``
     / ``mlp.experts.down_proj`` (:class:`Q4Experts`) and optionally
     ``mlp.shared_experts.{gate,up,down}_proj.weight`` (:class:`~spilltune_amd.ops.Q4Weight`).
@@ -406,8 +425,9 @@ def deepseek_moe_feed_forward(hidden, weights, *, num_experts, top_k, groups, gr
         raise ValueError("unsupported_capability: experts must be Q4Experts")
     shape = hidden.shape
     flat = hidden.reshape(-1, shape[-1])
-    if flat.dtype != _BF16 or router.dtype != _BF16:
-        raise ValueError("deepseek_moe_feed_forward expects bf16 hidden states and router")
+    if flat.dtype != _BF16 or router.dtype not in (_BF16, _F32):
+        raise ValueError("deepseek_moe_feed_forward expects bf16 hidden states and a bf16 or "
+                         "fp32 router")
     E, H = router.shape
     I = down.in_features
     if (gate_up.experts, gate_up.out_features, gate_up.in_features) != (E, 2 * I, H) or \

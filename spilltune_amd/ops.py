@@ -94,10 +94,19 @@ def concat_rows(weights) -> Q4Weight | None:
         return None
     if (K % GROUP) != 0 or any(w.out_features % 32 for w in weights[:-1]):
         return None  # flat groups must not straddle parts; LoRA segments end on 32-column blocks
-    for a, b in zip(weights, weights[1:]):
-        if a.payload.data_ptr() + a.payload.numel() != b.payload.data_ptr():
+    # adjacency must hold inside ONE storage: two allocations that merely lie
+    # back to back are not one buffer (the view below would run off the first)
+    for part in ("payload", "scales"):
+        ts = [getattr(w, part) for w in weights]
+        storage = ts[0].untyped_storage()
+        if any(not t.is_contiguous() or t.dim() != 1 for t in ts):
             return None
-        if a.scales.data_ptr() + a.scales.numel() * 4 != b.scales.data_ptr():
+        off = ts[0].storage_offset()
+        for t in ts:
+            if t.untyped_storage().data_ptr() != storage.data_ptr() or t.storage_offset() != off:
+                return None
+            off += t.numel()
+        if off * ts[0].element_size() > storage.nbytes():
             return None
     rows = sum(w.out_features for w in weights)
     base_p, base_s = first.payload, first.scales
@@ -444,10 +453,12 @@ def linear_bf16_dgrad(dy: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
 
 def supervised_chunk_intervals(labels: torch.Tensor, token_chunk: int) -> tuple:
     """Token chunks [start, end) of the shifted targets that hold at least one
-    supervised label (native_terminal.py:44-46), from host labels."""
+    supervised label (native_terminal.py:44-46), from host labels (prepared
+    once per batch, before the step)."""
     if type(token_chunk) is not int or token_chunk < 1:
         raise ValueError("invalid terminal token chunk")
-    labels = labels.cpu()
+    if labels.device.type != "cpu":
+        raise RuntimeError("supervised chunks are prepared from host labels")
     S = labels.shape[1]
     return tuple((start, min(start + token_chunk, S - 1)) for start in range(0, S - 1, token_chunk)
                  if bool((labels[:, start + 1:min(start + token_chunk, S - 1) + 1] != -100).any()))
@@ -473,10 +484,15 @@ class _ChunkedCE(torch.autograd.Function):
         B, S, H = normalized.shape
         V = head.shape[0]
         dev = normalized.device
+        if labels.device.type == "cpu":
+            # host labels are checked here, before the copy; device labels are
+            # never scanned (a scan is a device->host sync inside the step,
+            # native_terminal.py:1-5): st_cross_entropy_rows turns a label
+            # outside [0, vocab) into a NaN row loss without reading the row
+            bad = ((labels < 0) & (labels != -100)) | (labels >= V)
+            if bool(bad.any()):
+                raise ValueError("terminal labels must be -100 or in [0, vocab)")
         labels = labels.to(dev, torch.int64)
-        bad = ((labels < 0) & (labels != -100)) | (labels >= V)
-        if bool(bad.any()):
-            raise ValueError("terminal labels must be -100 or in [0, vocab)")
         head = head.detach().contiguous()
         vjp = torch.zeros_like(normalized)
         total = torch.zeros((), dtype=_F32, device=dev)
@@ -511,8 +527,11 @@ def chunked_causal_loss(normalized, head, labels, *, normalization, token_chunk,
                         supervised_chunks=None):
     """``sum CE(shifted) / normalization`` with the chunked terminal above
     (native_terminal.py:39-47); chunk intervals default to those of the host
-    labels."""
+    labels.  Device labels need prepared ``supervised_chunks``: they are never
+    scanned on the host (native_terminal.py:41-42)."""
     if supervised_chunks is None:
+        if labels.device.type != "cpu":
+            raise RuntimeError("device terminal requires startup-prepared supervised chunks")
         supervised_chunks = supervised_chunk_intervals(labels, token_chunk)
     return _ChunkedCE.apply(normalized, head, labels, normalization, token_chunk,
                             tuple(supervised_chunks))

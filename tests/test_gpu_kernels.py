@@ -95,26 +95,6 @@ def test_dequant_unaligned_output_and_group64(dev, oracle_codec):
     assert buf[0].item() == 0 and buf[n + 1:].float().abs().sum().item() == 0
 
 
-def test_dequant_dq_vs_oracle(dev, oracle_codec):
-    rng = np.random.default_rng(2)
-    n = 64 * 1000 + 13
-    packed = rng.integers(0, 256, (n + 1) // 2, dtype=np.uint8)
-    blocks = (n + 63) // 64
-    u8 = rng.integers(0, 256, blocks, dtype=np.uint8)
-    nested = (rng.random((blocks + 255) // 256) + 0.5).astype(np.float32)
-    nmap = np.sort(rng.standard_normal(256)).astype(np.float32)
-    offset = 0.0123
-    expect = oracle_codec.decode4_dq(packed, u8, nested, nmap, offset, n)
-    out = torch.empty(n, dtype=BF, device=dev)
-    # keep every device input alive for the duration of the call
-    d_packed, d_u8, d_nested, d_map = (torch.from_numpy(a).to(dev) for a in (packed, u8, nested, nmap))
-    _lib.call("st_dequant4_dq", _lib.ptr(d_packed), _lib.ptr(d_u8), _lib.ptr(d_nested),
-              _lib.ptr(d_map), offset, n, _lib.lut_array(codecs.NF4_CODEBOOK),
-              _lib.ST_FLAG_HI_NIBBLE_FIRST, _lib.ptr(out), _lib.stream_handle(dev))
-    torch.cuda.synchronize()
-    assert torch.equal(out.cpu().view(torch.int16), bits_tensor(expect).view(torch.int16))
-
-
 # ---------------------------------------------------------------- GEMMs
 class _L:
     def __init__(self, A, B, alpha):

@@ -23,7 +23,7 @@ def cosine(a, b):
     return (a @ b / (a.norm() * b.norm()).clamp_min(1e-300)).item()
 
 
-def case(B, S, H, V, chunk, seed, ignore_every=0, dead_chunk=False):
+def case(B, S, H, V, chunk, seed, ignore_every=0, dead_chunk=False, oracle_chunk=None):
     g = torch.Generator().manual_seed(seed)
     hidden = torch.randn(B, S, H, generator=g).to(BF)
     norm = (1 + 0.1 * torch.randn(H, generator=g)).to(BF)
@@ -35,12 +35,16 @@ def case(B, S, H, V, chunk, seed, ignore_every=0, dead_chunk=False):
     if dead_chunk:
         labels[:, 1:chunk + 1] = -100  # the first chunk has no supervised target
     normalization = float((labels[:, 1:] != -100).sum().clamp_min(1))
+    # the oracle's chunking does not change the sum it computes; a smaller
+    # chunk only bounds its fp32 logits in host memory
     loss_ref, grad_ref = OL.causal_lm_terminal(hidden, norm, head, labels, eps=1e-5,
-                                               normalization=normalization, token_chunk=chunk)
+                                               normalization=normalization,
+                                               token_chunk=oracle_chunk or chunk)
     dev = torch.device("cuda:0")
     x = hidden.to(dev).requires_grad_(True)
     normalized = ops.rms_norm(x.view(B * S, H), norm.to(dev), 1e-5).view(B, S, H)
-    loss = ops.chunked_causal_loss(normalized, head.to(dev), labels.to(dev),
+    # host labels: checked and turned into supervised chunks on the host
+    loss = ops.chunked_causal_loss(normalized, head.to(dev), labels,
                                    normalization=normalization, token_chunk=chunk)
     (gx,) = torch.autograd.grad(loss, x)
     torch.cuda.synchronize()
@@ -60,6 +64,34 @@ def test_terminal_ignored_targets_and_unsupervised_chunk():
 
 def test_terminal_qwen3_vocab_rows():
     case(1, 96, 512, 151936, 40, 2)
+
+
+@pytest.mark.timeout(600)
+def test_terminal_qwen3_vocab_row_split():
+    """Config 3's vocabulary with a token chunk of 2 x 4095 = 8190 rows: the
+    bf16 logits block would pass the GEMM's 2 GiB operand limit, so the chunk
+    runs as 7067 + 1123 rows (ops._ChunkedCE's row split)."""
+    V = 151936
+    assert 2 * 4095 > ((1 << 31) - 1) // (2 * V)
+    case(2, 4096, 128, V, 4096, 4, ignore_every=5, oracle_chunk=512)
+
+
+def test_terminal_device_labels_with_prepared_chunks():
+    """Device labels with startup-prepared chunks (the reference's CUDA
+    terminal contract, native_terminal.py:39-47): no host scan, same loss."""
+    g = torch.Generator().manual_seed(5)
+    B, S, H, V, chunk = 2, 64, 128, 512, 16
+    hidden = torch.randn(B, S, H, generator=g).to(BF)
+    head = (0.05 * torch.randn(V, H, generator=g)).to(BF)
+    labels = torch.randint(0, V, (B, S), generator=g)
+    chunks = ops.supervised_chunk_intervals(labels, chunk)
+    dev = torch.device("cuda:0")
+    h = hidden.to(dev)
+    host = ops.chunked_causal_loss(h, head.to(dev), labels, normalization=100.0,
+                                   token_chunk=chunk)
+    device = ops.chunked_causal_loss(h, head.to(dev), labels.to(dev), normalization=100.0,
+                                     token_chunk=chunk, supervised_chunks=chunks)
+    assert float(host) == float(device)
 
 
 def test_cross_entropy_rows_matches_fp32_softmax():

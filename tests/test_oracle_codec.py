@@ -123,25 +123,6 @@ def test_hi_nibble_first_is_a_byte_swap(oracle_codec):
     np.testing.assert_array_equal(a, b)
 
 
-def test_dq_decode_reduces_to_plain_decode(oracle_codec):
-    """With a nested map whose entry k is k/255, nested absmax 1 and offset 0,
-    the double-quantised absmax of block j is exactly u8_j/255 (one fp32
-    multiply by 1): the DQ decode must equal the plain g64 decode with those
-    scales.  (bitsandbytes' own bytes stay unpinned.)"""
-    rng = np.random.default_rng(11)
-    n = 64 * 300 + 5
-    packed = rng.integers(0, 256, (n + 1) // 2, dtype=np.uint8)
-    blocks = (n + 63) // 64
-    u8 = rng.integers(0, 256, blocks, dtype=np.uint8)
-    nmap = (np.arange(256, dtype=np.float32) / np.float32(255)).astype(np.float32)
-    nested = np.ones((blocks + 255) // 256, dtype=np.float32)
-    got = oracle_codec.decode4_dq(packed, u8, nested, nmap, 0.0, n)
-    scales = nmap[u8]
-    plain = oracle_codec.decode4(packed, scales, n, lut=oracle_codec.NF4_LUT, group=64,
-                                 hi_first=True)
-    np.testing.assert_array_equal(got, plain)
-
-
 @pytest.mark.parametrize("case", range(5))
 @pytest.mark.parametrize("fmt", ["int4-sym-g128", "nf4-g128"])
 def test_product_host_encoder_matches_oracle(oracle_codec, case, fmt):
