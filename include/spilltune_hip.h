@@ -142,6 +142,23 @@ int st_lora_gemm(int64_t Mo, int64_t No, int64_t Kc,
                  void* workspace, int64_t workspace_bytes, st_stream_t stream);
 
 /*
+ * st_lora_gemm without a workspace argument, for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  The split-K partials live in
+ * a static 32 MiB device array of the library (one per GPU, held until the
+ * process ends); a product that needs more (st_lora_gemm_workspace_bytes >
+ * 32 MiB) is rejected with ST_EUNSUPPORTED.  Nothing is allocated or freed.
+ * Every call on one GPU shares that array: calls that overlap in time on one
+ * GPU (two streams, two threads) race and must be ordered by the caller.
+ * Results equal st_lora_gemm's bit for bit (same kernels, same order).
+ */
+int st_lora_gemm_noalloc(int64_t Mo, int64_t No, int64_t Kc,
+                         const void* a, int32_t a_dtype, int64_t sam, int64_t sak,
+                         const void* b, int32_t b_dtype, int64_t sbk, int64_t sbn,
+                         float alpha, float* out, int64_t ldo, int32_t accumulate,
+                         st_stream_t stream);
+
+/*
  * The two products of the LoRA VJP that read dY (the autograd of
  * finetune/lora.py:219 inside training/recompute.py:102-105), for a
  * projection of nseg N-concatenated segments (ends seg_end[], rank r each):

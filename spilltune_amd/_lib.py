@@ -41,6 +41,8 @@ _SIGNATURES = {
     "st_lora_gemm_workspace_bytes": (_I64, [_I64, _I64, _I64]),
     "st_lora_gemm": (_I32, [_I64, _I64, _I64, _P, _I32, _I64, _I64, _P, _I32, _I64, _I64, _F, _P,
                             _I64, _I32, _P, _I64, _P]),
+    "st_lora_gemm_noalloc": (_I32, [_I64, _I64, _I64, _P, _I32, _I64, _I64, _P, _I32, _I64, _I64,
+                                    _F, _P, _I64, _I32, _P]),
     "st_lora_bwd_dy_workspace_bytes": (_I64, [_I64, _I64, _I32, _I32, _P]),
     "st_lora_bwd_dy": (_I32, [_P, _I64, _I64, _I64, _P, _P, _I64, _I32, _I32, _P, _F, _P, _I64,
                               _P, _P, _I64, _P]),

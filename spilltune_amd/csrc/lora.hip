@@ -11,6 +11,8 @@
 // second kernel, so results are deterministic run to run.
 #include "rank_r.h"
 
+#include <mutex>
+
 namespace {
 
 constexpr int TM = 64, TN = 64, TK = 32, NTH = 256;
@@ -291,10 +293,12 @@ extern "C" int64_t st_lora_gemm_workspace_bytes(int64_t Mo, int64_t No, int64_t 
   return generic > rk ? generic : rk;
 }
 
-extern "C" int st_lora_gemm(int64_t Mo, int64_t No, int64_t Kc, const void* a, int32_t a_dtype,
-                            int64_t sam, int64_t sak, const void* b, int32_t b_dtype, int64_t sbk,
-                            int64_t sbn, float alpha, float* out, int64_t ldo, int32_t accumulate,
-                            void* workspace, int64_t workspace_bytes, st_stream_t stream) {
+namespace {
+
+int lora_gemm_impl(int64_t Mo, int64_t No, int64_t Kc, const void* a, int32_t a_dtype,
+                   int64_t sam, int64_t sak, const void* b, int32_t b_dtype, int64_t sbk,
+                   int64_t sbn, float alpha, float* out, int64_t ldo, int32_t accumulate,
+                   void* workspace, int64_t workspace_bytes, st_stream_t stream) {
   ST_CHECK_ARG(Mo >= 0 && No >= 0 && Kc >= 0, "st_lora_gemm: negative shape");
   if (Mo == 0 || No == 0) return ST_OK;
   ST_CHECK_ARG(out && ldo >= No, "st_lora_gemm: bad output");
@@ -375,6 +379,68 @@ extern "C" int st_lora_gemm(int64_t Mo, int64_t No, int64_t Kc, const void* a, i
   lora_reduce<<<(unsigned)st::cdiv(Mo * No, NTH), NTH, 0, s>>>(Mo, No, ks, part, alpha, out, ldo,
                                                                accumulate);
   return st::check_launch("lora_reduce");
+}
+
+// Scratch of the allocation-free variant: the split-K partials live in this
+// file-scope device array (one copy per GPU, held until the process ends).
+// Host code never passes `scratch` itself to a kernel -- on the host the name
+// is only a stand-in -- but the device address hipGetSymbolAddress returns,
+// fetched once per device and kept in scratch_ptr.
+constexpr int64_t kScratchBytes = 32ll << 20;
+constexpr int kMaxDevices = 64;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+void* scratch_ptr[kMaxDevices];
+std::mutex scratch_mu;
+
+int scratch_for_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return st::fail(ST_EDEVICE, "st_lora_gemm_noalloc: hipGetDevice: %s",
+                                       hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return st::fail(ST_EUNSUPPORTED, "st_lora_gemm_noalloc: device %d beyond %d", dev,
+                    kMaxDevices);
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (!scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return st::fail(ST_EDEVICE, "st_lora_gemm_noalloc: hipGetSymbolAddress: %s",
+                      hipGetErrorString(e));
+    scratch_ptr[dev] = p;
+  }
+  *out = scratch_ptr[dev];
+  return ST_OK;
+}
+
+}  // namespace
+
+extern "C" int st_lora_gemm(int64_t Mo, int64_t No, int64_t Kc, const void* a, int32_t a_dtype,
+                            int64_t sam, int64_t sak, const void* b, int32_t b_dtype, int64_t sbk,
+                            int64_t sbn, float alpha, float* out, int64_t ldo, int32_t accumulate,
+                            void* workspace, int64_t workspace_bytes, st_stream_t stream) {
+  return lora_gemm_impl(Mo, No, Kc, a, a_dtype, sam, sak, b, b_dtype, sbk, sbn, alpha, out, ldo,
+                        accumulate, workspace, workspace_bytes, stream);
+}
+
+extern "C" int st_lora_gemm_noalloc(int64_t Mo, int64_t No, int64_t Kc, const void* a,
+                                    int32_t a_dtype, int64_t sam, int64_t sak, const void* b,
+                                    int32_t b_dtype, int64_t sbk, int64_t sbn, float alpha,
+                                    float* out, int64_t ldo, int32_t accumulate,
+                                    st_stream_t stream) {
+  ST_CHECK_ARG(Mo >= 0 && No >= 0 && Kc >= 0, "st_lora_gemm_noalloc: negative shape");
+  const int64_t need = st_lora_gemm_workspace_bytes(Mo, No, Kc);
+  if (need > kScratchBytes)
+    return st::fail(ST_EUNSUPPORTED,
+                    "st_lora_gemm_noalloc: the product needs %lld scratch bytes, more than the "
+                    "%lld-byte static scratch (use st_lora_gemm with a workspace)",
+                    (long long)need, (long long)kScratchBytes);
+  void* ws = nullptr;
+  if (need > 0) {
+    if (int rc = scratch_for_current_device(&ws)) return rc;
+  }
+  return lora_gemm_impl(Mo, No, Kc, a, a_dtype, sam, sak, b, b_dtype, sbk, sbn, alpha, out, ldo,
+                        accumulate, ws, kScratchBytes, stream);
 }
 
 // ------------------------------------------- backward rank-r products of dY
