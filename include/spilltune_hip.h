@@ -28,6 +28,8 @@
  *  - adapters/dense.py:115-117 rms, :137-141 rotate, :153 silu(gate)*up
  *                                          -> st_rmsnorm_*, st_rope_*, st_swiglu_*
  *  - adapters/dense.py:142-148 eager GQA attention -> st_flash_attn_*
+ *  - adapters/deepseek.py:129-157 MLA attention (q/kv latent projections,
+ *    shared rope key, qk 192 against v 128)   -> st_mla_*
  *  - adapters/qwen3_moe.py:95-113 and adapters/deepseek.py:115-176 (routers
  *    and the routed-expert loop)          -> st_moe_*, st_q4_grouped_*,
  *                                             st_linear_bf16_*
@@ -249,6 +251,51 @@ int st_flash_attn_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                       int64_t S, int64_t H, int64_t Hkv, int64_t D, float scale, uint16_t* dq,
                       uint16_t* dk, uint16_t* dv, void* workspace, int64_t workspace_bytes,
                       st_stream_t stream);
+
+/* ---------------------------------------------------------------------
+ * Causal multi-head latent attention of DeepSeek-V3 (adapters/deepseek.py:
+ * 150-153: query = cat(q_nope, rotate(q_rope)), key = cat(k_nope,
+ * rotate(k_rope) shared by every head), scores * attention_scale + causal
+ * mask, fp32 softmax, probabilities @ value), the same flash kernels with
+ * query/key heads of DQ and value heads of DV: q, k [B,H,S,DQ], v [B,H,S,DV]
+ * head-major bf16 (no grouping: every head has its own key); out token-major
+ * [B,S,H*DV]; lse [B,H,S] as st_flash_attn_fwd.  (DQ, DV) = (192, 128), the
+ * V3 shape (qk_nope 128 + qk_rope 64, v 128), or 64/64, 128/128.
+ * --------------------------------------------------------------------- */
+/* Query/key/value assembly of deepseek.py:137-150 (and its VJP): from q
+ * [M, H*(nope+rope)] (row stride ldq; per head q_nope | q_rope), kv
+ * [M, H*(nope+v_dim)] (ldkv; per head k_nope | value) and the shared rope key
+ * kr [M, rope] (ldkr; the last rope columns of kv_a_proj_with_mqa), M = B*S
+ * token rows, writes Q = cat(q_nope, rotate(q_rope)) and K = cat(k_nope,
+ * rotate(kr)) [B,H,S,nope+rope] and V [B,H,S,v_dim].  rotate is the default
+ * (t*cos + cat(-t2, t1)*sin) or, with interleave, the pairwise form of
+ * deepseek.py:146-148; cos/sin [B,S,rope] bf16; every product and sum rounds to
+ * bf16 as the reference's bf16 ops do.  nope, v_dim % 8 == 0; rope % 16 == 0,
+ * rope <= 128 and dividing 256. */
+int st_mla_rope_fwd(const uint16_t* q, int64_t ldq, const uint16_t* kv, int64_t ldkv,
+                    const uint16_t* kr, int64_t ldkr, const uint16_t* cos, const uint16_t* sin,
+                    int64_t B, int64_t S, int64_t H, int64_t nope, int64_t rope, int64_t v_dim,
+                    int32_t interleave, uint16_t* Q, uint16_t* K, uint16_t* V,
+                    st_stream_t stream);
+/* VJP: dq [M, H*(nope+rope)], dkv [M, H*(nope+v_dim)] and dkr [M, rope] (the
+ * rope key's gradient: the sum over heads of dK's rope part, rounded once to
+ * bf16, through the VJP of rotate). */
+int st_mla_rope_bwd(const uint16_t* dQ, const uint16_t* dK, const uint16_t* dV,
+                    const uint16_t* cos, const uint16_t* sin, int64_t B, int64_t S, int64_t H,
+                    int64_t nope, int64_t rope, int64_t v_dim, int32_t interleave, uint16_t* dq,
+                    int64_t lddq, uint16_t* dkv, int64_t lddkv, uint16_t* dkr, int64_t lddkr,
+                    st_stream_t stream);
+int64_t st_mla_attn_workspace_bytes(int64_t B, int64_t S, int64_t H, int64_t DQ, int64_t DV,
+                                    int32_t backward);
+int st_mla_attn_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, int64_t B,
+                    int64_t S, int64_t H, int64_t DQ, int64_t DV, float scale, uint16_t* out,
+                    float* lse, void* workspace, int64_t workspace_bytes, st_stream_t stream);
+/* VJP of st_mla_attn_fwd: dq, dk [B,H,S,DQ], dv [B,H,S,DV]. */
+int st_mla_attn_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                    const uint16_t* out, const float* lse, const uint16_t* dout, int64_t B,
+                    int64_t S, int64_t H, int64_t DQ, int64_t DV, float scale, uint16_t* dq,
+                    uint16_t* dk, uint16_t* dv, void* workspace, int64_t workspace_bytes,
+                    st_stream_t stream);
 
 /* ---------------------------------------------------------------------
  * Plain bf16 linear (router logits and their input gradient).

@@ -2,9 +2,12 @@
 // deterministic passes), replacing the eager scores/softmax/probabilities
 // chain of adapters/dense.py:142-148.
 //
-// Layout: q [B, H, S, D], k/v [B, Hkv, S, D] (head-major bf16); the output is
-// written token-major [B, S, H*D]; lse [B, H, S] fp32 is the base-2 log-sum-exp
-// of each query row of x = scale * log2(e) * q.k.
+// Layout: q [B, H, S, DQ], k [B, Hkv, S, DQ], v [B, Hkv, S, DV] (head-major
+// bf16); the output is written token-major [B, S, H*DV]; lse [B, H, S] fp32 is
+// the base-2 log-sum-exp of each query row of x = scale * log2(e) * q.k.
+// DQ = DV = D for the dense layers (adapters/dense.py:142-148); DeepSeek's
+// multi-head latent attention has query/key heads of DQ = 192 (128 + 64 rope
+// dims) against value heads of DV = 128 (adapters/deepseek.py:150-153).
 //
 // Transposed formulation: every MFMA tile is S^T = K Q^T (rows = keys,
 // columns = queries), so one lane owns one query column: the softmax max/sum
@@ -94,36 +97,36 @@ template <int BKT>
 constexpr int VSLOTS = BKT / 8 + 1;      // per padded V^T row
 constexpr float RESCALE_LOG2 = 8.0f;     // running max may lag by up to 2^8
 
-template <int D, int BKT, int G>
+template <int DQ, int DV, int BKT, int G>
 constexpr int fwd_lds_elems() {
-  return G * 2 * (BKT * KSLOTS<D> + D * VSLOTS<BKT>) * 8;
+  return G * 2 * (BKT * KSLOTS<DQ> + DV * VSLOTS<BKT>) * 8;
 }
 
 // G = 1: 4 waves over all keys.  G = 2: 8 waves in two groups of 4 over the
 // same queries, group r taking K/V tiles r, r+2, ...; group 1's softmax state
 // (max, partial sums, O) is merged into group 0's at the end.
-template <int D, int BKT, int G>
+template <int DQ, int DV, int BKT, int G>
 __device__ __forceinline__ void fa_fwd_tile(const uint16_t* __restrict__ q,
                                             const uint16_t* __restrict__ k,
                                             const uint16_t* __restrict__ vt, int S, int H,
                                             int Hkv, float sl2, uint16_t* __restrict__ out,
                                             float* __restrict__ lse, int qt, int h, int b,
                                             uint16_t* lds) {
-  constexpr int DS = D / 16;   // contraction steps over d
-  constexpr int DB = D / 32;   // 32-row d blocks of O^T
-  constexpr int KS = KSLOTS<D>, VS = VSLOTS<BKT>;
-  constexpr int LK = BKT * KS * 8, LV = D * VS * 8;  // bf16 per padded tile
-  constexpr int KI = BKT * KS / 64, VI = D * VS / 64;  // wave copies (1 KiB each) per tile
-  static_assert((BKT * KS) % 64 == 0 && (D * VS) % 64 == 0, "tiles are whole wave copies");
+  constexpr int DS = DQ / 16;  // contraction steps over the query/key dims
+  constexpr int DB = DV / 32;  // 32-row blocks of O^T
+  constexpr int KS = KSLOTS<DQ>, VS = VSLOTS<BKT>;
+  constexpr int LK = BKT * KS * 8, LV = DV * VS * 8;  // bf16 per padded tile
+  constexpr int KI = BKT * KS / 64, VI = DV * VS / 64;  // wave copies (1 KiB each) per tile
+  static_assert((BKT * KS) % 64 == 0 && (DV * VS) % 64 == 0, "tiles are whole wave copies");
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int grp = (tid >> 6) / 4, wave = (tid >> 6) % 4;  // key group, wave in group
   const int g = lane >> 5, c = lane & 31;
   const int hk = h / (H / Hkv);
-  const uint16_t* qb = q + ((int64_t)(b * H + h) * S) * D;
-  const uint16_t* kb = k + ((int64_t)(b * Hkv + hk) * S) * D;
+  const uint16_t* qb = q + ((int64_t)(b * H + h) * S) * DQ;
+  const uint16_t* kb = k + ((int64_t)(b * Hkv + hk) * S) * DQ;
   const int Sp = (S + 15) & ~15;                // staged V^T row length
-  const uint16_t* vb = vt + ((int64_t)(b * Hkv + hk) * D) * Sp;
+  const uint16_t* vb = vt + ((int64_t)(b * Hkv + hk) * DV) * Sp;
   const int q0 = qt * BQ + wave * 32;
   const int myq = q0 + c;
   uint16_t* glds = lds + grp * 2 * (LK + LV);   // this group's two tile buffers
@@ -131,7 +134,7 @@ __device__ __forceinline__ void fa_fwd_tile(const uint16_t* __restrict__ q,
   bf16x8 qf[DS];
 #pragma unroll
   for (int s = 0; s < DS; ++s)
-    qf[s] = as_bf16x8(myq < S ? ld_global16(qb + (int64_t)myq * D + 16 * s + 8 * g)
+    qf[s] = as_bf16x8(myq < S ? ld_global16(qb + (int64_t)myq * DQ + 16 * s + 8 * g)
                               : make_uint4(0, 0, 0, 0));
 
   f32x16 oacc[DB];
@@ -156,7 +159,7 @@ __device__ __forceinline__ void fa_fwd_tile(const uint16_t* __restrict__ q,
         const int P = wi * 64 + lane;
         const int row = min(P / KS, BKT - 1), ch = P % KS;
         const int key = min(k0 + row, S - 1);
-        g2lds16(kb + (int64_t)key * D + min(ch, D / 8 - 1) * 8, ks + wi * 64 * 8);
+        g2lds16(kb + (int64_t)key * DQ + min(ch, DQ / 8 - 1) * 8, ks + wi * 64 * 8);
       }
     }
 #pragma unroll
@@ -164,7 +167,7 @@ __device__ __forceinline__ void fa_fwd_tile(const uint16_t* __restrict__ q,
       const int wi = i * 4 + wave;
       if (wi < VI) {
         const int P = wi * 64 + lane;
-        const int d = min(P / VS, D - 1), ch = min(P % VS, BKT / 8 - 1);
+        const int d = min(P / VS, DV - 1), ch = min(P % VS, BKT / 8 - 1);
         const int col = min(k0 + ch * 8, Sp - 8);
         g2lds16(vb + (int64_t)d * Sp + col, vs + wi * 64 * 8);
       }
@@ -331,7 +334,7 @@ __device__ __forceinline__ void fa_fwd_tile(const uint16_t* __restrict__ q,
   const float inv = 1.0f / l_tot;
   if (g == 0 && myq < S) lse[((int64_t)(b * H + h)) * S + myq] = m_run + log2f(l_tot);
   // stage O (query rows) through LDS for 16-byte token-major stores
-  constexpr int LDO = D + 8;
+  constexpr int LDO = DV + 8;
   uint16_t* os = lds + wave * 32 * LDO;
 #pragma unroll
   for (int db = 0; db < DB; ++db)
@@ -345,14 +348,14 @@ __device__ __forceinline__ void fa_fwd_tile(const uint16_t* __restrict__ q,
   // each wave reads back only its own rows: a wave-level fence suffices
   __builtin_amdgcn_s_waitcnt(0);
   __builtin_amdgcn_wave_barrier();
-  const int64_t ld_out = (int64_t)H * D;
-  for (int i = lane; i < 32 * (D / 8); i += 64) {
-    const int r = i / (D / 8), ch = i % (D / 8);
+  const int64_t ld_out = (int64_t)H * DV;
+  for (int i = lane; i < 32 * (DV / 8); i += 64) {
+    const int r = i / (DV / 8), ch = i % (DV / 8);
     const int qq = q0 + r;
     if (qq < S) {
       const u32x2 a = *(const u32x2*)(os + r * LDO + ch * 8);
       const u32x2 bb = *(const u32x2*)(os + r * LDO + ch * 8 + 4);
-      *(uint4*)(out + ((int64_t)b * S + qq) * ld_out + (int64_t)h * D + ch * 8) =
+      *(uint4*)(out + ((int64_t)b * S + qq) * ld_out + (int64_t)h * DV + ch * 8) =
           make_uint4(a.x, a.y, bb.x, bb.y);
     }
   }
@@ -365,12 +368,12 @@ __device__ __forceinline__ int pair_tile(int x, int it, int nq, int paired) {
   return it == 0 ? nq - 1 - x : x;
 }
 
-template <int D, int BKT, int G>
-__global__ __launch_bounds__(NTH * G, G == 1 && BKT == 64 ? 2 : 1) void fa_fwd(
+template <int DQ, int DV, int BKT, int G>
+__global__ __launch_bounds__(NTH * G, G == 1 && BKT == 64 && DQ <= 128 ? 2 : 1) void fa_fwd(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ vt, int S, int H, int Hkv, float sl2,
     uint16_t* __restrict__ out, float* __restrict__ lse, int nq, int paired) {
-  __shared__ __attribute__((aligned(16))) uint16_t lds[fwd_lds_elems<D, BKT, G>()];
+  __shared__ __attribute__((aligned(16))) uint16_t lds[fwd_lds_elems<DQ, DV, BKT, G>()];
   const WgIdx w = wg_index(paired ? (nq + 1) / 2 : nq, H);
   for (int it = 0; it < 1 + paired; ++it) {
     const int qt = pair_tile(w.x, it, nq, paired);
@@ -378,7 +381,7 @@ __global__ __launch_bounds__(NTH * G, G == 1 && BKT == 64 ? 2 : 1) void fa_fwd(
       if (qt == pair_tile(w.x, 0, nq, paired)) break;
       __syncthreads();  // the previous tile's output staging still reads LDS
     }
-    fa_fwd_tile<D, BKT, G>(q, k, vt, S, H, Hkv, sl2, out, lse, qt, w.h, w.b, lds);
+    fa_fwd_tile<DQ, DV, BKT, G>(q, k, vt, S, H, Hkv, sl2, out, lse, qt, w.h, w.b, lds);
   }
 }
 
@@ -416,41 +419,43 @@ __device__ __forceinline__ bf16x8 tile_tr(const uint16_t* t, int kb, int nb, int
 // dQ (and Delta = rowsum(dO * O)) per 128-query tile: S^T = K Q^T,
 // P^T = exp2(S^T - lse), dP^T = V dO^T, dS^T = P^T (dP^T - Delta),
 // dQ^T += K^T dS^T; keys up to the diagonal.
-template <int D, int BKT, int G>
+template <int DQ, int DV, int BKT, int G>
 __device__ __forceinline__ void fa_bwd_dq_tile(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ o,
     const uint16_t* __restrict__ dout, const float* __restrict__ lse, int S, int H, int Hkv,
     float sl2, float scale, float* __restrict__ delta, uint16_t* __restrict__ dq, int qt, int h,
     int b, uint16_t* lds) {
-  constexpr int DS = D / 16, DB = D / 32;
-  constexpr int LT = BKT * D;           // bf16 per K (or V) tile
-  constexpr int PER = BKT * D / 8 / NTH;  // 16-byte chunks per thread per tile
+  constexpr int DSQ = DQ / 16, DSV = DV / 16, DB = DQ / 32;
+  constexpr int LTK = BKT * DQ, LTV = BKT * DV;  // bf16 per K / V tile
+  constexpr int PERK = BKT * DQ / 8 / NTH, PERV = BKT * DV / 8 / NTH;  // 16-byte chunks per thread
+  static_assert(PERK * NTH * 8 == LTK && PERV * NTH * 8 == LTV, "tiles are whole thread copies");
   const int tid = threadIdx.x, lane = tid & 63;
   const int grp = (tid >> 6) / 4, wave = (tid >> 6) % 4;  // key group, wave in group
   const int gtid = tid % NTH;
   const int g = lane >> 5, c = lane & 31;
   const int hk = h / (H / Hkv);
-  const int64_t ldt = (int64_t)H * D;  // token-major row stride
-  const uint16_t* qb = q + ((int64_t)(b * H + h) * S) * D;
-  const uint16_t* kb = k + ((int64_t)(b * Hkv + hk) * S) * D;
-  const uint16_t* vb = v + ((int64_t)(b * Hkv + hk) * S) * D;
+  const int64_t ldt = (int64_t)H * DV;  // token-major row stride of O and dO
+  const uint16_t* qb = q + ((int64_t)(b * H + h) * S) * DQ;
+  const uint16_t* kb = k + ((int64_t)(b * Hkv + hk) * S) * DQ;
+  const uint16_t* vb = v + ((int64_t)(b * Hkv + hk) * S) * DV;
   const int q0 = qt * BQ + wave * 32;
   const int myq = q0 + c;
   const bool qok = myq < S;
-  const int64_t trow = ((int64_t)b * S + myq) * ldt + (int64_t)h * D;
-  uint16_t* glds = lds + grp * 2 * 2 * LT;  // this group's two K|V buffers
+  const int64_t trow = ((int64_t)b * S + myq) * ldt + (int64_t)h * DV;
+  uint16_t* glds = lds + grp * 2 * (LTK + LTV);  // this group's two K|V buffers
 
-  bf16x8 qf[DS], dof[DS];
+  bf16x8 qf[DSQ], dof[DSV];
   float dl = 0.0f;
+  const uint4 z = make_uint4(0, 0, 0, 0);
 #pragma unroll
-  for (int s = 0; s < DS; ++s) {
+  for (int s = 0; s < DSQ; ++s)
+    qf[s] = as_bf16x8(qok ? ld_global16(qb + (int64_t)myq * DQ + 16 * s + 8 * g) : z);
+#pragma unroll
+  for (int s = 0; s < DSV; ++s) {
     const int d = 16 * s + 8 * g;
-    const uint4 z = make_uint4(0, 0, 0, 0);
-    const uint4 qv = qok ? ld_global16(qb + (int64_t)myq * D + d) : z;
     const uint4 gv = qok ? ld_global16(dout + trow + d) : z;
     const uint4 ov = qok ? ld_global16(o + trow + d) : z;
-    qf[s] = as_bf16x8(qv);
     dof[s] = as_bf16x8(gv);
     const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, ow[4] = {ov.x, ov.y, ov.z, ov.w};
 #pragma unroll
@@ -476,16 +481,21 @@ __device__ __forceinline__ void fa_bwd_dq_tile(
   // rows past S read a clamped (finite) row, masked out below
   auto issue = [&](int t, int buf) {
     const int k0 = t * BKT;
-    uint16_t* ks = glds + buf * 2 * LT;
-    uint16_t* vs = ks + LT;
+    uint16_t* ks = glds + buf * (LTK + LTV);
+    uint16_t* vs = ks + LTK;
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
+    for (int i = 0; i < PERK; ++i) {
       const int P = i * NTH + gtid;
-      const int row = P / (D / 8);
-      const int ch = (P % (D / 8)) ^ (((row & 7) << 1) & (D / 8 - 1));
-      const int64_t off = (int64_t)min(k0 + row, S - 1) * D + ch * 8;
-      g2lds16(kb + off, ks + (i * NTH + wave * 64) * 8);
-      g2lds16(vb + off, vs + (i * NTH + wave * 64) * 8);
+      const int row = P / (DQ / 8);
+      const int ch = (P % (DQ / 8)) ^ (((row & 7) << 1) & (DQ / 8 - 1));
+      g2lds16(kb + (int64_t)min(k0 + row, S - 1) * DQ + ch * 8, ks + (i * NTH + wave * 64) * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < PERV; ++i) {
+      const int P = i * NTH + gtid;
+      const int row = P / (DV / 8);
+      const int ch = (P % (DV / 8)) ^ (((row & 7) << 1) & (DV / 8 - 1));
+      g2lds16(vb + (int64_t)min(k0 + row, S - 1) * DV + ch * 8, vs + (i * NTH + wave * 64) * 8);
     }
   };
   // one 32-key block: S^T, dP^T, dS^T (masked when `edge`), dQ^T += K^T dS^T
@@ -494,11 +504,12 @@ __device__ __forceinline__ void fa_bwd_dq_tile(
 #pragma unroll
     for (int e = 0; e < 16; ++e) { sacc[e] = 0.0f; pacc[e] = 0.0f; }
 #pragma unroll
-    for (int s = 0; s < DS; ++s) {
-      sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_row<D>(ks, jb * 32 + c, s, g), qf[s],
+    for (int s = 0; s < DSQ; ++s) {
+      sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_row<DQ>(ks, jb * 32 + c, s, g), qf[s],
                                                      sacc, 0, 0, 0);
-      pacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_row<D>(vs, jb * 32 + c, s, g), dof[s],
-                                                     pacc, 0, 0, 0);
+      if (s < DSV)
+        pacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_row<DV>(vs, jb * 32 + c, s, g),
+                                                       dof[s < DSV ? s : 0], pacc, 0, 0, 0);
     }
     bf16x8 dsf[2];
 #pragma unroll
@@ -520,7 +531,7 @@ __device__ __forceinline__ void fa_bwd_dq_tile(
 #pragma unroll
       for (int db = 0; db < DB; ++db)
         dqacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            tile_tr<D>(ks, jb * 32 + 16 * hh, db * 32, lane), dsf[hh], dqacc[db], 0, 0, 0);
+            tile_tr<DQ>(ks, jb * 32 + 16 * hh, db * 32, lane), dsf[hh], dqacc[db], 0, 0, 0);
   };
   if (grp < ntiles) issue(grp, 0);
   __builtin_amdgcn_s_waitcnt(0);
@@ -529,8 +540,8 @@ __device__ __forceinline__ void fa_bwd_dq_tile(
     const int buf = u & 1;
     const int t = u * G + grp;
     if (t + G < ntiles) issue(t + G, buf ^ 1);
-    const uint16_t* ks = glds + buf * 2 * LT;
-    const uint16_t* vs = ks + LT;
+    const uint16_t* ks = glds + buf * (LTK + LTV);
+    const uint16_t* vs = ks + LTK;
     const int k0 = t * BKT;
     if (t < ntiles) {
 #pragma unroll
@@ -562,7 +573,7 @@ __device__ __forceinline__ void fa_bwd_dq_tile(
     if (grp == 1) return;
   }
   // dQ = scale * dQ^T^T, staged through LDS as query rows, head-major out
-  constexpr int LDO = D + 8;
+  constexpr int LDO = DQ + 8;
   uint16_t* os = lds + wave * 32 * LDO;
 #pragma unroll
   for (int db = 0; db < DB; ++db)
@@ -575,25 +586,25 @@ __device__ __forceinline__ void fa_bwd_dq_tile(
     }
   __builtin_amdgcn_s_waitcnt(0);
   __builtin_amdgcn_wave_barrier();  // each wave reads back only its own rows
-  uint16_t* dqb = dq + ((int64_t)(b * H + h) * S) * D;
-  for (int i = lane; i < 32 * (D / 8); i += 64) {
-    const int r = i / (D / 8), ch = i % (D / 8);
+  uint16_t* dqb = dq + ((int64_t)(b * H + h) * S) * DQ;
+  for (int i = lane; i < 32 * (DQ / 8); i += 64) {
+    const int r = i / (DQ / 8), ch = i % (DQ / 8);
     const int qq = q0 + r;
     if (qq < S) {
       const u32x2 a = *(const u32x2*)(os + r * LDO + ch * 8);
       const u32x2 bb = *(const u32x2*)(os + r * LDO + ch * 8 + 4);
-      *(uint4*)(dqb + (int64_t)qq * D + ch * 8) = make_uint4(a.x, a.y, bb.x, bb.y);
+      *(uint4*)(dqb + (int64_t)qq * DQ + ch * 8) = make_uint4(a.x, a.y, bb.x, bb.y);
     }
   }
 }
-template <int D, int BKT, int G>
-__global__ __launch_bounds__(NTH * G, G == 1 && BKT == 64 ? 2 : 1) void fa_bwd_dq(
+template <int DQ, int DV, int BKT, int G>
+__global__ __launch_bounds__(NTH * G, G == 1 && BKT == 64 && DQ <= 128 ? 2 : 1) void fa_bwd_dq(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ o,
     const uint16_t* __restrict__ dout, const float* __restrict__ lse, int S, int H, int Hkv,
     float sl2, float scale, float* __restrict__ delta, uint16_t* __restrict__ dq, int nq,
     int paired) {
-  __shared__ __attribute__((aligned(16))) uint16_t lds[G * 2 * 2 * BKT * D];
+  __shared__ __attribute__((aligned(16))) uint16_t lds[G * 2 * BKT * (DQ + DV)];
   const WgIdx w = wg_index(paired ? (nq + 1) / 2 : nq, H);
   for (int it = 0; it < 1 + paired; ++it) {
     const int qt = pair_tile(w.x, it, nq, paired);
@@ -601,8 +612,8 @@ __global__ __launch_bounds__(NTH * G, G == 1 && BKT == 64 ? 2 : 1) void fa_bwd_d
       if (qt == pair_tile(w.x, 0, nq, paired)) break;
       __syncthreads();
     }
-    fa_bwd_dq_tile<D, BKT, G>(q, k, v, o, dout, lse, S, H, Hkv, sl2, scale, delta, dq, qt, w.h,
-                              w.b, lds);
+    fa_bwd_dq_tile<DQ, DV, BKT, G>(q, k, v, o, dout, lse, S, H, Hkv, sl2, scale, delta, dq, qt,
+                                   w.h, w.b, lds);
   }
 }
 
@@ -610,49 +621,68 @@ __global__ __launch_bounds__(NTH * G, G == 1 && BKT == 64 ? 2 : 1) void fa_bwd_d
 // query halves), looping over 64-query tiles from the diagonal down:
 // S = Q K^T, P = exp2(S - lse), dP = dO V^T, dS = P (dP - Delta),
 // dV^T += dO^T P, dK^T += Q^T dS.  Writes fp32 per-query-head partials.
+// NBUF Q|dO buffers: 2 overlaps the next tile's copy with this one's MFMAs;
+// 1 when two do not fit in LDS next to the resident K and V (DQ = 192).
 constexpr int KT2 = 128, QT2 = 64, NTH2 = 512;
 
-template <int D>
+template <int DQ, int DV>
+constexpr int dkdv_nbuf() {
+  return (KT2 + 2 * QT2) * (DQ + DV) * 2 + 2 * 2 * QT2 * 4 <= 160 * 1024 ? 2 : 1;
+}
+template <int DQ, int DV>
+constexpr int dkdv_lds_elems() {
+  return (KT2 + dkdv_nbuf<DQ, DV>() * QT2) * (DQ + DV);
+}
+
+template <int DQ, int DV>
 __device__ __forceinline__ void fa_bwd_dkdv_tile(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, int S, int H, int Hkv,
     float sl2, float scale, float* __restrict__ dk_part, float* __restrict__ dv_part, int kt,
     int h, int b, uint16_t* lds, float (*lse_s)[QT2], float (*dl_s)[QT2]) {
-  constexpr int DS = D / 16, DB = D / 32;
-  constexpr int LK = KT2 * D, LQ = QT2 * D;
-  constexpr int PERQ = QT2 * D / 8 / NTH2;   // 16-byte chunks per thread per Q (dO) tile
+  constexpr int NBUF = dkdv_nbuf<DQ, DV>();
+  constexpr int DSQ = DQ / 16, DSV = DV / 16, DBQ = DQ / 32, DBV = DV / 32;
+  constexpr int LK = KT2 * DQ, LV = KT2 * DV, LQ = QT2 * DQ, LG = QT2 * DV;
+  constexpr int PERQ = LQ / 8 / NTH2, PERG = LG / 8 / NTH2;  // 16-byte chunks per thread
+  static_assert(PERQ * NTH2 * 8 == LQ && PERG * NTH2 * 8 == LG, "tiles are whole thread copies");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, c = lane & 31;
   const int kq = wave & 3, qh = wave >> 2;
   const int hk = h / (H / Hkv);
-  const int64_t ldt = (int64_t)H * D;
-  const uint16_t* qb = q + ((int64_t)(b * H + h) * S) * D;
-  const uint16_t* kb = k + ((int64_t)(b * Hkv + hk) * S) * D;
-  const uint16_t* vb = v + ((int64_t)(b * Hkv + hk) * S) * D;
-  const uint16_t* gb = dout + (int64_t)b * S * ldt + (int64_t)h * D;
+  const int64_t ldt = (int64_t)H * DV;
+  const uint16_t* qb = q + ((int64_t)(b * H + h) * S) * DQ;
+  const uint16_t* kb = k + ((int64_t)(b * Hkv + hk) * S) * DQ;
+  const uint16_t* vb = v + ((int64_t)(b * Hkv + hk) * S) * DV;
+  const uint16_t* gb = dout + (int64_t)b * S * ldt + (int64_t)h * DV;
   const int64_t srow = (int64_t)(b * H + h) * S;
   uint16_t* Ks = lds;
   uint16_t* Vs = lds + LK;
   const int k0 = kt * KT2;
 
   // resident K and V tiles
-  for (int id = tid; id < KT2 * D / 8; id += NTH2) {
-    const int row = id / (D / 8), ch = id % (D / 8);
-    const bool ok = k0 + row < S;
-    *(uint4*)(Ks + tswz<D>(row, ch)) =
-        ok ? ld_global16(kb + (int64_t)(k0 + row) * D + ch * 8) : make_uint4(0, 0, 0, 0);
-    *(uint4*)(Vs + tswz<D>(row, ch)) =
-        ok ? ld_global16(vb + (int64_t)(k0 + row) * D + ch * 8) : make_uint4(0, 0, 0, 0);
+  for (int id = tid; id < KT2 * DQ / 8; id += NTH2) {
+    const int row = id / (DQ / 8), ch = id % (DQ / 8);
+    *(uint4*)(Ks + tswz<DQ>(row, ch)) = k0 + row < S
+        ? ld_global16(kb + (int64_t)(k0 + row) * DQ + ch * 8) : make_uint4(0, 0, 0, 0);
+  }
+  for (int id = tid; id < KT2 * DV / 8; id += NTH2) {
+    const int row = id / (DV / 8), ch = id % (DV / 8);
+    *(uint4*)(Vs + tswz<DV>(row, ch)) = k0 + row < S
+        ? ld_global16(vb + (int64_t)(k0 + row) * DV + ch * 8) : make_uint4(0, 0, 0, 0);
   }
   const int kw0 = k0 + kq * 32;   // this wave's keys
   const int mykey = kw0 + c;
 
-  f32x16 dvacc[DB], dkacc[DB];
+  f32x16 dvacc[DBV], dkacc[DBQ];
 #pragma unroll
-  for (int i = 0; i < DB; ++i)
+  for (int i = 0; i < DBV; ++i)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) { dvacc[i][e] = 0.0f; dkacc[i][e] = 0.0f; }
+    for (int e = 0; e < 16; ++e) dvacc[i][e] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < DBQ; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) dkacc[i][e] = 0.0f;
 
   const int qt_first = k0 / QT2;
   const int qt_end = (S + QT2 - 1) / QT2;
@@ -661,15 +691,22 @@ __device__ __forceinline__ void fa_bwd_dkdv_tile(
   // (rows past S read a clamped row, masked below); lse and Delta via VGPRs
   auto issue = [&](int qt, int buf) {
     const int q0 = qt * QT2;
-    uint16_t* qs = lds + 2 * LK + buf * 2 * LQ;
+    uint16_t* qs = lds + LK + LV + buf * (LQ + LG);
     uint16_t* gs = qs + LQ;
 #pragma unroll
     for (int i = 0; i < PERQ; ++i) {
       const int P = i * NTH2 + tid;
-      const int row = P / (D / 8);
-      const int ch = (P % (D / 8)) ^ (((row & 7) << 1) & (D / 8 - 1));
+      const int row = P / (DQ / 8);
+      const int ch = (P % (DQ / 8)) ^ (((row & 7) << 1) & (DQ / 8 - 1));
       const int qq = min(q0 + row, S - 1);
-      g2lds16(qb + (int64_t)qq * D + ch * 8, qs + (i * NTH2 + wave * 64) * 8);
+      g2lds16(qb + (int64_t)qq * DQ + ch * 8, qs + (i * NTH2 + wave * 64) * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < PERG; ++i) {
+      const int P = i * NTH2 + tid;
+      const int row = P / (DV / 8);
+      const int ch = (P % (DV / 8)) ^ (((row & 7) << 1) & (DV / 8 - 1));
+      const int qq = min(q0 + row, S - 1);
       g2lds16(gb + (int64_t)qq * ldt + ch * 8, gs + (i * NTH2 + wave * 64) * 8);
     }
     if (tid < QT2) {
@@ -688,9 +725,16 @@ __device__ __forceinline__ void fa_bwd_dkdv_tile(
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   for (int qt = qt_first; qt < qt_end; ++qt) {
-    const int buf = (qt - qt_first) & 1;
-    if (qt + 1 < qt_end) issue(qt + 1, buf ^ 1);
-    const uint16_t* qs = lds + 2 * LK + buf * 2 * LQ;
+    const int buf = NBUF == 2 ? (qt - qt_first) & 1 : 0;
+    if (NBUF == 2 && qt + 1 < qt_end) issue(qt + 1, buf ^ 1);
+    if (NBUF == 1 && qt > qt_first) {
+      // one buffer: load this tile after every wave left the previous one
+      issue(qt, 0);
+      stats(0);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
+    const uint16_t* qs = lds + LK + LV + buf * (LQ + LG);
     const uint16_t* gs = qs + LQ;
     const int qw0 = qt * QT2 + qh * 32;   // this wave's queries
     if (qw0 + 31 >= kw0 && qw0 < S) {     // some query sees some key
@@ -698,13 +742,14 @@ __device__ __forceinline__ void fa_bwd_dkdv_tile(
 #pragma unroll
       for (int e = 0; e < 16; ++e) { sacc[e] = 0.0f; pacc[e] = 0.0f; }
 #pragma unroll
-      for (int s = 0; s < DS; ++s) {
-        sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_row<D>(qs, qh * 32 + c, s, g),
-                                                       tile_row<D>(Ks, kq * 32 + c, s, g), sacc,
+      for (int s = 0; s < DSQ; ++s) {
+        sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_row<DQ>(qs, qh * 32 + c, s, g),
+                                                       tile_row<DQ>(Ks, kq * 32 + c, s, g), sacc,
                                                        0, 0, 0);
-        pacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_row<D>(gs, qh * 32 + c, s, g),
-                                                       tile_row<D>(Vs, kq * 32 + c, s, g), pacc,
-                                                       0, 0, 0);
+        if (s < DSV)
+          pacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_row<DV>(gs, qh * 32 + c, s, g),
+                                                         tile_row<DV>(Vs, kq * 32 + c, s, g),
+                                                         pacc, 0, 0, 0);
       }
       bf16x8 pf[2], dsf[2];
 #pragma unroll
@@ -728,64 +773,84 @@ __device__ __forceinline__ void fa_bwd_dkdv_tile(
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-        for (int db = 0; db < DB; ++db) {
-          dvacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-              tile_tr<D>(gs, qh * 32 + 16 * hh, db * 32, lane), pf[hh], dvacc[db], 0, 0, 0);
+        for (int db = 0; db < DBQ; ++db) {
+          if (db < DBV)
+            dvacc[db < DBV ? db : 0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                tile_tr<DV>(gs, qh * 32 + 16 * hh, db * 32, lane), pf[hh],
+                dvacc[db < DBV ? db : 0], 0, 0, 0);
           dkacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-              tile_tr<D>(qs, qh * 32 + 16 * hh, db * 32, lane), dsf[hh], dkacc[db], 0, 0, 0);
+              tile_tr<DQ>(qs, qh * 32 + 16 * hh, db * 32, lane), dsf[hh], dkacc[db], 0, 0, 0);
         }
     }
-    if (qt + 1 < qt_end) stats(buf ^ 1);
+    if (NBUF == 2 && qt + 1 < qt_end) stats(buf ^ 1);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
   // the two query halves of each key quarter: qh = 1 parks its sums in LDS,
-  // qh = 0 adds them and writes [key][d] fp32 partials
-  float* red = (float*)lds;                 // 4 quarters x 2 arrays x (DB*16*64) floats
-  constexpr int PART = DB * 16 * 64;
+  // qh = 0 adds them and writes [key][d] fp32 partials; dV first, then dK
+  // (4 quarters x DB*16*64 floats at a time)
+  float* red = (float*)lds;
+  constexpr int PARTV = DBV * 16 * 64, PARTK = DBQ * 16 * 64;
+  static_assert(4 * PARTK * 4 <= dkdv_lds_elems<DQ, DV>() * 2, "dK partials fit in LDS");
   if (qh == 1) {
 #pragma unroll
-    for (int db = 0; db < DB; ++db)
+    for (int db = 0; db < DBV; ++db)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        red[(kq * 2 + 0) * PART + (db * 16 + e) * 64 + lane] = dvacc[db][e];
-        red[(kq * 2 + 1) * PART + (db * 16 + e) * 64 + lane] = dkacc[db][e];
-      }
+      for (int e = 0; e < 16; ++e) red[kq * PARTV + (db * 16 + e) * 64 + lane] = dvacc[db][e];
   }
   __syncthreads();
   if (qh == 0 && mykey < S) {
-    float* dvp = dv_part + (srow + mykey) * D;
-    float* dkp = dk_part + (srow + mykey) * D;
+    float* dvp = dv_part + (srow + mykey) * DV;
 #pragma unroll
-    for (int db = 0; db < DB; ++db)
+    for (int db = 0; db < DBV; ++db)
 #pragma unroll
       for (int v4 = 0; v4 < 4; ++v4) {
-        const int d = db * 32 + v4 * 8 + g * 4;
-        float4 a, bq;
+        float4 a;
         float* pa = &a.x;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int vv = 4 * v4 + e;
+          pa[e] = dvacc[db][vv] + red[kq * PARTV + (db * 16 + vv) * 64 + lane];
+        }
+        *(float4*)(dvp + db * 32 + v4 * 8 + g * 4) = a;
+      }
+  }
+  __syncthreads();
+  if (qh == 1) {
+#pragma unroll
+    for (int db = 0; db < DBQ; ++db)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) red[kq * PARTK + (db * 16 + e) * 64 + lane] = dkacc[db][e];
+  }
+  __syncthreads();
+  if (qh == 0 && mykey < S) {
+    float* dkp = dk_part + (srow + mykey) * DQ;
+#pragma unroll
+    for (int db = 0; db < DBQ; ++db)
+#pragma unroll
+      for (int v4 = 0; v4 < 4; ++v4) {
+        float4 bq;
         float* pb = &bq.x;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int vv = 4 * v4 + e;
-          pa[e] = dvacc[db][vv] + red[(kq * 2 + 0) * PART + (db * 16 + vv) * 64 + lane];
-          pb[e] = (dkacc[db][vv] + red[(kq * 2 + 1) * PART + (db * 16 + vv) * 64 + lane]) * scale;
+          pb[e] = (dkacc[db][vv] + red[kq * PARTK + (db * 16 + vv) * 64 + lane]) * scale;
         }
-        *(float4*)(dvp + d) = a;
-        *(float4*)(dkp + d) = bq;
+        *(float4*)(dkp + db * 32 + v4 * 8 + g * 4) = bq;
       }
   }
 }
 
 // key tiles kt and n-1-kt in one workgroup: the causal query range of the two
 // sums to a constant, so every workgroup does the same work
-template <int D>
-__global__ __launch_bounds__(NTH2, 2) void fa_bwd_dkdv(
+template <int DQ, int DV>
+__global__ __launch_bounds__(NTH2, DQ <= 128 ? 2 : 1) void fa_bwd_dkdv(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, int S, int H, int Hkv,
     float sl2, float scale, float* __restrict__ dk_part, float* __restrict__ dv_part, int nk,
     int paired) {
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * KT2 * D + 2 * 2 * QT2 * D];
+  __shared__ __attribute__((aligned(16))) uint16_t lds[dkdv_lds_elems<DQ, DV>()];
   __shared__ float lse_s[2][QT2], dl_s[2][QT2];
   const WgIdx w = wg_index(paired ? (nk + 1) / 2 : nk, H);
   for (int it = 0; it < 1 + paired; ++it) {
@@ -794,34 +859,33 @@ __global__ __launch_bounds__(NTH2, 2) void fa_bwd_dkdv(
       if (kt == w.x) break;
       __syncthreads();  // the previous tile's partial sums still occupy LDS
     }
-    fa_bwd_dkdv_tile<D>(q, k, v, dout, lse, delta, S, H, Hkv, sl2, scale, dk_part, dv_part, kt,
-                        w.h, w.b, lds, lse_s, dl_s);
+    fa_bwd_dkdv_tile<DQ, DV>(q, k, v, dout, lse, delta, S, H, Hkv, sl2, scale, dk_part, dv_part,
+                             kt, w.h, w.b, lds, lse_s, dl_s);
   }
 }
 
 // dk[b,hk] = bf16(sum over the group's query heads of dk_part), same for dv
+// (head dims DQ and DV; the sums run over the heads in ascending order)
 __global__ __launch_bounds__(NTH) void fa_bwd_reduce(const float* __restrict__ dk_part,
                                                      const float* __restrict__ dv_part,
-                                                     int64_t B, int64_t S, int H, int Hkv, int D,
-                                                     uint16_t* __restrict__ dk,
+                                                     int64_t B, int64_t S, int H, int Hkv, int DQ,
+                                                     int DV, uint16_t* __restrict__ dk,
                                                      uint16_t* __restrict__ dv) {
-  const int64_t per = S * D;
-  const int64_t n = B * Hkv * per / 4;
+  const int64_t nk = B * Hkv * S * DQ / 4, n = nk + B * Hkv * S * DV / 4;
   const int grp = H / Hkv;
   for (int64_t i = (int64_t)blockIdx.x * NTH + threadIdx.x; i < n; i += (int64_t)gridDim.x * NTH) {
-    const int64_t e = i * 4;
+    const bool isk = i < nk;
+    const int64_t per = S * (isk ? DQ : DV);
+    const int64_t e = (isk ? i : i - nk) * 4;
     const int64_t bh = e / per, off = e % per;
     const int64_t b = bh / Hkv, hk = bh % Hkv;
-    float4 sk = make_float4(0, 0, 0, 0), sv = make_float4(0, 0, 0, 0);
+    const float* part = isk ? dk_part : dv_part;
+    float4 sk = make_float4(0, 0, 0, 0);
     for (int j = 0; j < grp; ++j) {
-      const int64_t src = ((b * H + hk * grp + j) * per) + off;
-      const float4 a = *(const float4*)(dk_part + src);
-      const float4 bb = *(const float4*)(dv_part + src);
+      const float4 a = *(const float4*)(part + ((b * H + hk * grp + j) * per) + off);
       sk.x += a.x; sk.y += a.y; sk.z += a.z; sk.w += a.w;
-      sv.x += bb.x; sv.y += bb.y; sv.z += bb.z; sv.w += bb.w;
     }
-    *(u32x2*)(dk + e) = u32x2{st::pack_bf16x2(sk.x, sk.y), st::pack_bf16x2(sk.z, sk.w)};
-    *(u32x2*)(dv + e) = u32x2{st::pack_bf16x2(sv.x, sv.y), st::pack_bf16x2(sv.z, sv.w)};
+    *(u32x2*)((isk ? dk : dv) + e) = u32x2{st::pack_bf16x2(sk.x, sk.y), st::pack_bf16x2(sk.z, sk.w)};
   }
 }
 
@@ -835,59 +899,142 @@ int pair_mode(int nq, int64_t heads) {
   return nq >= 4 && nq * heads <= 1024 ? 1 : 0;
 }
 
+int64_t attn_workspace(int64_t B, int64_t S, int64_t H, int64_t Hkv, int64_t DQ, int64_t DV,
+                       int backward) {
+  if (!backward) return B * Hkv * ((S + 15) & ~15) * DV * 2 + 256;  // key-permuted V^T
+  // Delta [B,H,S] fp32, then fp32 dK and dV partials per query head
+  const int64_t dl = (B * H * S * 4 + 255) / 256 * 256;
+  return 256 + dl + B * H * S * (DQ + DV) * 4;
+}
+
+template <int DQ, int DV>
+int attn_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, int64_t B, int64_t S,
+             int64_t H, int64_t Hkv, float scale, uint16_t* out, float* lse, void* workspace,
+             hipStream_t s) {
+  uint16_t* vt = (uint16_t*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
+  const int64_t Sp = (S + 15) & ~15;
+  transpose_heads<<<dim3((unsigned)st::cdiv(Sp, 64), (unsigned)st::cdiv(DV, 64),
+                         (unsigned)(B * Hkv)), NTH, 0, s>>>(v, vt, S, Sp, DV);
+  int rc = st::check_launch("transpose_heads");
+  if (rc) return rc;
+  const int nq = (int)st::cdiv(S, BQ);
+  // paired schedules use two key groups (8 waves) so each SIMD still holds
+  // two waves; with DQ = 192 two groups' tiles do not fit in LDS
+  const int paired = DQ <= 128 ? pair_mode(nq, B * H) : 0;
+  dim3 grid((unsigned)((paired ? (nq + 1) / 2 : nq) * H * B));
+  const float sl2 = scale * LOG2E;
+  if (paired)
+    fa_fwd<DQ, DV, 64, (DQ <= 128 ? 2 : 1)><<<grid, NTH * (DQ <= 128 ? 2 : 1), 0, s>>>(
+        q, k, vt, (int)S, (int)H, (int)Hkv, sl2, out, lse, nq, paired);
+  else
+    fa_fwd<DQ, DV, 64, 1><<<grid, NTH, 0, s>>>(q, k, vt, (int)S, (int)H, (int)Hkv, sl2, out, lse,
+                                               nq, paired);
+  return st::check_launch("fa_fwd");
+}
+
+template <int DQ, int DV>
+int attn_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* out,
+             const float* lse, const uint16_t* dout, int64_t B, int64_t S, int64_t H, int64_t Hkv,
+             float scale, uint16_t* dq, uint16_t* dk, uint16_t* dv, void* workspace,
+             hipStream_t s) {
+  char* base = (char*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
+  float* delta = (float*)base;
+  float* dk_part = (float*)(base + (B * H * S * 4 + 255) / 256 * 256);
+  float* dv_part = dk_part + B * H * S * DQ;
+  const float sl2 = scale * LOG2E;
+  const int nq = (int)st::cdiv(S, BQ);
+  const int paired = DQ <= 128 ? pair_mode(nq, B * H) : 0;
+  dim3 g1((unsigned)((paired ? (nq + 1) / 2 : nq) * H * B));
+  const int nk = (int)st::cdiv(S, KT2);
+  const int paired_k = pair_mode(nk, B * H);
+  dim3 g2((unsigned)((paired_k ? (nk + 1) / 2 : nk) * H * B));
+  if (paired)
+    fa_bwd_dq<DQ, DV, 64, (DQ <= 128 ? 2 : 1)><<<g1, NTH * (DQ <= 128 ? 2 : 1), 0, s>>>(
+        q, k, v, out, dout, lse, (int)S, (int)H, (int)Hkv, sl2, scale, delta, dq, nq, paired);
+  else
+    fa_bwd_dq<DQ, DV, 64, 1><<<g1, NTH, 0, s>>>(q, k, v, out, dout, lse, (int)S, (int)H,
+                                                (int)Hkv, sl2, scale, delta, dq, nq, paired);
+  int rc = st::check_launch("fa_bwd_dq");
+  if (rc) return rc;
+  fa_bwd_dkdv<DQ, DV><<<g2, NTH2, 0, s>>>(q, k, v, dout, lse, delta, (int)S, (int)H, (int)Hkv,
+                                          sl2, scale, dk_part, dv_part, nk, paired_k);
+  rc = st::check_launch("fa_bwd_dkdv");
+  if (rc) return rc;
+  const int64_t n4 = B * Hkv * S * (DQ + DV) / 4;
+  const unsigned blocks = (unsigned)std::min<int64_t>(st::cdiv(n4, NTH), 4096);
+  fa_bwd_reduce<<<blocks, NTH, 0, s>>>(dk_part, dv_part, B, S, (int)H, (int)Hkv, DQ, DV, dk, dv);
+  return st::check_launch("fa_bwd_reduce");
+}
+
+bool dims_ok(int64_t DQ, int64_t DV) {
+  return (DQ == 64 && DV == 64) || (DQ == 128 && DV == 128) || (DQ == 192 && DV == 128);
+}
+
+int fwd_common(const char* name, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+               int64_t B, int64_t S, int64_t H, int64_t Hkv, int64_t DQ, int64_t DV, float scale,
+               uint16_t* out, float* lse, void* workspace, int64_t workspace_bytes,
+               st_stream_t stream) {
+  ST_CHECK_ARG(B >= 0 && S >= 0 && H > 0 && Hkv > 0 && H % Hkv == 0, "%s: bad head counts", name);
+  if (B == 0 || S == 0) return ST_OK;
+  if (!dims_ok(DQ, DV))
+    return st::fail(ST_EUNSUPPORTED, "%s: head dims %lld/%lld (64/64, 128/128 or 192/128 only)",
+                    name, (long long)DQ, (long long)DV);
+  ST_CHECK_ARG(S % 8 == 0 && S < (1 << 30), "%s: S must be a multiple of 8", name);
+  ST_CHECK_ARG(q && k && v && out && lse && al16(q) && al16(k) && al16(v) && al16(out),
+               "%s: NULL or unaligned pointer", name);
+  const int64_t need = attn_workspace(B, S, H, Hkv, DQ, DV, 0);
+  if (!workspace || workspace_bytes < need)
+    return st::fail(ST_EWORKSPACE, "%s: needs %lld workspace bytes", name, (long long)need);
+  hipStream_t s = (hipStream_t)stream;
+  if (DQ == 64) return attn_fwd<64, 64>(q, k, v, B, S, H, Hkv, scale, out, lse, workspace, s);
+  if (DQ == 128) return attn_fwd<128, 128>(q, k, v, B, S, H, Hkv, scale, out, lse, workspace, s);
+  return attn_fwd<192, 128>(q, k, v, B, S, H, Hkv, scale, out, lse, workspace, s);
+}
+
+int bwd_common(const char* name, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+               const uint16_t* out, const float* lse, const uint16_t* dout, int64_t B, int64_t S,
+               int64_t H, int64_t Hkv, int64_t DQ, int64_t DV, float scale, uint16_t* dq,
+               uint16_t* dk, uint16_t* dv, void* workspace, int64_t workspace_bytes,
+               st_stream_t stream) {
+  ST_CHECK_ARG(B >= 0 && S >= 0 && H > 0 && Hkv > 0 && H % Hkv == 0, "%s: bad head counts", name);
+  if (B == 0 || S == 0) return ST_OK;
+  if (!dims_ok(DQ, DV))
+    return st::fail(ST_EUNSUPPORTED, "%s: head dims %lld/%lld (64/64, 128/128 or 192/128 only)",
+                    name, (long long)DQ, (long long)DV);
+  ST_CHECK_ARG(S % 8 == 0 && S < (1 << 30), "%s: S must be a multiple of 8", name);
+  ST_CHECK_ARG(q && k && v && out && lse && dout && dq && dk && dv && al16(q) && al16(k) &&
+                   al16(v) && al16(out) && al16(dout) && al16(dq) && al16(dk) && al16(dv),
+               "%s: NULL or unaligned pointer", name);
+  const int64_t need = attn_workspace(B, S, H, Hkv, DQ, DV, 1);
+  if (!workspace || workspace_bytes < need)
+    return st::fail(ST_EWORKSPACE, "%s: needs %lld workspace bytes", name, (long long)need);
+  hipStream_t s = (hipStream_t)stream;
+  if (DQ == 64)
+    return attn_bwd<64, 64>(q, k, v, out, lse, dout, B, S, H, Hkv, scale, dq, dk, dv, workspace,
+                            s);
+  if (DQ == 128)
+    return attn_bwd<128, 128>(q, k, v, out, lse, dout, B, S, H, Hkv, scale, dq, dk, dv,
+                              workspace, s);
+  return attn_bwd<192, 128>(q, k, v, out, lse, dout, B, S, H, Hkv, scale, dq, dk, dv, workspace,
+                            s);
+}
+
 }  // namespace
 
 extern "C" int64_t st_flash_attn_workspace_bytes(int64_t B, int64_t S, int64_t H, int64_t Hkv,
                                                  int64_t D, int32_t backward) {
-  const int64_t kv = B * Hkv * ((S + 15) & ~15) * D * 2;
-  if (!backward) return kv + 256;  // key-permuted V^T
-  // Delta [B,H,S] fp32, then fp32 dK and dV partials per query head
-  const int64_t dl = (B * H * S * 4 + 255) / 256 * 256;
-  return 256 + dl + 2 * B * H * S * D * 4;
+  return attn_workspace(B, S, H, Hkv, D, D, backward);
 }
 
 extern "C" int st_flash_attn_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                                  int64_t B, int64_t S, int64_t H, int64_t Hkv, int64_t D,
                                  float scale, uint16_t* out, float* lse, void* workspace,
                                  int64_t workspace_bytes, st_stream_t stream) {
-  ST_CHECK_ARG(B >= 0 && S >= 0 && H > 0 && Hkv > 0 && H % Hkv == 0,
-               "st_flash_attn_fwd: bad head counts");
-  if (B == 0 || S == 0) return ST_OK;
   if (D != 64 && D != 128)
     return st::fail(ST_EUNSUPPORTED, "st_flash_attn_fwd: head_dim %lld (64 or 128 only)",
                     (long long)D);
-  ST_CHECK_ARG(S % 8 == 0 && S < (1 << 30), "st_flash_attn_fwd: S must be a multiple of 8");
-  ST_CHECK_ARG(q && k && v && out && lse && al16(q) && al16(k) && al16(v) && al16(out),
-               "st_flash_attn_fwd: NULL or unaligned pointer");
-  const int64_t need = st_flash_attn_workspace_bytes(B, S, H, Hkv, D, 0);
-  if (!workspace || workspace_bytes < need)
-    return st::fail(ST_EWORKSPACE, "st_flash_attn_fwd: needs %lld workspace bytes",
-                    (long long)need);
-  hipStream_t s = (hipStream_t)stream;
-  uint16_t* vt = (uint16_t*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
-  const int64_t Sp = (S + 15) & ~15;
-  transpose_heads<<<dim3((unsigned)st::cdiv(Sp, 64), (unsigned)st::cdiv(D, 64),
-                         (unsigned)(B * Hkv)), NTH, 0, s>>>(v, vt, S, Sp, (int)D);
-  int rc = st::check_launch("transpose_heads");
-  if (rc) return rc;
-  const int nq = (int)st::cdiv(S, BQ);
-  const int paired = pair_mode(nq, B * H);
-  dim3 grid((unsigned)((paired ? (nq + 1) / 2 : nq) * H * B));
-  const float sl2 = scale * LOG2E;
-  // paired schedules use two key groups (8 waves) so each SIMD still holds two waves
-  if (D == 128 && paired)
-    fa_fwd<128, 64, 2><<<grid, NTH * 2, 0, s>>>(q, k, vt, (int)S, (int)H, (int)Hkv, sl2, out,
-                                                lse, nq, paired);
-  else if (D == 128)
-    fa_fwd<128, 64, 1><<<grid, NTH, 0, s>>>(q, k, vt, (int)S, (int)H, (int)Hkv, sl2, out, lse,
-                                            nq, paired);
-  else if (paired)
-    fa_fwd<64, 64, 2><<<grid, NTH * 2, 0, s>>>(q, k, vt, (int)S, (int)H, (int)Hkv, sl2, out,
-                                               lse, nq, paired);
-  else
-    fa_fwd<64, 64, 1><<<grid, NTH, 0, s>>>(q, k, vt, (int)S, (int)H, (int)Hkv, sl2, out, lse,
-                                           nq, paired);
-  return st::check_launch("fa_fwd");
+  return fwd_common("st_flash_attn_fwd", q, k, v, B, S, H, Hkv, D, D, scale, out, lse, workspace,
+                    workspace_bytes, stream);
 }
 
 extern "C" int st_flash_attn_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
@@ -895,59 +1042,31 @@ extern "C" int st_flash_attn_bwd(const uint16_t* q, const uint16_t* k, const uin
                                  int64_t B, int64_t S, int64_t H, int64_t Hkv, int64_t D,
                                  float scale, uint16_t* dq, uint16_t* dk, uint16_t* dv,
                                  void* workspace, int64_t workspace_bytes, st_stream_t stream) {
-  ST_CHECK_ARG(B >= 0 && S >= 0 && H > 0 && Hkv > 0 && H % Hkv == 0,
-               "st_flash_attn_bwd: bad head counts");
-  if (B == 0 || S == 0) return ST_OK;
   if (D != 64 && D != 128)
     return st::fail(ST_EUNSUPPORTED, "st_flash_attn_bwd: head_dim %lld (64 or 128 only)",
                     (long long)D);
-  ST_CHECK_ARG(S % 8 == 0 && S < (1 << 30), "st_flash_attn_bwd: S must be a multiple of 8");
-  ST_CHECK_ARG(q && k && v && out && lse && dout && dq && dk && dv && al16(q) && al16(k) &&
-                   al16(v) && al16(out) && al16(dout) && al16(dq) && al16(dk) && al16(dv),
-               "st_flash_attn_bwd: NULL or unaligned pointer");
-  const int64_t need = st_flash_attn_workspace_bytes(B, S, H, Hkv, D, 1);
-  if (!workspace || workspace_bytes < need)
-    return st::fail(ST_EWORKSPACE, "st_flash_attn_bwd: needs %lld workspace bytes",
-                    (long long)need);
-  hipStream_t s = (hipStream_t)stream;
-  char* base = (char*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
-  float* delta = (float*)base;
-  float* dk_part = (float*)(base + (B * H * S * 4 + 255) / 256 * 256);
-  float* dv_part = dk_part + B * H * S * D;
-  const float sl2 = scale * LOG2E;
-  const int nq = (int)st::cdiv(S, BQ);
-  const int paired = pair_mode(nq, B * H);
-  dim3 g1((unsigned)((paired ? (nq + 1) / 2 : nq) * H * B));
-  const int nk = (int)st::cdiv(S, KT2);
-  const int paired_k = pair_mode(nk, B * H);
-  dim3 g2((unsigned)((paired_k ? (nk + 1) / 2 : nk) * H * B));
-  if (D == 128) {
-    if (paired)
-      fa_bwd_dq<128, 64, 2><<<g1, NTH * 2, 0, s>>>(q, k, v, out, dout, lse, (int)S, (int)H,
-                                                   (int)Hkv, sl2, scale, delta, dq, nq, paired);
-    else
-      fa_bwd_dq<128, 64, 1><<<g1, NTH, 0, s>>>(q, k, v, out, dout, lse, (int)S, (int)H, (int)Hkv,
-                                               sl2, scale, delta, dq, nq, paired);
-    int rc = st::check_launch("fa_bwd_dq");
-    if (rc) return rc;
-    fa_bwd_dkdv<128><<<g2, NTH2, 0, s>>>(q, k, v, dout, lse, delta, (int)S, (int)H, (int)Hkv,
-                                         sl2, scale, dk_part, dv_part, nk, paired_k);
-  } else {
-    if (paired)
-      fa_bwd_dq<64, 64, 2><<<g1, NTH * 2, 0, s>>>(q, k, v, out, dout, lse, (int)S, (int)H,
-                                                  (int)Hkv, sl2, scale, delta, dq, nq, paired);
-    else
-      fa_bwd_dq<64, 64, 1><<<g1, NTH, 0, s>>>(q, k, v, out, dout, lse, (int)S, (int)H, (int)Hkv,
-                                              sl2, scale, delta, dq, nq, paired);
-    int rc = st::check_launch("fa_bwd_dq");
-    if (rc) return rc;
-    fa_bwd_dkdv<64><<<g2, NTH2, 0, s>>>(q, k, v, dout, lse, delta, (int)S, (int)H, (int)Hkv,
-                                        sl2, scale, dk_part, dv_part, nk, paired_k);
-  }
-  int rc = st::check_launch("fa_bwd_dkdv");
-  if (rc) return rc;
-  const int64_t n4 = B * Hkv * S * D / 4;
-  const unsigned blocks = (unsigned)std::min<int64_t>(st::cdiv(n4, NTH), 4096);
-  fa_bwd_reduce<<<blocks, NTH, 0, s>>>(dk_part, dv_part, B, S, (int)H, (int)Hkv, (int)D, dk, dv);
-  return st::check_launch("fa_bwd_reduce");
+  return bwd_common("st_flash_attn_bwd", q, k, v, out, lse, dout, B, S, H, Hkv, D, D, scale, dq,
+                    dk, dv, workspace, workspace_bytes, stream);
+}
+
+extern "C" int64_t st_mla_attn_workspace_bytes(int64_t B, int64_t S, int64_t H, int64_t DQ,
+                                               int64_t DV, int32_t backward) {
+  return attn_workspace(B, S, H, H, DQ, DV, backward);
+}
+
+extern "C" int st_mla_attn_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                               int64_t B, int64_t S, int64_t H, int64_t DQ, int64_t DV,
+                               float scale, uint16_t* out, float* lse, void* workspace,
+                               int64_t workspace_bytes, st_stream_t stream) {
+  return fwd_common("st_mla_attn_fwd", q, k, v, B, S, H, H, DQ, DV, scale, out, lse, workspace,
+                    workspace_bytes, stream);
+}
+
+extern "C" int st_mla_attn_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                               const uint16_t* out, const float* lse, const uint16_t* dout,
+                               int64_t B, int64_t S, int64_t H, int64_t DQ, int64_t DV,
+                               float scale, uint16_t* dq, uint16_t* dk, uint16_t* dv,
+                               void* workspace, int64_t workspace_bytes, st_stream_t stream) {
+  return bwd_common("st_mla_attn_bwd", q, k, v, out, lse, dout, B, S, H, H, DQ, DV, scale, dq, dk,
+                    dv, workspace, workspace_bytes, stream);
 }

@@ -129,7 +129,9 @@ def create_lora_for_block(block_idx: int, block_type: str, weight_shapes: dict, 
 
 # projections the dense functional runs as one N-concatenated GEMM
 FUSED_GROUPS = (("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj"),
-                ("mlp.gate_proj", "mlp.up_proj"))
+                ("mlp.gate_proj", "mlp.up_proj"),
+                ("self_attn.q_a_proj", "self_attn.kv_a_proj_with_mqa"),
+                ("mlp.shared_experts.gate_proj", "mlp.shared_experts.up_proj"))
 
 
 def share_fused_storage(adapters: dict, groups=FUSED_GROUPS) -> None:

@@ -647,6 +647,102 @@ def causal_attention(q, k, v, scale):
     return _CausalAttention.apply(q.contiguous(), k.contiguous(), v.contiguous(), float(scale))
 
 
+# ----------------------------------------------------------------- MLA (DeepSeek-V3)
+class _MLARope(torch.autograd.Function):
+    """q [M, H*(nope+rope)], kv [M, H*(nope+v)] and the shared rope key
+    ``comp[:, kv_rank:kv_rank+rope]`` -> Q, K [B,H,S,nope+rope], V [B,H,S,v]
+    (deepseek.py:137-150).  The VJP returns dq, dkv and a gradient of ``comp``
+    holding only the rope key's columns (the latent columns get theirs through
+    the kv path)."""
+
+    @staticmethod
+    def forward(ctx, q, kv, comp, cos, sin, B, S, heads, nope, rope, v_dim, kv_rank, interleave):
+        dev = q.device
+        st = _lib.stream_handle(dev)
+        Q = torch.empty((B, heads, S, nope + rope), dtype=_BF16, device=dev)
+        K = torch.empty_like(Q)
+        V = torch.empty((B, heads, S, v_dim), dtype=_BF16, device=dev)
+        kr = comp[:, kv_rank:]
+        _lib.call("st_mla_rope_fwd", _lib.ptr(q), q.stride(0), _lib.ptr(kv), kv.stride(0),
+                  _lib.ptr(kr), comp.stride(0), _lib.ptr(cos), _lib.ptr(sin), B, S, heads, nope,
+                  rope, v_dim, int(interleave), _lib.ptr(Q), _lib.ptr(K), _lib.ptr(V), st)
+        ctx.meta = (q.shape, kv.shape, comp.shape, B, S, heads, nope, rope, v_dim, kv_rank,
+                    interleave)
+        ctx.save_for_backward(cos, sin)
+        return Q, K, V
+
+    @staticmethod
+    def backward(ctx, dQ, dK, dV):
+        qs, kvs, cs, B, S, heads, nope, rope, v_dim, kv_rank, interleave = ctx.meta
+        cos, sin = ctx.saved_tensors
+        dev = cos.device
+        z = lambda shape: torch.zeros(shape, dtype=_BF16, device=dev)  # noqa: E731
+        dQ = z((B, heads, S, nope + rope)) if dQ is None else dQ.contiguous()
+        dK = z((B, heads, S, nope + rope)) if dK is None else dK.contiguous()
+        dV = z((B, heads, S, v_dim)) if dV is None else dV.contiguous()
+        dq = torch.empty(qs, dtype=_BF16, device=dev)
+        dkv = torch.empty(kvs, dtype=_BF16, device=dev)
+        dcomp = torch.zeros(cs, dtype=_BF16, device=dev)
+        _lib.call("st_mla_rope_bwd", _lib.ptr(dQ), _lib.ptr(dK), _lib.ptr(dV), _lib.ptr(cos),
+                  _lib.ptr(sin), B, S, heads, nope, rope, v_dim, int(interleave), _lib.ptr(dq),
+                  dq.stride(0), _lib.ptr(dkv), dkv.stride(0), _lib.ptr(dcomp[:, kv_rank:]),
+                  dcomp.stride(0), _lib.stream_handle(dev))
+        return (dq, dkv, dcomp) + (None,) * 10
+
+
+def mla_rope(q, kv, comp, cos, sin, *, batch, seq, heads, nope, rope, v_dim, kv_rank,
+             interleave):
+    """Q, K, V of DeepSeek's multi-head latent attention (deepseek.py:137-150)
+    from the q_b (or q_proj) output ``q``, the kv_b output ``kv`` and the
+    kv_a_proj_with_mqa output ``comp`` (its columns ``kv_rank:kv_rank+rope`` are
+    the shared rope key; ``comp`` may be a column slice of a wider output)."""
+    if comp.stride(1) != 1 or q.stride(1) != 1 or kv.stride(1) != 1:
+        raise ValueError("mla_rope expects row-major operands")
+    return _MLARope.apply(q.contiguous(), kv.contiguous(), comp, cos.contiguous(),
+                          sin.contiguous(), batch, seq, heads, nope, rope, v_dim, kv_rank,
+                          bool(interleave))
+
+
+class _MLAAttention(torch.autograd.Function):
+    """Causal attention with query/key heads of DQ and value heads of DV
+    (deepseek.py:151-153) on the flash kernels."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, scale):
+        B, H, S, DQ = q.shape
+        DV = v.shape[-1]
+        dev = q.device
+        out = torch.empty((B, S, H * DV), dtype=_BF16, device=dev)
+        lse = torch.empty((B, H, S), dtype=_F32, device=dev)
+        ws = _ws.get(dev, _lib.query("st_mla_attn_workspace_bytes", B, S, H, DQ, DV, 0))
+        _lib.call("st_mla_attn_fwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), B, S, H, DQ, DV,
+                  float(scale), _lib.ptr(out), _lib.ptr(lse), _lib.ptr(ws),
+                  0 if ws is None else ws.numel(), _lib.stream_handle(dev))
+        ctx.save_for_backward(q, k, v, out, lse)
+        ctx.scale = scale
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, out, lse = ctx.saved_tensors
+        B, H, S, DQ = q.shape
+        DV = v.shape[-1]
+        dev = q.device
+        dout = dout.contiguous()
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        ws = _ws.get(dev, _lib.query("st_mla_attn_workspace_bytes", B, S, H, DQ, DV, 1))
+        _lib.call("st_mla_attn_bwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(out),
+                  _lib.ptr(lse), _lib.ptr(dout), B, S, H, DQ, DV, float(ctx.scale), _lib.ptr(dq),
+                  _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(ws), 0 if ws is None else ws.numel(),
+                  _lib.stream_handle(dev))
+        return dq, dk, dv, None
+
+
+def mla_attention(q, k, v, scale):
+    """q, k [B,H,S,DQ], v [B,H,S,DV] -> token-major [B,S,H*DV]."""
+    return _MLAAttention.apply(q.contiguous(), k.contiguous(), v.contiguous(), float(scale))
+
+
 # ----------------------------------------------------------------- SwiGLU
 class _SwiGLU(torch.autograd.Function):
     @staticmethod
@@ -711,6 +807,7 @@ def attention_scale(head_dim: int) -> float:
 
 __all__ = ["Q4Weight", "concat_rows", "q4_lora_linear", "rms_norm", "rope_qkv", "rope_heads",
            "causal_attention", "swiglu", "swiglu_pair", "lora_gemm", "attention_scale",
+           "mla_rope", "mla_attention",
            "rms_norm_residual",
            "linear_bf16", "linear_bf16_dgrad", "supervised_chunk_intervals",
            "chunked_causal_loss"]

@@ -33,9 +33,11 @@ from .ops import Q4Weight
 ALIGN = 256
 # projections whose storage is packed back to back (row-concatenation groups)
 FUSION_GROUPS = (("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj"),
+                 ("self_attn.q_a_proj", "self_attn.kv_a_proj_with_mqa"),
                  ("self_attn.o_proj",),
                  ("mlp.gate_proj", "mlp.up_proj"),
-                 ("mlp.down_proj",))
+                 ("mlp.down_proj",),
+                 ("mlp.shared_experts.gate_proj", "mlp.shared_experts.up_proj"))
 
 
 def _align(n: int) -> int:
@@ -121,13 +123,18 @@ def pack_image(block: BlockPlan, layout: SlotLayout, out: torch.Tensor) -> None:
 
 
 def views_of(buffer: torch.Tensor, layout: SlotLayout) -> dict:
-    """Weight views over a device (or host) image: Q4Weight for 4-bit parts."""
+    """Weight views over a device (or host) image: Q4Weight for 4-bit
+    matrices, Q4Experts for packed 3-D expert stacks [E, N, K]."""
+    from .moe import Q4Experts
     views = {}
     for name, e in layout.entries.items():
         if e[0] == "q4":
             _, codec, shape, po, pb, so, sb = e
-            views[name] = Q4Weight(buffer[po:po + pb], buffer[so:so + sb].view(torch.float32),
-                                   shape, codec)
+            payload, scales = buffer[po:po + pb], buffer[so:so + sb].view(torch.float32)
+            if len(shape) == 3:
+                views[name] = Q4Experts(payload, scales, shape[0], shape[1], shape[2], codec)
+            else:
+                views[name] = Q4Weight(payload, scales, shape, codec)
         else:
             _, dtype, shape, o, nb = e
             views[name] = buffer[o:o + nb].view(dtype).view(shape)

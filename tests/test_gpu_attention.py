@@ -86,3 +86,77 @@ def test_flash_bwd_vs_fp32_autograd(dev, B, H, Hkv, S, D):
         rel = ((got.float() - want).norm() / want.norm()).item()
         cos = torch.nn.functional.cosine_similarity(got.float().flatten(), want.flatten(), 0).item()
         assert rel < 2e-2 and cos > 0.9995, (name, rel, cos)
+
+
+# ----------------------------------------------------------------- MLA (DeepSeek-V3)
+def _ref_mla(q, k, v, scale):
+    B, H, S, DQ = q.shape
+    DV = v.shape[-1]
+    s = (q.float() @ k.float().transpose(-1, -2)) * scale
+    mask = torch.ones(S, S, dtype=torch.bool, device=q.device).triu(1)
+    s = s.masked_fill(mask, float("-inf"))
+    lse2 = torch.logsumexp(s, -1) / math.log(2.0)
+    o = torch.softmax(s, -1) @ v.float()
+    return o.transpose(1, 2).reshape(B, S, H * DV), lse2
+
+
+def _mla(q, k, v, scale, dout=None):
+    B, H, S, DQ = q.shape
+    DV = v.shape[-1]
+    dev, st = q.device, _lib.stream_handle(q.device)
+    out = torch.empty(B, S, H * DV, dtype=BF, device=dev)
+    lse = torch.empty(B, H, S, dtype=torch.float32, device=dev)
+    ws = torch.empty(_lib.query("st_mla_attn_workspace_bytes", B, S, H, DQ, DV, 0),
+                     dtype=torch.uint8, device=dev)
+    _lib.call("st_mla_attn_fwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), B, S, H, DQ, DV,
+              float(scale), _lib.ptr(out), _lib.ptr(lse), _lib.ptr(ws), ws.numel(), st)
+    if dout is None:
+        torch.cuda.synchronize()
+        return out, lse
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    wb = torch.empty(_lib.query("st_mla_attn_workspace_bytes", B, S, H, DQ, DV, 1),
+                     dtype=torch.uint8, device=dev)
+    _lib.call("st_mla_attn_bwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(out),
+              _lib.ptr(lse), _lib.ptr(dout), B, S, H, DQ, DV, float(scale), _lib.ptr(dq),
+              _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(wb), wb.numel(), st)
+    torch.cuda.synchronize()
+    return out, lse, dq, dk, dv
+
+
+@pytest.mark.parametrize("B,H,S", [(1, 4, 128), (2, 3, 200), (1, 8, 72), (1, 128, 2048)])
+def test_mla_attention_fwd_bwd_vs_fp32(dev, B, H, S):
+    """Query/key heads of 192 against value heads of 128 (DeepSeek-V3 MLA),
+    forward and VJP against float32 autograd; the last case is config 5's
+    full attention shape (128 heads x 2048 tokens)."""
+    DQ, DV = 192, 128
+    g = torch.Generator().manual_seed(B * 31 + H * 7 + S)
+    q = torch.randn(B, H, S, DQ, generator=g).to(BF).to(dev)
+    k = torch.randn(B, H, S, DQ, generator=g).to(BF).to(dev)
+    v = torch.randn(B, H, S, DV, generator=g).to(BF).to(dev)
+    dout = torch.randn(B, S, H * DV, generator=g).to(BF).to(dev)
+    scale = DQ ** -0.5
+    out, lse, dq, dk, dv = _mla(q, k, v, scale, dout)
+    qf, kf, vf = (t.float().requires_grad_(True) for t in (q, k, v))
+    ref, lse_ref = _ref_mla(qf, kf, vf, scale)
+    rel = ((out.float() - ref.detach()).norm() / ref.detach().norm()).item()
+    assert rel < 1e-2, rel
+    torch.testing.assert_close(lse, lse_ref.detach(), rtol=1e-4, atol=1e-4)
+    ref.backward(dout.float())
+    for got, want, name in ((dq, qf.grad, "dq"), (dk, kf.grad, "dk"), (dv, vf.grad, "dv")):
+        rel = ((got.float() - want).norm() / want.norm()).item()
+        cos = torch.nn.functional.cosine_similarity(got.float().flatten(), want.flatten(), 0).item()
+        assert rel < 2e-2 and cos > 0.9995, (name, rel, cos)
+
+
+def test_mla_entry_with_equal_dims_matches_flash_attention(dev):
+    """st_mla_attn_* with DQ = DV = 128 runs the dense kernels: the same bits
+    as st_flash_attn_* with Hkv = H."""
+    g = torch.Generator().manual_seed(9)
+    B, H, S, D = 1, 4, 256, 128
+    q, k, v = (torch.randn(B, H, S, D, generator=g).to(BF).to(dev) for _ in range(3))
+    dout = torch.randn(B, S, H * D, generator=g).to(BF).to(dev)
+    o1, l1, dq1, dk1, dv1 = _mla(q, k, v, D ** -0.5, dout)
+    o2, l2 = _fwd(q, k, v, D ** -0.5)
+    dq2, dk2, dv2 = _bwd(q, k, v, o2, l2, dout, D ** -0.5)
+    for a, b in ((o1, o2), (l1, l2), (dq1, dq2), (dk1, dk2), (dv1, dv2)):
+        assert torch.equal(a, b)
