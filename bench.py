@@ -45,6 +45,16 @@ DSMOE = dict(H=7168, I=2048, E=256, k=8, groups=8, group_k=4, scale=2.5, T=2048,
              shared_I=2048)
 DSMOE_METRIC = ("train tokens/s per DeepSeek-V3-shape MoE feed-forward fwd+recompute+bwd "
                 "(256 NF4 routed experts + shared expert)")
+# one streamed DeepSeek-V3-shape MLA + MoE layer
+DSV3 = dict(H=7168, heads=128, q_rank=1536, kv_rank=512, nope=128, rope=64, v=128, E=256, I=2048,
+            shared_I=2048, k=8, groups=8, group_k=4, scale=2.5, T=2048, r=8, alpha=16.0, eps=1e-6,
+            interleave=True,
+            rope_cfg={"rope_type": "yarn", "rope_theta": 10000.0, "factor": 40.0,
+                      "original_max_position_embeddings": 4096, "beta_fast": 32, "beta_slow": 1,
+                      "mscale": 1.0, "mscale_all_dim": 1.0})
+DSV3_METRIC = ("train tokens/s, one streamed DeepSeek-V3-shape MLA+MoE layer fwd+recompute+bwd "
+               "(NF4 image copied from pinned host RAM each step)")
+PCIE_GBPS = 64.0  # PCIe Gen5 x16, one direction, raw
 PROJ = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
         "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj")
 
@@ -78,6 +88,64 @@ def algorithmic_flops(c):
     attn = 4 * (4 * c["S"] * c["S"] * c["D"] * c["heads"] * c["B"]) // 2
     lora = 4 * 2 * M * c["r"] * sum(n + k for n, k in layer_shapes(c).values())
     return base + attn + lora
+
+
+def cpu_model():
+    """Host CPU model name (/proc/cpuinfo, as lscpu prints it)."""
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_config1(steps=20):
+    """BASELINE config 1 on the CPU path: the tiny Llama (2 layers, hidden 256,
+    intermediate 688, 4 heads of 64, vocab 1024, nf4-g128 weights, LoRA r=8 on
+    all seven projections), batch 2 x 128, 20 AdamW steps through the oracle's
+    training loop (engine.py:162-182 restated).  Returns seconds and tokens/s."""
+    import numpy as np
+    import torch
+    from oracle import codec as oc
+    from oracle import layer as OL
+    from spilltune_amd import codecs
+    g = torch.Generator().manual_seed(1234)
+    H, I, D, V = 256, 688, 64, 1024
+    shapes = {"self_attn.q_proj": (256, H), "self_attn.k_proj": (256, H),
+              "self_attn.v_proj": (256, H), "self_attn.o_proj": (H, 256),
+              "mlp.gate_proj": (I, H), "mlp.up_proj": (I, H), "mlp.down_proj": (H, I)}
+    layers, loras = [], []
+    for _ in range(2):
+        w = {}
+        for n, shp in shapes.items():
+            rec = codecs.encode((torch.randn(shp, generator=g) * 0.02).to(torch.bfloat16), "nf4-g128")
+            bits = oc.decode4(rec.parts["payload"].numpy(), rec.parts["scales"].numpy(),
+                              shp[0] * shp[1], lut=oc.NF4_LUT)
+            w[n + ".weight"] = torch.from_numpy(bits.astype(np.int16)).view(torch.bfloat16).view(shp)
+        w["input_layernorm.weight"] = torch.ones(H, dtype=torch.bfloat16)
+        w["post_attention_layernorm.weight"] = torch.ones(H, dtype=torch.bfloat16)
+        layers.append(w)
+        loras.append({n: OL.Lora(n, torch.randn(8, shp[1], generator=g) * 0.02,
+                                 torch.zeros(shp[0], 8), 16.0) for n, shp in shapes.items()})
+    emb = (torch.randn(V, H, generator=g) * 0.5).to(torch.bfloat16)
+    head = (torch.randn(V, H, generator=g) * 0.05).to(torch.bfloat16)
+    gd = torch.Generator().manual_seed(7)
+    rows = []
+    for _ in range(4):
+        ids = torch.randint(0, V, (2, 128), generator=gd)
+        rows.append((ids, ids.clone()))
+    t0 = time.perf_counter()
+    losses = OL.train_reference(emb, torch.ones(H, dtype=torch.bfloat16), head, layers, loras, rows,
+                                cfg=dict(heads=4, kv_heads=4, head_dim=D, eps=1e-5),
+                                theta=500000.0, steps=steps, lr=2e-3, token_chunk=64)
+    dt = time.perf_counter() - t0
+    return {"steps": steps, "seconds": round(dt, 3), "tokens_per_s": round(steps * 2 * 128 / dt, 1),
+            "loss_first_last": [round(losses[0], 4), round(losses[-1], 4)],
+            "workload": "config 1: tiny Llama, 2 layers, batch 2 x 128, nf4-g128, LoRA r=8 on 7 "
+                        "projections, 20 AdamW steps (oracle/layer.py train_reference)"}
 
 
 def cpu_baseline(c, block, tokens, min_seconds=10.0):
@@ -117,15 +185,18 @@ def cpu_baseline(c, block, tokens, min_seconds=10.0):
         if dt >= min_seconds or steps >= 64:
             break
     return {"value": tokens * steps / dt, "unit": "tokens/s", "cores": torch.get_num_threads(),
-            "kind": "port",
+            "kind": "port", "cpu_model": cpu_model(),
             "sample": f"{steps} layer steps (fwd + recompute + bwd) at {tokens} tokens (batch 1) of "
-                      f"the same layer, oracle/layer.py on {cores} host cores, {dt:.1f} s"}
+                      f"the same layer, oracle/layer.py on {cores} host cores, {dt:.1f} s",
+            "config1": cpu_config1()}
 
 
-def streamed(c, block, args, X, dY, rot, mask):
+def streamed(c, block, args, X, dY, rot, mask, resident_ms):
     """N copies of the layer streamed through a 2-slot session: forward over
     all layers, backward in reverse (each layer loaded per phase, the last
-    forward layer reused), H2D of the packed image on the copy stream."""
+    forward layer reused), H2D of the packed image on the copy stream.
+    ``resident_ms`` is the resident layer step; the difference per layer is
+    the copy time left exposed."""
     import torch
     from spilltune_amd import slots
     from spilltune_amd.recompute import streaming_block
@@ -160,12 +231,18 @@ def streamed(c, block, args, X, dY, rot, mask):
     copies = session.completed_copies
     h2d = sum(cp["bytes"] for cp in copies) / max(sum(cp["copy_cuda_ms"] for cp in copies), 1e-9) / 1e6
     per_layer_ms = dt * 1e3 / L
+    copy_ms = sum(cp["copy_cuda_ms"] for cp in copies) / n
     out = {"layers": L, "slots": 2, "ms_per_step": round(dt * 1e3, 3),
            "ms_per_layer": round(per_layer_ms, 4),
+           "resident_ms_per_layer": round(resident_ms, 4),
+           "exposed_copy_ms_per_layer": round(per_layer_ms - resident_ms, 4),
+           "copy_ms_per_step": round(copy_ms, 3),
+           "hidden_copy_frac": round(max(0.0, 1.0 - (per_layer_ms - resident_ms) * L / copy_ms), 4)
+           if copy_ms > 0 else None,
            "tokens_per_s_per_layer": round(c["B"] * c["S"] / (per_layer_ms * 1e-3), 1),
            "h2d_bytes_per_step": int(sum(cp["bytes"] for cp in copies) / n),
            "h2d_gbps_while_copying": round(h2d, 2), "copies_per_step": len(copies) / n,
-           "cache_hits": session.hits}
+           "pcie_ceiling_gbps": PCIE_GBPS, "cache_hits": session.hits}
     session.close()
     log(f"streamed {L} layers: {out}")
     return out
@@ -505,6 +582,167 @@ def deepseek_moe_bench(args):
     print(json.dumps(result), flush=True)
 
 
+def deepseek_bench(args):
+    """Config 5: one DeepSeek-V3-shape decoder layer (MLA: hidden 7168, 128
+    heads, q_lora_rank 1536, kv_lora_rank 512, qk 128 + 64 rope, v 128, YaRN,
+    interleaved rotary; MoE: 256 routed experts of width 2048, top-8 of the
+    sigmoid group-limited router, shared expert) stored nf4-g128 as one pinned
+    image, LoRA r=8 on the attention projections and the shared expert, 2048
+    tokens.  One step = the StreamingBlockFunction lifecycle (forward without
+    grad, recompute + backward) with the layer's image copied host -> device on
+    the copy stream first (the backward borrow is a cache hit, as for the
+    last layer of a streamed model).  Also timed: the same step with the image
+    already resident (compute only).  The 4-bit records are synthetic bytes
+    written straight into the pinned image (random codes, scales in [0.01,
+    0.03)): the cost does not depend on the values, and encoding 12 G weights
+    on the host would dominate the setup."""
+    import torch
+    from spilltune_amd import codecs, deepseek, ops, slots
+    from spilltune_amd.recompute import streaming_block
+    c = DSV3
+    H, E, I, T = c["H"], c["E"], c["I"], c["T"]
+    dev = torch.device("cuda:0")
+    heads, nope, rope, v = c["heads"], c["nope"], c["rope"], c["v"]
+    mats = {"self_attn.q_a_proj": (c["q_rank"], H),
+            "self_attn.q_b_proj": (heads * (nope + rope), c["q_rank"]),
+            "self_attn.kv_a_proj_with_mqa": (c["kv_rank"] + rope, H),
+            "self_attn.kv_b_proj": (heads * (nope + v), c["kv_rank"]),
+            "self_attn.o_proj": (H, heads * v),
+            "mlp.experts.gate_up_proj": (E, 2 * I, H), "mlp.experts.down_proj": (E, H, I),
+            "mlp.shared_experts.gate_proj": (c["shared_I"], H),
+            "mlp.shared_experts.up_proj": (c["shared_I"], H),
+            "mlp.shared_experts.down_proj": (H, c["shared_I"])}
+    weights = {}
+    for name, shape in mats.items():
+        n = 1
+        for d in shape:
+            n *= d
+        groups = n // codecs.GROUP
+        weights[f"{name}.weight" if "experts." not in name or "shared" in name else name] = \
+            codecs.Record({"version": 1, "shape": list(shape), "dtype": "bfloat16",
+                           "codec": "nf4-g128", "group_size": codecs.GROUP, "numel": n},
+                          {"payload": torch.empty(groups * codecs.STRIDE, dtype=torch.uint8,
+                                                  device="meta"),
+                           "scales": torch.empty(groups, dtype=torch.float32, device="meta")})
+    meta = lambda n, dt: torch.empty(n, dtype=dt, device="meta")  # noqa: E731
+    weights.update({"input_layernorm.weight": meta(H, torch.bfloat16),
+                    "post_attention_layernorm.weight": meta(H, torch.bfloat16),
+                    "self_attn.q_a_layernorm.weight": meta(c["q_rank"], torch.bfloat16),
+                    "self_attn.kv_a_layernorm.weight": meta(c["kv_rank"], torch.bfloat16),
+                    "mlp.gate.weight": torch.empty(E, H, dtype=torch.float32, device="meta"),
+                    "mlp.gate.e_score_correction_bias": meta(E, torch.float32)})
+    params = {"heads": heads, "nope": nope, "rope": rope, "value": v, "kv_rank": c["kv_rank"],
+              "q_rank": c["q_rank"], "eps": c["eps"],
+              "attention_scale": deepseek.attention_scale(nope, rope, c["rope_cfg"]),
+              "interleave": c["interleave"], "moe": True, "experts": E, "groups": c["groups"],
+              "group_k": c["group_k"], "top_k": c["k"], "normalize": True,
+              "router_scale": c["scale"]}
+    block = deepseek.make_deepseek_block(0, weights, codec="nf4-g128", parameters=params,
+                                         rank=c["r"], alpha=c["alpha"], device=dev,
+                                         shared_lora=True,
+                                         generator=torch.Generator().manual_seed(3))
+    gB = torch.Generator().manual_seed(4)
+    with torch.no_grad():
+        for name in sorted(block.adapters):
+            p = block.adapters[name]
+            p.B.copy_(torch.randn(p.B.shape, generator=gB) * 0.02)
+    gfill = torch.Generator().manual_seed(1234)
+
+    def fill(blk, layout, out):
+        """The pinned image written in place: random codes and scales for the
+        4-bit records, unit norms, an fp32 router ~N(0, H^-1/2), bias ~N(0, 0.01)."""
+        for name, e in layout.entries.items():
+            if e[0] == "q4":
+                _, _, _, po, pb, so, sb = e
+                out[po:po + pb].random_(0, 256, generator=gfill)
+                out[so:so + sb].view(torch.float32).uniform_(0.01, 0.03, generator=gfill)
+            else:
+                _, dtype, shape, o, nb = e
+                view = out[o:o + nb].view(dtype)
+                if name == "mlp.gate.weight":
+                    view.normal_(0.0, H ** -0.5, generator=gfill)
+                elif name.endswith("e_score_correction_bias"):
+                    view.normal_(0.0, 0.01, generator=gfill)
+                else:
+                    view.fill_(1.0)
+    t0 = time.perf_counter()
+    session = slots.Q4SlotSession([block], dev, host_budget_bytes=1 << 40,
+                                  device_budget_bytes=1 << 40, slots=2, image_loader=fill)
+    image = session.host_bytes
+    log(f"DeepSeek-V3-shape layer image: {image / 1e9:.2f} GB pinned, built in "
+        f"{time.perf_counter() - t0:.1f} s")
+    X = torch.randn(1, T, H, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16).to(dev)
+    dY = torch.randn(1, T, H, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).to(dev)
+    rot, mask = deepseek.positions_and_masks(torch.ones(1, T, dtype=torch.bool),
+                                             rope=c["rope_cfg"], rope_dim=rope, device=dev)
+
+    def step(cold):
+        if cold:
+            session.invalidate()
+        h = X.detach().requires_grad_(True)
+        with session.run():
+            out = streaming_block(h, rot, mask, block.functional, block.kwargs,
+                                  session.reloader(block), block.adapters, block.index)
+            out.backward(dY)
+
+    steps = max(2, min(args.steps, 10))
+    for _ in range(max(1, min(args.warmup, 2))):
+        step(True)
+    torch.cuda.synchronize()
+    # compute only: the image stays in its slot (every borrow a cache hit)
+    t1 = time.perf_counter()
+    for _ in range(steps):
+        step(False)
+    torch.cuda.synchronize()
+    warm_ms = (time.perf_counter() - t1) * 1e3 / steps
+    # streamed: the image is copied again at the start of every step
+    session.completed_copies = []
+    ops.TIMER = ops.KernelTimer()
+    t2 = time.perf_counter()
+    for _ in range(steps):
+        step(True)
+    torch.cuda.synchronize()
+    cold_s = (time.perf_counter() - t2) / steps
+    timer, ops.TIMER = ops.TIMER, None
+    copies = session.completed_copies
+    copy_ms = sum(cp["copy_cuda_ms"] for cp in copies) / steps
+    gbps = sum(cp["bytes"] for cp in copies) / max(sum(cp["copy_cuda_ms"] for cp in copies),
+                                                   1e-9) / 1e6
+    kern = timer.summary()
+    key, info = max(kern.items(), key=lambda kv: kv[1]["launches"] * kv[1]["avg_ms"])
+    _, M, N, K = key
+    achieved = 2.0 * M * N * K / (info["avg_ms"] * 1e-3) / 1e12
+    for k2, v2 in sorted(kern.items(), key=lambda kv: -kv[1]["launches"] * kv[1]["avg_ms"]):
+        tf = 2.0 * k2[1] * k2[2] * k2[3] / (v2["avg_ms"] * 1e-3) / 1e12
+        log(f"  {k2[0]:9s} M={k2[1]} N={k2[2]} K={k2[3]}: {v2['launches']} launches, "
+            f"{v2['avg_ms']:.3f} ms avg, {tf:.0f} TFLOP/s ({tf / PEAK_BF16_TFLOPS:.1%})")
+    log(f"streamed step {cold_s * 1e3:.1f} ms (copy {copy_ms:.1f} ms at {gbps:.1f} GB/s), "
+        f"resident step {warm_ms:.1f} ms")
+    session.close()
+    result = {
+        "metric": DSV3_METRIC, "value": round(T / cold_s, 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": steps, "warmup": 1, "ms_per_step": round(cold_s * 1e3, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random nf4-g128 codes and scales written into the pinned image, "
+                "fp32 router ~N(0, H^-1/2); N(0,1) activations/grads)",
+        "config": {"workload": f"deepseek: one streamed DeepSeek-V3-shape MLA+MoE layer, {T} "
+                               f"tokens, {heads} heads, {E} experts top-{c['k']}, shared expert, "
+                               f"LoRA r={c['r']} on attention + shared expert, nf4-g128",
+                   "global_batch": 1, "seq_len": T, "hidden": H, "experts": E,
+                   "parallelism": "single GPU"},
+        "resident_ms_per_step": round(warm_ms, 3),
+        "h2d": {"image_bytes": int(image), "copy_ms": round(copy_ms, 3),
+                "gbps_while_copying": round(gbps, 2), "pcie_ceiling_gbps": PCIE_GBPS,
+                "frac_of_ceiling": round(gbps / PCIE_GBPS, 4)},
+        "roofline": {"bound": "mfma", "kernel": f"{key[0]} M={M} N={N} K={K}",
+                     "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None, "avg_ms": round(info["avg_ms"], 4)},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(result), flush=True)
+
+
 def moe_bench(args):
     """Config 4: the MoE feed-forward forward + backward on 4096 tokens
     (router, permutation, grouped 4-bit gate|up and down GEMMs with per-expert
@@ -633,13 +871,14 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="llama8b",
-                    choices=sorted(CONFIGS) + ["moe", "deepseek-moe", "qwen3-stream", "memory"])
+                    choices=sorted(CONFIGS) + ["moe", "deepseek-moe", "deepseek", "qwen3-stream",
+                                               "memory"])
     ap.add_argument("--cpu-tokens", type=int, default=2048)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 3 device copies of 256 MiB (the reference kernel for scaling "
                          "rocprofv3 FETCH_SIZE/WRITE_SIZE counters to bytes) and exit")
-    ap.add_argument("--streamed-layers", type=int, default=0,
+    ap.add_argument("--streamed-layers", type=int, default=4,
                     help="also time N layers streamed from pinned host RAM through 2 device "
                          "slots with one-layer prefetch (reported under 'streamed')")
     args = ap.parse_args()
@@ -668,6 +907,9 @@ def main():
         return
     if args.config == "deepseek-moe":
         deepseek_moe_bench(args)
+        return
+    if args.config == "deepseek":
+        deepseek_bench(args)
         return
     from spilltune_amd import ops, slots
     from spilltune_amd.dense import CausalMask
@@ -716,13 +958,18 @@ def main():
             log("first step done")
     torch.cuda.synchronize()
     ops.TIMER = ops.KernelTimer()
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     t_start = time.perf_counter()
-    for _ in range(args.steps):
+    marks[0].record()
+    for i in range(args.steps):
         step()
+        marks[i + 1].record()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t_start
     timer, ops.TIMER = ops.TIMER, None
     ms = elapsed * 1e3 / args.steps
+    per_step = sorted(marks[i].elapsed_time(marks[i + 1]) for i in range(args.steps))
+    median_ms = per_step[len(per_step) // 2]
     tokens = B * S
     value = tokens * args.steps / elapsed
     flops = algorithmic_flops(c)
@@ -751,6 +998,7 @@ def main():
     result = {
         "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "median_ms_per_step": round(median_ms, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded N(0,0.02) weights -> nf4-g128, N(0,1) activations/grads)",
         "config": {"workload": f"{args.config}: one decoder layer fwd+recompute+bwd, "
@@ -766,7 +1014,7 @@ def main():
         "cpu_baseline": None,
     }
     if args.streamed_layers > 0:
-        result["streamed"] = streamed(c, block, args, X, dY, rot, mask)
+        result["streamed"] = streamed(c, block, args, X, dY, rot, mask, median_ms)
     if not args.no_cpu_baseline:
         log(f"timing the CPU path at {args.cpu_tokens} tokens")
         result["cpu_baseline"] = cpu_baseline(c, block, args.cpu_tokens)

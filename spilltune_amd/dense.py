@@ -59,9 +59,20 @@ def _weight(weights, name):
 
 def dense_block(hidden_states, position_embeddings, attention_mask, *, heads, kv_heads, head_dim,
                 eps, lora_q=None, lora_k=None, lora_v=None, lora_o=None, lora_gate=None,
-                lora_up=None, lora_down=None, qk_norm=False, feed_forward=None, **weights):
+                lora_up=None, lora_down=None, qk_norm=False, feed_forward=None, moe=None,
+                lora_experts_gate_up=None, lora_experts_down=None, **weights):
+    """``moe`` (``num_experts``, ``top_k``, ``norm_topk_prob``) makes the
+    feed-forward the Qwen3-MoE block of qwen3_moe.py:95-113 over the slot's
+    ``mlp.experts.*`` stacks, with the optional per-expert LoRA objects
+    ``lora_experts_gate_up`` / ``lora_experts_down``."""
     if attention_mask is not None and not isinstance(attention_mask, CausalMask):
         raise ValueError("unsupported_capability: only the causal mask marker is supported")
+    if moe is not None and feed_forward is None:
+        from . import moe as moe_ops
+
+        def feed_forward(x, w):
+            return moe_ops.moe_feed_forward(x, w, lora_gate_up=lora_experts_gate_up,
+                                            lora_down=lora_experts_down, **moe)
     B, S, Hd = hidden_states.shape
     cos, sin = position_embeddings
     x2d = hidden_states.reshape(B * S, Hd)
@@ -119,5 +130,7 @@ def lora_kwargs(adapters: dict) -> dict:
     """Map target paths to the functional's ``lora_*`` keyword arguments."""
     names = {"self_attn.q_proj": "lora_q", "self_attn.k_proj": "lora_k",
              "self_attn.v_proj": "lora_v", "self_attn.o_proj": "lora_o",
-             "mlp.gate_proj": "lora_gate", "mlp.up_proj": "lora_up", "mlp.down_proj": "lora_down"}
+             "mlp.gate_proj": "lora_gate", "mlp.up_proj": "lora_up", "mlp.down_proj": "lora_down",
+             "mlp.experts.gate_up_proj": "lora_experts_gate_up",
+             "mlp.experts.down_proj": "lora_experts_down"}
     return {names[t]: p for t, p in adapters.items()}

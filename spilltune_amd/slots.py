@@ -318,6 +318,16 @@ class Q4SlotSession:
             finally:
                 self._borrow_lock.release()
 
+    def invalidate(self):
+        """Forget which blocks the slots hold, so the next borrow of every
+        block copies its image again (a cold start; used to time the copy of
+        a layer that a previous step left in a slot).  Outside ``run()``."""
+        if self._run_lock.locked():
+            raise RuntimeError("cannot invalidate slots during a run")
+        for slot in self.slots:
+            slot["block"] = None
+            slot["views"] = {}
+
     def _finalize_copies(self):
         done = []
         for r in self.copy_records:
@@ -414,18 +424,26 @@ def make_archive_block(reader, index: int, *, heads: int, kv_heads: int, head_di
 
 def make_dense_block(index: int, weights: dict, *, codec: str, heads: int, kv_heads: int,
                      head_dim: int, eps: float, rank: int, alpha: float, targets, device,
-                     functional=None, generator=None, qk_norm: bool = False) -> BlockPlan:
+                     functional=None, generator=None, qk_norm: bool = False, moe=None,
+                     expert_lora_rank: int = 0, expert_lora_alpha: float = 16.0) -> BlockPlan:
     """Encode one dense decoder layer (``weights``: name -> CPU fp32/bf16 tensor,
     HF names without the ``model.layers.{i}.`` prefix) into a BlockPlan whose
     host weights are the flattened 4-bit records (codecs.flatten layout of the
-    reference: ``@<name>/payload``, ``@<name>/scales``) plus raw norm vectors."""
+    reference: ``@<name>/payload``, ``@<name>/scales``) plus raw norm vectors.
+
+    A Qwen3-MoE layer (``moe`` = ``{num_experts, top_k, norm_topk_prob}``)
+    stores its packed ``mlp.experts.gate_up_proj [E, 2I, H]`` /
+    ``mlp.experts.down_proj [E, H, I]`` stacks 4-bit in the same image, so the
+    whole decoder layer, every expert included, moves through the slot as in
+    qwen3_moe.py:146-152; the router ``mlp.gate.weight`` stays bf16.
+    ``expert_lora_rank`` > 0 adds per-expert LoRA on gate|up and down."""
     from .dense import dense_block, lora_kwargs
     from .lora import create_lora_for_block
     host, specs = {}, {}
     for name, t in weights.items():
-        if t.dim() == 2 and t.numel() >= codecs.GROUP:
-            rec = codecs.encode(t.contiguous(), codec)
-            specs[name] = {"spec": rec.spec, "parts": {}}
+        if name != "mlp.gate.weight" and t.dim() in (2, 3) and t.numel() >= codecs.GROUP:
+            rec = codecs.encode(t.reshape(-1, t.shape[-1]).contiguous(), codec)
+            specs[name] = {"spec": dict(rec.spec, shape=list(t.shape)), "parts": {}}
             for part, tensor in rec.parts.items():
                 key = f"@{name}/{part}"
                 host[key] = tensor
@@ -436,10 +454,21 @@ def make_dense_block(index: int, weights: dict, *, codec: str, heads: int, kv_he
     adapters = create_lora_for_block(index, "full_attention", shapes, rank=rank, alpha=alpha,
                                      device=device, targets=tuple(targets), architecture="llama",
                                      generator=generator)
+    if moe is not None and expert_lora_rank:
+        from .moe import make_expert_lora
+        E, I2, H = weights["mlp.experts.gate_up_proj"].shape
+        adapters["mlp.experts.gate_up_proj"] = make_expert_lora(
+            "mlp.experts.gate_up_proj", E, H, I2, rank=expert_lora_rank, alpha=expert_lora_alpha,
+            device=device, segments=2, generator=generator)
+        adapters["mlp.experts.down_proj"] = make_expert_lora(
+            "mlp.experts.down_proj", E, I2 // 2, H, rank=expert_lora_rank,
+            alpha=expert_lora_alpha, device=device, generator=generator)
     kwargs = {"heads": heads, "kv_heads": kv_heads, "head_dim": head_dim, "eps": eps,
               **lora_kwargs(adapters)}
     if qk_norm:  # Qwen3 (dense.py:128-133); q_norm/k_norm vectors travel as raw entries
         kwargs["qk_norm"] = True
+    if moe is not None:
+        kwargs["moe"] = dict(moe)
     return BlockPlan(index, "full_attention", functional or dense_block, kwargs, host, adapters,
                      specs)
 

@@ -472,3 +472,85 @@ def test_dense_block_with_moe_feed_forward(dev, oracle_codec):
 
 def M_ffn(x, router, Wgu, Wd, k, loras):
     return OM.qwen3_moe_ffn(x, router, Wgu, Wd, top_k=k, norm_topk_prob=True, loras=loras)
+
+
+def test_qwen3_moe_layer_streamed_whole_vs_oracle(dev, oracle_codec):
+    """A Qwen3-MoE decoder layer built by make_dense_block(moe=...): attention,
+    router and every expert stack in ONE slot image (qwen3_moe.py:146-152),
+    streamed through two slots with the recompute driver, per-expert LoRA;
+    against the oracle block with the oracle MoE feed-forward."""
+    from oracle import layer as OL
+    from spilltune_amd import slots
+    from spilltune_amd.dense import CausalMask
+    from spilltune_amd.recompute import streaming_block
+    g = torch.Generator().manual_seed(78)
+    B, S, H, heads, kv, D, E, I, k, r = 1, 80, 256, 4, 2, 64, 16, 128, 4, 8
+    w = {}
+    for name, shape in (("self_attn.q_proj", (heads * D, H)), ("self_attn.k_proj", (kv * D, H)),
+                        ("self_attn.v_proj", (kv * D, H)), ("self_attn.o_proj", (H, heads * D))):
+        w[name + ".weight"] = torch.randn(shape, generator=g) * 0.02
+    for nm in ("input_layernorm.weight", "post_attention_layernorm.weight"):
+        w[nm] = 1 + 0.05 * torch.randn(H, generator=g)
+    w["mlp.gate.weight"] = torch.randn(E, H, generator=g) * 3 * H ** -0.5   # well-separated logits
+    w["mlp.experts.gate_up_proj"] = torch.randn(E, 2 * I, H, generator=g) * 0.02
+    w["mlp.experts.down_proj"] = torch.randn(E, H, I, generator=g) * 0.02
+    block = slots.make_dense_block(0, w, codec="nf4-g128", heads=heads, kv_heads=kv, head_dim=D,
+                                   eps=1e-6, rank=r, alpha=16.0,
+                                   targets=("self_attn.q_proj", "self_attn.v_proj",
+                                            "self_attn.o_proj"),
+                                   device=dev, generator=g,
+                                   moe={"num_experts": E, "top_k": k, "norm_topk_prob": True},
+                                   expert_lora_rank=r)
+    with torch.no_grad():
+        for p in block.adapters.values():
+            p.B.copy_(torch.randn(p.B.shape, generator=g) * 0.02)
+    lay = slots.plan_layout(block)
+    assert lay.entries["mlp.experts.gate_up_proj"][2] == (E, 2 * I, H)   # expert stacks in the image
+    # oracle weights: exact bf16 decode of every stored record
+    exact = {}
+    for name, entry in block.storage_specs.items():
+        spec = entry["spec"]
+        bits = oracle_codec.decode4(block.host_weights[entry["parts"]["payload"]].numpy(),
+                                    block.host_weights[entry["parts"]["scales"]].numpy(),
+                                    spec["numel"], lut=oracle_codec.NF4_LUT)
+        exact[name] = torch.from_numpy(np.asarray(bits, dtype=np.uint16).astype(np.int16)).view(
+            BF).view(spec["shape"])
+    for kk, v in block.host_weights.items():
+        if not kk.startswith("@"):
+            exact[kk] = v
+    hidden = torch.randn(B, S, H, generator=g).to(BF)
+    dy = torch.randn(B, S, H, generator=g).to(BF)
+    cos, sin = OL.rotary(B, S, D, 500000.0, BF)
+    session = slots.Q4SlotSession([block], dev, host_budget_bytes=1 << 34,
+                                  device_budget_bytes=1 << 34, slots=2)
+    h = hidden.to(dev).requires_grad_(True)
+    with session.run():
+        out = streaming_block(h, (cos.to(dev), sin.to(dev)), CausalMask(B, S), block.functional,
+                              block.kwargs, session.reloader(block), block.adapters, block.index)
+        out.backward(dy.to(dev))
+    torch.cuda.synchronize()
+    assert session.actual_h2d_bytes >= lay.nbytes
+    lgu, ldn = block.adapters["mlp.experts.gate_up_proj"], block.adapters["mlp.experts.down_proj"]
+    leaves = [t.detach().cpu().clone().requires_grad_(True) for t in (lgu.A, lgu.B, ldn.A, ldn.B)]
+    loras = {"gate": (leaves[0][:, :r], leaves[1][:, :I], lgu.scale),
+             "up": (leaves[0][:, r:], leaves[1][:, I:], lgu.scale),
+             "down": (leaves[2], leaves[3], ldn.scale)}
+    dense_l = {n: OL.Lora(n, p.A.detach().cpu(), p.B.detach().cpu(), p.alpha)
+               for n, p in block.adapters.items() if not n.startswith("mlp.experts")}
+    ffr = lambda x, wts: OM.qwen3_moe_ffn(x, exact["mlp.gate.weight"],  # noqa: E731
+                                         exact["mlp.experts.gate_up_proj"],
+                                         exact["mlp.experts.down_proj"], top_k=k,
+                                         norm_topk_prob=True, loras=loras)
+    x = hidden.clone().requires_grad_(True)
+    ref = OL.dense_block(x, (cos, sin), OL.causal_mask(B, S, BF), heads=heads, kv_heads=kv,
+                         head_dim=D, eps=1e-6, weights=exact, loras=dense_l, feed_forward=ffr)
+    ref.backward(dy)
+    assert _rel(out, ref) < 2e-2
+    assert _cos(h.grad, x.grad) > 0.999
+    for n, l in dense_l.items():
+        assert _cos(block.adapters[n].grad_A, l.A.grad) > 0.999, n
+        assert _cos(block.adapters[n].grad_B, l.B.grad) > 0.999, n
+    for got, leaf, name in ((lgu.grad_A, leaves[0], "A_gu"), (lgu.grad_B, leaves[1], "B_gu"),
+                            (ldn.grad_A, leaves[2], "A_d"), (ldn.grad_B, leaves[3], "B_d")):
+        assert _cos(got, leaf.grad) > 0.999, name
+    session.close()
