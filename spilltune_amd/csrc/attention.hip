@@ -894,8 +894,6 @@ bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 // pair light and heavy query tiles in one workgroup when the unpaired grid
 // would fit the GPU in one round anyway (then its longest tile sets the time)
 int pair_mode(int nq, int64_t heads) {
-  const char* env = getenv("ST_FA_PAIRED");
-  if (env) return atoi(env) ? 1 : 0;
   return nq >= 4 && nq * heads <= 1024 ? 1 : 0;
 }
 

@@ -7,9 +7,9 @@
 // Default kernel (dequant4_word): one packed word = 8 consecutive elements per
 // lane per step (a word never straddles a group of 64/128), decoded through
 // the per-scale v_perm table of decode4.h and written as one 16-byte store, so
-// each store instruction of a wave writes 1 KiB of whole cache lines.  The
-// earlier form (dequant4_vec: 16 payload bytes per lane, codebook in LDS, four
-// 16-byte stores 64 bytes apart) stays behind ST_DEQUANT_KERNEL=0.
+// each store instruction of a wave writes 1 KiB of whole cache lines.  A
+// payload that is not 4-byte aligned or an output that is not 16-byte aligned
+// takes the element-wise kernel.
 // Per element: 0.5 B read + 2 B written (+4/group B scale).
 #include "common.h"
 #include "decode4.h"
@@ -50,46 +50,6 @@ __global__ __launch_bounds__(kThreads) void dequant4_word(const uint32_t* __rest
   }
 }
 
-__device__ __forceinline__ unsigned nib(uint32_t w, int e, int hi_first) {
-  int sh = 4 * (e ^ hi_first);
-  return (w >> sh) & 15u;
-}
-
-// 8 elements of one packed dword -> 4 packed bf16x2 words
-__device__ __forceinline__ void decode_dword(uint32_t w, float s, const float* lut, int hi_first,
-                                             uint32_t* o) {
-#pragma unroll
-  for (int e = 0; e < 8; e += 2) {
-    float a = lut[nib(w, e, hi_first)] * s;
-    float b = lut[nib(w, e + 1, hi_first)] * s;
-    o[e / 2] = st::pack_bf16x2(a, b);
-  }
-}
-
-__global__ __launch_bounds__(kThreads) void dequant4_vec(const uint4* __restrict__ payload,
-                                                        const float* __restrict__ scales,
-                                                        int64_t nchunks, int group_shift,
-                                                        Lut16 lut, int hi_first,
-                                                        uint4* __restrict__ out) {
-  __shared__ float lut_s[16];
-  if (threadIdx.x < 16) lut_s[threadIdx.x] = lut.v[threadIdx.x];
-  __syncthreads();
-  int64_t c = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (c >= nchunks) return;
-  uint4 p = payload[c];
-  float s = scales[(c * 32) >> group_shift];
-  uint32_t o[16];
-  decode_dword(p.x, s, lut_s, hi_first, o + 0);
-  decode_dword(p.y, s, lut_s, hi_first, o + 4);
-  decode_dword(p.z, s, lut_s, hi_first, o + 8);
-  decode_dword(p.w, s, lut_s, hi_first, o + 12);
-  uint4* dst = out + c * 4;
-  dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
-  dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
-  dst[2] = make_uint4(o[8], o[9], o[10], o[11]);
-  dst[3] = make_uint4(o[12], o[13], o[14], o[15]);
-}
-
 // element-wise tail / unaligned path: one element per thread
 __global__ __launch_bounds__(kThreads) void dequant4_scalar(const uint8_t* __restrict__ payload,
                                                            const float* __restrict__ scales,
@@ -114,13 +74,8 @@ int launch_dequant4(const uint8_t* payload, const float* scales, int64_t numel, 
   for (int i = 0; i < 16; ++i) lut.v[i] = lut16[i];
   int hi = (flags & ST_FLAG_HI_NIBBLE_FIRST) ? 1 : 0;
   int64_t vec_elems = 0;
-  // ST_DEQUANT_KERNEL=0: the LDS-codebook kernel (64 output bytes per lane)
-  static const int kind = [] {
-    const char* e = getenv("ST_DEQUANT_KERNEL");
-    return e ? atoi(e) : 1;
-  }();
   const int shift = group == 128 ? 7 : 6;
-  if (kind != 0 && ((uintptr_t)payload & 3u) == 0 && aligned16(out)) {
+  if (((uintptr_t)payload & 3u) == 0 && aligned16(out)) {
     const int64_t nwords = numel / 8;
     if (nwords > 0) {
       const unsigned blocks = (unsigned)cdiv(nwords, RW * kThreads);
@@ -131,13 +86,6 @@ int launch_dequant4(const uint8_t* payload, const float* scales, int64_t numel, 
         dequant4_word<false><<<blocks, kThreads, 0, stream>>>((const uint32_t*)payload, scales,
                                                               nwords, shift, lut, (uint4*)out);
       vec_elems = nwords * 8;
-    }
-  } else if (aligned16(payload) && aligned16(out)) {
-    int64_t nchunks = numel / 32;
-    if (nchunks > 0) {
-      dequant4_vec<<<(unsigned)cdiv(nchunks, kThreads), kThreads, 0, stream>>>(
-          (const uint4*)payload, scales, nchunks, shift, lut, hi, (uint4*)out);
-      vec_elems = nchunks * 32;
     }
   }
   if (vec_elems < numel) {

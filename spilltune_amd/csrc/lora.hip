@@ -246,15 +246,10 @@ __global__ __launch_bounds__(NTH) void lora_rk_reduce(int64_t Mo, int64_t R, int
   *o = v;
 }
 
-int env_int(const char* name, int dflt) {
-  const char* e = getenv(name);
-  return e ? atoi(e) : dflt;
-}
-
 int rk_ksplit(int64_t Mo, int64_t Kc) {
-  // enough workgroups to keep loads in flight on every CU, each streaming at
-  // least `chunk` contraction elements
-  static const int target = env_int("ST_RK_WG", 512), chunk = env_int("ST_RK_CHUNK", 256);
+  // enough workgroups (512) to keep loads in flight on every CU, each
+  // streaming at least `chunk` contraction elements
+  constexpr int target = 512, chunk = 256;
   int64_t tiles = st::cdiv(Mo, RK_BM);
   int64_t ks = st::cdiv(target, tiles);
   int64_t maxk = st::cdiv(Kc, chunk);

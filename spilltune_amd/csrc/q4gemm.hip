@@ -409,7 +409,11 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const f32x16 
     blocks(std::false_type{}, std::false_type{});
 }
 
-template <int MODE, int BM, int BN, int WAVES, int WAVES_M>
+// FLAT (4-bit modes, 128x128 tiles): K is not a multiple of 128, so the flat
+// 128-element scale groups of W straddle its rows; every packed word (8
+// weights, which K % 8 == 0 keeps inside one group) then reads its own scale
+// at (flat element index) / 128 and gets its own decode table.
+template <int MODE, int BM, int BN, int WAVES, int WAVES_M, bool FLAT = false>
 __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
   using TL = Tile<MODE, BM, BN, WAVES, WAVES_M>;
   constexpr int NT = TL::NT;
@@ -497,23 +501,26 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
   const int drow = tid / DTR, dsub = tid % DTR;       // DGRAD_Q4 mapping
   const int pb = tid % PB, qb = tid / PB;             // DGRAD_BF16 mapping
   // FWD_Q4 byte offsets at k = 0 of the thread's packed weights and of its
-  // row's first scale (kOOB beyond P).  K (= ldw) is a multiple of 128 here,
-  // so k-step kt adds kt*BK/2 payload bytes and scale group kt/2.
-  uint32_t w_po = kOOB, w_so = kOOB;
+  // row's first scale (kOOB beyond P).  Unless FLAT, K (= ldw) is a multiple
+  // of 128, so k-step kt adds kt*BK/2 payload bytes and scale group kt/2.
+  // FLAT keeps the flat element index w_eo of the thread's first weight.
+  uint32_t w_po = kOOB, w_so = kOOB, w_eo = kOOB;
   if constexpr (MODE == FWD_Q4) {
     int64_t n = p0 + brow;
     if (n < p.P) {
-      w_po = (uint32_t)((n * p.ldw + bsub * EPT) >> 1);
+      w_eo = (uint32_t)(n * p.ldw + bsub * EPT);
+      w_po = w_eo >> 1;
       w_so = (uint32_t)((n * p.ldw) >> 7) * 4;
     }
   }
   const bool dcol_ok = p0 + dsub * DE < p.P;
   static_assert(MODE != DGRAD_Q4 || NT / DTR == BK, "DGRAD_Q4: one thread row per contraction row");
 
+  static_assert(!FLAT || (TL::Q4 && BM == 128 && BN == 128), "FLAT: 4-bit 128x128 tiles only");
   struct WRegs {
     uint4 q[WQ];      // bf16 modes
     uint32_t w[NW];   // 4-bit modes
-    float s[1];
+    float s[FLAT ? NW : 1];  // scale of the tile's group, or of each word (FLAT)
   };
   // NW packed words from byte offset po (kOOB: zeros)
   auto load_words = [&](uint32_t po, uint32_t (&w)[NW]) {
@@ -535,7 +542,14 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
   auto load_W = [&](int kt, WRegs& w) {
     if constexpr (MODE == FWD_Q4) {
       load_words(w_po + (uint32_t)(kt * (BK / 2)), w.w);
-      w.s[0] = __builtin_bit_cast(float, ld4(rsS, w_so + (uint32_t)(kt >> 1) * 4));
+      if constexpr (FLAT) {
+#pragma unroll
+        for (int j = 0; j < NW; ++j)
+          w.s[j] = __builtin_bit_cast(
+              float, ld4(rsS, w_eo == kOOB ? kOOB : ((w_eo + (uint32_t)(kt * BK + 8 * j)) >> 7) * 4));
+      } else {
+        w.s[0] = __builtin_bit_cast(float, ld4(rsS, w_so + (uint32_t)(kt >> 1) * 4));
+      }
     } else if constexpr (MODE == FWD_BF16) {
 #pragma unroll
       for (int i = 0; i < WQ; ++i) {
@@ -547,9 +561,12 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
     } else if constexpr (MODE == DGRAD_Q4) {
       const int64_t n = (int64_t)kt * BK + drow;
       const bool ok = dcol_ok && n < p.Q;
-      const int64_t e = n * p.ldw + p0 + dsub * DE;   // DE-aligned: one scale group
+      // DE-aligned: one scale group unless FLAT
+      const int64_t e = n * p.ldw + p0 + dsub * DE;
       load_words(ok ? (uint32_t)(e >> 1) : kOOB, w.w);
-      w.s[0] = __builtin_bit_cast(float, ld4(rsS, ok ? (uint32_t)((e >> 7) * 4) : kOOB));
+#pragma unroll
+      for (int j = 0; j < (FLAT ? NW : 1); ++j)
+        w.s[j] = __builtin_bit_cast(float, ld4(rsS, ok ? (uint32_t)(((e + 8 * j) >> 7) * 4) : kOOB));
     } else {
       int64_t pc = p0 + pb * 8;
 #pragma unroll
@@ -573,7 +590,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
       for (int ch = 0; ch < NW; ++ch) {
         if (ch * 4 / NW != part) continue;
         uint32_t o[4];
-        deq8(w.w[ch], tbl, sh_e, 4u - sh_e, o);
+        if constexpr (FLAT)
+          deq8(w.w[ch], make_tbl(p.lut, w.s[ch]), sh_e, 4u - sh_e, o);
+        else
+          deq8(w.w[ch], tbl, sh_e, 4u - sh_e, o);
         const int ot = fresh_tid();
         const int idx = MODE == FWD_Q4 ? pad(ot / TPR, ((ot % TPR) * EPT) / 8 + ch)
                                        : dswz(ot / DTR, (ot % DTR) * NW + ch);
@@ -610,7 +630,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
     }
   };
   auto prep_B = [&](const WRegs& w) {
-    if constexpr (MODE == FWD_Q4 || MODE == DGRAD_Q4) tbl = make_tbl(p.lut, w.s[0]);
+    if constexpr (!FLAT && (MODE == FWD_Q4 || MODE == DGRAD_Q4)) tbl = make_tbl(p.lut, w.s[0]);
   };
 
   f32x16 acc[FM][FN];
@@ -1257,7 +1277,7 @@ int launch_rb(const GemmParams& p, hipStream_t stream) {
   return st::check_launch("q4gemm");
 }
 
-template <int MODE, int BM, int BN, int WAVES, int WAVES_M = 2>
+template <int MODE, int BM, int BN, int WAVES, int WAVES_M = 2, bool FLAT = false>
 int launch(const GemmParams& p, hipStream_t stream) {
   constexpr int NT = 64 * WAVES;
   int64_t tiles = row_tiles(p, BM) * st::cdiv(p.P, BN);
@@ -1274,7 +1294,7 @@ int launch(const GemmParams& p, hipStream_t stream) {
   using TL = Tile<MODE, BM, BN, WAVES, WAVES_M>;
   GemmParams q = p;
   if (int rc = choose_epilogue<TL::DGRAD, BM, BN>(q, (int64_t)TL::LDS_CHUNKS * 4, WAVES)) return rc;
-  gemm_kernel<MODE, BM, BN, WAVES, WAVES_M><<<(unsigned)tiles, NT, 0, stream>>>(q);
+  gemm_kernel<MODE, BM, BN, WAVES, WAVES_M, FLAT><<<(unsigned)tiles, NT, 0, stream>>>(q);
   return st::check_launch("q4gemm");
 }
 
@@ -1282,10 +1302,10 @@ int launch(const GemmParams& p, hipStream_t stream) {
 // enough tiles to cover the 256 CUs.  Forward with >= 192 tiles of 256x256:
 // the 256x256 register-operand kernel (the LDS-operand 8-wave kernel with
 // ST_GEMM_RB=0); otherwise the warp-specialised 256x128 kernel (2562) where it
-// yields >= 192 tiles; else 128x128 (4 waves).  ST_GEMM_TILE forces one (128,
-// 256, 2561 = 256x128 8 waves, 2562, 2564 = 256x256 4 waves; forward only:
-// register-operand 2565 = 256x256 4 waves, 2566 = 256x256 8 waves, 2567 =
-// 256x128 4 waves, 2568 = 128x256 8 waves).  For the N = 4096 forwards (o,
+// yields >= 192 tiles; else 128x128 (4 waves).  ST_GEMM_TILE forces one, so
+// tests can cover every tile the dispatch takes (128, 256, 2562; forward only,
+// register-operand: 2566 = 256x256 8 waves, 2567 = 256x128 4 waves (the
+// split tail), 2568 = 128x256 8 waves (the grouped forward)).  For the N = 4096 forwards (o,
 // down) the 256x128 register-operand and the 128x256 tiles measured no faster
 // than the warp-specialised kernel.
 int tile_choice(int mode, int64_t M, int64_t P) {
@@ -1381,11 +1401,8 @@ int dispatch(const GemmParams& p, hipStream_t stream) {
       if (t == 256 && rb) return launch_rb<1, 8>(p, stream);
     }
     if (t == 256) return launch<MODE, 256, 256, 8>(p, stream);
-    if (t == 2561) return launch<MODE, 256, 128, 8, 4>(p, stream);
     if (t == 2562) return launch_ws<MODE>(p, stream);
     if constexpr (MODE == FWD_Q4) {
-      if (t == 2564) return launch<MODE, 256, 256, 4>(p, stream);
-      if (t == 2565 && p.Q % (RB_ST * BK) == 0) return launch_rb<2, 4>(p, stream);
       if (t == 2566 && p.Q % (RB_ST * BK) == 0) return launch_rb<1, 8>(p, stream);
       if (t == 2567 && p.Q % (RB_ST * BK) == 0) return launch_rb<1, 4>(p, stream);
       if (t == 2568 && p.Q % (RB_ST * BK) == 0) return launch_rb<1, 8, 4>(p, stream);
@@ -1407,19 +1424,17 @@ bool al16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
 }  // namespace
 
-namespace st {
-int launch_dequant4(const uint8_t* payload, const float* scales, int64_t numel, int32_t group,
-                    const float* lut16, int32_t flags, uint16_t* out, hipStream_t stream);
-}
-
+// Every shape runs from the packed weight (K % 128 != 0 on the flat-group
+// kernels), so the fused linears take no workspace; the queries stay for
+// callers that size one.
 extern "C" int64_t st_q4_linear_fwd_workspace_bytes(int64_t M, int64_t N, int64_t K) {
-  (void)M;
-  return (K % 128 == 0) ? 0 : N * K * 2;
+  (void)M; (void)N; (void)K;
+  return 0;
 }
 
 extern "C" int64_t st_q4_linear_dgrad_workspace_bytes(int64_t M, int64_t N, int64_t K) {
-  (void)M;
-  return (K % 128 == 0) ? 0 : N * K * 2;
+  (void)M; (void)N; (void)K;
+  return 0;
 }
 
 static int check_lora_common(int64_t rank, int64_t cols) {
@@ -1473,22 +1488,14 @@ extern "C" int st_q4_linear_fwd(const uint16_t* x, int64_t M, int64_t K, int64_t
   p.a_bytes = ((M - 1) * ldx + K) * 2;
   ST_CHECK_ARG(p.a_bytes < (1ll << 31) && N * K * 2 < (1ll << 31),
                "st_q4_linear_fwd: operands above 2 GiB are not supported");
-  if (K % 128 == 0 && al16(payload)) {
-    p.Wq = payload; p.Ws = scales; p.ldw = K;
-    p.w_bytes = N * K / 2; p.s_bytes = N * K / 128 * 4;
-    return run_gemm(FWD_Q4, p, s);
-  }
-  // flat groups straddle rows: decode W once into the workspace, bf16 GEMM
-  int64_t need = N * K * 2;
-  if (!workspace || workspace_bytes < need)
-    return st::fail(ST_EWORKSPACE, "st_q4_linear_fwd: K=%lld needs %lld workspace bytes",
-                    (long long)K, (long long)need);
-  ST_CHECK_ARG(al16(workspace), "st_q4_linear_fwd: workspace not 16-byte aligned");
-  int rc = st::launch_dequant4(payload, scales, N * K, 128, lut16, flags, (uint16_t*)workspace, s);
-  if (rc) return rc;
-  p.Wb = (const uint16_t*)workspace; p.ldw = K;
-  p.w_bytes = N * K * 2; p.s_bytes = 0;
-  return run_gemm(FWD_BF16, p, s);
+  (void)workspace; (void)workspace_bytes;
+  ST_CHECK_ARG(((uintptr_t)payload & 3u) == 0, "st_q4_linear_fwd: payload not 4-byte aligned");
+  p.Wq = payload; p.Ws = scales; p.ldw = K;
+  p.w_bytes = N * K / 2; p.s_bytes = (N * K + 127) / 128 * 4;
+  if (K % 128 == 0 && al16(payload)) return run_gemm(FWD_Q4, p, s);
+  // flat scale groups straddle W's rows (or 16-byte loads would be misaligned):
+  // per-word scales on the 128x128 tile
+  return launch<FWD_Q4, 128, 128, 4, 2, true>(p, s);
 }
 
 static int dgrad_impl(const uint16_t* dy, int64_t M, int64_t N, int64_t lddy,
@@ -1526,22 +1533,13 @@ static int dgrad_impl(const uint16_t* dy, int64_t M, int64_t N, int64_t lddy,
   p.a_bytes = ((M - 1) * lddy + N) * 2;
   ST_CHECK_ARG(p.a_bytes < (1ll << 31) && N * K * 2 < (1ll << 31),
                "st_q4_linear_dgrad: operands above 2 GiB are not supported");
-  if (K % 128 == 0) {
-    ST_CHECK_ARG(((uintptr_t)payload & 3u) == 0, "st_q4_linear_dgrad: payload not 4-byte aligned");
-    p.Wq = payload; p.Ws = scales; p.ldw = K;
-    p.w_bytes = N * K / 2; p.s_bytes = N * K / 128 * 4;
-    return run_gemm(DGRAD_Q4, p, s);
-  }
-  int64_t need = N * K * 2;
-  if (!workspace || workspace_bytes < need)
-    return st::fail(ST_EWORKSPACE, "st_q4_linear_dgrad: K=%lld needs %lld workspace bytes",
-                    (long long)K, (long long)need);
-  ST_CHECK_ARG(al16(workspace), "st_q4_linear_dgrad: workspace not 16-byte aligned");
-  int rc = st::launch_dequant4(payload, scales, N * K, 128, lut16, flags, (uint16_t*)workspace, s);
-  if (rc) return rc;
-  p.Wb = (const uint16_t*)workspace; p.ldw = K;
-  p.w_bytes = N * K * 2; p.s_bytes = 0;
-  return run_gemm(DGRAD_BF16, p, s);
+  (void)workspace; (void)workspace_bytes;
+  ST_CHECK_ARG(((uintptr_t)payload & 3u) == 0, "st_q4_linear_dgrad: payload not 4-byte aligned");
+  p.Wq = payload; p.Ws = scales; p.ldw = K;
+  p.w_bytes = N * K / 2; p.s_bytes = (N * K + 127) / 128 * 4;
+  if (K % 128 == 0) return run_gemm(DGRAD_Q4, p, s);
+  // flat scale groups straddle W's rows: per-word scales on the 128x128 tile
+  return launch<DGRAD_Q4, 128, 128, 4, 2, true>(p, s);
 }
 
 extern "C" int st_q4_linear_dgrad(const uint16_t* dy, int64_t M, int64_t N, int64_t lddy,
@@ -1569,8 +1567,8 @@ extern "C" int st_q4_linear_dgrad_swiglu(const uint16_t* dy, int64_t M, int64_t 
 // ---------------------------------------------------------------- grouped (MoE)
 namespace {
 // Grouped (per-expert) launches take the dense kernels' tiles; ST_GROUPED_TILE
-// forces one (128, 2561, 2562; forward only: 256, and the register-operand
-// 2566 = 256x256, 2567 = 256x128, 2568 = 128x256).
+// forces one (128, 2562; forward only: the register-operand 2566 = 256x256,
+// 2568 = 128x256).
 template <int MODE>
 int launch_grouped(const GemmParams& p, hipStream_t stream) {
   // default: register-operand 128x256 tiles for the forward (K % 256 == 0;
@@ -1579,12 +1577,9 @@ int launch_grouped(const GemmParams& p, hipStream_t stream) {
   const char* env = getenv("ST_GROUPED_TILE");
   const int t = env ? atoi(env) : (MODE == FWD_Q4 && p.Q % (RB_ST * BK) == 0) ? 2568 : 128;
   if (t == 2562) return launch_ws<MODE>(p, stream);
-  if (t == 2561) return launch<MODE, 256, 128, 8, 4>(p, stream);
   if constexpr (MODE == FWD_Q4) {
-    if (t == 256) return launch<MODE, 256, 256, 8>(p, stream);
     // register-operand tiles (K % 256 == 0)
     if (t == 2566 && p.Q % (RB_ST * BK) == 0) return launch_rb<1, 8>(p, stream);
-    if (t == 2567 && p.Q % (RB_ST * BK) == 0) return launch_rb<1, 4>(p, stream);
     if (t == 2568 && p.Q % (RB_ST * BK) == 0) return launch_rb<1, 8, 4>(p, stream);
   }
   return launch<MODE, 128, 128, 4>(p, stream);

@@ -241,8 +241,6 @@ class _Q4LoRALinear(torch.autograd.Function):
             # T = x_f32 A_cat^T   (lora.py:219 inner linear)
             lora_gemm(M, nseg * rank, K, x, K, 1, A_cat, 1, K, 1.0, T)
             ends = _lib.i64_array(torch.tensor(weight.segments).cumsum(0).tolist())
-        need = _lib.query("st_q4_linear_fwd_workspace_bytes", M, N, K)
-        ws = _ws.get(dev, need)
         _launch(("fwd", M, N, K), lambda: _lib.call(
             "st_q4_linear_fwd", _lib.ptr(x), M, K, K, _lib.ptr(weight.payload),
             _lib.ptr(weight.scales), N, weight.lut(), weight.flags,
@@ -250,7 +248,7 @@ class _Q4LoRALinear(torch.autograd.Function):
             _lib.ptr(B_cat) if ab else None, rank if ab else 0, float(scale),
             nseg if ab else 0, ends if ab else None,
             _lib.ptr(residual), 0 if residual is None else residual.stride(0),
-            _lib.ptr(y), N, _lib.ptr(ws), 0 if ws is None else ws.numel(), stream))
+            _lib.ptr(y), N, None, 0, stream))
         ctx.weight, ctx.rank, ctx.scale = weight, rank, scale
         ctx.has_residual = residual is not None
         ctx.nlora = len(ab)
@@ -308,8 +306,6 @@ class _Q4LoRALinear(torch.autograd.Function):
                 grads_ab += [dA_cat[s * rank:(s + 1) * rank], dBs[s]]
         else:
             x, gu = ctx.saved_tensors
-        need = _lib.query("st_q4_linear_dgrad_workspace_bytes", M, N, K)
-        ws = _ws.get(dev, need)
         lora_args = (_lib.ptr(dT), 0 if dT is None else dT.stride(0), _lib.ptr(A_cat),
                      0 if dT is None else dT.shape[1])
         if ctx.swiglu_I:
@@ -318,14 +314,13 @@ class _Q4LoRALinear(torch.autograd.Function):
             _launch(("dgrad", M, N, K), lambda: _lib.call(
                 "st_q4_linear_dgrad_swiglu", _lib.ptr(dy), M, N, N, _lib.ptr(weight.payload),
                 _lib.ptr(weight.scales), K, weight.lut(), weight.flags, *lora_args,
-                _lib.ptr(gu), gu.stride(0), _lib.ptr(dx), dx.stride(0),
-                _lib.ptr(ws), 0 if ws is None else ws.numel(), stream))
+                _lib.ptr(gu), gu.stride(0), _lib.ptr(dx), dx.stride(0), None, 0, stream))
         else:
             dx = torch.empty((M, K), dtype=_BF16, device=dev)
             _launch(("dgrad", M, N, K), lambda: _lib.call(
                 "st_q4_linear_dgrad", _lib.ptr(dy), M, N, N, _lib.ptr(weight.payload),
                 _lib.ptr(weight.scales), K, weight.lut(), weight.flags, *lora_args,
-                _lib.ptr(dx), K, _lib.ptr(ws), 0 if ws is None else ws.numel(), stream))
+                _lib.ptr(dx), K, None, 0, stream))
         dres = dy if ctx.has_residual else None
         return (dx, None, dres, None, None, None, *grads_ab)
 

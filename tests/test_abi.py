@@ -47,8 +47,9 @@ def test_abi_version_and_error_mapping():
 
 def test_workspace_queries():
     assert _lib.query("st_q4_linear_fwd_workspace_bytes", 16, 256, 4096) == 0
-    assert _lib.query("st_q4_linear_fwd_workspace_bytes", 16, 256, 688) == 256 * 688 * 2
-    assert _lib.query("st_q4_linear_dgrad_workspace_bytes", 16, 256, 688) == 256 * 688 * 2
+    # K % 128 != 0 runs on the flat-group kernels from the packed weight
+    assert _lib.query("st_q4_linear_fwd_workspace_bytes", 16, 256, 688) == 0
+    assert _lib.query("st_q4_linear_dgrad_workspace_bytes", 16, 256, 688) == 0
     ws = _lib.query("st_lora_gemm_workspace_bytes", 2048, 16, 4096)
     assert ws > 0 and ws % (2048 * 16 * 4) == 0
 
