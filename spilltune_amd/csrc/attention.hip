@@ -40,23 +40,34 @@ __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast
 __host__ __device__ __forceinline__ int vpos(int j) {
   return (j & ~12) | ((j & 4) << 1) | ((j & 8) >> 1);
 }
-// dst[n][d][vpos(s)] = src[n][s][d] (rows of Sp >= S elements, zero past S)
+// dst[n][d][vpos(s)] = src[n][s][d] (rows of Sp >= S elements, zero past S).
+// A workgroup moves a 64-key x 64-d block: 16-byte loads of source rows into
+// LDS, then each thread gathers 8 keys of one d column and writes them as one
+// 16-byte store (Sp is a multiple of 16, so every output chunk is aligned).
+// D is a multiple of 8 and src 16-byte aligned (checked by the host).
 __global__ __launch_bounds__(NTH) void transpose_heads(const uint16_t* __restrict__ src,
                                                        uint16_t* __restrict__ dst, int64_t S,
                                                        int64_t Sp, int D) {
-  __shared__ uint16_t t[64][66];
+  __shared__ __attribute__((aligned(16))) uint16_t t[64][72];  // [key][d], 16-byte rows
   const int64_t n = blockIdx.z;
   const int64_t s0 = (int64_t)blockIdx.x * 64, d0 = (int64_t)blockIdx.y * 64;
   const uint16_t* in = src + n * S * D;
   uint16_t* out = dst + n * Sp * D;
-  for (int i = threadIdx.x; i < 64 * 64; i += NTH) {
-    const int r = i / 64, c = i % 64;
-    t[r][c] = (s0 + r < S && d0 + c < D) ? in[(s0 + r) * D + d0 + c] : 0;
+  for (int i = threadIdx.x; i < 64 * 8; i += NTH) {
+    const int r = i / 8, c = (i % 8) * 8;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (s0 + r < S && d0 + c < D) v = *(const uint4*)(in + (s0 + r) * D + d0 + c);
+    *(uint4*)&t[r][c] = v;
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < 64 * 64; i += NTH) {
-    const int r = i / 64, c = i % 64;  // r: d, c: position in the 64-key block
-    if (d0 + r < D && s0 + c < Sp) out[(d0 + r) * Sp + s0 + c] = t[vpos(c)][r];
+  for (int i = threadIdx.x; i < 64 * 8; i += NTH) {
+    const int r = i / 8, c = (i % 8) * 8;  // r: d, c: first of 8 positions in the 64-key block
+    if (d0 + r >= D || s0 + c >= Sp) continue;
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      w[e] = (uint32_t)t[vpos(c + 2 * e)][r] | ((uint32_t)t[vpos(c + 2 * e + 1)][r] << 16);
+    *(uint4*)(out + (d0 + r) * Sp + s0 + c) = make_uint4(w[0], w[1], w[2], w[3]);
   }
 }
 

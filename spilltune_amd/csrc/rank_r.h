@@ -98,12 +98,17 @@ __device__ __forceinline__ void rk_accumulate(f32x16 (&acc)[NB], int64_t mend, i
           off = gbase[i] + (uint32_t)k0 * 2;
         }
       }
+      // the offset is materialised before the load: left to itself the
+      // compiler turns a select of two offsets into two loads on divergent
+      // paths, each behind a wait for every load in flight
+      asm volatile("" : "+v"(off));
       g[i] = ld16(rsG, off);
     }
 #pragma unroll
     for (int i = 0; i < SIT; ++i) {
       const int k = k0 + s_kk(i), j = s_j(i);
-      const uint32_t off = (k < ke && j < R) ? (uint32_t)k * ssk4 + (uint32_t)j * ssj4 : kOOB;
+      uint32_t off = (k < ke && j < R) ? (uint32_t)k * ssk4 + (uint32_t)j * ssj4 : kOOB;
+      asm volatile("" : "+v"(off));
       sv[i] = __builtin_bit_cast(float, ld4(rsS, off));
     }
   };
@@ -129,6 +134,22 @@ __device__ __forceinline__ void rk_accumulate(f32x16 (&acc)[NB], int64_t mend, i
     }
   };
 
+  auto chunk_mfmas = [&]() {
+#pragma unroll
+    for (int s = 0; s < RK_BK / 16; ++s) {
+      const int ko = s * 16 + (lane >> 5) * 8;
+      const bf16x8 a = COL ? tr_operand<RK_BM>((const uint4*)Gs, s * 16, wave * 32, lane)
+                           : *(const bf16x8*)&Gs[(wave * 32 + (lane & 31)) * RK_LD + ko];
+#pragma unroll
+      for (int cc = 0; cc < NB; ++cc)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const bf16x8 b = *(const bf16x8*)&Ss[(h * RK_RP + cc * 32 + (lane & 31)) * RK_LD + ko];
+          acc[cc] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[cc], 0, 0, 0);
+        }
+    }
+  };
+
 #pragma unroll
   for (int c = 0; c < RK_PF; ++c)
     if (kb + c * RK_BK < ke) load(kb + c * RK_BK, gr[c], sr[c]);
@@ -140,20 +161,7 @@ __device__ __forceinline__ void rk_accumulate(f32x16 (&acc)[NB], int64_t mend, i
       store(gr[c], sr[c]);
       __syncthreads();
       if (k0 + RK_PF * RK_BK < ke) load(k0 + RK_PF * RK_BK, gr[c], sr[c]);
-#pragma unroll
-      for (int s = 0; s < RK_BK / 16; ++s) {
-        const int ko = s * 16 + (lane >> 5) * 8;
-        const bf16x8 a = COL ? tr_operand<RK_BM>((const uint4*)Gs, s * 16, wave * 32, lane)
-                             : *(const bf16x8*)&Gs[(wave * 32 + (lane & 31)) * RK_LD + ko];
-#pragma unroll
-        for (int cc = 0; cc < NB; ++cc)
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const bf16x8 b =
-                *(const bf16x8*)&Ss[(h * RK_RP + cc * 32 + (lane & 31)) * RK_LD + ko];
-            acc[cc] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[cc], 0, 0, 0);
-          }
-      }
+      chunk_mfmas();
       __syncthreads();
     }
   }
