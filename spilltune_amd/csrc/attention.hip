@@ -397,11 +397,24 @@ __global__ __launch_bounds__(NTH * G, G == 1 && BKT == 64 && DQ <= 128 ? 2 : 1) 
 }
 
 // ---------------------------------------------------------------- backward
-// Row-major [rows][D] LDS tile, 16-byte chunks XOR-swizzled so that both
-// 16-byte row reads and the transposing 8-byte reads below avoid conflicts.
+// Row-major [rows][D] LDS tile, 16-byte chunks XOR-swizzled by row.  For
+// D = 128 (rows of 256 bytes, each starting at bank 0) the XOR value
+// ((row & 3) << 2) | ((row >> 2) & 3) is a permutation of row & 15, so the
+// 16 rows of a quarter-wave 16-byte read (tile_row) land on 16 distinct chunk
+// positions, and the 4 rows x 4 chunks of a half-wave transposing 8-byte read
+// (tile_tr: rows 4 apart in bits 2-3 of the XOR value, chunks in bits 0-1)
+// land on 16 distinct chunks: both are free of bank conflicts.  Other widths
+// keep the XOR value ((row & 7) << 1), which stays inside the row's chunks.
+template <int D>
+__device__ __forceinline__ int swz(int row) {
+  if constexpr (D == 128)
+    return ((row & 3) << 2) | ((row >> 2) & 3);
+  else
+    return ((row & 7) << 1) & (D / 8 - 1);
+}
 template <int D>
 __device__ __forceinline__ int tswz(int row, int chunk) {
-  return row * D + ((chunk ^ (((row & 7) << 1) & (D / 8 - 1))) << 3);
+  return row * D + ((chunk ^ swz<D>(row)) << 3);
 }
 template <int D>
 __device__ __forceinline__ bf16x8 tile_row(const uint16_t* t, int row, int s, int g) {
@@ -498,14 +511,14 @@ __device__ __forceinline__ void fa_bwd_dq_tile(
     for (int i = 0; i < PERK; ++i) {
       const int P = i * NTH + gtid;
       const int row = P / (DQ / 8);
-      const int ch = (P % (DQ / 8)) ^ (((row & 7) << 1) & (DQ / 8 - 1));
+      const int ch = (P % (DQ / 8)) ^ swz<DQ>(row);
       g2lds16(kb + (int64_t)min(k0 + row, S - 1) * DQ + ch * 8, ks + (i * NTH + wave * 64) * 8);
     }
 #pragma unroll
     for (int i = 0; i < PERV; ++i) {
       const int P = i * NTH + gtid;
       const int row = P / (DV / 8);
-      const int ch = (P % (DV / 8)) ^ (((row & 7) << 1) & (DV / 8 - 1));
+      const int ch = (P % (DV / 8)) ^ swz<DV>(row);
       g2lds16(vb + (int64_t)min(k0 + row, S - 1) * DV + ch * 8, vs + (i * NTH + wave * 64) * 8);
     }
   };
@@ -708,7 +721,7 @@ __device__ __forceinline__ void fa_bwd_dkdv_tile(
     for (int i = 0; i < PERQ; ++i) {
       const int P = i * NTH2 + tid;
       const int row = P / (DQ / 8);
-      const int ch = (P % (DQ / 8)) ^ (((row & 7) << 1) & (DQ / 8 - 1));
+      const int ch = (P % (DQ / 8)) ^ swz<DQ>(row);
       const int qq = min(q0 + row, S - 1);
       g2lds16(qb + (int64_t)qq * DQ + ch * 8, qs + (i * NTH2 + wave * 64) * 8);
     }
@@ -716,7 +729,7 @@ __device__ __forceinline__ void fa_bwd_dkdv_tile(
     for (int i = 0; i < PERG; ++i) {
       const int P = i * NTH2 + tid;
       const int row = P / (DV / 8);
-      const int ch = (P % (DV / 8)) ^ (((row & 7) << 1) & (DV / 8 - 1));
+      const int ch = (P % (DV / 8)) ^ swz<DV>(row);
       const int qq = min(q0 + row, S - 1);
       g2lds16(gb + (int64_t)qq * ldt + ch * 8, gs + (i * NTH2 + wave * 64) * 8);
     }
