@@ -83,15 +83,33 @@ __device__ __forceinline__ uint32_t ld4(__amdgpu_buffer_rsrc_t r, uint32_t off) 
 }
 
 // Transposed-operand tile: rows n (the contraction) of BN bf16 held as BN/8
-// 16-byte chunks, chunk c of row n at n*(BN/8) + (c ^ 5*(n & 3)).  XOR with
-// 5r moves bits 0-1 and 2-3 of the chunk by the row's r = n & 3, so each
-// quarter-wave of 16-byte stores (one row x 16 chunks, two rows x 8 even or
-// odd chunks, or four rows x 4 chunks 4 apart) and each half-wave of the
-// transposing reads below (4 rows x 4 consecutive chunks) covers all 64
-// banks once.  Index in 16-byte units; BN >= 128.
+// 16-byte chunks, chunk c of row n at n*(BN/8) + (c ^ x(n)).  For BN = 128
+// (rows of 256 bytes, each starting at bank 0) x(n) = ((n & 3) << 2) |
+// ((n >> 2) & 3), a permutation of n & 15; wider tiles use x(n) = 5*(n & 3).
+// The transposing reads below (4 rows x 4 consecutive chunks per half-wave)
+// and the 16-byte stores of the dgrad kernels (each lane writes the 4 chunks
+// of its 32-column group in an order rotated by that group's index, see
+// rot4) are free of bank conflicts with the BN = 128 form (measured with
+// SQ_LDS_BANK_CONFLICT; the earlier 5*(n & 3) form cost 8 conflict cycles
+// per store instruction).  Index in 16-byte units; BN >= 128.
 template <int BN>
 __device__ __forceinline__ int trswz(int n, int c) {
-  return n * (BN / 8) + (c ^ (5 * (n & 3)));
+  if constexpr (BN == 128)
+    return n * 16 + (c ^ (((n & 3) << 2) | ((n >> 2) & 3)));
+  else
+    return n * (BN / 8) + (c ^ (5 * (n & 3)));
+}
+// Rotates four words left by r (0..3): w[i] <- w[(i + r) & 3], with selects
+// (no dynamic register indexing).
+template <typename T>
+__device__ __forceinline__ void rot4(T (&w)[4], int r) {
+  const bool r2 = r & 2, r1 = r & 1;
+  const T a0 = r2 ? w[2] : w[0], a1 = r2 ? w[3] : w[1], a2 = r2 ? w[0] : w[2],
+          a3 = r2 ? w[1] : w[3];
+  w[0] = r1 ? a1 : a0;
+  w[1] = r1 ? a2 : a1;
+  w[2] = r1 ? a3 : a2;
+  w[3] = r1 ? a0 : a3;
 }
 // MFMA 32x32x16 operand from such a tile: lane (column kc + lane%32, half
 // g = lane/32) gets rows n0 + 8g + s, s = 0..7.  ds_read_b64_tr_b16: within

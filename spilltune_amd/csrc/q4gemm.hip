@@ -517,6 +517,11 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
   static_assert(MODE != DGRAD_Q4 || NT / DTR == BK, "DGRAD_Q4: one thread row per contraction row");
 
   static_assert(!FLAT || (TL::Q4 && BM == 128 && BN == 128), "FLAT: 4-bit 128x128 tiles only");
+  // DGRAD_Q4 with 128-wide B rows: each thread's 4 words are dequantised and
+  // stored in an order rotated by its group dsub, free of LDS bank conflicts
+  // with st::trswz<128> (every store instruction of a quarter-wave then
+  // writes each 4-chunk group's chunk (ch + group) & 3)
+  constexpr bool DROT = MODE == DGRAD_Q4 && BN == 128 && NW == 4 && DTR == 4;
   struct WRegs {
     uint4 q[WQ];      // bf16 modes
     uint32_t w[NW];   // 4-bit modes
@@ -567,6 +572,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
 #pragma unroll
       for (int j = 0; j < (FLAT ? NW : 1); ++j)
         w.s[j] = __builtin_bit_cast(float, ld4(rsS, ok ? (uint32_t)(((e + 8 * j) >> 7) * 4) : kOOB));
+      if constexpr (DROT) {  // stored in rotated order, see store_B_part
+        st::rot4(w.w, dsub);
+        if constexpr (FLAT) st::rot4(w.s, dsub);
+      }
     } else {
       int64_t pc = p0 + pb * 8;
 #pragma unroll
@@ -595,8 +604,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
         else
           deq8(w.w[ch], tbl, sh_e, 4u - sh_e, o);
         const int ot = fresh_tid();
-        const int idx = MODE == FWD_Q4 ? pad(ot / TPR, ((ot % TPR) * EPT) / 8 + ch)
-                                       : dswz(ot / DTR, (ot % DTR) * NW + ch);
+        const int idx =
+            MODE == FWD_Q4 ? pad(ot / TPR, ((ot % TPR) * EPT) / 8 + ch)
+            : DROT         ? dswz(ot / DTR, (ot % DTR) * NW + ((ch + ot % DTR) & 3))
+                           : dswz(ot / DTR, (ot % DTR) * NW + ch);
         bs[idx] = make_uint4(o[0], o[1], o[2], o[3]);
       }
     } else if constexpr (MODE == FWD_BF16) {
@@ -849,7 +860,10 @@ __global__ __launch_bounds__(512) void gemm_ws_kernel(GemmParams p) {
     Tbl tbl;
     const uint32_t sh_e = p.hi_first ? 4u : 0u;
     auto store_B = [&](uint4* bs, const WR& w) {
-      const uint32_t words[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
+      uint32_t words[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
+      // dgrad: chunk (ch + bsub) & 3 of the thread's group goes out in store
+      // ch, which keeps every store instruction free of bank conflicts
+      if constexpr (MODE == DGRAD_Q4) st::rot4(words, bsub);
 #pragma unroll
       for (int ch = 0; ch < 4; ++ch) {
         uint32_t o[4];
@@ -859,7 +873,7 @@ __global__ __launch_bounds__(512) void gemm_ws_kernel(GemmParams p) {
           // fragment (n-block brow/32, slice 2*bsub + ch/2), lane brow%32 + 32*(ch&1)
           idx = ((brow >> 5) * 4 + 2 * bsub + (ch >> 1)) * 64 + (brow & 31) + 32 * (ch & 1);
         } else {
-          idx = st::trswz<BN>(brow, bsub * 4 + ch);
+          idx = st::trswz<BN>(brow, bsub * 4 + ((ch + bsub) & 3));
         }
         bs[idx] = make_uint4(o[0], o[1], o[2], o[3]);
       }
