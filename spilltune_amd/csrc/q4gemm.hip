@@ -467,12 +467,14 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
       xr[i] = ld16(rsA, off);
     }
   };
-  // LDS store addresses are rebuilt from an opaque copy of tid at each use
-  // (a few VALU) rather than kept live across the loop, where they would be
-  // the first values the 256x256 tile spills.
+  // LDS addresses of the 256-wide tiles are rebuilt from an opaque copy of
+  // tid at each use (a few VALU) rather than kept live across the loop, where
+  // they would be the first values the 256x256 tile spills.  The 128x128
+  // tile has registers to spare: its addresses stay loop-invariant (rebuilt,
+  // the dgrad's transposed-operand addresses alone cost ~160 VALU per k-step).
   auto fresh_tid = [&]() {
     int t = tid;
-    asm volatile("" : "+v"(t));
+    if constexpr (BM * BN > 128 * 128) asm volatile("" : "+v"(t));
     return t;
   };
   auto store_A = [&](uint4* as, const uint4 (&xr)[TL::A_IT]) {
