@@ -214,6 +214,23 @@ int st_rope_qkv_bwd(const uint16_t* dq, const uint16_t* dk, const uint16_t* dv,
                     const uint16_t* cos, const uint16_t* sin, int64_t B, int64_t S,
                     int64_t heads, int64_t kv_heads, int64_t D, uint16_t* dx, int64_t lddx,
                     st_stream_t stream);
+/* Qwen3 qk_norm fused with st_rope_qkv_fwd (dense.py:128-141 with qk_norm):
+ * every query head and key head of the fused q|k|v rows is RMS-normalised over
+ * its D elements (weights wq / wk [D], eps; rounding of st_rmsnorm_fwd) and
+ * then rotated; value heads are copied.  rstd [B*S, heads+kv_heads] fp32 is
+ * kept for the backward.  D = 64 or 128, 16-byte aligned operands. */
+int st_rope_qkv_norm_fwd(const uint16_t* x, int64_t ldx, const uint16_t* cos, const uint16_t* sin,
+                         int64_t B, int64_t S, int64_t heads, int64_t kv_heads, int64_t D,
+                         const uint16_t* wq, const uint16_t* wk, float eps, uint16_t* q,
+                         uint16_t* k, uint16_t* v, float* rstd, st_stream_t stream);
+/* VJP of st_rope_qkv_norm_fwd (x: the forward's input rows): the rotation's
+ * VJP then the norm's (rounding of st_rope_qkv_bwd, st_rmsnorm_bwd); dx rows
+ * of stride lddx. */
+int st_rope_qkv_norm_bwd(const uint16_t* dq, const uint16_t* dk, const uint16_t* dv,
+                         const uint16_t* x, int64_t ldx, const uint16_t* cos, const uint16_t* sin,
+                         const uint16_t* wq, const uint16_t* wk, const float* rstd, int64_t B,
+                         int64_t S, int64_t heads, int64_t kv_heads, int64_t D, uint16_t* dx,
+                         int64_t lddx, st_stream_t stream);
 /* [B,heads,S,D] -> [B,S,heads*D] copy (attention output relayout). */
 int st_heads_to_tokens(const uint16_t* x, int64_t B, int64_t S, int64_t heads, int64_t D,
                        uint16_t* out, st_stream_t stream);

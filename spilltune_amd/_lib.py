@@ -52,6 +52,10 @@ _SIGNATURES = {
     "st_rope_bwd": (_I32, [_P, _P, _P, _I64, _I64, _I64, _I64, _I32, _P, _I64, _P]),
     "st_rope_qkv_fwd": (_I32, [_P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P]),
     "st_rope_qkv_bwd": (_I32, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P]),
+    "st_rope_qkv_norm_fwd": (_I32, [_P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _F,
+                                    _P, _P, _P, _P, _P]),
+    "st_rope_qkv_norm_bwd": (_I32, [_P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _I64, _I64,
+                                    _I64, _I64, _P, _I64, _P]),
     "st_heads_to_tokens": (_I32, [_P, _I64, _I64, _I64, _I64, _P, _P]),
     "st_tokens_to_heads": (_I32, [_P, _I64, _I64, _I64, _I64, _P, _P]),
     "st_swiglu_fwd": (_I32, [_P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P]),

@@ -451,6 +451,143 @@ bool vec8(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 unsigned nblk(int64_t total) { return (unsigned)st::cdiv(total, NTH); }
 
+
+// Qwen3's per-head q/k RMSNorm fused with the rotation (dense.py:128-141):
+// every query and key head of a fused q|k|v row is normalised over its D
+// elements (weights wq / wk, the rounding of rmsnorm_fwd: w * bf16(x * r)) and
+// then rotated (rope_chunk_fwd's rounding); value heads are copied.  One
+// workgroup per token; CH = D/8 consecutive lanes hold one head (lane c has
+// chunk c), so the head's sum of squares is a CH-lane xor reduction and the
+// rotation's partner chunk c ^ CH/2 comes from a lane of the same group.  The
+// loop runs the same number of steps on every wave; groups past the last head
+// only skip their loads and stores.
+template <int D>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int o = D / 16; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ void shfl8(const float (&v)[8], int o, float (&p)[8]) {
+  const uint4 q = pack8(v);
+  uint4 r;
+  r.x = __shfl_xor(q.x, o, 64);
+  r.y = __shfl_xor(q.y, o, 64);
+  r.z = __shfl_xor(q.z, o, 64);
+  r.w = __shfl_xor(q.w, o, 64);
+  unpack8(r, p);
+}
+template <int D>
+__global__ __launch_bounds__(NTH) void rope_qkv_norm_fwd(
+    const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ cs,
+    const uint16_t* __restrict__ sn, int S, QkvHeads qh, const uint16_t* __restrict__ wq,
+    const uint16_t* __restrict__ wk, float eps, float* __restrict__ rstd) {
+  constexpr int CH = D / 8, HALF = CH / 2, GPB = NTH / CH;  // lanes per head, heads per pass
+  const int64_t t = blockIdx.x;
+  const int64_t b = t / S, s = t % S;
+  const int nn = qh.h[0] + qh.h[1], nh = nn + qh.h[2];
+  const int c = threadIdx.x % CH;
+  for (int h0 = 0; h0 < nh; h0 += GPB) {
+    const int hh = h0 + threadIdx.x / CH;
+    const bool ok = hh < nh;
+    const int seg = hh < qh.h[0] ? 0 : hh < nn ? 1 : 2;
+    const int hl = hh - (seg == 0 ? 0 : seg == 1 ? qh.h[0] : nn);
+    float v[8];
+    unpack8(ok ? *(const uint4*)(x + t * ldx + (int64_t)hh * D + c * 8) : make_uint4(0, 0, 0, 0), v);
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
+    ss = group_sum<D>(ss);
+    const float r = 1.0f / sqrtf(ss / (float)D + eps);
+    float n[8], p[8], o[8];
+    if (seg < 2) {
+      float g[8];
+      unpack8(*(const uint4*)((seg == 0 ? wq : wk) + c * 8), g);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) n[e] = st::bf16r(g[e] * st::bf16r(v[e] * r));
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) n[e] = v[e];
+    }
+    shfl8(n, HALF, p);
+    if (!ok) continue;
+    if (seg < 2) {
+      float cv[8], sv[8];
+      unpack8(*(const uint4*)(cs + t * D + c * 8), cv);
+      unpack8(*(const uint4*)(sn + t * D + c * 8), sv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float rot = c < HALF ? -p[e] : p[e];
+        o[e] = st::bf16r(n[e] * cv[e]) + st::bf16r(rot * sv[e]);
+      }
+      if (c == 0) rstd[t * nn + hh] = r;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = n[e];
+    }
+    *(uint4*)(qh.o[seg] + ((b * qh.h[seg] + hl) * S + s) * D + c * 8) = pack8(o);
+  }
+}
+
+// VJP of rope_qkv_norm_fwd: rope_chunk_bwd's rotation VJP (rounded to bf16),
+// then rmsnorm_bwd's VJP of the head norm with the saved rstd; value heads
+// are copied.  dx rows of stride lddx.
+template <int D>
+__global__ __launch_bounds__(NTH) void rope_qkv_norm_bwd(
+    const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ cs,
+    const uint16_t* __restrict__ sn, int S, QkvHeads qh, const uint16_t* __restrict__ wq,
+    const uint16_t* __restrict__ wk, const float* __restrict__ rstd, uint16_t* __restrict__ dx,
+    int64_t lddx) {
+  constexpr int CH = D / 8, HALF = CH / 2, GPB = NTH / CH;
+  const int64_t t = blockIdx.x;
+  const int64_t b = t / S, s = t % S;
+  const int nn = qh.h[0] + qh.h[1], nh = nn + qh.h[2];
+  const int c = threadIdx.x % CH;
+  for (int h0 = 0; h0 < nh; h0 += GPB) {
+    const int hh = h0 + threadIdx.x / CH;
+    const bool ok = hh < nh;
+    const int seg = hh < qh.h[0] ? 0 : hh < nn ? 1 : 2;
+    const int hl = hh - (seg == 0 ? 0 : seg == 1 ? qh.h[0] : nn);
+    float gv[8], gp[8];
+    unpack8(ok ? *(const uint4*)(qh.g[seg] + ((b * qh.h[seg] + hl) * S + s) * D + c * 8)
+               : make_uint4(0, 0, 0, 0), gv);
+    shfl8(gv, HALF, gp);
+    float d[8], xv[8], g[8], dn[8];
+    float dot = 0.0f, r = 0.0f;
+    if (seg < 2) {
+      float cv[8], sp[8];
+      unpack8(*(const uint4*)(cs + t * D + c * 8), cv);
+      unpack8(*(const uint4*)(sn + t * D + (c ^ HALF) * 8), sp);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float a = st::bf16r(gv[e] * cv[e]);
+        const float gs = st::bf16r(gp[e] * sp[e]);
+        d[e] = st::bf16r(a + (c < HALF ? gs : -gs));
+      }
+      unpack8(ok ? *(const uint4*)(x + t * ldx + (int64_t)hh * D + c * 8) : make_uint4(0, 0, 0, 0),
+              xv);
+      unpack8(*(const uint4*)((seg == 0 ? wq : wk) + c * 8), g);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        dn[e] = st::bf16r(d[e] * g[e]);
+        dot += dn[e] * xv[e];
+      }
+      r = ok ? rstd[t * nn + hh] : 0.0f;
+    }
+    dot = group_sum<D>(dot);
+    if (!ok) continue;
+    float o[8];
+    if (seg < 2) {
+      const float cc = r * r * r * dot / (float)D;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = st::bf16r(r * dn[e] - xv[e] * cc);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = gv[e];
+    }
+    *(uint4*)(dx + t * lddx + (int64_t)hh * D + c * 8) = pack8(o);
+  }
+}
+
 }  // namespace
 
 extern "C" int st_rmsnorm_fwd(const uint16_t* x, const uint16_t* w, int64_t rows, int64_t H,
@@ -573,6 +710,65 @@ extern "C" int st_rope_qkv_bwd(const uint16_t* dq, const uint16_t* dk, const uin
   rope_qkv_bwd_vec<<<(unsigned)(B * S), NTH, 0, (hipStream_t)stream>>>(cos, sin, (int)S, (int)D,
                                                                       qh, dx, lddx);
   return st::check_launch("rope_qkv_bwd");
+}
+
+// Per-head q/k RMSNorm + rotation of a fused q|k|v row (Qwen3 qk_norm), one launch
+extern "C" int st_rope_qkv_norm_fwd(const uint16_t* x, int64_t ldx, const uint16_t* cos,
+                                    const uint16_t* sin, int64_t B, int64_t S, int64_t heads,
+                                    int64_t kv_heads, int64_t D, const uint16_t* wq,
+                                    const uint16_t* wk, float eps, uint16_t* q, uint16_t* k,
+                                    uint16_t* v, float* rstd, st_stream_t stream) {
+  ST_CHECK_ARG(B >= 0 && S >= 0 && heads > 0 && kv_heads > 0 && (D == 64 || D == 128),
+               "st_rope_qkv_norm_fwd: bad shape (D must be 64 or 128)");
+  if (B * S == 0) return ST_OK;
+  ST_CHECK_ARG(x && cos && sin && wq && wk && q && k && v && rstd,
+               "st_rope_qkv_norm_fwd: NULL pointer");
+  ST_CHECK_ARG(ldx >= (heads + 2 * kv_heads) * D && ldx % 8 == 0 && B * S <= 0x7fffffff,
+               "st_rope_qkv_norm_fwd: ldx must be >= (heads + 2*kv_heads)*D and a multiple of 8");
+  ST_CHECK_ARG(((((uintptr_t)x | (uintptr_t)cos | (uintptr_t)sin | (uintptr_t)wq |
+                  (uintptr_t)wk | (uintptr_t)q | (uintptr_t)k | (uintptr_t)v) & 15u) == 0),
+               "st_rope_qkv_norm_fwd: operands must be 16-byte aligned");
+  QkvHeads qh{};
+  qh.o[0] = q; qh.o[1] = k; qh.o[2] = v;
+  qh.h[0] = (int)heads; qh.h[1] = (int)kv_heads; qh.h[2] = (int)kv_heads;
+  if (D == 128)
+    rope_qkv_norm_fwd<128><<<(unsigned)(B * S), NTH, 0, (hipStream_t)stream>>>(
+        x, ldx, cos, sin, (int)S, qh, wq, wk, eps, rstd);
+  else
+    rope_qkv_norm_fwd<64><<<(unsigned)(B * S), NTH, 0, (hipStream_t)stream>>>(
+        x, ldx, cos, sin, (int)S, qh, wq, wk, eps, rstd);
+  return st::check_launch("rope_qkv_norm_fwd");
+}
+
+extern "C" int st_rope_qkv_norm_bwd(const uint16_t* dq, const uint16_t* dk, const uint16_t* dv,
+                                    const uint16_t* x, int64_t ldx, const uint16_t* cos,
+                                    const uint16_t* sin, const uint16_t* wq, const uint16_t* wk,
+                                    const float* rstd, int64_t B, int64_t S, int64_t heads,
+                                    int64_t kv_heads, int64_t D, uint16_t* dx, int64_t lddx,
+                                    st_stream_t stream) {
+  ST_CHECK_ARG(B >= 0 && S >= 0 && heads > 0 && kv_heads > 0 && (D == 64 || D == 128),
+               "st_rope_qkv_norm_bwd: bad shape (D must be 64 or 128)");
+  if (B * S == 0) return ST_OK;
+  ST_CHECK_ARG(dq && dk && dv && x && cos && sin && wq && wk && rstd && dx,
+               "st_rope_qkv_norm_bwd: NULL pointer");
+  const int64_t width = (heads + 2 * kv_heads) * D;
+  ST_CHECK_ARG(ldx >= width && lddx >= width && ldx % 8 == 0 && lddx % 8 == 0 &&
+                   B * S <= 0x7fffffff,
+               "st_rope_qkv_norm_bwd: row strides must be >= (heads + 2*kv_heads)*D, multiples of 8");
+  ST_CHECK_ARG(((((uintptr_t)dq | (uintptr_t)dk | (uintptr_t)dv | (uintptr_t)x |
+                  (uintptr_t)cos | (uintptr_t)sin | (uintptr_t)wq | (uintptr_t)wk |
+                  (uintptr_t)dx) & 15u) == 0),
+               "st_rope_qkv_norm_bwd: operands must be 16-byte aligned");
+  QkvHeads qh{};
+  qh.g[0] = dq; qh.g[1] = dk; qh.g[2] = dv;
+  qh.h[0] = (int)heads; qh.h[1] = (int)kv_heads; qh.h[2] = (int)kv_heads;
+  if (D == 128)
+    rope_qkv_norm_bwd<128><<<(unsigned)(B * S), NTH, 0, (hipStream_t)stream>>>(
+        x, ldx, cos, sin, (int)S, qh, wq, wk, rstd, dx, lddx);
+  else
+    rope_qkv_norm_bwd<64><<<(unsigned)(B * S), NTH, 0, (hipStream_t)stream>>>(
+        x, ldx, cos, sin, (int)S, qh, wq, wk, rstd, dx, lddx);
+  return st::check_launch("rope_qkv_norm_bwd");
 }
 
 extern "C" int st_heads_to_tokens(const uint16_t* x, int64_t B, int64_t S, int64_t heads,

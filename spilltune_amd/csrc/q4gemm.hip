@@ -102,7 +102,6 @@ struct Tile {
   static constexpr bool Q4 = (MODE == FWD_Q4 || MODE == DGRAD_Q4);
   static constexpr bool DGRAD = (MODE == DGRAD_Q4 || MODE == DGRAD_BF16);
   static constexpr int BF_IT = BN * 8 / NT;        // FWD_BF16 chunks per thread
-  static constexpr int QB = BN * BK / (NT * 8);    // DGRAD_BF16: contraction rows per thread block
   static constexpr int LDS_CHUNKS = 2 * (BM + BN) * RS;
 };
 
@@ -489,19 +488,18 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
   // B operand source.  FWD_Q4: thread owns EPT consecutive weights of one W row.
   constexpr int TPR = NT / BN;          // threads per W row (1, 2 or 4)
   constexpr int EPT = BK / TPR;         // elements per thread per k-step (64, 32 or 16)
-  // DGRAD_Q4: the B tile is W[n][k] for BK contraction rows n and BN output
-  // columns k, kept in that (natural) orientation; each thread dequantises
-  // DE consecutive k of one row n, and the MFMA operand is read transposed.
-  constexpr int DE = BN * BK / NT;      // DGRAD_Q4 elements per thread per k-step (32 or 16)
-  constexpr int DTR = BN / DE;          // DGRAD_Q4 threads per contraction row
+  // DGRAD_Q4 / DGRAD_BF16: the B tile is W[n][k] for BK contraction rows n
+  // and BN output columns k, kept in that (natural) orientation; each thread
+  // dequantises (or copies) DE consecutive k of one row n, and the MFMA
+  // operand is read transposed.
+  constexpr int DE = BN * BK / NT;      // dgrad elements per thread per k-step (32 or 16)
+  constexpr int DTR = BN / DE;          // dgrad threads per contraction row
   // packed 4-bit words (8 codes each) per thread per k-step
   constexpr int NW = MODE == FWD_Q4 ? EPT / 8 : MODE == DGRAD_Q4 ? DE / 8 : 1;
   static_assert(!TL::Q4 || NW == 2 || NW % 4 == 0, "packed W loads are 8 bytes or whole 16-byte pieces");
-  constexpr int WQ = TL::Q4 ? 1 : (TL::DGRAD ? TL::QB : TL::BF_IT);
-  constexpr int PB = BN / 8;
+  constexpr int WQ = TL::Q4 ? 1 : (TL::DGRAD ? DE / 8 : TL::BF_IT);
   const int brow = tid / TPR, bsub = tid % TPR;       // FWD_Q4 mapping
-  const int drow = tid / DTR, dsub = tid % DTR;       // DGRAD_Q4 mapping
-  const int pb = tid % PB, qb = tid / PB;             // DGRAD_BF16 mapping
+  const int drow = tid / DTR, dsub = tid % DTR;       // dgrad mapping
   // FWD_Q4 byte offsets at k = 0 of the thread's packed weights and of its
   // row's first scale (kOOB beyond P).  Unless FLAT, K (= ldw) is a multiple
   // of 128, so k-step kt adds kt*BK/2 payload bytes and scale group kt/2.
@@ -516,14 +514,14 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
     }
   }
   const bool dcol_ok = p0 + dsub * DE < p.P;
-  static_assert(MODE != DGRAD_Q4 || NT / DTR == BK, "DGRAD_Q4: one thread row per contraction row");
+  static_assert(!TL::DGRAD || NT / DTR == BK, "dgrad: one thread row per contraction row");
 
   static_assert(!FLAT || (TL::Q4 && BM == 128 && BN == 128), "FLAT: 4-bit 128x128 tiles only");
-  // DGRAD_Q4 with 128-wide B rows: each thread's 4 words are dequantised and
-  // stored in an order rotated by its group dsub, free of LDS bank conflicts
-  // with st::trswz<128> (every store instruction of a quarter-wave then
-  // writes each 4-chunk group's chunk (ch + group) & 3)
-  constexpr bool DROT = MODE == DGRAD_Q4 && BN == 128 && NW == 4 && DTR == 4;
+  // dgrad with 128-wide B rows: each thread's 4 chunks are dequantised (or
+  // copied) and stored in an order rotated by its group dsub, free of LDS
+  // bank conflicts with st::trswz<128> (every store instruction of a
+  // quarter-wave then writes each 4-chunk group's chunk (ch + group) & 3)
+  constexpr bool DROT = TL::DGRAD && BN == 128 && DE == 32 && DTR == 4;
   struct WRegs {
     uint4 q[WQ];      // bf16 modes
     uint32_t w[NW];   // 4-bit modes
@@ -578,15 +576,15 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
         st::rot4(w.w, dsub);
         if constexpr (FLAT) st::rot4(w.s, dsub);
       }
-    } else {
-      int64_t pc = p0 + pb * 8;
+    } else {  // DGRAD_BF16: DE consecutive columns of contraction row n
+      const int64_t n = (int64_t)kt * BK + drow;
+      const int64_t e = n * p.ldw + p0 + dsub * DE;
 #pragma unroll
-      for (int i = 0; i < TL::QB; ++i) {
-        int64_t q = (int64_t)kt * BK + qb * TL::QB + i;
-        bool ok = pc < p.P && q < p.Q;
-        int64_t e = q * p.ldw + pc;
-        w.q[i] = ld16(rsW, ok ? (uint32_t)(e * 2) : kOOB);
+      for (int i = 0; i < WQ; ++i) {
+        const bool ok = n < p.Q && p0 + dsub * DE + 8 * i < p.P;
+        w.q[i] = ld16(rsW, ok ? (uint32_t)((e + 8 * i) * 2) : kOOB);
       }
+      if constexpr (DROT) st::rot4(w.q, dsub);
     }
   };
 
@@ -619,27 +617,11 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
         int id = tid + i * NT;
         bs[pad(id >> 3, id & 7)] = w.q[i];
       }
-    } else {
-      // columns j = 2*part, 2*part+1 of the thread's QB x 8 block, written transposed
-#pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        const int j = 2 * part + jj;
-        float v[TL::QB];
-#pragma unroll
-        for (int i = 0; i < TL::QB; ++i) {
-          uint32_t word = (j >> 1) == 0 ? w.q[i].x : (j >> 1) == 1 ? w.q[i].y
-                          : (j >> 1) == 2 ? w.q[i].z : w.q[i].w;
-          v[i] = st::bf16_to_f32((uint16_t)(word >> (16 * (j & 1))));
-        }
-        const int prow = pb * 8 + j;
-        if constexpr (TL::QB == 8) {
-          bs[pad(prow, qb)] = make_uint4(st::pack_bf16x2(v[0], v[1]), st::pack_bf16x2(v[2], v[3]),
-                                         st::pack_bf16x2(v[4], v[5]), st::pack_bf16x2(v[6], v[7]));
-        } else {
-          ((uint2*)&bs[pad(prow, qb >> 1)])[qb & 1] =
-              make_uint2(st::pack_bf16x2(v[0], v[1]), st::pack_bf16x2(v[2], v[3]));
-        }
-      }
+    } else {  // DGRAD_BF16: chunk `part` of the thread's row, transposed-operand layout
+      const int ot = fresh_tid();
+      const int d = ot % DTR;
+      const int c = DROT ? d * 4 + ((part + d) & 3) : d * WQ + part;
+      if (part < WQ) bs[dswz(ot / DTR, c)] = w.q[part < WQ ? part : 0];
     }
   };
   auto prep_B = [&](const WRegs& w) {
@@ -664,7 +646,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
       a[i] = __builtin_bit_cast(bf16x8, as[pad(wm * WM + i * 32 + (ln & 31), c)]);
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
-      if constexpr (MODE == DGRAD_Q4)
+      if constexpr (TL::DGRAD)
         b[j] = b_tr(bs, s * 16, wn * WN + j * 32, ln);
       else
         b[j] = __builtin_bit_cast(bf16x8, bs[pad(wn * WN + j * 32 + (ln & 31), c)]);
@@ -1033,7 +1015,7 @@ __device__ __forceinline__ void rb_order() {
 }
 #undef RB_G
 template <int FN, int WAVES, bool HI, int FM = 8>
-__global__ __launch_bounds__(64 * WAVES, FM == 4 ? 2 : 1) void gemm_rb_kernel(GemmParams p) {
+__global__ __launch_bounds__(64 * WAVES, FM == 4 ? 4 : 1) void gemm_rb_kernel(GemmParams p) {
   constexpr int BM = 32 * FM, NT = 64 * WAVES, WN = 32 * FN, BN = WN * WAVES;
   constexpr int WM = BM;
   constexpr int A_ST = BM * BK / 8;       // 16-byte units per A stage

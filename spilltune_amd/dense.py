@@ -90,11 +90,12 @@ def dense_block(hidden_states, position_embeddings, attention_mask, *, heads, kv
     if qkv is not None and (all(l is None for l in loras_qkv) or all(l is not None for l in loras_qkv)):
         y = ops.q4_lora_linear(xn, qkv, loras_qkv)
         if qk_norm:
-            nq, nk = heads * head_dim, kv_heads * head_dim
-            y = torch.cat((head_norm(y[:, :nq], "self_attn.q_norm.weight"),
-                           head_norm(y[:, nq:nq + nk], "self_attn.k_norm.weight"),
-                           y[:, nq + nk:]), 1)
-        q, k, v = ops.rope_qkv(y, B, S, heads, kv_heads, head_dim, cos, sin)
+            # per-head q/k RMSNorm and the rotation in one kernel each way
+            q, k, v = ops.rope_qkv_norm(y, B, S, heads, kv_heads, head_dim, cos, sin,
+                                        weights["self_attn.q_norm.weight"],
+                                        weights["self_attn.k_norm.weight"], eps)
+        else:
+            q, k, v = ops.rope_qkv(y, B, S, heads, kv_heads, head_dim, cos, sin)
     else:
         q = ops.rope_heads(head_norm(ops.q4_lora_linear(xn, wq, [lora_q]), "self_attn.q_norm.weight"),
                            0, B, S, heads, head_dim, cos, sin)

@@ -596,6 +596,51 @@ def rope_qkv(y, B, S, heads, kv_heads, D, cos, sin):
     return _RopeQKV.apply(y, B, S, heads, kv_heads, D, cos.contiguous(), sin.contiguous())
 
 
+class _RopeQKVNorm(torch.autograd.Function):
+    """Qwen3 qk_norm + rotation of a fused q|k|v projection output in one
+    launch each way (dense.py:128-141): per-head RMSNorm of q and k, then the
+    rotation, v copied to head layout."""
+
+    @staticmethod
+    def forward(ctx, y, B, S, heads, kv_heads, D, cos, sin, wq, wk, eps):
+        ld = y.stride(0)
+        dev = y.device
+        st = _lib.stream_handle(dev)
+        q = torch.empty((B, heads, S, D), dtype=_BF16, device=dev)
+        k = torch.empty((B, kv_heads, S, D), dtype=_BF16, device=dev)
+        v = torch.empty((B, kv_heads, S, D), dtype=_BF16, device=dev)
+        rstd = torch.empty((B * S, heads + kv_heads), dtype=_F32, device=dev)
+        _lib.call("st_rope_qkv_norm_fwd", _lib.ptr(y), ld, _lib.ptr(cos), _lib.ptr(sin), B, S,
+                  heads, kv_heads, D, _lib.ptr(wq), _lib.ptr(wk), float(eps), _lib.ptr(q),
+                  _lib.ptr(k), _lib.ptr(v), _lib.ptr(rstd), st)
+        ctx.meta = (y.shape, ld, B, S, heads, kv_heads, D)
+        ctx.save_for_backward(y, cos, sin, wq, wk, rstd)
+        return q, k, v
+
+    @staticmethod
+    def backward(ctx, dq, dk, dv):
+        shape, ld, B, S, heads, kv_heads, D = ctx.meta
+        y, cos, sin, wq, wk, rstd = ctx.saved_tensors
+        dev = cos.device
+        st = _lib.stream_handle(dev)
+        dy = torch.empty(shape, dtype=_BF16, device=dev)
+        gs = [torch.zeros((B, h, S, D), dtype=_BF16, device=dev) if g is None else g.contiguous()
+              for g, h in ((dq, heads), (dk, kv_heads), (dv, kv_heads))]
+        _lib.call("st_rope_qkv_norm_bwd", *(_lib.ptr(g) for g in gs), _lib.ptr(y), ld,
+                  _lib.ptr(cos), _lib.ptr(sin), _lib.ptr(wq), _lib.ptr(wk), _lib.ptr(rstd), B, S,
+                  heads, kv_heads, D, _lib.ptr(dy), shape[1], st)
+        return dy, None, None, None, None, None, None, None, None, None, None
+
+
+def rope_qkv_norm(y, B, S, heads, kv_heads, D, cos, sin, wq, wk, eps):
+    """q, k, v head-major from a fused q|k|v output with Qwen3's per-head
+    q/k RMSNorm applied before the rotation (one kernel each way)."""
+    if y.dtype != _BF16 or wq.dtype != _BF16 or wk.dtype != _BF16:
+        raise ValueError("rope_qkv_norm expects bf16 inputs and norm weights")
+    return _RopeQKVNorm.apply(y, B, S, heads, kv_heads, D, cos.contiguous(), sin.contiguous(),
+                              wq.detach().contiguous(), wk.detach().contiguous(), eps)
+
+
 def rope_heads(y, col0, B, S, heads, D, cos, sin, rotate=True):
     return _RopeHeads.apply(y, col0, B, S, heads, D, cos.contiguous(), sin.contiguous(), rotate)
 

@@ -493,3 +493,41 @@ def test_rope_qkv_fused_matches_separate_calls(dev, D, pad):
     torch.cuda.synchronize()
     for a, b in zip(outs + [dbig], refs + [dref]):
         assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+@pytest.mark.parametrize("D,H,Hkv", [(128, 4, 2), (64, 6, 2), (128, 32, 8)])
+def test_rope_qkv_norm_matches_norm_then_rope(dev, D, H, Hkv):
+    """st_rope_qkv_norm_fwd/bwd (Qwen3's per-head q/k RMSNorm fused with the
+    rotation) against the separate ops it replaces: st_rmsnorm_fwd/bwd on the
+    head rows, then st_rope_qkv_fwd/bwd.  The rounding points are the same;
+    only the fp32 order of the per-head sums differs (the fused kernel sums a
+    head across 16 lanes), so outputs and gradients agree to one bf16 ulp."""
+    g = torch.Generator().manual_seed(D + H)
+    B, S = 2, 40
+    W = (H + 2 * Hkv) * D
+    y = (torch.randn(B * S, W, generator=g) * 3).to(BF).to(dev)
+    wq = (1 + 0.2 * torch.randn(D, generator=g)).to(BF).to(dev)
+    wk = (1 + 0.2 * torch.randn(D, generator=g)).to(BF).to(dev)
+    ang = torch.randn(B, S, D, generator=g)
+    cos, sin = ang.cos().to(BF).to(dev), ang.sin().to(BF).to(dev)
+    eps = 1e-6
+    yf = y.clone().requires_grad_(True)
+    q, k, v = ops.rope_qkv_norm(yf, B, S, H, Hkv, D, cos, sin, wq, wk, eps)
+    yr = y.clone().requires_grad_(True)
+    nq, nk = H * D, Hkv * D
+    qn = ops.rms_norm(yr[:, :nq].reshape(-1, D), wq, eps).reshape(B * S, -1)
+    kn = ops.rms_norm(yr[:, nq:nq + nk].reshape(-1, D), wk, eps).reshape(B * S, -1)
+    qr, kr, vr = ops.rope_qkv(torch.cat((qn, kn, yr[:, nq + nk:]), 1), B, S, H, Hkv, D, cos, sin)
+    grads = [torch.randn(t.shape, generator=g).to(BF).to(dev) for t in (q, k, v)]
+    torch.autograd.backward((q, k, v), grads)
+    torch.autograd.backward((qr, kr, vr), grads)
+    torch.cuda.synchronize()
+
+    def ulp_close(a, b, what):
+        a, b = a.float().cpu(), b.float().cpu()
+        err = (a - b).abs()
+        tol = b.abs().clamp_min(2 ** -20) * 2 ** -7 + 1e-30
+        assert bool((err <= tol).all()), f"{what}: beyond one bf16 ulp"
+        assert (err == 0).float().mean().item() > 0.97, f"{what}: too many 1-ulp differences"
+    for a, b, n in ((q, qr, "q"), (k, kr, "k"), (v, vr, "v"), (yf.grad, yr.grad, "dy")):
+        ulp_close(a, b, n)
+    assert torch.equal(v.view(torch.int16), vr.view(torch.int16))
