@@ -517,11 +517,12 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
   static_assert(!TL::DGRAD || NT / DTR == BK, "dgrad: one thread row per contraction row");
 
   static_assert(!FLAT || (TL::Q4 && BM == 128 && BN == 128), "FLAT: 4-bit 128x128 tiles only");
-  // dgrad with 128-wide B rows: each thread's 4 chunks are dequantised (or
-  // copied) and stored in an order rotated by its group dsub, free of LDS
-  // bank conflicts with st::trswz<128> (every store instruction of a
-  // quarter-wave then writes each 4-chunk group's chunk (ch + group) & 3)
-  constexpr bool DROT = TL::DGRAD && BN == 128 && DE == 32 && DTR == 4;
+  // DGRAD_Q4 with 128-wide B rows: each thread's 4 words are dequantised and
+  // stored in an order rotated by its group dsub, free of LDS bank conflicts
+  // with st::trswz<128> (every store instruction of a quarter-wave then
+  // writes each 4-chunk group's chunk (ch + group) & 3)
+  constexpr bool DROT = MODE == DGRAD_Q4 && BN == 128 && NW == 4 && DTR == 4;
+  static_assert(MODE != DGRAD_BF16 || WQ * (NT / (BN / 8)) == BK, "DGRAD_BF16: whole rows per thread block");
   struct WRegs {
     uint4 q[WQ];      // bf16 modes
     uint32_t w[NW];   // 4-bit modes
@@ -576,15 +577,16 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
         st::rot4(w.w, dsub);
         if constexpr (FLAT) st::rot4(w.s, dsub);
       }
-    } else {  // DGRAD_BF16: DE consecutive columns of contraction row n
-      const int64_t n = (int64_t)kt * BK + drow;
-      const int64_t e = n * p.ldw + p0 + dsub * DE;
+    } else {  // DGRAD_BF16: chunk (row, tid % CPR) for rows tid / CPR + i * NT / CPR
+      // (whole 16-byte-chunk rows per load instruction)
+      constexpr int CPR = BN / 8;
+      const int64_t col = p0 + (tid % CPR) * 8;
 #pragma unroll
       for (int i = 0; i < WQ; ++i) {
-        const bool ok = n < p.Q && p0 + dsub * DE + 8 * i < p.P;
-        w.q[i] = ld16(rsW, ok ? (uint32_t)((e + 8 * i) * 2) : kOOB);
+        const int64_t n = (int64_t)kt * BK + tid / CPR + i * (NT / CPR);
+        const bool ok = n < p.Q && col < p.P;
+        w.q[i] = ld16(rsW, ok ? (uint32_t)((n * p.ldw + col) * 2) : kOOB);
       }
-      if constexpr (DROT) st::rot4(w.q, dsub);
     }
   };
 
@@ -617,11 +619,11 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
         int id = tid + i * NT;
         bs[pad(id >> 3, id & 7)] = w.q[i];
       }
-    } else {  // DGRAD_BF16: chunk `part` of the thread's row, transposed-operand layout
+    } else {  // DGRAD_BF16: the loaded chunks as they lie, transposed-operand layout
+      constexpr int CPR = BN / 8;
       const int ot = fresh_tid();
-      const int d = ot % DTR;
-      const int c = DROT ? d * 4 + ((part + d) & 3) : d * WQ + part;
-      if (part < WQ) bs[dswz(ot / DTR, c)] = w.q[part < WQ ? part : 0];
+      if (part < WQ)
+        bs[dswz(ot / CPR + part * (NT / CPR), ot % CPR)] = w.q[part < WQ ? part : 0];
     }
   };
   auto prep_B = [&](const WRegs& w) {

@@ -531,3 +531,21 @@ def test_rope_qkv_norm_matches_norm_then_rope(dev, D, H, Hkv):
     for a, b, n in ((q, qr, "q"), (k, kr, "k"), (v, vr, "v"), (yf.grad, yr.grad, "dy")):
         ulp_close(a, b, n)
     assert torch.equal(v.view(torch.int16), vr.view(torch.int16))
+
+
+@pytest.mark.parametrize("M,N,K,ldw_pad", [(64, 256, 256, 0), (100, 384, 520, 8), (37, 1000, 136, 0),
+                                           (1024, 4096, 2048, 0)])
+def test_linear_bf16_fwd_and_dgrad_vs_fp32(dev, M, N, K, ldw_pad):
+    """The plain bf16 GEMMs (terminal head, MoE router): y = bf16(x W^T) and
+    dx = bf16(dy W) with fp32 accumulation against torch fp32 matmul, ragged
+    M/N/K and a padded W row stride."""
+    g = torch.Generator().manual_seed(M + N + K)
+    x = torch.randn(M, K, generator=g).to(BF)
+    dy = torch.randn(M, N, generator=g).to(BF)
+    wbig = (torch.randn(N, K + ldw_pad, generator=g) * 0.05).to(BF)
+    w = wbig[:, :K]
+    y = ops.linear_bf16(x.to(dev), wbig.to(dev)[:, :K])
+    dx = ops.linear_bf16_dgrad(dy.to(dev), wbig.to(dev)[:, :K])
+    torch.cuda.synchronize()
+    _close_bf16(y, (x.float() @ w.float().T).to(BF), f"bf16 fwd {M}x{N}x{K}")
+    _close_bf16(dx, (dy.float() @ w.float()).to(BF), f"bf16 dgrad {M}x{N}x{K}")
