@@ -169,8 +169,9 @@ int st_lora_gemm_noalloc(int64_t Mo, int64_t No, int64_t Kc,
  * dy [M, N] bf16 (lddy), b [N, r] fp32 (the segments' B stacked), t [M, nseg*r]
  * fp32 (ldt; the forward's x_f32 A_cat^T), dt [M, nseg*r] (lddt), db [N, r].
  * All 2*nseg products run in one launch, their split-K sums in one more (fixed
- * order).  nseg <= 4, r <= 64; segment starts and widths must be multiples of
+ * order).  nseg <= 8, r <= 64; segment starts and widths must be multiples of
  * 8 (the workspace query returns 0 otherwise: use st_lora_gemm per product).
+ * db == NULL runs the dt products only (db formed later, e.g. by st_rk_batch).
  */
 int64_t st_lora_bwd_dy_workspace_bytes(int64_t M, int64_t N, int32_t rank, int32_t nseg,
                                        const int64_t* seg_end);
@@ -179,6 +180,33 @@ int st_lora_bwd_dy(const uint16_t* dy, int64_t M, int64_t N, int64_t lddy,
                    int32_t nseg, const int64_t* seg_end, float scale,
                    float* dt, int64_t lddt, float* db,
                    void* workspace, int64_t workspace_bytes, st_stream_t stream);
+
+/*
+ * Independent rank-r products in one launch (+ one fixed-order reduction):
+ * the deferred adapter gradients of a layer's backward (dB_s = s*dY_s^T*T_s and
+ * dA_s = dT_s^T*x for every projection of the layer, training/recompute.py:
+ * 102-133 / finetune/lora.py:219), written straight into the adapters' gradient
+ * buffers (accumulate: add, as across microbatches of an accumulation window).
+ * Each product: out[m*so_m + j*so_j] (+)= alpha * sum_{k<Kc} g(m,k) * S[k*ssk + j*ssj]
+ * for m < big, j < r (r <= 64), with g(m,k) = G[m*ldg + k] (col = 0) or
+ * G[k*ldg + m] (col = 1), G bf16 with 16-byte aligned rows of multiples of 8.
+ * n <= 16 products per call.
+ */
+typedef struct st_rk_product {
+  const uint16_t* G;
+  int64_t ldg;
+  int32_t col;
+  const float* S;
+  int64_t ssk, ssj;
+  int64_t big, r, Kc;
+  float alpha;
+  float* out;
+  int64_t so_m, so_j;
+  int32_t accumulate;
+} st_rk_product;
+int64_t st_rk_batch_workspace_bytes(int32_t n, const st_rk_product* products);
+int st_rk_batch(int32_t n, const st_rk_product* products, void* workspace,
+                int64_t workspace_bytes, st_stream_t stream);
 
 /* ------------------------------------------------------- layer elementwise */
 /* y = w * bf16(x * rsqrt(mean(x^2) + eps)) (dense.py:115-117); rstd[row] saved. */

@@ -52,6 +52,8 @@ _SIGNATURES = {
     "st_rope_bwd": (_I32, [_P, _P, _P, _I64, _I64, _I64, _I64, _I32, _P, _I64, _P]),
     "st_rope_qkv_fwd": (_I32, [_P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P]),
     "st_rope_qkv_bwd": (_I32, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P]),
+    "st_rk_batch_workspace_bytes": (_I64, [_I32, _P]),
+    "st_rk_batch": (_I32, [_I32, _P, _P, _I64, _P]),
     "st_rope_qkv_norm_fwd": (_I32, [_P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _F,
                                     _P, _P, _P, _P, _P]),
     "st_rope_qkv_norm_bwd": (_I32, [_P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _I64, _I64,
@@ -151,6 +153,15 @@ def ptr(t: torch.Tensor | None):
 
 def stream_handle(device: torch.device | None = None):
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+class RkProduct(ctypes.Structure):
+    """``st_rk_product`` (include/spilltune_hip.h): one product of st_rk_batch."""
+    _fields_ = [("G", ctypes.c_void_p), ("ldg", ctypes.c_int64), ("col", ctypes.c_int32),
+                ("S", ctypes.c_void_p), ("ssk", ctypes.c_int64), ("ssj", ctypes.c_int64),
+                ("big", ctypes.c_int64), ("r", ctypes.c_int64), ("Kc", ctypes.c_int64),
+                ("alpha", ctypes.c_float), ("out", ctypes.c_void_p), ("so_m", ctypes.c_int64),
+                ("so_j", ctypes.c_int64), ("accumulate", ctypes.c_int32)]
 
 
 def lut_array(values) -> ctypes.Array:

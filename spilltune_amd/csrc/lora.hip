@@ -154,7 +154,7 @@ __global__ __launch_bounds__(NTH) void lora_rk(int64_t Mo, int64_t R, int64_t Kc
 // Each problem is a lora_rk product with its own operands, split count and
 // partial slice; workgroup b runs problem p when wg0[p] <= b < wg0[p+1], and
 // one reduction launch sums every problem's partials into its output.
-constexpr int RK_MAXP = 8;
+constexpr int RK_MAXP = 16;
 struct RkProblem {
   const uint16_t* G;
   const float* S;
@@ -162,12 +162,12 @@ struct RkProblem {
   float* out;    // out[m*so_m + j*so_j] (+)= alpha * sum
   int64_t ldg, g_bytes, ssk, ssj, s_bytes, big, R, Kc, klen, so_m, so_j;
   int64_t wg0, e0;  // first workgroup / first reduction element of the problem
-  int col, tiles, ks;
+  int col, tiles, ks, acc;
   float alpha;
 };
 struct RkBatch {
   RkProblem p[RK_MAXP];
-  int n, accumulate;
+  int n;
   int64_t wgs, elems;
 };
 
@@ -215,7 +215,7 @@ __global__ __launch_bounds__(NTH) void lora_rk_reduce_batch(const RkBatch b) {
   const int64_t m = le / q.R, j = le % q.R;
   float v = q.alpha * s;
   float* o = q.out + m * q.so_m + j * q.so_j;
-  if (b.accumulate) v += *o;
+  if (q.acc) v += *o;
   *o = v;
 }
 
@@ -448,14 +448,15 @@ namespace {
 int64_t plan_bwd_dy(RkBatch& b, bool fill, const uint16_t* dy, int64_t M, int64_t N,
                     int64_t lddy, const float* B, const float* T, int64_t ldt, int r, int nseg,
                     const int64_t* seg_end, float scale, float* dt, int64_t lddt, float* db,
-                    float* part) {
+                    float* part, bool with_db = true) {
   b = RkBatch{};
-  b.n = 2 * nseg;
+  const int per = with_db ? 2 : 1;
+  b.n = per * nseg;
   int64_t wgs = 0, elems = 0, floats = 0, start = 0;
   for (int s = 0; s < nseg; ++s) {
     const int64_t width = seg_end[s] - start;
-    for (int h = 0; h < 2; ++h) {
-      RkProblem& q = b.p[2 * s + h];
+    for (int h = 0; h < per; ++h) {
+      RkProblem& q = b.p[per * s + h];
       q.col = h;
       q.R = r;
       q.big = h ? width : M;
@@ -526,13 +527,14 @@ extern "C" int st_lora_bwd_dy(const uint16_t* dy, int64_t M, int64_t N, int64_t 
   ST_CHECK_ARG(rank >= 1 && rank <= 64, "st_lora_bwd_dy: rank must be 1..64");
   if (int rc = check_segments(N, nseg, seg_end)) return rc;
   if (M == 0) return ST_OK;
-  ST_CHECK_ARG(dy && b && t && dt && db, "st_lora_bwd_dy: NULL pointer");
+  ST_CHECK_ARG(dy && b && t && dt, "st_lora_bwd_dy: NULL pointer");
   ST_CHECK_ARG(lddy >= N && ldt >= (int64_t)nseg * rank && lddt >= (int64_t)nseg * rank,
                "st_lora_bwd_dy: leading dimension too small");
   ST_CHECK_ARG(((uintptr_t)dy & 15u) == 0, "st_lora_bwd_dy: dy must be 16-byte aligned");
   RkBatch bt;
+  // db == NULL: the dT products only (the caller forms dB elsewhere)
   const int64_t floats = plan_bwd_dy(bt, true, dy, M, N, lddy, b, t, ldt, rank, nseg, seg_end,
-                                     scale, dt, lddt, db, (float*)workspace);
+                                     scale, dt, lddt, db, (float*)workspace, db != nullptr);
   if (floats < 0)
     return st::fail(ST_EUNSUPPORTED,
                     "st_lora_bwd_dy: segments need 8-element-aligned starts and widths, "
@@ -549,5 +551,94 @@ extern "C" int st_lora_bwd_dy(const uint16_t* dy, int64_t M, int64_t N, int64_t 
   int rc = st::check_launch("lora_rk_batch");
   if (rc) return rc;
   lora_rk_reduce_batch<<<(unsigned)st::cdiv(bt.elems, NTH), NTH, 0, s>>>(bt);
+  return st::check_launch("lora_rk_reduce_batch");
+}
+
+// ------------------------------------------------ batched independent products
+namespace {
+
+// One st_rk_product as a streaming-kernel problem; false when its operands
+// break the kernel's layout rules (16-byte G rows, 32-bit offsets, r <= 64).
+bool rk_problem(const st_rk_product& x, RkProblem& q) {
+  q = RkProblem{};
+  if (x.big <= 0 || x.r <= 0 || x.r > 64 || x.Kc <= 0 || !x.G || !x.S || !x.out) return false;
+  q.G = x.G;
+  q.S = x.S;
+  q.out = x.out;
+  q.col = x.col ? 1 : 0;
+  q.ldg = x.ldg;
+  q.ssk = x.ssk;
+  q.ssj = x.ssj;
+  q.big = x.big;
+  q.R = x.r;
+  q.Kc = x.Kc;
+  q.so_m = x.so_m;
+  q.so_j = x.so_j;
+  q.alpha = x.alpha;
+  q.acc = x.accumulate ? 1 : 0;
+  q.g_bytes = q.col ? ((x.Kc - 1) * x.ldg + x.big) * 2 : ((x.big - 1) * x.ldg + x.Kc) * 2;
+  q.s_bytes = ((x.Kc - 1) * x.ssk + (x.r - 1) * x.ssj + 1) * 4;
+  q.tiles = (int)st::cdiv(x.big, RK_BM);
+  q.ks = rk_ksplit(x.big, x.Kc);
+  q.klen = st::cdiv(st::cdiv(x.Kc, q.ks), RK_BK) * RK_BK;
+  return ((uintptr_t)x.G & 15u) == 0 && x.ldg % 8 == 0 && (q.col ? x.big : x.Kc) % 8 == 0 &&
+         x.ssk >= 0 && x.ssj >= 0 && q.g_bytes < (1ll << 31) && q.s_bytes < (1ll << 31);
+}
+
+// plans a batch; returns the partial floats needed, or -1 for a bad problem
+int64_t plan_batch(RkBatch& b, int32_t n, const st_rk_product* p, float* part) {
+  b = RkBatch{};
+  b.n = n;
+  int64_t wgs = 0, elems = 0, floats = 0;
+  for (int i = 0; i < n; ++i) {
+    RkProblem& q = b.p[i];
+    if (!rk_problem(p[i], q)) return -1;
+    q.wg0 = wgs;
+    q.e0 = elems;
+    q.part = part ? part + floats : nullptr;
+    wgs += (int64_t)q.tiles * q.ks;
+    elems += q.big * q.R;
+    floats += (int64_t)q.ks * q.big * q.R;
+  }
+  b.wgs = wgs;
+  b.elems = elems;
+  return floats;
+}
+
+}  // namespace
+
+extern "C" int64_t st_rk_batch_workspace_bytes(int32_t n, const st_rk_product* products) {
+  if (n <= 0 || n > RK_MAXP || !products) return 0;
+  RkBatch b;
+  const int64_t floats = plan_batch(b, n, products, nullptr);
+  return floats < 0 ? 0 : floats * 4;
+}
+
+extern "C" int st_rk_batch(int32_t n, const st_rk_product* products, void* workspace,
+                           int64_t workspace_bytes, st_stream_t stream) {
+  ST_CHECK_ARG(n >= 0 && n <= RK_MAXP, "st_rk_batch: 0..%d products per call", RK_MAXP);
+  if (n == 0) return ST_OK;
+  ST_CHECK_ARG(products != nullptr, "st_rk_batch: NULL product list");
+  RkBatch b;
+  const int64_t floats = plan_batch(b, n, products, (float*)workspace);
+  if (floats < 0)
+    return st::fail(ST_EUNSUPPORTED,
+                    "st_rk_batch: a product breaks the streaming kernel's rules (16-byte "
+                    "aligned bf16 rows of multiples of 8, r <= 64, operands below 2 GiB)");
+  if (!workspace || workspace_bytes < floats * 4)
+    return st::fail(ST_EWORKSPACE, "st_rk_batch: needs %lld workspace bytes",
+                    (long long)(floats * 4));
+  ST_CHECK_ARG(b.wgs <= 0x7fffffff && b.elems <= 0x7fffffffll * NTH,
+               "st_rk_batch: too many workgroups");
+  bool wide = false;
+  for (int i = 0; i < n; ++i) wide = wide || b.p[i].R > 32;
+  hipStream_t s = (hipStream_t)stream;
+  if (wide)
+    lora_rk_batch<2><<<(unsigned)b.wgs, NTH, 0, s>>>(b);
+  else
+    lora_rk_batch<1><<<(unsigned)b.wgs, NTH, 0, s>>>(b);
+  int rc = st::check_launch("lora_rk_batch");
+  if (rc) return rc;
+  lora_rk_reduce_batch<<<(unsigned)st::cdiv(b.elems, NTH), NTH, 0, s>>>(b);
   return st::check_launch("lora_rk_reduce_batch");
 }

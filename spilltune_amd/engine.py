@@ -31,7 +31,8 @@ import torch.nn.functional as F
 
 from . import ops, slots
 from .dense import positions_and_masks
-from .recompute import _borrow_weights, _call_functional_block, streaming_block
+from .recompute import (_borrow_weights, _call_functional_block, block_adapter_backward,
+                        streaming_block)
 
 
 def flatten(model) -> dict:
@@ -126,20 +127,8 @@ def window_layer_major(model, session, items, *, normalization, token_chunk):
                 with torch.enable_grad():
                     out = _call_functional_block(block.functional, hidden, mb["pos"],
                                                  mb["masks"][block.kind], weights, block.kwargs)
-                grads = torch.autograd.grad(out, [hidden] + [t for p in ordered for t in (p.A, p.B)],
-                                            mb["g"])
-                dst = [t for p in ordered for t in (p.grad_A, p.grad_B)]
-                src = [g.detach().to(d) for g, d in zip(grads[1:], dst)]
                 # the first microbatch replaces (zero + add), later ones accumulate
-                if k == 0:
-                    for p in ordered:
-                        for t in (p.A.grad, p.B.grad):
-                            if t is not None:
-                                t.zero_()
-                    torch._foreach_copy_(dst, src)
-                else:
-                    torch._foreach_add_(dst, src)
-                mb["g"] = grads[0]
+                mb["g"] = block_adapter_backward(out, hidden, ordered, mb["g"], k > 0, block.index)
     return losses
 
 

@@ -21,6 +21,7 @@ to another implementation.
 from __future__ import annotations
 
 import math
+from contextlib import contextmanager
 
 from dataclasses import dataclass, field
 
@@ -183,6 +184,75 @@ def lora_gemm(Mo, No, Kc, a, sam, sak, b, sbk, sbn, alpha, out, accumulate=False
               _lib.ptr(ws), 0 if ws is None else ws.numel(), _lib.stream_handle(out.device))
 
 
+# ------------------------------------------------------- deferred adapter grads
+class LoraGradSink:
+    """Collects the adapter-gradient products of one layer's backward while
+    autograd runs -- dB_s = s*dY_s^T*T_s and dA_s = dT_s^T*x of every
+    projection -- and launches them together (``st_rk_batch``, 16 products per
+    call) straight into each adapter's ``grad_A`` / ``grad_B``: added when
+    ``accumulate`` (later microbatches of an accumulation window), written
+    otherwise.  Only dT, which the input-gradient GEMM needs, runs inside
+    autograd.  Each product keeps its split count and summation order, so the
+    gradients equal the immediate path's bit for bit."""
+
+    def __init__(self, device, accumulate: bool):
+        self.device = torch.device(device)
+        self.accumulate = bool(accumulate)
+        self.products, self.keep = [], []
+        self.written = set()
+
+    def wants(self, lora) -> bool:
+        ga, gb = getattr(lora, "grad_A", None), getattr(lora, "grad_B", None)
+        return all(isinstance(g, torch.Tensor) and g.dtype == _F32 and g.is_contiguous()
+                   and g.device == self.device and tuple(g.shape) == tuple(t.shape)
+                   for g, t in ((ga, lora.A), (gb, lora.B)))
+
+    def add(self, lora, products, keep):
+        self.products += products
+        self.keep += keep
+        self.written.add(id(lora))
+
+    def flush(self):
+        if not self.products:
+            return
+        st = _lib.stream_handle(self.device)
+        for i in range(0, len(self.products), 16):
+            chunk = self.products[i:i + 16]
+            arr = (_lib.RkProduct * len(chunk))(*chunk)
+            need = _lib.query("st_rk_batch_workspace_bytes", len(chunk), arr)
+            ws = _ws.get(self.device, need)
+            _lib.call("st_rk_batch", len(chunk), arr, _lib.ptr(ws),
+                      0 if ws is None else ws.numel(), st)
+        self.products, self.keep = [], []
+
+
+_SINKS: dict = {}
+
+
+@contextmanager
+def lora_grad_sink(device, accumulate: bool = False):
+    """Route the adapter gradients of q4_lora_linear backwards on ``device``
+    into a :class:`LoraGradSink` (call its ``flush()`` before reading them)."""
+    key = torch.device(device).index
+    prev = _SINKS.get(key)
+    sink = LoraGradSink(device, accumulate)
+    _SINKS[key] = sink
+    try:
+        yield sink
+    finally:
+        if prev is None:
+            _SINKS.pop(key, None)
+        else:
+            _SINKS[key] = prev
+
+
+def _rk(G, ldg, S, ssk, big, r, Kc, alpha, out, so_m, so_j, accumulate):
+    """One column-form st_rk_product (contraction over G's rows)."""
+    return _lib.RkProduct(G=G.data_ptr(), ldg=ldg, col=1, S=S.data_ptr(), ssk=ssk, ssj=1, big=big,
+                          r=r, Kc=Kc, alpha=float(alpha), out=out.data_ptr(), so_m=so_m,
+                          so_j=so_j, accumulate=int(accumulate))
+
+
 # ----------------------------------------------------------------- projection
 def _lora_meta(weight: Q4Weight, loras):
     loras = list(loras) if loras is not None else []
@@ -218,7 +288,7 @@ def _stack_rows(ts):
 
 class _Q4LoRALinear(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, weight, residual, rank, scale, swiglu_I, *ab):
+    def forward(ctx, x, weight, residual, rank, scale, swiglu_I, loras, *ab):
         gu = None
         if swiglu_I:  # x is a fused gate|up pre-activation: the input is silu(gate) * up
             gu = x
@@ -250,6 +320,7 @@ class _Q4LoRALinear(torch.autograd.Function):
             _lib.ptr(residual), 0 if residual is None else residual.stride(0),
             _lib.ptr(y), N, None, 0, stream))
         ctx.weight, ctx.rank, ctx.scale = weight, rank, scale
+        ctx.loras = loras
         ctx.has_residual = residual is not None
         ctx.nlora = len(ab)
         ctx.swiglu_I = swiglu_I
@@ -270,10 +341,47 @@ class _Q4LoRALinear(torch.autograd.Function):
         grads_ab = []
         dT = None
         A_cat = None
+        sink = _SINKS.get(dev.index) if ctx.nlora else None
         if ctx.nlora:
             x, T, A_cat, B_cat, gu = ctx.saved_tensors
             nseg = len(weight.segments)
             dT = torch.empty((M, nseg * rank), dtype=_F32, device=dev)
+            starts = [0]
+            for width in weight.segments:
+                starts.append(starts[-1] + width)
+            if sink is not None and not (
+                    ctx.loras is not None and all(sink.wants(l) for l in ctx.loras)
+                    and all(st % 8 == 0 for st in starts) and N % 8 == 0 and K % 8 == 0
+                    and dy.data_ptr() % 16 == 0 and x.data_ptr() % 16 == 0):
+                sink = None
+        if ctx.nlora and sink is not None:
+            # dT now (the dgrad epilogue reads it); dB_s and dA_s go to the sink
+            ends = _lib.i64_array(starts[1:])
+            need = _lib.query("st_lora_bwd_dy_workspace_bytes", M, N, rank, nseg, ends)
+            if need > 0:
+                ws = _ws.get(dev, need)
+                _lib.call("st_lora_bwd_dy", _lib.ptr(dy), M, N, N, _lib.ptr(B_cat), _lib.ptr(T),
+                          T.stride(0), rank, nseg, ends, float(scale), _lib.ptr(dT), dT.stride(0),
+                          None, _lib.ptr(ws), ws.numel(), stream)
+            else:
+                for s_ in range(nseg):
+                    off, width = starts[s_], weight.segments[s_]
+                    lora_gemm(M, rank, width, dy[:, off:off + width], N, 1,
+                              B_cat[off:off + width], rank, 1, scale,
+                              dT[:, s_ * rank:(s_ + 1) * rank])
+            acc = sink.accumulate
+            for s_, lo in enumerate(ctx.loras):
+                off, width = starts[s_], weight.segments[s_]
+                Ts, dTs = T[:, s_ * rank:], dT[:, s_ * rank:]
+                sink.add(lo, [
+                    # dB_s[n, j] = s * sum_m dY[m, off + n] T[m, s*r + j]
+                    _rk(dy[:, off:], N, Ts, T.stride(0), width, rank, M, scale, lo.grad_B,
+                        rank, 1, acc),
+                    # dA_s[j, k] = sum_m dT[m, s*r + j] x[m, k]
+                    _rk(x, K, dTs, dT.stride(0), K, rank, M, 1.0, lo.grad_A, 1, K, acc),
+                ], (dy, T, dT, x))
+            grads_ab = [None, None] * nseg
+        elif ctx.nlora:
             dB_all = torch.empty((N, rank), dtype=_F32, device=dev)
             # dT_s = s * dY_s B_s and dB_s = s * dY_s^T T_s for every segment:
             # one launch of partial products and one reduction
@@ -322,7 +430,7 @@ class _Q4LoRALinear(torch.autograd.Function):
                 _lib.ptr(weight.scales), K, weight.lut(), weight.flags, *lora_args,
                 _lib.ptr(dx), K, None, 0, stream))
         dres = dy if ctx.has_residual else None
-        return (dx, None, dres, None, None, None, *grads_ab)
+        return (dx, None, dres, None, None, None, None, *grads_ab)
 
 
 def q4_lora_linear(x: torch.Tensor, weight: Q4Weight, loras=None, residual=None,
@@ -348,13 +456,13 @@ def q4_lora_linear(x: torch.Tensor, weight: Q4Weight, loras=None, residual=None,
         if residual.shape != (x.shape[0], weight.out_features) or residual.dtype != _BF16:
             raise ValueError("residual must be a bf16 [M, out_features] tensor")
     if meta is None:
-        return _Q4LoRALinear.apply(x, weight, residual, 0, 1.0, swiglu_I)
+        return _Q4LoRALinear.apply(x, weight, residual, 0, 1.0, swiglu_I, None)
     rank, scale = meta
     ab = [t for l in loras for t in (l.A, l.B)]
     for l in loras:
         if l.A.dtype != _F32 or l.B.dtype != _F32:
             raise ValueError("LoRA A/B must be fp32")
-    return _Q4LoRALinear.apply(x, weight, residual, rank, scale, swiglu_I, *ab)
+    return _Q4LoRALinear.apply(x, weight, residual, rank, scale, swiglu_I, tuple(loras), *ab)
 
 
 # ----------------------------------------------------------------- RMSNorm

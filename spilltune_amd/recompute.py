@@ -16,6 +16,8 @@ from typing import Callable, Optional
 
 import torch
 
+from . import ops
+
 
 class StreamingBlockFunction(torch.autograd.Function):
     @staticmethod
@@ -39,34 +41,53 @@ class StreamingBlockFunction(torch.autograd.Function):
     def backward(ctx, grad_output):
         hidden = ctx.saved_tensors[0].detach().requires_grad_(True)
         ordered = sorted(ctx.lora_dict.values(), key=lambda p: p.name)
-        inputs = [hidden] + [t for p in ordered for t in (p.A, p.B)]
         with _borrow_weights(ctx.weight_reloader, "backward") as weights:
             with torch.enable_grad():
                 output = _call_functional_block(ctx.func_block, hidden, ctx.position_embeddings,
                                                 ctx.attention_mask, weights, ctx.func_kwargs)
-            grads = torch.autograd.grad(output, inputs, grad_output, allow_unused=True)
-            if grads[0] is None:
-                raise RuntimeError(f"block {ctx.block_idx} lost its input gradient")
-            dst, src = [], []
-            for i, proj in enumerate(ordered):
-                ga, gb = grads[1 + 2 * i], grads[2 + 2 * i]
-                if ga is None or gb is None:
-                    missing = [n for n, g in (("A", ga), ("B", gb)) if g is None]
-                    raise RuntimeError(f"block {ctx.block_idx} adapter {proj.name} is disconnected; "
-                                       f"missing gradients for {missing}")
-                if not ctx.accumulate_adapter_grads:
-                    for t in (proj.A.grad, proj.B.grad):
-                        if t is not None:
-                            t.zero_()
-                dst += [proj.grad_A, proj.grad_B]
-                src += [ga.detach().to(proj.grad_A), gb.detach().to(proj.grad_B)]
-            # one multi-tensor launch for every adapter: replace (zero + add in
-            # the reference) or accumulate
-            if ctx.accumulate_adapter_grads:
-                torch._foreach_add_(dst, src)
-            else:
-                torch._foreach_copy_(dst, src)
-        return (grads[0],) + (None,) * 8
+            dx = block_adapter_backward(output, hidden, ordered, grad_output,
+                                        ctx.accumulate_adapter_grads, ctx.block_idx)
+        return (dx,) + (None,) * 8
+
+
+def block_adapter_backward(output, hidden, ordered, grad_output, accumulate, block_idx):
+    """Backward of one recomputed block: returns d hidden and replaces (or,
+    with ``accumulate``, adds to) every projection's ``grad_A``/``grad_B``
+    (training/recompute.py:102-133).
+
+    The q4 projections hand their adapter products to a gradient sink that
+    writes the buffers directly after autograd returns (one batched launch per
+    16 products); the gradients autograd still returns (adapters outside those
+    projections) go through one multi-tensor copy or add."""
+    inputs = [hidden] + [t for p in ordered for t in (p.A, p.B)]
+    with ops.lora_grad_sink(hidden.device, accumulate) as sink:
+        grads = torch.autograd.grad(output, inputs, grad_output, allow_unused=True)
+        sink.flush()
+    if grads[0] is None:
+        raise RuntimeError(f"block {block_idx} lost its input gradient")
+    dst, src = [], []
+    for i, proj in enumerate(ordered):
+        if not accumulate:
+            for t in (proj.A.grad, proj.B.grad):
+                if t is not None:
+                    t.zero_()
+        if id(proj) in sink.written:
+            continue
+        ga, gb = grads[1 + 2 * i], grads[2 + 2 * i]
+        if ga is None or gb is None:
+            missing = [n for n, g in (("A", ga), ("B", gb)) if g is None]
+            raise RuntimeError(f"block {block_idx} adapter {proj.name} is disconnected; "
+                               f"missing gradients for {missing}")
+        dst += [proj.grad_A, proj.grad_B]
+        src += [ga.detach().to(proj.grad_A), gb.detach().to(proj.grad_B)]
+    # one multi-tensor launch for the rest: replace (zero + add in the
+    # reference) or accumulate
+    if dst:
+        if accumulate:
+            torch._foreach_add_(dst, src)
+        else:
+            torch._foreach_copy_(dst, src)
+    return grads[0]
 
 
 @contextmanager

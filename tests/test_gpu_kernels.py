@@ -264,6 +264,52 @@ def test_fused_segments_match_separate_projections(dev, oracle_codec):
     assert torch.equal(y.view(torch.int16), sep.view(torch.int16))
 
 
+@pytest.mark.parametrize("widths,r", [((256, 128, 128), 8), ((256, 128, 128), 16), ((384,), 64)])
+def test_lora_grad_sink_matches_autograd_grads(dev, oracle_codec, widths, r):
+    """Adapter gradients deferred to the sink (written into grad_A/grad_B by
+    st_rk_batch after autograd) equal the ones the projection's backward
+    returns, for a fused q|k|v of three segments: replace, then accumulate
+    onto what the buffers hold (the second microbatch of a window)."""
+    g = torch.Generator().manual_seed(5)
+    M, K = 320, 512
+    ws = [(torch.randn(n, K, generator=g) * 0.02).numpy() for n in widths]
+    qs = [q4_from_oracle(oracle_codec, w, "nf4-g128", dev)[0] for w in ws]
+    payload, scales = torch.cat([q.payload for q in qs]), torch.cat([q.scales for q in qs])
+    parts, po, so = [], 0, 0
+    for q, n in zip(qs, widths):
+        parts.append(ops.Q4Weight(payload[po:po + q.payload.numel()],
+                                  scales[so:so + q.scales.numel()], (n, K), "nf4-g128"))
+        po, so = po + q.payload.numel(), so + q.scales.numel()
+    fused = ops.concat_rows(parts) if len(parts) > 1 else parts[0]
+    loras = []
+    for n in widths:
+        lo = _L((torch.randn(r, K, generator=g) * 0.05).to(dev).requires_grad_(True),
+                (torch.randn(n, r, generator=g) * 0.05).to(dev).requires_grad_(True), 16.0)
+        lo.grad_A, lo.grad_B = torch.zeros_like(lo.A), torch.zeros_like(lo.B)
+        loras.append(lo)
+    x = torch.randn(M, K, generator=g).to(BF).to(dev).requires_grad_(True)
+    dy = torch.randn(M, sum(widths), generator=g).to(BF).to(dev)
+    ab = [t for lo in loras for t in (lo.A, lo.B)]
+    ref = torch.autograd.grad(ops.q4_lora_linear(x, fused, loras), [x] + ab, dy)
+    prior = [torch.randn(t.shape, generator=g).to(dev) for t in ab]
+    for accumulate in (False, True):
+        for lo, (pa, pb) in zip(loras, zip(prior[::2], prior[1::2])):
+            lo.grad_A.copy_(pa)
+            lo.grad_B.copy_(pb)
+        with ops.lora_grad_sink(dev, accumulate) as sink:
+            got = torch.autograd.grad(ops.q4_lora_linear(x, fused, loras), [x] + ab, dy,
+                                      allow_unused=True)
+            sink.flush()
+        torch.cuda.synchronize()
+        assert all(t is None for t in got[1:]) and len(sink.written) == len(loras)
+        assert torch.equal(got[0].view(torch.int16), ref[0].view(torch.int16))
+        for i, lo in enumerate(loras):
+            for buf, want, base in ((lo.grad_A, ref[1 + 2 * i], prior[2 * i]),
+                                    (lo.grad_B, ref[2 + 2 * i], prior[2 * i + 1])):
+                exp = (base + want) if accumulate else want
+                torch.testing.assert_close(buf, exp, rtol=1e-5, atol=1e-6 * exp.abs().max().item())
+
+
 def test_lora_gemm_strided_vs_float64(dev):
     g = torch.Generator().manual_seed(4)
     for Mo, No, Kc in [(2048, 16, 4096), (16, 4096, 2048), (4096, 16, 2048), (5, 7, 3), (70, 33, 1000)]:
