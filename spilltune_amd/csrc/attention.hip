@@ -641,13 +641,21 @@ __global__ __launch_bounds__(NTH * G, G == 1 && BKT == 64 && DQ <= 128 ? 2 : 1) 
   }
 }
 
-// dK, dV of one query head over a 128-key tile (8 waves: 4 key quarters x 2
-// query halves), looping over 64-query tiles from the diagonal down:
-// S = Q K^T, P = exp2(S - lse), dP = dO V^T, dS = P (dP - Delta),
-// dV^T += dO^T P, dK^T += Q^T dS.  Writes fp32 per-query-head partials.
+// dK, dV of one query head over a 128-key tile, looping over 64-query tiles
+// from the diagonal down: S = Q K^T, P = exp2(S - lse), dP = dO V^T,
+// dS = P (dP - Delta), dV^T += dO^T P, dK^T += Q^T dS.  Writes fp32
+// per-query-head partials.  DQ <= 128: 8 waves (4 key quarters x 2 query
+// halves, two waves per SIMD; the halves' sums meet in LDS at the end).
+// DQ = 192: 4 waves, one per key quarter, each taking both query halves in
+// turn: one wave per SIMD has the whole register file for its 160 columns of
+// dK and dV accumulators (two waves per SIMD spilled 70 registers).
 // NBUF Q|dO buffers: 2 overlaps the next tile's copy with this one's MFMAs;
 // 1 when two do not fit in LDS next to the resident K and V (DQ = 192).
-constexpr int KT2 = 128, QT2 = 64, NTH2 = 512;
+constexpr int KT2 = 128, QT2 = 64;
+template <int DQ>
+constexpr int dkdv_waves() {
+  return DQ <= 128 ? 8 : 4;
+}
 
 template <int DQ, int DV>
 constexpr int dkdv_nbuf() {
@@ -668,11 +676,12 @@ __device__ __forceinline__ void fa_bwd_dkdv_tile(
   constexpr int NBUF = dkdv_nbuf<DQ, DV>();
   constexpr int DSQ = DQ / 16, DSV = DV / 16, DBQ = DQ / 32, DBV = DV / 32;
   constexpr int LK = KT2 * DQ, LV = KT2 * DV, LQ = QT2 * DQ, LG = QT2 * DV;
+  constexpr int NW = dkdv_waves<DQ>(), NTH2 = 64 * NW, QH = 8 / NW;  // query halves per wave
   constexpr int PERQ = LQ / 8 / NTH2, PERG = LG / 8 / NTH2;  // 16-byte chunks per thread
   static_assert(PERQ * NTH2 * 8 == LQ && PERG * NTH2 * 8 == LG, "tiles are whole thread copies");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, c = lane & 31;
-  const int kq = wave & 3, qh = wave >> 2;
+  const int kq = wave & 3, qh0 = NW == 8 ? wave >> 2 : 0;
   const int hk = h / (H / Hkv);
   const int64_t ldt = (int64_t)H * DV;
   const uint16_t* qb = q + ((int64_t)(b * H + h) * S) * DQ;
@@ -760,6 +769,9 @@ __device__ __forceinline__ void fa_bwd_dkdv_tile(
     }
     const uint16_t* qs = lds + LK + LV + buf * (LQ + LG);
     const uint16_t* gs = qs + LQ;
+#pragma unroll
+    for (int hq = 0; hq < QH; ++hq) {
+    const int qh = NW == 8 ? qh0 : hq;
     const int qw0 = qt * QT2 + qh * 32;   // this wave's queries
     if (qw0 + 31 >= kw0 && qw0 < S) {     // some query sees some key
       f32x16 sacc, pacc;
@@ -806,17 +818,20 @@ __device__ __forceinline__ void fa_bwd_dkdv_tile(
               tile_tr<DQ>(qs, qh * 32 + 16 * hh, db * 32, lane), dsf[hh], dkacc[db], 0, 0, 0);
         }
     }
+    }
     if (NBUF == 2 && qt + 1 < qt_end) stats(buf ^ 1);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
-  // the two query halves of each key quarter: qh = 1 parks its sums in LDS,
-  // qh = 0 adds them and writes [key][d] fp32 partials; dV first, then dK
-  // (4 quarters x DB*16*64 floats at a time)
+  // 8 waves: the two query halves of each key quarter: qh = 1 parks its sums
+  // in LDS, qh = 0 adds them and writes [key][d] fp32 partials; dV first,
+  // then dK (4 quarters x DB*16*64 floats at a time).  4 waves: each writes
+  // its own sums.
+  const int qh = qh0;
   float* red = (float*)lds;
   constexpr int PARTV = DBV * 16 * 64, PARTK = DBQ * 16 * 64;
   static_assert(4 * PARTK * 4 <= dkdv_lds_elems<DQ, DV>() * 2, "dK partials fit in LDS");
-  if (qh == 1) {
+  if (NW == 8 && qh == 1) {
 #pragma unroll
     for (int db = 0; db < DBV; ++db)
 #pragma unroll
@@ -834,13 +849,14 @@ __device__ __forceinline__ void fa_bwd_dkdv_tile(
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int vv = 4 * v4 + e;
-          pa[e] = dvacc[db][vv] + red[kq * PARTV + (db * 16 + vv) * 64 + lane];
+          pa[e] = NW == 8 ? dvacc[db][vv] + red[kq * PARTV + (db * 16 + vv) * 64 + lane]
+                          : dvacc[db][vv];
         }
         *(float4*)(dvp + db * 32 + v4 * 8 + g * 4) = a;
       }
   }
   __syncthreads();
-  if (qh == 1) {
+  if (NW == 8 && qh == 1) {
 #pragma unroll
     for (int db = 0; db < DBQ; ++db)
 #pragma unroll
@@ -858,7 +874,8 @@ __device__ __forceinline__ void fa_bwd_dkdv_tile(
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int vv = 4 * v4 + e;
-          pb[e] = (dkacc[db][vv] + red[kq * PARTK + (db * 16 + vv) * 64 + lane]) * scale;
+          pb[e] = (NW == 8 ? dkacc[db][vv] + red[kq * PARTK + (db * 16 + vv) * 64 + lane]
+                           : dkacc[db][vv]) * scale;
         }
         *(float4*)(dkp + db * 32 + v4 * 8 + g * 4) = bq;
       }
@@ -868,7 +885,7 @@ __device__ __forceinline__ void fa_bwd_dkdv_tile(
 // key tiles kt and n-1-kt in one workgroup: the causal query range of the two
 // sums to a constant, so every workgroup does the same work
 template <int DQ, int DV>
-__global__ __launch_bounds__(NTH2, DQ <= 128 ? 2 : 1) void fa_bwd_dkdv(
+__global__ __launch_bounds__(64 * dkdv_waves<DQ>(), DQ <= 128 ? 2 : 1) void fa_bwd_dkdv(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, int S, int H, int Hkv,
@@ -978,7 +995,7 @@ int attn_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint
                                                 (int)Hkv, sl2, scale, delta, dq, nq, paired);
   int rc = st::check_launch("fa_bwd_dq");
   if (rc) return rc;
-  fa_bwd_dkdv<DQ, DV><<<g2, NTH2, 0, s>>>(q, k, v, dout, lse, delta, (int)S, (int)H, (int)Hkv,
+  fa_bwd_dkdv<DQ, DV><<<g2, 64 * dkdv_waves<DQ>(), 0, s>>>(q, k, v, dout, lse, delta, (int)S, (int)H, (int)Hkv,
                                           sl2, scale, dk_part, dv_part, nk, paired_k);
   rc = st::check_launch("fa_bwd_dkdv");
   if (rc) return rc;
