@@ -645,25 +645,23 @@ __global__ __launch_bounds__(NTH * G, G == 1 && BKT == 64 && DQ <= 128 ? 2 : 1) 
 // from the diagonal down: S = Q K^T, P = exp2(S - lse), dP = dO V^T,
 // dS = P (dP - Delta), dV^T += dO^T P, dK^T += Q^T dS.  Writes fp32
 // per-query-head partials.  DQ <= 128: 8 waves (4 key quarters x 2 query
-// halves, two waves per SIMD; the halves' sums meet in LDS at the end).
-// DQ = 192: 4 waves, one per key quarter, each taking both query halves in
-// turn: one wave per SIMD has the whole register file for its 160 columns of
-// dK and dV accumulators (two waves per SIMD spilled 70 registers).
-// NBUF Q|dO buffers: 2 overlaps the next tile's copy with this one's MFMAs;
-// 1 when two do not fit in LDS next to the resident K and V (DQ = 192).
+// halves, two waves per SIMD; the halves' sums meet in LDS at the end), K and
+// V tiles in LDS.  DQ = 192: 4 waves, one per key quarter, each taking both
+// query halves in turn; a wave only ever reads its own 32 keys, so their K
+// and V fragments stay in registers (one wave per SIMD has the whole register
+// file: the dK and dV accumulators spilled 70 registers at two waves per
+// SIMD) and LDS holds only the Q|dO tiles.  The Q|dO tiles are double
+// buffered: the next tile's copy overlaps this one's MFMAs.  (The 4-wave form
+// at DQ = 128 measured 172 us against 125 us for the 8-wave one: one wave per
+// SIMD hides less latency than it saves in LDS reads.)
 constexpr int KT2 = 128, QT2 = 64;
 template <int DQ>
 constexpr int dkdv_waves() {
   return DQ <= 128 ? 8 : 4;
 }
-
-template <int DQ, int DV>
-constexpr int dkdv_nbuf() {
-  return (KT2 + 2 * QT2) * (DQ + DV) * 2 + 2 * 2 * QT2 * 4 <= 160 * 1024 ? 2 : 1;
-}
 template <int DQ, int DV>
 constexpr int dkdv_lds_elems() {
-  return (KT2 + dkdv_nbuf<DQ, DV>() * QT2) * (DQ + DV);
+  return (dkdv_waves<DQ>() == 8 ? KT2 + 2 * QT2 : 2 * QT2) * (DQ + DV);
 }
 
 template <int DQ, int DV>
@@ -673,10 +671,10 @@ __device__ __forceinline__ void fa_bwd_dkdv_tile(
     const float* __restrict__ lse, const float* __restrict__ delta, int S, int H, int Hkv,
     float sl2, float scale, float* __restrict__ dk_part, float* __restrict__ dv_part, int kt,
     int h, int b, uint16_t* lds, float (*lse_s)[QT2], float (*dl_s)[QT2]) {
-  constexpr int NBUF = dkdv_nbuf<DQ, DV>();
   constexpr int DSQ = DQ / 16, DSV = DV / 16, DBQ = DQ / 32, DBV = DV / 32;
   constexpr int LK = KT2 * DQ, LV = KT2 * DV, LQ = QT2 * DQ, LG = QT2 * DV;
   constexpr int NW = dkdv_waves<DQ>(), NTH2 = 64 * NW, QH = 8 / NW;  // query halves per wave
+  constexpr bool KREG = NW == 4;  // K and V fragments in registers
   constexpr int PERQ = LQ / 8 / NTH2, PERG = LG / 8 / NTH2;  // 16-byte chunks per thread
   static_assert(PERQ * NTH2 * 8 == LQ && PERG * NTH2 * 8 == LG, "tiles are whole thread copies");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -691,9 +689,24 @@ __device__ __forceinline__ void fa_bwd_dkdv_tile(
   const int64_t srow = (int64_t)(b * H + h) * S;
   uint16_t* Ks = lds;
   uint16_t* Vs = lds + LK;
+  uint16_t* qg = KREG ? lds : lds + LK + LV;  // Q|dO buffers
   const int k0 = kt * KT2;
+  const int kw0 = k0 + kq * 32;   // this wave's keys
+  const int mykey = kw0 + c;
+  // KREG: the wave's K and V rows as MFMA operands (tile_row's fragments)
+  bf16x8 kfr[KREG ? DSQ : 1], vfr[KREG ? DSV : 1];
+  if constexpr (KREG) {
+    const uint4 z = make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int s = 0; s < DSQ; ++s)
+      kfr[s] = as_bf16x8(mykey < S ? ld_global16(kb + (int64_t)mykey * DQ + 16 * s + 8 * g) : z);
+#pragma unroll
+    for (int s = 0; s < DSV; ++s)
+      vfr[s] = as_bf16x8(mykey < S ? ld_global16(vb + (int64_t)mykey * DV + 16 * s + 8 * g) : z);
+  }
 
   // resident K and V tiles
+  if constexpr (!KREG) {
   for (int id = tid; id < KT2 * DQ / 8; id += NTH2) {
     const int row = id / (DQ / 8), ch = id % (DQ / 8);
     *(uint4*)(Ks + tswz<DQ>(row, ch)) = k0 + row < S
@@ -704,8 +717,7 @@ __device__ __forceinline__ void fa_bwd_dkdv_tile(
     *(uint4*)(Vs + tswz<DV>(row, ch)) = k0 + row < S
         ? ld_global16(vb + (int64_t)(k0 + row) * DV + ch * 8) : make_uint4(0, 0, 0, 0);
   }
-  const int kw0 = k0 + kq * 32;   // this wave's keys
-  const int mykey = kw0 + c;
+  }
 
   f32x16 dvacc[DBV], dkacc[DBQ];
 #pragma unroll
@@ -724,7 +736,7 @@ __device__ __forceinline__ void fa_bwd_dkdv_tile(
   // (rows past S read a clamped row, masked below); lse and Delta via VGPRs
   auto issue = [&](int qt, int buf) {
     const int q0 = qt * QT2;
-    uint16_t* qs = lds + LK + LV + buf * (LQ + LG);
+    uint16_t* qs = qg + buf * (LQ + LG);
     uint16_t* gs = qs + LQ;
 #pragma unroll
     for (int i = 0; i < PERQ; ++i) {
@@ -758,16 +770,9 @@ __device__ __forceinline__ void fa_bwd_dkdv_tile(
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   for (int qt = qt_first; qt < qt_end; ++qt) {
-    const int buf = NBUF == 2 ? (qt - qt_first) & 1 : 0;
-    if (NBUF == 2 && qt + 1 < qt_end) issue(qt + 1, buf ^ 1);
-    if (NBUF == 1 && qt > qt_first) {
-      // one buffer: load this tile after every wave left the previous one
-      issue(qt, 0);
-      stats(0);
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
-    }
-    const uint16_t* qs = lds + LK + LV + buf * (LQ + LG);
+    const int buf = (qt - qt_first) & 1;
+    if (qt + 1 < qt_end) issue(qt + 1, buf ^ 1);
+    const uint16_t* qs = qg + buf * (LQ + LG);
     const uint16_t* gs = qs + LQ;
 #pragma unroll
     for (int hq = 0; hq < QH; ++hq) {
@@ -779,13 +784,14 @@ __device__ __forceinline__ void fa_bwd_dkdv_tile(
       for (int e = 0; e < 16; ++e) { sacc[e] = 0.0f; pacc[e] = 0.0f; }
 #pragma unroll
       for (int s = 0; s < DSQ; ++s) {
-        sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_row<DQ>(qs, qh * 32 + c, s, g),
-                                                       tile_row<DQ>(Ks, kq * 32 + c, s, g), sacc,
-                                                       0, 0, 0);
+        sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            tile_row<DQ>(qs, qh * 32 + c, s, g),
+            KREG ? kfr[KREG ? s : 0] : tile_row<DQ>(Ks, kq * 32 + c, s, g), sacc, 0, 0, 0);
         if (s < DSV)
-          pacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_row<DV>(gs, qh * 32 + c, s, g),
-                                                         tile_row<DV>(Vs, kq * 32 + c, s, g),
-                                                         pacc, 0, 0, 0);
+          pacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              tile_row<DV>(gs, qh * 32 + c, s, g),
+              KREG ? vfr[KREG && s < DSV ? s : 0] : tile_row<DV>(Vs, kq * 32 + c, s, g), pacc,
+              0, 0, 0);
       }
       bf16x8 pf[2], dsf[2];
 #pragma unroll
@@ -819,7 +825,7 @@ __device__ __forceinline__ void fa_bwd_dkdv_tile(
         }
     }
     }
-    if (NBUF == 2 && qt + 1 < qt_end) stats(buf ^ 1);
+    if (qt + 1 < qt_end) stats(buf ^ 1);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
@@ -830,7 +836,7 @@ __device__ __forceinline__ void fa_bwd_dkdv_tile(
   const int qh = qh0;
   float* red = (float*)lds;
   constexpr int PARTV = DBV * 16 * 64, PARTK = DBQ * 16 * 64;
-  static_assert(4 * PARTK * 4 <= dkdv_lds_elems<DQ, DV>() * 2, "dK partials fit in LDS");
+  static_assert(NW == 4 || 4 * PARTK * 4 <= dkdv_lds_elems<DQ, DV>() * 2, "dK partials fit in LDS");
   if (NW == 8 && qh == 1) {
 #pragma unroll
     for (int db = 0; db < DBV; ++db)
@@ -885,7 +891,7 @@ __device__ __forceinline__ void fa_bwd_dkdv_tile(
 // key tiles kt and n-1-kt in one workgroup: the causal query range of the two
 // sums to a constant, so every workgroup does the same work
 template <int DQ, int DV>
-__global__ __launch_bounds__(64 * dkdv_waves<DQ>(), DQ <= 128 ? 2 : 1) void fa_bwd_dkdv(
+__global__ __launch_bounds__(64 * dkdv_waves<DQ>(), dkdv_waves<DQ>() == 8 ? 2 : 1) void fa_bwd_dkdv(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, int S, int H, int Hkv,
