@@ -32,9 +32,12 @@ CONFIGS = {
     "tiny": dict(H=256, I=688, heads=4, kv=4, D=64, eps=1e-5, r=8, alpha=16.0, B=2, S=128,
                  theta=500000.0),
 }
-# full streamed Qwen3-8B-shape training step
+# full streamed Qwen3-8B-shape training step.  The terminal's
+# token chunk bounds only the logits held at once (the loss and gradients do not depend
+# on it beyond the fp32 order of the per-chunk loss sum); 4096 takes the whole sequence
+# in one pass (1.24 GB of bf16 logits), so the head GEMMs get tiles enough for 256x256
 QWEN3 = dict(H=4096, I=12288, heads=32, kv=8, D=128, eps=1e-6, r=16, alpha=32.0, layers=36,
-             vocab=151936, S=4096, accumulation=4, theta=1000000.0, token_chunk=1024)
+             vocab=151936, S=4096, accumulation=4, theta=1000000.0, token_chunk=4096)
 QWEN3_METRIC = ("train tokens/s, full streamed Qwen3-8B-shape step (36 nf4-g128 layers from "
                 "pinned host RAM, 2 device slots, grad accumulation 4)")
 # Qwen3-MoE-30B-A3B-shape MoE feed-forward

@@ -1693,6 +1693,10 @@ extern "C" int st_linear_bf16_fwd(const uint16_t* x, int64_t M, int64_t K, int64
   p.w_bytes = ((N - 1) * ldw + K) * 2;
   ST_CHECK_ARG(p.a_bytes < (1ll << 31) && p.w_bytes < (1ll << 31),
                "st_linear_bf16_fwd: operands above 2 GiB are not supported");
+  // 256x256 tiles where they fill the GPU (the terminal's head GEMM over a
+  // whole sequence), 128x128 otherwise
+  if (st::cdiv(M, 256) * st::cdiv(N, 256) >= 192)
+    return launch<FWD_BF16, 256, 256, 8>(p, (hipStream_t)stream);
   return launch<FWD_BF16, 128, 128, 4>(p, (hipStream_t)stream);
 }
 
@@ -1713,5 +1717,10 @@ extern "C" int st_linear_bf16_dgrad(const uint16_t* dy, int64_t M, int64_t N, in
   p.w_bytes = ((N - 1) * ldw + K) * 2;
   ST_CHECK_ARG(p.a_bytes < (1ll << 31) && p.w_bytes < (1ll << 31),
                "st_linear_bf16_dgrad: operands above 2 GiB are not supported");
+  // 256x256 tiles where they fill the GPU (measured on the terminal's
+  // [4095, 4096] input gradient over vocab 151936: 256x256 ahead of 256x128,
+  // 128x256 and 128x128), 128x128 otherwise
+  if (st::cdiv(M, 256) * st::cdiv(K, 256) >= 192)
+    return launch<DGRAD_BF16, 256, 256, 8>(p, (hipStream_t)stream);
   return launch<DGRAD_BF16, 128, 128, 4>(p, (hipStream_t)stream);
 }

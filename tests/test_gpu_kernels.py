@@ -580,11 +580,12 @@ def test_rope_qkv_norm_matches_norm_then_rope(dev, D, H, Hkv):
 
 
 @pytest.mark.parametrize("M,N,K,ldw_pad", [(64, 256, 256, 0), (100, 384, 520, 8), (37, 1000, 136, 0),
-                                           (1024, 4096, 2048, 0)])
+                                           (1024, 4096, 2048, 0), (1800, 6200, 6152, 8)])
 def test_linear_bf16_fwd_and_dgrad_vs_fp32(dev, M, N, K, ldw_pad):
     """The plain bf16 GEMMs (terminal head, MoE router): y = bf16(x W^T) and
     dx = bf16(dy W) with fp32 accumulation against torch fp32 matmul, ragged
-    M/N/K and a padded W row stride."""
+    M/N/K and a padded W row stride; the last shape takes the 256x256 tiles
+    both ways (>= 192 tiles)."""
     g = torch.Generator().manual_seed(M + N + K)
     x = torch.randn(M, K, generator=g).to(BF)
     dy = torch.randn(M, N, generator=g).to(BF)
