@@ -223,9 +223,14 @@ class Q4SlotSession:
             self.poisoned = True
             raise
         finally:
+            # a failed drain or copy finalisation poisons the session too
+            # (prefetch.py:115-131); the run capability is released either way
             try:
                 torch.cuda.synchronize(self.device)
                 self._finalize_copies()
+            except BaseException:
+                self.poisoned = True
+                raise
             finally:
                 self._owner = self._token = None
                 self._run_lock.release()
@@ -311,8 +316,15 @@ class Q4SlotSession:
         finally:
             try:
                 if slot is not None and slot["active"]:
-                    consumed = torch.cuda.Event()
-                    consumed.record(torch.cuda.current_stream(self.device))
+                    # the slot may be overwritten only after this event; if it
+                    # cannot be recorded the slot stays active and the session
+                    # is poisoned (nf4_cuda_pool.py:543-565)
+                    try:
+                        consumed = torch.cuda.Event()
+                        consumed.record(torch.cuda.current_stream(self.device))
+                    except BaseException:
+                        self.poisoned = True
+                        raise
                     slot["consumed"] = consumed
                     slot["active"] = False
             finally:
@@ -351,7 +363,13 @@ class Q4SlotSession:
         if self._run_lock.locked() or self._borrow_lock.locked():
             raise RuntimeError("cannot close an active slot session/lease")
         if not self.closed:
-            torch.cuda.synchronize(self.device)
+            # a failed drain poisons the session and keeps its buffers, so a
+            # later close() can retry the cleanup
+            try:
+                torch.cuda.synchronize(self.device)
+            except BaseException:
+                self.poisoned = True
+                raise
             self.slots.clear()
             self.images.clear()
             self.closed = True
