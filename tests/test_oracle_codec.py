@@ -155,3 +155,95 @@ def test_validate_spec_rejections():
         codecs.encode(torch.ones(1, 128), "nf4")
     with pytest.raises(ValueError, match="nonfinite"):
         codecs.encode(torch.full((1, 128), float("nan")), "nf4-g128")
+
+
+# ---- validation across bounded chunks (the reference's
+# tests/test_validation_chunks.py:1-76, for the 4-bit formats of this build)
+GROUPS_V = 2048 + 3   # codecs.VALIDATION_CHUNK_GROUPS + 3
+POSITIONS_V = (0, 2047, 2048, GROUPS_V - 1)
+
+
+def _zero_record(mode, tail=False):
+    from spilltune_amd import codecs
+    assert codecs.VALIDATION_CHUNK_GROUPS == 2048
+    return codecs.encode(torch.zeros(GROUPS_V * 128 - (1 if tail else 0)), mode)
+
+
+@pytest.mark.parametrize("group", POSITIONS_V)
+def test_reserved_code_at_chunk_boundaries(group):
+    from spilltune_amd import codecs
+    r = _zero_record("int4-sym-g128")
+    r.parts["payload"][group * 64] = 0
+    with pytest.raises(ValueError, match="reserved"):
+        codecs.validate_spec(r.spec, r.parts)
+
+
+@pytest.mark.parametrize("mode", ["int4-sym-g128", "nf4-g128"])
+@pytest.mark.parametrize("group", POSITIONS_V)
+@pytest.mark.parametrize("bad", [0.0, -1.0, float("nan"), float("inf")])
+def test_invalid_scale_at_chunk_boundaries(mode, group, bad):
+    from spilltune_amd import codecs
+    r = _zero_record(mode)
+    r.parts["scales"][group] = bad
+    with pytest.raises(ValueError, match="scales"):
+        codecs.validate_spec(r.spec, r.parts)
+
+
+@pytest.mark.parametrize("mode", ["int4-sym-g128", "nf4-g128"])
+@pytest.mark.parametrize("group", POSITIONS_V)
+def test_finite_fp32_product_but_bf16_overflow_is_rejected(mode, group):
+    from spilltune_amd import codecs
+    r = _zero_record(mode)
+    p = r.parts["payload"]
+    # first element of the group decodes to +1: int4 code 9, NF4 code 15
+    p[group * 64] = (int(p[group * 64]) & 0xF0) | (9 if mode == "int4-sym-g128" else 15)
+    r.parts["scales"][group] = 3.4e38
+    assert torch.isfinite(r.parts["scales"][group]) and \
+        not torch.isfinite(r.parts["scales"][group].bfloat16())
+    with pytest.raises(ValueError, match="BF16"):
+        codecs.validate_spec(r.spec, r.parts)
+
+
+@pytest.mark.parametrize("mode", ["int4-sym-g128", "nf4-g128"])
+def test_large_scale_with_small_codes_is_accepted(mode):
+    """The overflow rule is per decoded value: a scale of 1e38 whose group
+    holds only +-1 (int4) or 0.0796 (NF4 code 8) fits bf16, though 7x or 1x
+    of it might not."""
+    from spilltune_amd import codecs
+    r = _zero_record(mode)
+    p = r.parts["payload"]
+    p[5] = (int(p[5]) & 0xF0) | (9 if mode == "int4-sym-g128" else 8)
+    r.parts["scales"][0] = 1e38 if mode == "int4-sym-g128" else 3.3e38
+    codecs.validate_spec(r.spec, r.parts)
+    if mode == "int4-sym-g128":  # code 15 (+7) in the same group overflows
+        p[6] = (int(p[6]) & 0xF0) | 15
+        with pytest.raises(ValueError, match="BF16"):
+            codecs.validate_spec(r.spec, r.parts)
+
+
+@pytest.mark.parametrize("mode", ["int4-sym-g128", "nf4-g128"])
+def test_tail_of_last_chunk_is_checked(mode):
+    from spilltune_amd import codecs
+    r = _zero_record(mode, tail=True)
+    r.parts["payload"][-1] ^= 16
+    with pytest.raises(ValueError, match="padding"):
+        codecs.validate_spec(r.spec, r.parts)
+
+
+@pytest.mark.parametrize("mode", ["int4-sym-g128", "nf4-g128"])
+def test_valid_multichunk_storage_bytes_remain_frozen(mode):
+    from spilltune_amd import codecs
+    g = torch.Generator().manual_seed(3)
+    r = codecs.encode(torch.randn(GROUPS_V * 128 - 5, generator=g), mode)
+    saved = {k: t.clone() for k, t in r.parts.items()}
+    codecs.validate_spec(r.spec, r.parts)
+    assert all(torch.equal(t, saved[k]) for k, t in r.parts.items())
+
+
+@pytest.mark.parametrize("mode", ["int4-sym-g128", "nf4-g128"])
+def test_fp32_multiply_overflow_remains_rejected(mode):
+    from spilltune_amd import codecs
+    r = codecs.encode(torch.ones(128), mode)
+    r.parts["scales"].fill_(1e38 if mode == "int4-sym-g128" else 3.4e38)
+    with pytest.raises(ValueError, match="BF16"):
+        codecs.validate_spec(r.spec, r.parts)
