@@ -82,8 +82,17 @@ def test_tiny_llama_50_step_loss_curve_matches_oracle(oracle_codec, streamed):
     else:
         session = slots.ResidentSession(model.blocks, dev)
     oracle_layers = [decoded(b, oracle_codec) for b in model.blocks]
+    original = {f"{b.index}/{k}": v.clone() for b in model.blocks for k, v in b.host_weights.items()}
+    images = {k: v.clone() for k, v in getattr(session, "images", {}).items()}
     steps, lr = 50, 2e-3
     gpu = engine.train(model, session, rows, steps=steps, lr=lr, token_chunk=64)
+    # the frozen base is never written: host records and pinned slot images
+    # are bit-identical after 50 optimizer steps (test_cpu_training.py:151-153)
+    for b in model.blocks:
+        for k, v in b.host_weights.items():
+            assert torch.equal(v, original[f"{b.index}/{k}"]), k
+    for k, v in images.items():
+        assert torch.equal(session.images[k], v)
     cfg = dict(heads=CFG["heads"], kv_heads=CFG["kv"], head_dim=CFG["D"], eps=CFG["eps"])
     cpu = OL.train_reference(emb, norm, head, oracle_layers, oracle_loras, rows, cfg=cfg,
                              theta=CFG["theta"], steps=steps, lr=lr, token_chunk=64)
