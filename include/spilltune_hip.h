@@ -441,6 +441,18 @@ int st_q4_grouped_dgrad(const uint16_t* dy, int64_t lddy, int64_t rows, int64_t 
                         const float* scales, int64_t K, const float* lut16, int32_t flags,
                         const float* dt, int64_t lddt, const float* lora_a, int32_t lora_k,
                         uint16_t* dx, int64_t lddx, st_stream_t stream);
+/* st_q4_grouped_dgrad of the experts' down projection through the SwiGLU of
+ * qwen3_moe.py:108 (silu(gate) * up per expert): with gu the permuted
+ * gate|up pre-activation [rows, 2I] (row stride ldgu), writes dgate|dup
+ * [rows, 2I] (lddgu) from the dX values instead of dX, with the rounding of
+ * st_swiglu_bwd.  I = the down projection's in_features; gu, dgu 16-byte
+ * aligned with row strides that are multiples of 8. */
+int st_q4_grouped_dgrad_swiglu(const uint16_t* dy, int64_t lddy, int64_t rows, int64_t N,
+                               const int32_t* offsets, int32_t groups, const uint8_t* payload,
+                               const float* scales, int64_t I, const float* lut16, int32_t flags,
+                               const float* dt, int64_t lddt, const float* lora_a,
+                               int32_t lora_k, const uint16_t* gu, int64_t ldgu, uint16_t* dgu,
+                               int64_t lddgu, st_stream_t stream);
 /* Grouped low-rank products over permuted rows (per-expert LoRA), fp32 out.
  * rows form: out[r, z*R + j] = alpha * sum_{k < seg_len} g[row(r), z*seg_len + k]
  *            * s[e(r)*s_gstride + (z*seg_len + k)*ssk + j*ssj]

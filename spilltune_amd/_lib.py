@@ -77,6 +77,8 @@ _SIGNATURES = {
                                  _I32, _P, _I64, _P, _I32, _F, _I32, _P, _P, _I64, _P]),
     "st_q4_grouped_dgrad": (_I32, [_P, _I64, _I64, _I64, _P, _I32, _P, _P, _I64, _P, _I32, _P,
                                    _I64, _P, _I32, _P, _I64, _P]),
+    "st_q4_grouped_dgrad_swiglu": (_I32, [_P, _I64, _I64, _I64, _P, _I32, _P, _P, _I64, _P, _I32,
+                                          _P, _I64, _P, _I32, _P, _I64, _P, _I64, _P]),
     "st_moe_lora_rows": (_I32, [_I64, _I32, _I64, _I32, _P, _I64, _I64, _P, _P, _I64, _I64, _I64,
                                 _P, _I32, _F, _P, _I64, _P]),
     "st_flash_attn_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64, _I32]),

@@ -1636,12 +1636,12 @@ extern "C" int st_q4_grouped_fwd(const uint16_t* x, int64_t x_rows, int64_t ldx,
   return launch_grouped<FWD_Q4>(p, (hipStream_t)stream);
 }
 
-extern "C" int st_q4_grouped_dgrad(const uint16_t* dy, int64_t lddy, int64_t rows, int64_t N,
-                                   const int32_t* offsets, int32_t groups, const uint8_t* payload,
-                                   const float* scales, int64_t K, const float* lut16,
-                                   int32_t flags, const float* dt, int64_t lddt,
-                                   const float* lora_a, int32_t lora_k, uint16_t* dx,
-                                   int64_t lddx, st_stream_t stream) {
+static int grouped_dgrad_impl(const uint16_t* dy, int64_t lddy, int64_t rows, int64_t N,
+                              const int32_t* offsets, int32_t groups, const uint8_t* payload,
+                              const float* scales, int64_t K, const float* lut16, int32_t flags,
+                              const float* dt, int64_t lddt, const float* lora_a, int32_t lora_k,
+                              uint16_t* dx, int64_t lddx, const uint16_t* gu, int64_t ldgu,
+                              st_stream_t stream) {
   ST_CHECK_ARG(rows >= 0 && N > 0 && K > 0 && groups > 0, "st_q4_grouped_dgrad: bad shape");
   if (rows == 0) return ST_OK;
   ST_CHECK_ARG(dy && offsets && payload && scales && dx && lut16,
@@ -1650,10 +1650,14 @@ extern "C" int st_q4_grouped_dgrad(const uint16_t* dy, int64_t lddy, int64_t row
   ST_CHECK_ARG(N % 8 == 0, "st_q4_grouped_dgrad: N (contraction) must be a multiple of 8");
   ST_CHECK_ARG(lddy % 8 == 0 && lddy >= N && al16(dy), "st_q4_grouped_dgrad: dy rows not 16-byte");
   ST_CHECK_ARG(((uintptr_t)payload & 3u) == 0, "st_q4_grouped_dgrad: payload not 4-byte aligned");
-  ST_CHECK_ARG(lddx >= K, "st_q4_grouped_dgrad: lddx < K");
+  ST_CHECK_ARG(lddx >= (gu ? 2 * K : K), "st_q4_grouped_dgrad: output row stride too small");
   GemmParams p{};
   p.A = dy; p.lda = lddy; p.M = rows; p.P = K; p.Q = N;
   p.C = dx; p.ldc = lddx;
+  if (gu) {
+    ST_CHECK_ARG(ldgu >= 2 * K, "st_q4_grouped_dgrad_swiglu: ldgu < 2 * I");
+    p.swi_gu = gu; p.swi_ld = ldgu; p.swi_I = K;
+  }
   p.hi_first = (flags & ST_FLAG_HI_NIBBLE_FIRST) ? 1 : 0;
   for (int i = 0; i < 16; ++i) p.lut.v[i] = lut16[i];
   if (dt) {
@@ -1673,6 +1677,30 @@ extern "C" int st_q4_grouped_dgrad(const uint16_t* dy, int64_t lddy, int64_t row
   p.w_bytes = N * K / 2; p.s_bytes = N * K / 128 * 4;
   p.w_gstride = N * K / 2; p.s_gstride = N * K / 128;
   return launch_grouped<DGRAD_Q4>(p, (hipStream_t)stream);
+}
+
+extern "C" int st_q4_grouped_dgrad(const uint16_t* dy, int64_t lddy, int64_t rows, int64_t N,
+                                   const int32_t* offsets, int32_t groups, const uint8_t* payload,
+                                   const float* scales, int64_t K, const float* lut16,
+                                   int32_t flags, const float* dt, int64_t lddt,
+                                   const float* lora_a, int32_t lora_k, uint16_t* dx,
+                                   int64_t lddx, st_stream_t stream) {
+  return grouped_dgrad_impl(dy, lddy, rows, N, offsets, groups, payload, scales, K, lut16, flags,
+                            dt, lddt, lora_a, lora_k, dx, lddx, nullptr, 0, stream);
+}
+
+// the experts' down-projection input gradient through SwiGLU: dgate|dup of the
+// permuted gate|up rows instead of dX (as st_q4_linear_dgrad_swiglu per expert)
+extern "C" int st_q4_grouped_dgrad_swiglu(const uint16_t* dy, int64_t lddy, int64_t rows,
+                                          int64_t N, const int32_t* offsets, int32_t groups,
+                                          const uint8_t* payload, const float* scales, int64_t I,
+                                          const float* lut16, int32_t flags, const float* dt,
+                                          int64_t lddt, const float* lora_a, int32_t lora_k,
+                                          const uint16_t* gu, int64_t ldgu, uint16_t* dgu,
+                                          int64_t lddgu, st_stream_t stream) {
+  ST_CHECK_ARG(gu != nullptr, "st_q4_grouped_dgrad_swiglu: NULL gate|up");
+  return grouped_dgrad_impl(dy, lddy, rows, N, offsets, groups, payload, scales, I, lut16, flags,
+                            dt, lddt, lora_a, lora_k, dgu, lddgu, gu, ldgu, stream);
 }
 
 // ---------------------------------------------------------------- plain bf16

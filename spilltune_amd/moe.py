@@ -290,15 +290,13 @@ class _MoEFeedForward(torch.autograd.Function):
             _lib.call("st_moe_lora_grads", R, d_rank, I, 1, _lib.ptr(h), I, R, None,
                       _lib.ptr(dT_d), d_rank, 1, _lib.ptr(offsets), E, 1.0,
                       _lib.ptr(dA_d), d_rank * I, 1, I, 0, st)
-        dh = torch.empty((R, I), dtype=_BF16, device=dev)
+        # the down dgrad's epilogue applies the SwiGLU VJP: dgate|dup directly
+        dgu = torch.empty((R, 2 * I), dtype=_BF16, device=dev)
         _launch(("moe_dgrad", R, H, I), lambda: _lib.call(
-            "st_q4_grouped_dgrad", _lib.ptr(dv), H, R, H, _lib.ptr(offsets), E,
+            "st_q4_grouped_dgrad_swiglu", _lib.ptr(dv), H, R, H, _lib.ptr(offsets), E,
             _lib.ptr(down.payload), _lib.ptr(down.scales), I, down.lut(), down.flags,
             _lib.ptr(dT_d), d_rank if has_lora else 0, _lib.ptr(A_d), d_rank if has_lora else 0,
-            _lib.ptr(dh), I, st))
-        dgu = torch.empty((R, 2 * I), dtype=_BF16, device=dev)
-        _lib.call("st_swiglu_bwd", _lib.ptr(dh), I, _lib.ptr(gu), 2 * I, _lib.ptr(gu[:, I:]),
-                  2 * I, R, I, _lib.ptr(dgu), 2 * I, _lib.ptr(dgu[:, I:]), 2 * I, st)
+            _lib.ptr(gu), 2 * I, _lib.ptr(dgu), 2 * I, st))
         if has_lora:
             dT_gu = torch.empty((R, 2 * gu_rank), dtype=_F32, device=dev)
             _lib.call("st_moe_lora_rows", R, gu_rank, I, 2, _lib.ptr(dgu), 2 * I, R, None,

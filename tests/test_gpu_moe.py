@@ -261,6 +261,43 @@ def test_grouped_fwd_and_dgrad_vs_oracle(dev, oracle_codec, monkeypatch, E, N, K
         assert _rel(got, ref) < 4e-3 and bad < 1e-3, what
 
 
+@pytest.mark.parametrize("E,H,I,T,k,lora", [(8, 256, 256, 100, 2, True), (16, 384, 128, 333, 4, False),
+                                          (32, 2048, 768, 512, 8, True)])
+def test_grouped_dgrad_swiglu_equals_dgrad_then_swiglu_bwd(dev, oracle_codec, E, H, I, T, k, lora):
+    """st_q4_grouped_dgrad_swiglu (the SwiGLU VJP in the experts' down dgrad
+    epilogue) == st_q4_grouped_dgrad then st_swiglu_bwd, bit for bit, with
+    and without the per-expert LoRA term, over ragged expert groups."""
+    g = torch.Generator().manual_seed(E + H + I)
+    H_ = _Held(dev)
+    q, _ = _experts(oracle_codec, torch.randn(E, H, I, generator=g) * 0.02, dev)
+    idx = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)]).int()
+    R = T * k
+    offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    row_token = torch.empty(R, dtype=torch.int32, device=dev)
+    pick_row = torch.empty(R, dtype=torch.int32, device=dev)
+    _lib.call("st_moe_permute", H_(idx), T, k, E, _lib.ptr(offsets),
+              _lib.ptr(row_token), _lib.ptr(pick_row), _st(dev))
+    dy = torch.randn(R, H, generator=g).to(BF).to(dev)
+    gu = torch.randn(R, 2 * I, generator=g).to(BF).to(dev)
+    r = 8
+    dt = (torch.randn(R, r, generator=g) * 0.1).to(dev) if lora else None
+    a = (torch.randn(E, r, I, generator=g) * 0.05).to(dev) if lora else None
+    kr = r if lora else 0
+    dh = torch.empty(R, I, dtype=BF, device=dev)
+    _lib.call("st_q4_grouped_dgrad", _lib.ptr(dy), H, R, H, _lib.ptr(offsets), E,
+              _lib.ptr(q.payload), _lib.ptr(q.scales), I, q.lut(), 0, _lib.ptr(dt), kr,
+              _lib.ptr(a), kr, _lib.ptr(dh), I, _st(dev))
+    ref = torch.empty(R, 2 * I, dtype=BF, device=dev)
+    _lib.call("st_swiglu_bwd", _lib.ptr(dh), I, _lib.ptr(gu), 2 * I, _lib.ptr(gu[:, I:]), 2 * I,
+              R, I, _lib.ptr(ref), 2 * I, _lib.ptr(ref[:, I:]), 2 * I, _st(dev))
+    got = torch.empty(R, 2 * I, dtype=BF, device=dev)
+    _lib.call("st_q4_grouped_dgrad_swiglu", _lib.ptr(dy), H, R, H, _lib.ptr(offsets), E,
+              _lib.ptr(q.payload), _lib.ptr(q.scales), I, q.lut(), 0, _lib.ptr(dt), kr,
+              _lib.ptr(a), kr, _lib.ptr(gu), 2 * I, _lib.ptr(got), 2 * I, _st(dev))
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+
+
 # ----------------------------------------------------------------- whole feed-forward
 def _oracle_ffn(flat, router, Wgu, Wd, idx, norm, lora):
     """Oracle forward + VJP on the GPU's picks; returns out and grads."""
