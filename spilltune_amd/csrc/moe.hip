@@ -267,58 +267,79 @@ __global__ __launch_bounds__(NTH) void route_sigmoid_bwd(const float* __restrict
 // all (token, slot) picks, takes its offset from the prefix, then places its
 // picks in ascending (token, slot) order: row_token[row] = token of the pick,
 // pick_row[token * k + slot] = its permuted row (-1 for an out-of-range
-// expert).  Deterministic, no global atomics.  1024 threads per workgroup:
-// the ordered pass is a serial walk over all picks in workgroup-sized steps.
+// expert).  Deterministic, no global atomics.  Wave w owns a contiguous block
+// of picks and walks it in 64-pick rounds (coalesced loads, lane order = pick
+// order, ballot ranks within a round); the waves' match counts are scanned
+// once, so the placement needs no workgroup barrier per round.
 constexpr int NTHP = 1024;
 __global__ __launch_bounds__(NTHP) void permute(const int32_t* __restrict__ idx, int64_t n, int k,
                                                 int E, int32_t* __restrict__ offsets,
                                                 int32_t* __restrict__ row_token,
                                                 int32_t* __restrict__ pick_row) {
-  constexpr int NTH = NTHP;
+  constexpr int NTH = NTHP, NW = NTH / 64;
   __shared__ int hist[1024];
-  __shared__ int wsum[NTH / 64];
+  __shared__ int wsum[NW];
   __shared__ int base_s;
   const int e = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   for (int i = tid; i < E; i += NTH) hist[i] = 0;
   __syncthreads();
-  for (int64_t i = tid; i < n; i += NTH) {
-    const int x = idx[i];
-    if (x >= 0 && x < E) atomicAdd(&hist[x], 1);
+  const int64_t blk = (n + NTH - 1) / NTH * 64;  // picks per wave, whole rounds
+  const int64_t b0 = min(n, wave * blk), b1 = min(n, b0 + blk);
+  const uint64_t below = (1ull << lane) - 1ull;
+  // eight rounds of loads in flight at a time
+  constexpr int U = 8;
+  auto load = [&](int64_t c, int (&xs)[U]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = c + u * 64 + lane;
+      xs[u] = i < b1 ? idx[i] : -1;
+    }
+  };
+  int cnt = 0;
+  for (int64_t c = b0; c < b1; c += U * 64) {
+    int xs[U];
+    load(c, xs);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (xs[u] >= 0 && xs[u] < E) atomicAdd(&hist[xs[u]], 1);
+      cnt += __popcll(__ballot(xs[u] == e));
+    }
   }
-  __syncthreads();
+  if (lane == 0) wsum[wave] = cnt;
+  __syncthreads();  // the histogram and the wave counts are complete
   if (tid == 0) {
     int acc = 0;
     for (int i = 0; i < e; ++i) acc += hist[i];
     base_s = acc;
     if (e == 0) {
       int run = 0;
-      for (int i = 0; i < E; ++i) { offsets[i] = run; run += hist[i]; }
+      for (int i = 0; i < E; ++i) {
+        offsets[i] = run;
+        run += hist[i];
+      }
       offsets[E] = run;
     }
   }
   __syncthreads();
-  int base = base_s;
-  for (int64_t c = 0; c < n; c += NTH) {
-    const int64_t i = c + tid;
-    const int x = i < n ? idx[i] : -1;
-    const bool mine = x == e;
-    const unsigned long long b = __ballot(mine);
-    const int before = __popcll(b & ((1ull << lane) - 1ull));
-    if (lane == 0) wsum[wave] = __popcll(b);
-    __syncthreads();
-    int wb = 0, tot = 0;
-    for (int w = 0; w < NTH / 64; ++w) {
-      if (w < wave) wb += wsum[w];
-      tot += wsum[w];
+  int r = base_s;
+  for (int w = 0; w < wave; ++w) r += wsum[w];
+  for (int64_t c = b0; c < b1; c += U * 64) {
+    int xs[U];
+    load(c, xs);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = c + u * 64 + lane;
+      const int x = xs[u];
+      const uint64_t b = __ballot(x == e);
+      if (x == e) {
+        const int rr = r + __popcll(b & below);
+        row_token[rr] = (int32_t)(i / k);
+        pick_row[i] = rr;
+      } else if (e == 0 && i < b1 && (x < 0 || x >= E)) {
+        pick_row[i] = -1;
+      }
+      r += __popcll(b);
     }
-    if (mine) {
-      const int r = base + wb + before;
-      row_token[r] = (int32_t)(i / k);
-      pick_row[i] = r;
-    }
-    if (e == 0 && i < n && (x < 0 || x >= E)) pick_row[i] = -1;
-    base += tot;
-    __syncthreads();
   }
 }
 

@@ -138,13 +138,41 @@ def test_route_sigmoid_vs_oracle(dev, E, groups, group_k, k):
 
 
 # ----------------------------------------------------------------- permutation / combine
-@pytest.mark.parametrize("T,E,k", [(4096, 128, 8), (33, 7, 3), (1, 4, 4), (500, 256, 1)])
-def test_permute_exact(dev, T, E, k):
+@pytest.mark.parametrize("T,E,k,invalid", [(4096, 128, 8, False), (33, 7, 3, False), (1, 4, 4, False),
+                                           (500, 256, 1, False), (2048, 256, 8, False),
+                                           (300, 16, 2, True)])
+def test_permute_exact(dev, T, E, k, invalid):
+    """Rows grouped by expert in ascending pick order (skewed loads, fewer
+    picks than threads, more picks than a thread run); picks of an expert id
+    outside [0, E) get row -1 and count nowhere."""
     g = torch.Generator().manual_seed(T * k + E)
     H_ = _Held(dev)
     hot = max(k, 5)     # skewed load: a third of the tokens pick among the first experts only
     idx = torch.stack([torch.randperm(hot if t < T // 3 else E, generator=g)[:k]
                        for t in range(T)]).int()
+    if invalid:
+        bad = torch.randperm(T * k, generator=g)[:T // 4]
+        idx.view(-1)[bad[: len(bad) // 2]] = -1
+        idx.view(-1)[bad[len(bad) // 2:]] = E
+        valid = (idx.flatten() >= 0) & (idx.flatten() < E)
+        offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
+        row_token = torch.full((T * k,), -7, dtype=torch.int32, device=dev)
+        pick_row = torch.empty(T * k, dtype=torch.int32, device=dev)
+        _lib.call("st_moe_permute", H_(idx), T, k, E, _lib.ptr(offsets),
+                  _lib.ptr(row_token), _lib.ptr(pick_row), _st(dev))
+        torch.cuda.synchronize()
+        flat = idx.flatten().long()
+        counts = torch.bincount(flat[valid], minlength=E)
+        assert torch.equal(offsets.cpu().long(),
+                           torch.cat([torch.zeros(1, dtype=torch.long), counts.cumsum(0)]))
+        picks = torch.arange(T * k)[valid]
+        order = picks[torch.argsort(flat[valid] * (T * k) + picks, stable=True)]
+        n = int(valid.sum())
+        assert torch.equal(row_token.cpu().long()[:n], order // k)
+        expect = torch.full((T * k,), -1, dtype=torch.long)
+        expect[order] = torch.arange(n)
+        assert torch.equal(pick_row.cpu().long(), expect)
+        return
     offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
     row_token = torch.empty(T * k, dtype=torch.int32, device=dev)
     pick_row = torch.empty(T * k, dtype=torch.int32, device=dev)
