@@ -200,14 +200,23 @@ class LoraGradSink:
         self.accumulate = bool(accumulate)
         self.products, self.keep = [], []
         self.written = set()
+        self.stream = None
 
     def wants(self, lora) -> bool:
+        """Fp32 contiguous gradient buffers shaped like A and B, and no product
+        of this adapter taken yet (a second use in the layer returns its
+        gradients through autograd, which the caller adds)."""
+        if id(lora) in self.written:
+            return False
         ga, gb = getattr(lora, "grad_A", None), getattr(lora, "grad_B", None)
         return all(isinstance(g, torch.Tensor) and g.dtype == _F32 and g.is_contiguous()
                    and g.device == self.device and tuple(g.shape) == tuple(t.shape)
                    for g, t in ((ga, lora.A), (gb, lora.B)))
 
     def add(self, lora, products, keep):
+        # the products run on the stream the backward recorded them on
+        if self.stream is None:
+            self.stream = torch.cuda.current_stream(self.device)
         self.products += products
         self.keep += keep
         self.written.add(id(lora))
@@ -215,7 +224,7 @@ class LoraGradSink:
     def flush(self):
         if not self.products:
             return
-        st = _lib.stream_handle(self.device)
+        st = ctypes_stream(self.stream)
         for i in range(0, len(self.products), 16):
             chunk = self.products[i:i + 16]
             arr = (_lib.RkProduct * len(chunk))(*chunk)
@@ -227,6 +236,10 @@ class LoraGradSink:
 
 
 _SINKS: dict = {}
+
+
+def ctypes_stream(stream):
+    return _lib.ctypes.c_void_p(stream.cuda_stream)
 
 
 @contextmanager

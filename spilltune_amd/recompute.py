@@ -65,28 +65,37 @@ def block_adapter_backward(output, hidden, ordered, grad_output, accumulate, blo
         sink.flush()
     if grads[0] is None:
         raise RuntimeError(f"block {block_idx} lost its input gradient")
-    dst, src = [], []
+    dst, src, dst_add, src_add = [], [], [], []
     for i, proj in enumerate(ordered):
         if not accumulate:
             for t in (proj.A.grad, proj.B.grad):
                 if t is not None:
                     t.zero_()
-        if id(proj) in sink.written:
-            continue
         ga, gb = grads[1 + 2 * i], grads[2 + 2 * i]
+        if id(proj) in sink.written:
+            # the sink wrote (or added) this adapter's products; a further use
+            # of it in the block came back through autograd and is added
+            for buf, g in ((proj.grad_A, ga), (proj.grad_B, gb)):
+                if g is not None:
+                    dst_add.append(buf)
+                    src_add.append(g.detach().to(buf))
+            continue
         if ga is None or gb is None:
             missing = [n for n, g in (("A", ga), ("B", gb)) if g is None]
             raise RuntimeError(f"block {block_idx} adapter {proj.name} is disconnected; "
                                f"missing gradients for {missing}")
-        dst += [proj.grad_A, proj.grad_B]
-        src += [ga.detach().to(proj.grad_A), gb.detach().to(proj.grad_B)]
-    # one multi-tensor launch for the rest: replace (zero + add in the
-    # reference) or accumulate
-    if dst:
         if accumulate:
-            torch._foreach_add_(dst, src)
+            dst_add += [proj.grad_A, proj.grad_B]
+            src_add += [ga.detach().to(proj.grad_A), gb.detach().to(proj.grad_B)]
         else:
-            torch._foreach_copy_(dst, src)
+            dst += [proj.grad_A, proj.grad_B]
+            src += [ga.detach().to(proj.grad_A), gb.detach().to(proj.grad_B)]
+    # one multi-tensor launch each: replace (zero + add in the reference) or
+    # accumulate
+    if dst:
+        torch._foreach_copy_(dst, src)
+    if dst_add:
+        torch._foreach_add_(dst_add, src_add)
     return grads[0]
 
 

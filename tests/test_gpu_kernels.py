@@ -310,6 +310,33 @@ def test_lora_grad_sink_matches_autograd_grads(dev, oracle_codec, widths, r):
                 torch.testing.assert_close(buf, exp, rtol=1e-5, atol=1e-6 * exp.abs().max().item())
 
 
+def test_lora_grad_sink_adapter_used_twice(dev, oracle_codec):
+    """An adapter used by two projections in one backward: the first use's
+    products go to the sink, the second's come back through autograd, and
+    their sum equals the autograd gradients of both uses."""
+    g = torch.Generator().manual_seed(9)
+    M, K, N, r = 256, 256, 128, 8
+    q = q4_from_oracle(oracle_codec, (torch.randn(N, K, generator=g) * 0.02).numpy(),
+                       "nf4-g128", dev)[0]
+    lo = _L((torch.randn(r, K, generator=g) * 0.05).to(dev).requires_grad_(True),
+            (torch.randn(N, r, generator=g) * 0.05).to(dev).requires_grad_(True), 16.0)
+    lo.grad_A, lo.grad_B = torch.zeros_like(lo.A), torch.zeros_like(lo.B)
+    x1 = torch.randn(M, K, generator=g).to(BF).to(dev)
+    x2 = torch.randn(M, K, generator=g).to(BF).to(dev)
+    dy = torch.randn(M, N, generator=g).to(BF).to(dev)
+
+    def out():
+        return ops.q4_lora_linear(x1, q, [lo]).float() + ops.q4_lora_linear(x2, q, [lo]).float()
+    ref = torch.autograd.grad(out(), [lo.A, lo.B], dy.float())
+    with ops.lora_grad_sink(dev, False) as sink:
+        got = torch.autograd.grad(out(), [lo.A, lo.B], dy.float(), allow_unused=True)
+        sink.flush()
+    torch.cuda.synchronize()
+    assert id(lo) in sink.written and got[0] is not None and got[1] is not None
+    for buf, extra, want in ((lo.grad_A, got[0], ref[0]), (lo.grad_B, got[1], ref[1])):
+        torch.testing.assert_close(buf + extra, want, rtol=1e-5, atol=1e-6 * want.abs().max().item())
+
+
 def test_lora_gemm_strided_vs_float64(dev):
     g = torch.Generator().manual_seed(4)
     for Mo, No, Kc in [(2048, 16, 4096), (16, 4096, 2048), (4096, 16, 2048), (5, 7, 3), (70, 33, 1000)]:
