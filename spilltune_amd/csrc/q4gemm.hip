@@ -941,31 +941,47 @@ __global__ __launch_bounds__(512) void gemm_ws_kernel(GemmParams p) {
         for (int j = 0; j < FN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
     };
-    bf16x8 fa0[FM], fb0[FN], fa1[FM], fb1[FN];
+    // Fragments two slices ahead, in three register sets used in rotation
+    // (set X holds slice 0 of the step's tile, Y slice 1, Z takes slice 2):
+    // the barrier sits after slice 1's MFMAs, once this wave's reads of the
+    // tile are done, and slices 0 and 1 of tile kt+1 are read under slices 2
+    // and 3 of tile kt.  The rotation repeats every three steps.
+    bf16x8 fa[3][FM], fb[3][FN];
     __syncthreads();
-    read_frags(As0, Bs0, 0, fa0, fb0);
-    // fragments one slice ahead; the barrier before slice 3 (as in gemm_kernel)
-    auto step = [&](int kt, int cur) {
+    read_frags(As0, Bs0, 0, fa[0], fb[0]);
+    read_frags(As0, Bs0, 1, fa[1], fb[1]);
+    auto step = [&](int kt, auto rot) {
+      constexpr int X = decltype(rot)::value, Y = (X + 1) % 3, Z = (X + 2) % 3;
       const uint4* as = As0 + (kt % WS_DA) * A_ST;
-      const uint4* bs = Bs0 + cur * B_ST;
-      read_frags(as, bs, 1, fa1, fb1);
-      mfmas(fa0, fb0);
+      const uint4* bs = Bs0 + (kt & 1) * B_ST;
+      read_frags(as, bs, 2, fa[Z], fb[Z]);
+      mfmas(fa[X], fb[X]);
       __builtin_amdgcn_sched_barrier(0);
-      read_frags(as, bs, 2, fa0, fb0);
-      mfmas(fa1, fb1);
+      read_frags(as, bs, 3, fa[X], fb[X]);
+      mfmas(fa[Y], fb[Y]);
       __builtin_amdgcn_sched_barrier(0);
-      read_frags(as, bs, 3, fa1, fb1);
-      mfmas(fa0, fb0);
-      wait_cnt<63, 0>();  // this tile's last fragment reads are done
+      wait_cnt<63, 0>();  // this tile's fragment reads are done
       bar();
-      read_frags(As0 + ((kt + 1) % WS_DA) * A_ST, Bs0 + (cur ^ 1) * B_ST, 0, fa0, fb0);
-      mfmas(fa1, fb1);
+      const uint4* as1 = As0 + ((kt + 1) % WS_DA) * A_ST;
+      const uint4* bs1 = Bs0 + ((kt + 1) & 1) * B_ST;
+      read_frags(as1, bs1, 0, fa[Y], fb[Y]);
+      mfmas(fa[Z], fb[Z]);
+      __builtin_amdgcn_sched_barrier(0);
+      read_frags(as1, bs1, 1, fa[Z], fb[Z]);
+      mfmas(fa[X], fb[X]);
       __builtin_amdgcn_sched_barrier(0);
     };
-    for (int kt = 0; kt < KT; kt += 2) {
-      step(kt, 0);
-      if (kt + 1 < KT) step(kt + 1, 1);
+    using R0 = std::integral_constant<int, 0>;
+    using R1 = std::integral_constant<int, 1>;
+    using R2 = std::integral_constant<int, 2>;
+    int kt = 0;
+    for (; kt + 3 <= KT; kt += 3) {
+      step(kt, R0{});
+      step(kt + 1, R1{});
+      step(kt + 2, R2{});
     }
+    if (kt < KT) step(kt, R0{});
+    if (kt + 1 < KT) step(kt + 1, R1{});
   }
   // every wave's last LDS reads are done before the epilogue reuses LDS
   __syncthreads();

@@ -207,9 +207,12 @@ def test_q4_linear_fwd_flat_kernel_equals_aligned(dev, oracle_codec, monkeypatch
 
 
 @pytest.mark.parametrize("tile", ["128", "2562", "256"])
-@pytest.mark.parametrize("M,N,K", [(64, 256, 256), (100, 384, 512), (37, 128, 688), (300, 512, 1024)])
+@pytest.mark.parametrize("M,N,K", [(64, 256, 256), (100, 384, 512), (37, 128, 688), (300, 512, 1024),
+                                   (77, 200, 256)])
 @pytest.mark.parametrize("lora", [False, True])
 def test_q4_linear_dgrad_and_lora_grads_vs_oracle(dev, oracle_codec, monkeypatch, tile, M, N, K, lora):
+    """dX (and the LoRA grads) against autograd over the oracle's decode; N =
+    200 leaves a ragged last k-tile of the dgrad contraction (8 of 64 rows)."""
     monkeypatch.setenv("ST_GEMM_TILE", tile)
     g = torch.Generator().manual_seed(M + N * 3 + K)
     w = (torch.randn(N, K, generator=g) * 0.02).numpy()

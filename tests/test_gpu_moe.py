@@ -244,13 +244,15 @@ def test_combine_bit_exact_and_vjp(dev):
 
 
 # ----------------------------------------------------------------- grouped GEMMs
-@pytest.mark.parametrize("tile", ["128", "2566", "2568"])
+@pytest.mark.parametrize("tile", ["128", "2562", "2566", "2568"])
 @pytest.mark.parametrize("E,N,K,T,k", [(8, 256, 256, 100, 2), (16, 96, 384, 333, 4),
                                        (32, 1536, 2048, 512, 8)])
 def test_grouped_fwd_and_dgrad_vs_oracle(dev, oracle_codec, monkeypatch, E, N, K, T, k, tile):
-    """Grouped forward on the default 128x128 tile and on the register-operand
-    256x256 and 128x256 tiles (ST_GROUPED_TILE; K = 384 is not a multiple of
-    256 and keeps the 128x128 tile), and the grouped dgrad."""
+    """Grouped forward on the default 128x128 tile, the warp-specialised
+    256x128 tile (forward and dgrad; N = 96 leaves the dgrad a ragged k-tile)
+    and the register-operand 256x256 and 128x256 tiles (ST_GROUPED_TILE;
+    K = 384 is not a multiple of 256 and keeps the 128x128 tile), and the
+    grouped dgrad."""
     monkeypatch.setenv("ST_GROUPED_TILE", tile)
     g = torch.Generator().manual_seed(E + N + K)
     H_ = _Held(dev)
