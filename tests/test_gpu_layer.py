@@ -187,6 +187,28 @@ def test_swiglu_vs_oracle():
     assert rel(ad, a) < 4e-3 and rel(d.grad, r.grad) < 1e-2
 
 
+@pytest.mark.parametrize("I", [1024, 300])
+def test_swiglu_forward_elementwise_vs_torch(I):
+    """silu(g) * u per element against torch's bf16 ops on the CPU (silu in
+    fp32, rounded to bf16, then the bf16 product), over the range where silu
+    changes shape.  The device exp may differ from the host's by an fp32 ulp
+    and so move silu(g) across a bf16 rounding boundary (one ulp of silu,
+    which the product with u can turn into at most two of the result) on a
+    handful of elements.  (A hardware 2^x / reciprocal sigmoid, as in the
+    VJP, measured 0.12% of elements off here, and the forward keeps expf and
+    the IEEE division.)  I = 1024 takes the 8-wide kernel, 300 the scalar
+    one."""
+    g = torch.Generator().manual_seed(I)
+    M = 2048
+    gate = (torch.rand(M, I, generator=g) * 24 - 12).to(BF)
+    up = torch.randn(M, I, generator=g).to(BF)
+    ref = F.silu(gate) * up
+    got = ops.swiglu(torch.cat([gate, up], 1).cuda(), I).cpu()
+    diff = (got.view(torch.int16).int() - ref.view(torch.int16).int()).abs()
+    assert int(diff.max()) <= 2
+    assert (diff > 0).float().mean().item() < 1e-4
+
+
 def test_causal_attention_vs_oracle():
     g = torch.Generator().manual_seed(3)
     B, H, kv, S, D = 2, 8, 2, 96, 64
