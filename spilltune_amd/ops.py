@@ -232,6 +232,11 @@ class LoraGradSink:
             ws = _ws.get(self.device, need)
             _lib.call("st_rk_batch", len(chunk), arr, _lib.ptr(ws),
                       0 if ws is None else ws.numel(), st)
+        # the operands may be freed before the products finish: the allocator
+        # must not hand their memory to another stream until they have
+        for t in self.keep:
+            if isinstance(t, torch.Tensor) and t.is_cuda:
+                t.record_stream(self.stream)
         self.products, self.keep = [], []
 
 
