@@ -276,7 +276,7 @@ int st_swiglu_bwd(const uint16_t* da, int64_t ldda, const uint16_t* g, int64_t l
  * Causal GQA flash attention, replacing the eager chain of
  * adapters/dense.py:142-148 (repeat k/v over the group, scores = q k^T *
  * scale + causal mask, fp32 softmax, probabilities @ v, relayout to tokens).
- * q [B,H,S,D], k/v [B,Hkv,S,D] head-major bf16; D in {64, 128}; S % 8 == 0.
+ * q [B,H,S,D], k/v [B,Hkv,S,D] head-major bf16; D in {64, 128}; any S >= 0.
  * out is token-major [B,S,H*D] bf16; lse [B,H,S] fp32 is the base-2
  * log-sum-exp of scale*log2(e)*q.k per query (the backward's statistics).
  * Probabilities are kept in fp32 until the bf16 P.V product (the reference

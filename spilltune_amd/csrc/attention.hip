@@ -1024,7 +1024,7 @@ int fwd_common(const char* name, const uint16_t* q, const uint16_t* k, const uin
   if (!dims_ok(DQ, DV))
     return st::fail(ST_EUNSUPPORTED, "%s: head dims %lld/%lld (64/64, 128/128 or 192/128 only)",
                     name, (long long)DQ, (long long)DV);
-  ST_CHECK_ARG(S % 8 == 0 && S < (1 << 30), "%s: S must be a multiple of 8", name);
+  ST_CHECK_ARG(S < (1 << 30), "%s: S must be below 2^30", name);
   ST_CHECK_ARG(q && k && v && out && lse && al16(q) && al16(k) && al16(v) && al16(out),
                "%s: NULL or unaligned pointer", name);
   const int64_t need = attn_workspace(B, S, H, Hkv, DQ, DV, 0);
@@ -1046,7 +1046,7 @@ int bwd_common(const char* name, const uint16_t* q, const uint16_t* k, const uin
   if (!dims_ok(DQ, DV))
     return st::fail(ST_EUNSUPPORTED, "%s: head dims %lld/%lld (64/64, 128/128 or 192/128 only)",
                     name, (long long)DQ, (long long)DV);
-  ST_CHECK_ARG(S % 8 == 0 && S < (1 << 30), "%s: S must be a multiple of 8", name);
+  ST_CHECK_ARG(S < (1 << 30), "%s: S must be below 2^30", name);
   ST_CHECK_ARG(q && k && v && out && lse && dout && dq && dk && dv && al16(q) && al16(k) &&
                    al16(v) && al16(out) && al16(dout) && al16(dq) && al16(dk) && al16(dv),
                "%s: NULL or unaligned pointer", name);

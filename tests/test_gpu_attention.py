@@ -40,8 +40,13 @@ def _fwd(q, k, v, scale):
     return out, lse
 
 
+# sequence lengths of any size: 1, 17, 100 and 129 leave ragged key and
+# query tiles (and a V^T staging row longer than S)
+ODD_S = [(1, 2, 1, 1, 64), (2, 4, 2, 17, 128), (1, 4, 4, 100, 64), (1, 8, 2, 129, 128)]
+
+
 @pytest.mark.parametrize("B,H,Hkv,S,D", [(1, 4, 2, 128, 64), (2, 4, 4, 200, 64), (1, 8, 2, 256, 128),
-                                         (1, 4, 1, 72, 128), (1, 32, 8, 2048, 128)])
+                                         (1, 4, 1, 72, 128), (1, 32, 8, 2048, 128)] + ODD_S)
 def test_flash_fwd_vs_fp32(dev, B, H, Hkv, S, D):
     g = torch.Generator().manual_seed(B * 1000 + H * 10 + S + D)
     q = torch.randn(B, H, S, D, generator=g).to(BF).to(dev)
@@ -69,7 +74,7 @@ def _bwd(q, k, v, out, lse, dout, scale):
 
 
 @pytest.mark.parametrize("B,H,Hkv,S,D", [(1, 4, 2, 128, 64), (2, 4, 4, 200, 64), (1, 8, 2, 256, 128),
-                                         (1, 4, 1, 72, 128), (1, 32, 8, 2048, 128)])
+                                         (1, 4, 1, 72, 128), (1, 32, 8, 2048, 128)] + ODD_S)
 def test_flash_bwd_vs_fp32_autograd(dev, B, H, Hkv, S, D):
     g = torch.Generator().manual_seed(B * 999 + H * 7 + S + D)
     q = torch.randn(B, H, S, D, generator=g).to(BF).to(dev)
@@ -83,6 +88,11 @@ def test_flash_bwd_vs_fp32_autograd(dev, B, H, Hkv, S, D):
     ref, _ = _ref(qf, kf, vf, scale)
     ref.backward(dout.float())
     for got, want, name in ((dq, qf.grad, "dq"), (dk, kf.grad, "dk"), (dv, vf.grad, "dv")):
+        if S == 1 and name != "dv":
+            # one key: P = 1 and dS = P (dP - rowsum(dO o O)) = 0, so dq = dk = 0
+            # (the fp32 reference leaves rounding noise)
+            assert got.float().abs().max().item() < 1e-3 and want.abs().max().item() < 1e-3
+            continue
         rel = ((got.float() - want).norm() / want.norm()).item()
         cos = torch.nn.functional.cosine_similarity(got.float().flatten(), want.flatten(), 0).item()
         assert rel < 2e-2 and cos > 0.9995, (name, rel, cos)
@@ -123,7 +133,8 @@ def _mla(q, k, v, scale, dout=None):
     return out, lse, dq, dk, dv
 
 
-@pytest.mark.parametrize("B,H,S", [(1, 4, 128), (2, 3, 200), (1, 8, 72), (1, 128, 2048)])
+@pytest.mark.parametrize("B,H,S", [(1, 4, 128), (2, 3, 200), (1, 8, 72), (1, 128, 2048), (1, 2, 13),
+                                   (2, 3, 130)])
 def test_mla_attention_fwd_bwd_vs_fp32(dev, B, H, S):
     """Query/key heads of 192 against value heads of 128 (DeepSeek-V3 MLA),
     forward and VJP against float32 autograd; the last case is config 5's

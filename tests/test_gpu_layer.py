@@ -133,6 +133,12 @@ def test_qwen3_qk_norm_layer_step_vs_oracle(oracle_codec):
                      targets=("self_attn.q_proj", "self_attn.v_proj", "self_attn.o_proj")))
 
 
+def test_odd_sequence_length_layer_step_vs_oracle(oracle_codec):
+    """A sequence length that is no multiple of 8 (or of any tile): 2 x 100
+    tokens through the whole layer step, GQA, streamed."""
+    _assert(run_case(dict(GQA, B=2, S=100), 25, oracle_codec, streamed=True))
+
+
 def test_llama8b_dims_short_sequence(oracle_codec):
     cfg = dict(H=4096, I=14336, heads=32, kv=8, D=128, eps=1e-5, r=16, alpha=32.0, B=1, S=64)
     _assert(run_case(cfg, 40, oracle_codec))

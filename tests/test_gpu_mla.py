@@ -257,12 +257,13 @@ def test_deepseek_layer_step_v3_head_dims(oracle_codec, monkeypatch, q_rank, int
                       monkeypatch=monkeypatch))
 
 
-def test_deepseek_layer_step_small_heads_resident(oracle_codec, monkeypatch):
+@pytest.mark.parametrize("S", [40, 37])
+def test_deepseek_layer_step_small_heads_resident(oracle_codec, monkeypatch, S):
     """qk 48 + 16 against v 64 (the 64/64 attention kernel), ragged tokens,
-    batch 2, weights resident."""
+    batch 2, weights resident; S = 37 is no multiple of 8."""
     c = _params(heads=3, nope=48, rope=16, vdim=64, kv_rank=128, q_rank=128, interleave=True,
                 moe=True, rope_cfg=DEFAULT, E=8, groups=4, group_k=2, top_k=2)
-    _assert(run_layer(c, H=128, E=8, S=40, B=2, oracle_codec=oracle_codec, seed=5,
+    _assert(run_layer(c, H=128, E=8, S=S, B=2, oracle_codec=oracle_codec, seed=5,
                       streamed=False, monkeypatch=monkeypatch))
 
 
