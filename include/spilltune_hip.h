@@ -80,10 +80,12 @@ int st_dequant4(const uint8_t* payload, const float* scales, int64_t numel, int3
  *   base[m,n] = bf16( sum_k x[m,k] * W[n,k] )            (W = dequant, bf16)
  *   y[m,n]    = bf16( base + lora_scale * sum_j t[m, seg(n)*rank + j] * lora_b[n,j] )
  *   y[m,n]    = bf16( residual[m,n] + y[m,n] )            (if residual)
- * W [N,K] is payload/scales in flat groups of 128.  W is dequantised into LDS
- * inside the GEMM (never written to HBM as bf16) when K % 128 == 0; other K go
- * through a bf16 copy of W in `workspace` (st_q4_linear_fwd_workspace_bytes).
- * `t` = x_f32 A_cat^T from st_lora_gemm ([M, nseg*rank] fp32) or NULL for no LoRA.
+ * W [N,K] is payload/scales in flat groups of 128, dequantised inside the
+ * GEMM and never written to HBM as bf16 (K % 128 != 0, where the groups
+ * straddle W's rows: each packed word reads its own group's scale).  K % 8 ==
+ * 0.  `workspace` is not used (the query returns 0).
+ * `t` = x_f32 A_cat^T from st_lora_gemm ([M, nseg*rank] fp32) or NULL for no
+ * LoRA; 1 <= rank and nseg * rank <= 64 (any parity).
  * nseg/seg_end describe N-concatenated projections (fused q|k|v, gate|up):
  * column n belongs to segment s = #{seg_end[i] <= n}; segment ends must be
  * multiples of 32.  nseg = 1 with seg_end[0] = N for a single projection.
@@ -103,8 +105,8 @@ int st_q4_linear_fwd(const uint16_t* x, int64_t M, int64_t K, int64_t ldx,
  *   dx[m,k] = bf16( bf16(sum_n dy[m,n] W[n,k]) + bf16(sum_j dt[m,j] lora_a[j,k]) )
  * with dt = lora_scale * dy_f32 B ([M, lora_k] fp32, from st_lora_bwd_dy;
  * N-concatenated projections stack their dt columns and lora_a rows) or
- * dt == NULL for no LoRA term.  W [N,K] as above; dequantised transposed into
- * LDS when K % 128 == 0.
+ * dt == NULL for no LoRA term; 1 <= lora_k <= 64.  W [N,K] as above,
+ * dequantised into LDS in its natural orientation and read transposed.
  */
 int64_t st_q4_linear_dgrad_workspace_bytes(int64_t M, int64_t N, int64_t K);
 int st_q4_linear_dgrad(const uint16_t* dy, int64_t M, int64_t N, int64_t lddy,

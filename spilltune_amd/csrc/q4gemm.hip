@@ -151,7 +151,7 @@ template <bool DGRAD, int BM, int BN>
 __host__ __device__ __forceinline__ int64_t epi_stage_offset(const GemmParams& p) {
   if (!p.T) return 0;
   const int64_t f = (int64_t)BM * (p.lora_cols + 1) +
-                    (DGRAD ? (int64_t)p.lora_k * BN : (int64_t)BN * (p.lora_k + 1));
+                    (int64_t)BN * (p.lora_k + 1);
   return (f + 3) & ~(int64_t)3;
 }
 
@@ -184,6 +184,16 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const f32x16 
     else
       stage_f32<NT>(Ls, lstride, make_rsrc(Lg, 0x7fffffff), p.ldl, p0, 0, BN, p.lora_k, p.P - p0,
                     p.lora_k, tid);
+    // zeros past the contraction (T's spare column, the right operand's spare
+    // column or row): lora_term takes the rank two at a time, so an odd rank
+    // reads index lora_k once, as 0 x (a finite T value or 0)
+    for (int r = tid; r < BM; r += NT) Ts[r * tstride + p.lora_cols] = 0.0f;
+    for (int c = tid; c < BN; c += NT) {
+      if (DGRAD)
+        Ls[p.lora_k * lstride + c] = 0.0f;
+      else
+        Ls[c * lstride + p.lora_k] = 0.0f;
+    }
     __syncthreads();
   }
   if (!has_acc) return;
@@ -1258,7 +1268,7 @@ int launch_ws(const GemmParams& p, hipStream_t stream) {
   if (tiles > 0x7fffffff) return st::fail(ST_EUNSUPPORTED, "q4gemm: too many tiles");
   if (p.T) {
     const int64_t need = (int64_t)BM * (p.lora_cols + 1) +
-                         (MODE == DGRAD_Q4 ? (int64_t)p.lora_k * BN : (int64_t)BN * (p.lora_k + 1));
+                         (int64_t)BN * (p.lora_k + 1);
     if (need > (int64_t)WS_DA * BM * BK / 8 * 4)
       return st::fail(ST_EUNSUPPORTED, "q4gemm: LoRA epilogue (%d columns) exceeds tile LDS",
                       p.lora_cols);
@@ -1301,7 +1311,7 @@ int launch(const GemmParams& p, hipStream_t stream) {
   if (p.T) {  // the LoRA epilogue stages T and the right operand in the tile's LDS
     using TL = Tile<MODE, BM, BN, WAVES, WAVES_M>;
     int64_t need = (int64_t)BM * (p.lora_cols + 1) +
-                   (TL::DGRAD ? (int64_t)p.lora_k * BN : (int64_t)BN * (p.lora_k + 1));
+                   (int64_t)BN * (p.lora_k + 1);
     if (need > (int64_t)TL::LDS_CHUNKS * 4)
       return st::fail(ST_EUNSUPPORTED, "q4gemm: LoRA epilogue (%d columns) exceeds tile LDS",
                       p.lora_cols);
@@ -1454,8 +1464,8 @@ extern "C" int64_t st_q4_linear_dgrad_workspace_bytes(int64_t M, int64_t N, int6
 }
 
 static int check_lora_common(int64_t rank, int64_t cols) {
-  if (rank <= 0 || rank % 2 || rank > 64)
-    return st::fail(ST_EUNSUPPORTED, "q4 linear: LoRA contraction %lld must be even and <= 64",
+  if (rank <= 0 || rank > 64)
+    return st::fail(ST_EUNSUPPORTED, "q4 linear: LoRA contraction %lld must be in [1, 64]",
                     (long long)rank);
   if (cols > 64)
     return st::fail(ST_EUNSUPPORTED, "q4 linear: %lld LoRA columns exceed 64", (long long)cols);

@@ -120,10 +120,10 @@ def _weight(weights, name):
 
 def _pair(weights, a, b, la, lb):
     """Fused N-concatenation of two projections that read the same input when
-    their storage is adjacent and their LoRA configuration matches."""
+    their storage is adjacent and their adapters fit one fused GEMM."""
     wa, wb = _weight(weights, a), _weight(weights, b)
     fused = ops.concat_rows([wa, wb])
-    if fused is not None and (la is None) == (lb is None):
+    if fused is not None and ops.lora_fusable([la, lb]):
         return fused
     return None
 

@@ -87,7 +87,7 @@ def dense_block(hidden_states, position_embeddings, attention_mask, *, heads, kv
     wq, wk, wv = (_weight(weights, f"self_attn.{p}_proj") for p in "qkv")
     qkv = ops.concat_rows([wq, wk, wv])
     loras_qkv = [lora_q, lora_k, lora_v]
-    if qkv is not None and (all(l is None for l in loras_qkv) or all(l is not None for l in loras_qkv)):
+    if qkv is not None and ops.lora_fusable(loras_qkv):
         y = ops.q4_lora_linear(xn, qkv, loras_qkv)
         if qk_norm:
             # per-head q/k RMSNorm and the rotation in one kernel each way
@@ -115,7 +115,7 @@ def dense_block(hidden_states, position_embeddings, attention_mask, *, heads, kv
     loras_gu = [lora_gate, lora_up]
     inter = wg.out_features
     wd = _weight(weights, "mlp.down_proj")
-    if gu is not None and (all(l is None for l in loras_gu) or all(l is not None for l in loras_gu)):
+    if gu is not None and ops.lora_fusable(loras_gu):
         # down reads silu(gate) * up of the fused gate|up output; its input-
         # gradient GEMM applies the SwiGLU VJP in the epilogue
         out = ops.q4_lora_linear(ops.q4_lora_linear(xn2, gu, loras_gu), wd, [lora_down],

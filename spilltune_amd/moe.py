@@ -445,7 +445,7 @@ def deepseek_moe_feed_forward(hidden, weights, *, num_experts, top_k, groups, gr
         wd = weights[prefix + "down_proj.weight"]
         lg, lu, ldn = ls.get("gate"), ls.get("up"), ls.get("down")
         gu = ops.concat_rows([wg, wu])
-        if gu is not None and (lg is None) == (lu is None):
+        if gu is not None and ops.lora_fusable([lg, lu]):
             shared = ops.q4_lora_linear(ops.q4_lora_linear(flat, gu, [lg, lu]), wd, [ldn],
                                         swiglu=True)
         else:

@@ -81,6 +81,24 @@ class Q4Weight:
         return out
 
 
+MAX_LORA_COLS = 64  # LoRA columns (segments x rank) one fused GEMM epilogue stages
+
+
+def lora_fusable(loras) -> bool:
+    """Whether N-concatenated projections with these adapters can run as one
+    fused GEMM: no adapter at all, or one on every part with a single rank and
+    scale and at most MAX_LORA_COLS LoRA columns in all (the epilogue's
+    limit).  Otherwise callers run the projections one by one."""
+    loras = list(loras)
+    if all(l is None for l in loras):
+        return True
+    if any(l is None for l in loras):
+        return False
+    ranks = {int(l.rank) for l in loras}
+    scales = {float(l.scale) for l in loras}
+    return len(ranks) == 1 and len(scales) == 1 and len(loras) * ranks.pop() <= MAX_LORA_COLS
+
+
 def concat_rows(weights) -> Q4Weight | None:
     """Zero-copy view of row-concatenated 4-bit weights when their payloads and
     scales are adjacent in memory and each matrix holds whole groups (then the
@@ -971,7 +989,7 @@ def attention_scale(head_dim: int) -> float:
     return float(head_dim) ** -0.5
 
 
-__all__ = ["Q4Weight", "concat_rows", "q4_lora_linear", "rms_norm", "rope_qkv", "rope_heads",
+__all__ = ["Q4Weight", "concat_rows", "lora_fusable", "q4_lora_linear", "rms_norm", "rope_qkv", "rope_heads",
            "causal_attention", "swiglu", "swiglu_pair", "lora_gemm", "attention_scale",
            "mla_rope", "mla_attention",
            "rms_norm_residual",

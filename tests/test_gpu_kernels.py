@@ -143,6 +143,28 @@ def test_q4_linear_fwd_vs_oracle(dev, oracle_codec, monkeypatch, tile, fmt, M, N
     _close_bf16(y, ref, f"fwd {fmt} {M}x{N}x{K} tile{tile}")
 
 
+@pytest.mark.parametrize("tile", ["128", "2562", "256", "2566", "2567", "2568"])
+@pytest.mark.parametrize("r", [1, 3, 7])
+def test_q4_linear_fwd_odd_rank_vs_oracle(dev, oracle_codec, monkeypatch, tile, r):
+    """Odd LoRA ranks on every forward tile, with a residual: the epilogue's
+    fp32 MFMA takes the rank two at a time and reads a zero past the last
+    rank column."""
+    monkeypatch.setenv("ST_GEMM_TILE", tile)
+    M, N, K = 300, 512, 1024
+    g = torch.Generator().manual_seed(r * 101 + M)
+    w = (torch.randn(N, K, generator=g) * 0.02).numpy()
+    q, W = q4_from_oracle(oracle_codec, w, "nf4-g128", dev)
+    x = torch.randn(M, K, generator=g).to(BF)
+    lo = _L(torch.randn(r, K, generator=g) * 0.05, torch.randn(N, r, generator=g) * 0.05, 2.0 * r)
+    res = torch.randn(M, N, generator=g).to(BF)
+    ref = (F.linear(x.float(), W.float()).to(BF).float() + (x.float() @ lo.A.T @ lo.B.T) * lo.scale)
+    ref = (res.float() + ref.to(BF).float()).to(BF)
+    y = ops.q4_lora_linear(x.to(dev), q, [_L(lo.A.to(dev), lo.B.to(dev), 2.0 * r)],
+                           residual=res.to(dev))
+    torch.cuda.synchronize()
+    _close_bf16(y, ref, f"odd rank {r} tile{tile}")
+
+
 @pytest.mark.parametrize("tile", ["128", "2562", "256", "2566", "2568"])
 @pytest.mark.parametrize("M,N,K", [(100, 384, 512), (300, 512, 1024)])
 def test_q4_linear_high_nibble_first_vs_oracle(dev, oracle_codec, monkeypatch, tile, M, N, K):
@@ -209,17 +231,19 @@ def test_q4_linear_fwd_flat_kernel_equals_aligned(dev, oracle_codec, monkeypatch
 @pytest.mark.parametrize("tile", ["128", "2562", "256"])
 @pytest.mark.parametrize("M,N,K", [(64, 256, 256), (100, 384, 512), (37, 128, 688), (300, 512, 1024),
                                    (77, 200, 256)])
-@pytest.mark.parametrize("lora", [False, True])
-def test_q4_linear_dgrad_and_lora_grads_vs_oracle(dev, oracle_codec, monkeypatch, tile, M, N, K, lora):
+@pytest.mark.parametrize("lora,r", [(False, 8), (True, 8), (True, 5)])
+def test_q4_linear_dgrad_and_lora_grads_vs_oracle(dev, oracle_codec, monkeypatch, tile, M, N, K, lora,
+                                                  r):
     """dX (and the LoRA grads) against autograd over the oracle's decode; N =
-    200 leaves a ragged last k-tile of the dgrad contraction (8 of 64 rows)."""
+    200 leaves a ragged last k-tile of the dgrad contraction (8 of 64 rows);
+    r = 5 is an odd rank (the epilogue takes the rank two at a time)."""
     monkeypatch.setenv("ST_GEMM_TILE", tile)
     g = torch.Generator().manual_seed(M + N * 3 + K)
     w = (torch.randn(N, K, generator=g) * 0.02).numpy()
     q, W = q4_from_oracle(oracle_codec, w, "nf4-g128", dev)
     x = torch.randn(M, K, generator=g).to(BF)
     dy = torch.randn(M, N, generator=g).to(BF)
-    r, alpha = 8, 16.0
+    alpha = 2.0 * r
     A = torch.randn(r, K, generator=g) * 0.05
     B = torch.randn(N, r, generator=g) * 0.05
     # oracle: autograd of lora.py:218-220 on CPU
@@ -240,11 +264,13 @@ def test_q4_linear_dgrad_and_lora_grads_vs_oracle(dev, oracle_codec, monkeypatch
             torch.testing.assert_close(got, ref, rtol=1e-4, atol=1e-5 * ref.abs().max().item())
 
 
-def test_fused_segments_match_separate_projections(dev, oracle_codec):
+@pytest.mark.parametrize("r", [4, 5])
+def test_fused_segments_match_separate_projections(dev, oracle_codec, r):
     """q|k|v as one N-concatenated GEMM == three separate GEMMs (same bits for
-    the forward: every output element has the same reduction)."""
+    the forward: every output element has the same reduction), for an even
+    and an odd rank."""
     g = torch.Generator().manual_seed(0)
-    M, K, widths, r = 96, 256, (256, 64, 64), 4
+    M, K, widths = 96, 256, (256, 64, 64)
     ws = [(torch.randn(n, K, generator=g) * 0.02).numpy() for n in widths]
     qs = [q4_from_oracle(oracle_codec, w, "nf4-g128", dev)[0] for w in ws]
     payload = torch.cat([q.payload for q in qs])

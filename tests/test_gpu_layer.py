@@ -133,6 +133,15 @@ def test_qwen3_qk_norm_layer_step_vs_oracle(oracle_codec):
                      targets=("self_attn.q_proj", "self_attn.v_proj", "self_attn.o_proj")))
 
 
+@pytest.mark.parametrize("r", [5, 32])
+def test_layer_step_lora_ranks_vs_oracle(oracle_codec, r):
+    """An odd rank (5: fused q|k|v and gate|up with 15 and 10 LoRA columns) and
+    rank 32 (q|k|v would need 96 LoRA columns, more than one fused GEMM
+    takes, so the functional runs q, k and v one by one; gate|up fused at
+    64)."""
+    _assert(run_case(dict(GQA, r=r, alpha=2.0 * r), 60 + r, oracle_codec))
+
+
 def test_odd_sequence_length_layer_step_vs_oracle(oracle_codec):
     """A sequence length that is no multiple of 8 (or of any tile): 2 x 100
     tokens through the whole layer step, GQA, streamed."""
