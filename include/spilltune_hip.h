@@ -279,6 +279,10 @@ int st_swiglu_bwd(const uint16_t* da, int64_t ldda, const uint16_t* g, int64_t l
  * adapters/dense.py:142-148 (repeat k/v over the group, scores = q k^T *
  * scale + causal mask, fp32 softmax, probabilities @ v, relayout to tokens).
  * q [B,H,S,D], k/v [B,Hkv,S,D] head-major bf16; D in {64, 128}; any S >= 0.
+ * kv_len: NULL (every key valid) or a device int32 [B] of valid key counts
+ * for right-padded rows (dense.py:237-246): keys >= kv_len[b] are masked for
+ * every query of row b, padded queries included, as the reference's additive
+ * finfo.min mask does; values are clamped to [1, S].
  * out is token-major [B,S,H*D] bf16; lse [B,H,S] fp32 is the base-2
  * log-sum-exp of scale*log2(e)*q.k per query (the backward's statistics).
  * Probabilities are kept in fp32 until the bf16 P.V product (the reference
@@ -287,17 +291,19 @@ int st_swiglu_bwd(const uint16_t* da, int64_t ldda, const uint16_t* g, int64_t l
 int64_t st_flash_attn_workspace_bytes(int64_t B, int64_t S, int64_t H, int64_t Hkv, int64_t D,
                                       int32_t backward);
 int st_flash_attn_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, int64_t B,
-                      int64_t S, int64_t H, int64_t Hkv, int64_t D, float scale, uint16_t* out,
-                      float* lse, void* workspace, int64_t workspace_bytes, st_stream_t stream);
+                      int64_t S, int64_t H, int64_t Hkv, int64_t D, float scale,
+                      const int32_t* kv_len, uint16_t* out, float* lse, void* workspace,
+                      int64_t workspace_bytes, st_stream_t stream);
 /* VJP of st_flash_attn_fwd (autograd of dense.py:142-148): from dout
  * (token-major [B,S,H*D]), the forward's out and lse, writes dq [B,H,S,D]
  * and dk, dv [B,Hkv,S,D] head-major bf16 (GQA group sums in fp32, one
- * rounding).  Deterministic: no atomics. */
+ * rounding).  Deterministic: no atomics.  kv_len as in the forward (masked
+ * keys get zero dk, dv). */
 int st_flash_attn_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                       const uint16_t* out, const float* lse, const uint16_t* dout, int64_t B,
-                      int64_t S, int64_t H, int64_t Hkv, int64_t D, float scale, uint16_t* dq,
-                      uint16_t* dk, uint16_t* dv, void* workspace, int64_t workspace_bytes,
-                      st_stream_t stream);
+                      int64_t S, int64_t H, int64_t Hkv, int64_t D, float scale,
+                      const int32_t* kv_len, uint16_t* dq, uint16_t* dk, uint16_t* dv,
+                      void* workspace, int64_t workspace_bytes, st_stream_t stream);
 
 /* ---------------------------------------------------------------------
  * Causal multi-head latent attention of DeepSeek-V3 (adapters/deepseek.py:
@@ -306,8 +312,9 @@ int st_flash_attn_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
  * mask, fp32 softmax, probabilities @ value), the same flash kernels with
  * query/key heads of DQ and value heads of DV: q, k [B,H,S,DQ], v [B,H,S,DV]
  * head-major bf16 (no grouping: every head has its own key); out token-major
- * [B,S,H*DV]; lse [B,H,S] as st_flash_attn_fwd.  (DQ, DV) = (192, 128), the
- * V3 shape (qk_nope 128 + qk_rope 64, v 128), or 64/64, 128/128.
+ * [B,S,H*DV]; lse [B,H,S] and kv_len as st_flash_attn_fwd.  (DQ, DV) =
+ * (192, 128), the V3 shape (qk_nope 128 + qk_rope 64, v 128), or 64/64,
+ * 128/128.
  * --------------------------------------------------------------------- */
 /* Query/key/value assembly of deepseek.py:137-150 (and its VJP): from q
  * [M, H*(nope+rope)] (row stride ldq; per head q_nope | q_rope), kv
@@ -335,14 +342,15 @@ int st_mla_rope_bwd(const uint16_t* dQ, const uint16_t* dK, const uint16_t* dV,
 int64_t st_mla_attn_workspace_bytes(int64_t B, int64_t S, int64_t H, int64_t DQ, int64_t DV,
                                     int32_t backward);
 int st_mla_attn_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, int64_t B,
-                    int64_t S, int64_t H, int64_t DQ, int64_t DV, float scale, uint16_t* out,
-                    float* lse, void* workspace, int64_t workspace_bytes, st_stream_t stream);
+                    int64_t S, int64_t H, int64_t DQ, int64_t DV, float scale,
+                    const int32_t* kv_len, uint16_t* out, float* lse, void* workspace,
+                    int64_t workspace_bytes, st_stream_t stream);
 /* VJP of st_mla_attn_fwd: dq, dk [B,H,S,DQ], dv [B,H,S,DV]. */
 int st_mla_attn_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                     const uint16_t* out, const float* lse, const uint16_t* dout, int64_t B,
-                    int64_t S, int64_t H, int64_t DQ, int64_t DV, float scale, uint16_t* dq,
-                    uint16_t* dk, uint16_t* dv, void* workspace, int64_t workspace_bytes,
-                    st_stream_t stream);
+                    int64_t S, int64_t H, int64_t DQ, int64_t DV, float scale,
+                    const int32_t* kv_len, uint16_t* dq, uint16_t* dk, uint16_t* dv,
+                    void* workspace, int64_t workspace_bytes, st_stream_t stream);
 
 /* ---------------------------------------------------------------------
  * Plain bf16 linear (router logits and their input gradient).

@@ -82,18 +82,19 @@ _SIGNATURES = {
     "st_moe_lora_rows": (_I32, [_I64, _I32, _I64, _I32, _P, _I64, _I64, _P, _P, _I64, _I64, _I64,
                                 _P, _I32, _F, _P, _I64, _P]),
     "st_flash_attn_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64, _I32]),
-    "st_flash_attn_fwd": (_I32, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _P, _P, _P, _I64,
-                                 _P]),
+    "st_flash_attn_fwd": (_I32, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _P, _P, _P, _P,
+                                 _I64, _P]),
     "st_flash_attn_bwd": (_I32, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _P, _P,
-                                 _P, _P, _I64, _P]),
+                                 _P, _P, _P, _I64, _P]),
     "st_mla_rope_fwd": (_I32, [_P, _I64, _P, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64,
                                _I64, _I32, _P, _P, _P, _P]),
     "st_mla_rope_bwd": (_I32, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P,
                                _I64, _P, _I64, _P, _I64, _P]),
     "st_mla_attn_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64, _I32]),
-    "st_mla_attn_fwd": (_I32, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _P, _P, _P, _I64, _P]),
+    "st_mla_attn_fwd": (_I32, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _P, _P, _P, _P, _I64,
+                               _P]),
     "st_mla_attn_bwd": (_I32, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _P, _P,
-                               _P, _P, _I64, _P]),
+                               _P, _P, _P, _I64, _P]),
     "st_cross_entropy_rows": (_I32, [_P, _I64, _I64, _I64, _P, _I64, _F, _P, _P]),
     "st_moe_lora_grads": (_I32, [_I64, _I32, _I64, _I32, _P, _I64, _I64, _P, _P, _I64, _I64, _P,
                                  _I32, _F, _P, _I64, _I64, _I64, _I32, _P]),

@@ -122,7 +122,7 @@ __device__ __forceinline__ void fa_fwd_tile(const uint16_t* __restrict__ q,
                                             const uint16_t* __restrict__ vt, int S, int H,
                                             int Hkv, float sl2, uint16_t* __restrict__ out,
                                             float* __restrict__ lse, int qt, int h, int b,
-                                            uint16_t* lds) {
+                                            int Sk, uint16_t* lds) {
   constexpr int DS = DQ / 16;  // contraction steps over the query/key dims
   constexpr int DB = DV / 32;  // 32-row blocks of O^T
   constexpr int KS = KSLOTS<DQ>, VS = VSLOTS<BKT>;
@@ -156,7 +156,8 @@ __device__ __forceinline__ void fa_fwd_tile(const uint16_t* __restrict__ q,
   float m_run = -INFINITY, l_run = 0.0f;
 
   const int qlast = min(qt * BQ + BQ, S) - 1;   // last query of the workgroup
-  const int ntiles = qlast / BKT + 1;           // causal: keys <= qlast
+  // causal: keys <= qlast; keys >= Sk (right padding) are masked out
+  const int ntiles = min(qlast, Sk - 1) / BKT + 1;
   const int nsteps = (ntiles + G - 1) / G;      // group steps (tile u*G + grp)
   // Rows past S read a clamped (finite) row: those keys are masked out.
   auto issue = [&](int t, int buf) {
@@ -201,7 +202,7 @@ __device__ __forceinline__ void fa_fwd_tile(const uint16_t* __restrict__ q,
     const int k0 = t * BKT;
     if (t >= ntiles) {
       // this group has no tile in the last step
-    } else if (k0 + BKT - 1 <= q0 && k0 + BKT <= S) {
+    } else if (k0 + BKT - 1 <= q0 && k0 + BKT <= Sk) {
       // interior tile (every key visible to every query of this wave): the
       // blocks' MFMA chains are independent and nothing is masked
       f32x16 sacc[BKT / 32];
@@ -257,7 +258,7 @@ __device__ __forceinline__ void fa_fwd_tile(const uint16_t* __restrict__ q,
   #pragma unroll
       for (int jb = 0; jb < BKT / 32; ++jb) {
         const int kb0 = k0 + jb * 32;
-        if (kb0 > q0 + 31 || kb0 >= S) continue;  // wave-uniform
+        if (kb0 > q0 + 31 || kb0 >= Sk) continue;  // wave-uniform
         f32x16 sacc;
   #pragma unroll
         for (int v = 0; v < 16; ++v) sacc[v] = 0.0f;
@@ -266,11 +267,11 @@ __device__ __forceinline__ void fa_fwd_tile(const uint16_t* __restrict__ q,
           const bf16x8 a = as_bf16x8(*(const uint4*)(kl + (jb * 32 * KS + 2 * s) * 8));
           sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[s], sacc, 0, 0, 0);
         }
-        if (kb0 + 31 > q0 || kb0 + 31 >= S) {  // diagonal / ragged block: mask
+        if (kb0 + 31 > q0 || kb0 + 31 >= Sk) {  // diagonal / ragged block: mask
   #pragma unroll
           for (int v = 0; v < 16; ++v) {
             const int key = kb0 + (v >> 2) * 8 + g * 4 + (v & 3);
-            if (key > myq || key >= S) sacc[v] = -INFINITY;
+            if (key > myq || key >= Sk) sacc[v] = -INFINITY;
           }
         }
         float mt = sacc[0];
@@ -372,6 +373,12 @@ __device__ __forceinline__ void fa_fwd_tile(const uint16_t* __restrict__ q,
   }
 }
 
+// Valid keys of batch row b: all S, or (right padding) the first kvlen[b],
+// clamped to [1, S] so no bound can pass S.
+__device__ __forceinline__ int key_len(const int* __restrict__ kvlen, int b, int S) {
+  return kvlen ? min(max(kvlen[b], 1), S) : S;
+}
+
 // Causal work per 128-query tile grows with its index; with `paired` each
 // workgroup takes tiles i and n-1-i (equal total work per workgroup).
 __device__ __forceinline__ int pair_tile(int x, int it, int nq, int paired) {
@@ -383,7 +390,8 @@ template <int DQ, int DV, int BKT, int G>
 __global__ __launch_bounds__(NTH * G, G == 1 && BKT == 64 && DQ <= 128 ? 2 : 1) void fa_fwd(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ vt, int S, int H, int Hkv, float sl2,
-    uint16_t* __restrict__ out, float* __restrict__ lse, int nq, int paired) {
+    uint16_t* __restrict__ out, float* __restrict__ lse, int nq, int paired,
+    const int* __restrict__ kvlen) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[fwd_lds_elems<DQ, DV, BKT, G>()];
   const WgIdx w = wg_index(paired ? (nq + 1) / 2 : nq, H);
   for (int it = 0; it < 1 + paired; ++it) {
@@ -392,7 +400,8 @@ __global__ __launch_bounds__(NTH * G, G == 1 && BKT == 64 && DQ <= 128 ? 2 : 1) 
       if (qt == pair_tile(w.x, 0, nq, paired)) break;
       __syncthreads();  // the previous tile's output staging still reads LDS
     }
-    fa_fwd_tile<DQ, DV, BKT, G>(q, k, vt, S, H, Hkv, sl2, out, lse, qt, w.h, w.b, lds);
+    fa_fwd_tile<DQ, DV, BKT, G>(q, k, vt, S, H, Hkv, sl2, out, lse, qt, w.h, w.b,
+                                key_len(kvlen, w.b, S), lds);
   }
 }
 
@@ -449,7 +458,7 @@ __device__ __forceinline__ void fa_bwd_dq_tile(
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ o,
     const uint16_t* __restrict__ dout, const float* __restrict__ lse, int S, int H, int Hkv,
     float sl2, float scale, float* __restrict__ delta, uint16_t* __restrict__ dq, int qt, int h,
-    int b, uint16_t* lds) {
+    int b, int Sk, uint16_t* lds) {
   constexpr int DSQ = DQ / 16, DSV = DV / 16, DB = DQ / 32;
   constexpr int LTK = BKT * DQ, LTV = BKT * DV;  // bf16 per K / V tile
   constexpr int PERK = BKT * DQ / 8 / NTH, PERV = BKT * DV / 8 / NTH;  // 16-byte chunks per thread
@@ -499,7 +508,7 @@ __device__ __forceinline__ void fa_bwd_dq_tile(
     for (int e = 0; e < 16; ++e) dqacc[i][e] = 0.0f;
 
   const int qlast = min(qt * BQ + BQ, S) - 1;
-  const int ntiles = qlast / BKT + 1;
+  const int ntiles = min(qlast, Sk - 1) / BKT + 1;
   const int nsteps = (ntiles + G - 1) / G;
   // K and V tiles [key][D] (tswz layout) by direct global -> LDS copies;
   // rows past S read a clamped (finite) row, masked out below
@@ -543,7 +552,7 @@ __device__ __forceinline__ void fa_bwd_dq_tile(
       for (int e = 0; e < 8; ++e) {
         const int vv = 8 * hh + e;
         const int key = kb0 + (vv >> 2) * 8 + g * 4 + (vv & 3);
-        const bool keep = !edge || (key <= myq && key < S && qok);
+        const bool keep = !edge || (key <= myq && key < Sk && qok);
         const float p = keep ? __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[vv], sl2, -lq)) : 0.0f;
         ds[e] = p * (pacc[vv] - dl);
       }
@@ -571,8 +580,8 @@ __device__ __forceinline__ void fa_bwd_dq_tile(
 #pragma unroll
       for (int jb = 0; jb < BKT / 32; ++jb) {
         const int kb0 = k0 + jb * 32;
-        if (kb0 > q0 + 31 || kb0 >= S) continue;  // wave-uniform
-        block(ks, vs, jb, kb0, kb0 + 31 > q0 || kb0 + 31 >= S || q0 + 31 >= S);
+        if (kb0 > q0 + 31 || kb0 >= Sk) continue;  // wave-uniform
+        block(ks, vs, jb, kb0, kb0 + 31 > q0 || kb0 + 31 >= Sk || q0 + 31 >= S);
       }
     }
     __builtin_amdgcn_s_waitcnt(0);
@@ -627,7 +636,7 @@ __global__ __launch_bounds__(NTH * G, G == 1 && BKT == 64 && DQ <= 128 ? 2 : 1) 
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ o,
     const uint16_t* __restrict__ dout, const float* __restrict__ lse, int S, int H, int Hkv,
     float sl2, float scale, float* __restrict__ delta, uint16_t* __restrict__ dq, int nq,
-    int paired) {
+    int paired, const int* __restrict__ kvlen) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[G * 2 * BKT * (DQ + DV)];
   const WgIdx w = wg_index(paired ? (nq + 1) / 2 : nq, H);
   for (int it = 0; it < 1 + paired; ++it) {
@@ -637,7 +646,7 @@ __global__ __launch_bounds__(NTH * G, G == 1 && BKT == 64 && DQ <= 128 ? 2 : 1) 
       __syncthreads();
     }
     fa_bwd_dq_tile<DQ, DV, BKT, G>(q, k, v, o, dout, lse, S, H, Hkv, sl2, scale, delta, dq, qt,
-                                   w.h, w.b, lds);
+                                   w.h, w.b, key_len(kvlen, w.b, S), lds);
   }
 }
 
@@ -670,7 +679,7 @@ __device__ __forceinline__ void fa_bwd_dkdv_tile(
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, int S, int H, int Hkv,
     float sl2, float scale, float* __restrict__ dk_part, float* __restrict__ dv_part, int kt,
-    int h, int b, uint16_t* lds, float (*lse_s)[QT2], float (*dl_s)[QT2]) {
+    int h, int b, int Sk, uint16_t* lds, float (*lse_s)[QT2], float (*dl_s)[QT2]) {
   constexpr int DSQ = DQ / 16, DSV = DV / 16, DBQ = DQ / 32, DBV = DV / 32;
   constexpr int LK = KT2 * DQ, LV = KT2 * DV, LQ = QT2 * DQ, LG = QT2 * DV;
   constexpr int NW = dkdv_waves<DQ>(), NTH2 = 64 * NW, QH = 8 / NW;  // query halves per wave
@@ -802,7 +811,7 @@ __device__ __forceinline__ void fa_bwd_dkdv_tile(
           const int vv = 8 * hh + e;
           const int r = qh * 32 + (vv >> 2) * 8 + g * 4 + (vv & 3);  // query row in tile
           const int qq = qt * QT2 + r;
-          const bool keep = mykey <= qq && mykey < S && qq < S;
+          const bool keep = mykey <= qq && mykey < Sk && qq < S;
           const float p = keep ? __builtin_amdgcn_exp2f(sacc[vv] * sl2 - lse_s[buf][r]) : 0.0f;
           p8[e] = p;
           d8[e] = p * (pacc[vv] - dl_s[buf][r]);
@@ -896,7 +905,7 @@ __global__ __launch_bounds__(64 * dkdv_waves<DQ>(), dkdv_waves<DQ>() == 8 ? 2 : 
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, int S, int H, int Hkv,
     float sl2, float scale, float* __restrict__ dk_part, float* __restrict__ dv_part, int nk,
-    int paired) {
+    int paired, const int* __restrict__ kvlen) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[dkdv_lds_elems<DQ, DV>()];
   __shared__ float lse_s[2][QT2], dl_s[2][QT2];
   const WgIdx w = wg_index(paired ? (nk + 1) / 2 : nk, H);
@@ -907,7 +916,7 @@ __global__ __launch_bounds__(64 * dkdv_waves<DQ>(), dkdv_waves<DQ>() == 8 ? 2 : 
       __syncthreads();  // the previous tile's partial sums still occupy LDS
     }
     fa_bwd_dkdv_tile<DQ, DV>(q, k, v, dout, lse, delta, S, H, Hkv, sl2, scale, dk_part, dv_part,
-                             kt, w.h, w.b, lds, lse_s, dl_s);
+                             kt, w.h, w.b, key_len(kvlen, w.b, S), lds, lse_s, dl_s);
   }
 }
 
@@ -954,8 +963,8 @@ int64_t attn_workspace(int64_t B, int64_t S, int64_t H, int64_t Hkv, int64_t DQ,
 
 template <int DQ, int DV>
 int attn_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, int64_t B, int64_t S,
-             int64_t H, int64_t Hkv, float scale, uint16_t* out, float* lse, void* workspace,
-             hipStream_t s) {
+             int64_t H, int64_t Hkv, float scale, const int32_t* kvlen, uint16_t* out, float* lse,
+             void* workspace, hipStream_t s) {
   uint16_t* vt = (uint16_t*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
   const int64_t Sp = (S + 15) & ~15;
   transpose_heads<<<dim3((unsigned)st::cdiv(Sp, 64), (unsigned)st::cdiv(DV, 64),
@@ -970,18 +979,18 @@ int attn_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, int64_t B,
   const float sl2 = scale * LOG2E;
   if (paired)
     fa_fwd<DQ, DV, 64, (DQ <= 128 ? 2 : 1)><<<grid, NTH * (DQ <= 128 ? 2 : 1), 0, s>>>(
-        q, k, vt, (int)S, (int)H, (int)Hkv, sl2, out, lse, nq, paired);
+        q, k, vt, (int)S, (int)H, (int)Hkv, sl2, out, lse, nq, paired, kvlen);
   else
     fa_fwd<DQ, DV, 64, 1><<<grid, NTH, 0, s>>>(q, k, vt, (int)S, (int)H, (int)Hkv, sl2, out, lse,
-                                               nq, paired);
+                                               nq, paired, kvlen);
   return st::check_launch("fa_fwd");
 }
 
 template <int DQ, int DV>
 int attn_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* out,
              const float* lse, const uint16_t* dout, int64_t B, int64_t S, int64_t H, int64_t Hkv,
-             float scale, uint16_t* dq, uint16_t* dk, uint16_t* dv, void* workspace,
-             hipStream_t s) {
+             float scale, const int32_t* kvlen, uint16_t* dq, uint16_t* dk, uint16_t* dv,
+             void* workspace, hipStream_t s) {
   char* base = (char*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
   float* delta = (float*)base;
   float* dk_part = (float*)(base + (B * H * S * 4 + 255) / 256 * 256);
@@ -995,14 +1004,16 @@ int attn_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint
   dim3 g2((unsigned)((paired_k ? (nk + 1) / 2 : nk) * H * B));
   if (paired)
     fa_bwd_dq<DQ, DV, 64, (DQ <= 128 ? 2 : 1)><<<g1, NTH * (DQ <= 128 ? 2 : 1), 0, s>>>(
-        q, k, v, out, dout, lse, (int)S, (int)H, (int)Hkv, sl2, scale, delta, dq, nq, paired);
+        q, k, v, out, dout, lse, (int)S, (int)H, (int)Hkv, sl2, scale, delta, dq, nq, paired,
+        kvlen);
   else
     fa_bwd_dq<DQ, DV, 64, 1><<<g1, NTH, 0, s>>>(q, k, v, out, dout, lse, (int)S, (int)H,
-                                                (int)Hkv, sl2, scale, delta, dq, nq, paired);
+                                                (int)Hkv, sl2, scale, delta, dq, nq, paired, kvlen);
   int rc = st::check_launch("fa_bwd_dq");
   if (rc) return rc;
-  fa_bwd_dkdv<DQ, DV><<<g2, 64 * dkdv_waves<DQ>(), 0, s>>>(q, k, v, dout, lse, delta, (int)S, (int)H, (int)Hkv,
-                                          sl2, scale, dk_part, dv_part, nk, paired_k);
+  fa_bwd_dkdv<DQ, DV><<<g2, 64 * dkdv_waves<DQ>(), 0, s>>>(
+      q, k, v, dout, lse, delta, (int)S, (int)H, (int)Hkv, sl2, scale, dk_part, dv_part, nk,
+      paired_k, kvlen);
   rc = st::check_launch("fa_bwd_dkdv");
   if (rc) return rc;
   const int64_t n4 = B * Hkv * S * (DQ + DV) / 4;
@@ -1017,8 +1028,8 @@ bool dims_ok(int64_t DQ, int64_t DV) {
 
 int fwd_common(const char* name, const uint16_t* q, const uint16_t* k, const uint16_t* v,
                int64_t B, int64_t S, int64_t H, int64_t Hkv, int64_t DQ, int64_t DV, float scale,
-               uint16_t* out, float* lse, void* workspace, int64_t workspace_bytes,
-               st_stream_t stream) {
+               const int32_t* kv_len, uint16_t* out, float* lse, void* workspace,
+               int64_t workspace_bytes, st_stream_t stream) {
   ST_CHECK_ARG(B >= 0 && S >= 0 && H > 0 && Hkv > 0 && H % Hkv == 0, "%s: bad head counts", name);
   if (B == 0 || S == 0) return ST_OK;
   if (!dims_ok(DQ, DV))
@@ -1031,15 +1042,17 @@ int fwd_common(const char* name, const uint16_t* q, const uint16_t* k, const uin
   if (!workspace || workspace_bytes < need)
     return st::fail(ST_EWORKSPACE, "%s: needs %lld workspace bytes", name, (long long)need);
   hipStream_t s = (hipStream_t)stream;
-  if (DQ == 64) return attn_fwd<64, 64>(q, k, v, B, S, H, Hkv, scale, out, lse, workspace, s);
-  if (DQ == 128) return attn_fwd<128, 128>(q, k, v, B, S, H, Hkv, scale, out, lse, workspace, s);
-  return attn_fwd<192, 128>(q, k, v, B, S, H, Hkv, scale, out, lse, workspace, s);
+  if (DQ == 64)
+    return attn_fwd<64, 64>(q, k, v, B, S, H, Hkv, scale, kv_len, out, lse, workspace, s);
+  if (DQ == 128)
+    return attn_fwd<128, 128>(q, k, v, B, S, H, Hkv, scale, kv_len, out, lse, workspace, s);
+  return attn_fwd<192, 128>(q, k, v, B, S, H, Hkv, scale, kv_len, out, lse, workspace, s);
 }
 
 int bwd_common(const char* name, const uint16_t* q, const uint16_t* k, const uint16_t* v,
                const uint16_t* out, const float* lse, const uint16_t* dout, int64_t B, int64_t S,
-               int64_t H, int64_t Hkv, int64_t DQ, int64_t DV, float scale, uint16_t* dq,
-               uint16_t* dk, uint16_t* dv, void* workspace, int64_t workspace_bytes,
+               int64_t H, int64_t Hkv, int64_t DQ, int64_t DV, float scale, const int32_t* kv_len,
+               uint16_t* dq, uint16_t* dk, uint16_t* dv, void* workspace, int64_t workspace_bytes,
                st_stream_t stream) {
   ST_CHECK_ARG(B >= 0 && S >= 0 && H > 0 && Hkv > 0 && H % Hkv == 0, "%s: bad head counts", name);
   if (B == 0 || S == 0) return ST_OK;
@@ -1055,13 +1068,13 @@ int bwd_common(const char* name, const uint16_t* q, const uint16_t* k, const uin
     return st::fail(ST_EWORKSPACE, "%s: needs %lld workspace bytes", name, (long long)need);
   hipStream_t s = (hipStream_t)stream;
   if (DQ == 64)
-    return attn_bwd<64, 64>(q, k, v, out, lse, dout, B, S, H, Hkv, scale, dq, dk, dv, workspace,
-                            s);
+    return attn_bwd<64, 64>(q, k, v, out, lse, dout, B, S, H, Hkv, scale, kv_len, dq, dk, dv,
+                            workspace, s);
   if (DQ == 128)
-    return attn_bwd<128, 128>(q, k, v, out, lse, dout, B, S, H, Hkv, scale, dq, dk, dv,
+    return attn_bwd<128, 128>(q, k, v, out, lse, dout, B, S, H, Hkv, scale, kv_len, dq, dk, dv,
                               workspace, s);
-  return attn_bwd<192, 128>(q, k, v, out, lse, dout, B, S, H, Hkv, scale, dq, dk, dv, workspace,
-                            s);
+  return attn_bwd<192, 128>(q, k, v, out, lse, dout, B, S, H, Hkv, scale, kv_len, dq, dk, dv,
+                            workspace, s);
 }
 
 }  // namespace
@@ -1073,25 +1086,26 @@ extern "C" int64_t st_flash_attn_workspace_bytes(int64_t B, int64_t S, int64_t H
 
 extern "C" int st_flash_attn_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                                  int64_t B, int64_t S, int64_t H, int64_t Hkv, int64_t D,
-                                 float scale, uint16_t* out, float* lse, void* workspace,
-                                 int64_t workspace_bytes, st_stream_t stream) {
+                                 float scale, const int32_t* kv_len, uint16_t* out, float* lse,
+                                 void* workspace, int64_t workspace_bytes, st_stream_t stream) {
   if (D != 64 && D != 128)
     return st::fail(ST_EUNSUPPORTED, "st_flash_attn_fwd: head_dim %lld (64 or 128 only)",
                     (long long)D);
-  return fwd_common("st_flash_attn_fwd", q, k, v, B, S, H, Hkv, D, D, scale, out, lse, workspace,
-                    workspace_bytes, stream);
+  return fwd_common("st_flash_attn_fwd", q, k, v, B, S, H, Hkv, D, D, scale, kv_len, out, lse,
+                    workspace, workspace_bytes, stream);
 }
 
 extern "C" int st_flash_attn_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                                  const uint16_t* out, const float* lse, const uint16_t* dout,
                                  int64_t B, int64_t S, int64_t H, int64_t Hkv, int64_t D,
-                                 float scale, uint16_t* dq, uint16_t* dk, uint16_t* dv,
-                                 void* workspace, int64_t workspace_bytes, st_stream_t stream) {
+                                 float scale, const int32_t* kv_len, uint16_t* dq, uint16_t* dk,
+                                 uint16_t* dv, void* workspace, int64_t workspace_bytes,
+                                 st_stream_t stream) {
   if (D != 64 && D != 128)
     return st::fail(ST_EUNSUPPORTED, "st_flash_attn_bwd: head_dim %lld (64 or 128 only)",
                     (long long)D);
-  return bwd_common("st_flash_attn_bwd", q, k, v, out, lse, dout, B, S, H, Hkv, D, D, scale, dq,
-                    dk, dv, workspace, workspace_bytes, stream);
+  return bwd_common("st_flash_attn_bwd", q, k, v, out, lse, dout, B, S, H, Hkv, D, D, scale,
+                    kv_len, dq, dk, dv, workspace, workspace_bytes, stream);
 }
 
 extern "C" int64_t st_mla_attn_workspace_bytes(int64_t B, int64_t S, int64_t H, int64_t DQ,
@@ -1101,17 +1115,18 @@ extern "C" int64_t st_mla_attn_workspace_bytes(int64_t B, int64_t S, int64_t H, 
 
 extern "C" int st_mla_attn_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                                int64_t B, int64_t S, int64_t H, int64_t DQ, int64_t DV,
-                               float scale, uint16_t* out, float* lse, void* workspace,
-                               int64_t workspace_bytes, st_stream_t stream) {
-  return fwd_common("st_mla_attn_fwd", q, k, v, B, S, H, H, DQ, DV, scale, out, lse, workspace,
-                    workspace_bytes, stream);
+                               float scale, const int32_t* kv_len, uint16_t* out, float* lse,
+                               void* workspace, int64_t workspace_bytes, st_stream_t stream) {
+  return fwd_common("st_mla_attn_fwd", q, k, v, B, S, H, H, DQ, DV, scale, kv_len, out, lse,
+                    workspace, workspace_bytes, stream);
 }
 
 extern "C" int st_mla_attn_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                                const uint16_t* out, const float* lse, const uint16_t* dout,
                                int64_t B, int64_t S, int64_t H, int64_t DQ, int64_t DV,
-                               float scale, uint16_t* dq, uint16_t* dk, uint16_t* dv,
-                               void* workspace, int64_t workspace_bytes, st_stream_t stream) {
-  return bwd_common("st_mla_attn_bwd", q, k, v, out, lse, dout, B, S, H, H, DQ, DV, scale, dq, dk,
-                    dv, workspace, workspace_bytes, stream);
+                               float scale, const int32_t* kv_len, uint16_t* dq, uint16_t* dk,
+                               uint16_t* dv, void* workspace, int64_t workspace_bytes,
+                               st_stream_t stream) {
+  return bwd_common("st_mla_attn_bwd", q, k, v, out, lse, dout, B, S, H, H, DQ, DV, scale, kv_len,
+                    dq, dk, dv, workspace, workspace_bytes, stream);
 }

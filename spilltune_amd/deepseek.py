@@ -30,7 +30,7 @@ import math
 import torch
 
 from . import moe, ops
-from .dense import CausalMask
+from .dense import CausalMask, key_lengths
 
 ATTENTION_TARGETS_Q_LORA = ("self_attn.q_a_proj", "self_attn.q_b_proj",
                             "self_attn.kv_a_proj_with_mqa", "self_attn.kv_b_proj",
@@ -96,19 +96,18 @@ def attention_scale(nope: int, rope_dim: int, rope: dict) -> float:
 def positions_and_masks(valid: torch.Tensor, *, rope: dict, rope_dim: int, device,
                         dtype=torch.bfloat16):
     """bf16 (cos, sin) [B, S, rope_dim] scaled by the YaRN amplitude and the
-    causal mask marker (deepseek.py:234-243); right padding is rejected."""
+    causal mask marker with the valid prefix lengths of right-padded rows
+    (deepseek.py:234-243)."""
     if valid.dtype != torch.bool or valid.ndim != 2 or valid.shape[1] < 1:
-        raise ValueError("unsupported_capability: mask must be 2D bool")
-    if not bool(valid.all()):
-        raise ValueError("unsupported_capability: right-padding masks are not supported on the "
-                         "HIP path")
+        raise ValueError("unsupported_deepseek: invalid mask/context")
+    lengths = key_lengths(valid, device, "unsupported_deepseek: all-valid/right padding only")
     batch, length = valid.shape
     inverse, amplitude = rope_parameters(rope, rope_dim, device)
     pos = torch.arange(length, device=device).expand(batch, -1)
     phase = (inverse[None, :, None].expand(batch, -1, 1) @ pos[:, None].float()).transpose(1, 2)
     phase = torch.cat((phase, phase), -1)
     return ((phase.cos() * amplitude).to(dtype), (phase.sin() * amplitude).to(dtype)), \
-        CausalMask(batch, length)
+        CausalMask(batch, length, lengths)
 
 
 def _weight(weights, name):
@@ -158,7 +157,8 @@ def deepseek_block(hidden_states, position_embeddings, attention_mask, *, parame
     kv = ops.q4_lora_linear(kvn, _weight(w, "self_attn.kv_b_proj"), [lora_kvb])
     Q, K, V = ops.mla_rope(q, kv, comp, cos, sin, batch=B, seq=S, heads=heads, nope=nope,
                            rope=rope, v_dim=vdim, kv_rank=kv_rank, interleave=c["interleave"])
-    attended = ops.mla_attention(Q, K, V, c["attention_scale"]).reshape(B * S, heads * vdim)
+    kv_len = attention_mask.lengths if attention_mask is not None else None
+    attended = ops.mla_attention(Q, K, V, c["attention_scale"], kv_len).reshape(B * S, heads * vdim)
     h1 = ops.q4_lora_linear(attended, _weight(w, "self_attn.o_proj"), [lora_o], residual=residual)
     h1, xn2 = ops.rms_norm_residual(h1, w["post_attention_layernorm.weight"], c["eps"])
     if not c["moe"]:  # dense layer: residual + down(silu(gate) * up)

@@ -13,14 +13,14 @@ no reference to slot memory.  Differences in *how*, not *what*:
   the concatenated rows, and the residual adds run in the o/down epilogues;
 * ``qk_norm`` (Qwen3): each head of q and k is RMS-normalised over head_dim
   by the HIP RMSNorm kernel before RoPE;
-* ``attention_mask`` is a :class:`CausalMask` marker (all-valid causal
-  attention, the only mask the engine builds for unpadded rows) -- the mask
-  is applied structurally by the softmax kernel, exactly as adding
-  ``finfo(bf16).min`` does (exp underflows to 0).
+* ``attention_mask`` is a :class:`CausalMask` marker: causal attention with
+  each row's keys past its valid prefix masked (right padding; none for the
+  all-valid rows the engine builds) -- applied structurally by the softmax
+  kernel, exactly as adding ``finfo(bf16).min`` does (exp underflows to 0).
 """
 from __future__ import annotations
 
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 
 import torch
 
@@ -29,25 +29,40 @@ from . import ops
 
 @dataclass(frozen=True)
 class CausalMask:
-    """All-valid causal additive mask of shape [batch, 1, S, S] (dense.py:246-247)."""
+    """The additive mask of dense.py:246-247, [batch, 1, S, S]: causal, and
+    with right padding the keys past each row's valid prefix blocked.
+    ``lengths`` is None when every row is all valid, else the device int32
+    [batch] prefix lengths."""
     batch: int
     length: int
+    lengths: torch.Tensor | None = field(default=None, compare=False)
+
+
+def key_lengths(valid: torch.Tensor, device, what: str = "unsupported_capability: only "
+                "all-valid or right-padding masks"):
+    """None for all-valid rows, else each row's valid prefix length (device
+    int32 [batch]); rows must start valid and never turn valid again after a
+    padded position (dense.py:236-237)."""
+    if not bool(valid[:, 0].all()) or bool(((~valid[:, :-1]) & valid[:, 1:]).any()):
+        raise ValueError(what)
+    if bool(valid.all()):
+        return None
+    return valid.sum(1).to(device=device, dtype=torch.int32)
 
 
 def positions_and_masks(valid: torch.Tensor, *, head_dim: int, theta: float, device,
                         dtype=torch.bfloat16):
     """Rotary tables (bf16 cos/sin [B,S,D]) and the causal mask marker
-    (dense.py:232-248).  Right padding is rejected (unsupported here)."""
+    (dense.py:232-248), with the valid prefix lengths of right-padded rows."""
     if valid.dtype != torch.bool or valid.ndim != 2 or valid.shape[1] < 1:
         raise ValueError("unsupported_capability: mask must be 2D bool")
-    if not bool(valid.all()):
-        raise ValueError("unsupported_capability: right-padding masks are not supported on the HIP path")
+    lengths = key_lengths(valid, device)
     batch, length = valid.shape
     positions = torch.arange(length, device=device).expand(batch, -1)
     inv = 1.0 / theta ** (torch.arange(0, head_dim, 2, device=device).float() / head_dim)
     freq = (inv[None, :, None].expand(batch, -1, 1) @ positions[:, None].float()).transpose(1, 2)
     phase = torch.cat((freq, freq), -1)
-    return (phase.cos().to(dtype), phase.sin().to(dtype)), CausalMask(batch, length)
+    return (phase.cos().to(dtype), phase.sin().to(dtype)), CausalMask(batch, length, lengths)
 
 
 def _weight(weights, name):
@@ -104,7 +119,9 @@ def dense_block(hidden_states, position_embeddings, attention_mask, *, heads, kv
         v = ops.rope_heads(ops.q4_lora_linear(xn, wv, [lora_v]), 0, B, S, kv_heads, head_dim, cos,
                            sin, rotate=False)
 
-    attended = ops.causal_attention(q, k, v, ops.attention_scale(head_dim)).reshape(B * S, heads * head_dim)
+    kv_len = attention_mask.lengths if attention_mask is not None else None
+    attended = ops.causal_attention(q, k, v, ops.attention_scale(head_dim),
+                                    kv_len).reshape(B * S, heads * head_dim)
     h1 = ops.q4_lora_linear(attended, _weight(weights, "self_attn.o_proj"), [lora_o], residual=residual)
 
     h1, xn2 = ops.rms_norm_residual(h1, weights["post_attention_layernorm.weight"], eps)

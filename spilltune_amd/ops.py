@@ -790,13 +790,24 @@ def rope_heads(y, col0, B, S, heads, D, cos, sin, rotate=True):
 
 
 # ----------------------------------------------------------------- attention
+def _kv_len_arg(kv_len, B, dev):
+    """Device int32 [B] of valid key counts (right padding) or None."""
+    if kv_len is None:
+        return None
+    if kv_len.dtype != torch.int32 or kv_len.device != dev or tuple(kv_len.shape) != (B,):
+        raise ValueError("unsupported_capability: kv_len must be an int32 [batch] tensor on the "
+                         "attention's device")
+    return kv_len.contiguous()
+
+
 class _CausalAttention(torch.autograd.Function):
     """GQA causal attention of dense.py:142-148 as flash attention: no
     [S, S] scores in memory; the backward recomputes probabilities from the
-    saved base-2 log-sum-exp."""
+    saved base-2 log-sum-exp.  ``kv_len`` masks the keys past each row's
+    valid prefix (right padding, dense.py:237-246)."""
 
     @staticmethod
-    def forward(ctx, q, k, v, scale):
+    def forward(ctx, q, k, v, scale, kv_len):
         B, H, S, D = q.shape
         Hkv = k.shape[1]
         dev = q.device
@@ -804,10 +815,10 @@ class _CausalAttention(torch.autograd.Function):
         lse = torch.empty((B, H, S), dtype=_F32, device=dev)
         ws = _ws.get(dev, _lib.query("st_flash_attn_workspace_bytes", B, S, H, Hkv, D, 0))
         _lib.call("st_flash_attn_fwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), B, S, H, Hkv, D,
-                  float(scale), _lib.ptr(out), _lib.ptr(lse), _lib.ptr(ws),
+                  float(scale), _lib.ptr(kv_len), _lib.ptr(out), _lib.ptr(lse), _lib.ptr(ws),
                   0 if ws is None else ws.numel(), _lib.stream_handle(dev))
         ctx.save_for_backward(q, k, v, out, lse)
-        ctx.scale = scale
+        ctx.scale, ctx.kv_len = scale, kv_len
         return out
 
     @staticmethod
@@ -820,15 +831,17 @@ class _CausalAttention(torch.autograd.Function):
         dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
         ws = _ws.get(dev, _lib.query("st_flash_attn_workspace_bytes", B, S, H, Hkv, D, 1))
         _lib.call("st_flash_attn_bwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(out),
-                  _lib.ptr(lse), _lib.ptr(dout), B, S, H, Hkv, D, float(ctx.scale), _lib.ptr(dq),
-                  _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(ws), 0 if ws is None else ws.numel(),
-                  _lib.stream_handle(dev))
-        return dq, dk, dv, None
+                  _lib.ptr(lse), _lib.ptr(dout), B, S, H, Hkv, D, float(ctx.scale),
+                  _lib.ptr(ctx.kv_len), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(ws),
+                  0 if ws is None else ws.numel(), _lib.stream_handle(dev))
+        return dq, dk, dv, None, None
 
 
-def causal_attention(q, k, v, scale):
-    """q [B,H,S,D], k/v [B,Hkv,S,D] -> token-major [B,S,H*D]."""
-    return _CausalAttention.apply(q.contiguous(), k.contiguous(), v.contiguous(), float(scale))
+def causal_attention(q, k, v, scale, kv_len=None):
+    """q [B,H,S,D], k/v [B,Hkv,S,D] -> token-major [B,S,H*D]; ``kv_len``
+    (int32 [B] on the device, or None) gives each row's valid key count."""
+    return _CausalAttention.apply(q.contiguous(), k.contiguous(), v.contiguous(), float(scale),
+                                  _kv_len_arg(kv_len, q.shape[0], q.device))
 
 
 # ----------------------------------------------------------------- MLA (DeepSeek-V3)
@@ -889,10 +902,11 @@ def mla_rope(q, kv, comp, cos, sin, *, batch, seq, heads, nope, rope, v_dim, kv_
 
 class _MLAAttention(torch.autograd.Function):
     """Causal attention with query/key heads of DQ and value heads of DV
-    (deepseek.py:151-153) on the flash kernels."""
+    (deepseek.py:151-153) on the flash kernels; ``kv_len`` as in
+    :func:`causal_attention`."""
 
     @staticmethod
-    def forward(ctx, q, k, v, scale):
+    def forward(ctx, q, k, v, scale, kv_len):
         B, H, S, DQ = q.shape
         DV = v.shape[-1]
         dev = q.device
@@ -900,10 +914,10 @@ class _MLAAttention(torch.autograd.Function):
         lse = torch.empty((B, H, S), dtype=_F32, device=dev)
         ws = _ws.get(dev, _lib.query("st_mla_attn_workspace_bytes", B, S, H, DQ, DV, 0))
         _lib.call("st_mla_attn_fwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), B, S, H, DQ, DV,
-                  float(scale), _lib.ptr(out), _lib.ptr(lse), _lib.ptr(ws),
+                  float(scale), _lib.ptr(kv_len), _lib.ptr(out), _lib.ptr(lse), _lib.ptr(ws),
                   0 if ws is None else ws.numel(), _lib.stream_handle(dev))
         ctx.save_for_backward(q, k, v, out, lse)
-        ctx.scale = scale
+        ctx.scale, ctx.kv_len = scale, kv_len
         return out
 
     @staticmethod
@@ -916,15 +930,16 @@ class _MLAAttention(torch.autograd.Function):
         dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
         ws = _ws.get(dev, _lib.query("st_mla_attn_workspace_bytes", B, S, H, DQ, DV, 1))
         _lib.call("st_mla_attn_bwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(out),
-                  _lib.ptr(lse), _lib.ptr(dout), B, S, H, DQ, DV, float(ctx.scale), _lib.ptr(dq),
-                  _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(ws), 0 if ws is None else ws.numel(),
-                  _lib.stream_handle(dev))
-        return dq, dk, dv, None
+                  _lib.ptr(lse), _lib.ptr(dout), B, S, H, DQ, DV, float(ctx.scale),
+                  _lib.ptr(ctx.kv_len), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(ws),
+                  0 if ws is None else ws.numel(), _lib.stream_handle(dev))
+        return dq, dk, dv, None, None
 
 
-def mla_attention(q, k, v, scale):
+def mla_attention(q, k, v, scale, kv_len=None):
     """q, k [B,H,S,DQ], v [B,H,S,DV] -> token-major [B,S,H*DV]."""
-    return _MLAAttention.apply(q.contiguous(), k.contiguous(), v.contiguous(), float(scale))
+    return _MLAAttention.apply(q.contiguous(), k.contiguous(), v.contiguous(), float(scale),
+                               _kv_len_arg(kv_len, q.shape[0], q.device))
 
 
 # ----------------------------------------------------------------- SwiGLU

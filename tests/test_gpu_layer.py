@@ -65,7 +65,7 @@ def oracle_weights(block, oracle_codec):
 
 
 def run_case(cfg, seed, oracle_codec, codec="nf4-g128", streamed=False, targets=PROJ,
-             qk_norm=False):
+             qk_norm=False, valid=None):
     block, _ = make_layer(cfg, seed, codec, targets=targets, qk_norm=qk_norm)
     g = torch.Generator().manual_seed(seed + 1)
     B, S, H = cfg["B"], cfg["S"], cfg["H"]
@@ -77,7 +77,7 @@ def run_case(cfg, seed, oracle_codec, codec="nf4-g128", streamed=False, targets=
            for n, p in block.adapters.items()}
     kw = dict(heads=cfg["heads"], kv_heads=cfg["kv"], head_dim=cfg["D"], eps=cfg["eps"],
               qk_norm=qk_norm)
-    out_ref, gh_ref = OL.streaming_step(hidden, (cos, sin), OL.causal_mask(B, S, BF), dy,
+    out_ref, gh_ref = OL.streaming_step(hidden, (cos, sin), OL.causal_mask(B, S, BF, valid), dy,
                                         weights=oracle_weights(block, oracle_codec), loras=lor, cfg=kw)
     # ---- HIP path through the recompute driver
     dev = torch.device("cuda:0")
@@ -88,7 +88,9 @@ def run_case(cfg, seed, oracle_codec, codec="nf4-g128", streamed=False, targets=
         session = slots.ResidentSession([block], dev)
     h = hidden.to(dev).requires_grad_(True)
     with session.run():
-        out = streaming_block(h, (cos.to(dev), sin.to(dev)), CausalMask(B, S), block.functional,
+        lengths = None if valid is None else valid.sum(1).to(device=dev, dtype=torch.int32)
+        out = streaming_block(h, (cos.to(dev), sin.to(dev)), CausalMask(B, S, lengths),
+                              block.functional,
                               block.kwargs, session.reloader(block), block.adapters, block.index)
         out.backward(dy.to(dev))
     torch.cuda.synchronize()
@@ -140,6 +142,31 @@ def test_layer_step_lora_ranks_vs_oracle(oracle_codec, r):
     takes, so the functional runs q, k and v one by one; gate|up fused at
     64)."""
     _assert(run_case(dict(GQA, r=r, alpha=2.0 * r), 60 + r, oracle_codec))
+
+
+def test_right_padded_batch_layer_step_vs_oracle(oracle_codec):
+    """Right-padded rows (dense.py:237-246, the reference's additive
+    finfo.min mask in the oracle): every output row, padded ones included,
+    and every gradient."""
+    valid = torch.ones(3, 100, dtype=torch.bool)
+    valid[1, 61:] = False
+    valid[2, 1:] = False
+    _assert(run_case(dict(GQA, B=3, S=100), 26, oracle_codec, valid=valid))
+
+
+def test_positions_and_masks_right_padding():
+    """The lengths the mask marker carries, and the reference's rejections
+    (a leading padded position, a valid position after padding)."""
+    from spilltune_amd.dense import positions_and_masks
+    valid = torch.tensor([[True] * 5, [True, True, False, False, False]])
+    _, mask = positions_and_masks(valid, head_dim=8, theta=10000.0, device="cuda:0")
+    assert mask.lengths.tolist() == [5, 2] and mask.lengths.dtype == torch.int32
+    _, mask = positions_and_masks(torch.ones(2, 5, dtype=torch.bool), head_dim=8, theta=1e4,
+                                  device="cuda:0")
+    assert mask.lengths is None
+    for bad in ([[False, True]], [[True, False, True]]):
+        with pytest.raises(ValueError, match="unsupported_capability"):
+            positions_and_masks(torch.tensor(bad), head_dim=8, theta=1e4, device="cuda:0")
 
 
 def test_odd_sequence_length_layer_step_vs_oracle(oracle_codec):
