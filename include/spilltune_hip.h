@@ -85,7 +85,9 @@ int st_dequant4(const uint8_t* payload, const float* scales, int64_t numel, int3
  * straddle W's rows: each packed word reads its own group's scale).  K % 8 ==
  * 0.  `workspace` is not used (the query returns 0).
  * `t` = x_f32 A_cat^T from st_lora_gemm ([M, nseg*rank] fp32) or NULL for no
- * LoRA; 1 <= rank and nseg * rank <= 64 (any parity).
+ * LoRA; any rank >= 1 (up to 65536 T columns).  Up to 64 T columns the
+ * epilogue stages t and lora_b in the tile's LDS; wider ones it reads from
+ * global memory (L2) in the same order, with the same result.
  * nseg/seg_end describe N-concatenated projections (fused q|k|v, gate|up):
  * column n belongs to segment s = #{seg_end[i] <= n}; segment ends must be
  * multiples of 32.  nseg = 1 with seg_end[0] = N for a single projection.
@@ -105,7 +107,8 @@ int st_q4_linear_fwd(const uint16_t* x, int64_t M, int64_t K, int64_t ldx,
  *   dx[m,k] = bf16( bf16(sum_n dy[m,n] W[n,k]) + bf16(sum_j dt[m,j] lora_a[j,k]) )
  * with dt = lora_scale * dy_f32 B ([M, lora_k] fp32, from st_lora_bwd_dy;
  * N-concatenated projections stack their dt columns and lora_a rows) or
- * dt == NULL for no LoRA term; 1 <= lora_k <= 64.  W [N,K] as above,
+ * dt == NULL for no LoRA term; 1 <= lora_k <= 65536 (above 64 the epilogue
+ * reads dt and lora_a from global memory).  W [N,K] as above,
  * dequantised into LDS in its natural orientation and read transposed.
  */
 int64_t st_q4_linear_dgrad_workspace_bytes(int64_t M, int64_t N, int64_t K);
@@ -172,7 +175,8 @@ int st_lora_gemm_noalloc(int64_t Mo, int64_t No, int64_t Kc,
  * fp32 (ldt; the forward's x_f32 A_cat^T), dt [M, nseg*r] (lddt), db [N, r].
  * All 2*nseg products run in one launch, their split-K sums in one more (fixed
  * order).  nseg <= 8, r <= 64; segment starts and widths must be multiples of
- * 8 (the workspace query returns 0 otherwise: use st_lora_gemm per product).
+ * 8 (the workspace query returns 0 otherwise, a rank above 64 included: use
+ * st_lora_gemm per product).
  * db == NULL runs the dt products only (db formed later, e.g. by st_rk_batch).
  */
 int64_t st_lora_bwd_dy_workspace_bytes(int64_t M, int64_t N, int32_t rank, int32_t nseg,
@@ -468,7 +472,8 @@ int st_q4_grouped_dgrad_swiglu(const uint16_t* dy, int64_t lddy, int64_t rows, i
  *            * s[e(r)*s_gstride + (z*seg_len + k)*ssk + j*ssj]
  * grads form: out[e*o_gstride + (z*seg_len + m)*so_m + j*so_j] (+)= alpha *
  *            sum_{r in e} g[row(r), z*seg_len + m] * s[r*ssk + (z*R + j)*ssj]
- * for segments z < nseg, R <= 64; row(r) = gather[r] (NULL: r), bounded by
+ * for segments z < nseg, any R >= 1 (64 output columns per launch); row(r) =
+ * gather[r] (NULL: r), bounded by
  * g_rows.  The grads form writes every expert (zero rows -> 0). */
 int st_moe_lora_rows(int64_t rows, int32_t R, int64_t seg_len, int32_t nseg, const uint16_t* g,
                      int64_t ldg, int64_t g_rows, const int32_t* gather, const float* s,

@@ -307,18 +307,18 @@ int lora_gemm_impl(int64_t Mo, int64_t No, int64_t Kc, const void* a, int32_t a_
     return st::check_launch("lora_reduce");
   }
   ST_CHECK_ARG(a && b, "st_lora_gemm: NULL operand");
-  // fp32-MFMA path: the bf16 operand is contiguous along one of its dims and
-  // the fp32 operand has <= 64 columns of the output.
+  // fp32-MFMA path: the bf16 operand is contiguous along one of its dims; the
+  // fp32 operand's output columns run 64 at a time (one launch pair each).
   {
     const uint16_t* G = nullptr;
     const float* S = nullptr;
     int64_t ldg = 0, ssk = 0, ssj = 0, big = 0, small = 0, so_m = 0, so_j = 0;
     int col = -1;
-    if (a_dtype == ST_DTYPE_BF16 && b_dtype == ST_DTYPE_F32 && No <= 64) {
+    if (a_dtype == ST_DTYPE_BF16 && b_dtype == ST_DTYPE_F32) {
       G = (const uint16_t*)a; S = (const float*)b; ssk = sbk; ssj = sbn;
       big = Mo; small = No; so_m = ldo; so_j = 1;
       if (sak == 1) { col = 0; ldg = sam; } else if (sam == 1) { col = 1; ldg = sak; }
-    } else if (a_dtype == ST_DTYPE_F32 && b_dtype == ST_DTYPE_BF16 && Mo <= 64) {
+    } else if (a_dtype == ST_DTYPE_F32 && b_dtype == ST_DTYPE_BF16) {
       // out^T[n, m] = sum_k b(k, n) a(m, k)
       G = (const uint16_t*)b; S = (const float*)a; ssk = sak; ssj = sam;
       big = No; small = Mo; so_m = 1; so_j = ldo;
@@ -330,30 +330,39 @@ int lora_gemm_impl(int64_t Mo, int64_t No, int64_t Kc, const void* a, int32_t a_
     const bool vec = ((uintptr_t)G & 15u) == 0 && ldg % 8 == 0 && (col ? big : Kc) % 8 == 0 &&
                      ssk >= 0 && ssj >= 0 && g_bytes < (1ll << 31) && s_bytes < (1ll << 31);
     if (col >= 0 && vec) {
-      int ks = rk_ksplit(big, Kc);
-      int64_t need = (int64_t)ks * big * small * 4;
+      const int ks = rk_ksplit(big, Kc);
+      const int64_t need = (int64_t)ks * big * (small < 64 ? small : 64) * 4;
       if (!workspace || workspace_bytes < need)
         return st::fail(ST_EWORKSPACE, "st_lora_gemm: needs %lld workspace bytes", (long long)need);
-      int64_t klen = st::cdiv(st::cdiv(Kc, ks), RK_BK) * RK_BK;
-      dim3 grid((unsigned)st::cdiv(big, RK_BM), (unsigned)ks);
+      const int64_t klen = st::cdiv(st::cdiv(Kc, ks), RK_BK) * RK_BK;
+      const dim3 grid((unsigned)st::cdiv(big, RK_BM), (unsigned)ks);
       float* part = (float*)workspace;
-      auto go = [&](auto kern) {
-        kern<<<grid, NTH, 0, s>>>(big, small, Kc, G, ldg, g_bytes, S, ssk, ssj, s_bytes, klen,
-                                  part);
-      };
-      const bool sk1 = ssk == 1, nb2 = small > 32;
-      if (col) {
-        if (sk1) nb2 ? go(lora_rk<true, true, 2>) : go(lora_rk<true, true, 1>);
-        else nb2 ? go(lora_rk<true, false, 2>) : go(lora_rk<true, false, 1>);
-      } else {
-        if (sk1) nb2 ? go(lora_rk<false, true, 2>) : go(lora_rk<false, true, 1>);
-        else nb2 ? go(lora_rk<false, false, 2>) : go(lora_rk<false, false, 1>);
+      // more than 64 fp32 columns: chunks of 64 in turn (the partials buffer
+      // is reused; the stream orders the chunks)
+      for (int64_t c0 = 0; c0 < small; c0 += 64) {
+        const int64_t sc = small - c0 < 64 ? small - c0 : 64;
+        const float* Sc = S + c0 * ssj;
+        const int64_t sc_bytes = ((Kc - 1) * ssk + (sc - 1) * ssj + 1) * 4;
+        auto go = [&](auto kern) {
+          kern<<<grid, NTH, 0, s>>>(big, sc, Kc, G, ldg, g_bytes, Sc, ssk, ssj, sc_bytes, klen,
+                                    part);
+        };
+        const bool sk1 = ssk == 1, nb2 = sc > 32;
+        if (col) {
+          if (sk1) nb2 ? go(lora_rk<true, true, 2>) : go(lora_rk<true, true, 1>);
+          else nb2 ? go(lora_rk<true, false, 2>) : go(lora_rk<true, false, 1>);
+        } else {
+          if (sk1) nb2 ? go(lora_rk<false, true, 2>) : go(lora_rk<false, true, 1>);
+          else nb2 ? go(lora_rk<false, false, 2>) : go(lora_rk<false, false, 1>);
+        }
+        int rc = st::check_launch("lora_rk");
+        if (rc) return rc;
+        lora_rk_reduce<<<(unsigned)st::cdiv(big * sc, NTH), NTH, 0, s>>>(
+            big, sc, ks, part, alpha, out + c0 * so_j, so_m, so_j, accumulate);
+        rc = st::check_launch("lora_rk_reduce");
+        if (rc) return rc;
       }
-      int rc = st::check_launch("lora_rk");
-      if (rc) return rc;
-      lora_rk_reduce<<<(unsigned)st::cdiv(big * small, NTH), NTH, 0, s>>>(
-          big, small, ks, part, alpha, out, so_m, so_j, accumulate);
-      return st::check_launch("lora_rk_reduce");
+      return ST_OK;
     }
   }
   int ks = ksplit_for(Mo, No, Kc);
@@ -510,7 +519,7 @@ int check_segments(int64_t N, int32_t nseg, const int64_t* seg_end) {
 
 extern "C" int64_t st_lora_bwd_dy_workspace_bytes(int64_t M, int64_t N, int32_t rank,
                                                   int32_t nseg, const int64_t* seg_end) {
-  if (M <= 0 || N <= 0 || rank <= 0 || check_segments(N, nseg, seg_end)) return 0;
+  if (M <= 0 || N <= 0 || rank <= 0 || rank > 64 || check_segments(N, nseg, seg_end)) return 0;
   RkBatch b;
   const int64_t floats = plan_bwd_dy(b, false, nullptr, M, N, N, nullptr, nullptr,
                                      (int64_t)nseg * rank, rank, nseg, seg_end, 1.0f, nullptr, 0,

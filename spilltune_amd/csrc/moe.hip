@@ -484,7 +484,8 @@ constexpr int GK_LD = GK_BK + 8;
 
 struct GroupedRk {
   int64_t rows;     // permuted rows
-  int64_t R;        // output columns per segment (<= 64)
+  int64_t R;        // output columns of this launch (<= 64)
+  int64_t Rseg;     // output columns per segment (segment z starts at z * Rseg)
   int64_t seg_len;  // ROW: contraction per segment; COL: G columns per segment
   const uint16_t* G;
   int64_t ldg, g_rows;
@@ -525,7 +526,7 @@ __global__ __launch_bounds__(NTH) void grouped_rk(GroupedRk a) {
     if (kb < 0) kb = 0;
     if (ke > a.rows) ke = a.rows;
     gcol0 = (int64_t)z * a.seg_len;
-    S += (int64_t)z * a.R * a.ssj;
+    S += (int64_t)z * a.Rseg * a.ssj;
   }
   const int nb = a.R > 32 ? 2 : 1;
   const int RP = nb * 32;
@@ -656,7 +657,7 @@ __global__ __launch_bounds__(NTH) void grouped_rk(GroupedRk a) {
   int64_t om, oj;
   if (!COL) {
     om = a.so_m; oj = a.so_j;
-    dst += (int64_t)z * a.R * a.so_j;
+    dst += (int64_t)z * a.Rseg * a.so_j;
   } else {
     om = a.so_m; oj = a.so_j;
     dst += grp * a.o_gstride + (int64_t)z * a.seg_len * a.so_m;
@@ -705,7 +706,7 @@ __global__ __launch_bounds__(st::RK_NTH) void grouped_rk_stream(GroupedRk a, int
     ke = a.offsets[grp + 1];
     if (kb < 0) kb = 0;
     if (ke > a.rows) ke = a.rows;
-    S += (int64_t)z * a.R * a.ssj;
+    S += (int64_t)z * a.Rseg * a.ssj;
   }
   f32x16 acc[NB];
 #pragma unroll
@@ -731,7 +732,7 @@ __global__ __launch_bounds__(st::RK_NTH) void grouped_rk_stream(GroupedRk a, int
   }
   float* dst = a.out;
   if (!COL)
-    dst += (int64_t)z * a.R * a.so_j;
+    dst += (int64_t)z * a.Rseg * a.so_j;
   else
     dst += grp * a.o_gstride + (int64_t)z * a.seg_len * a.so_m;
 #pragma unroll
@@ -894,24 +895,31 @@ extern "C" int st_moe_lora_rows(int64_t rows, int32_t R, int64_t seg_len, int32_
                                 const int32_t* gather, const float* s, int64_t ssk, int64_t ssj,
                                 int64_t s_gstride, const int32_t* offsets, int32_t groups,
                                 float alpha, float* out, int64_t ldo, st_stream_t stream) {
-  ST_CHECK_ARG(rows >= 0 && R > 0 && R <= 64 && seg_len > 0 && nseg > 0 && groups > 0,
-               "st_moe_lora_rows: need 0 < R <= 64");
+  ST_CHECK_ARG(rows >= 0 && R > 0 && seg_len > 0 && nseg > 0 && groups > 0,
+               "st_moe_lora_rows: need 0 < R");
   if (rows == 0) return ST_OK;
   ST_CHECK_ARG(g && s && offsets && out && ldo >= (int64_t)R * nseg,
                "st_moe_lora_rows: NULL pointer or ldo too small");
   ST_CHECK_ARG(ldg >= seg_len * nseg && (!gather || g_rows > 0),
                "st_moe_lora_rows: ldg < nseg * seg_len");
   GroupedRk a{};
-  a.rows = rows; a.R = R; a.seg_len = seg_len;
+  a.rows = rows; a.Rseg = R; a.seg_len = seg_len;
   a.G = g; a.ldg = ldg; a.g_rows = gather ? g_rows : rows; a.gather = gather;
-  a.S = s; a.ssk = ssk; a.ssj = ssj; a.s_gstride = s_gstride;
+  a.ssk = ssk; a.ssj = ssj; a.s_gstride = s_gstride;
   a.offsets = offsets; a.groups = groups;
-  a.out = out; a.so_m = ldo; a.so_j = 1; a.alpha = alpha; a.accumulate = 0;
+  a.so_m = ldo; a.so_j = 1; a.alpha = alpha; a.accumulate = 0;
   a.vec = (al16(g) && ldg % 8 == 0 && seg_len % 8 == 0) ? 1 : 0;
   dim3 grid((unsigned)(st::cdiv(rows, GK_BM) + groups), 1, (unsigned)nseg);
-  if (!launch_grouped_stream<false>(a, grid, (hipStream_t)stream))
-    grouped_rk<false><<<grid, NTH, 0, (hipStream_t)stream>>>(a);
-  return st::check_launch("grouped_rk rows");
+  // output columns 64 at a time (one launch each)
+  for (int32_t c0 = 0; c0 < R; c0 += 64) {
+    a.R = R - c0 < 64 ? R - c0 : 64;
+    a.S = s + c0 * ssj;
+    a.out = out + c0;
+    if (!launch_grouped_stream<false>(a, grid, (hipStream_t)stream))
+      grouped_rk<false><<<grid, NTH, 0, (hipStream_t)stream>>>(a);
+    if (int rc = st::check_launch("grouped_rk rows")) return rc;
+  }
+  return ST_OK;
 }
 
 extern "C" int st_moe_lora_grads(int64_t rows, int32_t R, int64_t seg_len, int32_t nseg,
@@ -920,20 +928,27 @@ extern "C" int st_moe_lora_grads(int64_t rows, int32_t R, int64_t seg_len, int32
                                  const int32_t* offsets, int32_t groups, float alpha, float* out,
                                  int64_t o_gstride, int64_t so_m, int64_t so_j,
                                  int32_t accumulate, st_stream_t stream) {
-  ST_CHECK_ARG(rows >= 0 && R > 0 && R <= 64 && seg_len > 0 && nseg > 0 && groups > 0,
-               "st_moe_lora_grads: need 0 < R <= 64");
+  ST_CHECK_ARG(rows >= 0 && R > 0 && seg_len > 0 && nseg > 0 && groups > 0,
+               "st_moe_lora_grads: need 0 < R");
   ST_CHECK_ARG(offsets && out && (rows == 0 || (g && s)), "st_moe_lora_grads: NULL pointer");
   ST_CHECK_ARG(ldg >= seg_len * nseg, "st_moe_lora_grads: ldg < nseg * seg_len");
   GroupedRk a{};
-  a.rows = rows; a.R = R; a.seg_len = seg_len;
+  a.rows = rows; a.Rseg = R; a.seg_len = seg_len;
   a.G = g; a.ldg = ldg; a.g_rows = gather ? g_rows : rows; a.gather = gather;
-  a.S = s; a.ssk = ssk; a.ssj = ssj;
+  a.ssk = ssk; a.ssj = ssj;
   a.offsets = offsets; a.groups = groups;
-  a.out = out; a.o_gstride = o_gstride; a.so_m = so_m; a.so_j = so_j;
+  a.o_gstride = o_gstride; a.so_m = so_m; a.so_j = so_j;
   a.alpha = alpha; a.accumulate = accumulate;
   a.vec = (al16(g) && ldg % 8 == 0 && seg_len % 8 == 0) ? 1 : 0;
   dim3 grid((unsigned)st::cdiv(seg_len, GK_BM), (unsigned)groups, (unsigned)nseg);
-  if (!launch_grouped_stream<true>(a, grid, (hipStream_t)stream))
-    grouped_rk<true><<<grid, NTH, 0, (hipStream_t)stream>>>(a);
-  return st::check_launch("grouped_rk grads");
+  // output columns 64 at a time (one launch each)
+  for (int32_t c0 = 0; c0 < R; c0 += 64) {
+    a.R = R - c0 < 64 ? R - c0 : 64;
+    a.S = s ? s + c0 * ssj : nullptr;
+    a.out = out + c0 * so_j;
+    if (!launch_grouped_stream<true>(a, grid, (hipStream_t)stream))
+      grouped_rk<true><<<grid, NTH, 0, (hipStream_t)stream>>>(a);
+    if (int rc = st::check_launch("grouped_rk grads")) return rc;
+  }
+  return ST_OK;
 }

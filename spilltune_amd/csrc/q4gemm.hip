@@ -48,6 +48,7 @@ struct GemmParams {
   int64_t ldl;
   int lora_k;
   int lora_cols;  // columns of T staged (fwd: nseg*rank, dgrad: lora_k)
+  int lora_global;  // LoRA operands read from global memory (more than 64 columns)
   float lora_scale;
   int nseg;
   int64_t seg_end[4];
@@ -147,9 +148,16 @@ struct EpiIn {
 // Per-wave LDS staging of the vector epilogue (dwords), placed after the LoRA
 // operands the epilogue stages (16-byte aligned).
 constexpr int EPI_STG = 16 * 36;
+// Floats of LDS the LoRA epilogue stages T and the right operand in (none
+// when they are read from global memory)
+template <int BM, int BN>
+__host__ __device__ __forceinline__ int64_t lora_lds_floats(const GemmParams& p) {
+  if (!p.T || p.lora_global) return 0;
+  return (int64_t)BM * (p.lora_cols + 1) + (int64_t)BN * (p.lora_k + 1);
+}
 template <bool DGRAD, int BM, int BN>
 __host__ __device__ __forceinline__ int64_t epi_stage_offset(const GemmParams& p) {
-  if (!p.T) return 0;
+  if (!p.T || p.lora_global) return 0;
   const int64_t f = (int64_t)BM * (p.lora_cols + 1) +
                     (int64_t)BN * (p.lora_k + 1);
   return (f + 3) & ~(int64_t)3;
@@ -173,7 +181,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const f32x16 
   const int tstride = p.lora_cols + 1;
   float* Ls = Ts + BM * tstride;
   const int lstride = DGRAD ? BN : (p.lora_k + 1);
-  if (lora) {
+  if (lora && !p.lora_global) {
     // T rows [m0, m0+BM) x [0, lora_cols) and the LoRA right operand
     // (dgrad: A_cat [lora_k, P] columns p0..; forward: B_lora [P, rank] rows p0..)
     stage_f32<NT>(Ts, tstride, make_rsrc(p.T, 0x7fffffff), p.ldt, m0, 0, BM, p.lora_cols,
@@ -206,17 +214,36 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const f32x16 
   // 16-byte row-pair reads of a quarter-wave cover all 64 banks once)
   uint32_t* stg = (uint32_t*)lds + epi_stage_offset<DGRAD, BM, BN>(p) + (tid >> 6) * EPI_STG;
 
-  // LoRA term of block (i, j) on v_mfma_f32_32x32x2_f32
+  // LoRA term of block (i, j) on v_mfma_f32_32x32x2_f32.  More than 64 LoRA
+  // columns do not fit the tile's LDS: the same operands (same guards, same
+  // products in the same order) then come from global memory through L2.
+  const auto rsTg = make_rsrc(p.T, 0x7fffffff), rsLg = make_rsrc(Lg, 0x7fffffff);
   auto lora_term = [&](int rl, int cl, int coff) {
     f32x16 la;
 #pragma unroll
     for (int v = 0; v < 16; ++v) la[v] = 0.0f;
-    for (int kk = 0; kk < p.lora_k; kk += 2) {
-      int kx = kk + (lane >> 5);
-      float av = Ts[(rl + (lane & 31)) * tstride + coff + kx];
-      float bv = DGRAD ? Ls[kx * lstride + cl + (lane & 31)]
-                       : Ls[(cl + (lane & 31)) * lstride + kx];
-      la = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, la, 0, 0, 0);
+    if (!p.lora_global) {
+      for (int kk = 0; kk < p.lora_k; kk += 2) {
+        int kx = kk + (lane >> 5);
+        float av = Ts[(rl + (lane & 31)) * tstride + coff + kx];
+        float bv = DGRAD ? Ls[kx * lstride + cl + (lane & 31)]
+                         : Ls[(cl + (lane & 31)) * lstride + kx];
+        la = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, la, 0, 0, 0);
+      }
+    } else {
+      const int64_t row = m0 + rl + (lane & 31), col = p0 + cl + (lane & 31);
+      const bool rok = row < mend, cok = col < p.P;
+      for (int kk = 0; kk < p.lora_k; kk += 2) {
+        const int kx = kk + (lane >> 5);
+        const bool kok = kx < p.lora_k;
+        const uint32_t ta = rok && kok ? (uint32_t)((row * p.ldt + coff + kx) * 4) : kOOB;
+        const uint32_t tb = !(cok && kok) ? kOOB
+                            : DGRAD ? (uint32_t)(((int64_t)kx * p.ldl + col) * 4)
+                                    : (uint32_t)((col * p.ldl + kx) * 4);
+        const float av = __builtin_bit_cast(float, ld4(rsTg, ta));
+        const float bv = __builtin_bit_cast(float, ld4(rsLg, tb));
+        la = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, la, 0, 0, 0);
+      }
     }
     return la;
   };
@@ -1266,15 +1293,10 @@ int launch_ws(const GemmParams& p, hipStream_t stream) {
   constexpr int BM = 256, BN = 128;
   int64_t tiles = row_tiles(p, BM) * st::cdiv(p.P, BN);
   if (tiles > 0x7fffffff) return st::fail(ST_EUNSUPPORTED, "q4gemm: too many tiles");
-  if (p.T) {
-    const int64_t need = (int64_t)BM * (p.lora_cols + 1) +
-                         (int64_t)BN * (p.lora_k + 1);
-    if (need > (int64_t)WS_DA * BM * BK / 8 * 4)
-      return st::fail(ST_EUNSUPPORTED, "q4gemm: LoRA epilogue (%d columns) exceeds tile LDS",
-                      p.lora_cols);
-  }
   if (int rc = check_epilogue_extents(p)) return rc;
   GemmParams q = p;
+  // LoRA operands that do not fit the tile's LDS are read from global memory
+  if (lora_lds_floats<BM, BN>(q) > (int64_t)WS_DA * BM * BK / 8 * 4) q.lora_global = 1;
   if (int rc = choose_epilogue<MODE == DGRAD_Q4, BM, BN>(q, (int64_t)WS_DA * BM * BK / 8 * 4, 4))
     return rc;
   gemm_ws_kernel<MODE><<<(unsigned)tiles, 512, 0, stream>>>(q);
@@ -1290,11 +1312,9 @@ int launch_rb(const GemmParams& p, hipStream_t stream) {
   if (p.Q % (RB_ST * BK))
     return st::fail(ST_EUNSUPPORTED, "q4gemm: register-operand tile needs K %% %d == 0",
                     RB_ST * BK);
-  if (p.T && (int64_t)BM * (p.lora_cols + 1) + (int64_t)BN * (p.lora_k + 1) > lds_dwords)
-    return st::fail(ST_EUNSUPPORTED, "q4gemm: LoRA epilogue (%d columns) exceeds tile LDS",
-                    p.lora_cols);
   if (int rc = check_epilogue_extents(p)) return rc;
   GemmParams q = p;
+  if (lora_lds_floats<BM, BN>(q) > lds_dwords) q.lora_global = 1;
   if (int rc = choose_epilogue<false, BM, BN>(q, lds_dwords, NT / 64)) return rc;
   if (q.hi_first)
     gemm_rb_kernel<FN, WAVES, true, FM><<<(unsigned)tiles, NT, 0, stream>>>(q);
@@ -1308,17 +1328,12 @@ int launch(const GemmParams& p, hipStream_t stream) {
   constexpr int NT = 64 * WAVES;
   int64_t tiles = row_tiles(p, BM) * st::cdiv(p.P, BN);
   if (tiles > 0x7fffffff) return st::fail(ST_EUNSUPPORTED, "q4gemm: too many tiles");
-  if (p.T) {  // the LoRA epilogue stages T and the right operand in the tile's LDS
-    using TL = Tile<MODE, BM, BN, WAVES, WAVES_M>;
-    int64_t need = (int64_t)BM * (p.lora_cols + 1) +
-                   (int64_t)BN * (p.lora_k + 1);
-    if (need > (int64_t)TL::LDS_CHUNKS * 4)
-      return st::fail(ST_EUNSUPPORTED, "q4gemm: LoRA epilogue (%d columns) exceeds tile LDS",
-                      p.lora_cols);
-  }
   if (int rc = check_epilogue_extents(p)) return rc;
   using TL = Tile<MODE, BM, BN, WAVES, WAVES_M>;
   GemmParams q = p;
+  // the LoRA epilogue stages T and the right operand in the tile's LDS when
+  // they fit, and reads them from global memory otherwise
+  if (lora_lds_floats<BM, BN>(q) > (int64_t)TL::LDS_CHUNKS * 4) q.lora_global = 1;
   if (int rc = choose_epilogue<TL::DGRAD, BM, BN>(q, (int64_t)TL::LDS_CHUNKS * 4, WAVES)) return rc;
   gemm_kernel<MODE, BM, BN, WAVES, WAVES_M, FLAT><<<(unsigned)tiles, NT, 0, stream>>>(q);
   return st::check_launch("q4gemm");
@@ -1464,11 +1479,9 @@ extern "C" int64_t st_q4_linear_dgrad_workspace_bytes(int64_t M, int64_t N, int6
 }
 
 static int check_lora_common(int64_t rank, int64_t cols) {
-  if (rank <= 0 || rank > 64)
-    return st::fail(ST_EUNSUPPORTED, "q4 linear: LoRA contraction %lld must be in [1, 64]",
-                    (long long)rank);
-  if (cols > 64)
-    return st::fail(ST_EUNSUPPORTED, "q4 linear: %lld LoRA columns exceed 64", (long long)cols);
+  if (rank <= 0 || rank > 65536 || cols > 65536)
+    return st::fail(ST_EUNSUPPORTED, "q4 linear: LoRA contraction %lld (%lld columns) out of range",
+                    (long long)rank, (long long)cols);
   return ST_OK;
 }
 

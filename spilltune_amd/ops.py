@@ -386,7 +386,7 @@ class _Q4LoRALinear(torch.autograd.Function):
             for width in weight.segments:
                 starts.append(starts[-1] + width)
             if sink is not None and not (
-                    ctx.loras is not None and all(sink.wants(l) for l in ctx.loras)
+                    ctx.loras is not None and rank <= 64 and all(sink.wants(l) for l in ctx.loras)
                     and all(st % 8 == 0 for st in starts) and N % 8 == 0 and K % 8 == 0
                     and dy.data_ptr() % 16 == 0 and x.data_ptr() % 16 == 0):
                 sink = None

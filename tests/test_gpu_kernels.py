@@ -144,11 +144,12 @@ def test_q4_linear_fwd_vs_oracle(dev, oracle_codec, monkeypatch, tile, fmt, M, N
 
 
 @pytest.mark.parametrize("tile", ["128", "2562", "256", "2566", "2567", "2568"])
-@pytest.mark.parametrize("r", [1, 3, 7])
+@pytest.mark.parametrize("r", [1, 3, 7, 65, 96, 128])
 def test_q4_linear_fwd_odd_rank_vs_oracle(dev, oracle_codec, monkeypatch, tile, r):
     """Odd LoRA ranks on every forward tile, with a residual: the epilogue's
     fp32 MFMA takes the rank two at a time and reads a zero past the last
-    rank column."""
+    rank column.  Ranks above 64 exceed what the tile's LDS stages: the
+    epilogue reads T and B from global memory."""
     monkeypatch.setenv("ST_GEMM_TILE", tile)
     M, N, K = 300, 512, 1024
     g = torch.Generator().manual_seed(r * 101 + M)
@@ -231,12 +232,14 @@ def test_q4_linear_fwd_flat_kernel_equals_aligned(dev, oracle_codec, monkeypatch
 @pytest.mark.parametrize("tile", ["128", "2562", "256"])
 @pytest.mark.parametrize("M,N,K", [(64, 256, 256), (100, 384, 512), (37, 128, 688), (300, 512, 1024),
                                    (77, 200, 256)])
-@pytest.mark.parametrize("lora,r", [(False, 8), (True, 8), (True, 5)])
+@pytest.mark.parametrize("lora,r", [(False, 8), (True, 8), (True, 5), (True, 97)])
 def test_q4_linear_dgrad_and_lora_grads_vs_oracle(dev, oracle_codec, monkeypatch, tile, M, N, K, lora,
                                                   r):
     """dX (and the LoRA grads) against autograd over the oracle's decode; N =
     200 leaves a ragged last k-tile of the dgrad contraction (8 of 64 rows);
-    r = 5 is an odd rank (the epilogue takes the rank two at a time)."""
+    r = 5 is an odd rank (the epilogue takes the rank two at a time); r = 97
+    is above what the tile's LDS stages (dT and A read from global memory,
+    the rank-r products one by one on the general LoRA GEMM)."""
     monkeypatch.setenv("ST_GEMM_TILE", tile)
     g = torch.Generator().manual_seed(M + N * 3 + K)
     w = (torch.randn(N, K, generator=g) * 0.02).numpy()
@@ -291,6 +294,49 @@ def test_fused_segments_match_separate_projections(dev, oracle_codec, r):
     sep = torch.cat([ops.q4_lora_linear(x, p, [l]) for p, l in zip(parts, loras)], 1)
     torch.cuda.synchronize()
     assert torch.equal(y.view(torch.int16), sep.view(torch.int16))
+
+
+@pytest.mark.parametrize("tile", ["128", "2562", "256", "2566", "2568"])
+@pytest.mark.parametrize("r", [23, 32])
+def test_lora_epilogue_from_global_matches_lds(dev, oracle_codec, monkeypatch, tile, r):
+    """Above 64 LoRA columns the forward epilogue reads T and B from global
+    memory instead of staging them in the tile's LDS: a fused q|k|v with 3r
+    columns (69, 96) gives the bits of three single-segment calls (r columns
+    each, staged in LDS) on the same T and B, through the C ABI."""
+    monkeypatch.setenv("ST_GEMM_TILE", tile)
+    g = torch.Generator().manual_seed(r)
+    M, K, widths = 300, 1024, (256, 128, 128)
+    ws = [(torch.randn(n, K, generator=g) * 0.02).numpy() for n in widths]
+    qs = [q4_from_oracle(oracle_codec, w, "nf4-g128", dev)[0] for w in ws]
+    payload = torch.cat([q.payload for q in qs])
+    scales = torch.cat([q.scales for q in qs])
+    parts = []
+    po = so = 0
+    for q, n in zip(qs, widths):
+        parts.append(ops.Q4Weight(payload[po:po + q.payload.numel()],
+                                  scales[so:so + q.scales.numel()], (n, K), "nf4-g128"))
+        po += q.payload.numel()
+        so += q.scales.numel()
+    fused = ops.concat_rows(parts)
+    x = torch.randn(M, K, generator=g).to(BF).to(dev)
+    T = (torch.randn(M, 3 * r, generator=g) * 0.5).to(dev)
+    B = (torch.randn(sum(widths), r, generator=g) * 0.05).to(dev)
+
+    def fwd(w, t, b, ends):
+        y = torch.empty((M, w.out_features), dtype=BF, device=dev)
+        _lib.call("st_q4_linear_fwd", _lib.ptr(x), M, K, K, _lib.ptr(w.payload),
+                  _lib.ptr(w.scales), w.out_features, w.lut(), w.flags, _lib.ptr(t), 3 * r,
+                  _lib.ptr(b), r, 2.0, len(ends), _lib.i64_array(ends), None, 0, _lib.ptr(y),
+                  w.out_features, None, 0, _lib.stream_handle(dev))
+        return y
+
+    y = fwd(fused, T, B, [256, 384, 512])
+    sep, off = [], 0
+    for s_, (p, n) in enumerate(zip(parts, widths)):
+        sep.append(fwd(p, T[:, s_ * r:], B[off:off + n], [n]))
+        off += n
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int16), torch.cat(sep, 1).view(torch.int16))
 
 
 @pytest.mark.parametrize("widths,r", [((256, 128, 128), 8), ((256, 128, 128), 16), ((384,), 64)])
@@ -367,8 +413,12 @@ def test_lora_grad_sink_adapter_used_twice(dev, oracle_codec):
 
 
 def test_lora_gemm_strided_vs_float64(dev):
+    """Both operand orders and layouts; (300, 150) and (97, 2000) have more
+    than 64 columns on the fp32 operand's side (the rank-r kernel takes them
+    64 at a time)."""
     g = torch.Generator().manual_seed(4)
-    for Mo, No, Kc in [(2048, 16, 4096), (16, 4096, 2048), (4096, 16, 2048), (5, 7, 3), (70, 33, 1000)]:
+    for Mo, No, Kc in [(2048, 16, 4096), (16, 4096, 2048), (4096, 16, 2048), (5, 7, 3), (70, 33, 1000),
+                       (300, 150, 1024), (97, 2000, 512)]:
         a = torch.randn(Mo, Kc, generator=g).to(BF)
         b = torch.randn(Kc, No, generator=g)
         out = torch.empty(Mo, No, device=dev)

@@ -135,12 +135,12 @@ def test_qwen3_qk_norm_layer_step_vs_oracle(oracle_codec):
                      targets=("self_attn.q_proj", "self_attn.v_proj", "self_attn.o_proj")))
 
 
-@pytest.mark.parametrize("r", [5, 32])
+@pytest.mark.parametrize("r", [5, 32, 80])
 def test_layer_step_lora_ranks_vs_oracle(oracle_codec, r):
-    """An odd rank (5: fused q|k|v and gate|up with 15 and 10 LoRA columns) and
-    rank 32 (q|k|v would need 96 LoRA columns, more than one fused GEMM
-    takes, so the functional runs q, k and v one by one; gate|up fused at
-    64)."""
+    """An odd rank (5: fused q|k|v and gate|up with 15 and 10 LoRA columns),
+    rank 32 (q|k|v would need 96 LoRA columns: the functional runs q, k and v
+    one by one; gate|up fused at 64) and rank 80 (every projection on its
+    own, its LoRA operands read from global memory in the GEMM epilogues)."""
     _assert(run_case(dict(GQA, r=r, alpha=2.0 * r), 60 + r, oracle_codec))
 
 

@@ -345,19 +345,22 @@ def _oracle_ffn(flat, router, Wgu, Wd, idx, norm, lora):
     return x, out, leaves
 
 
-@pytest.mark.parametrize("T,H,I,E,k,norm,use_lora", [
-    (64, 256, 128, 8, 2, True, True),
-    (203, 256, 256, 16, 4, False, True),
-    (96, 128, 128, 4, 4, True, False),
-    (256, 2048, 768, 64, 8, True, True),       # config 4 expert shapes, fewer experts/tokens
+@pytest.mark.parametrize("T,H,I,E,k,norm,use_lora,r", [
+    (64, 256, 128, 8, 2, True, True, 8),
+    (203, 256, 256, 16, 4, False, True, 8),
+    (96, 128, 128, 4, 4, True, False, 8),
+    (256, 2048, 768, 64, 8, True, True, 8),       # config 4 expert shapes, fewer experts/tokens
+    (100, 256, 128, 8, 2, True, True, 80),        # rank 80: 160 gate|up LoRA columns
 ])
-def test_moe_ffn_fwd_bwd_vs_oracle(dev, oracle_codec, T, H, I, E, k, norm, use_lora):
+def test_moe_ffn_fwd_bwd_vs_oracle(dev, oracle_codec, T, H, I, E, k, norm, use_lora, r):
+    """Routed experts through the grouped GEMMs against the oracle's expert
+    loop.  Rank 80 takes the expert LoRA products 64 columns per launch and
+    the grouped GEMM epilogues' LoRA operands from global memory."""
     g = torch.Generator().manual_seed(T + H + I + E)
     router = (torch.randn(E, H, generator=g) * H ** -0.5).to(BF)
     qgu, Wgu = _experts(oracle_codec, torch.randn(E, 2 * I, H, generator=g) * 0.02, dev)
     qd, Wd = _experts(oracle_codec, torch.randn(E, H, I, generator=g) * 0.02, dev)
     flat = torch.randn(T, H, generator=g).to(BF)
-    r = 8
     lgu = ld = None
     if use_lora:
         lgu = moe.make_expert_lora("mlp.experts.gate_up_proj", E, H, 2 * I, rank=r, alpha=16.0,
