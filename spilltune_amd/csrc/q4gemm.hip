@@ -48,7 +48,7 @@ struct GemmParams {
   int64_t ldl;
   int lora_k;
   int lora_cols;  // columns of T staged (fwd: nseg*rank, dgrad: lora_k)
-  int lora_global;  // LoRA operands read from global memory (more than 64 columns)
+  int lora_global;  // LoRA operands read from global memory (they do not fit the tile's LDS)
   float lora_scale;
   int nseg;
   int64_t seg_end[4];
@@ -214,9 +214,10 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const f32x16 
   // 16-byte row-pair reads of a quarter-wave cover all 64 banks once)
   uint32_t* stg = (uint32_t*)lds + epi_stage_offset<DGRAD, BM, BN>(p) + (tid >> 6) * EPI_STG;
 
-  // LoRA term of block (i, j) on v_mfma_f32_32x32x2_f32.  More than 64 LoRA
-  // columns do not fit the tile's LDS: the same operands (same guards, same
-  // products in the same order) then come from global memory through L2.
+  // LoRA term of block (i, j) on v_mfma_f32_32x32x2_f32.  When T and the
+  // right operand do not fit the tile's LDS (above 64 LoRA columns) the same
+  // operands (same guards, same products in the same order) come from global
+  // memory through L2.
   const auto rsTg = make_rsrc(p.T, 0x7fffffff), rsLg = make_rsrc(Lg, 0x7fffffff);
   auto lora_term = [&](int rl, int cl, int coff) {
     f32x16 la;
