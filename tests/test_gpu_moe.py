@@ -291,6 +291,66 @@ def test_grouped_fwd_and_dgrad_vs_oracle(dev, oracle_codec, monkeypatch, E, N, K
         assert _rel(got, ref) < 4e-3 and bad < 1e-3, what
 
 
+@pytest.mark.parametrize("tile", ["128", "2562", "2566", "2568"])
+@pytest.mark.parametrize("r,nseg", [(8, 2), (5, 1), (40, 2), (80, 1)])
+def test_grouped_lora_epilogue_vs_reference(dev, oracle_codec, monkeypatch, tile, r, nseg):
+    """Per-expert LoRA terms in the grouped GEMM epilogues on every grouped
+    tile: forward y = bf16(bf16(x W_e^T) + s T B_e^T) with nseg segments of
+    rank r, dgrad dx = bf16(bf16(dy W_e) + bf16(dT A_e)) with nseg * r LoRA
+    rows.  80 and 2 x 40 LoRA columns exceed what a tile's LDS stages: the
+    epilogue reads them from global memory."""
+    monkeypatch.setenv("ST_GROUPED_TILE", tile)
+    E, N, K, T, k = 8, 256, 256, 100, 2
+    g = torch.Generator().manual_seed(r * 7 + nseg)
+    H_ = _Held(dev)
+    q, W = _experts(oracle_codec, torch.randn(E, N, K, generator=g) * 0.02, dev)
+    x = torch.randn(T, K, generator=g).to(BF)
+    idx = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)]).int()
+    R, C = T * k, nseg * r
+    offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    row_token = torch.empty(R, dtype=torch.int32, device=dev)
+    pick_row = torch.empty(R, dtype=torch.int32, device=dev)
+    _lib.call("st_moe_permute", H_(idx), T, k, E, _lib.ptr(offsets),
+              _lib.ptr(row_token), _lib.ptr(pick_row), _st(dev))
+    Tm = torch.randn(R, C, generator=g) * 0.5
+    Bl = torch.randn(E, N, r, generator=g) * 0.05
+    dT = torch.randn(R, C, generator=g) * 0.5
+    Al = torch.randn(E, C, K, generator=g) * 0.05
+    scale = 2.0
+    ends = [N // nseg * (i + 1) for i in range(nseg)]
+    y = torch.empty(R, N, dtype=BF, device=dev)
+    _lib.call("st_q4_grouped_fwd", H_(x), T, K, _lib.ptr(row_token), R, K,
+              _lib.ptr(offsets), E, _lib.ptr(q.payload), _lib.ptr(q.scales), N, q.lut(), 0,
+              H_(Tm), C, H_(Bl), r, scale, nseg, _lib.i64_array(ends), _lib.ptr(y), N, _st(dev))
+    dy = torch.randn(R, N, generator=g).to(BF)
+    dx = torch.empty(R, K, dtype=BF, device=dev)
+    _lib.call("st_q4_grouped_dgrad", H_(dy), N, R, N, _lib.ptr(offsets), E,
+              _lib.ptr(q.payload), _lib.ptr(q.scales), K, q.lut(), 0, H_(dT), C, H_(Al), C,
+              _lib.ptr(dx), K, _st(dev))
+    torch.cuda.synchronize()
+    off = offsets.cpu().long()
+    tok = row_token.cpu().long()
+    y_ref = torch.empty(R, N, dtype=BF)
+    dx_ref = torch.empty(R, K, dtype=BF)
+    seg = torch.zeros(N, dtype=torch.long)
+    for e_ in ends[:-1]:
+        seg[e_:] += 1
+    for e in range(E):
+        a, b = int(off[e]), int(off[e + 1])
+        if b > a:
+            base = F.linear(x[tok[a:b]].float(), W[e].float()).to(BF).double()
+            Ts = Tm[a:b].double().view(b - a, nseg, r)[:, seg, :]       # [rows, N, r]
+            lora = (Ts * Bl[e].double().unsqueeze(0)).sum(-1) * scale
+            y_ref[a:b] = (base + lora).to(BF)
+            dbase = (dy[a:b].float() @ W[e].float()).to(BF).double()
+            dx_ref[a:b] = (dbase + (dT[a:b].double() @ Al[e].double()).to(BF).double()).to(BF)
+    for got, ref, what in ((y, y_ref, "fwd"), (dx, dx_ref, "dgrad")):
+        got, ref = got.float().cpu(), ref.float()
+        err = (got - ref).abs()
+        bad = (err > ref.abs() * 2 ** -7 + 1e-6).float().mean().item()
+        assert _rel(got, ref) < 4e-3 and bad < 1e-3, (what, _rel(got, ref), bad)
+
+
 @pytest.mark.parametrize("E,H,I,T,k,lora", [(8, 256, 256, 100, 2, True), (16, 384, 128, 333, 4, False),
                                           (32, 2048, 768, 512, 8, True)])
 def test_grouped_dgrad_swiglu_equals_dgrad_then_swiglu_bwd(dev, oracle_codec, E, H, I, T, k, lora):
