@@ -191,6 +191,7 @@ class _MoEFeedForward(torch.autograd.Function):
         st = _stream(dev)
         lut_gu, lut_d = gate_up.lut(), down.lut()
         has_lora = bool(lora)
+        has_gu, has_d = gu_rank > 0, d_rank > 0
         # 1. router
         weights = torch.empty((T, top_k), dtype=_F32, device=dev)
         indices = torch.empty((T, top_k), dtype=_I32, device=dev)
@@ -216,7 +217,8 @@ class _MoEFeedForward(torch.autograd.Function):
         # 3. gate|up with per-expert LoRA (segments gate, up)
         A_gu = B_gu = A_d = B_d = T_gu = T_d = None
         if has_lora:
-            A_gu, B_gu, A_d, B_d = (t.detach() for t in lora)
+            A_gu, B_gu, A_d, B_d = (None if t is None else t.detach() for t in lora)
+        if has_gu:
             T_gu = torch.empty((R, 2 * gu_rank), dtype=_F32, device=dev)
             _lib.call("st_moe_lora_rows", R, 2 * gu_rank, H, 1, _lib.ptr(flat), H, T,
                       _lib.ptr(row_token), _lib.ptr(A_gu), 1, H, 2 * gu_rank * H,
@@ -225,15 +227,15 @@ class _MoEFeedForward(torch.autograd.Function):
         _launch(("moe_fwd", R, 2 * I, H), lambda: _lib.call(
             "st_q4_grouped_fwd", _lib.ptr(flat), T, H, _lib.ptr(row_token), R, H,
             _lib.ptr(offsets), E, _lib.ptr(gate_up.payload), _lib.ptr(gate_up.scales), 2 * I,
-            lut_gu, gate_up.flags, _lib.ptr(T_gu), 2 * gu_rank if has_lora else 0,
-            _lib.ptr(B_gu), gu_rank if has_lora else 0, float(gu_scale),
-            2 if has_lora else 0, _lib.i64_array([I, 2 * I]) if has_lora else None,
+            lut_gu, gate_up.flags, _lib.ptr(T_gu), 2 * gu_rank if has_gu else 0,
+            _lib.ptr(B_gu), gu_rank if has_gu else 0, float(gu_scale),
+            2 if has_gu else 0, _lib.i64_array([I, 2 * I]) if has_gu else None,
             _lib.ptr(gu), 2 * I, st))
         # 4. SwiGLU and down
         h = torch.empty((R, I), dtype=_BF16, device=dev)
         _lib.call("st_swiglu_fwd", _lib.ptr(gu), 2 * I, _lib.ptr(gu[:, I:]), 2 * I, R, I,
                   _lib.ptr(h), I, st)
-        if has_lora:
+        if has_d:
             T_d = torch.empty((R, d_rank), dtype=_F32, device=dev)
             _lib.call("st_moe_lora_rows", R, d_rank, I, 1, _lib.ptr(h), I, R, None,
                       _lib.ptr(A_d), 1, I, d_rank * I, _lib.ptr(offsets), E, 1.0,
@@ -242,14 +244,14 @@ class _MoEFeedForward(torch.autograd.Function):
         _launch(("moe_fwd", R, H, I), lambda: _lib.call(
             "st_q4_grouped_fwd", _lib.ptr(h), R, I, None, R, I, _lib.ptr(offsets), E,
             _lib.ptr(down.payload), _lib.ptr(down.scales), H, lut_d, down.flags,
-            _lib.ptr(T_d), d_rank if has_lora else 0, _lib.ptr(B_d), d_rank if has_lora else 0,
-            float(d_scale), 1 if has_lora else 0, _lib.i64_array([H]) if has_lora else None,
+            _lib.ptr(T_d), d_rank if has_d else 0, _lib.ptr(B_d), d_rank if has_d else 0,
+            float(d_scale), 1 if has_d else 0, _lib.i64_array([H]) if has_d else None,
             _lib.ptr(v), H, st))
         # 5. combine
         out = torch.empty((T, H), dtype=_BF16, device=dev)
         _lib.call("st_moe_combine", _lib.ptr(v), R, _lib.ptr(weights), _lib.ptr(indices),
                   _lib.ptr(pick_row), T, top_k, H, _lib.ptr(out), st)
-        ctx.meta = (gate_up, down, cfg, has_lora)
+        ctx.meta = (gate_up, down, cfg, has_lora, has_gu, has_d)
         ctx.save_for_backward(flat, router, logits, weights, indices, offsets, row_token,
                               pick_row, gu, h, v, T_gu, T_d, A_gu, B_gu, A_d, B_d)
         ctx.mark_non_differentiable(logits, weights, indices)
@@ -257,7 +259,7 @@ class _MoEFeedForward(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dout, _dlogits, _dweights, _dindices):
-        gate_up, down, cfg, has_lora = ctx.meta
+        gate_up, down, cfg, has_lora, has_gu, has_d = ctx.meta
         top_k, norm, gu_rank, gu_scale, d_rank, d_scale, sig, groups, group_k, rscale = cfg
         (flat, router, logits, weights, indices, offsets, row_token, pick_row, gu, h, v,
          T_gu, T_d, A_gu, B_gu, A_d, B_d) = ctx.saved_tensors
@@ -275,9 +277,9 @@ class _MoEFeedForward(torch.autograd.Function):
         _lib.call("st_moe_combine_bwd", _lib.ptr(dout), _lib.ptr(v), R, _lib.ptr(weights),
                   _lib.ptr(pick_row), T, top_k, H, 0 if sig else 1, _lib.ptr(dv), _lib.ptr(dw),
                   st)
-        grads = []
+        grads = [None, None, None, None] if has_lora else []
         dT_d = dT_gu = None
-        if has_lora:
+        if has_d:
             dT_d = torch.empty((R, d_rank), dtype=_F32, device=dev)
             _lib.call("st_moe_lora_rows", R, d_rank, H, 1, _lib.ptr(dv), H, R, None,
                       _lib.ptr(B_d), d_rank, 1, H * d_rank, _lib.ptr(offsets), E,
@@ -290,14 +292,15 @@ class _MoEFeedForward(torch.autograd.Function):
             _lib.call("st_moe_lora_grads", R, d_rank, I, 1, _lib.ptr(h), I, R, None,
                       _lib.ptr(dT_d), d_rank, 1, _lib.ptr(offsets), E, 1.0,
                       _lib.ptr(dA_d), d_rank * I, 1, I, 0, st)
+            grads[2:] = [dA_d, dB_d]
         # the down dgrad's epilogue applies the SwiGLU VJP: dgate|dup directly
         dgu = torch.empty((R, 2 * I), dtype=_BF16, device=dev)
         _launch(("moe_dgrad", R, H, I), lambda: _lib.call(
             "st_q4_grouped_dgrad_swiglu", _lib.ptr(dv), H, R, H, _lib.ptr(offsets), E,
             _lib.ptr(down.payload), _lib.ptr(down.scales), I, down.lut(), down.flags,
-            _lib.ptr(dT_d), d_rank if has_lora else 0, _lib.ptr(A_d), d_rank if has_lora else 0,
+            _lib.ptr(dT_d), d_rank if has_d else 0, _lib.ptr(A_d), d_rank if has_d else 0,
             _lib.ptr(gu), 2 * I, _lib.ptr(dgu), 2 * I, st))
-        if has_lora:
+        if has_gu:
             dT_gu = torch.empty((R, 2 * gu_rank), dtype=_F32, device=dev)
             _lib.call("st_moe_lora_rows", R, gu_rank, I, 2, _lib.ptr(dgu), 2 * I, R, None,
                       _lib.ptr(B_gu), gu_rank, 1, 2 * I * gu_rank, _lib.ptr(offsets), E,
@@ -310,13 +313,13 @@ class _MoEFeedForward(torch.autograd.Function):
             _lib.call("st_moe_lora_grads", R, 2 * gu_rank, H, 1, _lib.ptr(flat), H, T,
                       _lib.ptr(row_token), _lib.ptr(dT_gu), 2 * gu_rank, 1, _lib.ptr(offsets),
                       E, 1.0, _lib.ptr(dA_gu), 2 * gu_rank * H, 1, H, 0, st)
-            grads = [dA_gu, dB_gu, dA_d, dB_d]
+            grads[:2] = [dA_gu, dB_gu]
         dxs = torch.empty((R, H), dtype=_BF16, device=dev)
         _launch(("moe_dgrad", R, 2 * I, H), lambda: _lib.call(
             "st_q4_grouped_dgrad", _lib.ptr(dgu), 2 * I, R, 2 * I, _lib.ptr(offsets), E,
             _lib.ptr(gate_up.payload), _lib.ptr(gate_up.scales), H, gate_up.lut(),
-            gate_up.flags, _lib.ptr(dT_gu), 2 * gu_rank if has_lora else 0, _lib.ptr(A_gu),
-            2 * gu_rank if has_lora else 0, _lib.ptr(dxs), H, st))
+            gate_up.flags, _lib.ptr(dT_gu), 2 * gu_rank if has_gu else 0, _lib.ptr(A_gu),
+            2 * gu_rank if has_gu else 0, _lib.ptr(dxs), H, st))
         # router VJP and the input gradient over every use of flat
         if sig:
             # the router is frozen; its input gradient is fp32 dlogits @ W
@@ -357,7 +360,7 @@ def moe_feed_forward(hidden, weights, *, num_experts, top_k, norm_topk_prob, lor
     ``mlp.experts.gate_up_proj`` and ``mlp.experts.down_proj``
     (:class:`Q4Experts`, ``[E, 2I, H]`` and ``[E, H, I]``).  Optional
     ``lora_gate_up`` (:class:`ExpertLoRA`, 2 segments) and ``lora_down``
-    (1 segment) adapt every expert.  With ``return_routing`` also returns the
+    (1 segment), either or both, adapt every expert.  With ``return_routing`` also returns the
     ``(weights, indices)`` the router picked."""
     router = weights["mlp.gate.weight"]
     gate_up = weights["mlp.experts.gate_up_proj"]
@@ -382,15 +385,20 @@ def moe_feed_forward(hidden, weights, *, num_experts, top_k, norm_topk_prob, lor
 
 
 def _lora_cfg(top_k, normalize, lora_gate_up, lora_down, router_cfg):
-    if (lora_gate_up is None) != (lora_down is None):
-        raise ValueError("unsupported_capability: LoRA on gate_up and down together or not at all")
-    if lora_gate_up is None:
+    """Router/LoRA configuration tuple and the adapter leaves (A_gu, B_gu,
+    A_d, B_d; None for an absent adapter, nothing without any): gate_up and
+    down are adapted independently."""
+    if lora_gate_up is None and lora_down is None:
         return (int(top_k), bool(normalize), 0, 1.0, 0, 1.0) + router_cfg, ()
-    if lora_gate_up.segments != 2 or lora_down.segments != 1:
-        raise ValueError("gate_up LoRA needs 2 segments, down LoRA 1")
-    return ((int(top_k), bool(normalize), lora_gate_up.rank, lora_gate_up.scale, lora_down.rank,
-             lora_down.scale) + router_cfg,
-            (lora_gate_up.A, lora_gate_up.B, lora_down.A, lora_down.B))
+    if lora_gate_up is not None and lora_gate_up.segments != 2:
+        raise ValueError("gate_up LoRA needs 2 segments")
+    if lora_down is not None and lora_down.segments != 1:
+        raise ValueError("down LoRA needs 1 segment")
+    gu = (lora_gate_up.rank, lora_gate_up.scale) if lora_gate_up is not None else (0, 1.0)
+    dn = (lora_down.rank, lora_down.scale) if lora_down is not None else (0, 1.0)
+    leaves = (getattr(lora_gate_up, "A", None), getattr(lora_gate_up, "B", None),
+              getattr(lora_down, "A", None), getattr(lora_down, "B", None))
+    return (int(top_k), bool(normalize)) + gu + dn + router_cfg, leaves
 
 
 def deepseek_moe_feed_forward(hidden, weights, *, num_experts, top_k, groups, group_k,

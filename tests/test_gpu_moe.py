@@ -396,11 +396,15 @@ def _oracle_ffn(flat, router, Wgu, Wd, idx, norm, lora):
     loras, leaves = None, []
     if lora is not None:
         A_gu, B_gu, A_d, B_d, r, s_gu, s_d = lora
-        leaves = [t.clone().requires_grad_(True) for t in (A_gu, B_gu, A_d, B_d)]
+        leaves = [None if t is None else t.clone().requires_grad_(True)
+                  for t in (A_gu, B_gu, A_d, B_d)]
         I = Wd.shape[2]
-        loras = {"gate": (leaves[0][:, :r], leaves[1][:, :I], s_gu),
-                 "up": (leaves[0][:, r:], leaves[1][:, I:], s_gu),
-                 "down": (leaves[2], leaves[3], s_d)}
+        loras = {}
+        if A_gu is not None:
+            loras["gate"] = (leaves[0][:, :r], leaves[1][:, :I], s_gu)
+            loras["up"] = (leaves[0][:, r:], leaves[1][:, I:], s_gu)
+        if A_d is not None:
+            loras["down"] = (leaves[2], leaves[3], s_d)
     out = OM.expert_loop(x, routing, idx, Wgu, Wd, num_experts=Wgu.shape[0], loras=loras)
     return x, out, leaves
 
@@ -411,20 +415,24 @@ def _oracle_ffn(flat, router, Wgu, Wd, idx, norm, lora):
     (96, 128, 128, 4, 4, True, False, 8),
     (256, 2048, 768, 64, 8, True, True, 8),       # config 4 expert shapes, fewer experts/tokens
     (100, 256, 128, 8, 2, True, True, 80),        # rank 80: 160 gate|up LoRA columns
+    (80, 256, 128, 8, 2, False, "gate_up", 8),
+    (80, 256, 128, 8, 2, True, "down", 8),
 ])
 def test_moe_ffn_fwd_bwd_vs_oracle(dev, oracle_codec, T, H, I, E, k, norm, use_lora, r):
     """Routed experts through the grouped GEMMs against the oracle's expert
     loop.  Rank 80 takes the expert LoRA products 64 columns per launch and
-    the grouped GEMM epilogues' LoRA operands from global memory."""
+    the grouped GEMM epilogues' LoRA operands from global memory;
+    "gate_up" / "down" adapt only that projection of every expert."""
     g = torch.Generator().manual_seed(T + H + I + E)
     router = (torch.randn(E, H, generator=g) * H ** -0.5).to(BF)
     qgu, Wgu = _experts(oracle_codec, torch.randn(E, 2 * I, H, generator=g) * 0.02, dev)
     qd, Wd = _experts(oracle_codec, torch.randn(E, H, I, generator=g) * 0.02, dev)
     flat = torch.randn(T, H, generator=g).to(BF)
     lgu = ld = None
-    if use_lora:
+    if use_lora in (True, "gate_up"):
         lgu = moe.make_expert_lora("mlp.experts.gate_up_proj", E, H, 2 * I, rank=r, alpha=16.0,
                                    device=dev, segments=2, generator=g, b_std=0.02)
+    if use_lora in (True, "down"):
         ld = moe.make_expert_lora("mlp.experts.down_proj", E, I, H, rank=r, alpha=16.0,
                                   device=dev, generator=g, b_std=0.02)
     weights = {"mlp.gate.weight": router.to(dev), "mlp.experts.gate_up_proj": qgu,
@@ -440,16 +448,19 @@ def test_moe_ffn_fwd_bwd_vs_oracle(dev, oracle_codec, T, H, I, E, k, norm, use_l
     assert torch.equal(idx_c, ref_idx)
     lora = None
     if use_lora:
-        lora = (lgu.A.detach().cpu(), lgu.B.detach().cpu(), ld.A.detach().cpu(),
-                ld.B.detach().cpu(), r, lgu.scale, ld.scale)
+        cpu = lambda l, f: None if l is None else getattr(l, f).detach().cpu()  # noqa: E731
+        lora = (cpu(lgu, "A"), cpu(lgu, "B"), cpu(ld, "A"), cpu(ld, "B"), r,
+                1.0 if lgu is None else lgu.scale, 1.0 if ld is None else ld.scale)
     x, ref, leaves = _oracle_ffn(flat, router, Wgu, Wd, idx_c, norm, lora)
     ref.backward(dout)
     assert _rel(out, ref) < 2e-2, "output"
     assert _cos(xd.grad, x.grad) > 0.999, "input grad"
     if use_lora:
-        for got, leaf, name in ((lgu.A.grad, leaves[0], "A_gu"), (lgu.B.grad, leaves[1], "B_gu"),
-                                (ld.A.grad, leaves[2], "A_d"), (ld.B.grad, leaves[3], "B_d")):
-            assert _cos(got, leaf.grad) > 0.999, name
+        for ad, i, name in ((lgu, 0, "gu"), (ld, 2, "d")):
+            if ad is None:
+                continue
+            for got, leaf, part in ((ad.A.grad, leaves[i], "A"), (ad.B.grad, leaves[i + 1], "B")):
+                assert _cos(got, leaf.grad) > 0.999, part + "_" + name
 
 
 class _SharedLora:
