@@ -195,6 +195,28 @@ def test_rmsnorm_fwd_bwd_vs_oracle():
     assert rel(yd, yr) < 4e-3 and rel(xd.grad, xr.grad) < 1e-2
 
 
+@pytest.mark.parametrize("H", [512, 2048, 4096, 7168, 8192, 8200])
+def test_rmsnorm_row_kernels_vs_oracle(H):
+    """The 16-byte row kernels of st_rmsnorm_fwd/bwd at the hidden sizes of
+    the BASELINE models and around 8192 against the oracle's norm and its
+    autograd VJP plus a residual gradient (the dres operand)."""
+    g = torch.Generator().manual_seed(H)
+    x = torch.randn(33, H, generator=g).to(BF)
+    w = (1 + 0.1 * torch.randn(H, generator=g)).to(BF)
+    dy = torch.randn(33, H, generator=g).to(BF)
+    dres = torch.randn(33, H, generator=g).to(BF)
+    xr = x.clone().requires_grad_(True)
+    yr = OL.rms(xr, w, 1e-5)
+    torch.autograd.backward([yr, xr], [dy, dres])
+    xd = x.cuda().requires_grad_(True)
+    res, yd = ops.rms_norm_residual(xd, w.cuda(), 1e-5)
+    torch.autograd.backward([yd, res], [dy.cuda(), dres.cuda()])
+    torch.cuda.synchronize()
+    err = (yd.float().cpu() - yr.float()).abs()
+    assert (err > yr.float().abs() * 2 ** -7 + 1e-6).float().mean().item() < 1e-3
+    assert rel(yd, yr) < 4e-3 and rel(xd.grad, xr.grad) < 1e-2
+
+
 def test_rope_relayout_vs_oracle():
     g = torch.Generator().manual_seed(1)
     B, S, heads, kv, D = 2, 16, 4, 2, 64
