@@ -45,6 +45,30 @@ def test_abi_version_and_error_mapping():
                   1, 1, 1.0, ctypes.c_void_p(16), 4, 0, None, 0, None)
 
 
+def test_lora_rank_limits_rejected_before_any_launch():
+    """Rank bounds of the LoRA entry points: checked on the host, before any
+    device work (fake pointers never reach a kernel)."""
+    lut = _lib.lut_array(range(16))
+    p = ctypes.c_void_p(16)
+    ends = _lib.i64_array([256])
+
+    def fwd(rank):
+        _lib.call("st_q4_linear_fwd", p, 4, 256, 256, p, p, 256, lut, 0, p, 256, p, rank, 1.0, 1,
+                  ends, None, 0, p, 256, None, 0, None)
+    for rank in (0, -3, 70000):
+        with pytest.raises(ValueError, match="out of range"):
+            fwd(rank)
+    # the batched dY-side products take r <= 64: the query says so with 0
+    assert _lib.query("st_lora_bwd_dy_workspace_bytes", 2048, 4096, 16, 1, _lib.i64_array([4096])) > 0
+    assert _lib.query("st_lora_bwd_dy_workspace_bytes", 2048, 4096, 65, 1, _lib.i64_array([4096])) == 0
+    with pytest.raises(ValueError, match="rank must be 1..64"):
+        _lib.call("st_lora_bwd_dy", p, 4, 256, 256, p, p, 65, 65, 1, ends, 1.0, p, 65, None, p,
+                  1 << 20, None)
+    with pytest.raises(ValueError, match="0 < R"):
+        _lib.call("st_moe_lora_rows", 4, 0, 256, 1, p, 256, 4, None, p, 1, 256, 0, p, 1, 1.0, p,
+                  1, None)
+
+
 def test_workspace_queries():
     assert _lib.query("st_q4_linear_fwd_workspace_bytes", 16, 256, 4096) == 0
     # K % 128 != 0 runs on the flat-group kernels from the packed weight
