@@ -85,9 +85,10 @@ int st_dequant4(const uint8_t* payload, const float* scales, int64_t numel, int3
  * straddle W's rows: each packed word reads its own group's scale).  K % 8 ==
  * 0.  `workspace` is not used (the query returns 0).
  * `t` = x_f32 A_cat^T from st_lora_gemm ([M, nseg*rank] fp32) or NULL for no
- * LoRA; any rank >= 1 (up to 65536 T columns).  Up to 64 T columns the
- * epilogue stages t and lora_b in the tile's LDS; wider ones it reads from
- * global memory (L2) in the same order, with the same result.
+ * LoRA; any rank >= 1 (up to 65536 T columns).  The epilogue stages t and
+ * lora_b in the tile's LDS; when they do not fit (more than 64 T columns on
+ * the 256-wide tiles), the GEMM runs on 128x128 tiles whose epilogue reads
+ * them from global memory (L2), with the same products in the same order.
  * nseg/seg_end describe N-concatenated projections (fused q|k|v, gate|up):
  * column n belongs to segment s = #{seg_end[i] <= n}; segment ends must be
  * multiples of 32.  nseg = 1 with seg_end[0] = N for a single projection.
@@ -107,8 +108,8 @@ int st_q4_linear_fwd(const uint16_t* x, int64_t M, int64_t K, int64_t ldx,
  *   dx[m,k] = bf16( bf16(sum_n dy[m,n] W[n,k]) + bf16(sum_j dt[m,j] lora_a[j,k]) )
  * with dt = lora_scale * dy_f32 B ([M, lora_k] fp32, from st_lora_bwd_dy;
  * N-concatenated projections stack their dt columns and lora_a rows) or
- * dt == NULL for no LoRA term; 1 <= lora_k <= 65536 (above 64 the epilogue
- * reads dt and lora_a from global memory).  W [N,K] as above,
+ * dt == NULL for no LoRA term; 1 <= lora_k <= 65536 (operands beyond the
+ * tile's LDS as in the forward).  W [N,K] as above,
  * dequantised into LDS in its natural orientation and read transposed.
  */
 int64_t st_q4_linear_dgrad_workspace_bytes(int64_t M, int64_t N, int64_t K);

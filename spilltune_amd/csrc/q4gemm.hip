@@ -48,7 +48,7 @@ struct GemmParams {
   int64_t ldl;
   int lora_k;
   int lora_cols;  // columns of T staged (fwd: nseg*rank, dgrad: lora_k)
-  int lora_global;  // LoRA operands read from global memory (they do not fit the tile's LDS)
+  int lora_global;  // LoRA operands read from global memory (gemm_kernel<..., LG = true>)
   float lora_scale;
   int nseg;
   int64_t seg_end[4];
@@ -165,13 +165,17 @@ __host__ __device__ __forceinline__ int64_t epi_stage_offset(const GemmParams& p
 
 // Epilogue shared by the GEMM kernels: y = bf16(acc) (+ LoRA term, + residual)
 // for this tile; waves with `has_acc` false only help stage the LoRA operands.
+// LG: T and the LoRA right operand are read from global memory instead of
+// being staged in LDS (only the 128x128 kernel is built with it, for LoRA
+// operands that do not fit its LDS; the other kernels keep the staged form
+// only, so their register allocation does not carry the global loop).
 // LDS (`lds`, at least BM*(lora_cols+1) + the LoRA right operand floats) is
 // reused, so the caller has finished every LDS read of the main loop.
 // Residual loads and output stores go through buffer resources with masked
 // 32-bit offsets (the host keeps C and R below 2 GiB): a 32x32 block's 16
 // residual loads are all in flight before the LoRA products, and rows or
 // columns outside the problem are skipped without branches.
-template <bool DGRAD, int BM, int BN, int NT, int FM, int FN, int WM, int WN>
+template <bool DGRAD, int BM, int BN, int NT, int FM, int FN, int WM, int WN, bool LG = false>
 __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const f32x16 (&acc)[FM][FN],
                                               uint4* lds, int64_t m0, int64_t mend, int64_t p0,
                                               int wm, int wn, int tid, int lane, bool has_acc,
@@ -181,7 +185,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const f32x16 
   const int tstride = p.lora_cols + 1;
   float* Ls = Ts + BM * tstride;
   const int lstride = DGRAD ? BN : (p.lora_k + 1);
-  if (lora && !p.lora_global) {
+  if (!LG && lora) {
     // T rows [m0, m0+BM) x [0, lora_cols) and the LoRA right operand
     // (dgrad: A_cat [lora_k, P] columns p0..; forward: B_lora [P, rank] rows p0..)
     stage_f32<NT>(Ts, tstride, make_rsrc(p.T, 0x7fffffff), p.ldt, m0, 0, BM, p.lora_cols,
@@ -214,16 +218,14 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const f32x16 
   // 16-byte row-pair reads of a quarter-wave cover all 64 banks once)
   uint32_t* stg = (uint32_t*)lds + epi_stage_offset<DGRAD, BM, BN>(p) + (tid >> 6) * EPI_STG;
 
-  // LoRA term of block (i, j) on v_mfma_f32_32x32x2_f32.  When T and the
-  // right operand do not fit the tile's LDS (above 64 LoRA columns) the same
+  // LoRA term of block (i, j) on v_mfma_f32_32x32x2_f32.  LG: the same
   // operands (same guards, same products in the same order) come from global
   // memory through L2.
-  const auto rsTg = make_rsrc(p.T, 0x7fffffff), rsLg = make_rsrc(Lg, 0x7fffffff);
   auto lora_term = [&](int rl, int cl, int coff) {
     f32x16 la;
 #pragma unroll
     for (int v = 0; v < 16; ++v) la[v] = 0.0f;
-    if (!p.lora_global) {
+    if constexpr (!LG) {
       for (int kk = 0; kk < p.lora_k; kk += 2) {
         int kx = kk + (lane >> 5);
         float av = Ts[(rl + (lane & 31)) * tstride + coff + kx];
@@ -232,6 +234,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const f32x16 
         la = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, la, 0, 0, 0);
       }
     } else {
+      const auto rsTg = make_rsrc(p.T, 0x7fffffff), rsLg = make_rsrc(Lg, 0x7fffffff);
       const int64_t row = m0 + rl + (lane & 31), col = p0 + cl + (lane & 31);
       const bool rok = row < mend, cok = col < p.P;
       for (int kk = 0; kk < p.lora_k; kk += 2) {
@@ -450,7 +453,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const f32x16 
 // 128-element scale groups of W straddle its rows; every packed word (8
 // weights, which K % 8 == 0 keeps inside one group) then reads its own scale
 // at (flat element index) / 128 and gets its own decode table.
-template <int MODE, int BM, int BN, int WAVES, int WAVES_M, bool FLAT = false>
+template <int MODE, int BM, int BN, int WAVES, int WAVES_M, bool FLAT = false, bool LG = false>
 __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
   using TL = Tile<MODE, BM, BN, WAVES, WAVES_M>;
   constexpr int NT = TL::NT;
@@ -762,7 +765,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
   // before the epilogue reuses LDS
   __syncthreads();
 
-  gemm_epilogue<TL::DGRAD, BM, BN, NT, FM, FN, WM, WN>(p, acc, lds, m0, mend, p0, wm, wn, tid,
+  gemm_epilogue<TL::DGRAD, BM, BN, NT, FM, FN, WM, WN, LG>(p, acc, lds, m0, mend, p0, wm, wn, tid,
                                                        lane, true, Lg);
 }
 
@@ -1289,15 +1292,19 @@ int check_epilogue_extents(const GemmParams& p) {
   return ok ? ST_OK : st::fail(ST_EUNSUPPORTED, "q4gemm: output, residual or LoRA operand above 2 GiB");
 }
 
+template <int MODE, int BM, int BN, int WAVES, int WAVES_M = 2, bool FLAT = false, bool LG = false>
+int launch(const GemmParams& p, hipStream_t stream);
+
 template <int MODE>
 int launch_ws(const GemmParams& p, hipStream_t stream) {
   constexpr int BM = 256, BN = 128;
   int64_t tiles = row_tiles(p, BM) * st::cdiv(p.P, BN);
   if (tiles > 0x7fffffff) return st::fail(ST_EUNSUPPORTED, "q4gemm: too many tiles");
   if (int rc = check_epilogue_extents(p)) return rc;
+  // LoRA operands that do not fit this tile's LDS: the 128x128 kernel
+  if (lora_lds_floats<BM, BN>(p) > (int64_t)WS_DA * BM * BK / 8 * 4)
+    return launch<MODE, 128, 128, 4>(p, stream);
   GemmParams q = p;
-  // LoRA operands that do not fit the tile's LDS are read from global memory
-  if (lora_lds_floats<BM, BN>(q) > (int64_t)WS_DA * BM * BK / 8 * 4) q.lora_global = 1;
   if (int rc = choose_epilogue<MODE == DGRAD_Q4, BM, BN>(q, (int64_t)WS_DA * BM * BK / 8 * 4, 4))
     return rc;
   gemm_ws_kernel<MODE><<<(unsigned)tiles, 512, 0, stream>>>(q);
@@ -1314,8 +1321,8 @@ int launch_rb(const GemmParams& p, hipStream_t stream) {
     return st::fail(ST_EUNSUPPORTED, "q4gemm: register-operand tile needs K %% %d == 0",
                     RB_ST * BK);
   if (int rc = check_epilogue_extents(p)) return rc;
+  if (lora_lds_floats<BM, BN>(p) > lds_dwords) return launch<FWD_Q4, 128, 128, 4>(p, stream);
   GemmParams q = p;
-  if (lora_lds_floats<BM, BN>(q) > lds_dwords) q.lora_global = 1;
   if (int rc = choose_epilogue<false, BM, BN>(q, lds_dwords, NT / 64)) return rc;
   if (q.hi_first)
     gemm_rb_kernel<FN, WAVES, true, FM><<<(unsigned)tiles, NT, 0, stream>>>(q);
@@ -1324,7 +1331,7 @@ int launch_rb(const GemmParams& p, hipStream_t stream) {
   return st::check_launch("q4gemm");
 }
 
-template <int MODE, int BM, int BN, int WAVES, int WAVES_M = 2, bool FLAT = false>
+template <int MODE, int BM, int BN, int WAVES, int WAVES_M, bool FLAT, bool LG>
 int launch(const GemmParams& p, hipStream_t stream) {
   constexpr int NT = 64 * WAVES;
   int64_t tiles = row_tiles(p, BM) * st::cdiv(p.P, BN);
@@ -1333,10 +1340,16 @@ int launch(const GemmParams& p, hipStream_t stream) {
   using TL = Tile<MODE, BM, BN, WAVES, WAVES_M>;
   GemmParams q = p;
   // the LoRA epilogue stages T and the right operand in the tile's LDS when
-  // they fit, and reads them from global memory otherwise
-  if (lora_lds_floats<BM, BN>(q) > (int64_t)TL::LDS_CHUNKS * 4) q.lora_global = 1;
+  // they fit; otherwise the 128x128 kernel built to read them from global
+  // memory runs the GEMM
+  if constexpr (LG) {
+    q.lora_global = q.T ? 1 : 0;
+  } else if constexpr (TL::Q4) {
+    if (lora_lds_floats<BM, BN>(q) > (int64_t)TL::LDS_CHUNKS * 4)
+      return launch<MODE, 128, 128, 4, 2, FLAT, true>(p, stream);
+  }
   if (int rc = choose_epilogue<TL::DGRAD, BM, BN>(q, (int64_t)TL::LDS_CHUNKS * 4, WAVES)) return rc;
-  gemm_kernel<MODE, BM, BN, WAVES, WAVES_M, FLAT><<<(unsigned)tiles, NT, 0, stream>>>(q);
+  gemm_kernel<MODE, BM, BN, WAVES, WAVES_M, FLAT, LG><<<(unsigned)tiles, NT, 0, stream>>>(q);
   return st::check_launch("q4gemm");
 }
 

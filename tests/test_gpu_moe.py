@@ -297,8 +297,9 @@ def test_grouped_lora_epilogue_vs_reference(dev, oracle_codec, monkeypatch, tile
     """Per-expert LoRA terms in the grouped GEMM epilogues on every grouped
     tile: forward y = bf16(bf16(x W_e^T) + s T B_e^T) with nseg segments of
     rank r, dgrad dx = bf16(bf16(dy W_e) + bf16(dT A_e)) with nseg * r LoRA
-    rows.  80 and 2 x 40 LoRA columns exceed what a tile's LDS stages: the
-    epilogue reads them from global memory."""
+    rows.  80 and 2 x 40 LoRA columns exceed what the 128x256 and 256x128
+    tiles' LDS stages and run on the 128x128 kernel, which stages 2 x 40 and
+    reads rank 80 from global memory."""
     monkeypatch.setenv("ST_GROUPED_TILE", tile)
     E, N, K, T, k = 8, 256, 256, 100, 2
     g = torch.Generator().manual_seed(r * 7 + nseg)
