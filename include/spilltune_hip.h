@@ -55,6 +55,8 @@ enum {
 
 /* storage flags */
 #define ST_FLAG_HI_NIBBLE_FIRST 1 /* element 2i in the high nibble (bitsandbytes) */
+#define ST_FLAG_GROUP64 2         /* fused GEMMs: one fp32 scale per 64 flat elements
+                                     (bitsandbytes' blocksize) instead of 128 */
 
 /* dtype codes for st_lora_gemm operands */
 #define ST_DTYPE_BF16 0
@@ -74,16 +76,33 @@ const char* st_last_error(void);
 int st_dequant4(const uint8_t* payload, const float* scales, int64_t numel, int32_t group,
                 const float* lut16, int32_t flags, uint16_t* out, st_stream_t stream);
 
+/*
+ * Block scales of bitsandbytes' double-quantised NF4 state (blocksize 64,
+ * nested blocksize 256; nf4_backend.py:200-240 state layout, :292-298
+ * quantize_4bit(blocksize=64, compress_statistics=True); staged on the device
+ * by nf4_backend_cuda.py:748-837 and consumed by linear_cuda -> matmul_4bit,
+ * nf4_backend_cuda.py:888-917):
+ *   scales[j] = fp32( fp32(nested_map[absmax_q[j]] * nested_absmax[j / nested_block])
+ *                     + offset )                      for j < blocks
+ * (no fused multiply-add).  The result is the fp32 per-64 scale array the
+ * fused GEMMs and st_dequant4 (group 64) take with the high-nibble-first
+ * payload as it lies.  nested_map has 256 entries.
+ */
+int st_nf4_dq_scales(const uint8_t* absmax_q, const float* nested_absmax, const float* nested_map,
+                     float offset, int64_t blocks, int32_t nested_block, float* scales,
+                     st_stream_t stream);
+
 /* ------------------------------------------------- fused projection GEMMs */
 /*
  * Forward of a frozen 4-bit projection with LoRA (lora.py:218-220):
  *   base[m,n] = bf16( sum_k x[m,k] * W[n,k] )            (W = dequant, bf16)
  *   y[m,n]    = bf16( base + lora_scale * sum_j t[m, seg(n)*rank + j] * lora_b[n,j] )
  *   y[m,n]    = bf16( residual[m,n] + y[m,n] )            (if residual)
- * W [N,K] is payload/scales in flat groups of 128, dequantised inside the
- * GEMM and never written to HBM as bf16 (K % 128 != 0, where the groups
- * straddle W's rows: each packed word reads its own group's scale).  K % 8 ==
- * 0.  `workspace` is not used (the query returns 0).
+ * W [N,K] is payload/scales in flat groups of 128 (64 with ST_FLAG_GROUP64:
+ * bitsandbytes' NF4 blocksize, scales from st_nf4_dq_scales), dequantised
+ * inside the GEMM and never written to HBM as bf16 (K % group != 0, where
+ * the groups straddle W's rows: each packed word reads its own group's
+ * scale).  K % 8 == 0.  `workspace` is not used (the query returns 0).
  * `t` = x_f32 A_cat^T from st_lora_gemm ([M, nseg*rank] fp32) or NULL for no
  * LoRA; any rank >= 1 (up to 65536 T columns).  The epilogue stages t and
  * lora_b in the tile's LDS; when they do not fit (more than 64 T columns on

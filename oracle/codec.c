@@ -144,3 +144,22 @@ int st_oracle_encode_nf4(const float* x, int64_t numel, int hi_first, uint8_t* p
   }
   return 0;
 }
+
+/*
+ * bitsandbytes NF4 double-quantised block statistics (bitsandbytes==0.50.2,
+ * absent here; the reference's call sites are nf4_backend.py:292-298
+ * quantize_4bit(blocksize=64, compress_statistics=True) and
+ * nf4_backend_cuda.py:888-917 matmul_4bit; state layout nf4_backend.py:
+ * 219-240).  The library's published dequantisation of the statistics is a
+ * blockwise dequantize of the uint8 codes with the nested state followed by
+ * `absmax += offset`:
+ *   absmax_j = fp32( fp32(map[q_j] * nested[j / nested_block]) + offset ).
+ * Each operation rounds to fp32 (no contraction: -ffp-contract=off, SSE).
+ */
+void st_oracle_dq_absmax(const uint8_t* q, const float* nested, int64_t blocks, int nested_block,
+                         const float* map256, float offset, float* out) {
+  for (int64_t j = 0; j < blocks; ++j) {
+    float prod = map256[q[j]] * nested[j / nested_block];
+    out[j] = prod + offset;
+  }
+}

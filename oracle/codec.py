@@ -12,6 +12,18 @@ Pinning:
 * ``decode4`` with the NF4 codebook: brute force of all 16 codes x edge
   scales against Python float arithmetic, the invariants |w| <= absmax,
   code 7 -> +0, codes 0/15 -> -/+absmax.
+* ``dq_absmax`` (bitsandbytes' double-quantised NF4 statistics; the library,
+  bitsandbytes==0.50.2, is absent and no reference test holds its bytes):
+  closed forms a plausible mistake fails -- a zero map gives the offset
+  exactly; nested scales that change every 256 blocks (j // 256 against
+  j // 64); an offset added after the rounded product (not folded into the
+  scale); power-of-two operands where every step is exact against Python
+  float arithmetic; ragged block counts.
+* ``dynamic_map`` / ``encode_nf4_dq``: test inputs only (a restatement of
+  bitsandbytes' ``create_dynamic_map`` from its published description and a
+  nearest-entry quantiser).  Parity unpinned: bitsandbytes' own tables and
+  quantiser choices are not reproduced bit for bit; nothing checked against
+  the GPU depends on them (the decode takes the map and codes as data).
 """
 from __future__ import annotations
 
@@ -57,6 +69,8 @@ def lib():
         L.st_oracle_encode_int4.restype = ctypes.c_int
         L.st_oracle_encode_nf4.argtypes = [P, I64, ctypes.c_int, P, P]
         L.st_oracle_encode_nf4.restype = ctypes.c_int
+        L.st_oracle_dq_absmax.argtypes = [P, P, I64, ctypes.c_int, P, ctypes.c_float, P]
+        L.st_oracle_dq_absmax.restype = None
         L.st_oracle_bf16_rne.argtypes = [ctypes.c_float]
         L.st_oracle_bf16_rne.restype = ctypes.c_uint16
         _lib = L
@@ -117,3 +131,69 @@ def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
     u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
     u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
     return u.astype(np.uint16)
+
+
+def dq_absmax(q: np.ndarray, nested: np.ndarray, nested_map: np.ndarray, offset: float,
+              nested_block: int = 256) -> np.ndarray:
+    """fp32 block absmax of a double-quantised NF4 state:
+    fp32(fp32(map[q_j] * nested[j // nested_block]) + offset)."""
+    q = np.ascontiguousarray(q, dtype=np.uint8).reshape(-1)
+    nested = np.ascontiguousarray(nested, dtype=np.float32).reshape(-1)
+    m = np.ascontiguousarray(nested_map, dtype=np.float32).reshape(-1)
+    if m.size != 256 or nested.size < (q.size + nested_block - 1) // nested_block:
+        raise ValueError("nested map must have 256 entries and one scale per nested block")
+    out = np.empty(q.size, dtype=np.float32)
+    lib().st_oracle_dq_absmax(_ptr(q), _ptr(nested), q.size, nested_block, _ptr(m),
+                              float(np.float32(offset)), _ptr(out))
+    return out
+
+
+def dynamic_map() -> np.ndarray:
+    """256-entry signed map of dynamic (tree) quantisation, the nested map
+    bitsandbytes' double quantisation uses (create_dynamic_map(signed=True,
+    max_exponent_bits=7, total_bits=8)): for exponents i = 0..6, the 2**i
+    midpoints of a uniform split of [0.1, 1] scaled by 10**(i - 6), both
+    signs, plus 0 and 1, sorted.  Test input only (see the module header)."""
+    vals = [0.0, 1.0]
+    for i in range(7):
+        b = np.linspace(0.1, 1.0, 2 ** i + 1, dtype=np.float32)
+        mid = ((b[:-1] + b[1:]) / np.float32(2.0)).astype(np.float32)
+        scaled = (mid * np.float32(10.0 ** (i - 6))).astype(np.float32)
+        vals += scaled.tolist() + (-scaled).tolist()
+    assert len(vals) == 256
+    return np.array(sorted(vals), dtype=np.float32)
+
+
+def encode_nf4_dq(w: np.ndarray, nested_map: np.ndarray | None = None):
+    """A double-quantised NF4 state for tests: per 64 flat elements absmax
+    (0 -> every code 7), codes = nearest NF4 entry (ties to the lower code),
+    packed HIGH nibble first into (n+1)//2 bytes; offset = mean absmax; per
+    256 blocks nested = max |absmax - offset| (0 -> 1), code = nearest map
+    entry to (absmax - offset) / nested.  Returns (packed uint8, absmax_q
+    uint8, nested fp32, offset float, nested_map fp32)."""
+    x = np.ascontiguousarray(w, dtype=np.float32).reshape(-1)
+    n = x.size
+    m = dynamic_map() if nested_map is None else np.asarray(nested_map, dtype=np.float32)
+    blocks = (n + 63) // 64
+    xp = np.zeros(blocks * 64, dtype=np.float32)
+    xp[:n] = x
+    xb = xp.reshape(blocks, 64)
+    absmax = np.abs(xb).max(1).astype(np.float32)
+    safe = np.where(absmax > 0, absmax, np.float32(1.0)).astype(np.float32)
+    v = (xb / safe[:, None]).astype(np.float32)
+    codes = np.abs(v[..., None] - NF4_LUT[None, None, :]).argmin(-1).astype(np.uint8)
+    codes[absmax == 0] = 7
+    flat = codes.reshape(-1)[:n]
+    if n % 2:
+        flat = np.concatenate([flat, np.zeros(1, np.uint8)])
+    packed = ((flat[0::2] << 4) | flat[1::2]).astype(np.uint8)
+    offset = np.float32(absmax.mean(dtype=np.float32))
+    centred = (absmax - offset).astype(np.float32)
+    nb = (blocks + 255) // 256
+    cp = np.zeros(nb * 256, dtype=np.float32)
+    cp[:blocks] = centred
+    nested = np.abs(cp.reshape(nb, 256)).max(1).astype(np.float32)
+    nested = np.where(nested > 0, nested, np.float32(1.0)).astype(np.float32)
+    ratio = (cp.reshape(nb, 256) / nested[:, None]).reshape(-1)[:blocks]
+    q = np.abs(ratio[:, None] - m[None, :]).argmin(-1).astype(np.uint8)
+    return packed, q, nested, float(offset), m

@@ -18,6 +18,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libspilltune_hip.so"
 
 ST_OK, ST_EINVAL, ST_EUNSUPPORTED, ST_EDEVICE, ST_EWORKSPACE = range(5)
 ST_FLAG_HI_NIBBLE_FIRST = 1
+ST_FLAG_GROUP64 = 2
 ST_DTYPE_BF16, ST_DTYPE_F32 = 0, 1
 
 _P = ctypes.c_void_p
@@ -30,6 +31,7 @@ _SIGNATURES = {
     "st_abi_version": (_I32, []),
     "st_last_error": (ctypes.c_char_p, []),
     "st_dequant4": (_I32, [_P, _P, _I64, _I32, _P, _I32, _P, _P]),
+    "st_nf4_dq_scales": (_I32, [_P, _P, _P, _F, _I64, _I32, _P, _P]),
     "st_q4_linear_fwd_workspace_bytes": (_I64, [_I64, _I64, _I64]),
     "st_q4_linear_fwd": (_I32, [_P, _I64, _I64, _I64, _P, _P, _I64, _P, _I32, _P, _I64, _P, _I32,
                                 _F, _I32, _P, _P, _I64, _P, _I64, _P, _I64, _P]),

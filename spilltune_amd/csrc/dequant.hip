@@ -11,6 +11,8 @@
 // payload that is not 4-byte aligned or an output that is not 16-byte aligned
 // takes the element-wise kernel.
 // Per element: 0.5 B read + 2 B written (+4/group B scale).
+#include <algorithm>
+
 #include "common.h"
 #include "decode4.h"
 
@@ -65,6 +67,30 @@ __global__ __launch_bounds__(kThreads) void dequant4_scalar(const uint8_t* __res
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// bitsandbytes' double-quantised NF4 statistics (quantize_4bit(blocksize=64,
+// compress_statistics=True), nf4_backend.py:292-298; state layout
+// nf4_backend.py:219-240): the absmax of 64-element block j is a uint8 code
+// into a 256-entry fp32 map, with one fp32 scale per `nested_block` (256)
+// codes and one fp32 offset, and decodes to
+//   absmax_j = fp32( fp32(map[q_j] * nested[j / nested_block]) + offset )
+// -- the product rounded to fp32 before the offset is added (the library's
+// blockwise dequantize followed by its `absmax += offset`).  The fused GEMMs
+// then read these as their fp32 per-64 scales (ST_FLAG_GROUP64).
+__global__ __launch_bounds__(kThreads) void nf4_dq_scales_kernel(
+    const uint8_t* __restrict__ q, const float* __restrict__ nested,
+    const float* __restrict__ map256, float offset, int64_t blocks, int nested_block,
+    float* __restrict__ out) {
+  static_assert(kThreads == 256, "one map entry per thread");
+  __shared__ float map[256];
+  map[threadIdx.x] = map256[threadIdx.x];
+  __syncthreads();
+  for (int64_t j = (int64_t)blockIdx.x * kThreads + threadIdx.x; j < blocks;
+       j += (int64_t)gridDim.x * kThreads) {
+    const float prod = map[q[j]] * nested[j / nested_block];
+    out[j] = prod + offset;
+  }
+}
+
 }  // namespace
 
 namespace st {
@@ -109,3 +135,16 @@ extern "C" int st_dequant4(const uint8_t* payload, const float* scales, int64_t 
                              (hipStream_t)stream);
 }
 
+
+extern "C" int st_nf4_dq_scales(const uint8_t* absmax_q, const float* nested_absmax,
+                                const float* nested_map, float offset, int64_t blocks,
+                                int32_t nested_block, float* scales, st_stream_t stream) {
+  ST_CHECK_ARG(blocks >= 0 && nested_block > 0, "st_nf4_dq_scales: bad sizes");
+  if (blocks == 0) return ST_OK;
+  ST_CHECK_ARG(absmax_q && nested_absmax && nested_map && scales,
+               "st_nf4_dq_scales: NULL device pointer");
+  const int64_t grid = std::min<int64_t>(st::cdiv(blocks, kThreads), 4096);
+  nf4_dq_scales_kernel<<<(unsigned)grid, kThreads, 0, (hipStream_t)stream>>>(
+      absmax_q, nested_absmax, nested_map, offset, blocks, nested_block, scales);
+  return st::check_launch("nf4_dq_scales");
+}

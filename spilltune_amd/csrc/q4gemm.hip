@@ -38,6 +38,9 @@ struct GemmParams {
   int64_t M, P, Q;
   Lut16 lut;
   int hi_first;
+  // log2 of the flat scale group: 7 (128 elements) or 6 (64, ST_FLAG_GROUP64:
+  // bitsandbytes' blocksize).  The register-operand kernel takes 7 only.
+  int gshift;
   uint16_t* C;
   int64_t ldc;
   const uint16_t* R;
@@ -148,19 +151,25 @@ struct EpiIn {
 // Per-wave LDS staging of the vector epilogue (dwords), placed after the LoRA
 // operands the epilogue stages (16-byte aligned).
 constexpr int EPI_STG = 16 * 36;
-// Floats of LDS the LoRA epilogue stages T and the right operand in (none
-// when they are read from global memory)
-template <int BM, int BN>
-__host__ __device__ __forceinline__ int64_t lora_lds_floats(const GemmParams& p) {
-  if (!p.T || p.lora_global) return 0;
-  return (int64_t)BM * (p.lora_cols + 1) + (int64_t)BN * (p.lora_k + 1);
-}
+// Dwords of LDS the LoRA epilogue stages T and the right operand in, rounded
+// to 16 bytes (none when they are read from global memory)
 template <bool DGRAD, int BM, int BN>
 __host__ __device__ __forceinline__ int64_t epi_stage_offset(const GemmParams& p) {
   if (!p.T || p.lora_global) return 0;
   const int64_t f = (int64_t)BM * (p.lora_cols + 1) +
                     (int64_t)BN * (p.lora_k + 1);
   return (f + 3) & ~(int64_t)3;
+}
+// Whether the LoRA operands staged in LDS leave room for what the epilogue
+// cannot do without: the SwiGLU VJP always moves 16-byte rows, so it needs
+// `waves` staging areas after them.  When they do not fit, the GEMM runs on
+// the 128x128 kernel that reads the LoRA operands from global memory.
+template <bool DGRAD, int BM, int BN>
+__host__ __forceinline__ bool lora_staged_fits(const GemmParams& p, int64_t lds_dwords,
+                                               int waves) {
+  if (!p.T || p.lora_global) return true;
+  return epi_stage_offset<DGRAD, BM, BN>(p) + (p.swi_gu ? (int64_t)waves * EPI_STG : 0) <=
+         lds_dwords;
 }
 
 // Epilogue shared by the GEMM kernels: y = bf16(acc) (+ LoRA term, + residual)
@@ -449,10 +458,13 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const f32x16 
     blocks(std::false_type{}, std::false_type{});
 }
 
-// FLAT (4-bit modes, 128x128 tiles): K is not a multiple of 128, so the flat
-// 128-element scale groups of W straddle its rows; every packed word (8
-// weights, which K % 8 == 0 keeps inside one group) then reads its own scale
-// at (flat element index) / 128 and gets its own decode table.
+// FLAT (4-bit modes, 128x128 tiles): K is not a multiple of the scale group
+// (128, or 64 with gshift 6), so the flat groups of W straddle its rows; every
+// packed word (8 weights, which K % 8 == 0 keeps inside one group) then reads
+// its own scale at (flat element index) >> gshift and gets its own decode
+// table.  Otherwise a k-step of 64 lies inside one group: its scale is group
+// kt >> (gshift - 6) of the row, and with 64-element groups every k-step
+// rebuilds the decode table.
 template <int MODE, int BM, int BN, int WAVES, int WAVES_M, bool FLAT = false, bool LG = false>
 __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
   using TL = Tile<MODE, BM, BN, WAVES, WAVES_M>;
@@ -543,17 +555,19 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
   const int drow = tid / DTR, dsub = tid % DTR;       // dgrad mapping
   // FWD_Q4 byte offsets at k = 0 of the thread's packed weights and of its
   // row's first scale (kOOB beyond P).  Unless FLAT, K (= ldw) is a multiple
-  // of 128, so k-step kt adds kt*BK/2 payload bytes and scale group kt/2.
-  // FLAT keeps the flat element index w_eo of the thread's first weight.
+  // of the group, so k-step kt adds kt*BK/2 payload bytes and scale group
+  // kt >> (gshift - 6).  FLAT keeps the flat element index w_eo of the
+  // thread's first weight.
   uint32_t w_po = kOOB, w_so = kOOB, w_eo = kOOB;
   if constexpr (MODE == FWD_Q4) {
     int64_t n = p0 + brow;
     if (n < p.P) {
       w_eo = (uint32_t)(n * p.ldw + bsub * EPT);
       w_po = w_eo >> 1;
-      w_so = (uint32_t)((n * p.ldw) >> 7) * 4;
+      w_so = (uint32_t)((n * p.ldw) >> p.gshift) * 4;
     }
   }
+  const int gstep = p.gshift - 6;  // k-steps per scale group: 1 << gstep
   const bool dcol_ok = p0 + dsub * DE < p.P;
   static_assert(!TL::DGRAD || NT / DTR == BK, "dgrad: one thread row per contraction row");
 
@@ -593,9 +607,9 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
 #pragma unroll
         for (int j = 0; j < NW; ++j)
           w.s[j] = __builtin_bit_cast(
-              float, ld4(rsS, w_eo == kOOB ? kOOB : ((w_eo + (uint32_t)(kt * BK + 8 * j)) >> 7) * 4));
+              float, ld4(rsS, w_eo == kOOB ? kOOB : ((w_eo + (uint32_t)(kt * BK + 8 * j)) >> p.gshift) * 4));
       } else {
-        w.s[0] = __builtin_bit_cast(float, ld4(rsS, w_so + (uint32_t)(kt >> 1) * 4));
+        w.s[0] = __builtin_bit_cast(float, ld4(rsS, w_so + (uint32_t)(kt >> gstep) * 4));
       }
     } else if constexpr (MODE == FWD_BF16) {
 #pragma unroll
@@ -613,7 +627,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
       load_words(ok ? (uint32_t)(e >> 1) : kOOB, w.w);
 #pragma unroll
       for (int j = 0; j < (FLAT ? NW : 1); ++j)
-        w.s[j] = __builtin_bit_cast(float, ld4(rsS, ok ? (uint32_t)(((e + 8 * j) >> 7) * 4) : kOOB));
+        w.s[j] = __builtin_bit_cast(float, ld4(rsS, ok ? (uint32_t)(((e + 8 * j) >> p.gshift) * 4) : kOOB));
       if constexpr (DROT) {  // stored in rotated order, see store_B_part
         st::rot4(w.w, dsub);
         if constexpr (FLAT) st::rot4(w.s, dsub);
@@ -714,7 +728,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
   WRegs w0, w1;
   bf16x8 fa0[FM], fb0[FN], fa1[FM], fb1[FN];
   // new_group: the tile dequantised in this step starts a 128-wide scale group
-  // (even tile index), so its decode table must be rebuilt; odd tiles reuse it.
+  // (even tile index), so its decode table must be rebuilt; odd tiles reuse it
+  // (with 64-wide groups every tile starts one).
   auto body = [&](int kt, WRegs& wnext, WRegs& wfar, bool new_group) {
     const int cur = kt & 1;
     uint4* as_n = As(cur ^ 1);
@@ -724,7 +739,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
     store_A(as_n, xr);
     load_A(kt + 2, xr);
     load_W(kt + 2, wfar);
-    if (new_group || MODE == DGRAD_Q4) prep_B(wnext);
+    if (new_group || MODE == DGRAD_Q4 || gstep == 0) prep_B(wnext);
     read_frags(as, bs, 1, fa1, fb1);
     mfmas(fa0, fb0);
     store_B_part(bs_n, wnext, 0);
@@ -864,9 +879,10 @@ __global__ __launch_bounds__(512) void gemm_ws_kernel(GemmParams p) {
       const int64_t n = p0 + brow;
       if (n < p.P) {
         w_po = (uint32_t)((n * p.ldw + bsub * 32) >> 1);
-        w_so = (uint32_t)((n * p.ldw) >> 7) * 4;
+        w_so = (uint32_t)((n * p.ldw) >> p.gshift) * 4;
       }
     }
+    const int gstep = p.gshift - 6;  // k-steps per scale group: 1 << gstep
     const bool dcol_ok = p0 + bsub * 32 < p.P;
     struct WR {
       uint4 q;
@@ -875,13 +891,13 @@ __global__ __launch_bounds__(512) void gemm_ws_kernel(GemmParams p) {
     auto load_W = [&](int kt, WR& w) {
       if constexpr (MODE == FWD_Q4) {
         w.q = ld16(rsW, w_po + (uint32_t)(kt * (BK / 2)));
-        w.s = __builtin_bit_cast(float, ld4(rsS, w_so + (uint32_t)(kt >> 1) * 4));
+        w.s = __builtin_bit_cast(float, ld4(rsS, w_so + (uint32_t)(kt >> gstep) * 4));
       } else {
         const int64_t n = (int64_t)kt * BK + brow;
         const bool ok = dcol_ok && n < p.Q;
         const int64_t e = n * p.ldw + p0 + bsub * 32;
         w.q = ld16(rsW, ok ? (uint32_t)(e >> 1) : kOOB);
-        w.s = __builtin_bit_cast(float, ld4(rsS, ok ? (uint32_t)((e >> 7) * 4) : kOOB));
+        w.s = __builtin_bit_cast(float, ld4(rsS, ok ? (uint32_t)((e >> p.gshift) * 4) : kOOB));
       }
     };
     Tbl tbl;
@@ -931,7 +947,7 @@ __global__ __launch_bounds__(512) void gemm_ws_kernel(GemmParams p) {
       dma_A(kt + WS_DA - 1);
       __builtin_amdgcn_sched_barrier(0);
       const int nb = u & 1;
-      if (MODE == DGRAD_Q4 || nb == 0) tbl = make_tbl(p.lut, wr[u].s);
+      if (MODE == DGRAD_Q4 || nb == 0 || gstep == 0) tbl = make_tbl(p.lut, wr[u].s);
       store_B(Bs0 + nb * B_ST, wr[u]);
       load_W(kt + 1 + WS_PW, wr[u]);
       __builtin_amdgcn_sched_barrier(0);
@@ -1302,7 +1318,7 @@ int launch_ws(const GemmParams& p, hipStream_t stream) {
   if (tiles > 0x7fffffff) return st::fail(ST_EUNSUPPORTED, "q4gemm: too many tiles");
   if (int rc = check_epilogue_extents(p)) return rc;
   // LoRA operands that do not fit this tile's LDS: the 128x128 kernel
-  if (lora_lds_floats<BM, BN>(p) > (int64_t)WS_DA * BM * BK / 8 * 4)
+  if (!lora_staged_fits<MODE == DGRAD_Q4, BM, BN>(p, (int64_t)WS_DA * BM * BK / 8 * 4, 4))
     return launch<MODE, 128, 128, 4>(p, stream);
   GemmParams q = p;
   if (int rc = choose_epilogue<MODE == DGRAD_Q4, BM, BN>(q, (int64_t)WS_DA * BM * BK / 8 * 4, 4))
@@ -1321,7 +1337,8 @@ int launch_rb(const GemmParams& p, hipStream_t stream) {
     return st::fail(ST_EUNSUPPORTED, "q4gemm: register-operand tile needs K %% %d == 0",
                     RB_ST * BK);
   if (int rc = check_epilogue_extents(p)) return rc;
-  if (lora_lds_floats<BM, BN>(p) > lds_dwords) return launch<FWD_Q4, 128, 128, 4>(p, stream);
+  if (!lora_staged_fits<false, BM, BN>(p, lds_dwords, NT / 64))
+    return launch<FWD_Q4, 128, 128, 4>(p, stream);
   GemmParams q = p;
   if (int rc = choose_epilogue<false, BM, BN>(q, lds_dwords, NT / 64)) return rc;
   if (q.hi_first)
@@ -1345,7 +1362,7 @@ int launch(const GemmParams& p, hipStream_t stream) {
   if constexpr (LG) {
     q.lora_global = q.T ? 1 : 0;
   } else if constexpr (TL::Q4) {
-    if (lora_lds_floats<BM, BN>(q) > (int64_t)TL::LDS_CHUNKS * 4)
+    if (!lora_staged_fits<TL::DGRAD, BM, BN>(q, (int64_t)TL::LDS_CHUNKS * 4, WAVES))
       return launch<MODE, 128, 128, 4, 2, FLAT, true>(p, stream);
   }
   if (int rc = choose_epilogue<TL::DGRAD, BM, BN>(q, (int64_t)TL::LDS_CHUNKS * 4, WAVES)) return rc;
@@ -1395,9 +1412,9 @@ GemmParams column_slice(const GemmParams& p, int64_t c0, int64_t c1) {
   q.C = p.C + c0;
   if (p.R) q.R = p.R + c0;
   q.Wq = p.Wq + c0 * p.ldw / 2;
-  q.Ws = p.Ws + c0 * p.ldw / 128;
+  q.Ws = p.Ws + ((c0 * p.ldw) >> p.gshift);
   q.w_bytes = p.w_bytes - c0 * p.ldw / 2;
-  q.s_bytes = p.s_bytes - c0 * p.ldw / 128 * 4;
+  q.s_bytes = p.s_bytes - ((c0 * p.ldw) >> p.gshift) * 4;
   if (p.T) {
     q.L = p.L + c0 * p.ldl;
     int drop = 0;
@@ -1443,7 +1460,7 @@ int dispatch(const GemmParams& p, hipStream_t stream) {
       // tile, which sums each output in the same order, so a split stays
       // bit-identical to one launch
       const char* rbe = getenv("ST_GEMM_RB");
-      const bool rb = (!rbe || atoi(rbe)) && p.Q % (RB_ST * BK) == 0;
+      const bool rb = (!rbe || atoi(rbe)) && p.Q % (RB_ST * BK) == 0 && p.gshift == 7;
       if (const int64_t c1 = split_column(t, p.M, p.P)) {
         const GemmParams head = column_slice(p, 0, c1), tail = column_slice(p, c1, p.P);
         if (rb) {
@@ -1458,9 +1475,10 @@ int dispatch(const GemmParams& p, hipStream_t stream) {
     if (t == 256) return launch<MODE, 256, 256, 8>(p, stream);
     if (t == 2562) return launch_ws<MODE>(p, stream);
     if constexpr (MODE == FWD_Q4) {
-      if (t == 2566 && p.Q % (RB_ST * BK) == 0) return launch_rb<1, 8>(p, stream);
-      if (t == 2567 && p.Q % (RB_ST * BK) == 0) return launch_rb<1, 4>(p, stream);
-      if (t == 2568 && p.Q % (RB_ST * BK) == 0) return launch_rb<1, 8, 4>(p, stream);
+      const bool rbk = p.Q % (RB_ST * BK) == 0 && p.gshift == 7;
+      if (t == 2566 && rbk) return launch_rb<1, 8>(p, stream);
+      if (t == 2567 && rbk) return launch_rb<1, 4>(p, stream);
+      if (t == 2568 && rbk) return launch_rb<1, 8, 4>(p, stream);
     }
   }
   return launch<MODE, 128, 128, 4>(p, stream);
@@ -1518,6 +1536,7 @@ extern "C" int st_q4_linear_fwd(const uint16_t* x, int64_t M, int64_t K, int64_t
   p.A = x; p.lda = ldx; p.M = M; p.P = N; p.Q = K;
   p.C = y; p.ldc = ldy; p.R = residual; p.ldr = ldr;
   p.hi_first = (flags & ST_FLAG_HI_NIBBLE_FIRST) ? 1 : 0;
+  p.gshift = (flags & ST_FLAG_GROUP64) ? 6 : 7;
   for (int i = 0; i < 16; ++i) p.lut.v[i] = lut16[i];
   if (residual) ST_CHECK_ARG(ldr >= N, "st_q4_linear_fwd: ldr < N");
   if (t) {
@@ -1544,8 +1563,8 @@ extern "C" int st_q4_linear_fwd(const uint16_t* x, int64_t M, int64_t K, int64_t
   (void)workspace; (void)workspace_bytes;
   ST_CHECK_ARG(((uintptr_t)payload & 3u) == 0, "st_q4_linear_fwd: payload not 4-byte aligned");
   p.Wq = payload; p.Ws = scales; p.ldw = K;
-  p.w_bytes = N * K / 2; p.s_bytes = (N * K + 127) / 128 * 4;
-  if (K % 128 == 0 && al16(payload)) return run_gemm(FWD_Q4, p, s);
+  p.w_bytes = N * K / 2; p.s_bytes = st::cdiv(N * K, 1ll << p.gshift) * 4;
+  if (K % (1 << p.gshift) == 0 && al16(payload)) return run_gemm(FWD_Q4, p, s);
   // flat scale groups straddle W's rows (or 16-byte loads would be misaligned):
   // per-word scales on the 128x128 tile
   return launch<FWD_Q4, 128, 128, 4, 2, true>(p, s);
@@ -1573,6 +1592,7 @@ static int dgrad_impl(const uint16_t* dy, int64_t M, int64_t N, int64_t lddy,
     p.swi_gu = gu; p.swi_ld = ldgu; p.swi_I = K;
   }
   p.hi_first = (flags & ST_FLAG_HI_NIBBLE_FIRST) ? 1 : 0;
+  p.gshift = (flags & ST_FLAG_GROUP64) ? 6 : 7;
   for (int i = 0; i < 16; ++i) p.lut.v[i] = lut16[i];
   if (dt) {
     ST_CHECK_ARG(lora_a != nullptr, "st_q4_linear_dgrad: dt without lora_a");
@@ -1589,8 +1609,8 @@ static int dgrad_impl(const uint16_t* dy, int64_t M, int64_t N, int64_t lddy,
   (void)workspace; (void)workspace_bytes;
   ST_CHECK_ARG(((uintptr_t)payload & 3u) == 0, "st_q4_linear_dgrad: payload not 4-byte aligned");
   p.Wq = payload; p.Ws = scales; p.ldw = K;
-  p.w_bytes = N * K / 2; p.s_bytes = (N * K + 127) / 128 * 4;
-  if (K % 128 == 0) return run_gemm(DGRAD_Q4, p, s);
+  p.w_bytes = N * K / 2; p.s_bytes = st::cdiv(N * K, 1ll << p.gshift) * 4;
+  if (K % (1 << p.gshift) == 0) return run_gemm(DGRAD_Q4, p, s);
   // flat scale groups straddle W's rows: per-word scales on the 128x128 tile
   return launch<DGRAD_Q4, 128, 128, 4, 2, true>(p, s);
 }
@@ -1652,6 +1672,8 @@ extern "C" int st_q4_grouped_fwd(const uint16_t* x, int64_t x_rows, int64_t ldx,
   ST_CHECK_ARG(x && offsets && payload && scales && y && lut16, "st_q4_grouped_fwd: NULL pointer");
   ST_CHECK_ARG(K % 128 == 0, "st_q4_grouped_fwd: K must be a multiple of 128, got %lld",
                (long long)K);
+  if (flags & ST_FLAG_GROUP64)
+    return st::fail(ST_EUNSUPPORTED, "st_q4_grouped_fwd: expert weights take 128-element groups");
   ST_CHECK_ARG(ldx % 8 == 0 && ldx >= K && al16(x) && al16(payload),
                "st_q4_grouped_fwd: x rows / payload must be 16-byte aligned");
   ST_CHECK_ARG(gather || x_rows >= rows, "st_q4_grouped_fwd: x_rows < rows without gather");
@@ -1683,6 +1705,7 @@ extern "C" int st_q4_grouped_fwd(const uint16_t* x, int64_t x_rows, int64_t ldx,
   ST_CHECK_ARG(x_rows > 0 && p.a_bytes < (1ll << 31) && N * K * 2 < (1ll << 31),
                "st_q4_grouped_fwd: operands above 2 GiB are not supported");
   p.gather = gather; p.goff = offsets; p.ngroups = groups;
+  p.gshift = 7;
   p.Wq = payload; p.Ws = scales; p.ldw = K;
   p.w_bytes = N * K / 2; p.s_bytes = N * K / 128 * 4;
   p.w_gstride = N * K / 2; p.s_gstride = N * K / 128;
@@ -1700,6 +1723,8 @@ static int grouped_dgrad_impl(const uint16_t* dy, int64_t lddy, int64_t rows, in
   ST_CHECK_ARG(dy && offsets && payload && scales && dx && lut16,
                "st_q4_grouped_dgrad: NULL pointer");
   ST_CHECK_ARG(K % 128 == 0, "st_q4_grouped_dgrad: K must be a multiple of 128");
+  if (flags & ST_FLAG_GROUP64)
+    return st::fail(ST_EUNSUPPORTED, "st_q4_grouped_dgrad: expert weights take 128-element groups");
   ST_CHECK_ARG(N % 8 == 0, "st_q4_grouped_dgrad: N (contraction) must be a multiple of 8");
   ST_CHECK_ARG(lddy % 8 == 0 && lddy >= N && al16(dy), "st_q4_grouped_dgrad: dy rows not 16-byte");
   ST_CHECK_ARG(((uintptr_t)payload & 3u) == 0, "st_q4_grouped_dgrad: payload not 4-byte aligned");
@@ -1726,6 +1751,7 @@ static int grouped_dgrad_impl(const uint16_t* dy, int64_t lddy, int64_t rows, in
   ST_CHECK_ARG(p.a_bytes < (1ll << 31) && N * K * 2 < (1ll << 31),
                "st_q4_grouped_dgrad: operands above 2 GiB are not supported");
   p.goff = offsets; p.ngroups = groups;
+  p.gshift = 7;
   p.Wq = payload; p.Ws = scales; p.ldw = K;
   p.w_bytes = N * K / 2; p.s_bytes = N * K / 128 * 4;
   p.w_gstride = N * K / 2; p.s_gstride = N * K / 128;
@@ -1769,7 +1795,7 @@ extern "C" int st_linear_bf16_fwd(const uint16_t* x, int64_t M, int64_t K, int64
   GemmParams p{};
   p.A = x; p.lda = ldx; p.M = M; p.P = N; p.Q = K;
   p.C = y; p.ldc = ldy;
-  p.Wb = w; p.ldw = ldw;
+  p.Wb = w; p.ldw = ldw; p.gshift = 7;
   p.a_bytes = ((M - 1) * ldx + K) * 2;
   p.w_bytes = ((N - 1) * ldw + K) * 2;
   ST_CHECK_ARG(p.a_bytes < (1ll << 31) && p.w_bytes < (1ll << 31),
@@ -1793,7 +1819,7 @@ extern "C" int st_linear_bf16_dgrad(const uint16_t* dy, int64_t M, int64_t N, in
   GemmParams p{};
   p.A = dy; p.lda = lddy; p.M = M; p.P = K; p.Q = N;
   p.C = dx; p.ldc = lddx;
-  p.Wb = w; p.ldw = ldw;
+  p.Wb = w; p.ldw = ldw; p.gshift = 7;
   p.a_bytes = ((M - 1) * lddy + N) * 2;
   p.w_bytes = ((N - 1) * ldw + K) * 2;
   ST_CHECK_ARG(p.a_bytes < (1ll << 31) && p.w_bytes < (1ll << 31),

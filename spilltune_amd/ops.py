@@ -69,6 +69,11 @@ class Q4Weight:
     def requires_grad(self):
         return False
 
+    @property
+    def group(self):
+        """Flat elements per scale: 128, or 64 with ST_FLAG_GROUP64."""
+        return 64 if self.flags & _lib.ST_FLAG_GROUP64 else GROUP
+
     def lut(self):
         return _lib.lut_array(codebook(self.codec))
 
@@ -76,7 +81,7 @@ class Q4Weight:
         """bf16 copy of the matrix (for checks / reference-side use only)."""
         out = torch.empty(self.shape, dtype=_BF16, device=self.device)
         _lib.call("st_dequant4", _lib.ptr(self.payload), _lib.ptr(self.scales),
-                  self.shape[0] * self.shape[1], GROUP, self.lut(), self.flags,
+                  self.shape[0] * self.shape[1], self.group, self.lut(), self.flags,
                   _lib.ptr(out), _lib.stream_handle(self.device))
         return out
 
@@ -111,7 +116,7 @@ def concat_rows(weights) -> Q4Weight | None:
     if any(w.in_features != K or w.codec != first.codec or w.flags != first.flags
            or len(w.segments) != 1 for w in weights):
         return None
-    if (K % GROUP) != 0 or any(w.out_features % 32 for w in weights[:-1]):
+    if (K % first.group) != 0 or any(w.out_features % 32 for w in weights[:-1]):
         return None  # flat groups must not straddle parts; LoRA segments end on 32-column blocks
     # adjacency must hold inside ONE storage: two allocations that merely lie
     # back to back are not one buffer (the view below would run off the first)
@@ -132,7 +137,7 @@ def concat_rows(weights) -> Q4Weight | None:
     payload = torch.empty(0, dtype=torch.uint8, device=base_p.device).set_(
         base_p.untyped_storage(), base_p.storage_offset(), (rows * K // 2,), (1,))
     scales = torch.empty(0, dtype=_F32, device=base_s.device).set_(
-        base_s.untyped_storage(), base_s.storage_offset(), (rows * K // GROUP,), (1,))
+        base_s.untyped_storage(), base_s.storage_offset(), (rows * K // first.group,), (1,))
     return Q4Weight(payload, scales, (rows, K), first.codec,
                     tuple(w.out_features for w in weights), first.flags)
 

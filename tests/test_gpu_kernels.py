@@ -584,20 +584,27 @@ def test_lora_bwd_dy_matches_per_product(dev, widths, rank):
     assert _lib.query("st_lora_bwd_dy_workspace_bytes", M, N, rank, 2, bad) == 0
 
 
-@pytest.mark.parametrize("I,lora", [(512, True), (384, False), (688, True)])
-def test_swiglu_input_projection_matches_separate_ops(dev, oracle_codec, I, lora):
+@pytest.mark.parametrize("I,lora,r,tile", [(512, True, 8, None), (384, False, 8, None),
+                                         (688, True, 8, None), (512, True, 64, None),
+                                         (512, True, 71, None), (512, True, 80, "2562")])
+def test_swiglu_input_projection_matches_separate_ops(dev, oracle_codec, monkeypatch, I, lora, r,
+                                                      tile):
     """q4_lora_linear(gate|up, W, swiglu=True) == q4_lora_linear(swiglu(gate|up), W):
     the forward and every gradient bit for bit (the dgrad epilogue applies the
     SwiGLU VJP with st_swiglu_bwd's roundings), on the 4-bit path and on the
-    bf16 fallback (I % 128 != 0)."""
+    bf16 fallback (I % 128 != 0).  Ranks 64 and 71 (128x128) and 80 (256x128
+    warp-specialised) leave no LDS for the SwiGLU staging beside the LoRA
+    operands, so that dgrad reads them from global memory."""
+    if tile is not None:
+        monkeypatch.setenv("ST_GEMM_TILE", tile)
     g = torch.Generator().manual_seed(I)
     M, H = 200, 256
     w = (torch.randn(H, I, generator=g) * 0.02).numpy()
     q, _ = q4_from_oracle(oracle_codec, w, "nf4-g128", dev)
     gu0 = torch.randn(M, 2 * I, generator=g).to(BF).to(dev)
     dy = torch.randn(M, H, generator=g).to(BF).to(dev)
-    A = torch.randn(8, I, generator=g) * 0.05
-    Bm = torch.randn(H, 8, generator=g) * 0.05
+    A = torch.randn(r, I, generator=g) * 0.05
+    Bm = torch.randn(H, r, generator=g) * 0.05
     outs = []
     for fused in (True, False):
         gu = gu0.clone().requires_grad_(True)

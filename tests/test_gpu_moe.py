@@ -352,12 +352,25 @@ def test_grouped_lora_epilogue_vs_reference(dev, oracle_codec, monkeypatch, tile
         assert _rel(got, ref) < 4e-3 and bad < 1e-3, (what, _rel(got, ref), bad)
 
 
-@pytest.mark.parametrize("E,H,I,T,k,lora", [(8, 256, 256, 100, 2, True), (16, 384, 128, 333, 4, False),
-                                          (32, 2048, 768, 512, 8, True)])
-def test_grouped_dgrad_swiglu_equals_dgrad_then_swiglu_bwd(dev, oracle_codec, E, H, I, T, k, lora):
+@pytest.mark.parametrize("E,H,I,T,k,r,tile", [
+    (8, 256, 256, 100, 2, 8, None), (16, 384, 128, 333, 4, 0, None), (32, 2048, 768, 512, 8, 8, None),
+    # LoRA operands that fill the tile's LDS up to or past the SwiGLU staging:
+    # 128x128 at 256*(r+1) + 2304 > 18432 dwords for r >= 63, the 256x128
+    # warp-specialised tile at lora_k >= 79
+    (8, 256, 256, 100, 2, 62, None), (8, 256, 256, 100, 2, 63, None), (8, 256, 256, 100, 2, 64, None),
+    (8, 256, 256, 100, 2, 71, None), (8, 256, 256, 100, 2, 72, None),
+    (8, 256, 256, 100, 2, 78, "2562"), (8, 256, 256, 100, 2, 80, "2562"),
+])
+def test_grouped_dgrad_swiglu_equals_dgrad_then_swiglu_bwd(dev, oracle_codec, monkeypatch,
+                                                           E, H, I, T, k, r, tile):
     """st_q4_grouped_dgrad_swiglu (the SwiGLU VJP in the experts' down dgrad
     epilogue) == st_q4_grouped_dgrad then st_swiglu_bwd, bit for bit, with
-    and without the per-expert LoRA term, over ragged expert groups."""
+    and without the per-expert LoRA term, over ragged expert groups.  Ranks
+    whose LoRA operands leave no room for the SwiGLU staging run on the
+    global-operand kernel instead of failing."""
+    if tile is not None:
+        monkeypatch.setenv("ST_GROUPED_TILE", tile)
+    lora = r > 0
     g = torch.Generator().manual_seed(E + H + I)
     H_ = _Held(dev)
     q, _ = _experts(oracle_codec, torch.randn(E, H, I, generator=g) * 0.02, dev)
@@ -370,7 +383,6 @@ def test_grouped_dgrad_swiglu_equals_dgrad_then_swiglu_bwd(dev, oracle_codec, E,
               _lib.ptr(row_token), _lib.ptr(pick_row), _st(dev))
     dy = torch.randn(R, H, generator=g).to(BF).to(dev)
     gu = torch.randn(R, 2 * I, generator=g).to(BF).to(dev)
-    r = 8
     dt = (torch.randn(R, r, generator=g) * 0.1).to(dev) if lora else None
     a = (torch.randn(E, r, I, generator=g) * 0.05).to(dev) if lora else None
     kr = r if lora else 0
@@ -416,6 +428,11 @@ def _oracle_ffn(flat, router, Wgu, Wd, idx, norm, lora):
     (96, 128, 128, 4, 4, True, False, 8),
     (256, 2048, 768, 64, 8, True, True, 8),       # config 4 expert shapes, fewer experts/tokens
     (100, 256, 128, 8, 2, True, True, 80),        # rank 80: 160 gate|up LoRA columns
+    (100, 256, 128, 8, 2, True, True, 62),        # down LoRA beside the SwiGLU staging
+    (100, 256, 128, 8, 2, True, True, 63),
+    (100, 256, 128, 8, 2, True, True, 64),
+    (100, 256, 128, 8, 2, True, True, 71),
+    (100, 256, 128, 8, 2, True, True, 72),
     (80, 256, 128, 8, 2, False, "gate_up", 8),
     (80, 256, 128, 8, 2, True, "down", 8),
 ])
