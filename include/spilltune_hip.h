@@ -321,8 +321,9 @@ int st_flash_attn_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, i
 /* VJP of st_flash_attn_fwd (autograd of dense.py:142-148): from dout
  * (token-major [B,S,H*D]), the forward's out and lse, writes dq [B,H,S,D]
  * and dk, dv [B,Hkv,S,D] head-major bf16 (GQA group sums in fp32, one
- * rounding).  Deterministic: no atomics.  kv_len as in the forward (masked
- * keys get zero dk, dv). */
+ * rounding; with H == Hkv the dK/dV pass writes them directly and the
+ * workspace holds no fp32 partials).  Deterministic: no atomics.  kv_len as
+ * in the forward (masked keys get zero dk, dv). */
 int st_flash_attn_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                       const uint16_t* out, const float* lse, const uint16_t* dout, int64_t B,
                       int64_t S, int64_t H, int64_t Hkv, int64_t D, float scale,

@@ -678,8 +678,9 @@ __device__ __forceinline__ void fa_bwd_dkdv_tile(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, int S, int H, int Hkv,
-    float sl2, float scale, float* __restrict__ dk_part, float* __restrict__ dv_part, int kt,
-    int h, int b, int Sk, uint16_t* lds, float (*lse_s)[QT2], float (*dl_s)[QT2]) {
+    float sl2, float scale, float* __restrict__ dk_part, float* __restrict__ dv_part,
+    uint16_t* __restrict__ dk_out, uint16_t* __restrict__ dv_out, int kt, int h, int b, int Sk,
+    uint16_t* lds, float (*lse_s)[QT2], float (*dl_s)[QT2]) {
   constexpr int DSQ = DQ / 16, DSV = DV / 16, DBQ = DQ / 32, DBV = DV / 32;
   constexpr int LK = KT2 * DQ, LV = KT2 * DV, LQ = QT2 * DQ, LG = QT2 * DV;
   constexpr int NW = dkdv_waves<DQ>(), NTH2 = 64 * NW, QH = 8 / NW;  // query halves per wave
@@ -867,7 +868,12 @@ __device__ __forceinline__ void fa_bwd_dkdv_tile(
           pa[e] = NW == 8 ? dvacc[db][vv] + red[kq * PARTV + (db * 16 + vv) * 64 + lane]
                           : dvacc[db][vv];
         }
-        *(float4*)(dvp + db * 32 + v4 * 8 + g * 4) = a;
+        const int col = db * 32 + v4 * 8 + g * 4;
+        if (dv_out)
+          *(u32x2*)(dv_out + (srow + mykey) * DV + col) =
+              u32x2{st::pack_bf16x2(a.x, a.y), st::pack_bf16x2(a.z, a.w)};
+        else
+          *(float4*)(dvp + col) = a;
       }
   }
   __syncthreads();
@@ -892,7 +898,12 @@ __device__ __forceinline__ void fa_bwd_dkdv_tile(
           pb[e] = (NW == 8 ? dkacc[db][vv] + red[kq * PARTK + (db * 16 + vv) * 64 + lane]
                            : dkacc[db][vv]) * scale;
         }
-        *(float4*)(dkp + db * 32 + v4 * 8 + g * 4) = bq;
+        const int col = db * 32 + v4 * 8 + g * 4;
+        if (dk_out)
+          *(u32x2*)(dk_out + (srow + mykey) * DQ + col) =
+              u32x2{st::pack_bf16x2(bq.x, bq.y), st::pack_bf16x2(bq.z, bq.w)};
+        else
+          *(float4*)(dkp + col) = bq;
       }
   }
 }
@@ -904,8 +915,9 @@ __global__ __launch_bounds__(64 * dkdv_waves<DQ>(), dkdv_waves<DQ>() == 8 ? 2 : 
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, int S, int H, int Hkv,
-    float sl2, float scale, float* __restrict__ dk_part, float* __restrict__ dv_part, int nk,
-    int paired, const int* __restrict__ kvlen) {
+    float sl2, float scale, float* __restrict__ dk_part, float* __restrict__ dv_part,
+    uint16_t* __restrict__ dk_out, uint16_t* __restrict__ dv_out, int nk, int paired,
+    const int* __restrict__ kvlen) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[dkdv_lds_elems<DQ, DV>()];
   __shared__ float lse_s[2][QT2], dl_s[2][QT2];
   const WgIdx w = wg_index(paired ? (nk + 1) / 2 : nk, H);
@@ -916,7 +928,8 @@ __global__ __launch_bounds__(64 * dkdv_waves<DQ>(), dkdv_waves<DQ>() == 8 ? 2 : 
       __syncthreads();  // the previous tile's partial sums still occupy LDS
     }
     fa_bwd_dkdv_tile<DQ, DV>(q, k, v, dout, lse, delta, S, H, Hkv, sl2, scale, dk_part, dv_part,
-                             kt, w.h, w.b, key_len(kvlen, w.b, S), lds, lse_s, dl_s);
+                             dk_out, dv_out, kt, w.h, w.b, key_len(kvlen, w.b, S), lds, lse_s,
+                             dl_s);
   }
 }
 
@@ -956,9 +969,10 @@ int pair_mode(int nq, int64_t heads) {
 int64_t attn_workspace(int64_t B, int64_t S, int64_t H, int64_t Hkv, int64_t DQ, int64_t DV,
                        int backward) {
   if (!backward) return B * Hkv * ((S + 15) & ~15) * DV * 2 + 256;  // key-permuted V^T
-  // Delta [B,H,S] fp32, then fp32 dK and dV partials per query head
+  // Delta [B,H,S] fp32, then fp32 dK and dV partials per query head (none when
+  // every KV head has one query head: the dK/dV pass then writes bf16)
   const int64_t dl = (B * H * S * 4 + 255) / 256 * 256;
-  return 256 + dl + B * H * S * (DQ + DV) * 4;
+  return 256 + dl + (H == Hkv ? 0 : B * H * S * (DQ + DV) * 4);
 }
 
 template <int DQ, int DV>
@@ -1011,11 +1025,14 @@ int attn_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint
                                                 (int)Hkv, sl2, scale, delta, dq, nq, paired, kvlen);
   int rc = st::check_launch("fa_bwd_dq");
   if (rc) return rc;
+  // one query head per KV head (MLA): the pass writes dK and dV in bf16 itself,
+  // the rounding of the group sum over a single head
+  const bool direct = H == Hkv;
   fa_bwd_dkdv<DQ, DV><<<g2, 64 * dkdv_waves<DQ>(), 0, s>>>(
-      q, k, v, dout, lse, delta, (int)S, (int)H, (int)Hkv, sl2, scale, dk_part, dv_part, nk,
-      paired_k, kvlen);
+      q, k, v, dout, lse, delta, (int)S, (int)H, (int)Hkv, sl2, scale, dk_part, dv_part,
+      direct ? dk : nullptr, direct ? dv : nullptr, nk, paired_k, kvlen);
   rc = st::check_launch("fa_bwd_dkdv");
-  if (rc) return rc;
+  if (rc || direct) return rc;
   const int64_t n4 = B * Hkv * S * (DQ + DV) / 4;
   const unsigned blocks = (unsigned)std::min<int64_t>(st::cdiv(n4, NTH), 4096);
   fa_bwd_reduce<<<blocks, NTH, 0, s>>>(dk_part, dv_part, B, S, (int)H, (int)Hkv, DQ, DV, dk, dv);
