@@ -144,7 +144,7 @@ __global__ __launch_bounds__(NTH) void lora_rk(int64_t Mo, int64_t R, int64_t Kc
                                               int64_t ssk, int64_t ssj, int64_t s_bytes,
                                               int64_t klen, float* __restrict__ part) {
   __shared__ __attribute__((aligned(16))) uint16_t Gs[RK_BM * RK_LD];
-  __shared__ __attribute__((aligned(16))) uint16_t Ss[2 * RK_RP * RK_LD];
+  __shared__ __attribute__((aligned(16))) uint16_t Ss[st::RK_SS];
   rk_tile<COL, SK1, NB>(Mo, R, Kc, G, ldg, g_bytes, S, ssk, ssj, s_bytes, klen, part, blockIdx.x,
                         blockIdx.y, Gs, Ss);
 }
@@ -182,7 +182,7 @@ __device__ __forceinline__ int rk_find(const RkBatch& b, int64_t v, bool by_elem
 template <int NB>
 __global__ __launch_bounds__(NTH) void lora_rk_batch(const RkBatch b) {
   __shared__ __attribute__((aligned(16))) uint16_t Gs[RK_BM * RK_LD];
-  __shared__ __attribute__((aligned(16))) uint16_t Ss[2 * RK_RP * RK_LD];
+  __shared__ __attribute__((aligned(16))) uint16_t Ss[st::RK_SS];
   const int i = rk_find(b, blockIdx.x, false);
   const RkProblem& q = b.p[i];
   const int64_t w = blockIdx.x - q.wg0;

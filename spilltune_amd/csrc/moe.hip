@@ -477,8 +477,9 @@ __global__ __launch_bounds__(NTH) void gather_sum(const uint16_t* __restrict__ r
 // ---------------------------------------------------------------- grouped low-rank
 // out[m, j] = alpha * sum_k G[row(m), k] S_g[k, j]       (ROW: rows of one group per tile)
 // out_g[m, j] = alpha * sum_{r in g} G[row(r), m] S[r, j] (COL: contraction over a group)
-// G is bf16 (row gather optional), S fp32 split into bf16 hi + lo for the
-// MFMA; grid.z selects a segment (LoRA of gate | up side by side).
+// G is bf16 (row gather optional), S fp32 split into three bf16 parts for the
+// MFMA (st::split3: the exact fp32 products); grid.z selects a segment (LoRA
+// of gate | up side by side).
 constexpr int GK_BM = 128, GK_BK = 64, GK_RP = 64;
 constexpr int GK_LD = GK_BK + 8;
 
@@ -504,7 +505,7 @@ struct GroupedRk {
 template <bool COL>
 __global__ __launch_bounds__(NTH) void grouped_rk(GroupedRk a) {
   __shared__ __attribute__((aligned(16))) uint16_t Gs[GK_BM * GK_LD];
-  __shared__ __attribute__((aligned(16))) uint16_t Ss[2 * GK_RP * GK_LD];
+  __shared__ __attribute__((aligned(16))) uint16_t Ss[st::RK_SPLIT * GK_RP * GK_LD];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int z = blockIdx.z;
   int grp = 0;
@@ -623,10 +624,11 @@ __global__ __launch_bounds__(NTH) void grouped_rk(GroupedRk a) {
       const int e = tid + i * NTH;
       int kk, j;
       if (a.ssk == 1) { kk = e % GK_BK; j = e / GK_BK; } else { kk = e / RP; j = e % RP; }
-      const uint16_t hb = st::f32_to_bf16(sr[i]);
-      const uint16_t lb = st::f32_to_bf16(sr[i] - st::bf16_to_f32(hb));
+      uint16_t hb, mb, lb;
+      st::split3(sr[i], hb, mb, lb);
       Ss[j * GK_LD + kk] = hb;
-      Ss[(GK_RP + j) * GK_LD + kk] = lb;
+      Ss[(GK_RP + j) * GK_LD + kk] = mb;
+      Ss[(2 * GK_RP + j) * GK_LD + kk] = lb;
     }
   };
 
@@ -645,7 +647,7 @@ __global__ __launch_bounds__(NTH) void grouped_rk(GroupedRk a) {
       for (int c = 0; c < 2; ++c) {
         if (c >= nb) break;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int h = 0; h < st::RK_SPLIT; ++h) {
           const bf16x8 bv = *(const bf16x8*)&Ss[(h * GK_RP + c * 32 + (lane & 31)) * GK_LD + ko];
           acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, acc[c], 0, 0, 0);
         }
@@ -686,7 +688,7 @@ constexpr int GK_IDX = 2048;
 template <bool COL, bool SK1, int NB, bool GATHER>
 __global__ __launch_bounds__(st::RK_NTH) void grouped_rk_stream(GroupedRk a, int64_t g_bytes) {
   __shared__ __attribute__((aligned(16))) uint16_t Gs[st::RK_BM * st::RK_LD];
-  __shared__ __attribute__((aligned(16))) uint16_t Ss[2 * st::RK_RP * st::RK_LD];
+  __shared__ __attribute__((aligned(16))) uint16_t Ss[st::RK_SS];
   __shared__ int idx[COL && GATHER ? GK_IDX : 1];
   const int tid = threadIdx.x;
   const int z = blockIdx.z;

@@ -8,9 +8,12 @@
 // with row(r) = r, or (GATHER) the source row of permuted row r: ROW reads
 // gather[r] (a value outside [0, g_rows) reads as zero); COL reads it from
 // the caller's LDS copy idx[r - idx0] of the gather rows for [kb, ke).
-// S is fp32, split into hi = bf16(s) and lo = bf16(s - hi): bf16 products are
-// exact in fp32, so g*hi + g*lo on v_mfma_f32_32x32x16_bf16 with fp32
-// accumulation carries s to ~16 significant bits at bf16 matrix-core rate.
+// S is fp32, split into three bf16 parts hi = bf16(s), mid = bf16(s - hi),
+// lo = bf16(s - hi - mid) with s == hi + mid + lo exactly (24 significant bits
+// in three pieces of 8; normal range): each bf16 x bf16 product is exact in
+// fp32, so g*hi + g*mid + g*lo on v_mfma_f32_32x32x16_bf16 with fp32
+// accumulation is the fp32 product g*s summed in fp32, at bf16 matrix-core
+// rate.
 //
 // Streaming pipeline: a ring of RK_PF chunks of G (4 x 16 bytes per thread)
 // and S lives in registers; as soon as a chunk is staged into LDS its slot is
@@ -29,9 +32,19 @@ constexpr int RK_NTH = 256;  // 4 waves, 32 output rows each
 constexpr int RK_BM = 128, RK_BK = 64, RK_RP = 64;
 constexpr int RK_LD = RK_BK + 8;  // bf16 per LDS row (144 bytes: 16-byte aligned, bank-spread)
 constexpr int RK_PF = 3;          // chunks of loads in flight per workgroup
+constexpr int RK_SPLIT = 3;       // bf16 parts of each fp32 S value
+constexpr int RK_SS = RK_SPLIT * RK_RP * RK_LD;  // bf16 of the staged S parts
+
+// s = hi + mid + lo exactly for normal-range fp32 s (each part bf16-exact)
+__device__ __forceinline__ void split3(float s, uint16_t& hi, uint16_t& mid, uint16_t& lo) {
+  hi = f32_to_bf16(s);
+  const float r1 = s - bf16_to_f32(hi);
+  mid = f32_to_bf16(r1);
+  lo = f32_to_bf16(r1 - bf16_to_f32(mid));
+}
 
 // Gs: RK_BM * RK_LD bf16 (ROW: G as [m][k] rows; COL: [k][m] in the
-// transposed-operand layout); Ss: 2 * RK_RP * RK_LD bf16 (S as [hi|lo][j][k]).
+// transposed-operand layout); Ss: RK_SS bf16 (S as [hi|mid|lo][j][k]).
 template <bool COL, bool SK1, int NB, bool GATHER>
 __device__ __forceinline__ void rk_accumulate(f32x16 (&acc)[NB], int64_t mend, int64_t R,
                                               int64_t m0, int kb, int ke,
@@ -127,10 +140,11 @@ __device__ __forceinline__ void rk_accumulate(f32x16 (&acc)[NB], int64_t mend, i
 #pragma unroll
     for (int i = 0; i < SIT; ++i) {
       const int kk = s_kk(i), j = s_j(i);
-      const uint16_t hb = f32_to_bf16(sv[i]);
-      const uint16_t lb = f32_to_bf16(sv[i] - bf16_to_f32(hb));
+      uint16_t hb, mb, lb;
+      split3(sv[i], hb, mb, lb);
       Ss[j * RK_LD + kk] = hb;
-      Ss[(RK_RP + j) * RK_LD + kk] = lb;
+      Ss[(RK_RP + j) * RK_LD + kk] = mb;
+      Ss[(2 * RK_RP + j) * RK_LD + kk] = lb;
     }
   };
 
@@ -143,7 +157,7 @@ __device__ __forceinline__ void rk_accumulate(f32x16 (&acc)[NB], int64_t mend, i
 #pragma unroll
       for (int cc = 0; cc < NB; ++cc)
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int h = 0; h < RK_SPLIT; ++h) {
           const bf16x8 b = *(const bf16x8*)&Ss[(h * RK_RP + cc * 32 + (lane & 31)) * RK_LD + ko];
           acc[cc] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[cc], 0, 0, 0);
         }

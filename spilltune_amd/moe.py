@@ -159,23 +159,17 @@ def sigmoid_router_logits(flat: torch.Tensor, router: torch.Tensor) -> torch.Ten
     deepseek.py:117 for bf16 ``flat [T, H]`` and a bf16 or fp32 ``router [E, H]``.
 
     They run in slices of 64 experts on the streaming MFMA rank-r kernel,
-    which splits its fp32 operand into bf16 hi + lo parts (16 significant
-    bits).  A bf16 router passes that split exactly; an fp32 router (the
-    reference keeps DeepSeek routers in fp32) is first split as
-    ``w = bf16(w) + r``, where ``r`` holds at most 16 significant bits, so both
-    parts pass exactly: every product is the fp32 product, summed in fp32."""
+    which splits its fp32 operand into three bf16 parts that sum to it
+    exactly, so every product is the fp32 product, summed in fp32 -- for a
+    bf16 router and for an fp32 one (the reference keeps DeepSeek routers in
+    fp32)."""
     T, H = flat.shape
     E = router.shape[0]
     logits = torch.empty((T, E), dtype=_F32, device=flat.device)
-    parts = [router.float()]
-    if router.dtype == _F32:
-        hi = router.to(_BF16).float()
-        parts = [hi, router - hi]
+    w = router.float()
     for e0 in range(0, E, 64):
         e1 = min(E, e0 + 64)
-        for i, wp in enumerate(parts):
-            lora_gemm(T, e1 - e0, H, flat, H, 1, wp[e0:e1], 1, H, 1.0, logits[:, e0:e1],
-                      accumulate=i > 0)
+        lora_gemm(T, e1 - e0, H, flat, H, 1, w[e0:e1], 1, H, 1.0, logits[:, e0:e1])
     return logits
 
 

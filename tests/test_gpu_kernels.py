@@ -431,20 +431,44 @@ def test_lora_gemm_strided_vs_float64(dev):
             ops.lora_gemm(Mo, No, Kc, a.to(dev), Kc, 1, b.to(dev), No, 1, 0.5, out)
         ref = 0.5 * (a.double() @ b.double())
         torch.cuda.synchronize()
-        torch.testing.assert_close(out.cpu().double(), ref, rtol=1e-5, atol=1e-4 * Kc ** 0.5)
+        # exact products summed in fp32: |error| ~ 5.5e-7 sqrt(Kc) for N(0, 1)
+        # operands (numpy emulation of chunked fp32 sums); 7x margin
+        tol = 4e-6 * Kc ** 0.5
+        torch.testing.assert_close(out.cpu().double(), ref, rtol=1e-5, atol=tol)
         acc = out.clone()
         ops.lora_gemm(Mo, No, Kc, a.to(dev), Kc, 1, b.to(dev), No, 1, 0.5, acc, accumulate=True)
-        torch.testing.assert_close(acc.cpu().double(), 2 * ref, rtol=1e-5, atol=2e-4 * Kc ** 0.5)
+        torch.testing.assert_close(acc.cpu().double(), 2 * ref, rtol=1e-5, atol=2 * tol)
         # fp32 left operand, bf16 right operand (the dA = dT^T x shape), both layouts of b
         a32 = torch.randn(Mo, Kc, generator=g)
         b16 = torch.randn(Kc, No, generator=g).to(BF)
         ref2 = a32.double() @ b16.double()
         out2 = torch.empty(Mo, No, device=dev)
         ops.lora_gemm(Mo, No, Kc, a32.T.contiguous().to(dev), 1, Mo, b16.to(dev), No, 1, 1.0, out2)
-        torch.testing.assert_close(out2.cpu().double(), ref2, rtol=1e-5, atol=1e-4 * Kc ** 0.5)
+        torch.testing.assert_close(out2.cpu().double(), ref2, rtol=1e-5, atol=tol)
         out3 = torch.empty(Mo, No, device=dev)
         ops.lora_gemm(Mo, No, Kc, a32.to(dev), Kc, 1, b16.T.contiguous().to(dev), 1, Kc, 1.0, out3)
-        torch.testing.assert_close(out3.cpu().double(), ref2, rtol=1e-5, atol=1e-4 * Kc ** 0.5)
+        torch.testing.assert_close(out3.cpu().double(), ref2, rtol=1e-5, atol=tol)
+
+
+@pytest.mark.parametrize("Mo,No,Kc", [(2048, 16, 4096), (300, 48, 1024), (16, 64, 2048)])
+def test_lora_gemm_carries_fp32_operands_exactly(dev, Mo, No, Kc):
+    """The fp32 operand keeps all 24 bits: with a one-hot bf16 operand every
+    output is a single product 1 * s, so out == S[perm] bit for bit (a split
+    into two bf16 parts would keep ~16 bits and miss by up to ~2^-17
+    relative).  Both layouts of the fp32 operand."""
+    g = torch.Generator().manual_seed(Mo + Kc)
+    perm = torch.randperm(Kc, generator=g)[:Mo] if Mo <= Kc else torch.randint(0, Kc, (Mo,), generator=g)
+    a = torch.zeros(Mo, Kc, dtype=BF)
+    a[torch.arange(Mo), perm] = 1.0
+    b = torch.randn(Kc, No, generator=g) * torch.exp2(torch.randint(-20, 20, (Kc, No), generator=g).float())
+    out = torch.empty(Mo, No, device=dev)
+    ops.lora_gemm(Mo, No, Kc, a.to(dev), Kc, 1, b.to(dev), No, 1, 1.0, out)
+    out_t = torch.empty(Mo, No, device=dev)
+    ops.lora_gemm(Mo, No, Kc, a.to(dev), Kc, 1, b.T.contiguous().to(dev), 1, Kc, 1.0, out_t)
+    torch.cuda.synchronize()
+    want = b[perm]
+    assert torch.equal(out.cpu().view(torch.int32), want.view(torch.int32))
+    assert torch.equal(out_t.cpu().view(torch.int32), want.view(torch.int32))
 
 
 def test_q4_linear_full_size_vs_torch_fp32(dev):
