@@ -55,6 +55,10 @@ class BlockPlan:
     adapters: dict
     storage_specs: dict | None = None
     buffer_contract: Any = None
+    # this build: a packed pinned image of the block (uint8, plan_layout's
+    # nbytes) filled ahead of the session, e.g. by adapter.ArchiveDenseAdapter
+    # straight from archive files; Q4SlotSession adopts it instead of packing
+    host_image: Any = None
 
 
 @dataclass
@@ -182,8 +186,16 @@ class Q4SlotSession:
         fill = image_loader or pack_image
         self.images = {}
         for b in self.blocks:
-            img = torch.empty(self.layouts[id(b)].nbytes, dtype=torch.uint8, pin_memory=pin)
-            fill(b, self.layouts[id(b)], img)
+            nbytes = self.layouts[id(b)].nbytes
+            img = getattr(b, "host_image", None)
+            if img is not None and image_loader is None:
+                # a prefilled image of this layout (pinned when the session pins)
+                if img.dtype != torch.uint8 or img.numel() != nbytes or img.device.type != "cpu" \
+                        or (pin and not img.is_pinned()):
+                    raise ValueError("block host_image does not match its slot layout")
+            else:
+                img = torch.empty(nbytes, dtype=torch.uint8, pin_memory=pin)
+                fill(b, self.layouts[id(b)], img)
             self.images[id(b)] = img
         self.pinned_capacity_bytes = self.host_bytes if pin else 0
         self.upload_capacity = 0
