@@ -885,6 +885,51 @@ def moe_cpu_baseline(router, gate_up, down, lgu, ld, tokens, min_seconds=10.0):
                       f"layer, oracle/moe.py on {cores} host cores, {dt:.1f} s"}
 
 
+def hipblaslt_bench(args):
+    """The eight GEMM shapes of the Llama-3-8B layer step (M = 2048 tokens) in
+    plain bf16 through torch (hipBLASLt), without any dequantisation: the
+    library ceiling the fused 4-bit kernels are compared with.  Forward
+    y = x W^T (F.linear), input gradient dx = dy W; W random bf16 [N, K]."""
+    import torch
+    import torch.nn.functional as F
+    c = CONFIGS["llama8b"]
+    M, H, I = c["B"] * c["S"], c["H"], c["I"]
+    qkv = (c["heads"] + 2 * c["kv"]) * c["D"]
+    shapes = [("fwd q|k|v", qkv, H), ("fwd o", H, H), ("fwd gate|up", 2 * I, H), ("fwd down", H, I),
+              ("dgrad q|k|v", qkv, H), ("dgrad o", H, H), ("dgrad gate|up", 2 * I, H),
+              ("dgrad down", H, I)]
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(1)
+    out = []
+    for name, N, K in shapes:
+        W = (torch.randn(N, K, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+        if name.startswith("fwd"):
+            a = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+            fn = lambda: F.linear(a, W)  # noqa: E731
+        else:
+            a = torch.randn(M, N, device=dev, generator=g).to(torch.bfloat16)
+            fn = lambda: torch.matmul(a, W)  # noqa: E731
+        for _ in range(args.warmup):
+            fn()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        ev[0].record()
+        for _ in range(args.steps):
+            fn()
+        ev[1].record()
+        torch.cuda.synchronize()
+        ms = ev[0].elapsed_time(ev[1]) / args.steps
+        tf = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+        log(f"  hipBLASLt bf16 {name:14s} M={M} N={N} K={K}: {ms * 1e3:7.1f} us, {tf:6.0f} TFLOP/s "
+            f"({tf / PEAK_BF16_TFLOPS:.1%})")
+        out.append({"gemm": name, "M": M, "N": N, "K": K, "us": round(ms * 1e3, 1),
+                    "tflops": round(tf, 1), "frac": round(tf / PEAK_BF16_TFLOPS, 4)})
+    total_us = sum(r["us"] for r in out)
+    print(json.dumps({"metric": "hipBLASLt bf16 (torch) time of the layer step's eight GEMM shapes",
+                      "unit": "us", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+                      "dtype": "bf16", "data": "synthetic", "total_us": round(total_us, 1),
+                      "gemms": out}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -892,7 +937,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="llama8b",
                     choices=sorted(CONFIGS) + ["moe", "deepseek-moe", "deepseek", "qwen3-stream",
-                                               "memory"])
+                                               "memory", "hipblaslt"])
     ap.add_argument("--cpu-tokens", type=int, default=2048)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -924,6 +969,9 @@ def main():
         return
     if args.config == "memory":
         memory_bench(args)
+        return
+    if args.config == "hipblaslt":
+        hipblaslt_bench(args)
         return
     if args.config == "deepseek-moe":
         deepseek_moe_bench(args)

@@ -102,7 +102,11 @@ int st_nf4_dq_scales(const uint8_t* absmax_q, const float* nested_absmax, const 
  * bitsandbytes' NF4 blocksize, scales from st_nf4_dq_scales), dequantised
  * inside the GEMM and never written to HBM as bf16 (K % group != 0, where
  * the groups straddle W's rows: each packed word reads its own group's
- * scale).  K % 8 == 0.  `workspace` is not used (the query returns 0).
+ * scale).  K % 8 == 0.  `workspace`: split-K partials for shapes whose
+ * 256x128 tiles leave CUs idle on a long contraction (fp32 [splits, M, N],
+ * summed in split order by a second kernel before the epilogue); the query
+ * returns the bytes it takes, 0 when the shape runs unsplit.  Without that
+ * workspace the call runs unsplit (same epilogue, another fp32 order).
  * `t` = x_f32 A_cat^T from st_lora_gemm ([M, nseg*rank] fp32) or NULL for no
  * LoRA; any rank >= 1 (up to 65536 T columns).  The epilogue stages t and
  * lora_b in the tile's LDS; when they do not fit (more than 64 T columns on
@@ -130,6 +134,7 @@ int st_q4_linear_fwd(const uint16_t* x, int64_t M, int64_t K, int64_t ldx,
  * dt == NULL for no LoRA term; 1 <= lora_k <= 65536 (operands beyond the
  * tile's LDS as in the forward).  W [N,K] as above,
  * dequantised into LDS in its natural orientation and read transposed.
+ * `workspace` as in the forward (the split runs over N).
  */
 int64_t st_q4_linear_dgrad_workspace_bytes(int64_t M, int64_t N, int64_t K);
 int st_q4_linear_dgrad(const uint16_t* dy, int64_t M, int64_t N, int64_t lddy,

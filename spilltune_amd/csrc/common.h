@@ -137,6 +137,26 @@ __device__ __forceinline__ int64_t xcd_remap(int64_t b, int64_t nb) {
   return (b % 8) * (nb / 8) + b / 8;
 }
 
+// Tile (row tile mt, column tile pt) of logical tile t in a grouped raster:
+// logical tiles walk `gm` row tiles for each column tile before the next
+// column tile, group after group of gm row tiles (gm <= 1: row-major, the
+// column tile fastest).  With xcd_remap, an XCD's consecutive logical tiles
+// then cover gm row panels x (its share / gm) column panels, so its L2 serves
+// each A panel and each W panel to several of its CUs.
+__device__ __forceinline__ void raster(int64_t t, int64_t tiles_m, int64_t tiles_p, int gm,
+                                       int64_t& mt, int64_t& pt) {
+  if (gm <= 1) {
+    mt = t / tiles_p;
+    pt = t % tiles_p;
+    return;
+  }
+  const int64_t per = (int64_t)gm * tiles_p;
+  const int64_t m0 = t / per * gm, r = t % per;
+  const int64_t h = tiles_m - m0 < gm ? tiles_m - m0 : gm;  // rows of a short last group
+  mt = m0 + r % h;
+  pt = r / h;
+}
+
 // Grouped (per-expert) row tiles: group g owns rows [off[g], off[g+1]) and
 // cdiv(rows_g, BM) tiles, numbered consecutively over the groups.  Maps tile
 // `slot` to its group, first row and the group's row end (clamped to `rows`).

@@ -71,6 +71,14 @@ struct GemmParams {
   // and moves 16-byte rows (C, residual, gate|up 16-byte aligned with row
   // strides and P multiples of 8, and the staging fits the tile's LDS)
   int vec_epi;
+  // row tiles per raster group (st::raster); grouped launches take 1
+  int raster_m;
+  // split-K (gemm_ws_kernel, dense launches): the grid holds `splits` copies
+  // of the tiles, copy s taking contraction k-steps [s*ks_len, (s+1)*ks_len),
+  // and each writes its raw fp32 sums to part[s][M][P] (no epilogue);
+  // splitk_epilogue then sums them in split order and applies the epilogue
+  float* part;
+  int splits, ks_len;
 };
 
 // LDS tile rows hold 64 bf16 (8 chunks of 16 bytes) plus one chunk of padding:
@@ -476,11 +484,13 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmParams p) {
   const int wm = wave / TL::WAVES_N, wn = wave % TL::WAVES_N;
   const int64_t tiles_p = st::cdiv(p.P, BN);
   const int64_t t = st::xcd_remap(blockIdx.x, gridDim.x);
-  const int64_t p0 = (t % tiles_p) * BN;
-  int64_t m0 = (t / tiles_p) * BM, mend = p.M;
+  int64_t mt, pt;
+  st::raster(t, st::cdiv(p.M, BM), tiles_p, p.raster_m, mt, pt);
+  const int64_t p0 = pt * BN;
+  int64_t m0 = mt * BM, mend = p.M;
   int grp = 0;
   if (p.goff) {  // whole workgroup leaves together, before any barrier
-    if (!st::find_group(p.goff, p.ngroups, BM, t / tiles_p, p.M, grp, m0, mend)) return;
+    if (!st::find_group(p.goff, p.ngroups, BM, mt, p.M, grp, m0, mend)) return;
   }
   const int KT = (int)st::cdiv(p.Q, BK);
 
@@ -826,14 +836,28 @@ __global__ __launch_bounds__(512) void gemm_ws_kernel(GemmParams p) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t tiles_p = st::cdiv(p.P, BN);
-  const int64_t t = st::xcd_remap(blockIdx.x, gridDim.x);
-  const int64_t p0 = (t % tiles_p) * BN;
-  int64_t m0 = (t / tiles_p) * BM, mend = p.M;
+  int64_t t = st::xcd_remap(blockIdx.x, gridDim.x);
+  // split-K: split s covers contraction [q0, q0 + qlen) (q0 a multiple of
+  // 4*BK, so ring slots and scale groups keep their phase); the operands'
+  // bases move by q0 and every index below stays relative to it
+  int64_t q0 = 0, qlen = p.Q;
+  int split = 0;
+  if (p.splits > 1) {
+    const int64_t nt = st::cdiv(p.M, BM) * tiles_p;
+    split = (int)(t / nt);
+    t -= split * nt;
+    q0 = (int64_t)split * p.ks_len * BK;
+    qlen = p.Q - q0 < (int64_t)p.ks_len * BK ? p.Q - q0 : (int64_t)p.ks_len * BK;
+  }
+  int64_t mt, pt;
+  st::raster(t, st::cdiv(p.M, BM), tiles_p, p.raster_m, mt, pt);
+  const int64_t p0 = pt * BN;
+  int64_t m0 = mt * BM, mend = p.M;
   int grp = 0;
   if (p.goff) {  // whole workgroup leaves together, before any barrier
-    if (!st::find_group(p.goff, p.ngroups, BM, t / tiles_p, p.M, grp, m0, mend)) return;
+    if (!st::find_group(p.goff, p.ngroups, BM, mt, p.M, grp, m0, mend)) return;
   }
-  const int KT = (int)st::cdiv(p.Q, BK);
+  const int KT = (int)st::cdiv(qlen, BK);
   uint4* const As0 = ldsA;  // stage a at As0 + a*A_ST
   uint4* const Bs0 = ldsB;  // buffer b at Bs0 + b*B_ST
   const float* Lg = p.L + grp * p.l_gstride;
@@ -843,9 +867,12 @@ __global__ __launch_bounds__(512) void gemm_ws_kernel(GemmParams p) {
   if (wave >= 4) {
     // ------------------------------------------------------------ producer
     const int pw = wave - 4, ptid = tid - NP;
-    const auto rsA = make_rsrc(p.A, p.a_bytes);
-    const auto rsW = make_rsrc(p.Wq + grp * p.w_gstride, p.w_bytes);
-    const auto rsS = make_rsrc(p.Ws + grp * p.s_gstride, p.s_bytes);
+    // contraction offset of the W operand: along its rows (FWD) or over them
+    const int64_t wq0 = MODE == FWD_Q4 ? q0 : q0 * p.ldw;
+    const auto rsA = make_rsrc(p.A + q0, p.a_bytes - q0 * 2);
+    const auto rsW = make_rsrc(p.Wq + grp * p.w_gstride + wq0 / 2, p.w_bytes - wq0 / 2);
+    const auto rsS = make_rsrc(p.Ws + grp * p.s_gstride + (wq0 >> p.gshift),
+                               p.s_bytes - (wq0 >> p.gshift) * 4);
     // A: producer wave pw moves rows 64*pw + 8*q + l/8 (q < 8) of each stage;
     // lane l fills position l%8 of its row, i.e. chunk (l%8) ^ ((row>>1) & 7).
     uint32_t a_row[8];
@@ -862,7 +889,7 @@ __global__ __launch_bounds__(512) void gemm_ws_kernel(GemmParams p) {
       uint4* st_base = As0 + (kt % WS_DA) * A_ST;
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
-        const bool ok = a_row[q] != kOOB && kt * BK + a_c[q] * 8 < p.Q;
+        const bool ok = a_row[q] != kOOB && kt * BK + a_c[q] * 8 < qlen;
         const uint32_t off = ok ? a_row[q] + (uint32_t)(kt * BK * 2) : kOOB;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             rsA, (__attribute__((address_space(3))) void*)(st_base + (8 * pw + q) * 64), 16, off,
@@ -894,7 +921,7 @@ __global__ __launch_bounds__(512) void gemm_ws_kernel(GemmParams p) {
         w.s = __builtin_bit_cast(float, ld4(rsS, w_so + (uint32_t)(kt >> gstep) * 4));
       } else {
         const int64_t n = (int64_t)kt * BK + brow;
-        const bool ok = dcol_ok && n < p.Q;
+        const bool ok = dcol_ok && n < qlen;
         const int64_t e = n * p.ldw + p0 + bsub * 32;
         w.q = ld16(rsW, ok ? (uint32_t)(e >> 1) : kOOB);
         w.s = __builtin_bit_cast(float, ld4(rsS, ok ? (uint32_t)((e >> p.gshift) * 4) : kOOB));
@@ -1042,8 +1069,72 @@ __global__ __launch_bounds__(512) void gemm_ws_kernel(GemmParams p) {
   }
   // every wave's last LDS reads are done before the epilogue reuses LDS
   __syncthreads();
+  if (p.splits > 1) {  // raw fp32 sums of this split; splitk_epilogue does the rest
+    if (wave < 4) {
+      const auto rsP = make_rsrc(p.part + (int64_t)split * p.M * p.P, p.M * p.P * 4);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int64_t col = p0 + wn * WN + j * 32 + (lane & 31);
+          const int64_t rb = m0 + wm * WM + i * 32 + (lane >> 5) * 4;
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int64_t row = rb + (v >> 2) * 8 + (v & 3);
+            const bool ok = row < mend && col < p.P;
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][j][v]), rsP,
+                                                  (int)(ok ? (uint32_t)((row * p.P + col) * 4) : kOOB),
+                                                  0, 0);
+          }
+        }
+    }
+    return;
+  }
   gemm_epilogue<MODE == DGRAD_Q4, BM, BN, NT, FM, FN, WM, WN>(p, acc, ldsA, m0, mend, p0, wm, wn,
                                                               tid, lane, wave < 4, Lg);
+}
+
+// Split-K epilogue: y[m, n] = the GEMM epilogue of sum_s part[s][m][n], the
+// splits summed in ascending order: y = bf16(sum), + the LoRA term
+// (forward: bf16(y + scale * sum_j T[m, seg(n)*r + j] B[n, j]); dgrad:
+// bf16(y + bf16(sum_j dT[m, j] A[j, n]))), + the residual (bf16(R + y)).
+// One thread per 4 consecutive outputs of a row (P % 4 == 0, checked by the
+// host), fp32 partials read as 16-byte vectors.
+template <bool DGRAD>
+__global__ __launch_bounds__(256) void splitk_epilogue(GemmParams p) {
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t per = p.P / 4;
+  if (q >= p.M * per) return;
+  const int64_t m = q / per, n0 = (q % per) * 4;
+  const int64_t mp = p.M * p.P;
+  float a[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < p.splits; ++s) {
+    const float4 v = *(const float4*)(p.part + s * mp + m * p.P + n0);
+    a[0] += v.x; a[1] += v.y; a[2] += v.z; a[3] += v.w;
+  }
+  uint16_t out[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int64_t n = n0 + e;
+    float y = st::bf16r(a[e]);
+    if (p.T) {
+      int coff = 0;
+      if (!DGRAD)
+        for (int i = 0; i < p.nseg; ++i) coff += p.seg_end[i] <= n ? p.lora_k : 0;
+      float la = 0.f;
+      for (int j = 0; j < p.lora_k; ++j) {
+        const float tv = p.T[m * p.ldt + coff + j];
+        const float lv = DGRAD ? p.L[(int64_t)j * p.ldl + n] : p.L[n * p.ldl + j];
+        la += tv * lv;
+      }
+      y = DGRAD ? st::bf16r(y + st::bf16r(la)) : st::bf16r(y + la * p.lora_scale);
+    }
+    if (p.R) y = st::bf16r(st::bf16_to_f32(p.R[m * p.ldr + n]) + y);
+    out[e] = st::f32_to_bf16(y);
+  }
+  uint16_t* c = p.C + m * p.ldc + n0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) c[e] = out[e];
 }
 
 // Register-operand forward, 256x256 tile.  In the forward the MFMA B operand
@@ -1105,11 +1196,13 @@ __global__ __launch_bounds__(64 * WAVES, FM == 4 ? 4 : 1) void gemm_rb_kernel(Ge
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t tiles_p = st::cdiv(p.P, BN);
   const int64_t t = st::xcd_remap(blockIdx.x, gridDim.x);
-  const int64_t p0 = (t % tiles_p) * BN;
-  int64_t m0 = (t / tiles_p) * BM, mend = p.M;
+  int64_t mt, pt;
+  st::raster(t, st::cdiv(p.M, BM), tiles_p, p.raster_m, mt, pt);
+  const int64_t p0 = pt * BN;
+  int64_t m0 = mt * BM, mend = p.M;
   int grp = 0;
   if (p.goff) {  // grouped (per-expert) rows: the whole workgroup leaves together
-    if (!st::find_group(p.goff, p.ngroups, BM, t / tiles_p, p.M, grp, m0, mend)) return;
+    if (!st::find_group(p.goff, p.ngroups, BM, mt, p.M, grp, m0, mend)) return;
   }
   const int KT = (int)(p.Q / BK);
   const auto rsA = make_rsrc(p.A, p.a_bytes);
@@ -1287,6 +1380,20 @@ int choose_epilogue(GemmParams& p, int64_t lds_dwords, int waves) {
   return ST_OK;
 }
 
+// Row tiles per raster group (st::raster) of a dense launch: 4, so each XCD's
+// 32 CUs take 4 row panels x 8 column panels at a time and its L2 serves each
+// A and W panel to several CUs (with row-major order one A panel and 32 W
+// panels: every XCD streamed all of W).  Measured on the Llama-8B layer step:
+// 3.84-3.86 ms with 1, 3.76 ms with 2 or 4, 3.78 ms with 8; every fused GEMM
+// of the step 1-3% faster.  ST_GEMM_RASTER overrides it; grouped launches
+// keep their expert order.
+int raster_choice(const GemmParams& p) {
+  if (p.goff) return 1;
+  const char* env = getenv("ST_GEMM_RASTER");
+  const int g = env ? atoi(env) : 4;
+  return g > 1 ? g : 1;
+}
+
 // Row-tile slots of a launch: grouped launches (per-expert row ranges) take
 // sum_g cdiv(rows_g, BM) <= cdiv(rows, BM) + groups; slots past the last
 // group's tiles exit at once.
@@ -1321,6 +1428,7 @@ int launch_ws(const GemmParams& p, hipStream_t stream) {
   if (!lora_staged_fits<MODE == DGRAD_Q4, BM, BN>(p, (int64_t)WS_DA * BM * BK / 8 * 4, 4))
     return launch<MODE, 128, 128, 4>(p, stream);
   GemmParams q = p;
+  q.raster_m = raster_choice(q);
   if (int rc = choose_epilogue<MODE == DGRAD_Q4, BM, BN>(q, (int64_t)WS_DA * BM * BK / 8 * 4, 4))
     return rc;
   gemm_ws_kernel<MODE><<<(unsigned)tiles, 512, 0, stream>>>(q);
@@ -1340,6 +1448,7 @@ int launch_rb(const GemmParams& p, hipStream_t stream) {
   if (!lora_staged_fits<false, BM, BN>(p, lds_dwords, NT / 64))
     return launch<FWD_Q4, 128, 128, 4>(p, stream);
   GemmParams q = p;
+  q.raster_m = raster_choice(q);
   if (int rc = choose_epilogue<false, BM, BN>(q, lds_dwords, NT / 64)) return rc;
   if (q.hi_first)
     gemm_rb_kernel<FN, WAVES, true, FM><<<(unsigned)tiles, NT, 0, stream>>>(q);
@@ -1356,6 +1465,7 @@ int launch(const GemmParams& p, hipStream_t stream) {
   if (int rc = check_epilogue_extents(p)) return rc;
   using TL = Tile<MODE, BM, BN, WAVES, WAVES_M>;
   GemmParams q = p;
+  q.raster_m = raster_choice(q);
   // the LoRA epilogue stages T and the right operand in the tile's LDS when
   // they fit; otherwise the 128x128 kernel built to read them from global
   // memory runs the GEMM
@@ -1449,6 +1559,74 @@ int64_t split_column(int t, int64_t M, int64_t P) {
   return split < (double)st::cdiv(tiles, cus) ? c1 : 0;
 }
 
+// Split-K of a dense 4-bit GEMM whose 256x128 warp-specialised tiles leave
+// CUs idle for a long contraction (DeepSeek MLA: kv_b's input gradient, 512
+// outputs from 32768; q_b's, 1536 from 24576).  Cost model per CU in k-steps:
+// rounds(tiles * splits) * (k-steps per split + 8 for each workgroup's
+// prologue and epilogue); splits that cut it below 3/4 of the unsplit cost.
+// K-steps per split are a multiple of 4 (the ring phase of gemm_ws_kernel).
+// Only GEMMs of 8 GFLOP or more split (smaller ones are latency-bound
+// either way), and none while ST_GEMM_TILE pins a tile for the tests.
+// ST_GEMM_SPLITK=0 disables, =n asks for n splits.
+struct SplitPlan {
+  int splits = 1, ks_len = 0;
+};
+SplitPlan split_plan(int64_t M, int64_t P, int64_t Q) {
+  SplitPlan plan;
+  const char* env = getenv("ST_GEMM_SPLITK");
+  if (env && atoi(env) == 0) return plan;
+  const int64_t tiles = st::cdiv(M, 256) * st::cdiv(P, 128), KT = st::cdiv(Q, BK);
+  const int64_t cus = cu_count();
+  if (KT < 16 || P % 4 || M * P * 4 >= (1ll << 31)) return plan;
+  if (!env && (getenv("ST_GEMM_TILE") || 2.0 * (double)M * (double)P * (double)Q < 8e9))
+    return plan;
+  auto shape = [&](int64_t s, int64_t& len) {
+    len = st::cdiv(st::cdiv(KT, s), 4) * 4;
+    return st::cdiv(KT, len);
+  };
+  auto cost = [&](int64_t s) {
+    int64_t len;
+    const int64_t ns = shape(s, len);
+    return st::cdiv(tiles * ns, cus) * (len + 8);
+  };
+  int64_t best = 1, bc = cost(1);
+  if (env) {
+    best = atoi(env);
+  } else {
+    if (tiles >= cus) return plan;
+    for (int64_t s = 2; s <= 32; ++s)
+      if (cost(s) < bc) bc = cost(s), best = s;
+    if (best == 1 || bc * 4 > cost(1) * 3) return plan;
+  }
+  int64_t len;
+  const int64_t ns = shape(best, len);
+  if (ns <= 1) return plan;
+  plan.splits = (int)ns;
+  plan.ks_len = (int)len;
+  return plan;
+}
+
+int64_t split_workspace(const SplitPlan& plan, int64_t M, int64_t P) {
+  return plan.splits > 1 ? (int64_t)plan.splits * M * P * 4 + 256 : 0;
+}
+
+// Split-K launch: the warp-specialised kernel writes each split's fp32 sums,
+// splitk_epilogue sums them in split order and applies the epilogue.
+template <int MODE>
+int launch_ws_split(GemmParams p, const SplitPlan& plan, void* workspace, hipStream_t stream) {
+  p.part = (float*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
+  p.splits = plan.splits;
+  p.ks_len = plan.ks_len;
+  p.raster_m = raster_choice(p);
+  const int64_t tiles = st::cdiv(p.M, 256) * st::cdiv(p.P, 128) * plan.splits;
+  if (tiles > 0x7fffffff) return st::fail(ST_EUNSUPPORTED, "q4gemm: too many tiles");
+  gemm_ws_kernel<MODE><<<(unsigned)tiles, 512, 0, stream>>>(p);
+  if (int rc = st::check_launch("q4gemm split-K")) return rc;
+  const int64_t threads = p.M * (p.P / 4);
+  splitk_epilogue<MODE == DGRAD_Q4><<<(unsigned)st::cdiv(threads, 256), 256, 0, stream>>>(p);
+  return st::check_launch("q4gemm split-K epilogue");
+}
+
 template <int MODE>
 int dispatch(const GemmParams& p, hipStream_t stream) {
   // the dense-W fallbacks (K not a multiple of 128) always use 128x128 tiles
@@ -1501,13 +1679,13 @@ bool al16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 // kernels), so the fused linears take no workspace; the queries stay for
 // callers that size one.
 extern "C" int64_t st_q4_linear_fwd_workspace_bytes(int64_t M, int64_t N, int64_t K) {
-  (void)M; (void)N; (void)K;
-  return 0;
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  return split_workspace(split_plan(M, N, K), M, N);
 }
 
 extern "C" int64_t st_q4_linear_dgrad_workspace_bytes(int64_t M, int64_t N, int64_t K) {
-  (void)M; (void)N; (void)K;
-  return 0;
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  return split_workspace(split_plan(M, K, N), M, K);
 }
 
 static int check_lora_common(int64_t rank, int64_t cols) {
@@ -1560,11 +1738,16 @@ extern "C" int st_q4_linear_fwd(const uint16_t* x, int64_t M, int64_t K, int64_t
   p.a_bytes = ((M - 1) * ldx + K) * 2;
   ST_CHECK_ARG(p.a_bytes < (1ll << 31) && N * K * 2 < (1ll << 31),
                "st_q4_linear_fwd: operands above 2 GiB are not supported");
-  (void)workspace; (void)workspace_bytes;
   ST_CHECK_ARG(((uintptr_t)payload & 3u) == 0, "st_q4_linear_fwd: payload not 4-byte aligned");
   p.Wq = payload; p.Ws = scales; p.ldw = K;
   p.w_bytes = N * K / 2; p.s_bytes = st::cdiv(N * K, 1ll << p.gshift) * 4;
-  if (K % (1 << p.gshift) == 0 && al16(payload)) return run_gemm(FWD_Q4, p, s);
+  if (K % (1 << p.gshift) == 0 && al16(payload)) {
+    // split-K when the caller brought the workspace the query asks for
+    const SplitPlan plan = split_plan(M, N, K);
+    if (plan.splits > 1 && workspace && workspace_bytes >= split_workspace(plan, M, N))
+      return launch_ws_split<FWD_Q4>(p, plan, workspace, s);
+    return run_gemm(FWD_Q4, p, s);
+  }
   // flat scale groups straddle W's rows (or 16-byte loads would be misaligned):
   // per-word scales on the 128x128 tile
   return launch<FWD_Q4, 128, 128, 4, 2, true>(p, s);
@@ -1606,11 +1789,16 @@ static int dgrad_impl(const uint16_t* dy, int64_t M, int64_t N, int64_t lddy,
   p.a_bytes = ((M - 1) * lddy + N) * 2;
   ST_CHECK_ARG(p.a_bytes < (1ll << 31) && N * K * 2 < (1ll << 31),
                "st_q4_linear_dgrad: operands above 2 GiB are not supported");
-  (void)workspace; (void)workspace_bytes;
   ST_CHECK_ARG(((uintptr_t)payload & 3u) == 0, "st_q4_linear_dgrad: payload not 4-byte aligned");
   p.Wq = payload; p.Ws = scales; p.ldw = K;
   p.w_bytes = N * K / 2; p.s_bytes = st::cdiv(N * K, 1ll << p.gshift) * 4;
-  if (K % (1 << p.gshift) == 0) return run_gemm(DGRAD_Q4, p, s);
+  if (K % (1 << p.gshift) == 0) {
+    // split-K (not with the SwiGLU VJP) when the caller brought the workspace
+    const SplitPlan plan = split_plan(M, K, N);
+    if (!gu && plan.splits > 1 && workspace && workspace_bytes >= split_workspace(plan, M, K))
+      return launch_ws_split<DGRAD_Q4>(p, plan, workspace, s);
+    return run_gemm(DGRAD_Q4, p, s);
+  }
   // flat scale groups straddle W's rows: per-word scales on the 128x128 tile
   return launch<DGRAD_Q4, 128, 128, 4, 2, true>(p, s);
 }

@@ -352,6 +352,8 @@ class _Q4LoRALinear(torch.autograd.Function):
             # T = x_f32 A_cat^T   (lora.py:219 inner linear)
             lora_gemm(M, nseg * rank, K, x, K, 1, A_cat, 1, K, 1.0, T)
             ends = _lib.i64_array(torch.tensor(weight.segments).cumsum(0).tolist())
+        # split-K partials for shapes whose tiles leave CUs idle (0 otherwise)
+        ws = _ws.get(dev, _lib.query("st_q4_linear_fwd_workspace_bytes", M, N, K))
         _launch(("fwd", M, N, K), lambda: _lib.call(
             "st_q4_linear_fwd", _lib.ptr(x), M, K, K, _lib.ptr(weight.payload),
             _lib.ptr(weight.scales), N, weight.lut(), weight.flags,
@@ -359,7 +361,7 @@ class _Q4LoRALinear(torch.autograd.Function):
             _lib.ptr(B_cat) if ab else None, rank if ab else 0, float(scale),
             nseg if ab else 0, ends if ab else None,
             _lib.ptr(residual), 0 if residual is None else residual.stride(0),
-            _lib.ptr(y), N, None, 0, stream))
+            _lib.ptr(y), N, _lib.ptr(ws), 0 if ws is None else ws.numel(), stream))
         ctx.weight, ctx.rank, ctx.scale = weight, rank, scale
         ctx.loras = loras
         ctx.has_residual = residual is not None
@@ -466,10 +468,11 @@ class _Q4LoRALinear(torch.autograd.Function):
                 _lib.ptr(gu), gu.stride(0), _lib.ptr(dx), dx.stride(0), None, 0, stream))
         else:
             dx = torch.empty((M, K), dtype=_BF16, device=dev)
+            ws = _ws.get(dev, _lib.query("st_q4_linear_dgrad_workspace_bytes", M, N, K))
             _launch(("dgrad", M, N, K), lambda: _lib.call(
                 "st_q4_linear_dgrad", _lib.ptr(dy), M, N, N, _lib.ptr(weight.payload),
                 _lib.ptr(weight.scales), K, weight.lut(), weight.flags, *lora_args,
-                _lib.ptr(dx), K, None, 0, stream))
+                _lib.ptr(dx), K, _lib.ptr(ws), 0 if ws is None else ws.numel(), stream))
         dres = dy if ctx.has_residual else None
         return (dx, None, dres, None, None, None, None, *grads_ab)
 

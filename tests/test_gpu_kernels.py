@@ -268,6 +268,102 @@ def test_q4_linear_dgrad_and_lora_grads_vs_oracle(dev, oracle_codec, monkeypatch
             torch.testing.assert_close(got, ref, rtol=1e-4, atol=1e-5 * ref.abs().max().item())
 
 
+@pytest.mark.parametrize("splits", ["2", "3", "8"])
+@pytest.mark.parametrize("M,N,K", [(300, 512, 1024), (517, 384, 2048), (64, 192, 4096),
+                                   (300, 2048, 512)])
+def test_split_k_vs_oracle(dev, oracle_codec, monkeypatch, splits, M, N, K):
+    """Split-K (ST_GEMM_SPLITK forces the split count; contractions of 16
+    k-steps or more split: the forward for K >= 1024, the dgrad for N = 2048):
+    the forward (fused two segments with LoRA and a residual) and the dgrad
+    with its LoRA term, against autograd over the oracle's decode.  The splits' fp32 partials
+    are summed in split order, then the usual epilogue roundings apply."""
+    monkeypatch.setenv("ST_GEMM_SPLITK", splits)
+    g = torch.Generator().manual_seed(M + N + K + int(splits))
+    w = (torch.randn(N, K, generator=g) * 0.02).numpy()
+    qw, W = q4_from_oracle(oracle_codec, w, "nf4-g128", dev)
+    q = ops.Q4Weight(qw.payload, qw.scales, (N, K), "nf4-g128", (N // 2, N - N // 2))
+    x = torch.randn(M, K, generator=g).to(BF)
+    dy = torch.randn(M, N, generator=g).to(BF)
+    res = torch.randn(M, N, generator=g).to(BF)
+    r = 8
+    A = [torch.randn(r, K, generator=g) * 0.05 for _ in range(2)]
+    B = [torch.randn(N // 2, r, generator=g) * 0.05, torch.randn(N - N // 2, r, generator=g) * 0.05]
+    xr = x.clone().requires_grad_(True)
+    Ar = [a.clone().requires_grad_(True) for a in A]
+    Br = [b.clone().requires_grad_(True) for b in B]
+    base = F.linear(xr, W)
+    # one fused projection: one x_f32 for both segments, so the LoRA input
+    # gradient is rounded to bf16 once (as the fused epilogue does)
+    xf = xr.float()
+    lora = torch.cat([F.linear(F.linear(xf, Ar[i]), Br[i]) for i in range(2)], 1) * 2.0
+    out = (res.float() + (base.float() + lora).to(BF).float()).to(BF)
+    out.backward(dy)
+    xd = x.to(dev).requires_grad_(True)
+    los = [_L(A[i].to(dev).requires_grad_(True), B[i].to(dev).requires_grad_(True), 16.0)
+           for i in range(2)]
+    y = ops.q4_lora_linear(xd, q, los, residual=res.to(dev))
+    y.backward(dy.to(dev))
+    torch.cuda.synchronize()
+    _close_bf16(y, out, f"split-K {splits} fwd {M}x{N}x{K}")
+    _close_bf16(xd.grad, xr.grad, f"split-K {splits} dgrad {M}x{N}x{K}")
+    for i in range(2):
+        for got, ref in ((los[i].A.grad.cpu(), Ar[i].grad), (los[i].B.grad.cpu(), Br[i].grad)):
+            torch.testing.assert_close(got, ref, rtol=1e-4, atol=1e-5 * ref.abs().max().item())
+
+
+@pytest.mark.parametrize("N,K", [(32768, 512), (24576, 1536)])
+def test_split_k_mla_dgrad_shapes_vs_torch_fp32(dev, N, K):
+    """DeepSeek-V3 MLA input gradients at 2048 tokens (kv_b: 512 outputs from
+    a 32768-long contraction; q_b: 1536 from 24576), where the dispatch
+    splits the contraction on its own, with a LoRA term, against torch fp32
+    matmul of the standalone decode (pinned bit-exact to the oracle)."""
+    M = 2048
+    assert _lib.query("st_q4_linear_dgrad_workspace_bytes", M, N, K) > 0
+    g = torch.Generator().manual_seed(N + K)
+    w = torch.randn(N, K, generator=g) * 0.02
+    rec = codecs.encode(w, "nf4-g128")
+    q = ops.Q4Weight(rec.parts["payload"].to(dev), rec.parts["scales"].to(dev), (N, K), "nf4-g128")
+    Wd = q.dequantize().float()
+    x = torch.randn(M, K, generator=g).to(BF).to(dev).requires_grad_(True)
+    dy = torch.randn(M, N, generator=g).to(BF).to(dev)
+    lo = _L((torch.randn(8, K, generator=g) * 0.05).to(dev).requires_grad_(True),
+            (torch.randn(N, 8, generator=g) * 0.05).to(dev).requires_grad_(True), 16.0)
+    y = ops.q4_lora_linear(x, q, [lo])
+    y.backward(dy)
+    dT = (dy.float() @ lo.B.detach()) * 2.0
+    ref = ((dy.float() @ Wd).to(BF).float() + (dT @ lo.A.detach()).to(BF).float()).to(BF)
+    torch.cuda.synchronize()
+    _close_bf16(x.grad, ref, f"MLA dgrad {M}x{N}->{K}")
+
+
+@pytest.mark.parametrize("tile", ["128", "2562", "256", "2566"])
+@pytest.mark.parametrize("M", [1300, 1024])
+def test_raster_order_gives_the_same_bits(dev, oracle_codec, monkeypatch, tile, M):
+    """The grouped tile raster (4 row tiles per group; M = 1300 leaves a short
+    last group) only reorders whole tiles: forward, dgrad and LoRA gradients
+    equal the row-major order bit for bit."""
+    monkeypatch.setenv("ST_GEMM_TILE", tile)
+    g = torch.Generator().manual_seed(M)
+    N, K = 1536, 512
+    q, _ = q4_from_oracle(oracle_codec, (torch.randn(N, K, generator=g) * 0.02).numpy(), "nf4-g128",
+                          dev)
+    x = torch.randn(M, K, generator=g).to(BF).to(dev)
+    dy = torch.randn(M, N, generator=g).to(BF).to(dev)
+    A = torch.randn(8, K, generator=g) * 0.05
+    B = torch.randn(N, 8, generator=g) * 0.05
+    outs = []
+    for raster in ("1", "4"):
+        monkeypatch.setenv("ST_GEMM_RASTER", raster)
+        xd = x.clone().requires_grad_(True)
+        lo = _L(A.to(dev).requires_grad_(True), B.to(dev).requires_grad_(True), 16.0)
+        y = ops.q4_lora_linear(xd, q, [lo])
+        y.backward(dy)
+        torch.cuda.synchronize()
+        outs.append((y.view(torch.int16), xd.grad.view(torch.int16), lo.A.grad, lo.B.grad))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("r", [4, 5])
 def test_fused_segments_match_separate_projections(dev, oracle_codec, r):
     """q|k|v as one N-concatenated GEMM == three separate GEMMs (same bits for
