@@ -133,6 +133,42 @@ def deepseek_block(hidden, rotary_tables, mask, *, parameters, weights, loras=No
     return residual + (routed.view_as(x) + mlp(x, "mlp.shared_experts."))
 
 
+def deepseek_block_rows(hidden, rotary_tables, mask, *, parameters, weights, loras, rows,
+                        indices, experts):
+    """``deepseek_block``'s output on the token rows ``rows`` only (flat
+    indices into [B*S]), with the MoE evaluated on those rows alone: the
+    attention runs over every token (each row's attention reads all earlier
+    tokens), while a row's routed and shared experts read only that row.  So
+    with an upstream gradient that is zero off ``rows``, autograd of this
+    output gives every gradient of the whole block (the other rows' MoE terms
+    get zero gradient).  ``indices`` [len(rows), top_k] are global expert ids
+    and ``weights["mlp.experts.*"]`` hold only the experts ``experts``
+    (ascending ids, stacked in that order), so only the experts these rows
+    hit need decoding.  Returns [len(rows), hidden]."""
+    c = parameters
+    loras = loras or {}
+
+    def linear(x, name):
+        return OL.lora_linear(x, weights[name + ".weight"], loras.get(name))
+
+    residual, x = _attention(hidden, rotary_tables, mask, c, weights, linear)
+    flat = x.reshape(-1, x.shape[-1])[rows]
+    res = residual.reshape(-1, residual.shape[-1])[rows]
+    remap = torch.full((c["experts"],), -1, dtype=torch.long)
+    remap[torch.as_tensor(experts)] = torch.arange(len(experts))
+    local = remap[indices]
+    if bool((local < 0).any()):
+        raise ValueError("a pick outside the decoded experts")
+    logits = F.linear(flat.float(), weights["mlp.gate.weight"].float())
+    routing = OM.deepseek_weights_given(logits, indices, normalize=c["normalize"],
+                                        scale=c["router_scale"])
+    routed = OM.expert_loop(flat, routing, local, weights["mlp.experts.gate_up_proj"],
+                            weights["mlp.experts.down_proj"], num_experts=len(experts))
+    shared = linear(F.silu(linear(flat, "mlp.shared_experts.gate_proj"))
+                    * linear(flat, "mlp.shared_experts.up_proj"), "mlp.shared_experts.down_proj")
+    return res + (routed + shared)
+
+
 def pre_moe_hidden(hidden, rotary_tables, mask, *, parameters, weights, loras=None):
     """The normalised hidden state the MoE router reads ([tokens, hidden])."""
     loras = loras or {}

@@ -5,16 +5,19 @@ CPU oracle (north-star criteria: outputs rel. err <= 2e-2, gradients cosine
 * config 2 -- one Llama-3-8B-shape layer step at 1 x 2048 tokens, nf4-g128,
   LoRA r=16 on all seven projections, compared whole with the oracle's
   streaming step;
-* config 3 -- Qwen3-8B-shape layers (qk_norm, 32/8 heads, intermediate
-  12288) at 4096 tokens streamed through two slots, layer-major window with
-  gradient accumulation 4, two optimizer steps, against the oracle's
-  training loop (the vocabulary-151936 terminal, including the row split of
-  a chunk, is tested in test_gpu_terminal.py);
+* config 3 -- four Qwen3-8B-shape layers (qk_norm, 32/8 heads,
+  intermediate 12288) at 4096 tokens streamed through two slots (so slots
+  are overwritten within each phase), the vocabulary-151936 terminal inside
+  every microbatch, layer-major window with gradient accumulation 4, two
+  optimizer steps, against the oracle's training loop;
 * config 4 -- the Qwen3-MoE-30B-A3B-shape feed-forward at 128 experts x 4096
   tokens with per-expert LoRA;
 * config 5 -- the DeepSeek-V3-shape MoE feed-forward (256 experts of
   [2 x 2048, 7168] + [7168, 2048], sigmoid group-limited routing on an fp32
-  router, shared expert with LoRA) at 2048 tokens.
+  router, shared expert with LoRA) at 2048 tokens, checked on 32 tokens
+  spread over the sequence (at least 128 distinct experts, including ones
+  whose packed gate|up lies past 2 GiB of the stack); the whole composed
+  config-5 layer (MLA + MoE) is test_gpu_mla.py.
 
 For the MoE layers the GPU runs the whole workload (every expert, ragged
 row counts); the oracle checks a subset of tokens.  Each token's output and
@@ -87,7 +90,7 @@ def test_config3_qwen3_8b_streamed_layer_major_accumulation4(oracle_codec):
     from tests.test_gpu_train import decoded
     g = torch.Generator().manual_seed(3)
     c = QWEN3_8B
-    V, S, n_layers, acc, steps, lr = 8192, 4096, 2, 4, 2, 1e-3
+    V, S, n_layers, acc, steps, lr = 151936, 4096, 4, 4, 2, 1e-3
     layers = _qwen3_layers(g, n_layers)
     emb = (torch.randn(V, c["H"], generator=g) * 0.5).to(BF)
     norm = (1 + 0.05 * torch.randn(c["H"], generator=g)).to(BF)
@@ -268,7 +271,7 @@ def test_config5_deepseek_moe_256_experts_2048_tokens(dev, oracle_codec):
     ls = {"gate": _SharedLora(g, r, H, I, 16.0, dev), "up": _SharedLora(g, r, H, I, 16.0, dev),
           "down": _SharedLora(g, r, I, H, 16.0, dev)}
     flat = torch.randn(T, H, generator=g).to(BF)
-    check = torch.arange(3, T, 512)                    # 4 checked tokens
+    check = torch.arange(3, T, 64)                     # 32 checked tokens
     dout = torch.zeros(T, H, dtype=BF)
     dout[check] = torch.randn(len(check), H, generator=g).to(BF)
     weights = {"mlp.gate.weight": router.to(dev), "mlp.gate.e_score_correction_bias": bias.to(dev),
@@ -300,6 +303,9 @@ def test_config5_deepseek_moe_256_experts_2048_tokens(dev, oracle_codec):
     routing = OM.deepseek_weights_given(logits, idx_c[check], normalize=True, scale=scale)
     torch.testing.assert_close(w.cpu()[check], routing.detach(), rtol=1e-5, atol=1e-6)
     hit, local = _compact(idx_c[check], E)
+    print(f"experts hit by the checked tokens: {len(hit)}, highest {max(hit)}", flush=True)
+    # packed gate|up of expert e starts at e * 2I*H/2 bytes: past 2 GiB from e = 147
+    assert len(hit) >= 128 and max(hit) * (2 * I * H // 2) >= 1 << 31
     Wgu, Wd = _decode_experts(oracle_codec, qgu, hit), _decode_experts(oracle_codec, qd, hit)
     routed = OM.expert_loop(x, routing, local, Wgu, Wd, num_experts=len(hit))
     Ws = [*_decode_experts(oracle_codec, qsgu, [0, 1]), _decode_experts(oracle_codec, qsd, [0])[0]]

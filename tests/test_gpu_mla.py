@@ -9,7 +9,11 @@
   default and YaRN tables;
 * config 5's attention dimensions (hidden 7168, 128 heads, q_lora_rank 1536,
   kv_lora_rank 512, qk 128 + 64, v 128) at 256 tokens with 16 routed experts
-  of width 2048 (the 256-expert MoE at 2048 tokens is test_gpu_configs.py).
+  of width 2048;
+* the composed config-5 layer at its real size -- 2048 tokens, 256 routed
+  experts, shared expert, LoRA -- with the attention checked over every
+  token and the MoE on 64 rows spread over the sequence (the upstream
+  gradient is zero elsewhere, so every gradient is the whole layer's).
 North-star criteria: output rel. err <= 2e-2, every gradient cosine >= 0.999."""
 import numpy as np
 import pytest
@@ -276,3 +280,149 @@ def test_config5_attention_dims_layer_step(oracle_codec, monkeypatch):
                 interleave=True, moe=True, rope_cfg=YARN, E=16, groups=8, group_k=4, top_k=8)
     _assert(run_layer(c, H=7168, I_moe=2048, E=16, S=256, oracle_codec=oracle_codec, seed=7,
                       monkeypatch=monkeypatch))
+
+
+@pytest.mark.timeout(1200)
+def test_config5_composed_layer_2048_tokens_256_experts(oracle_codec, monkeypatch):
+    """BASELINE config 5 whole: one DeepSeek-V3-shape layer (MLA with 128
+    heads, q_lora_rank 1536, kv_lora_rank 512, YaRN interleaved rotary; 256
+    routed experts of width 2048, top 8 of 8 groups / best 4, shared expert;
+    LoRA r=8 on the attention projections and the shared expert) at 2048
+    tokens, streamed through a slot, forward + recompute + backward.  The
+    4-bit records are random codes and scales written into the pinned image
+    (the oracle decodes the same bytes).  The oracle
+    (oracle.mla.deepseek_block_rows) runs the attention over all 2048 tokens
+    and the MoE on 64 rows spread over the sequence, with only the experts
+    those rows hit decoded (at least 64 of them, including experts whose
+    packed gate|up lies past 2 GiB of the stack)."""
+    from oracle import moe as OMoE
+    T, H, I, E = 2048, 7168, 2048, 256
+    c = _params(heads=128, nope=128, rope=64, vdim=128, kv_rank=512, q_rank=1536,
+                interleave=True, moe=True, rope_cfg=YARN, E=E, groups=8, group_k=4, top_k=8)
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(55)
+    heads, nope, rope, v = c["heads"], c["nope"], c["rope"], c["value"]
+    mats = {"self_attn.q_a_proj": (c["q_rank"], H),
+            "self_attn.q_b_proj": (heads * (nope + rope), c["q_rank"]),
+            "self_attn.kv_a_proj_with_mqa": (c["kv_rank"] + rope, H),
+            "self_attn.kv_b_proj": (heads * (nope + v), c["kv_rank"]),
+            "self_attn.o_proj": (H, heads * v),
+            "mlp.experts.gate_up_proj": (E, 2 * I, H), "mlp.experts.down_proj": (E, H, I),
+            "mlp.shared_experts.gate_proj": (I, H), "mlp.shared_experts.up_proj": (I, H),
+            "mlp.shared_experts.down_proj": (H, I)}
+    weights = {}
+    for name, shape in mats.items():
+        n = int(np.prod(shape))
+        key = name if ("experts." in name and "shared" not in name) else f"{name}.weight"
+        weights[key] = codecs_record(shape, n)
+    meta = lambda n, dt: torch.empty(n, dtype=dt, device="meta")  # noqa: E731
+    weights.update({"input_layernorm.weight": meta(H, BF),
+                    "post_attention_layernorm.weight": meta(H, BF),
+                    "self_attn.q_a_layernorm.weight": meta(c["q_rank"], BF),
+                    "self_attn.kv_a_layernorm.weight": meta(c["kv_rank"], BF),
+                    "mlp.gate.weight": torch.empty(E, H, dtype=torch.float32, device="meta"),
+                    "mlp.gate.e_score_correction_bias": meta(E, torch.float32)})
+    block = deepseek.make_deepseek_block(0, weights, codec="nf4-g128", parameters=c, rank=8,
+                                         alpha=16.0, device=dev, shared_lora=True, generator=g)
+    with torch.no_grad():
+        for p in block.adapters.values():
+            p.B.copy_(torch.randn(p.B.shape, generator=g) * 0.02)
+    gfill = torch.Generator().manual_seed(56)
+
+    def fill(blk, layout, out):
+        for name, e in layout.entries.items():
+            if e[0] == "q4":
+                _, _, _, po, pb, so, sb = e
+                out[po:po + pb].random_(0, 256, generator=gfill)
+                out[so:so + sb].view(torch.float32).uniform_(0.01, 0.03, generator=gfill)
+            else:
+                _, dtype, shape, o, nb = e
+                view = out[o:o + nb].view(dtype)
+                if name == "mlp.gate.weight":   # well-separated fp32 scores
+                    view.normal_(0.0, 3 * H ** -0.5, generator=gfill)
+                elif name.endswith("e_score_correction_bias"):
+                    view.normal_(0.0, 0.05, generator=gfill)
+                else:
+                    view.copy_((1 + 0.05 * torch.randn(view.shape, generator=gfill)).to(dtype))
+    session = slots.Q4SlotSession([block], dev, host_budget_bytes=1 << 40,
+                                  device_budget_bytes=1 << 40, slots=2, image_loader=fill)
+    layout, img = session.layouts[id(block)], session.images[id(block)]
+    picks = []
+    real = moe.deepseek_moe_feed_forward
+
+    def recording(*args, **kwargs):
+        out, _, idx = real(*args, return_routing=True, **kwargs)
+        picks.append(idx.detach().cpu().long())
+        return out
+    monkeypatch.setattr(moe, "deepseek_moe_feed_forward", recording)
+    hidden = torch.randn(1, T, H, generator=g).to(BF)
+    rows = torch.arange(5, T, 32)                      # 64 rows over the whole sequence
+    dy = torch.zeros(1, T, H, dtype=BF)
+    dy[0, rows] = torch.randn(len(rows), H, generator=g).to(BF)
+    cos, sin = OMLA.rotary(1, T, YARN, rope, BF)
+    mask = CausalMask(1, T)
+    h = hidden.to(dev).requires_grad_(True)
+    with session.run():
+        out = streaming_block(h, (cos.to(dev), sin.to(dev)), mask, block.functional, block.kwargs,
+                              session.reloader(block), block.adapters, block.index)
+        out.backward(dy.to(dev))
+    torch.cuda.synchronize()
+    print("device step done", flush=True)
+    assert len(picks) == 2 and torch.equal(picks[0], picks[1])
+    idx = picks[1]
+    hit = torch.unique(idx[rows]).tolist()
+    print(f"experts hit by the checked rows: {len(hit)}, highest {max(hit)}", flush=True)
+    per_expert = 2 * I * H // 2
+    assert len(hit) >= 64 and max(hit) * per_expert >= 1 << 31
+    # oracle weights: every attention / shared matrix and the hit experts,
+    # decoded from the pinned image the device copied
+    wref = {}
+    for name, e in layout.entries.items():
+        if e[0] == "q4":
+            _, _, shape, po, pb, so, sb = e
+            if name.startswith("mlp.experts."):
+                n_e = int(np.prod(shape[1:]))
+                stack = torch.empty(len(hit), *shape[1:], dtype=BF)
+                for i, ex in enumerate(hit):
+                    p0, s0 = po + ex * n_e // 2, so + ex * (n_e // 128) * 4
+                    bits = oracle_codec.decode4(img[p0:p0 + n_e // 2].numpy(),
+                                                img[s0:s0 + n_e // 32].view(torch.float32).numpy(),
+                                                n_e, lut=oracle_codec.NF4_LUT)
+                    stack[i] = torch.from_numpy(bits.astype(np.int16)).view(BF).view(shape[1:])
+                wref[name] = stack
+            else:
+                n = int(np.prod(shape))
+                bits = oracle_codec.decode4(img[po:po + pb].numpy(),
+                                            img[so:so + sb].view(torch.float32).numpy(), n,
+                                            lut=oracle_codec.NF4_LUT)
+                wref[name] = torch.from_numpy(bits.astype(np.int16)).view(BF).view(shape)
+        else:
+            _, dtype, shape, o, nb = e
+            wref[name] = img[o:o + nb].view(dtype).view(shape).clone()
+    lor = {n: OL.Lora(n, p.A.detach().cpu(), p.B.detach().cpu(), p.alpha)
+           for n, p in block.adapters.items()}
+    ordered = sorted(lor.values(), key=lambda q: q.name)
+    hr = hidden.clone().requires_grad_(True)
+    ref = OMLA.deepseek_block_rows(hr, (cos, sin), OL.causal_mask(1, T, BF), parameters=c,
+                                   weights=wref, loras=lor, rows=rows, indices=idx[rows],
+                                   experts=hit)
+    grads = torch.autograd.grad(ref, [hr] + [t for q in ordered for t in (q.A, q.B)],
+                                dy[0, rows])
+    res = {"out": _rel(out.reshape(T, H)[rows.to(dev)], ref), "dh": _cos(h.grad, grads[0])}
+    for i, q in enumerate(ordered):
+        p = block.adapters[q.name]
+        res[q.name + ".A"] = _cos(p.grad_A, grads[1 + 2 * i])
+        res[q.name + ".B"] = _cos(p.grad_B, grads[2 + 2 * i])
+    session.close()
+    _assert(res)
+
+
+def codecs_record(shape, n):
+    """Layout-only 4-bit record (meta tensors) of an nf4-g128 matrix or stack."""
+    from spilltune_amd import codecs
+    groups = n // codecs.GROUP
+    return codecs.Record({"version": 1, "shape": list(shape), "dtype": "bfloat16",
+                          "codec": "nf4-g128", "group_size": codecs.GROUP, "numel": n},
+                         {"payload": torch.empty(groups * codecs.STRIDE, dtype=torch.uint8,
+                                                 device="meta"),
+                          "scales": torch.empty(groups, dtype=torch.float32, device="meta")})

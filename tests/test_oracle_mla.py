@@ -147,3 +147,55 @@ def test_yarn_attention_scale_and_amplitude():
     assert amp == pytest.approx(1.0)          # mscale == mscale_all_dim
     default = OM.rope_parameters({"rope_type": "default", "rope_theta": 10000.0}, 8)
     assert torch.equal(default[0], 1.0 / 10000.0 ** (torch.arange(0, 8, 2).float() / 8))
+
+
+def test_block_rows_equals_the_whole_block_on_its_rows():
+    """oracle.mla.deepseek_block_rows (the MoE evaluated on a subset of rows,
+    only the experts those rows hit stacked): output equal to the whole
+    block's on those rows, and every gradient (input and each LoRA) equal to
+    the whole block's under an upstream gradient that is zero off the rows."""
+    torch.manual_seed(0)
+    H, I, E, S, heads = 64, 32, 8, 24, 4
+    c = {"heads": heads, "nope": 16, "rope": 8, "value": 12, "kv_rank": 16, "q_rank": 24,
+         "eps": 1e-6, "attention_scale": 0.2, "interleave": True, "moe": True, "experts": E,
+         "groups": 4, "group_k": 2, "top_k": 2, "normalize": True, "router_scale": 2.5}
+    mats = {"self_attn.q_a_proj": (24, H), "self_attn.q_b_proj": (heads * 24, 24),
+            "self_attn.kv_a_proj_with_mqa": (16 + 8, H), "self_attn.kv_b_proj": (heads * 28, 16),
+            "self_attn.o_proj": (H, heads * 12), "mlp.shared_experts.gate_proj": (I, H),
+            "mlp.shared_experts.up_proj": (I, H), "mlp.shared_experts.down_proj": (H, I)}
+    w = {f"{n}.weight": (torch.randn(s) * 0.1)for n, s in mats.items()}
+    for n, d in (("input_layernorm", H), ("post_attention_layernorm", H),
+                 ("self_attn.q_a_layernorm", 24), ("self_attn.kv_a_layernorm", 16)):
+        w[f"{n}.weight"] = 1 + 0.05 * torch.randn(d, dtype=torch.float32)
+    w["mlp.gate.weight"] = torch.randn(E, H, dtype=torch.float32) * 0.3
+    w["mlp.gate.e_score_correction_bias"] = torch.randn(E, dtype=torch.float32) * 0.05
+    w["mlp.experts.gate_up_proj"] = torch.randn(E, 2 * I, H, dtype=torch.float32) * 0.1
+    w["mlp.experts.down_proj"] = torch.randn(E, H, I, dtype=torch.float32) * 0.1
+    loras = {n: OL.Lora(n, torch.randn(4, s[1]) * 0.1, torch.randn(s[0], 4) * 0.1, 8.0)
+             for n, s in mats.items()}
+    hidden = torch.randn(1, S, H, dtype=torch.float32)
+    rot = OM.rotary(1, S, {"rope_type": "default", "rope_theta": 10000.0}, 8, torch.float32)
+    mask = OL.causal_mask(1, S, torch.float32)
+    rows = torch.tensor([2, 9, 10, 23])
+    dy = torch.zeros(1, S, H, dtype=torch.float32)
+    dy[0, rows] = torch.randn(len(rows), H, dtype=torch.float32)
+    leaves = [t for lo in loras.values() for t in (lo.A, lo.B)]
+    h1 = hidden.clone().requires_grad_(True)
+    with torch.no_grad():
+        x = OM.pre_moe_hidden(hidden, rot, mask, parameters=c, weights=w, loras=loras)
+        from oracle import moe as OMoE
+        _, _, idx = OMoE.deepseek_route(x, w["mlp.gate.weight"], w["mlp.gate.e_score_correction_bias"],
+                                        groups=4, group_k=2, top_k=2, normalize=True, scale=2.5)
+    whole = OM.deepseek_block(h1, rot, mask, parameters=c, weights=w, loras=loras, indices=idx)
+    g1 = torch.autograd.grad(whole, [h1] + leaves, dy)
+    hit = torch.unique(idx[rows]).tolist()
+    sub = dict(w, **{"mlp.experts.gate_up_proj": w["mlp.experts.gate_up_proj"][hit],
+                     "mlp.experts.down_proj": w["mlp.experts.down_proj"][hit]})
+    h2 = hidden.clone().requires_grad_(True)
+    part = OM.deepseek_block_rows(h2, rot, mask, parameters=c, weights=sub, loras=loras,
+                                  rows=rows, indices=idx[rows], experts=hit)
+    g2 = torch.autograd.grad(part, [h2] + leaves, dy[0, rows])
+    # fp32 throughout: only the BLAS blocking of fewer rows differs
+    torch.testing.assert_close(part, whole[0, rows], rtol=1e-5, atol=1e-6)
+    for a, b in zip(g1, g2):
+        torch.testing.assert_close(a, b, rtol=1e-4, atol=1e-6)
