@@ -251,6 +251,68 @@ def streamed(c, block, args, X, dY, rot, mask, resident_ms):
     return out
 
 
+def streamed_window(c, block, args, X, dY, rot, mask, resident_ms, window=2):
+    """The same N streamed layers with a gradient-accumulation window of
+    ``window`` microbatches run layer-major (engine.window_layer_major's
+    schedule without the terminal): each layer's image is borrowed once per
+    phase per window, so ``window`` microbatches' forward (or recompute +
+    backward) run behind each copy.  Reported per layer and microbatch
+    against the resident layer step."""
+    import torch
+    from spilltune_amd import slots
+    from spilltune_amd.recompute import (_borrow_weights, _call_functional_block,
+                                         block_adapter_backward)
+    L = args.streamed_layers
+    dev = X.device
+    blocks = [block] + [slots.BlockPlan(i, block.kind, block.functional, dict(block.kwargs),
+                                        block.host_weights, block.adapters, block.storage_specs)
+                        for i in range(1, L)]
+    session = slots.Q4SlotSession(blocks, dev, host_budget_bytes=1 << 40,
+                                  device_budget_bytes=1 << 40, slots=2)
+    ordered = sorted(block.adapters.values(), key=lambda p: p.name)
+
+    def step():
+        with session.run():
+            hs = [[X] for _ in range(window)]
+            for b in blocks:
+                with _borrow_weights(session.reloader(b), "forward") as w, torch.no_grad():
+                    for h in hs:
+                        h.append(_call_functional_block(b.functional, h[-1], rot, mask, w,
+                                                        b.kwargs))
+            gs = [dY] * window
+            for b in reversed(blocks):
+                with _borrow_weights(session.reloader(b), "backward") as w:
+                    for k, h in enumerate(hs):
+                        hin = h.pop().detach().requires_grad_(True)
+                        with torch.enable_grad():
+                            out = _call_functional_block(b.functional, hin, rot, mask, w, b.kwargs)
+                        gs[k] = block_adapter_backward(out, hin, ordered, gs[k],
+                                                       k > 0 or b.index > 0, b.index)
+
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize()
+    session.completed_copies = []
+    t0 = time.perf_counter()
+    n = max(2, args.steps // 4)
+    for _ in range(n):
+        step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / n
+    copies = session.completed_copies
+    per = dt * 1e3 / (L * window)
+    copy_ms = sum(cp["copy_cuda_ms"] for cp in copies) / n
+    out = {"layers": L, "slots": 2, "window": window, "ms_per_step": round(dt * 1e3, 3),
+           "ms_per_layer_microbatch": round(per, 4), "resident_ms_per_layer": round(resident_ms, 4),
+           "exposed_copy_ms_per_layer_microbatch": round(per - resident_ms, 4),
+           "copy_ms_per_step": round(copy_ms, 3), "copies_per_step": len(copies) / n,
+           "hidden_copy_frac": round(max(0.0, 1.0 - (per - resident_ms) * L * window / copy_ms), 4)
+           if copy_ms > 0 else None}
+    session.close()
+    log(f"streamed {L} layers, window {window} layer-major: {out}")
+    return out
+
+
 def synthetic_q4_block(index, c, device, generator, codec="nf4-g128"):
     """A Qwen3 decoder layer whose 4-bit records are synthetic bytes (random
     codes, scales |N(0,1)| * 0.02 / 0.7): the streamed step's cost does not
@@ -1083,6 +1145,7 @@ def main():
     }
     if args.streamed_layers > 0:
         result["streamed"] = streamed(c, block, args, X, dY, rot, mask, median_ms)
+        result["streamed_window2"] = streamed_window(c, block, args, X, dY, rot, mask, median_ms)
     if not args.no_cpu_baseline:
         log(f"timing the CPU path at {args.cpu_tokens} tokens")
         result["cpu_baseline"] = cpu_baseline(c, block, args.cpu_tokens)
