@@ -13,6 +13,8 @@
 // columns = queries), so one lane owns one query column: the softmax max/sum
 // are in-lane reductions plus one exchange between the two half-waves, and
 // the probabilities are already in the B-operand layout of O^T += V^T P^T.
+#include <type_traits>
+
 #include "common.h"
 
 namespace {
@@ -79,6 +81,27 @@ __device__ __forceinline__ void g2lds16(const uint16_t* src, uint16_t* lds_wave)
                                    (__attribute__((address_space(3))) void*)lds_wave, 16, 0, 0);
 }
 
+// Buffer copy of 16 bytes per lane into LDS, laid out like g2lds16; an
+// offset at or past the resource's extent reads zeros.  Tiles move the
+// resource base (scalar work) and keep each lane's offset fixed, so a copy
+// costs no vector instructions.
+__device__ __forceinline__ void b2lds16(__amdgpu_buffer_rsrc_t rs, uint32_t off,
+                                        uint16_t* lds_wave) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      rs, (__attribute__((address_space(3))) void*)lds_wave, 16, off, 0, 0, 0);
+}
+
+// Thread chunks of a row-major [rows][D] tile (tswz layout) copied by NT
+// threads, copy i covering rows i*R .. i*R+R-1 (R = NT/(D/8)).  When R is a
+// multiple of 16 every copy puts a thread at the same in-row position (the
+// swizzle repeats every 16 rows): one lane offset serves all copies, and
+// copy i moves the resource base by i*R rows instead.
+template <int D, int NT>
+struct RowCopy {
+  static constexpr bool uniform = NT % (D / 8) == 0 && (NT / (D / 8)) % 16 == 0;
+  static constexpr int rows = NT / (D / 8);
+};
+
 // Workgroup -> (x, h, b) for a 1-D grid of nx * H * B workgroups.  Blocks are
 // dispatched round-robin over the 8 XCDs; remapping keeps consecutive logical
 // indices on one XCD, and x runs fastest, then the query heads of a KV group,
@@ -131,7 +154,9 @@ __device__ __forceinline__ void fa_fwd_tile(const uint16_t* __restrict__ q,
   static_assert((BKT * KS) % 64 == 0 && (DV * VS) % 64 == 0, "tiles are whole wave copies");
 
   const int tid = threadIdx.x, lane = tid & 63;
-  const int grp = (tid >> 6) / 4, wave = (tid >> 6) % 4;  // key group, wave in group
+  // key group, wave in group (wave-uniform: tile indices and LDS bases are scalar)
+  const int grp = __builtin_amdgcn_readfirstlane((tid >> 6) / 4);
+  const int wave = __builtin_amdgcn_readfirstlane((tid >> 6) % 4);
   const int g = lane >> 5, c = lane & 31;
   const int hk = h / (H / Hkv);
   const uint16_t* qb = q + ((int64_t)(b * H + h) * S) * DQ;
@@ -159,31 +184,37 @@ __device__ __forceinline__ void fa_fwd_tile(const uint16_t* __restrict__ q,
   // causal: keys <= qlast; keys >= Sk (right padding) are masked out
   const int ntiles = min(qlast, Sk - 1) / BKT + 1;
   const int nsteps = (ntiles + G - 1) / G;      // group steps (tile u*G + grp)
-  // Rows past S read a clamped (finite) row: those keys are masked out.
+  // Copies: wave copy wi fills 1 KiB of the padded tile; pad slots repeat
+  // the row's last chunk.  Lane offsets are fixed, the tile's first key moves
+  // the resource base.  K rows past S read zeros; V^T columns past a row's
+  // end read the next row's first columns (or zeros past the head): every
+  // such key is masked out, so its probability is exactly 0.
+  constexpr int KW = (KI + 3) / 4, VW = (VI + 3) / 4;
+  uint32_t koff[KW], voff[VW];
+#pragma unroll
+  for (int i = 0; i < KW; ++i) {
+    const int P = (i * 4 + wave) * 64 + lane;
+    const int row = min(P / KS, BKT - 1), ch = min(P % KS, DQ / 8 - 1);
+    koff[i] = (uint32_t)(row * DQ + ch * 8) * 2;
+  }
+#pragma unroll
+  for (int i = 0; i < VW; ++i) {
+    const int P = (i * 4 + wave) * 64 + lane;
+    const int d = min(P / VS, DV - 1), ch = min(P % VS, BKT / 8 - 1);
+    voff[i] = (uint32_t)(d * Sp + ch * 8) * 2;
+  }
   auto issue = [&](int t, int buf) {
     const int k0 = t * BKT;
+    const auto rk = st::make_rsrc(kb + (int64_t)k0 * DQ, (int64_t)(S - k0) * DQ * 2);
+    const auto rv = st::make_rsrc(vb + k0, ((int64_t)DV * Sp - k0) * 2);
     uint16_t* ks = glds + buf * (LK + LV);
     uint16_t* vs = ks + LK;
 #pragma unroll
-    for (int i = 0; i < (KI + 3) / 4; ++i) {
-      const int wi = i * 4 + wave;
-      if (wi < KI) {
-        const int P = wi * 64 + lane;
-        const int row = min(P / KS, BKT - 1), ch = P % KS;
-        const int key = min(k0 + row, S - 1);
-        g2lds16(kb + (int64_t)key * DQ + min(ch, DQ / 8 - 1) * 8, ks + wi * 64 * 8);
-      }
-    }
+    for (int i = 0; i < KW; ++i)
+      if (i * 4 + wave < KI) b2lds16(rk, koff[i], ks + (i * 4 + wave) * 64 * 8);
 #pragma unroll
-    for (int i = 0; i < (VI + 3) / 4; ++i) {
-      const int wi = i * 4 + wave;
-      if (wi < VI) {
-        const int P = wi * 64 + lane;
-        const int d = min(P / VS, DV - 1), ch = min(P % VS, BKT / 8 - 1);
-        const int col = min(k0 + ch * 8, Sp - 8);
-        g2lds16(vb + (int64_t)d * Sp + col, vs + wi * 64 * 8);
-      }
-    }
+    for (int i = 0; i < VW; ++i)
+      if (i * 4 + wave < VI) b2lds16(rv, voff[i], vs + (i * 4 + wave) * 64 * 8);
   };
 
   if (grp < ntiles) issue(grp, 0);
@@ -464,7 +495,9 @@ __device__ __forceinline__ void fa_bwd_dq_tile(
   constexpr int PERK = BKT * DQ / 8 / NTH, PERV = BKT * DV / 8 / NTH;  // 16-byte chunks per thread
   static_assert(PERK * NTH * 8 == LTK && PERV * NTH * 8 == LTV, "tiles are whole thread copies");
   const int tid = threadIdx.x, lane = tid & 63;
-  const int grp = (tid >> 6) / 4, wave = (tid >> 6) % 4;  // key group, wave in group
+  // key group, wave in group (wave-uniform: tile indices and LDS bases are scalar)
+  const int grp = __builtin_amdgcn_readfirstlane((tid >> 6) / 4);
+  const int wave = __builtin_amdgcn_readfirstlane((tid >> 6) % 4);
   const int gtid = tid % NTH;
   const int g = lane >> 5, c = lane & 31;
   const int hk = h / (H / Hkv);
@@ -499,7 +532,7 @@ __device__ __forceinline__ void fa_bwd_dq_tile(
   dl += __shfl_xor(dl, 32);
   const int64_t srow = (int64_t)(b * H + h) * S;
   if (grp == 0 && g == 0 && qok) delta[srow + myq] = dl;
-  const float lq = qok ? lse[srow + myq] : 0.0f;
+  const float lq = qok ? lse[srow + myq] : INFINITY;  // rows past S: probability 0
 
   f32x16 dqacc[DB];
 #pragma unroll
@@ -510,29 +543,45 @@ __device__ __forceinline__ void fa_bwd_dq_tile(
   const int qlast = min(qt * BQ + BQ, S) - 1;
   const int ntiles = min(qlast, Sk - 1) / BKT + 1;
   const int nsteps = (ntiles + G - 1) / G;
-  // K and V tiles [key][D] (tswz layout) by direct global -> LDS copies;
-  // rows past S read a clamped (finite) row, masked out below
+  // K and V tiles [key][D] (tswz layout) by buffer copies into LDS: fixed
+  // lane offsets, the tile's first key in the resource base; keys past S
+  // read zeros and are masked out below
+  using CK = RowCopy<DQ, NTH>;
+  using CV = RowCopy<DV, NTH>;
+  uint32_t koff[CK::uniform ? 1 : PERK], voff[CV::uniform ? 1 : PERV];
+#pragma unroll
+  for (int i = 0; i < (CK::uniform ? 1 : PERK); ++i) {
+    const int P = i * NTH + gtid;
+    const int row = P / (DQ / 8);
+    koff[i] = (uint32_t)(row * DQ + ((P % (DQ / 8)) ^ swz<DQ>(row)) * 8) * 2;
+  }
+#pragma unroll
+  for (int i = 0; i < (CV::uniform ? 1 : PERV); ++i) {
+    const int P = i * NTH + gtid;
+    const int row = P / (DV / 8);
+    voff[i] = (uint32_t)(row * DV + ((P % (DV / 8)) ^ swz<DV>(row)) * 8) * 2;
+  }
   auto issue = [&](int t, int buf) {
     const int k0 = t * BKT;
     uint16_t* ks = glds + buf * (LTK + LTV);
     uint16_t* vs = ks + LTK;
 #pragma unroll
     for (int i = 0; i < PERK; ++i) {
-      const int P = i * NTH + gtid;
-      const int row = P / (DQ / 8);
-      const int ch = (P % (DQ / 8)) ^ swz<DQ>(row);
-      g2lds16(kb + (int64_t)min(k0 + row, S - 1) * DQ + ch * 8, ks + (i * NTH + wave * 64) * 8);
+      const int r0 = k0 + (CK::uniform ? i * CK::rows : 0);
+      const auto rk = st::make_rsrc(kb + (int64_t)r0 * DQ, (int64_t)max(S - r0, 0) * DQ * 2);
+      b2lds16(rk, koff[CK::uniform ? 0 : i], ks + (i * NTH + wave * 64) * 8);
     }
 #pragma unroll
     for (int i = 0; i < PERV; ++i) {
-      const int P = i * NTH + gtid;
-      const int row = P / (DV / 8);
-      const int ch = (P % (DV / 8)) ^ swz<DV>(row);
-      g2lds16(vb + (int64_t)min(k0 + row, S - 1) * DV + ch * 8, vs + (i * NTH + wave * 64) * 8);
+      const int r0 = k0 + (CV::uniform ? i * CV::rows : 0);
+      const auto rv = st::make_rsrc(vb + (int64_t)r0 * DV, (int64_t)max(S - r0, 0) * DV * 2);
+      b2lds16(rv, voff[CV::uniform ? 0 : i], vs + (i * NTH + wave * 64) * 8);
     }
   };
   // one 32-key block: S^T, dP^T, dS^T (masked when `edge`), dQ^T += K^T dS^T
-  auto block = [&](const uint16_t* ks, const uint16_t* vs, int jb, int kb0, bool edge) {
+  // `lim`: the largest kept key offset within the block less 4g (entry v of
+  // the accumulator holds key offset 8(v>>2) + 4g + (v&3)); 31 keeps all
+  auto block = [&](const uint16_t* ks, const uint16_t* vs, int jb, int lim) {
     f32x16 sacc, pacc;
 #pragma unroll
     for (int e = 0; e < 16; ++e) { sacc[e] = 0.0f; pacc[e] = 0.0f; }
@@ -551,10 +600,9 @@ __device__ __forceinline__ void fa_bwd_dq_tile(
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int vv = 8 * hh + e;
-        const int key = kb0 + (vv >> 2) * 8 + g * 4 + (vv & 3);
-        const bool keep = !edge || (key <= myq && key < Sk && qok);
-        const float p = keep ? __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[vv], sl2, -lq)) : 0.0f;
-        ds[e] = p * (pacc[vv] - dl);
+        float x = __builtin_fmaf(sacc[vv], sl2, -lq);
+        x = (vv >> 2) * 8 + (vv & 3) <= lim ? x : -INFINITY;  // exp2(-inf) = 0
+        ds[e] = __builtin_amdgcn_exp2f(x) * (pacc[vv] - dl);
       }
       dsf[hh] = as_bf16x8(make_uint4(st::pack_bf16x2(ds[0], ds[1]), st::pack_bf16x2(ds[2], ds[3]),
                                      st::pack_bf16x2(ds[4], ds[5]), st::pack_bf16x2(ds[6], ds[7])));
@@ -581,7 +629,8 @@ __device__ __forceinline__ void fa_bwd_dq_tile(
       for (int jb = 0; jb < BKT / 32; ++jb) {
         const int kb0 = k0 + jb * 32;
         if (kb0 > q0 + 31 || kb0 >= Sk) continue;  // wave-uniform
-        block(ks, vs, jb, kb0, kb0 + 31 > q0 || kb0 + 31 >= Sk || q0 + 31 >= S);
+        const bool edge = kb0 + 31 > q0 || kb0 + 31 >= Sk || q0 + 31 >= S;
+        block(ks, vs, jb, edge ? min(myq, Sk - 1) - kb0 - g * 4 : 31);
       }
     }
     __builtin_amdgcn_s_waitcnt(0);
@@ -687,7 +736,8 @@ __device__ __forceinline__ void fa_bwd_dkdv_tile(
   constexpr bool KREG = NW == 4;  // K and V fragments in registers
   constexpr int PERQ = LQ / 8 / NTH2, PERG = LG / 8 / NTH2;  // 16-byte chunks per thread
   static_assert(PERQ * NTH2 * 8 == LQ && PERG * NTH2 * 8 == LG, "tiles are whole thread copies");
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5, c = lane & 31;
   const int kq = wave & 3, qh0 = NW == 8 ? wave >> 2 : 0;
   const int hk = h / (H / Hkv);
@@ -742,31 +792,43 @@ __device__ __forceinline__ void fa_bwd_dkdv_tile(
   const int qt_first = k0 / QT2;
   const int qt_end = (S + QT2 - 1) / QT2;
   float lr = 0.0f, dr = 0.0f;
-  // Q and dO tiles [query][D] (tswz layout) by direct global -> LDS copies
-  // (rows past S read a clamped row, masked below); lse and Delta via VGPRs
+  // Q and dO tiles [query][D] (tswz layout) by buffer copies into LDS:
+  // fixed lane offsets, the tile's first query in the resource base; rows
+  // past S read zeros (masked below); lse and Delta via VGPRs
+  using CQ = RowCopy<DQ, NTH2>;
+  using CG = RowCopy<DV, NTH2>;
+  uint32_t qoff[CQ::uniform ? 1 : PERQ], goff[CG::uniform ? 1 : PERG];
+#pragma unroll
+  for (int i = 0; i < (CQ::uniform ? 1 : PERQ); ++i) {
+    const int P = i * NTH2 + tid;
+    const int row = P / (DQ / 8);
+    qoff[i] = (uint32_t)(row * DQ + ((P % (DQ / 8)) ^ swz<DQ>(row)) * 8) * 2;
+  }
+#pragma unroll
+  for (int i = 0; i < (CG::uniform ? 1 : PERG); ++i) {
+    const int P = i * NTH2 + tid;
+    const int row = P / (DV / 8);
+    goff[i] = (uint32_t)(row * ldt + ((P % (DV / 8)) ^ swz<DV>(row)) * 8) * 2;
+  }
   auto issue = [&](int qt, int buf) {
     const int q0 = qt * QT2;
     uint16_t* qs = qg + buf * (LQ + LG);
     uint16_t* gs = qs + LQ;
 #pragma unroll
     for (int i = 0; i < PERQ; ++i) {
-      const int P = i * NTH2 + tid;
-      const int row = P / (DQ / 8);
-      const int ch = (P % (DQ / 8)) ^ swz<DQ>(row);
-      const int qq = min(q0 + row, S - 1);
-      g2lds16(qb + (int64_t)qq * DQ + ch * 8, qs + (i * NTH2 + wave * 64) * 8);
+      const int r0 = q0 + (CQ::uniform ? i * CQ::rows : 0);
+      const auto rq = st::make_rsrc(qb + (int64_t)r0 * DQ, (int64_t)max(S - r0, 0) * DQ * 2);
+      b2lds16(rq, qoff[CQ::uniform ? 0 : i], qs + (i * NTH2 + wave * 64) * 8);
     }
 #pragma unroll
     for (int i = 0; i < PERG; ++i) {
-      const int P = i * NTH2 + tid;
-      const int row = P / (DV / 8);
-      const int ch = (P % (DV / 8)) ^ swz<DV>(row);
-      const int qq = min(q0 + row, S - 1);
-      g2lds16(gb + (int64_t)qq * ldt + ch * 8, gs + (i * NTH2 + wave * 64) * 8);
+      const int r0 = q0 + (CG::uniform ? i * CG::rows : 0);
+      const auto rg = st::make_rsrc(gb + (int64_t)r0 * ldt, (int64_t)max(S - r0, 0) * ldt * 2);
+      b2lds16(rg, goff[CG::uniform ? 0 : i], gs + (i * NTH2 + wave * 64) * 8);
     }
     if (tid < QT2) {
       const bool ok = q0 + tid < S;
-      lr = ok ? lse[srow + q0 + tid] : 0.0f;
+      lr = ok ? lse[srow + q0 + tid] : INFINITY;  // rows past S: probability 0
       dr = ok ? delta[srow + q0 + tid] : 0.0f;
     }
   };
@@ -789,6 +851,12 @@ __device__ __forceinline__ void fa_bwd_dkdv_tile(
     const int qh = NW == 8 ? qh0 : hq;
     const int qw0 = qt * QT2 + qh * 32;   // this wave's queries
     if (qw0 + 31 >= kw0 && qw0 < S) {     // some query sees some key
+      // kept query rows (offsets within the block, less 4g) from lo on:
+      // causal (query >= key), none for a key past Sk; rows past S carry an
+      // lse of +inf, so their probabilities are 0 as well
+      int lo = -64;
+      if (qw0 < kw0 + 31 || kw0 + 31 >= Sk)  // wave-uniform
+        lo = mykey < Sk ? mykey - qw0 - g * 4 : 64;
       f32x16 sacc, pacc;
 #pragma unroll
       for (int e = 0; e < 16; ++e) { sacc[e] = 0.0f; pacc[e] = 0.0f; }
@@ -810,10 +878,11 @@ __device__ __forceinline__ void fa_bwd_dkdv_tile(
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int vv = 8 * hh + e;
-          const int r = qh * 32 + (vv >> 2) * 8 + g * 4 + (vv & 3);  // query row in tile
-          const int qq = qt * QT2 + r;
-          const bool keep = mykey <= qq && mykey < Sk && qq < S;
-          const float p = keep ? __builtin_amdgcn_exp2f(sacc[vv] * sl2 - lse_s[buf][r]) : 0.0f;
+          const int ro = (vv >> 2) * 8 + (vv & 3);  // query row in the block, less 4g
+          const int r = qh * 32 + ro + g * 4;      // query row in tile
+          float x = __builtin_fmaf(sacc[vv], sl2, -lse_s[buf][r]);
+          x = ro >= lo ? x : -INFINITY;  // exp2(-inf) = 0
+          const float p = __builtin_amdgcn_exp2f(x);
           p8[e] = p;
           d8[e] = p * (pacc[vv] - dl_s[buf][r]);
         }
@@ -919,7 +988,8 @@ __global__ __launch_bounds__(64 * dkdv_waves<DQ>(), dkdv_waves<DQ>() == 8 ? 2 : 
     uint16_t* __restrict__ dk_out, uint16_t* __restrict__ dv_out, int nk, int paired,
     const int* __restrict__ kvlen) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[dkdv_lds_elems<DQ, DV>()];
-  __shared__ float lse_s[2][QT2], dl_s[2][QT2];
+  __shared__ __attribute__((aligned(16))) float lse_s[2][QT2];
+  __shared__ __attribute__((aligned(16))) float dl_s[2][QT2];
   const WgIdx w = wg_index(paired ? (nk + 1) / 2 : nk, H);
   for (int it = 0; it < 1 + paired; ++it) {
     const int kt = paired ? (it == 0 ? w.x : nk - 1 - w.x) : w.x;
@@ -1039,6 +1109,14 @@ int attn_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint
   return st::check_launch("fa_bwd_reduce");
 }
 
+// Tiles are copied through 32-bit buffer offsets from a head's base: the
+// head's Q/K rows (S*DQ), its staged V^T (DV*Sp) and the token-major rows of
+// the output gradient it reads (S rows of H*DV) must each span below 2 GiB.
+bool extents_ok(int64_t S, int64_t H, int64_t DQ, int64_t DV) {
+  const int64_t lim = (int64_t)1 << 31, Sp = (S + 15) & ~15;
+  return S * DQ * 2 < lim && Sp * DV * 2 < lim && S * H * DV * 2 < lim;
+}
+
 bool dims_ok(int64_t DQ, int64_t DV) {
   return (DQ == 64 && DV == 64) || (DQ == 128 && DV == 128) || (DQ == 192 && DV == 128);
 }
@@ -1053,6 +1131,8 @@ int fwd_common(const char* name, const uint16_t* q, const uint16_t* k, const uin
     return st::fail(ST_EUNSUPPORTED, "%s: head dims %lld/%lld (64/64, 128/128 or 192/128 only)",
                     name, (long long)DQ, (long long)DV);
   ST_CHECK_ARG(S < (1 << 30), "%s: S must be below 2^30", name);
+  if (!extents_ok(S, H, DQ, DV))
+    return st::fail(ST_EUNSUPPORTED, "%s: a head's rows must span below 2 GiB", name);
   ST_CHECK_ARG(q && k && v && out && lse && al16(q) && al16(k) && al16(v) && al16(out),
                "%s: NULL or unaligned pointer", name);
   const int64_t need = attn_workspace(B, S, H, Hkv, DQ, DV, 0);
@@ -1077,6 +1157,8 @@ int bwd_common(const char* name, const uint16_t* q, const uint16_t* k, const uin
     return st::fail(ST_EUNSUPPORTED, "%s: head dims %lld/%lld (64/64, 128/128 or 192/128 only)",
                     name, (long long)DQ, (long long)DV);
   ST_CHECK_ARG(S < (1 << 30), "%s: S must be below 2^30", name);
+  if (!extents_ok(S, H, DQ, DV))
+    return st::fail(ST_EUNSUPPORTED, "%s: a head's rows must span below 2 GiB", name);
   ST_CHECK_ARG(q && k && v && out && lse && dout && dq && dk && dv && al16(q) && al16(k) &&
                    al16(v) && al16(out) && al16(dout) && al16(dq) && al16(dk) && al16(dv),
                "%s: NULL or unaligned pointer", name);
