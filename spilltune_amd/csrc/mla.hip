@@ -78,6 +78,108 @@ __device__ __forceinline__ float rotate_vjp(const float* g, const float* cs, con
   return (j & 1) ? bf(bf(g2 * cs[i]) - bf(g1 * sn[i])) : bf(bf(g1 * cs[i]) + bf(g2 * sn[i]));
 }
 
+__device__ __forceinline__ uint4 ldg16(const uint16_t* p) { return *(const uint4*)p; }
+
+// Output chunk cr (elements 8cr .. 8cr+7) of rotate(t) for a head's rope
+// values t in global memory; it reads two 16-byte chunks of t.  Default:
+// chunk cr and its partner cr +- R8/2 (t[j +- half]); interleave: chunks 2p
+// and 2p+1, p = cr mod R8/2 (the pairs t[2i], t[2i+1]).  Same roundings as
+// rotate_chunk.
+__device__ __forceinline__ uint4 rotate_chunk_g(const uint16_t* t, const float* cs,
+                                                const float* sn, int ROPE, int interleave,
+                                                int cr) {
+  const int hc = ROPE / 16;  // chunks per half
+  float a[8], b[8], o[8];
+  if (!interleave) {
+    const int pc = cr < hc ? cr + hc : cr - hc;
+    unpack8(ldg16(t + 8 * cr), a);
+    unpack8(ldg16(t + 8 * pc), b);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int j = 8 * cr + e;
+      const float rot = cr < hc ? -b[e] : b[e];
+      o[e] = bf(bf(a[e] * cs[j]) + bf(rot * sn[j]));
+    }
+  } else {
+    const int pr = cr < hc ? cr : cr - hc;
+    unpack8(ldg16(t + 16 * pr), a);
+    unpack8(ldg16(t + 16 * pr + 8), b);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int i = 8 * pr + e;  // pair index within the half
+      const float x0 = e < 4 ? a[2 * e] : b[2 * e - 8], x1 = e < 4 ? a[2 * e + 1] : b[2 * e - 7];
+      o[e] = cr < hc ? bf(bf(x0 * cs[i]) - bf(x1 * sn[i])) : bf(bf(x1 * cs[i]) + bf(x0 * sn[i]));
+    }
+  }
+  return pack8(o);
+}
+
+// Chunk cr of the rotation's VJP for a head's output gradient g in global
+// memory (two 16-byte chunks of g; same roundings as rotate_vjp).  Default:
+// chunk cr and its partner cr +- R8/2; interleave: element j of the chunk
+// takes g[j/2] and g[half + j/2], chunks cr/2 and R8/2 + cr/2.
+__device__ __forceinline__ uint4 rotate_vjp_chunk_g(const uint16_t* g, const float* cs,
+                                                    const float* sn, int ROPE, int interleave,
+                                                    int cr) {
+  const int hc = ROPE / 16, half = ROPE / 2;
+  float a[8], b[8], o[8];
+  if (!interleave) {
+    const int pc = cr < hc ? cr + hc : cr - hc;
+    unpack8(ldg16(g + 8 * cr), a);
+    unpack8(ldg16(g + 8 * pc), b);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int j = 8 * cr + e;
+      const float direct = bf(a[e] * cs[j]);
+      o[e] = cr < hc ? bf(direct + bf(b[e] * sn[j + half])) : bf(direct - bf(b[e] * sn[j - half]));
+    }
+  } else {
+    unpack8(ldg16(g + 8 * (cr >> 1)), a);
+    unpack8(ldg16(g + 8 * (hc + (cr >> 1))), b);
+    const int e0 = 4 * (cr & 1);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int i = 4 * cr + (e >> 1);
+      const float g1 = a[e0 + (e >> 1)], g2 = b[e0 + (e >> 1)];
+      o[e] = (e & 1) ? bf(bf(g2 * cs[i]) - bf(g1 * sn[i])) : bf(bf(g1 * cs[i]) + bf(g2 * sn[i]));
+    }
+  }
+  return pack8(o);
+}
+
+// dst[h*dst_h + 8c .. +7] = src[h*src_h + 8c .. +7] for H heads of n8
+// 16-byte chunks: U chunks per thread are loaded before any is stored, so
+// each thread keeps U loads in flight.
+template <int U>
+__device__ __forceinline__ void copy_heads(uint16_t* __restrict__ dst, int64_t dst_h,
+                                           const uint16_t* __restrict__ src, int64_t src_h,
+                                           int n8, int H) {
+  const int total = H * n8;
+  for (int i0 = threadIdx.x; i0 < total; i0 += NT * U) {
+    uint4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = i0 + u * NT;
+      if (i < total) {
+        const int h = i / n8, c = i - h * n8;
+        v[u] = ldg16(src + h * src_h + 8 * c);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = i0 + u * NT;
+      if (i < total) {
+        const int h = i / n8, c = i - h * n8;
+        *(uint4*)(dst + h * dst_h + 8 * c) = v[u];
+      }
+    }
+  }
+}
+
+// One workgroup per token, 16-byte chunks: the nope parts of Q and K and the
+// value are copied head by head (several loads in flight per thread), then
+// the rotated q_rope chunks (each reading its two input chunks straight from
+// global memory) and the shared rotated key are written.
 __global__ __launch_bounds__(NT) void mla_rope_fwd(const uint16_t* __restrict__ q, int64_t ldq,
                                                    const uint16_t* __restrict__ kv, int64_t ldkv,
                                                    const uint16_t* __restrict__ kr, int64_t ldkr,
@@ -86,11 +188,11 @@ __global__ __launch_bounds__(NT) void mla_rope_fwd(const uint16_t* __restrict__ 
                                                    uint16_t* __restrict__ Q,
                                                    uint16_t* __restrict__ K,
                                                    uint16_t* __restrict__ V) {
-  __shared__ float cs[MAXROPE], sn[MAXROPE], kt[MAXROPE], kout[MAXROPE];
-  __shared__ float qt[NT / 64][MAXROPE];  // one head's q_rope per wave at a time
+  __shared__ float cs[MAXROPE], sn[MAXROPE], kt[MAXROPE];
+  __shared__ uint4 kpk[MAXROPE / 8];  // the rotated shared key, packed
   const int64_t row = blockIdx.x;
   const int64_t b = row / d.S, s = row % d.S;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x;
   const int DQ = d.NOPE + d.ROPE, DKV = d.NOPE + d.DV;
   const int R8 = d.ROPE / 8;
   for (int j = tid; j < d.ROPE; j += NT) {
@@ -102,45 +204,40 @@ __global__ __launch_bounds__(NT) void mla_rope_fwd(const uint16_t* __restrict__ 
   if (tid < R8) {  // the shared rotated key, once per token
     float o[8];
     rotate_chunk(kt, cs, sn, d.ROPE, d.interleave, tid, o);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) kout[8 * tid + e] = o[e];
+    kpk[tid] = pack8(o);
   }
   __syncthreads();
   const uint16_t* qr = q + row * ldq;
   const uint16_t* kvr = kv + row * ldkv;
-  // nope parts of Q and K, the value, and the rotated key: 16-byte copies
   const int nq8 = d.NOPE / 8, nv8 = d.DV / 8;
-  const int per_head = 2 * nq8 + nv8 + R8;
-  for (int i = tid; i < d.H * per_head; i += NT) {
-    const int h = i / per_head, c = i % per_head;
-    const int64_t hs = ((int64_t)(b * d.H + h) * d.S + s);
-    if (c < nq8) {
-      *(uint4*)(Q + hs * DQ + 8 * c) = *(const uint4*)(qr + (int64_t)h * DQ + 8 * c);
-    } else if (c < 2 * nq8) {
-      const int cc = c - nq8;
-      *(uint4*)(K + hs * DQ + 8 * cc) = *(const uint4*)(kvr + (int64_t)h * DKV + 8 * cc);
-    } else if (c < 2 * nq8 + nv8) {
-      const int cc = c - 2 * nq8;
-      *(uint4*)(V + hs * d.DV + 8 * cc) = *(const uint4*)(kvr + (int64_t)h * DKV + d.NOPE + 8 * cc);
-    } else {
-      const int cc = c - 2 * nq8 - nv8;
-      *(uint4*)(K + hs * DQ + d.NOPE + 8 * cc) = pack8(kout + 8 * cc);
+  const int64_t t0 = (int64_t)b * d.H * d.S + s;  // (b, head 0, s)
+  uint16_t* Qt = Q + t0 * DQ;
+  uint16_t* Kt = K + t0 * DQ;
+  const int64_t hq = d.S * DQ;  // head stride of Q and K
+  copy_heads<4>(Qt, hq, qr, DQ, nq8, d.H);
+  copy_heads<4>(Kt, hq, kvr, DKV, nq8, d.H);
+  copy_heads<4>(V + t0 * d.DV, d.S * d.DV, kvr + d.NOPE, DKV, nv8, d.H);
+  // rotated q_rope chunks (two input chunks each) and the shared rotated key
+  const int nr = d.H * R8;
+  for (int i0 = tid; i0 < nr; i0 += 2 * NT) {
+    uint4 v[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int i = i0 + u * NT;
+      if (i < nr) {
+        const int h = i / R8, cr = i - h * R8;
+        v[u] = rotate_chunk_g(qr + (int64_t)h * DQ + d.NOPE, cs, sn, d.ROPE, d.interleave, cr);
+      }
     }
-  }
-  // rotated q_rope: each wave takes one head at a time (the rotation mixes
-  // elements across the head's rope dims)
-  for (int h = wave; h < d.H; h += NT / 64) {
-    const uint16_t* src = qr + (int64_t)h * DQ + d.NOPE;
-    for (int j = lane; j < d.ROPE; j += 64) qt[wave][j] = st::bf16_to_f32(src[j]);
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_wave_barrier();
-    if (lane < R8) {
-      float o[8];
-      rotate_chunk(qt[wave], cs, sn, d.ROPE, d.interleave, lane, o);
-      const int64_t hs = ((int64_t)(b * d.H + h) * d.S + s);
-      *(uint4*)(Q + hs * DQ + d.NOPE + 8 * lane) = pack8(o);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int i = i0 + u * NT;
+      if (i < nr) {
+        const int h = i / R8, cr = i - h * R8;
+        *(uint4*)(Qt + h * hq + d.NOPE + 8 * cr) = v[u];
+        *(uint4*)(Kt + h * hq + d.NOPE + 8 * cr) = kpk[cr];
+      }
     }
-    __builtin_amdgcn_wave_barrier();
   }
 }
 
@@ -153,63 +250,70 @@ __global__ __launch_bounds__(NT) void mla_rope_bwd(const uint16_t* __restrict__ 
                                                    uint16_t* __restrict__ dkv, int64_t lddkv,
                                                    uint16_t* __restrict__ dkr, int64_t lddkr) {
   __shared__ float cs[MAXROPE], sn[MAXROPE], gk[MAXROPE];
-  __shared__ float part[NT];
-  __shared__ float gq[NT / 64][MAXROPE];
+  __shared__ float gpart[NT * 8];  // [head group][rope element] partial sums
   const int64_t row = blockIdx.x;
   const int64_t b = row / d.S, s = row % d.S;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x;
   const int DQ = d.NOPE + d.ROPE, DKV = d.NOPE + d.DV;
+  const int R8 = d.ROPE / 8, G = NT / R8;  // R8 divides NT (checked by the host)
   for (int j = tid; j < d.ROPE; j += NT) {
     cs[j] = st::bf16_to_f32(cos[row * d.ROPE + j]);
     sn[j] = st::bf16_to_f32(sin[row * d.ROPE + j]);
   }
   // gradient of the shared rope key before rotation: the sum over heads of
-  // dK's rope part (fp32, heads in a fixed order), rounded once to bf16
+  // dK's rope part in fp32, rounded once to bf16.  Thread (head group hg,
+  // chunk qc) sums heads hg, hg + G, ... of chunk qc with 16-byte loads; the
+  // G group sums are then added in group order (a fixed order).
   {
-    const int groups = NT / d.ROPE;  // ROPE divides NT
-    const int j = tid % d.ROPE, grp = tid / d.ROPE;
-    float acc = 0.0f;
-    for (int h = grp; h < d.H; h += groups)
-      acc += st::bf16_to_f32(dK[((int64_t)(b * d.H + h) * d.S + s) * DQ + d.NOPE + j]);
-    part[grp * d.ROPE + j] = acc;
+    const int qc = tid % R8, hg = tid / R8;
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int h = hg; h < d.H; h += G) {
+      float v[8];
+      unpack8(ldg16(dK + ((int64_t)(b * d.H + h) * d.S + s) * DQ + d.NOPE + 8 * qc), v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += v[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) gpart[hg * d.ROPE + 8 * qc + e] = acc[e];
   }
   __syncthreads();
   if (tid < d.ROPE) {
-    float acc = 0.0f;
-    for (int g = 0; g < NT / d.ROPE; ++g) acc += part[g * d.ROPE + tid];
-    gk[tid] = bf(acc);
+    float a = 0.0f;
+    for (int g = 0; g < G; ++g) a += gpart[g * d.ROPE + tid];
+    gk[tid] = bf(a);
   }
   __syncthreads();
   if (tid < d.ROPE)
     dkr[row * lddkr + tid] = st::f32_to_bf16(rotate_vjp(gk, cs, sn, d.ROPE, d.interleave, tid));
-  // dq nope, dk nope and dv: 16-byte copies into the projection layouts
+  // per head: the dq row [nope copy | rope VJP] and the dkv row [k_nope | v]
   const int nq8 = d.NOPE / 8, nv8 = d.DV / 8;
-  const int per_head = 2 * nq8 + nv8;
-  for (int i = tid; i < d.H * per_head; i += NT) {
-    const int h = i / per_head, c = i % per_head;
-    const int64_t hs = ((int64_t)(b * d.H + h) * d.S + s);
-    if (c < nq8) {
-      *(uint4*)(dq + row * lddq + (int64_t)h * DQ + 8 * c) = *(const uint4*)(dQ + hs * DQ + 8 * c);
-    } else if (c < 2 * nq8) {
-      const int cc = c - nq8;
-      *(uint4*)(dkv + row * lddkv + (int64_t)h * DKV + 8 * cc) =
-          *(const uint4*)(dK + hs * DQ + 8 * cc);
-    } else {
-      const int cc = c - 2 * nq8;
-      *(uint4*)(dkv + row * lddkv + (int64_t)h * DKV + d.NOPE + 8 * cc) =
-          *(const uint4*)(dV + hs * d.DV + 8 * cc);
+  const int64_t t0 = (int64_t)b * d.H * d.S + s;  // (b, head 0, s)
+  const uint16_t* dQt = dQ + t0 * DQ;
+  const int64_t hq = d.S * DQ;
+  uint16_t* dqr = dq + row * lddq;
+  uint16_t* dkvr = dkv + row * lddkv;
+  copy_heads<4>(dqr, DQ, dQt, hq, nq8, d.H);
+  copy_heads<4>(dkvr, DKV, dK + t0 * DQ, hq, nq8, d.H);
+  copy_heads<4>(dkvr + d.NOPE, DKV, dV + t0 * d.DV, d.S * d.DV, nv8, d.H);
+  const int nr = d.H * R8;
+  for (int i0 = tid; i0 < nr; i0 += 2 * NT) {
+    uint4 v[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int i = i0 + u * NT;
+      if (i < nr) {
+        const int h = i / R8, cr = i - h * R8;
+        v[u] = rotate_vjp_chunk_g(dQt + h * hq + d.NOPE, cs, sn, d.ROPE, d.interleave, cr);
+      }
     }
-  }
-  // q_rope gradient: VJP of the rotation, one head per wave at a time
-  for (int h = wave; h < d.H; h += NT / 64) {
-    const int64_t hs = ((int64_t)(b * d.H + h) * d.S + s);
-    for (int j = lane; j < d.ROPE; j += 64) gq[wave][j] = st::bf16_to_f32(dQ[hs * DQ + d.NOPE + j]);
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_wave_barrier();
-    for (int j = lane; j < d.ROPE; j += 64)
-      dq[row * lddq + (int64_t)h * DQ + d.NOPE + j] =
-          st::f32_to_bf16(rotate_vjp(gq[wave], cs, sn, d.ROPE, d.interleave, j));
-    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int i = i0 + u * NT;
+      if (i < nr) {
+        const int h = i / R8, cr = i - h * R8;
+        *(uint4*)(dqr + (int64_t)h * DQ + d.NOPE + 8 * cr) = v[u];
+      }
+    }
   }
 }
 
