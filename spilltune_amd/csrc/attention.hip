@@ -231,11 +231,14 @@ __device__ __forceinline__ void fa_fwd_tile(const uint16_t* __restrict__ q,
     const uint16_t* kl = ks + (c * KS + g) * 8;   // this lane's K operand row
     const uint16_t* vl = vs + (c * VS + g) * 8;   // this lane's V^T operand row
     const int k0 = t * BKT;
-    if (t >= ntiles) {
-      // this group has no tile in the last step
-    } else if (k0 + BKT - 1 <= q0 && k0 + BKT <= Sk) {
-      // interior tile (every key visible to every query of this wave): the
-      // blocks' MFMA chains are independent and nothing is masked
+    // One code path for every tile: S^T = K Q^T for the tile's keys, the
+    // causal / ragged mask as one per-lane key limit (entry v of block jb
+    // holds key offset 32jb + 8(v>>2) + 4g + (v&3); offsets above the limit
+    // become -inf), online softmax over the tile, O^T += V^T P^T.  A tile
+    // wholly above this wave's queries is skipped (wave-uniform).
+    if (t < ntiles && k0 <= q0 + 31) {
+      const bool edge = k0 + BKT - 1 > q0 || k0 + BKT > Sk;  // wave-uniform
+      const int limg = (edge ? min(myq, Sk - 1) - k0 : BKT) - g * 4;
       f32x16 sacc[BKT / 32];
 #pragma unroll
       for (int jb = 0; jb < BKT / 32; ++jb)
@@ -248,12 +251,20 @@ __device__ __forceinline__ void fa_fwd_tile(const uint16_t* __restrict__ q,
           const bf16x8 a = as_bf16x8(*(const uint4*)(kl + (jb * 32 * KS + 2 * s) * 8));
           sacc[jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[s], sacc[jb], 0, 0, 0);
         }
+      if (edge) {
+#pragma unroll
+        for (int jb = 0; jb < BKT / 32; ++jb)
+#pragma unroll
+          for (int v = 0; v < 16; ++v)
+            sacc[jb][v] = jb * 32 + (v >> 2) * 8 + (v & 3) <= limg ? sacc[jb][v] : -INFINITY;
+      }
       float mt = sacc[0][0];
 #pragma unroll
       for (int jb = 0; jb < BKT / 32; ++jb)
 #pragma unroll
         for (int v = 0; v < 16; ++v) mt = fmaxf(mt, sacc[jb][v]);
       mt = fmaxf(mt, __shfl_xor(mt, 32)) * sl2;
+      // rescale only when some query's max grew by more than 2^8
       if (__ballot(mt > m_run + RESCALE_LOG2)) {
         const float m_new = fmaxf(m_run, mt);
         const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
@@ -264,13 +275,16 @@ __device__ __forceinline__ void fa_fwd_tile(const uint16_t* __restrict__ q,
         l_run *= alpha;
         m_run = m_new;
       }
+      // a row with no visible key yet keeps m_run = -inf: its masked entries
+      // give exp2(-inf) = 0 against an offset of 0
+      const float m_use = m_run == -INFINITY ? 0.0f : m_run;
       bf16x8 pf[BKT / 16];
 #pragma unroll
       for (int cc = 0; cc < BKT / 16; ++cc) {
         float p[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[cc >> 1][8 * (cc & 1) + e], sl2, -m_run));
+          p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[cc >> 1][8 * (cc & 1) + e], sl2, -m_use));
           l_run += p[e];
         }
         pf[cc] = as_bf16x8(make_uint4(st::pack_bf16x2(p[0], p[1]), st::pack_bf16x2(p[2], p[3]),
@@ -283,65 +297,6 @@ __device__ __forceinline__ void fa_fwd_tile(const uint16_t* __restrict__ q,
           const bf16x8 a = as_bf16x8(*(const uint4*)(vl + (db * 32 * VS + 2 * cc) * 8));
           oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pf[cc], oacc[db], 0, 0, 0);
         }
-    } else {
-      // 32-key blocks, each: S^T = K Q^T, online softmax, O^T += V^T P^T.  A
-      // block wholly above this wave's queries (or past S) is skipped.
-  #pragma unroll
-      for (int jb = 0; jb < BKT / 32; ++jb) {
-        const int kb0 = k0 + jb * 32;
-        if (kb0 > q0 + 31 || kb0 >= Sk) continue;  // wave-uniform
-        f32x16 sacc;
-  #pragma unroll
-        for (int v = 0; v < 16; ++v) sacc[v] = 0.0f;
-  #pragma unroll
-        for (int s = 0; s < DS; ++s) {
-          const bf16x8 a = as_bf16x8(*(const uint4*)(kl + (jb * 32 * KS + 2 * s) * 8));
-          sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[s], sacc, 0, 0, 0);
-        }
-        if (kb0 + 31 > q0 || kb0 + 31 >= Sk) {  // diagonal / ragged block: mask
-  #pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int key = kb0 + (v >> 2) * 8 + g * 4 + (v & 3);
-            if (key > myq || key >= Sk) sacc[v] = -INFINITY;
-          }
-        }
-        float mt = sacc[0];
-  #pragma unroll
-        for (int v = 1; v < 16; ++v) mt = fmaxf(mt, sacc[v]);
-        mt = fmaxf(mt, __shfl_xor(mt, 32)) * sl2;
-        // rescale only when some query's max grew by more than 2^8
-        if (__ballot(mt > m_run + RESCALE_LOG2)) {
-          const float m_new = fmaxf(m_run, mt);
-          const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-  #pragma unroll
-          for (int i = 0; i < DB; ++i)
-  #pragma unroll
-            for (int v = 0; v < 16; ++v) oacc[i][v] *= alpha;
-          l_run *= alpha;
-          m_run = m_new;
-        }
-        bf16x8 pf[2];
-  #pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          float p[8];
-  #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[8 * hh + e], sl2, -m_run));
-            l_run += p[e];
-          }
-          pf[hh] = as_bf16x8(make_uint4(st::pack_bf16x2(p[0], p[1]), st::pack_bf16x2(p[2], p[3]),
-                                        st::pack_bf16x2(p[4], p[5]), st::pack_bf16x2(p[6], p[7])));
-        }
-  #pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          const int cc = jb * 2 + hh;
-  #pragma unroll
-          for (int db = 0; db < DB; ++db) {
-            const bf16x8 a = as_bf16x8(*(const uint4*)(vl + (db * 32 * VS + 2 * cc) * 8));
-            oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pf[hh], oacc[db], 0, 0, 0);
-          }
-        }
-      }
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
