@@ -149,6 +149,47 @@ __global__ __launch_bounds__(NTH) void lora_rk(int64_t Mo, int64_t R, int64_t Kc
                         blockIdx.y, Gs, Ss);
 }
 
+// The whole contraction in one workgroup (no split): output rows
+// [blockIdx.x*RK_BM, +RK_BM) and columns [64*blockIdx.z, +64) of
+// out[m*so_m + j*so_j] = alpha * sum (+ out when accumulating), written
+// directly -- no partials, no reduction launch, every column chunk in the
+// same launch.
+template <bool COL, bool SK1, int NB>
+__global__ __launch_bounds__(NTH) void lora_rk_direct(int64_t Mo, int64_t R, int64_t Kc,
+                                                     const uint16_t* __restrict__ G, int64_t ldg,
+                                                     int64_t g_bytes, const float* __restrict__ S,
+                                                     int64_t ssk, int64_t ssj, float alpha,
+                                                     float* __restrict__ out, int64_t so_m,
+                                                     int64_t so_j, int accumulate) {
+  __shared__ __attribute__((aligned(16))) uint16_t Gs[RK_BM * RK_LD];
+  __shared__ __attribute__((aligned(16))) uint16_t Ss[st::RK_SS];
+  const int64_t m0 = (int64_t)blockIdx.x * RK_BM, c0 = (int64_t)blockIdx.z * RK_RP;
+  const int64_t Rc = R - c0 < RK_RP ? R - c0 : RK_RP;
+  const float* Sc = S + c0 * ssj;
+  const int64_t sc_bytes = ((Kc - 1) * ssk + (Rc - 1) * ssj + 1) * 4;
+  f32x16 acc[NB];
+#pragma unroll
+  for (int c = 0; c < NB; ++c)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[c][v] = 0.0f;
+  st::rk_accumulate<COL, SK1, NB, false>(acc, Mo, Rc, m0, 0, (int)Kc, G, ldg, g_bytes, 0, Sc, ssk,
+                                         ssj, sc_bytes, nullptr, 0, nullptr, 0, Gs, Ss);
+#pragma unroll
+  for (int c = 0; c < NB; ++c) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int64_t m = m0 + st::rk_row(v);
+      const int j = st::rk_col(c);
+      if (m < Mo && j < Rc) {
+        float* o = out + m * so_m + (c0 + j) * so_j;
+        float y = alpha * acc[c][v];
+        if (accumulate) y += *o;
+        *o = y;
+      }
+    }
+  }
+}
+
 // ---- several rank-r products in one launch (the backward of a fused
 // projection: dT_s = dY_s B_s and dB_s = dY_s^T T_s for every segment s).
 // Each problem is a lora_rk product with its own operands, split count and
@@ -331,6 +372,26 @@ int lora_gemm_impl(int64_t Mo, int64_t No, int64_t Kc, const void* a, int32_t a_
                      ssk >= 0 && ssj >= 0 && g_bytes < (1ll << 31) && s_bytes < (1ll << 31);
     if (col >= 0 && vec) {
       const int ks = rk_ksplit(big, Kc);
+      const int64_t nchunk = st::cdiv(small, RK_RP);
+      // no split when the contraction is short or the row tiles and column
+      // chunks alone give every CU a few workgroups
+      if (ks == 1 || st::cdiv(big, RK_BM) * nchunk >= 512) {
+        // one workgroup per row tile and column chunk, no partials
+        const dim3 grid((unsigned)st::cdiv(big, RK_BM), 1u, (unsigned)st::cdiv(small, RK_RP));
+        auto go = [&](auto kern) {
+          kern<<<grid, NTH, 0, s>>>(big, small, Kc, G, ldg, g_bytes, S, ssk, ssj, alpha, out,
+                                    so_m, so_j, accumulate);
+        };
+        const bool sk1 = ssk == 1, nb2 = small > 32;
+        if (col) {
+          if (sk1) nb2 ? go(lora_rk_direct<true, true, 2>) : go(lora_rk_direct<true, true, 1>);
+          else nb2 ? go(lora_rk_direct<true, false, 2>) : go(lora_rk_direct<true, false, 1>);
+        } else {
+          if (sk1) nb2 ? go(lora_rk_direct<false, true, 2>) : go(lora_rk_direct<false, true, 1>);
+          else nb2 ? go(lora_rk_direct<false, false, 2>) : go(lora_rk_direct<false, false, 1>);
+        }
+        return st::check_launch("lora_rk_direct");
+      }
       const int64_t need = (int64_t)ks * big * (small < 64 ? small : 64) * 4;
       if (!workspace || workspace_bytes < need)
         return st::fail(ST_EWORKSPACE, "st_lora_gemm: needs %lld workspace bytes", (long long)need);

@@ -154,6 +154,24 @@ def _stream(dev):
     return _lib.stream_handle(dev)
 
 
+def _router_parts(router: torch.Tensor) -> torch.Tensor:
+    """``[hi; mid; lo]`` bf16 rows [3E, H] of an fp32 router with
+    hi + mid + lo == router exactly (normal-range values).  The router is
+    frozen: the split is kept on the tensor itself, remade only when its
+    version counter moves."""
+    cached = getattr(router, "_st_parts", None)
+    if cached is not None and cached[0] == router._version:
+        return cached[1]
+    w = router.detach().float()
+    hi = w.to(_BF16)
+    r1 = w - hi.float()
+    mid = r1.to(_BF16)
+    lo = (r1 - mid.float()).to(_BF16)
+    parts = torch.cat([hi, mid, lo], 0).contiguous()
+    router._st_parts = (router._version, parts)
+    return parts
+
+
 def sigmoid_router_logits(flat: torch.Tensor, router: torch.Tensor) -> torch.Tensor:
     """fp32 router logits ``F.linear(flat.float(), router.float())`` of
     deepseek.py:117 for bf16 ``flat [T, H]`` and a bf16 or fp32 ``router [E, H]``.
@@ -321,7 +339,14 @@ class _MoEFeedForward(torch.autograd.Function):
             _lib.call("st_moe_route_sigmoid_bwd", _lib.ptr(logits), _lib.ptr(indices),
                       _lib.ptr(dw), T, E, top_k, int(norm), float(rscale), _lib.ptr(dlogits), st)
             drouter = torch.empty((T, H), dtype=_F32, device=dev)
-            lora_gemm(T, H, E, dlogits, E, 1, router, H, 1, 1.0, drouter)
+            if router.dtype == _BF16:
+                lora_gemm(T, H, E, dlogits, E, 1, router, H, 1, 1.0, drouter)
+            else:
+                # fp32 router: W = hi + mid + lo exactly (bf16 parts), so
+                # dlogits @ W = [dlogits | dlogits | dlogits] @ [hi; mid; lo],
+                # one streaming product with every term an fp32 product
+                parts = _router_parts(router)
+                lora_gemm(T, H, 3 * E, dlogits.repeat(1, 3), 3 * E, 1, parts, H, 1, 1.0, drouter)
             dflat = torch.empty((T, H), dtype=_BF16, device=dev)
             _lib.call("st_moe_gather_sum", _lib.ptr(dxs), R, _lib.ptr(pick_row), T, top_k, H,
                       _lib.ptr(drouter), _lib.ST_DTYPE_F32, _lib.ptr(dflat), st)

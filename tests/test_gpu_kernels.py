@@ -546,6 +546,28 @@ def test_lora_gemm_strided_vs_float64(dev):
         torch.testing.assert_close(out3.cpu().double(), ref2, rtol=1e-5, atol=tol)
 
 
+@pytest.mark.parametrize("Kc", [256, 768])
+def test_lora_gemm_wide_output_without_split(dev, Kc):
+    """The router's input gradient shape: fp32 dlogits [2048, Kc] times a bf16
+    router [Kc, 7168].  Enough row tiles and 64-column chunks (56 x 32) to
+    fill the GPU, so every workgroup takes the whole contraction and writes
+    its outputs directly (one launch, no partials, no reduction); against
+    float64, written and accumulated."""
+    g = torch.Generator().manual_seed(Kc)
+    T, H = 2048, 7168
+    dl = torch.randn(T, Kc, generator=g) * 1e-3
+    w = (torch.randn(Kc, H, generator=g) * 0.02).to(BF)
+    ref = dl.double() @ w.double()
+    out = torch.empty(T, H, device=dev)
+    ops.lora_gemm(T, H, Kc, dl.to(dev), Kc, 1, w.to(dev), H, 1, 1.0, out)
+    torch.cuda.synchronize()
+    tol = 4e-6 * Kc ** 0.5 * ref.abs().max().item()
+    torch.testing.assert_close(out.cpu().double(), ref, rtol=1e-5, atol=tol)
+    ops.lora_gemm(T, H, Kc, dl.to(dev), Kc, 1, w.to(dev), H, 1, 0.5, out, accumulate=True)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out.cpu().double(), 1.5 * ref, rtol=1e-5, atol=2 * tol)
+
+
 @pytest.mark.parametrize("Mo,No,Kc", [(2048, 16, 4096), (300, 48, 1024), (16, 64, 2048)])
 def test_lora_gemm_carries_fp32_operands_exactly(dev, Mo, No, Kc):
     """The fp32 operand keeps all 24 bits: with a one-hot bf16 operand every
