@@ -136,10 +136,11 @@ constexpr int fwd_lds_elems() {
   return G * 2 * (BKT * KSLOTS<DQ> + DV * VSLOTS<BKT>) * 8;
 }
 
-// G = 1: 4 waves over all keys.  G = 2: 8 waves in two groups of 4 over the
-// same queries, group r taking K/V tiles r, r+2, ...; group 1's softmax state
-// (max, partial sums, O) is merged into group 0's at the end.
-template <int DQ, int DV, int BKT, int G>
+// QW query waves per key group (32 queries each, 32*QW per workgroup).
+// G = 1: one group over all keys.  G = 2: two groups over the same queries,
+// group r taking K/V tiles r, r+2, ...; group 1's softmax state (max, partial
+// sums, O) is merged into group 0's at the end.
+template <int DQ, int DV, int BKT, int G, int QW>
 __device__ __forceinline__ void fa_fwd_tile(const uint16_t* __restrict__ q,
                                             const uint16_t* __restrict__ k,
                                             const uint16_t* __restrict__ vt, int S, int H,
@@ -155,15 +156,16 @@ __device__ __forceinline__ void fa_fwd_tile(const uint16_t* __restrict__ q,
 
   const int tid = threadIdx.x, lane = tid & 63;
   // key group, wave in group (wave-uniform: tile indices and LDS bases are scalar)
-  const int grp = __builtin_amdgcn_readfirstlane((tid >> 6) / 4);
-  const int wave = __builtin_amdgcn_readfirstlane((tid >> 6) % 4);
+  constexpr int BQW = 32 * QW;  // queries per workgroup
+  const int grp = __builtin_amdgcn_readfirstlane((tid >> 6) / QW);
+  const int wave = __builtin_amdgcn_readfirstlane((tid >> 6) % QW);
   const int g = lane >> 5, c = lane & 31;
   const int hk = h / (H / Hkv);
   const uint16_t* qb = q + ((int64_t)(b * H + h) * S) * DQ;
   const uint16_t* kb = k + ((int64_t)(b * Hkv + hk) * S) * DQ;
   const int Sp = (S + 15) & ~15;                // staged V^T row length
   const uint16_t* vb = vt + ((int64_t)(b * Hkv + hk) * DV) * Sp;
-  const int q0 = qt * BQ + wave * 32;
+  const int q0 = qt * BQW + wave * 32;
   const int myq = q0 + c;
   uint16_t* glds = lds + grp * 2 * (LK + LV);   // this group's two tile buffers
 
@@ -180,7 +182,7 @@ __device__ __forceinline__ void fa_fwd_tile(const uint16_t* __restrict__ q,
     for (int v = 0; v < 16; ++v) oacc[i][v] = 0.0f;
   float m_run = -INFINITY, l_run = 0.0f;
 
-  const int qlast = min(qt * BQ + BQ, S) - 1;   // last query of the workgroup
+  const int qlast = min(qt * BQW + BQW, S) - 1;  // last query of the workgroup
   // causal: keys <= qlast; keys >= Sk (right padding) are masked out
   const int ntiles = min(qlast, Sk - 1) / BKT + 1;
   const int nsteps = (ntiles + G - 1) / G;      // group steps (tile u*G + grp)
@@ -189,17 +191,17 @@ __device__ __forceinline__ void fa_fwd_tile(const uint16_t* __restrict__ q,
   // the resource base.  K rows past S read zeros; V^T columns past a row's
   // end read the next row's first columns (or zeros past the head): every
   // such key is masked out, so its probability is exactly 0.
-  constexpr int KW = (KI + 3) / 4, VW = (VI + 3) / 4;
+  constexpr int KW = (KI + QW - 1) / QW, VW = (VI + QW - 1) / QW;
   uint32_t koff[KW], voff[VW];
 #pragma unroll
   for (int i = 0; i < KW; ++i) {
-    const int P = (i * 4 + wave) * 64 + lane;
+    const int P = (i * QW + wave) * 64 + lane;
     const int row = min(P / KS, BKT - 1), ch = min(P % KS, DQ / 8 - 1);
     koff[i] = (uint32_t)(row * DQ + ch * 8) * 2;
   }
 #pragma unroll
   for (int i = 0; i < VW; ++i) {
-    const int P = (i * 4 + wave) * 64 + lane;
+    const int P = (i * QW + wave) * 64 + lane;
     const int d = min(P / VS, DV - 1), ch = min(P % VS, BKT / 8 - 1);
     voff[i] = (uint32_t)(d * Sp + ch * 8) * 2;
   }
@@ -211,10 +213,10 @@ __device__ __forceinline__ void fa_fwd_tile(const uint16_t* __restrict__ q,
     uint16_t* vs = ks + LK;
 #pragma unroll
     for (int i = 0; i < KW; ++i)
-      if (i * 4 + wave < KI) b2lds16(rk, koff[i], ks + (i * 4 + wave) * 64 * 8);
+      if (i * QW + wave < KI) b2lds16(rk, koff[i], ks + (i * QW + wave) * 64 * 8);
 #pragma unroll
     for (int i = 0; i < VW; ++i)
-      if (i * 4 + wave < VI) b2lds16(rv, voff[i], vs + (i * 4 + wave) * 64 * 8);
+      if (i * QW + wave < VI) b2lds16(rv, voff[i], vs + (i * QW + wave) * 64 * 8);
   };
 
   if (grp < ntiles) issue(grp, 0);
@@ -372,12 +374,13 @@ __device__ __forceinline__ int pair_tile(int x, int it, int nq, int paired) {
   return it == 0 ? nq - 1 - x : x;
 }
 
-template <int DQ, int DV, int BKT, int G>
-__global__ __launch_bounds__(NTH * G, G == 1 && BKT == 64 && DQ <= 128 ? 2 : 1) void fa_fwd(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-    const uint16_t* __restrict__ vt, int S, int H, int Hkv, float sl2,
-    uint16_t* __restrict__ out, float* __restrict__ lse, int nq, int paired,
-    const int* __restrict__ kvlen) {
+template <int DQ, int DV, int BKT, int G, int QW = 4>
+__global__ __launch_bounds__(64 * QW * G, G == 1 && QW == 4 && BKT == 64 && DQ <= 128 ? 2 : 1)
+void fa_fwd(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+            const uint16_t* __restrict__ vt, int S, int H, int Hkv, float sl2,
+            uint16_t* __restrict__ out, float* __restrict__ lse, int nq, int paired,
+            const int* __restrict__ kvlen) {
+  static_assert(QW * 32 * (DV + 8) <= fwd_lds_elems<DQ, DV, BKT, G>(), "output staging fits");
   __shared__ __attribute__((aligned(16))) uint16_t lds[fwd_lds_elems<DQ, DV, BKT, G>()];
   const WgIdx w = wg_index(paired ? (nq + 1) / 2 : nq, H);
   for (int it = 0; it < 1 + paired; ++it) {
@@ -386,8 +389,8 @@ __global__ __launch_bounds__(NTH * G, G == 1 && BKT == 64 && DQ <= 128 ? 2 : 1) 
       if (qt == pair_tile(w.x, 0, nq, paired)) break;
       __syncthreads();  // the previous tile's output staging still reads LDS
     }
-    fa_fwd_tile<DQ, DV, BKT, G>(q, k, vt, S, H, Hkv, sl2, out, lse, qt, w.h, w.b,
-                                key_len(kvlen, w.b, S), lds);
+    fa_fwd_tile<DQ, DV, BKT, G, QW>(q, k, vt, S, H, Hkv, sl2, out, lse, qt, w.h, w.b,
+                                    key_len(kvlen, w.b, S), lds);
   }
 }
 
@@ -1010,18 +1013,28 @@ int attn_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, int64_t B,
                          (unsigned)(B * Hkv)), NTH, 0, s>>>(v, vt, S, Sp, DV);
   int rc = st::check_launch("transpose_heads");
   if (rc) return rc;
-  const int nq = (int)st::cdiv(S, BQ);
-  // paired schedules use two key groups (8 waves) so each SIMD still holds
-  // two waves; with DQ = 192 two groups' tiles do not fit in LDS
-  const int paired = DQ <= 128 ? pair_mode(nq, B * H) : 0;
-  dim3 grid((unsigned)((paired ? (nq + 1) / 2 : nq) * H * B));
   const float sl2 = scale * LOG2E;
-  if (paired)
-    fa_fwd<DQ, DV, 64, (DQ <= 128 ? 2 : 1)><<<grid, NTH * (DQ <= 128 ? 2 : 1), 0, s>>>(
-        q, k, vt, (int)S, (int)H, (int)Hkv, sl2, out, lse, nq, paired, kvlen);
-  else
-    fa_fwd<DQ, DV, 64, 1><<<grid, NTH, 0, s>>>(q, k, vt, (int)S, (int)H, (int)Hkv, sl2, out, lse,
-                                               nq, paired, kvlen);
+  if constexpr (DQ > 128) {
+    // two key groups' tiles do not fit in LDS: one group of 8 query waves
+    // (256 queries) over every key tile, so each SIMD still holds two waves
+    const int nq = (int)st::cdiv(S, 2 * BQ);
+    const int paired = pair_mode(nq, B * H);
+    dim3 grid((unsigned)((paired ? (nq + 1) / 2 : nq) * H * B));
+    fa_fwd<DQ, DV, 64, 1, 8><<<grid, NTH * 2, 0, s>>>(q, k, vt, (int)S, (int)H, (int)Hkv, sl2, out,
+                                                      lse, nq, paired, kvlen);
+  } else {
+    const int nq = (int)st::cdiv(S, BQ);
+    // paired schedules use two key groups (8 waves) so each SIMD still holds
+    // two waves
+    const int paired = pair_mode(nq, B * H);
+    dim3 grid((unsigned)((paired ? (nq + 1) / 2 : nq) * H * B));
+    if (paired)
+      fa_fwd<DQ, DV, 64, 2><<<grid, NTH * 2, 0, s>>>(q, k, vt, (int)S, (int)H, (int)Hkv, sl2, out,
+                                                     lse, nq, paired, kvlen);
+    else
+      fa_fwd<DQ, DV, 64, 1><<<grid, NTH, 0, s>>>(q, k, vt, (int)S, (int)H, (int)Hkv, sl2, out,
+                                                 lse, nq, paired, kvlen);
+  }
   return st::check_launch("fa_fwd");
 }
 
