@@ -441,7 +441,7 @@ __device__ __forceinline__ bf16x8 tile_tr(const uint16_t* t, int kb, int nb, int
 // dQ (and Delta = rowsum(dO * O)) per 128-query tile: S^T = K Q^T,
 // P^T = exp2(S^T - lse), dP^T = V dO^T, dS^T = P^T (dP^T - Delta),
 // dQ^T += K^T dS^T; keys up to the diagonal.
-template <int DQ, int DV, int BKT, int G>
+template <int DQ, int DV, int BKT, int G, int QW>
 __device__ __forceinline__ void fa_bwd_dq_tile(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ o,
@@ -450,20 +450,21 @@ __device__ __forceinline__ void fa_bwd_dq_tile(
     int b, int Sk, uint16_t* lds) {
   constexpr int DSQ = DQ / 16, DSV = DV / 16, DB = DQ / 32;
   constexpr int LTK = BKT * DQ, LTV = BKT * DV;  // bf16 per K / V tile
-  constexpr int PERK = BKT * DQ / 8 / NTH, PERV = BKT * DV / 8 / NTH;  // 16-byte chunks per thread
-  static_assert(PERK * NTH * 8 == LTK && PERV * NTH * 8 == LTV, "tiles are whole thread copies");
+  constexpr int NTG = 64 * QW;  // threads per key group
+  constexpr int PERK = BKT * DQ / 8 / NTG, PERV = BKT * DV / 8 / NTG;  // 16-byte chunks per thread
+  static_assert(PERK * NTG * 8 == LTK && PERV * NTG * 8 == LTV, "tiles are whole thread copies");
   const int tid = threadIdx.x, lane = tid & 63;
   // key group, wave in group (wave-uniform: tile indices and LDS bases are scalar)
-  const int grp = __builtin_amdgcn_readfirstlane((tid >> 6) / 4);
-  const int wave = __builtin_amdgcn_readfirstlane((tid >> 6) % 4);
-  const int gtid = tid % NTH;
+  const int grp = __builtin_amdgcn_readfirstlane((tid >> 6) / QW);
+  const int wave = __builtin_amdgcn_readfirstlane((tid >> 6) % QW);
+  const int gtid = tid % NTG;
   const int g = lane >> 5, c = lane & 31;
   const int hk = h / (H / Hkv);
   const int64_t ldt = (int64_t)H * DV;  // token-major row stride of O and dO
   const uint16_t* qb = q + ((int64_t)(b * H + h) * S) * DQ;
   const uint16_t* kb = k + ((int64_t)(b * Hkv + hk) * S) * DQ;
   const uint16_t* vb = v + ((int64_t)(b * Hkv + hk) * S) * DV;
-  const int q0 = qt * BQ + wave * 32;
+  const int q0 = qt * (32 * QW) + wave * 32;
   const int myq = q0 + c;
   const bool qok = myq < S;
   const int64_t trow = ((int64_t)b * S + myq) * ldt + (int64_t)h * DV;
@@ -498,24 +499,24 @@ __device__ __forceinline__ void fa_bwd_dq_tile(
 #pragma unroll
     for (int e = 0; e < 16; ++e) dqacc[i][e] = 0.0f;
 
-  const int qlast = min(qt * BQ + BQ, S) - 1;
+  const int qlast = min(qt * (32 * QW) + 32 * QW, S) - 1;
   const int ntiles = min(qlast, Sk - 1) / BKT + 1;
   const int nsteps = (ntiles + G - 1) / G;
   // K and V tiles [key][D] (tswz layout) by buffer copies into LDS: fixed
   // lane offsets, the tile's first key in the resource base; keys past S
   // read zeros and are masked out below
-  using CK = RowCopy<DQ, NTH>;
-  using CV = RowCopy<DV, NTH>;
+  using CK = RowCopy<DQ, NTG>;
+  using CV = RowCopy<DV, NTG>;
   uint32_t koff[CK::uniform ? 1 : PERK], voff[CV::uniform ? 1 : PERV];
 #pragma unroll
   for (int i = 0; i < (CK::uniform ? 1 : PERK); ++i) {
-    const int P = i * NTH + gtid;
+    const int P = i * NTG + gtid;
     const int row = P / (DQ / 8);
     koff[i] = (uint32_t)(row * DQ + ((P % (DQ / 8)) ^ swz<DQ>(row)) * 8) * 2;
   }
 #pragma unroll
   for (int i = 0; i < (CV::uniform ? 1 : PERV); ++i) {
-    const int P = i * NTH + gtid;
+    const int P = i * NTG + gtid;
     const int row = P / (DV / 8);
     voff[i] = (uint32_t)(row * DV + ((P % (DV / 8)) ^ swz<DV>(row)) * 8) * 2;
   }
@@ -527,13 +528,13 @@ __device__ __forceinline__ void fa_bwd_dq_tile(
     for (int i = 0; i < PERK; ++i) {
       const int r0 = k0 + (CK::uniform ? i * CK::rows : 0);
       const auto rk = st::make_rsrc(kb + (int64_t)r0 * DQ, (int64_t)max(S - r0, 0) * DQ * 2);
-      b2lds16(rk, koff[CK::uniform ? 0 : i], ks + (i * NTH + wave * 64) * 8);
+      b2lds16(rk, koff[CK::uniform ? 0 : i], ks + (i * NTG + wave * 64) * 8);
     }
 #pragma unroll
     for (int i = 0; i < PERV; ++i) {
       const int r0 = k0 + (CV::uniform ? i * CV::rows : 0);
       const auto rv = st::make_rsrc(vb + (int64_t)r0 * DV, (int64_t)max(S - r0, 0) * DV * 2);
-      b2lds16(rv, voff[CV::uniform ? 0 : i], vs + (i * NTH + wave * 64) * 8);
+      b2lds16(rv, voff[CV::uniform ? 0 : i], vs + (i * NTG + wave * 64) * 8);
     }
   };
   // one 32-key block: S^T, dP^T, dS^T (masked when `edge`), dQ^T += K^T dS^T
@@ -612,9 +613,14 @@ __device__ __forceinline__ void fa_bwd_dq_tile(
     __syncthreads();
     if (grp == 1) return;
   }
-  // dQ = scale * dQ^T^T, staged through LDS as query rows, head-major out
+  // dQ = scale * dQ^T^T, staged through LDS as query rows, head-major out;
+  // with 8 query waves the two halves take turns with the staging space
   constexpr int LDO = DQ + 8;
-  uint16_t* os = lds + wave * 32 * LDO;
+  static_assert(4 * 32 * LDO <= G * 2 * BKT * (DQ + DV), "four waves' staging fits");
+  uint16_t* os = lds + (wave % 4) * 32 * LDO;
+  for (int half = 0; half < QW / 4; ++half) {
+  if (half) __syncthreads();  // the previous half's read-back is done
+  if (wave / 4 != half) continue;
 #pragma unroll
   for (int db = 0; db < DB; ++db)
 #pragma unroll
@@ -636,9 +642,11 @@ __device__ __forceinline__ void fa_bwd_dq_tile(
       *(uint4*)(dqb + (int64_t)qq * DQ + ch * 8) = make_uint4(a.x, a.y, bb.x, bb.y);
     }
   }
+  }
 }
-template <int DQ, int DV, int BKT, int G>
-__global__ __launch_bounds__(NTH * G, G == 1 && BKT == 64 && DQ <= 128 ? 2 : 1) void fa_bwd_dq(
+template <int DQ, int DV, int BKT, int G, int QW = 4>
+__global__ __launch_bounds__(64 * QW * G, G == 1 && QW == 4 && BKT == 64 && DQ <= 128 ? 2 : 1)
+void fa_bwd_dq(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ o,
     const uint16_t* __restrict__ dout, const float* __restrict__ lse, int S, int H, int Hkv,
@@ -652,8 +660,8 @@ __global__ __launch_bounds__(NTH * G, G == 1 && BKT == 64 && DQ <= 128 ? 2 : 1) 
       if (qt == pair_tile(w.x, 0, nq, paired)) break;
       __syncthreads();
     }
-    fa_bwd_dq_tile<DQ, DV, BKT, G>(q, k, v, o, dout, lse, S, H, Hkv, sl2, scale, delta, dq, qt,
-                                   w.h, w.b, key_len(kvlen, w.b, S), lds);
+    fa_bwd_dq_tile<DQ, DV, BKT, G, QW>(q, k, v, o, dout, lse, S, H, Hkv, sl2, scale, delta, dq,
+                                       qt, w.h, w.b, key_len(kvlen, w.b, S), lds);
   }
 }
 
@@ -1048,19 +1056,31 @@ int attn_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint
   float* dk_part = (float*)(base + (B * H * S * 4 + 255) / 256 * 256);
   float* dv_part = dk_part + B * H * S * DQ;
   const float sl2 = scale * LOG2E;
-  const int nq = (int)st::cdiv(S, BQ);
-  const int paired = DQ <= 128 ? pair_mode(nq, B * H) : 0;
-  dim3 g1((unsigned)((paired ? (nq + 1) / 2 : nq) * H * B));
   const int nk = (int)st::cdiv(S, KT2);
   const int paired_k = pair_mode(nk, B * H);
   dim3 g2((unsigned)((paired_k ? (nk + 1) / 2 : nk) * H * B));
-  if (paired)
-    fa_bwd_dq<DQ, DV, 64, (DQ <= 128 ? 2 : 1)><<<g1, NTH * (DQ <= 128 ? 2 : 1), 0, s>>>(
-        q, k, v, out, dout, lse, (int)S, (int)H, (int)Hkv, sl2, scale, delta, dq, nq, paired,
-        kvlen);
-  else
-    fa_bwd_dq<DQ, DV, 64, 1><<<g1, NTH, 0, s>>>(q, k, v, out, dout, lse, (int)S, (int)H,
-                                                (int)Hkv, sl2, scale, delta, dq, nq, paired, kvlen);
+  if constexpr (DQ > 128) {
+    // two key groups' tiles do not fit in LDS: one group of 8 query waves
+    // (256 queries), paired light and heavy query tiles
+    const int nq = (int)st::cdiv(S, 2 * BQ);
+    const int paired = pair_mode(nq, B * H);
+    dim3 g1((unsigned)((paired ? (nq + 1) / 2 : nq) * H * B));
+    fa_bwd_dq<DQ, DV, 64, 1, 8><<<g1, NTH * 2, 0, s>>>(q, k, v, out, dout, lse, (int)S, (int)H,
+                                                      (int)Hkv, sl2, scale, delta, dq, nq, paired,
+                                                      kvlen);
+  } else {
+    const int nq = (int)st::cdiv(S, BQ);
+    const int paired = pair_mode(nq, B * H);
+    dim3 g1((unsigned)((paired ? (nq + 1) / 2 : nq) * H * B));
+    if (paired)
+      fa_bwd_dq<DQ, DV, 64, 2><<<g1, NTH * 2, 0, s>>>(q, k, v, out, dout, lse, (int)S, (int)H,
+                                                     (int)Hkv, sl2, scale, delta, dq, nq, paired,
+                                                     kvlen);
+    else
+      fa_bwd_dq<DQ, DV, 64, 1><<<g1, NTH, 0, s>>>(q, k, v, out, dout, lse, (int)S, (int)H,
+                                                  (int)Hkv, sl2, scale, delta, dq, nq, paired,
+                                                  kvlen);
+  }
   int rc = st::check_launch("fa_bwd_dq");
   if (rc) return rc;
   // one query head per KV head (MLA): the pass writes dK and dV in bf16 itself,
