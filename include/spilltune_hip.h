@@ -165,6 +165,12 @@ int st_q4_linear_dgrad_swiglu(const uint16_t* dy, int64_t M, int64_t N, int64_t 
  * Generic skinny fp32-accumulating product used by the LoRA terms:
  *   out[m,n] = (accumulate ? out[m,n] : 0) + alpha * sum_k a(m,k) * b(k,n)
  * a(m,k) = a[m*sam + k*sak], b(k,n) = b[k*sbk + n*sbn], each bf16 or fp32.
+ * With one bf16 and one fp32 operand the product streams the bf16 one and
+ * takes the fp32 one 64 columns at a time.  st_lora_gemm_workspace_bytes is
+ * the size that runs every 64-column chunk in one launch; a workspace down to
+ * one chunk's split-K partials runs the chunks in turn, with the same bits.
+ * Products whose row tiles and column chunks fill the GPU by themselves run
+ * without a split and use no workspace.
  */
 int64_t st_lora_gemm_workspace_bytes(int64_t Mo, int64_t No, int64_t Kc);
 int st_lora_gemm(int64_t Mo, int64_t No, int64_t Kc,
@@ -178,8 +184,8 @@ int st_lora_gemm(int64_t Mo, int64_t No, int64_t Kc,
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  No counterpart in the reference.  The split-K partials live in
  * a static 32 MiB device array of the library (one per GPU, held until the
- * process ends); a product that needs more (st_lora_gemm_workspace_bytes >
- * 32 MiB) is rejected with ST_EUNSUPPORTED.  Nothing is allocated or freed.
+ * process ends); a product whose partials need more even one 64-column chunk
+ * at a time is rejected with ST_EUNSUPPORTED.  Nothing is allocated or freed.
  * Every call on one GPU shares that array: calls that overlap in time on one
  * GPU (two streams, two threads) race and must be ordered by the caller.
  * Results equal st_lora_gemm's bit for bit (same kernels, same order).

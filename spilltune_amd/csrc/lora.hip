@@ -137,16 +137,22 @@ __device__ __forceinline__ void rk_tile(int64_t Mo, int64_t R, int64_t Kc,
   }
 }
 
+// blockIdx.z selects the 64-column chunk [64z, 64z + 64) of the R fp32
+// columns; chunk z's partials [ks][Mo][Rz] start at part + z*ks*Mo*64
 template <bool COL, bool SK1, int NB>
 __global__ __launch_bounds__(NTH) void lora_rk(int64_t Mo, int64_t R, int64_t Kc,
                                               const uint16_t* __restrict__ G, int64_t ldg,
                                               int64_t g_bytes, const float* __restrict__ S,
-                                              int64_t ssk, int64_t ssj, int64_t s_bytes,
-                                              int64_t klen, float* __restrict__ part) {
+                                              int64_t ssk, int64_t ssj, int64_t klen, int ks,
+                                              float* __restrict__ part) {
   __shared__ __attribute__((aligned(16))) uint16_t Gs[RK_BM * RK_LD];
   __shared__ __attribute__((aligned(16))) uint16_t Ss[st::RK_SS];
-  rk_tile<COL, SK1, NB>(Mo, R, Kc, G, ldg, g_bytes, S, ssk, ssj, s_bytes, klen, part, blockIdx.x,
-                        blockIdx.y, Gs, Ss);
+  const int64_t c0 = (int64_t)blockIdx.z * RK_RP;
+  const int64_t Rc = R - c0 < RK_RP ? R - c0 : RK_RP;
+  const int64_t sc_bytes = ((Kc - 1) * ssk + (Rc - 1) * ssj + 1) * 4;
+  rk_tile<COL, SK1, NB>(Mo, Rc, Kc, G, ldg, g_bytes, S + c0 * ssj, ssk, ssj, sc_bytes, klen,
+                        part + (int64_t)blockIdx.z * ks * Mo * RK_RP, blockIdx.x, blockIdx.y, Gs,
+                        Ss);
 }
 
 // The whole contraction in one workgroup (no split): output rows
@@ -260,27 +266,30 @@ __global__ __launch_bounds__(NTH) void lora_rk_reduce_batch(const RkBatch b) {
   *o = v;
 }
 
-// sums the split-K partials [ks][Mo][R] into out[m*so_m + j*so_j]
+// sums the split-K partials into out[m*so_m + j*so_j] (+ out): column j of
+// chunk z = j/64 reads [ks][Mo][Rz] at part + z*ks*Mo*64 (Rz = its width)
 __global__ __launch_bounds__(NTH) void lora_rk_reduce(int64_t Mo, int64_t R, int ks,
                                                      const float* __restrict__ part, float alpha,
                                                      float* __restrict__ out, int64_t so_m,
                                                      int64_t so_j, int accumulate) {
   int64_t e = (int64_t)blockIdx.x * NTH + threadIdx.x;
   if (e >= Mo * R) return;
-  // eight loads in flight, summed in ascending z (a fixed order: deterministic)
-  const float* p = part + e;
-  const int64_t st = Mo * R;
+  const int64_t m = e / R, j = e % R;
+  const int64_t z = j / RK_RP, jz = j % RK_RP;
+  const int64_t Rz = R - z * RK_RP < RK_RP ? R - z * RK_RP : RK_RP;
+  // eight loads in flight, summed in ascending split order (a fixed order: deterministic)
+  const float* p = part + z * ks * Mo * RK_RP + m * Rz + jz;
+  const int64_t st = Mo * Rz;
   float s = 0.0f;
-  int z = 0;
-  for (; z + 8 <= ks; z += 8) {
+  int q = 0;
+  for (; q + 8 <= ks; q += 8) {
     float v[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = p[(z + u) * st];
+    for (int u = 0; u < 8; ++u) v[u] = p[(q + u) * st];
 #pragma unroll
     for (int u = 0; u < 8; ++u) s += v[u];
   }
-  for (; z < ks; ++z) s += p[z * st];
-  const int64_t m = e / R, j = e % R;
+  for (; q < ks; ++q) s += p[q * st];
   float v = alpha * s;
   float* o = out + m * so_m + j * so_j;
   if (accumulate) v += *o;
@@ -321,12 +330,21 @@ void launch_partial(int64_t Mo, int64_t No, int64_t Kc, const void* a, int64_t s
 
 }  // namespace
 
-extern "C" int64_t st_lora_gemm_workspace_bytes(int64_t Mo, int64_t No, int64_t Kc) {
+// Workspace of one st_lora_gemm: the generic kernel's partials or the
+// streaming kernel's; `all_chunks` sizes the latter for every 64-column
+// chunk in one launch (preferred), else for one chunk at a time (the least
+// the call accepts).
+static int64_t lora_gemm_workspace(int64_t Mo, int64_t No, int64_t Kc, bool all_chunks) {
   if (Mo <= 0 || No <= 0 || Kc <= 0) return 0;
   int64_t generic = (int64_t)ksplit_for(Mo, No, Kc) * Mo * No * 4;
   int64_t big = Mo > No ? Mo : No, small = Mo > No ? No : Mo;
-  int64_t rk = (int64_t)rk_ksplit(big, Kc) * big * small * 4;
+  int64_t cols = small <= 64 ? small : all_chunks ? st::cdiv(small, 64) * 64 : 64;
+  int64_t rk = (int64_t)rk_ksplit(big, Kc) * big * cols * 4;
   return generic > rk ? generic : rk;
+}
+
+extern "C" int64_t st_lora_gemm_workspace_bytes(int64_t Mo, int64_t No, int64_t Kc) {
+  return lora_gemm_workspace(Mo, No, Kc, true);
 }
 
 namespace {
@@ -392,21 +410,22 @@ int lora_gemm_impl(int64_t Mo, int64_t No, int64_t Kc, const void* a, int32_t a_
         }
         return st::check_launch("lora_rk_direct");
       }
-      const int64_t need = (int64_t)ks * big * (small < 64 ? small : 64) * 4;
-      if (!workspace || workspace_bytes < need)
-        return st::fail(ST_EWORKSPACE, "st_lora_gemm: needs %lld workspace bytes", (long long)need);
+      // every 64-column chunk in one launch when the workspace holds all
+      // their partials, else chunk by chunk through one chunk's partials
+      const int64_t one = (int64_t)ks * big * (small < 64 ? small : 64) * 4;
+      const int64_t all = (int64_t)ks * big * nchunk * RK_RP * 4;
+      const bool together = nchunk == 1 || (workspace && workspace_bytes >= all);
+      if (!workspace || workspace_bytes < one)
+        return st::fail(ST_EWORKSPACE, "st_lora_gemm: needs %lld workspace bytes", (long long)one);
       const int64_t klen = st::cdiv(st::cdiv(Kc, ks), RK_BK) * RK_BK;
-      const dim3 grid((unsigned)st::cdiv(big, RK_BM), (unsigned)ks);
       float* part = (float*)workspace;
-      // more than 64 fp32 columns: chunks of 64 in turn (the partials buffer
-      // is reused; the stream orders the chunks)
-      for (int64_t c0 = 0; c0 < small; c0 += 64) {
-        const int64_t sc = small - c0 < 64 ? small - c0 : 64;
+      for (int64_t c0 = 0; c0 < small; c0 += together ? small : 64) {
+        const int64_t sc = together ? small : (small - c0 < 64 ? small - c0 : 64);
         const float* Sc = S + c0 * ssj;
-        const int64_t sc_bytes = ((Kc - 1) * ssk + (sc - 1) * ssj + 1) * 4;
+        const dim3 grid((unsigned)st::cdiv(big, RK_BM), (unsigned)ks,
+                        (unsigned)st::cdiv(sc, RK_RP));
         auto go = [&](auto kern) {
-          kern<<<grid, NTH, 0, s>>>(big, sc, Kc, G, ldg, g_bytes, Sc, ssk, ssj, sc_bytes, klen,
-                                    part);
+          kern<<<grid, NTH, 0, s>>>(big, sc, Kc, G, ldg, g_bytes, Sc, ssk, ssj, klen, ks, part);
         };
         const bool sk1 = ssk == 1, nb2 = sc > 32;
         if (col) {
@@ -494,7 +513,8 @@ extern "C" int st_lora_gemm_noalloc(int64_t Mo, int64_t No, int64_t Kc, const vo
                                     float* out, int64_t ldo, int32_t accumulate,
                                     st_stream_t stream) {
   ST_CHECK_ARG(Mo >= 0 && No >= 0 && Kc >= 0, "st_lora_gemm_noalloc: negative shape");
-  const int64_t need = st_lora_gemm_workspace_bytes(Mo, No, Kc);
+  // the least workspace the product accepts (chunk by chunk if need be)
+  const int64_t need = lora_gemm_workspace(Mo, No, Kc, false);
   if (need > kScratchBytes)
     return st::fail(ST_EUNSUPPORTED,
                     "st_lora_gemm_noalloc: the product needs %lld scratch bytes, more than the "

@@ -176,18 +176,15 @@ def sigmoid_router_logits(flat: torch.Tensor, router: torch.Tensor) -> torch.Ten
     """fp32 router logits ``F.linear(flat.float(), router.float())`` of
     deepseek.py:117 for bf16 ``flat [T, H]`` and a bf16 or fp32 ``router [E, H]``.
 
-    They run in slices of 64 experts on the streaming MFMA rank-r kernel,
-    which splits its fp32 operand into three bf16 parts that sum to it
+    They run on the streaming MFMA rank-r kernel (every 64-expert slice in
+    one launch), which splits its fp32 operand into three bf16 parts that sum to it
     exactly, so every product is the fp32 product, summed in fp32 -- for a
     bf16 router and for an fp32 one (the reference keeps DeepSeek routers in
     fp32)."""
     T, H = flat.shape
     E = router.shape[0]
     logits = torch.empty((T, E), dtype=_F32, device=flat.device)
-    w = router.float()
-    for e0 in range(0, E, 64):
-        e1 = min(E, e0 + 64)
-        lora_gemm(T, e1 - e0, H, flat, H, 1, w[e0:e1], 1, H, 1.0, logits[:, e0:e1])
+    lora_gemm(T, E, H, flat, H, 1, router.float(), 1, H, 1.0, logits)
     return logits
 
 
