@@ -1490,12 +1490,20 @@ int launch(const GemmParams& p, hipStream_t stream) {
 // split tail), 2568 = 128x256 8 waves (the grouped forward)).  For the N = 4096 forwards (o,
 // down) the 256x128 register-operand and the 128x256 tiles measured no faster
 // than the warp-specialised kernel.
+int cu_count();
+
 int tile_choice(int mode, int64_t M, int64_t P) {
   const char* env = getenv("ST_GEMM_TILE");
   if (env) return atoi(env);
   // the transposed-operand dgrad runs out of registers at 256x256 (8 waves)
   if (mode == FWD_Q4 && st::cdiv(M, 256) * st::cdiv(P, 256) >= 192) return 256;
-  if (st::cdiv(M, 256) * st::cdiv(P, 128) >= 192) return 2562;
+  const int64_t t2562 = st::cdiv(M, 256) * st::cdiv(P, 128);
+  if (t2562 >= 192) return 2562;
+  // a forward whose 256x128 tiles fit one round where 128x128 tiles need a
+  // second (the MLA q_a|kv_a projection, 2112 columns at 2048 tokens: 107
+  // against 167 us)
+  if (mode == FWD_Q4 && t2562 <= cu_count() && st::cdiv(M, 128) * st::cdiv(P, 128) > cu_count())
+    return 2562;
   return 128;
 }
 
