@@ -144,13 +144,20 @@ def concat_rows(weights) -> Q4Weight | None:
 
 # ----------------------------------------------------------------- timing hook
 class KernelTimer:
-    """Brackets every fused 4-bit GEMM launch with HIP events on the launch
-    stream, keyed ``(pass, M, N, K)``; durations are read after a sync."""
+    """Brackets fused 4-bit GEMM launches with HIP events on the launch
+    stream, keyed ``(pass, M, N, K)``; durations are read after a sync.
+    ``only``: time the launches with that key alone and run the others
+    unbracketed (each timing event leaves the stream idle for a few
+    microseconds, which a timed region should not carry for every launch)."""
 
-    def __init__(self):
+    def __init__(self, only=None):
         self.events = {}
+        self.only = only
 
     def record(self, key, fn):
+        if self.only is not None and key != self.only:
+            fn()
+            return
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
         start.record()
