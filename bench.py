@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Per-layer training throughput of the MI355X NF4 LoRA path.
 
-Workload: one Llama-3-8B-shape decoder layer
+Workload (benchmark config 2, the headline one): one Llama-3-8B-shape decoder layer
 (hidden 4096, intermediate 14336, 32 q / 8 kv heads of 128), frozen weights
 N(0, 0.02) stored nf4-g128 (fp32 absmax), LoRA r=16 alpha=32 on all seven
 projections (A = randn*0.02, B ~ N(0, 0.02)), batch 1 x 2048 tokens, bf16
@@ -32,7 +32,7 @@ CONFIGS = {
     "tiny": dict(H=256, I=688, heads=4, kv=4, D=64, eps=1e-5, r=8, alpha=16.0, B=2, S=128,
                  theta=500000.0),
 }
-# full streamed Qwen3-8B-shape training step.  The terminal's
+# Benchmark config 3: full streamed Qwen3-8B-shape training step.  The terminal's
 # token chunk bounds only the logits held at once (the loss and gradients do not depend
 # on it beyond the fp32 order of the per-chunk loss sum); 4096 takes the whole sequence
 # in one pass (1.24 GB of bf16 logits), so the head GEMMs get tiles enough for 256x256
@@ -40,15 +40,15 @@ QWEN3 = dict(H=4096, I=12288, heads=32, kv=8, D=128, eps=1e-6, r=16, alpha=32.0,
              vocab=151936, S=4096, accumulation=4, theta=1000000.0, token_chunk=4096)
 QWEN3_METRIC = ("train tokens/s, full streamed Qwen3-8B-shape step (36 nf4-g128 layers from "
                 "pinned host RAM, 2 device slots, grad accumulation 4)")
-# Qwen3-MoE-30B-A3B-shape MoE feed-forward
+# Benchmark config 4: Qwen3-MoE-30B-A3B-shape MoE feed-forward
 MOE = dict(H=2048, I=768, E=128, k=8, T=4096, r=8, alpha=16.0, norm=True)
 MOE_METRIC = "train tokens/s per MoE layer fwd+bwd (Qwen3-MoE-30B-A3B shape, NF4 experts)"
-# the MoE feed-forward of the DeepSeek-V3-shape layer
+# Benchmark config 5, its MoE part: the MoE feed-forward of the DeepSeek-V3-shape layer
 DSMOE = dict(H=7168, I=2048, E=256, k=8, groups=8, group_k=4, scale=2.5, T=2048, r=8, alpha=16.0,
              shared_I=2048)
 DSMOE_METRIC = ("train tokens/s per DeepSeek-V3-shape MoE feed-forward fwd+recompute+bwd "
                 "(256 NF4 routed experts + shared expert)")
-# one streamed DeepSeek-V3-shape MLA + MoE layer
+# Benchmark config 5: one streamed DeepSeek-V3-shape MLA + MoE layer
 DSV3 = dict(H=7168, heads=128, q_rank=1536, kv_rank=512, nope=128, rope=64, v=128, E=256, I=2048,
             shared_I=2048, k=8, groups=8, group_k=4, scale=2.5, T=2048, r=8, alpha=16.0, eps=1e-6,
             interleave=True,
@@ -127,7 +127,7 @@ def cpu_model():
 
 
 def cpu_config1(steps=20):
-    """BASELINE config 1 on the CPU path: the tiny Llama (2 layers, hidden 256,
+    """Benchmark config 1 on the CPU path: the tiny Llama (2 layers, hidden 256,
     intermediate 688, 4 heads of 64, vocab 1024, nf4-g128 weights, LoRA r=8 on
     all seven projections), batch 2 x 128, 20 AdamW steps through the oracle's
     training loop (engine.py:162-182 restated).  Returns seconds and tokens/s."""
@@ -572,7 +572,7 @@ def deepseek_moe_bench(args):
     """Config 5's MoE feed-forward: 2048 tokens through the sigmoid group-limited
     router (8 groups, best 4, top-8, bias, normalised, x2.5), 256 routed nf4-g128
     experts of [2x2048, 7168] + [7168, 2048] and the shared expert (same shape)
-    with LoRA r=8 on its gate/up/down (BASELINE: LoRA on the shared expert, not
+    with LoRA r=8 on its gate/up/down (the benchmark puts LoRA on the shared expert, not
     on the routed ones).  One step = forward without grad + forward with grad
     + backward (the StreamingBlockFunction lifecycle).  The experts are
     synthetic packed bytes (random codes, scales in [0.01, 0.03)): the cost
@@ -1030,7 +1030,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one MI355X; "
-              "see DESIGN.md for how the path would shard", file=sys.stderr)
+              "one process per GPU over RCCL is how the path would shard (not built)", file=sys.stderr)
         sys.exit(2)
 
     import torch

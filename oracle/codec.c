@@ -10,7 +10,7 @@
  *                  :66-116 (encode), :158-170 (decode_into).  Codes 1..15 map to
  *                  -7..7, code 0 (-8) is reserved, two codes per byte low nibble
  *                  first, one fp32 scale per 128 *flattened* elements.
- *   nf4-g128       The BASELINE storage format: same container as int4-sym-g128
+ *   nf4-g128       The benchmark storage format: same container as int4-sym-g128
  *                  (payload uint8[ceil(n/128)*64] low nibble first, fp32 absmax
  *                  per flat 128-group) with the published NF4 codebook (QLoRA,
  *                  Dettmers et al. 2023, arXiv:2305.14314, appendix E) in place

@@ -1,5 +1,5 @@
 """The adapter factory end to end on the GPU: a tiny Llama checkpoint
-(BASELINE config 1 shapes) exported to an nf4-g128 archive, built through
+(benchmark config 1 shapes) exported to an nf4-g128 archive, built through
 the reference's factory call, streamed through Q4SlotSession (the engine's
 one-line session swap) and trained for 30 AdamW steps on two cycled rows
 against the CPU oracle's loss curve (north-star criterion |d loss| <= 1e-2)."""

@@ -1,4 +1,4 @@
-"""The BASELINE workloads at their real shapes on the HIP path, against the
+"""The benchmark workloads at their real shapes on the HIP path, against the
 CPU oracle (north-star criteria: outputs rel. err <= 2e-2, gradients cosine
 >= 0.999, loss curves within 1e-2).
 

@@ -198,7 +198,7 @@ def test_rmsnorm_fwd_bwd_vs_oracle():
 @pytest.mark.parametrize("H", [512, 2048, 4096, 7168, 8192, 8200])
 def test_rmsnorm_row_kernels_vs_oracle(H):
     """The 16-byte row kernels of st_rmsnorm_fwd/bwd at the hidden sizes of
-    the BASELINE models and around 8192 against the oracle's norm and its
+    the benchmark models and around 8192 against the oracle's norm and its
     autograd VJP plus a residual gradient (the dres operand)."""
     g = torch.Generator().manual_seed(H)
     x = torch.randn(33, H, generator=g).to(BF)

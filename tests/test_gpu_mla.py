@@ -284,7 +284,7 @@ def test_config5_attention_dims_layer_step(oracle_codec, monkeypatch):
 
 @pytest.mark.timeout(1200)
 def test_config5_composed_layer_2048_tokens_256_experts(oracle_codec, monkeypatch):
-    """BASELINE config 5 whole: one DeepSeek-V3-shape layer (MLA with 128
+    """Benchmark config 5 whole: one DeepSeek-V3-shape layer (MLA with 128
     heads, q_lora_rank 1536, kv_lora_rank 512, YaRN interleaved rotary; 256
     routed experts of width 2048, top 8 of 8 groups / best 4, shared expert;
     LoRA r=8 on the attention projections and the shared expert) at 2048

@@ -1,4 +1,4 @@
-"""Seeded causal-LM training on the tiny Llama configuration (
+"""Seeded causal-LM training on the tiny Llama configuration (benchmark config 1:
 2 layers, hidden 256, intermediate 688, 4 heads of 64, vocab 1024, nf4-g128,
 LoRA r=8 alpha=16 on all seven projections, batch 2 x 128): the HIP path's
 loss curve must agree with the CPU oracle's to within 1e-2 at every step
