@@ -242,23 +242,38 @@ __global__ __launch_bounds__(NTH) void lora_rk_batch(const RkBatch b) {
                               q.s_bytes, q.klen, q.part, tile, split, Gs, Ss);
 }
 
+// p[0] + p[st] + ... + p[(ks-1)*st], summed in ascending split order (a
+// fixed order: deterministic); sixteen loads in flight per batch, so the
+// usual 16 splits cost one memory round trip
+__device__ __forceinline__ float sum_splits(const float* __restrict__ p, int64_t st, int ks) {
+  float s = 0.0f;
+  int q = 0;
+  for (; q + 16 <= ks; q += 16) {
+    float v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) v[u] = p[(q + u) * st];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) s += v[u];
+  }
+  if (q + 8 <= ks) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = p[(q + u) * st];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s += v[u];
+    q += 8;
+  }
+  for (; q < ks; ++q) s += p[q * st];
+  return s;
+}
+
 // sums each problem's partials in ascending split order (as lora_rk_reduce)
 __global__ __launch_bounds__(NTH) void lora_rk_reduce_batch(const RkBatch b) {
   const int64_t e = (int64_t)blockIdx.x * NTH + threadIdx.x;
   if (e >= b.elems) return;
   const RkProblem& q = b.p[rk_find(b, e, true)];
-  const int64_t le = e - q.e0, st = q.big * q.R;
-  const float* p = q.part + le;
-  float s = 0.0f;
-  int z = 0;
-  for (; z + 8 <= q.ks; z += 8) {
-    float v[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = p[(z + u) * st];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) s += v[u];
-  }
-  for (; z < q.ks; ++z) s += p[z * st];
+  const int64_t le = e - q.e0;
+  const float s = sum_splits(q.part + le, q.big * q.R, q.ks);
   const int64_t m = le / q.R, j = le % q.R;
   float v = q.alpha * s;
   float* o = q.out + m * q.so_m + j * q.so_j;
@@ -277,19 +292,7 @@ __global__ __launch_bounds__(NTH) void lora_rk_reduce(int64_t Mo, int64_t R, int
   const int64_t m = e / R, j = e % R;
   const int64_t z = j / RK_RP, jz = j % RK_RP;
   const int64_t Rz = R - z * RK_RP < RK_RP ? R - z * RK_RP : RK_RP;
-  // eight loads in flight, summed in ascending split order (a fixed order: deterministic)
-  const float* p = part + z * ks * Mo * RK_RP + m * Rz + jz;
-  const int64_t st = Mo * Rz;
-  float s = 0.0f;
-  int q = 0;
-  for (; q + 8 <= ks; q += 8) {
-    float v[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = p[(q + u) * st];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) s += v[u];
-  }
-  for (; q < ks; ++q) s += p[q * st];
+  const float s = sum_splits(part + z * ks * Mo * RK_RP + m * Rz + jz, Mo * Rz, ks);
   float v = alpha * s;
   float* o = out + m * so_m + j * so_j;
   if (accumulate) v += *o;
