@@ -568,6 +568,51 @@ def test_lora_gemm_wide_output_without_split(dev, Kc):
     torch.testing.assert_close(out.cpu().double(), 1.5 * ref, rtol=1e-5, atol=2 * tol)
 
 
+def _lora_gemm_ws(dev, Mo, No, Kc, a, sam, sak, b, sbk, sbn, alpha, out, ws_bytes):
+    """st_lora_gemm with a workspace of exactly ``ws_bytes``."""
+    dt = {BF: _lib.ST_DTYPE_BF16, torch.float32: _lib.ST_DTYPE_F32}
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+    _lib.call("st_lora_gemm", Mo, No, Kc, _lib.ptr(a), dt[a.dtype], sam, sak, _lib.ptr(b),
+              dt[b.dtype], sbk, sbn, float(alpha), _lib.ptr(out), out.stride(0), 0, _lib.ptr(ws),
+              ws_bytes, _lib.stream_handle(dev))
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("R", [65, 150])
+def test_lora_gemm_chunks_in_one_launch_equal_chunk_by_chunk(dev, R):
+    """More than 64 fp32 columns on the split path (too few row tiles to skip
+    the split): with the workspace st_lora_gemm_workspace_bytes asks for, every
+    64-column chunk runs in one launch and one reduction; with one chunk's
+    partials only, the chunks run in turn.  Same splits, same summation order:
+    the outputs are equal bit for bit, for the row form (T = x A^T) and the
+    column form (dA = dT^T x), and match float64."""
+    g = torch.Generator().manual_seed(R)
+    M, K = 2048, 4096
+    x = torch.randn(M, K, generator=g).to(BF)
+    A = torch.randn(R, K, generator=g) * 0.02
+    dT = torch.randn(M, R, generator=g)
+    xd, Ad, dTd = x.to(dev), A.to(dev), dT.to(dev)
+    # split counts (rk_ksplit: 512 workgroups over 128-row tiles, >= 256 contraction
+    # elements each): 16 for the 2048 rows x 4096 row form, 8 for the 4096 x 2048 column form
+    for Mo, No, Kc, args, big, ks, ref in (
+            (M, R, K, (xd, K, 1, Ad, 1, K), M, 16, x.double() @ A.double().T),
+            (R, K, M, (dTd, 1, R, xd, K, 1), K, 8, dT.double().T @ x.double())):
+        full = _lib.query("st_lora_gemm_workspace_bytes", Mo, No, Kc)
+        one = ks * big * 64 * 4  # one 64-column chunk's partials
+        assert full >= ks * big * 64 * ((R + 63) // 64) * 4 > one
+        outs = []
+        for ws_bytes in (full, one):
+            out = torch.empty(Mo, No, device=dev)
+            _lora_gemm_ws(dev, Mo, No, Kc, *args, 1.0, out, ws_bytes)
+            outs.append(out.cpu())
+        assert torch.equal(outs[0].view(torch.int32), outs[1].view(torch.int32)), (Mo, No, Kc)
+        tol = 4e-6 * Kc ** 0.5 * ref.abs().max().item()
+        torch.testing.assert_close(outs[0].double(), ref, rtol=1e-5, atol=tol)
+    with pytest.raises(ValueError, match="workspace"):
+        out = torch.empty(M, R, device=dev)
+        _lora_gemm_ws(dev, M, R, K, xd, K, 1, Ad, 1, K, 1.0, out, ks * M * 64 * 4 - 16)
+
+
 @pytest.mark.parametrize("Mo,No,Kc", [(2048, 16, 4096), (300, 48, 1024), (16, 64, 2048)])
 def test_lora_gemm_carries_fp32_operands_exactly(dev, Mo, No, Kc):
     """The fp32 operand keeps all 24 bits: with a one-hot bf16 operand every
