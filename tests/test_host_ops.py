@@ -62,3 +62,25 @@ def test_supervised_chunk_intervals_host_rule():
     assert ops.supervised_chunk_intervals(labels, 4) == ((4, 8),)
     with pytest.raises(ValueError, match="token chunk"):
         ops.supervised_chunk_intervals(labels, 0)
+
+
+def test_router_parts_sum_exactly_and_follow_the_version():
+    """The fp32 router's bf16 parts [hi; mid; lo] (the operand of its input
+    gradient on the rank-r kernel) sum back to every fp32 value exactly,
+    including values far from 1 and with low-order bits set; they are kept
+    on the tensor and remade only after an in-place change (version)."""
+    from spilltune_amd import moe
+    g = torch.Generator().manual_seed(5)
+    E, H = 8, 96
+    w = torch.randn(E, H, generator=g) * torch.exp2(torch.randint(-30, 30, (E, H), generator=g).float())
+    w[0, :4] = torch.tensor([1.0 + 2 ** -23, -(2 - 2 ** -22), 2 ** -100, 3.0e20])
+    parts = moe._router_parts(w)
+    assert parts.shape == (3 * E, H) and parts.dtype == torch.bfloat16
+    back = parts[:E].double() + parts[E:2 * E].double() + parts[2 * E:].double()
+    assert torch.equal(back, w.double())
+    assert moe._router_parts(w) is parts  # unchanged tensor: the kept split
+    w.mul_(0.5)
+    again = moe._router_parts(w)
+    assert again is not parts
+    back = again[:E].double() + again[E:2 * E].double() + again[2 * E:].double()
+    assert torch.equal(back, w.double())
